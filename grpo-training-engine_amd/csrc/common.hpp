@@ -1,0 +1,64 @@
+// Shared device helpers and C-ABI error plumbing for libgrpo_hip (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdarg.h>
+
+#include "../../include/grpo_hip.h"
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+namespace grpo {
+
+// ---------------------------------------------------------------- errors --
+void set_error(const char* fmt, ...);
+
+inline int einval(const char* what) {
+  set_error("invalid argument: %s", what);
+  return GRPO_EINVAL;
+}
+
+inline int hip_check(hipError_t e, const char* where) {
+  if (e == hipSuccess) return GRPO_OK;
+  set_error("%s: %s", where, hipGetErrorString(e));
+  return (int)e > 0 ? (int)e : 1;
+}
+
+// Launch status of the kernel just enqueued (catches bad launch configs).
+inline int launch_check(const char* name) { return hip_check(hipGetLastError(), name); }
+
+inline hipStream_t as_stream(grpo_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ---------------------------------------------------------------- bf16 ---
+// float -> bf16 round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  return __builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ float bf2f(uint16_t b) {
+  return __uint_as_float(((uint32_t)b) << 16);
+}
+// Round a float to the nearest bf16 value, returned as float.
+__device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
+// Two floats -> packed bf16 pair (lo in bits 0..15).
+__device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
+  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+}
+__device__ __forceinline__ float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+__device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
+  return __builtin_amdgcn_perm(hi, lo, sel);
+}
+
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__device__ __forceinline__ f32x4_t mfma16x16x32(uint4 a, uint4 b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+
+}  // namespace grpo

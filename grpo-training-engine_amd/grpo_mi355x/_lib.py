@@ -1,0 +1,133 @@
+"""ctypes binding of libgrpo_hip.so (the C ABI declared in include/grpo_hip.h).
+
+The library is loaded after ``torch`` so that it binds to the HIP runtime torch
+already loaded.  A missing library or a missing gfx950 device raises
+``ImportError`` -- the reference's convention for an unavailable kernel backend
+(``src/triton_kernels/__init__.py:297``, caught by ``src/core/lora.py:122`` and
+``src/grpo/trainer.py:401``).  There is no CPU fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+import torch  # noqa: F401  (must be imported before the HIP library is loaded)
+
+from ._build import LIB_PATH
+
+_c = ctypes
+_VP, _I64, _I32, _F32, _SZ = _c.c_void_p, _c.c_int64, _c.c_int, _c.c_float, _c.c_size_t
+
+# name -> (restype, argtypes); mirrors include/grpo_hip.h one to one.
+SIGNATURES = {
+    "grpo_version": (_I32, []),
+    "grpo_init": (_I32, []),
+    "grpo_last_error": (_c.c_char_p, []),
+    "grpo_nf4_dequant": (_I32, [_VP, _VP, _VP, _VP, _I64, _I32, _VP]),
+    "grpo_nf4_lora_linear_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
+    "grpo_nf4_lora_linear": (
+        _I32,
+        [_VP, _I64, _VP, _VP, _VP, _I32, _VP, _VP, _VP, _I32, _F32, _VP, _I64, _I32, _I32, _I32,
+         _VP, _SZ, _VP],
+    ),
+    "grpo_paged_kv_append": (
+        _I32,
+        [_VP, _VP, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _I32, _I32, _I32, _I32, _I32, _VP],
+    ),
+    "grpo_paged_attn_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "grpo_paged_attn_decode": (
+        _I32,
+        [_VP, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32,
+         _I32, _F32, _VP, _SZ, _VP],
+    ),
+}
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+_load_error: str | None = None
+_device_ok: bool | None = None
+_device_error: str | None = None
+
+
+def library_path() -> Path:
+    return LIB_PATH
+
+
+def _load() -> ctypes.CDLL:
+    global _lib, _load_error
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if _load_error is not None:
+            raise ImportError(_load_error)
+        if not LIB_PATH.exists():
+            _load_error = (f"libgrpo_hip.so not built ({LIB_PATH}); run "
+                           "__graft_entry__.build() or python -m grpo_mi355x._build")
+            raise ImportError(_load_error)
+        try:
+            lib = ctypes.CDLL(str(LIB_PATH))
+        except OSError as exc:  # pragma: no cover - depends on the host
+            _load_error = f"cannot load {LIB_PATH}: {exc}"
+            raise ImportError(_load_error) from exc
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = lib
+        return lib
+
+
+def library() -> ctypes.CDLL:
+    """The loaded library (no device needed); ImportError if it is not built."""
+    return _load()
+
+
+def device_library() -> ctypes.CDLL:
+    """The library after checking that a gfx950 device is usable.
+
+    Raises ImportError when there is no device, so callers that follow the
+    reference's ``except ImportError`` fallback chain behave as they do there.
+    """
+    global _device_ok, _device_error
+    lib = _load()
+    if _device_ok is None:
+        if not torch.cuda.is_available():
+            _device_ok, _device_error = False, "no ROCm/HIP device visible to torch"
+        else:
+            rc = lib.grpo_init()
+            _device_ok = rc == 0
+            if not _device_ok:
+                _device_error = lib.grpo_last_error().decode(errors="replace")
+    if not _device_ok:
+        raise ImportError(f"libgrpo_hip unavailable: {_device_error}")
+    return lib
+
+
+def available() -> bool:
+    """True when the library is built and a gfx950 device is usable."""
+    try:
+        device_library()
+        return True
+    except ImportError:
+        return False
+
+
+def check(rc: int, what: str) -> None:
+    """Map a C-ABI return code to the reference's exception types."""
+    if rc == 0:
+        return
+    msg = _load().grpo_last_error().decode(errors="replace")
+    if rc < 0:
+        raise ValueError(f"{what}: {msg}")
+    raise RuntimeError(f"{what}: HIP error {rc}: {msg}")
+
+
+def stream_handle(device: torch.device | None = None) -> int:
+    """hipStream_t of torch's current stream on ``device`` (as an integer)."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()

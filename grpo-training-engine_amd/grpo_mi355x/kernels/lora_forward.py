@@ -1,0 +1,163 @@
+"""``lora_fused_forward`` -- the NF4 + LoRA linear on the HIP kernel.
+
+Same call surface and dispatch as the reference's
+``src/triton_kernels/lora_forward.py:933-1037``:
+
+* ``lora_layer`` (a ``ManualLoRALayer``-like object) or explicit
+  ``base_layer/lora_A/lora_B/scaling/dropout``;
+* dropout p > 0 -> ``ValueError`` (``:958-960``);
+* a base weight with ``quant_state`` and ``prefer_base_layer=False`` -> the
+  fused kernel (``FusedLoRAFunction``, ``:966-984``); otherwise the adapter
+  branch ``base_layer(x) + B(A(x)) * scaling`` (``:986-1037``);
+* shape/dtype/device problems -> ``ValueError`` (``_validate_inputs``,
+  ``:435-487``); rank <= 0 -> ``ValueError`` (``:670-671``).
+
+The fused forward is one launch of ``grpo_nf4_lora_linear``.  Backward (the
+training-phase kernels of ``:761-930``) is not part of the rollout path and
+raises ``NotImplementedError``.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import ops
+
+
+def _validate_inputs(x: torch.Tensor, weight_4bit: torch.Tensor, quant_state,
+                     lora_A: torch.Tensor, lora_B: torch.Tensor):
+    """``lora_forward.py:435-487`` (same messages, same ValueError)."""
+    if x.ndim != 3:
+        raise ValueError(f"x must be [batch, seq_len, hidden], got {x.shape}.")
+    if lora_A.ndim != 2 or lora_B.ndim != 2:
+        raise ValueError("lora_A and lora_B must be 2D weight matrices.")
+    if not x.is_cuda:
+        raise ValueError("x must be on CUDA device.")
+    if not weight_4bit.is_cuda:
+        raise ValueError("weight_4bit must be on CUDA device.")
+    if not lora_A.is_cuda or not lora_B.is_cuda:
+        raise ValueError("lora_A and lora_B must be on CUDA device.")
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"x must be float16/bfloat16, got {x.dtype}.")
+    if lora_A.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"lora_A must be float16/bfloat16, got {lora_A.dtype}.")
+    if lora_B.dtype not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"lora_B must be float16/bfloat16, got {lora_B.dtype}.")
+    if lora_A.dtype != lora_B.dtype:
+        raise ValueError(
+            f"lora_A and lora_B must have the same dtype, got {lora_A.dtype} and {lora_B.dtype}.")
+    batch, seq_len, in_features = x.shape
+    out_features, in_features_w = tuple(quant_state.shape)
+    if in_features != in_features_w:
+        raise ValueError("Input hidden size does not match quantized weight shape: "
+                         f"{in_features} vs {in_features_w}.")
+    rank, in_features_a = lora_A.shape
+    out_features_b, rank_b = lora_B.shape
+    if in_features_a != in_features:
+        raise ValueError(f"lora_A input features mismatch: {in_features_a} vs {in_features}.")
+    if out_features_b != out_features or rank_b != rank:
+        raise ValueError("lora_B shape mismatch: expected "
+                         f"[{out_features}, {rank}], got {lora_B.shape}.")
+    return batch * seq_len, out_features, in_features, rank
+
+
+def _extract_quant_state(weight_4bit: torch.Tensor, quant_state):
+    """``lora_forward.py:527-576`` for the states this kernel decodes."""
+    if bool(getattr(quant_state, "nested", False)):
+        # Double-quantized absmax (lora_forward.py:187-199) is decoded by the
+        # reference kernel; the HIP kernel does not implement it yet.
+        raise ValueError("nested (double-quantized) NF4 quant_state is not supported by the "
+                         "HIP kernel yet.")
+    device = weight_4bit.device
+    absmax = quant_state.absmax.to(device=device).contiguous()
+    code = quant_state.code.to(device=device, dtype=torch.float32).contiguous()
+    if absmax.dtype != torch.float32:
+        raise ValueError(f"absmax must be float32 for a non-nested state, got {absmax.dtype}.")
+    if code.numel() != 16:
+        raise ValueError("quant_state.code must have 16 entries (a 4-bit codebook).")
+    return absmax, code, int(quant_state.blocksize)
+
+
+class FusedLoRAFunction(torch.autograd.Function):
+    """Forward = one fused NF4+LoRA kernel launch (``lora_forward.py:653-759``)."""
+
+    @staticmethod
+    def forward(ctx, x, weight_4bit, quant_state, lora_A, lora_B, scaling, bias):
+        m, n, k, r = _validate_inputs(x, weight_4bit, quant_state, lora_A, lora_B)
+        if r <= 0:
+            raise ValueError(f"LoRA rank must be > 0, got {r}.")
+        if x.dtype != torch.bfloat16 or lora_A.dtype != torch.bfloat16:
+            raise ValueError("the HIP NF4+LoRA kernel computes in bfloat16; got "
+                             f"x {x.dtype}, lora {lora_A.dtype}.")
+        absmax, code, blocksize = _extract_quant_state(weight_4bit, quant_state)
+        w = weight_4bit.contiguous().view(-1)
+        if w.dtype != torch.uint8:
+            w = w.view(torch.uint8)
+        x_flat = x.contiguous().view(m, k)
+        out = torch.empty((m, n), device=x.device, dtype=x.dtype)
+        if m > 0 and n > 0:
+            ops.nf4_lora_linear(x_flat, w, absmax, code, blocksize, n, bias=bias,
+                                lora_a=lora_A, lora_b=lora_B, scaling=float(scaling), out=out)
+        return out.view(x.shape[:-1] + (n,))
+
+    @staticmethod
+    def backward(ctx, grad_out):  # pragma: no cover - training path, out of scope
+        raise NotImplementedError(
+            "backward of the fused NF4+LoRA linear is not implemented in grpo_mi355x "
+            "(rollout decode runs under torch.no_grad).")
+
+
+def lora_fused_forward(x: torch.Tensor, base_layer=None, lora_A=None, lora_B=None,
+                       scaling: Optional[float] = None, dropout=None, lora_layer=None,
+                       prefer_base_layer: bool = False) -> torch.Tensor:
+    """Drop-in for ``src.triton_kernels.lora_forward.lora_fused_forward``."""
+    if lora_layer is not None:
+        base_layer = getattr(lora_layer, "base_layer", None)
+        lora_A = getattr(lora_layer, "lora_A", None)
+        lora_B = getattr(lora_layer, "lora_B", None)
+        scaling = getattr(lora_layer, "scaling", None)
+        dropout = getattr(lora_layer, "lora_dropout", None)
+    if base_layer is None or lora_A is None or lora_B is None or scaling is None:
+        raise ValueError("Provide lora_layer or base_layer/lora_A/lora_B/scaling for fused LoRA.")
+    dropout_p = getattr(dropout, "p", 0.0) if dropout is not None else 0.0
+    if dropout_p and dropout_p > 0.0:
+        raise ValueError("Dropout is not supported in lora_fused_forward.")
+
+    weight_4bit = getattr(base_layer, "weight", None)
+    lora_A_weight = getattr(lora_A, "weight", lora_A)
+    lora_B_weight = getattr(lora_B, "weight", lora_B)
+
+    if (not prefer_base_layer and weight_4bit is not None
+            and getattr(weight_4bit, "quant_state", None) is not None):
+        return FusedLoRAFunction.apply(x, weight_4bit, weight_4bit.quant_state, lora_A_weight,
+                                       lora_B_weight, float(scaling),
+                                       getattr(base_layer, "bias", None))
+
+    # Adapter branch (lora_forward.py:986-1037): base layer + the two adapter
+    # products, each rounded to the adapter dtype, scaled, cast, added.
+    if x.ndim != 3:
+        raise ValueError(f"x must be [batch, seq_len, hidden], got {x.shape}.")
+    if lora_A_weight.ndim != 2 or lora_B_weight.ndim != 2:
+        raise ValueError("lora_A and lora_B must be 2D weight matrices.")
+    if not x.is_cuda or not lora_A_weight.is_cuda or not lora_B_weight.is_cuda:
+        raise ValueError("x, lora_A and lora_B must be on CUDA device.")
+    r = lora_A_weight.shape[0]
+    if r <= 0:
+        raise ValueError(f"LoRA rank must be > 0, got {r}.")
+    if lora_A_weight.shape[1] != x.shape[-1] or lora_B_weight.shape[1] != r:
+        raise ValueError("lora_A/lora_B shape mismatch.")
+    base_output = base_layer(x.contiguous())
+    if getattr(base_output, "requires_grad", False):
+        base_output = base_output.clone()
+    x_lora = x.reshape(-1, x.shape[-1]).to(lora_A_weight.dtype)
+    t = (x_lora.float() @ lora_A_weight.float().t()).to(lora_A_weight.dtype)
+    u = (t.float() @ lora_B_weight.float().t()).to(lora_A_weight.dtype)
+    u = u * float(scaling)
+    if u.dtype != base_output.dtype:
+        u = u.to(base_output.dtype)
+    return base_output + u.view(base_output.shape)
+
+
+__all__ = ["lora_fused_forward", "FusedLoRAFunction"]

@@ -1,0 +1,214 @@
+"""Tensor-level wrappers of the C ABI (one call = one or two kernel launches).
+
+These validate shapes/dtypes on the host (``ValueError``, like the reference's
+``_validate_inputs``), pass raw device pointers and torch's current stream to
+``libgrpo_hip.so``, and manage the per-device workspaces the kernels need.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib
+
+# ----------------------------------------------------------- workspaces --
+
+_workspaces: dict[tuple[str, int], torch.Tensor] = {}
+
+
+def workspace(kind: str, nbytes: int, device: torch.device) -> torch.Tensor | None:
+    """A zero-initialised uint8 scratch tensor of at least ``nbytes`` per (kind, device).
+
+    The NF4 linear's split-K counters must start at zero and are left at zero
+    by every call; attention partials need no initialisation.  Kinds are never
+    shared, so one kind's data cannot corrupt another's counters.  Calls on
+    different streams must not run concurrently with the same workspace.
+    """
+    if nbytes <= 0:
+        return None
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    key = (kind, idx)
+    ws = _workspaces.get(key)
+    if ws is None or ws.numel() < nbytes:
+        size = max(nbytes, 1 << 20)
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _workspaces[key] = ws
+    return ws
+
+
+def reserve_workspace(kind: str, nbytes: int, device: torch.device) -> None:
+    """Pre-size a workspace (call before HIP-graph capture)."""
+    workspace(kind, nbytes, device)
+
+
+# ------------------------------------------------------------- helpers --
+
+def _need_cuda(*ts: torch.Tensor | None) -> None:
+    for t in ts:
+        if t is not None and not t.is_cuda:
+            raise ValueError("all tensors must be on the ROCm/HIP device.")
+
+
+def _need_dtype(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}.")
+
+
+# --------------------------------------------------------------- NF4 ---
+
+def nf4_dequant(packed: torch.Tensor, absmax: torch.Tensor, code: torch.Tensor, numel: int,
+                blocksize: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """Bit-exact NF4 dequantization to a flat bf16 tensor of ``numel`` elements."""
+    lib = _lib.device_library()
+    _need_cuda(packed, absmax, code)
+    _need_dtype(packed, torch.uint8, "packed weight")
+    _need_dtype(absmax, torch.float32, "absmax")
+    _need_dtype(code, torch.float32, "code")
+    if packed.numel() * 2 < numel:
+        raise ValueError(f"packed weight holds {packed.numel() * 2} nibbles, need {numel}.")
+    if absmax.numel() * blocksize < numel:
+        raise ValueError("absmax too short for numel/blocksize.")
+    if code.numel() != 16:
+        raise ValueError("code must have 16 entries.")
+    packed, absmax, code = packed.contiguous(), absmax.contiguous(), code.contiguous()
+    if out is None:
+        out = torch.empty(numel, dtype=torch.bfloat16, device=packed.device)
+    rc = lib.grpo_nf4_dequant(packed.data_ptr(), absmax.data_ptr(), code.data_ptr(),
+                              out.data_ptr(), numel, blocksize, _lib.stream_handle(packed.device))
+    _lib.check(rc, "grpo_nf4_dequant")
+    return out
+
+
+def nf4_lora_linear_workspace_bytes(m: int, n: int, k: int, r: int) -> int:
+    return int(_lib.library().grpo_nf4_lora_linear_workspace_bytes(m, n, k, r))
+
+
+def nf4_lora_linear(x2d: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor,
+                    code: torch.Tensor, blocksize: int, n: int, bias: torch.Tensor | None = None,
+                    lora_a: torch.Tensor | None = None, lora_b: torch.Tensor | None = None,
+                    scaling: float = 1.0, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``y[M, N] = W_nf4(x) + bias + B(A(x)) * scaling`` (bf16) -- one fused launch."""
+    lib = _lib.device_library()
+    _need_cuda(x2d, packed, absmax, code, bias, lora_a, lora_b)
+    if x2d.ndim != 2:
+        raise ValueError(f"x must be 2-D [M, K], got {tuple(x2d.shape)}.")
+    _need_dtype(x2d, torch.bfloat16, "x")
+    m, k = x2d.shape
+    if x2d.stride(1) != 1:
+        x2d = x2d.contiguous()
+    r = 0
+    if lora_a is not None:
+        r = lora_a.shape[0]
+        if lora_a.shape != (r, k) or lora_b is None or lora_b.shape != (n, r):
+            raise ValueError("lora_A must be [r, K] and lora_B [N, r].")
+        _need_dtype(lora_a, torch.bfloat16, "lora_A")
+        _need_dtype(lora_b, torch.bfloat16, "lora_B")
+        lora_a, lora_b = lora_a.contiguous(), lora_b.contiguous()
+    if bias is not None:
+        if bias.numel() != n:
+            raise ValueError(f"bias must have {n} elements.")
+        bias = bias.to(torch.bfloat16).contiguous()
+    if packed.numel() * 2 < n * k:
+        raise ValueError("packed weight smaller than N*K/2 bytes.")
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=x2d.device)
+    elif out.shape != (m, n) or out.stride(1) != 1 or out.dtype != torch.bfloat16:
+        raise ValueError("out must be a bf16 [M, N] tensor with unit column stride.")
+    nbytes = int(lib.grpo_nf4_lora_linear_workspace_bytes(m, n, k, r))
+    ws = workspace("nf4_linear", nbytes, x2d.device)
+    rc = lib.grpo_nf4_lora_linear(
+        x2d.data_ptr(), x2d.stride(0), packed.data_ptr(), absmax.data_ptr(), code.data_ptr(),
+        int(blocksize), _lib.ptr(bias), _lib.ptr(lora_a), _lib.ptr(lora_b), r, float(scaling),
+        out.data_ptr(), out.stride(0), m, n, k, _lib.ptr(ws), 0 if ws is None else ws.numel(),
+        _lib.stream_handle(x2d.device))
+    _lib.check(rc, "grpo_nf4_lora_linear")
+    return out
+
+
+# ----------------------------------------------------------- paged KV ---
+
+def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> None:
+    if k_cache.ndim != 4 or v_cache.ndim != 4:
+        raise ValueError("k_cache/v_cache must be [num_blocks, heads, block, head_dim].")
+    if k_cache.shape != v_cache.shape:
+        raise ValueError("k_cache and v_cache must have identical shapes.")
+    _need_dtype(k_cache, torch.bfloat16, "k_cache")
+    _need_dtype(v_cache, torch.bfloat16, "v_cache")
+    if not (k_cache.is_contiguous() and v_cache.is_contiguous()):
+        raise ValueError("k_cache/v_cache must be contiguous.")
+
+
+def _check_tables(block_tables: torch.Tensor, context_lens: torch.Tensor, b: int) -> None:
+    if block_tables.ndim != 2 or block_tables.shape[0] != b:
+        raise ValueError("block_tables must be [batch, max_blocks].")
+    if context_lens.ndim != 1 or context_lens.shape[0] != b:
+        raise ValueError("context_lens must be [batch].")
+    _need_dtype(block_tables, torch.int32, "block_tables")
+    _need_dtype(context_lens, torch.int32, "context_lens")
+    if block_tables.stride(1) != 1 or not context_lens.is_contiguous():
+        raise ValueError("block_tables rows and context_lens must be contiguous.")
+
+
+def paged_kv_append(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor,
+                    v_cache: torch.Tensor, block_tables: torch.Tensor,
+                    context_lens: torch.Tensor) -> None:
+    """Write ``k_new/v_new [B, Hkv, D]`` at slot ``context_lens[b]`` of each sequence."""
+    lib = _lib.device_library()
+    _need_cuda(k_new, v_new, k_cache, v_cache, block_tables, context_lens)
+    _check_cache(k_cache, v_cache)
+    nb, hkv, bs, d = k_cache.shape
+    if k_new.shape != v_new.shape or k_new.ndim != 3 or k_new.shape[1:] != (hkv, d):
+        raise ValueError(f"k_new/v_new must be [B, {hkv}, {d}].")
+    b = k_new.shape[0]
+    _check_tables(block_tables, context_lens, b)
+    k_new = k_new.to(torch.bfloat16)
+    v_new = v_new.to(torch.bfloat16)
+    if k_new.stride(2) != 1 or k_new.stride() != v_new.stride():
+        k_new, v_new = k_new.contiguous(), v_new.contiguous()
+    rc = lib.grpo_paged_kv_append(
+        k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1), k_cache.data_ptr(),
+        v_cache.data_ptr(), nb, block_tables.data_ptr(), block_tables.stride(0),
+        context_lens.data_ptr(), b, hkv, d, bs, block_tables.shape[1],
+        _lib.stream_handle(k_cache.device))
+    _lib.check(rc, "grpo_paged_kv_append")
+
+
+def paged_attention_workspace_bytes(b: int, hq: int, hkv: int, d: int, bs: int,
+                                    max_blocks: int) -> int:
+    return int(_lib.library().grpo_paged_attn_workspace_bytes(b, hq, hkv, d, bs, max_blocks))
+
+
+def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                           block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
+                           out_dtype: torch.dtype = torch.float32,
+                           out: torch.Tensor | None = None) -> torch.Tensor:
+    """GQA paged decode attention; ``q [B, Hq, D]`` bf16 -> ``[B, Hq, D]`` out_dtype."""
+    lib = _lib.device_library()
+    _need_cuda(q, k_cache, v_cache, block_tables, context_lens)
+    _check_cache(k_cache, v_cache)
+    nb, hkv, bs, d = k_cache.shape
+    if q.ndim != 3 or q.shape[2] != d:
+        raise ValueError(f"q must be [B, Hq, {d}].")
+    b, hq, _ = q.shape
+    if hq % hkv != 0:
+        raise ValueError(f"query heads ({hq}) must be a multiple of KV heads ({hkv}).")
+    _check_tables(block_tables, context_lens, b)
+    q = q.to(torch.bfloat16)
+    if q.stride(2) != 1:
+        q = q.contiguous()
+    if out_dtype not in (torch.float32, torch.bfloat16):
+        raise ValueError("out_dtype must be float32 or bfloat16.")
+    if out is None:
+        out = torch.empty((b, hq, d), dtype=out_dtype, device=q.device)
+    elif out.shape != (b, hq, d) or not out.is_contiguous() or out.dtype != out_dtype:
+        raise ValueError("out must be a contiguous [B, Hq, D] tensor of out_dtype.")
+    max_blocks = block_tables.shape[1]
+    nbytes = int(lib.grpo_paged_attn_workspace_bytes(b, hq, hkv, d, bs, max_blocks))
+    ws = workspace("paged_attn", nbytes, q.device)
+    rc = lib.grpo_paged_attn_decode(
+        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), nb,
+        block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(), out.data_ptr(),
+        1 if out_dtype == torch.bfloat16 else 0, b, hq, hkv, d, bs, max_blocks, float(scale),
+        _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_handle(q.device))
+    _lib.check(rc, "grpo_paged_attn_decode")
+    return out

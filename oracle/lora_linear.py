@@ -1,0 +1,72 @@
+"""NF4-dequant linear with the fused LoRA term -- test oracle.
+
+Restates ``_lora_forward_kernel`` (``src/triton_kernels/lora_forward.py:107-260``)
+with its rounding points:
+
+1. ``acc = sum_k bf16(x[m,k]) * bf16(w[n,k])`` accumulated in float32
+   (``:204-208``; here accumulated in float64, then rounded to float32);
+2. ``acc = bf16(acc)`` (``:246``), then ``acc = bf16(acc + bf16(bias))``
+   (``:247-251``);
+3. ``t = bf16(sum_k x[m,k] * A[r,k])`` (``:217-243``);
+4. ``u = bf16(sum_r t[m,r] * B[n,r])`` (``:244, 253``);
+5. ``u = bf16(u * bf16(scaling))`` (``:211, 254``);
+6. ``y = bf16(acc + u)`` (``:255-257``).
+
+The reference's PyTorch branch (``src/core/lora.py:125-137``) rounds at the same
+points except that bitsandbytes adds the bias inside ``F.linear``; both agree
+to within one bf16 ulp, far inside the 1e-2 tolerance used for this op.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from .bf16 import bf16_bits_to_f32, f32_to_bf16_bits, round_bf16
+from .nf4 import NF4_CODE, dequantize_nf4
+
+
+def _mm(a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    """float64 matmul rounded to float32 (the 'fp32 accumulate' of the kernel)."""
+    return (a.astype(np.float64) @ b.astype(np.float64)).astype(np.float32)
+
+
+def nf4_weight_bf16(packed, absmax, n: int, k: int, blocksize: int,
+                    code: np.ndarray = NF4_CODE, nested: dict | None = None) -> np.ndarray:
+    """Dequantized weight ``[N, K]`` as float32 holding exact bf16 values."""
+    bits = dequantize_nf4(packed, absmax, n * k, blocksize, code, nested)
+    return bf16_bits_to_f32(bits).reshape(n, k)
+
+
+def nf4_lora_linear(x_bits, packed, absmax, n: int, k: int, blocksize: int,
+                    bias_bits=None, a_bits=None, b_bits=None, scaling: float = 1.0,
+                    code: np.ndarray = NF4_CODE, nested: dict | None = None,
+                    weight_f32: np.ndarray | None = None) -> np.ndarray:
+    """``y = W_nf4(x) + bias + B(A(x)) * scaling``; bf16 bits in, bf16 bits out.
+
+    ``x_bits`` is ``[M, K]`` bf16 bits; ``a_bits`` ``[r, K]``; ``b_bits``
+    ``[N, r]``.  ``a_bits=None`` (or r = 0) drops the LoRA term, which is the
+    plain NF4 linear of the MLP projections.  ``weight_f32`` may pass a
+    pre-dequantized weight (from ``nf4_weight_bf16``) to skip that step.
+    """
+    x = bf16_bits_to_f32(np.asarray(x_bits)).reshape(-1, k)
+    w = weight_f32 if weight_f32 is not None else nf4_weight_bf16(
+        packed, absmax, n, k, blocksize, code, nested)
+    acc = round_bf16(_mm(x, w.T))
+    if bias_bits is not None:
+        acc = round_bf16(acc + bf16_bits_to_f32(bias_bits).reshape(1, n))
+    if a_bits is not None and np.asarray(a_bits).size > 0:
+        a = bf16_bits_to_f32(a_bits).reshape(-1, k)
+        b = bf16_bits_to_f32(b_bits).reshape(n, -1)
+        t = round_bf16(_mm(x, a.T))
+        u = round_bf16(_mm(t, b.T))
+        s = round_bf16(np.float32(scaling))
+        u = round_bf16(u * s)
+        acc = round_bf16(acc + u)
+    return f32_to_bf16_bits(acc)
+
+
+def lora_xa(x_bits, a_bits, k: int) -> np.ndarray:
+    """``t = bf16(x @ A^T)`` as float32 holding bf16 values (step 3 above)."""
+    x = bf16_bits_to_f32(np.asarray(x_bits)).reshape(-1, k)
+    a = bf16_bits_to_f32(a_bits).reshape(-1, k)
+    return round_bf16(_mm(x, a.T))
