@@ -1,0 +1,295 @@
+#!/usr/bin/env python
+"""Rollout decode benchmark on one MI355X.
+
+Workload: a random-init Qwen2-1.5B-shaped model (28 layers, hidden 1536, 12 Q / 2
+KV heads, head_dim 128, MLP 8960, vocab 151936) with NF4 base weights (blocksize
+64, float32 absmax) and rank-16 LoRA (alpha 32) on q/k/v/o; a group of G = 8
+samples of one 512-token prompt; greedy decoding with forced per-sequence stop
+lengths drawn uniformly from [64, 512] (seeded), so the batch is ragged.
+
+One benchmark "step" is one full ragged rollout: every decode step until the
+longest row stops (the prompt's KV is prefilled once before timing, shared by
+the 8 rows through the block pool, and excluded from the metric).  The metric is
+generated tokens of active rows / wall time of the decode loop.
+
+The JSON line also carries:
+* ``roofline`` -- the dominant kernel (the NF4 linear: q|k|v, o, gate|up, down)
+  over one rollout replayed with graph event-record nodes around each launch:
+  achieved = algorithmic bytes / summed launch durations, peak 8 TB/s;
+* ``cpu_baseline`` -- the numpy oracle (a restatement of the reference's
+  PyTorch semantics) running one decode step of the same model on the host.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "grpo-training-engine_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+PEAK_HBM_GBS = 8000.0
+METRIC = "rollout decode tok/s (Qwen2-1.5B arch, G=8, NF4+LoRA); % HBM roofline"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3, help="timed rollouts")
+    ap.add_argument("--warmup", type=int, default=1, help="untimed rollouts")
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--group", type=int, default=8)
+    ap.add_argument("--prompt-len", type=int, default=512)
+    ap.add_argument("--max-new", type=int, default=512)
+    ap.add_argument("--layers", type=int, default=28, help="(smaller only for debugging)")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-kernel-timing", action="store_true")
+    return ap.parse_args()
+
+
+def kv_bytes_per_token(cfg) -> int:
+    return 2 * cfg.num_key_value_heads * cfg.head_dim * 2 * cfg.num_hidden_layers
+
+
+def rollout_bytes(cfg, model, stops, prompt_len, group, block_size=16):
+    """Algorithmic HBM bytes of one rollout (weights once per decode step + KV read).
+
+    KV is counted per active row and step at its full context (logical bytes);
+    the physical count reads the shared prompt blocks once per step instead of
+    once per row.
+    """
+    wb = model.weight_bytes()
+    per_step_weights = wb["nf4"] + wb["absmax"] + wb["lora"] + wb["lm_head"]
+    kv_tok = kv_bytes_per_token(cfg)
+    shared = ((prompt_len - 1) // block_size) * block_size  # tokens in shared full blocks
+    steps = max(stops)
+    logical = physical = 0
+    for s in range(steps):
+        ctxs = [prompt_len + s for st in stops if st > s]
+        logical += sum(ctxs) * kv_tok
+        physical += (shared + sum(c - shared for c in ctxs)) * kv_tok if ctxs else 0
+    return dict(weights=per_step_weights * steps, kv_logical=logical, kv_physical=physical,
+                steps=steps, weight_per_step=per_step_weights)
+
+
+def cpu_baseline(model, cfg, group, ctx, seed):
+    """One decode step of the numpy oracle on the host (bounded sample)."""
+    import numpy as np
+
+    from oracle.decode import Qwen2DecodeOracle
+    import torch
+
+    def bits(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    def nf4(lin, bias=None, a=None, b=None):
+        d = dict(packed=lin.weight.detach().cpu().numpy().reshape(-1),
+                 absmax=lin.weight.quant_state.absmax.detach().cpu().numpy(),
+                 n=lin.out_features, k=lin.in_features)
+        if bias is not None:
+            d["bias"] = bits(bias)
+        if a is not None:
+            d["A"], d["B"] = bits(a), bits(b)
+        return d
+
+    layers = []
+    for L in model.model.layers:
+        at, mlp = L.self_attn, L.mlp
+        e = dict(input_norm=bits(L.input_layernorm.weight),
+                 post_norm=bits(L.post_attention_layernorm.weight))
+        for n in ("q", "k", "v", "o"):
+            m = getattr(at, f"{n}_proj")
+            e[n] = nf4(m.base_layer, m.base_layer.bias, m.lora_A.weight, m.lora_B.weight)
+        for n in ("gate", "up", "down"):
+            e[n] = nf4(getattr(mlp, f"{n}_proj"))
+        layers.append(e)
+    w = dict(embed=bits(model.model.embed_tokens.weight), norm=bits(model.model.norm.weight),
+             lm_head=bits(model.lm_head.weight), layers=layers)
+    c = dict(hidden=cfg.hidden_size, n_heads=cfg.num_attention_heads,
+             n_kv=cfg.num_key_value_heads, head_dim=cfg.head_dim, eps=cfg.rms_norm_eps,
+             theta=cfg.rope_theta, blocksize=cfg.nf4_blocksize,
+             scaling=cfg.lora_alpha / cfg.lora_rank)
+    oracle = Qwen2DecodeOracle(w, c, cache_dequant=False)
+    g = np.random.default_rng(seed)
+    width = -(-(ctx + 1) // 16)
+    nb = group * width
+    kcs = [g.integers(0, 1 << 16, (nb, cfg.num_key_value_heads, 16, cfg.head_dim),
+                      dtype=np.uint16) & 0xBFFF for _ in range(cfg.num_hidden_layers)]
+    vcs = [k.copy() for k in kcs]
+    tables = np.arange(nb, dtype=np.int32).reshape(group, width)
+    toks = g.integers(0, cfg.vocab_size, group)
+    pos = np.full(group, ctx, dtype=np.int64)
+    t0 = time.perf_counter()
+    oracle.step(toks, kcs, vcs, tables, pos)
+    dt = time.perf_counter() - t0
+    return dict(value=round(group / dt, 4), unit="tok/s", cores=os.cpu_count(), kind="port",
+                sample=(f"1 decode step of the numpy oracle, G={group} rows at context {ctx + 1}, "
+                        f"all 28 layers + lm_head, NF4 dequantized per call; {dt:.2f} s "
+                        "(numpy: elementwise single-threaded, BLAS matmuls multi-threaded)"))
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (got --gpus {args.gpus}); this build has no "
+              "multi-GPU path (rollout groups would shard data-parallel, one group per GPU).",
+              file=sys.stderr)
+        sys.exit(2)
+    import numpy as np
+    import torch
+
+    from grpo_mi355x import _lib
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine, prefill
+    from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
+
+    _lib.device_library()
+    dev = torch.device("cuda:0")
+    cfg = Qwen2Config.qwen2_1_5b()
+    cfg.num_hidden_layers = args.layers
+    G, P, NEW, BS = args.group, args.prompt_len, args.max_new, 16
+    rng = np.random.default_rng(args.seed)
+    stops = rng.integers(64, NEW + 1, G).tolist()
+    prompt = rng.integers(0, cfg.vocab_size, P).tolist()
+    log(f"building model (layers={cfg.num_hidden_layers}) ...")
+    t = time.time()
+    model = build_random_model(cfg, dev, seed=args.seed)
+    torch.cuda.synchronize()
+    log(f"model built in {time.time() - t:.1f}s; weight bytes {model.weight_bytes()}")
+    width = -(-(P + NEW) // BS)
+    pool = PagedKVPool(cfg.num_hidden_layers, width * (G + 2), cfg.num_key_value_heads,
+                       cfg.head_dim, BS, device=dev)
+    eng1 = DecodeEngine(model, pool, 1, width)
+    eng1.capture()
+    t = time.time()
+    parent = prefill(eng1, pool, tuple(prompt), width)
+    torch.cuda.synchronize()
+    log(f"prefill of {P - 1} tokens in {time.time() - t:.2f}s")
+    kids = pool.fork(parent, G, reserve_tokens=P - 1 + NEW + 1)
+    pool.free(parent)
+    pool.check_invariants()
+    del eng1
+    eng = DecodeEngine(model, pool, G, width)
+    tables = pool.block_table(kids, width, device=dev)
+    start = dict(tokens=torch.full((G,), prompt[-1], dtype=torch.int64, device=dev),
+                 positions=torch.full((G,), P - 1, device=dev), block_tables=tables,
+                 limits=torch.tensor(stops, device=dev), max_new_tokens=NEW)
+    eng.start(**start)
+    eng.capture()
+    nsteps = max(stops)
+
+    def rollout():
+        eng.start(**start)
+        eng.run(nsteps)
+
+    for _ in range(args.warmup):
+        rollout()
+    torch.cuda.synchronize()
+    gen = eng.generated.clone()
+    lengths = (torch.arange(NEW, device=dev)[None, :] < torch.tensor(stops, device=dev)[:, None])
+    log(f"warm-up done; rows stop at {stops}")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        rollout()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    elapsed = t1 - t0
+    assert torch.equal(eng.generated, gen), "rollouts are not deterministic"
+    tokens = sum(stops) * args.steps
+    value = tokens / elapsed
+    ms_rollout = elapsed / args.steps * 1e3
+    rb = rollout_bytes(cfg, model, stops, P, G, BS)
+    step_ms = ms_rollout / nsteps
+    alg = rb["weights"] + rb["kv_logical"]
+    log(f"{value:.1f} tok/s, {ms_rollout:.2f} ms/rollout, {step_ms * 1e3:.1f} us/decode step")
+
+    roofline = None
+    kernels = {}
+    if not args.no_kernel_timing:
+        # Same rollout, graph re-captured with event-record nodes around each launch.
+        eng.start(**start)
+        eng.capture(timing=True)
+        eng.start(**start)
+        acc: dict[str, list] = {}
+        attn_bytes = 0
+        for s in range(nsteps):
+            attn_bytes += eng.attention_bytes()
+            eng.step()
+            torch.cuda.synchronize()
+            for k, (ms, nb, n) in eng.kernel_times().items():
+                a = acc.setdefault(k, [0.0, 0, 0])
+                a[0] += ms
+                a[1] += nb
+                a[2] += n
+        acc.setdefault("paged_attention", [0.0, 0, 0])[1] = attn_bytes
+        for k, (ms, nb, n) in acc.items():
+            kernels[k] = dict(launches=n, avg_us=round(ms * 1e3 / max(n, 1), 3),
+                              achieved_GBs=round(nb / (ms * 1e-3) / 1e9, 1) if ms > 0 else None,
+                              bytes_per_launch=nb // max(n, 1))
+        lin = acc["nf4_linear"]
+        achieved = lin[1] / (lin[0] * 1e-3) / 1e9
+        roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
+                        frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None,
+                        kernel="nf4_linear_mfma (q|k|v, o, gate|up, down)",
+                        avg_launch_us=kernels["nf4_linear"]["avg_us"],
+                        bytes_per_launch=kernels["nf4_linear"]["bytes_per_launch"])
+        log(f"kernel timing: {kernels}")
+        eng.start(**start)
+        eng.capture()  # back to the untimed graph
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("CPU baseline (numpy oracle, one decode step) ...")
+        try:
+            cpu = cpu_baseline(model, cfg, G, P, args.seed)
+        except MemoryError as exc:  # pragma: no cover
+            cpu = dict(value=None, unit="tok/s", cores=os.cpu_count(), kind="port",
+                       sample=f"not run: {exc}")
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_rollout, 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init weights N(0,0.02) -> NF4, LoRA N(0,0.01); random prompt)",
+        "config": {
+            "workload": "BASELINE config 3: Qwen2-1.5B-shaped NF4+LoRA decode, G=8, 512-token "
+                        "prompt, greedy, per-sequence stops U[64,512]; step = one ragged rollout",
+            "group": G, "prompt_len": P, "max_new_tokens": NEW, "stops": stops,
+            "layers": cfg.num_hidden_layers, "block_size": BS, "parallelism": "single GPU",
+        },
+        "decode_steps_per_rollout": nsteps,
+        "us_per_decode_step": round(step_ms * 1e3, 2),
+        "step_hbm": {
+            "alg_bytes_per_rollout": alg,
+            "kv_bytes_logical": rb["kv_logical"], "kv_bytes_physical": rb["kv_physical"],
+            "weight_bytes_per_step": rb["weight_per_step"],
+            "achieved_GBs": round(alg / (elapsed / args.steps) / 1e9, 1),
+            "frac_of_peak": round(alg / (elapsed / args.steps) / 1e9 / PEAK_HBM_GBS, 4),
+        },
+        "roofline": roofline,
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

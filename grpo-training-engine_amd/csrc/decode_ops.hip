@@ -1,0 +1,227 @@
+// Per-step ops of the model-level decode around the two hot-path kernels
+// (src/triton_kernels/paged_kv.py:690-820 and fused_ops.py:34-251):
+// embedding gather, residual add + RMSNorm, RoPE fused with the KV append,
+// SiLU*mul, and greedy argmax.  All bf16 in / bf16 out with the reference's
+// rounding points; memory-bound, one workgroup per row.
+#include <math.h>
+
+#include "common.hpp"
+
+using namespace grpo;
+
+namespace {
+
+constexpr int ROW_T = 256;
+
+__device__ __forceinline__ float block_sum(float v, float* red) {
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = 0.f;
+  for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += red[w];
+  __syncthreads();
+  return t;
+}
+
+// out[b, :] = table[ids[b], :]; ids outside [0, V) give a zero row.
+__global__ void __launch_bounds__(ROW_T) embedding_kernel(const int64_t* __restrict__ ids,
+                                                          const uint16_t* __restrict__ table,
+                                                          int64_t V, int H,
+                                                          uint16_t* __restrict__ out) {
+  const int b = blockIdx.x;
+  const int64_t id = ids[b];
+  const bool ok = id >= 0 && id < V;
+  const uint16_t* src = table + (ok ? id : 0) * (int64_t)H;
+  for (int i = threadIdx.x; i < H; i += ROW_T) out[(int64_t)b * H + i] = ok ? src[i] : 0;
+}
+
+// h = residual ? bf16(x + residual) : x; y = bf16(bf16(h * rsqrt(mean(h^2) + eps)) * w)
+// (fused_ops.py:34-77; transformers' Qwen2RMSNorm).  h is written to h_out when given.
+__global__ void __launch_bounds__(ROW_T) add_rmsnorm_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* residual, uint16_t* h_out,
+    const uint16_t* __restrict__ w, uint16_t* __restrict__ y, int H, float eps) {
+  __shared__ float red[ROW_T / 64];
+  extern __shared__ float hs[];  // H floats
+  const int64_t row = (int64_t)blockIdx.x * H;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < H; i += ROW_T) {
+    float h = bf2f(x[row + i]);
+    if (residual) h = round_bf(h + bf2f(residual[row + i]));
+    hs[i] = h;
+    ss += h * h;
+  }
+  const float total = block_sum(ss, red);
+  const float inv = 1.f / sqrtf(total / (float)H + eps);
+  for (int i = threadIdx.x; i < H; i += ROW_T) {
+    const float h = hs[i];
+    if (residual && h_out) h_out[row + i] = f2bf(h);
+    y[row + i] = f2bf(round_bf(h * inv) * bf2f(w[i]));
+  }
+}
+
+// RoPE (x*cos + rotate_half(x)*sin in bf16 arithmetic, transformers'
+// apply_rotary_pos_emb) on q and k of one token per sequence, then the KV
+// append of paged_kv.py:253-319 at slot context_lens[b].
+//   qkv row: [q (Hq*D) | k (Hkv*D) | v (Hkv*D)], row stride ld
+__global__ void __launch_bounds__(ROW_T) rope_append_kernel(
+    const uint16_t* __restrict__ qkv, int64_t ld, int Hq, int Hkv, int D,
+    const uint16_t* __restrict__ cos_t, const uint16_t* __restrict__ sin_t, int max_pos,
+    const int32_t* __restrict__ context_lens, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t num_blocks,
+    const int32_t* __restrict__ bt, int64_t bts, int BS, int max_blocks) {
+  const int b = blockIdx.x;
+  const int pos = context_lens[b];
+  const int cpos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
+  const uint16_t* row = qkv + (int64_t)b * ld;
+  const uint16_t* cr = cos_t + (int64_t)cpos * D;
+  const uint16_t* sr = sin_t + (int64_t)cpos * D;
+  const int half = D / 2;
+  bool slot_ok = pos >= 0 && pos < max_blocks * BS;
+  int64_t slot_base = 0;
+  if (slot_ok) {
+    const int phys = bt[(int64_t)b * bts + pos / BS];
+    slot_ok = phys >= 0 && phys < num_blocks;
+    slot_base = ((int64_t)phys * Hkv * BS + (pos % BS)) * D;  // + h * BS * D + d
+  }
+  const int nrot = (Hq + Hkv) * D;
+  for (int i = threadIdx.x; i < nrot + Hkv * D; i += ROW_T) {
+    if (i < nrot) {
+      const int h = i / D, d = i - h * D;
+      const uint16_t* xh = row + (int64_t)h * D;  // q heads then k heads (contiguous)
+      const float xv = bf2f(xh[d]);
+      const float rv = d < half ? -bf2f(xh[d + half]) : bf2f(xh[d - half]);
+      const float o = round_bf(round_bf(xv * bf2f(cr[d])) + round_bf(rv * bf2f(sr[d])));
+      if (h < Hq) {
+        q_out[((int64_t)b * Hq + h) * D + d] = f2bf(o);
+      } else if (slot_ok) {
+        kc[slot_base + (int64_t)(h - Hq) * BS * D + d] = f2bf(o);
+      }
+    } else if (slot_ok) {
+      const int j = i - nrot, h = j / D, d = j - h * D;
+      vc[slot_base + (int64_t)h * BS * D + d] = row[nrot + j];
+    }
+  }
+}
+
+// out = bf16(bf16(silu(gate)) * up), gate = row[0:N], up = row[N:2N] (fused_ops.py:79-112).
+__global__ void __launch_bounds__(ROW_T) silu_mul_kernel(const uint16_t* __restrict__ gu,
+                                                         int64_t ld, int N,
+                                                         uint16_t* __restrict__ out,
+                                                         int64_t ldo) {
+  const int64_t m = blockIdx.y;
+  const int i = blockIdx.x * ROW_T + threadIdx.x;
+  if (i >= N) return;
+  const float g = bf2f(gu[m * ld + i]);
+  const float u = bf2f(gu[m * ld + N + i]);
+  const float s = round_bf(g * (1.f / (1.f + expf(-g))));
+  out[m * ldo + i] = f2bf(s * u);
+}
+
+// Greedy argmax over a bf16 row (first index of the maximum, NaNs ignored).
+constexpr int AMAX_T = 1024;
+__global__ void __launch_bounds__(AMAX_T) argmax_kernel(const uint16_t* __restrict__ logits,
+                                                        int64_t ld, int V,
+                                                        int64_t* __restrict__ out) {
+  __shared__ float sv[AMAX_T / 64];
+  __shared__ int si[AMAX_T / 64];
+  const uint16_t* row = logits + (int64_t)blockIdx.x * ld;
+  float best = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int i = threadIdx.x; i < V; i += AMAX_T) {
+    const float v = bf2f(row[i]);
+    if (v > best) {  // strictly greater keeps the first index per thread
+      best = v;
+      bi = i;
+    }
+  }
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ov = __shfl_xor(best, o);
+    const int oi = __shfl_xor(bi, o);
+    if (ov > best || (ov == best && oi < bi)) {
+      best = ov;
+      bi = oi;
+    }
+  }
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) {
+    sv[wave] = best;
+    si[wave] = bi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < AMAX_T / 64; ++w)
+      if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
+        best = sv[w];
+        bi = si[w];
+      }
+    out[blockIdx.x] = bi == 0x7fffffff ? 0 : bi;
+  }
+}
+
+}  // namespace
+
+extern "C" int grpo_embedding(const int64_t* ids, const void* table, int64_t V, int H, void* out,
+                              int B, grpo_stream_t stream) {
+  if (B < 0 || H <= 0 || V <= 0) return einval("bad embedding dimensions");
+  if (B == 0) return GRPO_OK;
+  if (!ids || !table || !out) return einval("null pointer");
+  embedding_kernel<<<dim3(B), ROW_T, 0, as_stream(stream)>>>(
+      ids, static_cast<const uint16_t*>(table), V, H, static_cast<uint16_t*>(out));
+  return launch_check("embedding");
+}
+
+extern "C" int grpo_add_rmsnorm(const void* x, const void* residual, void* h_out,
+                                const void* weight, void* y, int M, int H, float eps,
+                                grpo_stream_t stream) {
+  if (M < 0 || H <= 0 || H > 16384) return einval("bad rmsnorm dimensions (H <= 16384)");
+  if (M == 0) return GRPO_OK;
+  if (!x || !weight || !y) return einval("null pointer");
+  add_rmsnorm_kernel<<<dim3(M), ROW_T, H * sizeof(float), as_stream(stream)>>>(
+      static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(residual),
+      static_cast<uint16_t*>(h_out), static_cast<const uint16_t*>(weight),
+      static_cast<uint16_t*>(y), H, eps);
+  return launch_check("add_rmsnorm");
+}
+
+extern "C" int grpo_rope_append(const void* qkv, int64_t ld, int Hq, int Hkv, int D,
+                                const void* cos_table, const void* sin_table, int max_pos,
+                                const int32_t* context_lens, void* q_out, void* k_cache,
+                                void* v_cache, int64_t num_blocks, const int32_t* block_tables,
+                                int64_t bt_stride, int block_size, int max_blocks, int B,
+                                grpo_stream_t stream) {
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || D % 2 || block_size <= 0 || max_pos <= 0)
+    return einval("bad rope/append dimensions");
+  if (ld < (int64_t)(Hq + 2 * Hkv) * D) return einval("qkv row stride too small");
+  if (B == 0) return GRPO_OK;
+  if (!qkv || !cos_table || !sin_table || !context_lens || !q_out || !k_cache || !v_cache ||
+      !block_tables)
+    return einval("null pointer");
+  rope_append_kernel<<<dim3(B), ROW_T, 0, as_stream(stream)>>>(
+      static_cast<const uint16_t*>(qkv), ld, Hq, Hkv, D, static_cast<const uint16_t*>(cos_table),
+      static_cast<const uint16_t*>(sin_table), max_pos, context_lens,
+      static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache),
+      static_cast<uint16_t*>(v_cache), num_blocks, block_tables, bt_stride, block_size,
+      max_blocks);
+  return launch_check("rope_append");
+}
+
+extern "C" int grpo_silu_mul(const void* gate_up, int64_t ld, int N, void* out, int64_t ldo,
+                             int M, grpo_stream_t stream) {
+  if (M < 0 || N <= 0 || ld < 2 * (int64_t)N || ldo < N) return einval("bad silu_mul dimensions");
+  if (M == 0) return GRPO_OK;
+  if (!gate_up || !out) return einval("null pointer");
+  silu_mul_kernel<<<dim3((unsigned)cdiv(N, ROW_T), M), ROW_T, 0, as_stream(stream)>>>(
+      static_cast<const uint16_t*>(gate_up), ld, N, static_cast<uint16_t*>(out), ldo);
+  return launch_check("silu_mul");
+}
+
+extern "C" int grpo_argmax_bf16(const void* logits, int64_t ld, int V, int M, int64_t* out,
+                                grpo_stream_t stream) {
+  if (M < 0 || V <= 0 || ld < V) return einval("bad argmax dimensions");
+  if (M == 0) return GRPO_OK;
+  if (!logits || !out) return einval("null pointer");
+  argmax_kernel<<<dim3(M), AMAX_T, 0, as_stream(stream)>>>(static_cast<const uint16_t*>(logits),
+                                                           ld, V, out);
+  return launch_check("argmax");
+}

@@ -5,30 +5,42 @@
 // element e = n*K + k, byte e/2, even e = high nibble; one float32 absmax per
 // `blocksize` flat elements; value = bf16_rne(code[q] * absmax).
 //
-// Fast linear path (M <= 64, K % 256 == 0, N % 16 == 0, blocksize % 64 == 0,
-// r <= 16): D = A*B on v_mfma_f32_16x16x32_bf16 with A = x (rows m) and
-// B = W^T (columns n).  Each lane owns one 64-element chunk of one weight row
-// per 256-wide k-step (32 bytes, two 16-byte loads), builds a 16-entry bf16
-// codebook for that chunk's absmax block in registers (so every product is
-// exactly the reference's bf16(code*absmax) * x), and expands nibbles with
-// v_perm byte lookups.  The decode emits each dword's eight elements in the
-// order [0,2,4,6,1,3,5,7]; x is staged in LDS in that same order, so MFMA sums
-// the right pairs.  The LoRA-A product x*A^T is one more 16-column MFMA tile of
-// the same k-loop (A is bf16, no decode).  Split-K across workgroups reduces
-// through a caller workspace; the last workgroup of each 64-row group (found
-// with a device-scope counter, no spinning) sums the partials in split order
-// and runs the epilogue, so results do not depend on arrival order.
+// Fast linear path (M <= 64, K % 256 == 0, K <= 32768, N % 16 == 0,
+// blocksize % 64 == 0, r <= 16): D = A*B on v_mfma_f32_16x16x32_bf16 with
+// A = x (rows m) and B = W^T (columns n).
+//
+//  * Work unit: one wave = one 16-row n-tile x up to 4 k-steps of 256.  Lane
+//    (n = lane%16, group g = lane/16) owns the 64-element chunk
+//    [kstep*256 + 64g, +64) of row n: two 16-byte loads per k-step.  A wave
+//    issues ALL its weight and absmax loads before decoding anything, so the
+//    memory latency is paid once per wave, not once per k-step.
+//  * Decode: per chunk a 16-entry bf16 codebook of bf16(code[j] * absmax) is
+//    built in registers and nibbles are expanded with v_perm byte lookups, so
+//    every product is exactly the reference's bf16(code*absmax) * x.  decode8
+//    emits a dword's eight elements in the order [0,2,4,6,1,3,5,7]; x is
+//    permuted the same way, so MFMA sums matching pairs.
+//  * Split-K stays inside one workgroup: a workgroup has ntw n-tiles x kw
+//    k-groups of waves (<= 16 waves); the kw partial sums are added through
+//    LDS in fixed order, so results are deterministic and no cross-workgroup
+//    synchronisation (device-scope fences) is ever needed.
+//  * x is staged in LDS once per workgroup when it fits (gfx950 allows 160 KiB
+//    per workgroup), otherwise each wave reads its own x fragments from L2.
+//  * LoRA: x A^T is one more 16-column MFMA tile (A is bf16); the tile of
+//    k-group kg is computed by the wave of n-tile kg % ntw, so the extra work
+//    is spread over the workgroup; the epilogue applies the reference's
+//    rounding points (lora_forward.py:243-257).
 #include "common.hpp"
 
 using namespace grpo;
 
 namespace {
 
-constexpr int KSTEP = 256;       // k elements per step: 4 lane groups x 64
-constexpr int WG_ROWS = 64;      // weight rows per workgroup: 4 waves x 16
-constexpr int LDS_BYTES = 65536;
-constexpr int TARGET_WGS = 512;  // launch-shape heuristic (2 per CU on 256 CUs)
-constexpr size_t COUNTER_BYTES = 65536;  // split-K group counters: up to 16384 groups of 64 rows
+constexpr int KSTEP = 256;         // k elements per step: 4 lane groups x 64
+constexpr int KPW_MAX = 8;         // k-steps per wave (all loads in flight at once)
+constexpr int MAX_WAVES = 16;      // waves per workgroup (1024 threads)
+constexpr int LDS_BYTES = 163840;  // gfx950: 160 KiB of LDS per workgroup
+constexpr int TARGET_WAVES = 4096; // launch-shape heuristic (4 per SIMD on 256 CUs)
+constexpr int MAXSEG = 4;
 
 // ------------------------------------------------------------- dequant --
 
@@ -115,8 +127,15 @@ __device__ __forceinline__ uint4 deinterleave8(uint4 v) {
                     perm(v.y, v.x, 0x07060302u), perm(v.w, v.z, 0x07060302u));
 }
 
-// ------------------------------------------------------ fast linear --
+__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
+}
 
+// ---------------------------------------------------------- arguments --
+
+// Output rows [seg_end[s-1], seg_end[s]) form segment s, with its own bias,
+// LoRA A [r, K] and LoRA B [rows_s, r] (one segment for a plain projection;
+// q|k|v or gate|up stacked into one weight for a grouped launch).
 struct LinearArgs {
   const uint16_t* x;
   int64_t ldx;
@@ -124,92 +143,195 @@ struct LinearArgs {
   const float* absmax;
   const float* code16;
   int blocksize;
-  const uint16_t* bias;
-  const uint16_t* la;  // lora A [r, K]
-  const uint16_t* lb;  // lora B [N, r]
+  int nseg;
+  int seg_end[MAXSEG];
+  const uint16_t* bias[MAXSEG];
+  const uint16_t* la[MAXSEG];  // lora A [r, K] per segment
+  const uint16_t* lb[MAXSEG];  // lora B [rows_s, r] per segment
   int r;
   float scaling;
   uint16_t* y;
   int64_t ldy;
   int M, N, K;
-  int S, kps;      // k-splits and k-steps per split
-  float* ws_acc;   // [S][M][N]
-  float* ws_t;     // [NG][S][M][16]
-  int* ws_cnt;     // [NG]
+  int ntw, kw, kpw;  // n-tiles per workgroup, k-groups per workgroup, k-steps per wave
+  int bs_shift;      // log2(blocksize) (power-of-two blocksizes on the fast path)
+  int xstride;       // LDS row stride of staged x (elements)
+  int off_red, off_redt, off_tsum;  // LDS byte offsets of the reduction areas
 };
 
 struct LinearPlan {
-  int MT, KS, NG, S, kps;
-  size_t off_cnt, off_acc, off_t, bytes;
+  int MT, KS, NT, ntw, kw, kpw, grid;
+  bool xlds;
+  int xstride, off_red, off_redt, off_tsum;
+  size_t lds;
 };
 
-LinearPlan plan_linear(int M, int N, int K, int r) {
+__host__ __device__ inline bool aligned16(const void* ptr) {
+  return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0;
+}
+
+bool segments_aligned(const LinearArgs& a, int rows) {
+  for (int s = 0; s + 1 < a.nseg; ++s)
+    if (a.seg_end[s] % rows != 0) return false;
+  return true;
+}
+
+LinearPlan plan_linear(const LinearArgs& a) {
   LinearPlan p{};
-  p.MT = (M + 15) / 16;
-  p.KS = K / KSTEP;
-  p.NG = (N + WG_ROWS - 1) / WG_ROWS;
-  const int tred = 4 * p.MT * 16 * 16 * 4;
-  int kps_lds = ((LDS_BYTES - tred - 256) / (M * 2) - 8) / KSTEP;
-  if (kps_lds < 1) kps_lds = 1;
-  int S = (TARGET_WGS + p.NG - 1) / p.NG;
-  if (S > p.KS) S = p.KS;
-  if (S < 1) S = 1;
-  int kps = (p.KS + S - 1) / S;
-  if (kps > kps_lds) kps = kps_lds;
-  S = (p.KS + kps - 1) / kps;
-  p.S = S;
-  p.kps = kps;
-  if (S > 1) {
-    // Counters live at a fixed offset (0) for every shape: a workspace reused
-    // across shapes then always finds them where the last call left them (zero),
-    // never on top of another shape's partial sums.
-    auto align = [](size_t v) { return (v + 255) & ~(size_t)255; };
-    size_t acc = align((size_t)S * M * N * 4);
-    size_t tb = r > 0 ? align((size_t)p.NG * S * M * 16 * 4) : 0;
-    p.off_cnt = 0;
-    p.off_acc = COUNTER_BYTES;
-    p.off_t = COUNTER_BYTES + acc;
-    p.bytes = COUNTER_BYTES + acc + tb;
-  }
+  p.MT = (a.M + 15) / 16;
+  if (p.MT == 3) p.MT = 4;  // launched as the MT = 4 kernel (sizes below must match)
+  p.KS = a.K / KSTEP;
+  p.NT = a.N / 16;
+  int kw = (TARGET_WAVES + p.NT - 1) / p.NT;
+  if (kw > p.KS) kw = p.KS;
+  if (kw < 1) kw = 1;
+  int kpw = (p.KS + kw - 1) / kw;
+  const int kpw_min = (p.KS + MAX_WAVES - 1) / MAX_WAVES;  // at most 16 k-groups
+  if (kpw < kpw_min) kpw = kpw_min;
+  // LoRA waves also hold a LoRA-A chunk: keep their prefetch depth at <= 2
+  // k-steps so 16-wave workgroups fit in 128 registers per lane.
+  const int kpw_max = a.r > 0 ? 2 : KPW_MAX;
+  if (kpw > kpw_max) kpw = kpw_max;
+  kw = (p.KS + kpw - 1) / kpw;
+  int ntw = MAX_WAVES / kw;
+  ntw = ntw >= 4 ? 4 : (ntw >= 2 ? 2 : 1);
+  while (ntw > 1 && !segments_aligned(a, 16 * ntw)) ntw /= 2;
+  p.kw = kw;
+  p.kpw = kpw;
+  p.ntw = ntw;
+  p.grid = (p.NT + ntw - 1) / ntw;
+  const int red = (kw - 1) * ntw * p.MT * 256 * 4;
+  const int redt = a.r > 0 ? kw * p.MT * 256 * 4 : 0;
+  const int tsum = a.r > 0 ? p.MT * 16 * 16 * 4 : 0;
+  const int xbytes = ((a.M * (a.K + 8) * 2) + 15) & ~15;
+  p.xlds = xbytes + red + redt + tsum <= LDS_BYTES;
+  p.xstride = a.K + 8;
+  const int xb = p.xlds ? xbytes : 0;
+  p.off_red = xb;
+  p.off_redt = xb + red;
+  p.off_tsum = xb + red + redt;
+  p.lds = (size_t)xb + red + redt + tsum;
   return p;
 }
 
-template <int MT, bool LORA>
-__global__ void __launch_bounds__(256) nf4_linear_mfma(LinearArgs p) {
+// x fragment for MFMA: lane (m = mt*16 + lane%16) holds x[m][kcol .. kcol+8) in
+// decode8 order; rows >= M are zero.
+template <bool XLDS>
+__device__ __forceinline__ uint4 xfrag(const LinearArgs& p, const uint16_t* xs, int m, int kcol) {
+  if (m >= p.M) return make_uint4(0, 0, 0, 0);
+  if (XLDS) return *reinterpret_cast<const uint4*>(xs + m * p.xstride + kcol);
+  return deinterleave8(*reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kcol));
+}
+
+// ------------------------------------------------------ fast linear --
+
+template <int MT, bool LORA, bool XLDS, int KPW>
+__global__ void __launch_bounds__(1024) nf4_linear_mfma(LinearArgs p) {
   extern __shared__ __align__(16) uint8_t smem[];
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
-  const int ng = blockIdx.x, s = blockIdx.y;
+  const int nt_local = wave % p.ntw, kg = wave / p.ntw;
+  const int ntile = blockIdx.x * p.ntw + nt_local;
   const int KS = p.K / KSTEP;
-  const int ks0 = s * p.kps;
-  const int ks1 = min(ks0 + p.kps, KS);
-  const int nsteps = ks1 - ks0;
-  const int xstride = p.kps * KSTEP + 8;  // LDS row stride in elements (16B pad)
-  uint16_t* xs = reinterpret_cast<uint16_t*>(smem);
-  float* tred = reinterpret_cast<float*>(smem + (size_t)p.M * xstride * 2);  // [4][MT*16][16]
-  int* flag = reinterpret_cast<int*>(tred + 4 * MT * 16 * 16);
+  const int ks0 = kg * p.kpw;
+  const int nk = max(0, min(p.kpw, KS - ks0));
+  const int n_row = ntile * 16 + ln;
+  const bool row_ok = n_row < p.N;
 
-  // Stage x[0:M, ks0*256 : ks1*256] into LDS, 8 elements per 16 bytes,
-  // deinterleaved to the decode8 order.
+  // Segment of this workgroup (the host keeps workgroups inside one segment).
+  const int wg_row0 = blockIdx.x * p.ntw * 16;
+  int seg = 0;
+  while (seg + 1 < p.nseg && wg_row0 >= p.seg_end[seg]) ++seg;
+  const int seg_begin = seg > 0 ? p.seg_end[seg - 1] : 0;
+
+  // The LoRA-A tile of k-group kg is computed once, by the wave of n-tile kg % ntw.
+  const bool do_t = LORA && nt_local == kg % p.ntw;
+  const uint16_t* seg_la = p.la[seg];
+  const bool r_ok = ln < p.r;
+  const bool epi = kg == 0 && row_ok;  // waves of k-group 0 write the outputs
+  const int n_loc = n_row - seg_begin;
+
+  // 1. Every global load of the wave is issued before anything waits on one
+  //    (one memory round trip): weights + absmax of all its k-steps, the
+  //    LoRA-A chunk of its first k-step, the epilogue's bias and LoRA-B row,
+  //    and then the x staging loads.
+  uint4 wv[2 * KPW];
+  float av[KPW];
   {
-    const int chunks = nsteps * (KSTEP / 8);
-    const int total = p.M * chunks;
-    const int kg = ks0 * KSTEP;
-    for (int i = tid; i < total; i += 256) {
-      const int m = i / chunks, c = i - m * chunks;
-      const uint4 v = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kg + c * 8);
-      *reinterpret_cast<uint4*>(xs + m * xstride + c * 8) = deinterleave8(v);
+    const uint8_t* wrow = p.w + (int64_t)(row_ok ? n_row : 0) * (p.K / 2);
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      wv[2 * i] = make_uint4(0, 0, 0, 0);
+      wv[2 * i + 1] = make_uint4(0, 0, 0, 0);
+      av[i] = 0.f;
+      if (i < nk && row_ok) {
+        const int kc = (ks0 + i) * KSTEP + 64 * lg;
+        const uint4* wp = reinterpret_cast<const uint4*>(wrow + kc / 2);
+        wv[2 * i] = wp[0];
+        wv[2 * i + 1] = wp[1];
+        av[i] = p.absmax[((int64_t)n_row * p.K + kc) >> p.bs_shift];
+      }
     }
+  }
+  uint4 av4[8];  // LoRA-A chunk of the current k-step
+  if (do_t && nk > 0) {
+    const uint16_t* arow = seg_la + (int64_t)(r_ok ? ln : 0) * p.K + ks0 * KSTEP + 64 * lg;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      av4[j] = r_ok ? *reinterpret_cast<const uint4*>(arow + 8 * j) : make_uint4(0, 0, 0, 0);
+  }
+  const uint16_t* seg_bias = p.bias[seg];
+  const float bias = epi && seg_bias ? bf2f(seg_bias[n_loc]) : 0.f;
+  float bl[16];
+  if (LORA) {
+    const uint16_t* brow = p.lb[seg] + (int64_t)n_loc * p.r;
+    if (epi && p.r == 16 && aligned16(brow)) {
+      const uint4 b0 = reinterpret_cast<const uint4*>(brow)[0];
+      const uint4 b1 = reinterpret_cast<const uint4*>(brow)[1];
+      const uint32_t bw8[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        bl[2 * q] = bf_lo(bw8[q]);
+        bl[2 * q + 1] = bf_hi(bw8[q]);
+      }
+    } else {
+#pragma unroll
+      for (int q = 0; q < 16; ++q) bl[q] = epi && q < p.r ? bf2f(brow[q]) : 0.f;
+    }
+  }
+
+  // 2. Stage x (all K) in LDS in decode8 order: loads batched 4 per thread.
+  const uint16_t* xs = reinterpret_cast<const uint16_t*>(smem);
+  if (XLDS) {
+    uint16_t* xw = reinterpret_cast<uint16_t*>(smem);
+    const int chunks = p.K / 8;
+    const int total = p.M * chunks;
+    for (int base = 0; base < total; base += 4 * (int)blockDim.x) {
+      uint4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = base + u * (int)blockDim.x + tid;
+        if (i < total) {
+          const int m = i / chunks, c = i - m * chunks;
+          v[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + c * 8);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int i = base + u * (int)blockDim.x + tid;
+        if (i < total) {
+          const int m = i / chunks, c = i - m * chunks;
+          *reinterpret_cast<uint4*>(xw + m * p.xstride + c * 8) = deinterleave8(v[u]);
+        }
+      }
+    }
+    __syncthreads();
   }
   float code[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
-  __syncthreads();
 
-  const int n_row = ng * WG_ROWS + wave * 16 + ln;
-  const bool row_ok = n_row < p.N;
-  const uint8_t* wrow = p.w + (int64_t)(row_ok ? n_row : 0) * (p.K / 2);
   f32x4_t acc[MT];
   f32x4_t tacc[MT];
 #pragma unroll
@@ -218,118 +340,86 @@ __global__ void __launch_bounds__(256) nf4_linear_mfma(LinearArgs p) {
     tacc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  for (int it = 0; it < nsteps; ++it) {
-    const int kc = (ks0 + it) * KSTEP + 64 * lg;  // this lane's chunk (global k)
-    const int kl = it * KSTEP + 64 * lg;           // same chunk in LDS
-    uint4 w0 = make_uint4(0, 0, 0, 0), w1 = w0;
-    float a = 0.f;
-    if (row_ok) {
-      const uint4* wp = reinterpret_cast<const uint4*>(wrow + kc / 2);
-      w0 = wp[0];
-      w1 = wp[1];
-      a = p.absmax[((int64_t)n_row * p.K + kc) / p.blocksize];
+  // 3. Decode + MFMA, one k-step at a time.
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) {
+    if (i >= nk) break;
+    const int kc = (ks0 + i) * KSTEP + 64 * lg;
+    if (do_t && i > 0) {  // later LoRA-A chunks; latency overlaps the decode below
+      const uint16_t* arow = seg_la + (int64_t)(r_ok ? ln : 0) * p.K + kc;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        av4[j] = r_ok ? *reinterpret_cast<const uint4*>(arow + 8 * j) : make_uint4(0, 0, 0, 0);
     }
-    const Lut t = make_lut(code, a);
-    const uint32_t wd[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+    // x fragments of this k-step, read ahead of the decode (one m-tile).
+    uint4 xf[8];
+    constexpr bool PRE = MT == 1 && KPW <= 4;
+    if (PRE) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xf[j] = xfrag<XLDS>(p, xs, ln, kc + 8 * j);
+    }
+    const Lut t = make_lut(code, av[i]);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const uint4 bw = decode8(wd[j], t);
+      const uint4 bw = decode8(word(wv[2 * i + (j >> 2)], j & 3), t);
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int m = mt * 16 + ln;
-        uint4 ax = make_uint4(0, 0, 0, 0);
-        if (m < p.M) ax = *reinterpret_cast<const uint4*>(xs + m * xstride + kl + 8 * j);
-        acc[mt] = mfma16x16x32(ax, bw, acc[mt]);
-      }
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = mfma16x16x32(PRE ? xf[j] : xfrag<XLDS>(p, xs, mt * 16 + ln, kc + 8 * j), bw,
+                               acc[mt]);
     }
-    if (LORA && (it & 3) == wave) {
-      // LoRA-A tile: columns are the r rows of A (rows >= r read as zero).
-      const bool r_ok = ln < p.r;
-      const uint16_t* arow = p.la + (int64_t)(r_ok ? ln : 0) * p.K + kc;
+    if (do_t) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        uint4 bv = make_uint4(0, 0, 0, 0);
-        if (r_ok) bv = deinterleave8(*reinterpret_cast<const uint4*>(arow + 8 * j));
+        const uint4 bv = deinterleave8(av4[j]);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int m = mt * 16 + ln;
-          uint4 ax = make_uint4(0, 0, 0, 0);
-          if (m < p.M) ax = *reinterpret_cast<const uint4*>(xs + m * xstride + kl + 8 * j);
-          tacc[mt] = mfma16x16x32(ax, bv, tacc[mt]);
-        }
+        for (int mt = 0; mt < MT; ++mt)
+          tacc[mt] = mfma16x16x32(PRE ? xf[j] : xfrag<XLDS>(p, xs, mt * 16 + ln, kc + 8 * j),
+                                  bv, tacc[mt]);
       }
     }
   }
 
-  // Sum the four waves' LoRA-A partials: tred[wave][m][r].
-  if (LORA) {
+  // 4. Reduce the kw k-groups (fixed order) and the LoRA-A partials.
+  float* red = reinterpret_cast<float*>(smem + p.off_red);    // [kw-1][ntw][MT][256]
+  float* redt = reinterpret_cast<float*>(smem + p.off_redt);  // [kw][MT][256]
+  float* tsum = reinterpret_cast<float*>(smem + p.off_tsum);  // [MT*16][16]
+  if (p.kw > 1 && kg > 0) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
+      *reinterpret_cast<float4*>(red + (((kg - 1) * p.ntw + nt_local) * MT + mt) * 256 + lane * 4) =
+          make_float4(acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]);
+  }
+  if (do_t) {
 #pragma unroll
-      for (int q = 0; q < 4; ++q)
-        tred[(wave * MT * 16 + mt * 16 + 4 * lg + q) * 16 + ln] = tacc[mt][q];
+    for (int mt = 0; mt < MT; ++mt)
+      *reinterpret_cast<float4*>(redt + (kg * MT + mt) * 256 + lane * 4) =
+          make_float4(tacc[mt][0], tacc[mt][1], tacc[mt][2], tacc[mt][3]);
+  }
+  if (p.kw > 1 || LORA) __syncthreads();
+  if (LORA) {
+    // tacc lane (r = lane%16, g) slot q holds T[m = mt*16 + 4g + q][r]
+    for (int i = tid; i < MT * 256; i += blockDim.x) {
+      const int mt = i >> 8, idx = i & 255, l = idx >> 2, q = idx & 3;
+      float s = 0.f;
+      for (int k = 0; k < p.kw; ++k) s += redt[(k * MT + mt) * 256 + idx];
+      tsum[(mt * 16 + 4 * (l >> 4) + q) * 16 + (l & 15)] = round_bf(s);
+    }
     __syncthreads();
-    for (int i = tid; i < MT * 16 * 16; i += 256)
-      tred[i] = tred[i] + tred[MT * 256 + i] + tred[2 * MT * 256 + i] + tred[3 * MT * 256 + i];
-    __syncthreads();
+  }
+  if (kg != 0 || !row_ok) return;
+  for (int k = 1; k < p.kw; ++k) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const float4 v = *reinterpret_cast<const float4*>(
+          red + (((k - 1) * p.ntw + nt_local) * MT + mt) * 256 + lane * 4);
+      acc[mt][0] += v.x;
+      acc[mt][1] += v.y;
+      acc[mt][2] += v.z;
+      acc[mt][3] += v.w;
+    }
   }
 
-  if (p.S > 1) {
-    // Publish this split's partials, then let the last split of the group finish.
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = mt * 16 + 4 * lg + q;
-        if (m < p.M && row_ok) p.ws_acc[((int64_t)s * p.M + m) * p.N + n_row] = acc[mt][q];
-      }
-    if (LORA) {
-      float* dst = p.ws_t + ((int64_t)ng * p.S + s) * p.M * 16;
-      for (int i = tid; i < p.M * 16; i += 256) dst[i] = tred[i];
-    }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-      const int old = atomicAdd(p.ws_cnt + ng, 1);
-      *flag = (old == p.S - 1);
-    }
-    __syncthreads();
-    if (!*flag) return;
-    __threadfence();
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        const int m = mt * 16 + 4 * lg + q;
-        float v = 0.f;
-        if (m < p.M && row_ok)
-          for (int ss = 0; ss < p.S; ++ss) v += p.ws_acc[((int64_t)ss * p.M + m) * p.N + n_row];
-        acc[mt][q] = v;
-      }
-    if (LORA) {
-      const float* src = p.ws_t + (int64_t)ng * p.S * p.M * 16;
-      for (int i = tid; i < p.M * 16; i += 256) {
-        float v = 0.f;
-        for (int ss = 0; ss < p.S; ++ss) v += src[(int64_t)ss * p.M * 16 + i];
-        tred[i] = v;
-      }
-    }
-    if (tid == 0) p.ws_cnt[ng] = 0;
-    __syncthreads();
-  }
-
-  // Epilogue: y = bf16(bf16(bf16(acc) + bias) + bf16(bf16(bf16(T) B^T) * bf16(s))).
-  if (LORA) {
-    for (int i = tid; i < p.M * 16; i += 256) tred[i] = round_bf(tred[i]);
-    __syncthreads();
-  }
-  if (!row_ok) return;
-  const float bias = p.bias ? bf2f(p.bias[n_row]) : 0.f;
-  float bl[16];
-  if (LORA) {
-#pragma unroll
-    for (int q = 0; q < 16; ++q) bl[q] = q < p.r ? bf2f(p.lb[(int64_t)n_row * p.r + q]) : 0.f;
-  }
+  // 5. Epilogue: y = bf16(bf16(bf16(acc) + bias) + bf16(bf16(bf16(T) B^T) * bf16(s))).
   const float sc = round_bf(p.scaling);
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -338,9 +428,9 @@ __global__ void __launch_bounds__(256) nf4_linear_mfma(LinearArgs p) {
       const int m = mt * 16 + 4 * lg + q;
       if (m >= p.M) continue;
       float v = round_bf(acc[mt][q]);
-      if (p.bias) v = round_bf(v + bias);
+      if (seg_bias) v = round_bf(v + bias);
       if (LORA) {
-        const float* tr = tred + m * 16;
+        const float* tr = tsum + m * 16;
         float u = 0.f;
 #pragma unroll
         for (int rr = 0; rr < 16; ++rr) u += tr[rr] * bl[rr];
@@ -357,6 +447,9 @@ __global__ void __launch_bounds__(256) nf4_linear_generic(LinearArgs p) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)p.M * p.N) return;
   const int m = (int)(idx / p.N), n = (int)(idx % p.N);
+  int seg = 0;
+  while (seg + 1 < p.nseg && n >= p.seg_end[seg]) ++seg;
+  const int n_loc = n - (seg > 0 ? p.seg_end[seg - 1] : 0);
   const uint16_t* xr = p.x + (int64_t)m * p.ldx;
   float acc = 0.f;
   for (int k = 0; k < p.K; ++k) {
@@ -367,14 +460,14 @@ __global__ void __launch_bounds__(256) nf4_linear_generic(LinearArgs p) {
     acc += bf2f(xr[k]) * wv;
   }
   float v = round_bf(acc);
-  if (p.bias) v = round_bf(v + bf2f(p.bias[n]));
+  if (p.bias[seg]) v = round_bf(v + bf2f(p.bias[seg][n_loc]));
   if (p.r > 0) {
     float u = 0.f;
     for (int rr = 0; rr < p.r; ++rr) {
-      const uint16_t* ar = p.la + (int64_t)rr * p.K;
+      const uint16_t* ar = p.la[seg] + (int64_t)rr * p.K;
       float t = 0.f;
       for (int k = 0; k < p.K; ++k) t += bf2f(xr[k]) * bf2f(ar[k]);
-      u += round_bf(t) * bf2f(p.lb[(int64_t)n * p.r + rr]);
+      u += round_bf(t) * bf2f(p.lb[seg][(int64_t)n_loc * p.r + rr]);
     }
     u = round_bf(round_bf(u) * round_bf(p.scaling));
     v = round_bf(v + u);
@@ -382,24 +475,85 @@ __global__ void __launch_bounds__(256) nf4_linear_generic(LinearArgs p) {
   p.y[(int64_t)m * p.ldy + n] = f2bf(v);
 }
 
-bool aligned16(const void* ptr) { return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0; }
-
 bool use_fast_linear(const LinearArgs& a) {
-  return a.M <= 64 && a.K % KSTEP == 0 && a.N % 16 == 0 && a.blocksize % 64 == 0 && a.r <= 16 &&
-         (a.N + WG_ROWS - 1) / WG_ROWS <= (int)(COUNTER_BYTES / 4) &&
-         a.ldx % 8 == 0 && aligned16(a.x) && aligned16(a.w) && (a.r == 0 || a.K % 8 == 0) &&
-         (a.r == 0 || aligned16(a.la));
+  if ((a.blocksize & (a.blocksize - 1)) != 0) return false;
+  if (!(a.M >= 1 && a.M <= 64 && a.K > 0 && a.K % KSTEP == 0 &&
+        a.K <= MAX_WAVES * (a.r > 0 ? 2 : KPW_MAX) * KSTEP && a.N % 16 == 0 && a.blocksize % 64 == 0 &&
+        a.r <= 16 && a.ldx % 8 == 0 && aligned16(a.x) && aligned16(a.w) &&
+        segments_aligned(a, 16)))
+    return false;
+  for (int s = 0; s < a.nseg; ++s)
+    if (a.r > 0 && !aligned16(a.la[s])) return false;
+  return true;
+}
+
+// Allows a kernel more than the default dynamic LDS (once per instantiation).
+template <typename K>
+int allow_lds(K kernel) {
+  static int rc = -1;
+  if (rc < 0)
+    rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES),
+                   "hipFuncSetAttribute");
+  return rc;
+}
+
+template <int MT, bool LORA, int KPW>
+int launch_kpw(LinearArgs& a, const LinearPlan& plan, hipStream_t st) {
+  dim3 grid(plan.grid), block(64 * plan.ntw * plan.kw);
+  if (plan.xlds) {
+    if (int rc = allow_lds(nf4_linear_mfma<MT, LORA, true, KPW>)) return rc;
+    nf4_linear_mfma<MT, LORA, true, KPW><<<grid, block, plan.lds, st>>>(a);
+  } else {
+    if (int rc = allow_lds(nf4_linear_mfma<MT, LORA, false, KPW>)) return rc;
+    nf4_linear_mfma<MT, LORA, false, KPW><<<grid, block, plan.lds, st>>>(a);
+  }
+  return launch_check("nf4_linear_mfma");
 }
 
 template <int MT>
-int launch_fast(const LinearArgs& a, const LinearPlan& plan, hipStream_t st) {
-  const size_t lds = (size_t)a.M * (plan.kps * KSTEP + 8) * 2 + 4 * MT * 16 * 16 * 4 + 16;
-  dim3 grid(plan.NG, plan.S);
+int launch_fast(LinearArgs& a, const LinearPlan& plan, hipStream_t st) {
   if (a.r > 0)
-    nf4_linear_mfma<MT, true><<<grid, 256, lds, st>>>(a);
-  else
-    nf4_linear_mfma<MT, false><<<grid, 256, lds, st>>>(a);
-  return launch_check("nf4_linear_mfma");
+    return plan.kpw <= 1 ? launch_kpw<MT, true, 1>(a, plan, st)
+                         : launch_kpw<MT, true, 2>(a, plan, st);
+  if (plan.kpw <= 1) return launch_kpw<MT, false, 1>(a, plan, st);
+  if (plan.kpw <= 2) return launch_kpw<MT, false, 2>(a, plan, st);
+  if (plan.kpw <= 4) return launch_kpw<MT, false, 4>(a, plan, st);
+  return launch_kpw<MT, false, 8>(a, plan, st);
+}
+
+int run_linear(LinearArgs& a, hipStream_t st) {
+  if (use_fast_linear(a)) {
+    const LinearPlan plan = plan_linear(a);
+    a.ntw = plan.ntw;
+    a.kw = plan.kw;
+    a.kpw = plan.kpw;
+    a.bs_shift = __builtin_ctz((unsigned)a.blocksize);
+    a.xstride = plan.xstride;
+    a.off_red = plan.off_red;
+    a.off_redt = plan.off_redt;
+    a.off_tsum = plan.off_tsum;
+    switch (plan.MT) {
+      case 1: return launch_fast<1>(a, plan, st);
+      case 2: return launch_fast<2>(a, plan, st);
+      default: return launch_fast<4>(a, plan, st);  // M in (32, 64]: one zero m-tile at most
+    }
+  }
+  const int64_t total = (int64_t)a.M * a.N;
+  nf4_linear_generic<<<dim3((unsigned)cdiv(total, 256)), 256, 0, st>>>(a);
+  return launch_check("nf4_linear_generic");
+}
+
+int check_common(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                 const float* code16, int blocksize, int r, const void* y, int64_t ldy, int M,
+                 int N, int K) {
+  if (M < 0 || N < 0 || K < 0) return einval("negative dimension");
+  if (r < 0) return einval("r < 0");
+  if (blocksize <= 0) return einval("blocksize must be > 0");
+  if (M == 0 || N == 0) return GRPO_OK;
+  if (!x || !w || !absmax || !code16 || !y) return einval("null pointer");
+  if (ldx < K || ldy < N) return einval("row stride smaller than the row");
+  return GRPO_OK;
 }
 
 }  // namespace
@@ -426,25 +580,14 @@ extern "C" int grpo_nf4_dequant(const uint8_t* w, const float* absmax, const flo
   return launch_check("nf4_dequant");
 }
 
-extern "C" size_t grpo_nf4_lora_linear_workspace_bytes(int M, int N, int K, int r) {
-  if (M <= 0 || N <= 0 || K <= 0 || M > 64 || K % KSTEP != 0 || N % 16 != 0 || r > 16) return 0;
-  if ((N + WG_ROWS - 1) / WG_ROWS > (int)(COUNTER_BYTES / 4)) return 0;
-  return plan_linear(M, N, K, r).bytes;
-}
-
 extern "C" int grpo_nf4_lora_linear(const void* x, int64_t ldx, const uint8_t* w,
                                     const float* absmax, const float* code16, int blocksize,
                                     const void* bias, const void* lora_a, const void* lora_b, int r,
                                     float scaling, void* y, int64_t ldy, int M, int N, int K,
-                                    void* workspace, size_t workspace_bytes,
                                     grpo_stream_t stream) {
-  if (M < 0 || N < 0 || K < 0) return einval("negative dimension");
-  if (r < 0) return einval("r < 0");
-  if (blocksize <= 0) return einval("blocksize must be > 0");
+  if (int rc = check_common(x, ldx, w, absmax, code16, blocksize, r, y, ldy, M, N, K)) return rc;
   if (M == 0 || N == 0) return GRPO_OK;
-  if (!x || !w || !absmax || !code16 || !y) return einval("null pointer");
   if (r > 0 && (!lora_a || !lora_b)) return einval("r > 0 needs lora_a and lora_b");
-  if (ldx < K || ldy < N) return einval("row stride smaller than the row");
   LinearArgs a{};
   a.x = static_cast<const uint16_t*>(x);
   a.ldx = ldx;
@@ -452,9 +595,11 @@ extern "C" int grpo_nf4_lora_linear(const void* x, int64_t ldx, const uint8_t* w
   a.absmax = absmax;
   a.code16 = code16;
   a.blocksize = blocksize;
-  a.bias = static_cast<const uint16_t*>(bias);
-  a.la = static_cast<const uint16_t*>(lora_a);
-  a.lb = static_cast<const uint16_t*>(lora_b);
+  a.nseg = 1;
+  a.seg_end[0] = N;
+  a.bias[0] = static_cast<const uint16_t*>(bias);
+  a.la[0] = static_cast<const uint16_t*>(lora_a);
+  a.lb[0] = static_cast<const uint16_t*>(lora_b);
   a.r = r;
   a.scaling = scaling;
   a.y = static_cast<uint16_t*>(y);
@@ -462,30 +607,50 @@ extern "C" int grpo_nf4_lora_linear(const void* x, int64_t ldx, const uint8_t* w
   a.M = M;
   a.N = N;
   a.K = K;
-  hipStream_t st = as_stream(stream);
-  if (K > 0 && use_fast_linear(a)) {
-    const LinearPlan plan = plan_linear(M, N, K, r);
-    a.S = plan.S;
-    a.kps = plan.kps;
-    if (plan.S > 1) {
-      if (!workspace || workspace_bytes < plan.bytes) {
-        set_error("invalid argument: workspace of %zu bytes needed, %zu given", plan.bytes,
-                  workspace_bytes);
-        return GRPO_EWORKSPACE;
-      }
-      uint8_t* ws = static_cast<uint8_t*>(workspace);
-      a.ws_cnt = reinterpret_cast<int*>(ws + plan.off_cnt);
-      a.ws_acc = reinterpret_cast<float*>(ws + plan.off_acc);
-      a.ws_t = reinterpret_cast<float*>(ws + plan.off_t);
-    }
-    switch (plan.MT) {
-      case 1: return launch_fast<1>(a, plan, st);
-      case 2: return launch_fast<2>(a, plan, st);
-      case 3: return launch_fast<3>(a, plan, st);
-      default: return launch_fast<4>(a, plan, st);
-    }
+  return run_linear(a, as_stream(stream));
+}
+
+extern "C" int grpo_nf4_lora_linear_grouped(const void* x, int64_t ldx, const uint8_t* w,
+                                            const float* absmax, const float* code16,
+                                            int blocksize, int nseg, const int* seg_rows,
+                                            const void* const* bias, const void* const* lora_a,
+                                            const void* const* lora_b, int r, float scaling,
+                                            void* y, int64_t ldy, int M, int K,
+                                            grpo_stream_t stream) {
+  if (nseg < 1 || nseg > MAXSEG) return einval("nseg must be in [1, 4]");
+  if (!seg_rows) return einval("null seg_rows");
+  int N = 0;
+  for (int s = 0; s < nseg; ++s) {
+    if (seg_rows[s] <= 0) return einval("segment with no rows");
+    N += seg_rows[s];
   }
-  const int64_t total = (int64_t)M * N;
-  nf4_linear_generic<<<dim3((unsigned)cdiv(total, 256)), 256, 0, st>>>(a);
-  return launch_check("nf4_linear_generic");
+  if (int rc = check_common(x, ldx, w, absmax, code16, blocksize, r, y, ldy, M, N, K)) return rc;
+  if (M == 0) return GRPO_OK;
+  LinearArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.w = w;
+  a.absmax = absmax;
+  a.code16 = code16;
+  a.blocksize = blocksize;
+  a.nseg = nseg;
+  int end = 0;
+  for (int s = 0; s < nseg; ++s) {
+    end += seg_rows[s];
+    a.seg_end[s] = end;
+    a.bias[s] = bias ? static_cast<const uint16_t*>(bias[s]) : nullptr;
+    a.la[s] = r > 0 && lora_a ? static_cast<const uint16_t*>(lora_a[s]) : nullptr;
+    a.lb[s] = r > 0 && lora_b ? static_cast<const uint16_t*>(lora_b[s]) : nullptr;
+    if (r > 0 && (!a.la[s] || !a.lb[s])) return einval("r > 0 needs lora_a and lora_b per segment");
+    if (nseg > 1 && (int64_t)seg_rows[s] * K % blocksize != 0)
+      return einval("every segment must hold whole absmax blocks");
+  }
+  a.r = r;
+  a.scaling = scaling;
+  a.y = static_cast<uint16_t*>(y);
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  return run_linear(a, as_stream(stream));
 }

@@ -26,12 +26,25 @@ SIGNATURES = {
     "grpo_init": (_I32, []),
     "grpo_last_error": (_c.c_char_p, []),
     "grpo_nf4_dequant": (_I32, [_VP, _VP, _VP, _VP, _I64, _I32, _VP]),
-    "grpo_nf4_lora_linear_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32]),
     "grpo_nf4_lora_linear": (
         _I32,
         [_VP, _I64, _VP, _VP, _VP, _I32, _VP, _VP, _VP, _I32, _F32, _VP, _I64, _I32, _I32, _I32,
-         _VP, _SZ, _VP],
+         _VP],
     ),
+    "grpo_nf4_lora_linear_grouped": (
+        _I32,
+        [_VP, _I64, _VP, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _I32, _F32, _VP, _I64, _I32,
+         _I32, _VP],
+    ),
+    "grpo_embedding": (_I32, [_VP, _VP, _I64, _I32, _VP, _I32, _VP]),
+    "grpo_add_rmsnorm": (_I32, [_VP, _VP, _VP, _VP, _VP, _I32, _I32, _F32, _VP]),
+    "grpo_rope_append": (
+        _I32,
+        [_VP, _I64, _I32, _I32, _I32, _VP, _VP, _I32, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I32,
+         _I32, _I32, _VP],
+    ),
+    "grpo_silu_mul": (_I32, [_VP, _I64, _I32, _VP, _I64, _I32, _VP]),
+    "grpo_argmax_bf16": (_I32, [_VP, _I64, _I32, _I32, _VP, _VP]),
     "grpo_paged_kv_append": (
         _I32,
         [_VP, _VP, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _I32, _I32, _I32, _I32, _I32, _VP],

@@ -19,10 +19,9 @@ _workspaces: dict[tuple[str, int], torch.Tensor] = {}
 def workspace(kind: str, nbytes: int, device: torch.device) -> torch.Tensor | None:
     """A zero-initialised uint8 scratch tensor of at least ``nbytes`` per (kind, device).
 
-    The NF4 linear's split-K counters must start at zero and are left at zero
-    by every call; attention partials need no initialisation.  Kinds are never
-    shared, so one kind's data cannot corrupt another's counters.  Calls on
-    different streams must not run concurrently with the same workspace.
+    Used for the attention's split-context partials (no initialisation
+    needed).  Calls on different streams must not run concurrently with the
+    same workspace.
     """
     if nbytes <= 0:
         return None
@@ -79,10 +78,6 @@ def nf4_dequant(packed: torch.Tensor, absmax: torch.Tensor, code: torch.Tensor, 
     return out
 
 
-def nf4_lora_linear_workspace_bytes(m: int, n: int, k: int, r: int) -> int:
-    return int(_lib.library().grpo_nf4_lora_linear_workspace_bytes(m, n, k, r))
-
-
 def nf4_lora_linear(x2d: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor,
                     code: torch.Tensor, blocksize: int, n: int, bias: torch.Tensor | None = None,
                     lora_a: torch.Tensor | None = None, lora_b: torch.Tensor | None = None,
@@ -114,13 +109,10 @@ def nf4_lora_linear(x2d: torch.Tensor, packed: torch.Tensor, absmax: torch.Tenso
         out = torch.empty((m, n), dtype=torch.bfloat16, device=x2d.device)
     elif out.shape != (m, n) or out.stride(1) != 1 or out.dtype != torch.bfloat16:
         raise ValueError("out must be a bf16 [M, N] tensor with unit column stride.")
-    nbytes = int(lib.grpo_nf4_lora_linear_workspace_bytes(m, n, k, r))
-    ws = workspace("nf4_linear", nbytes, x2d.device)
     rc = lib.grpo_nf4_lora_linear(
         x2d.data_ptr(), x2d.stride(0), packed.data_ptr(), absmax.data_ptr(), code.data_ptr(),
         int(blocksize), _lib.ptr(bias), _lib.ptr(lora_a), _lib.ptr(lora_b), r, float(scaling),
-        out.data_ptr(), out.stride(0), m, n, k, _lib.ptr(ws), 0 if ws is None else ws.numel(),
-        _lib.stream_handle(x2d.device))
+        out.data_ptr(), out.stride(0), m, n, k, _lib.stream_handle(x2d.device))
     _lib.check(rc, "grpo_nf4_lora_linear")
     return out
 

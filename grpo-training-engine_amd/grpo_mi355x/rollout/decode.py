@@ -1,0 +1,432 @@
+"""Model-level paged decode on the HIP kernels.
+
+``DecodeEngine`` runs one decode step of a ``Qwen2ForCausalLM`` (NF4 + LoRA) for
+a fixed batch of sequences on a ``PagedKVPool``: the reference's ``_step``
+(``src/triton_kernels/paged_kv.py:690-820``) as a fixed list of C-ABI launches
+per layer --
+
+  add+RMSNorm -> q|k|v NF4+LoRA (one grouped launch) -> RoPE + KV append ->
+  paged GQA attention (bf16 out) -> o_proj NF4+LoRA -> add+RMSNorm ->
+  gate|up NF4 (one launch) -> SiLU*mul -> down NF4
+
+-- then the final norm, the bf16 lm_head and greedy argmax.  Lengths, block
+tables and the token buffer live on the device, so the whole step (including
+the per-row bookkeeping) is captured once into a HIP graph and replayed with no
+host synchronisation.  Rows stop at EOS or at a per-row length cap; a stopped
+row is masked out of the append (slot -1) and of attention (length 0).
+
+``paged_kv_decode_model`` is the drop-in for ``paged_kv.paged_kv_decode_model``
+(``paged_kv.py:589-837``) with the reference's contract (returns
+``[B, max_new_tokens]`` new tokens, pad after a row finishes) and per-sequence
+block tables instead of the reference's shared ``arange`` table.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional
+
+import torch
+
+from .. import _lib
+from ..core.kv_pool import PagedKVPool
+from ..kernels import ops
+from .qwen2 import Qwen2ForCausalLM
+
+
+def _vp(x) -> ctypes.c_void_p:
+    return ctypes.c_void_p(x)
+
+
+class DecodeEngine:
+    """Static-shape decode step for ``batch`` rows over a KV pool."""
+
+    def __init__(self, model: Qwen2ForCausalLM, pool: PagedKVPool, batch: int, max_blocks: int,
+                 max_pos: Optional[int] = None):
+        self.lib = _lib.device_library()
+        cfg = model.config
+        self.model, self.pool, self.cfg = model, pool, cfg
+        self.B, self.max_blocks = batch, max_blocks
+        dev = pool.k.device
+        self.device = dev
+        H, D = cfg.hidden_size, cfg.head_dim
+        self.Hq, self.Hkv, self.D, self.H = (cfg.num_attention_heads, cfg.num_key_value_heads, D,
+                                             H)
+        self.I, self.V = cfg.intermediate_size, cfg.vocab_size
+        self.nqkv = (self.Hq + 2 * self.Hkv) * D
+        self.max_pos = max_pos or max_blocks * pool.block_size
+        self.cos, self.sin = model.model.rotary_emb.tables(self.max_pos)
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        i32 = dict(dtype=torch.int32, device=dev)
+        B = batch
+        # device state
+        self.tokens = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.pos = torch.zeros(B, **i32)          # tokens already cached
+        self.append_pos = torch.zeros(B, **i32)   # pos, or -1 for a stopped row
+        self.attn_len = torch.zeros(B, **i32)     # pos + 1, or 0 for a stopped row
+        self.active = torch.zeros(B, dtype=torch.bool, device=dev)
+        self.count = torch.zeros(B, **i32)
+        self.limit = torch.zeros(B, **i32)
+        self.step_idx = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.eos = torch.full((1,), -1, dtype=torch.int64, device=dev)
+        self.pad = torch.zeros(1, dtype=torch.int64, device=dev)
+        self.block_tables = torch.full((B, max_blocks), -1, **i32)
+        self.generated: Optional[torch.Tensor] = None
+        # activations
+        self.h = torch.zeros(B, H, **bf)
+        self.x = torch.zeros(B, H, **bf)
+        self.qkv = torch.zeros(B, self.nqkv, **bf)
+        self.q = torch.zeros(B, self.Hq, D, **bf)
+        self.attn = torch.zeros(B, self.Hq * D, **bf)
+        self.o = torch.zeros(B, H, **bf)
+        self.gu = torch.zeros(B, 2 * self.I, **bf)
+        self.act = torch.zeros(B, self.I, **bf)
+        self.down = torch.zeros(B, H, **bf)
+        self.logits = torch.zeros(B, self.V, **bf)
+        self.next = torch.zeros(B, dtype=torch.int64, device=dev)
+        self._prepare_layers()
+        self.graph: Optional[torch.cuda.CUDAGraph] = None
+        # Optional timing: (kind, algorithmic bytes, start event, end event) per
+        # timed launch; events are graph event-record nodes when captured.
+        self.timing = False
+        self._events: list[tuple[str, int, torch.cuda.Event, torch.cuda.Event]] = []
+
+    # ------------------------------------------------------------- set-up --
+    def _prepare_layers(self):
+        cfg, B, dev = self.cfg, self.B, self.device
+        self.layers = []
+        self._keep = []  # ctypes arrays referenced by the launches
+        for layer in self.model.model.layers:
+            at, mlp = layer.self_attn, layer.mlp
+            qkv = at.qkv
+            projs = [at.q_proj, at.k_proj, at.v_proj]
+            for p in projs:
+                if p.base_layer.weight.data_ptr() < qkv.packed.data_ptr() or \
+                        p.base_layer.weight.data_ptr() >= qkv.packed.data_ptr() + qkv.packed.numel():
+                    raise ValueError("q/k/v weights are not views of the stacked buffer")
+            r = projs[0].rank
+            seg_rows = (ctypes.c_int * 3)(*qkv.seg_rows)
+            biases = (ctypes.c_void_p * 3)(*[p.base_layer.bias.data_ptr() for p in projs])
+            la = (ctypes.c_void_p * 3)(*[p.lora_A.weight.data_ptr() for p in projs])
+            lb = (ctypes.c_void_p * 3)(*[p.lora_B.weight.data_ptr() for p in projs])
+            self._keep += [seg_rows, biases, la, lb]
+            o = at.o_proj
+            oq = o.base_layer.weight.quant_state
+            dq = mlp.down_proj.weight.quant_state
+            self.layers.append(dict(
+                in_norm=layer.input_layernorm.weight, post_norm=layer.post_attention_layernorm.weight,
+                eps=float(layer.input_layernorm.variance_epsilon),
+                qkv=qkv, seg_rows=seg_rows, biases=biases, la=la, lb=lb, r=r,
+                scaling=float(projs[0].scaling),
+                o_w=o.base_layer.weight, o_absmax=oq.absmax, o_code=oq.code,
+                o_la=o.lora_A.weight, o_lb=o.lora_B.weight, o_r=o.rank, o_scaling=float(o.scaling),
+                gu=mlp.gate_up, down_w=mlp.down_proj.weight, down_absmax=dq.absmax,
+                down_code=dq.code))
+        self.final_norm = self.model.model.norm.weight
+        self.final_eps = float(self.model.model.norm.variance_epsilon)
+        self.embed = self.model.model.embed_tokens.weight
+        self.lm_head = self.model.lm_head.weight
+        bs = cfg.nf4_blocksize
+        H, I, Hq, D = self.H, self.I, self.Hq, self.D
+        # workspaces sized before any graph capture
+        self.ws_attn = ops.workspace("paged_attn", max(ops.paged_attention_workspace_bytes(
+            B, Hq, self.Hkv, D, self.pool.block_size, self.max_blocks), 1), dev)
+        self.bs = bs
+        r = 16
+        nf4 = lambda n, k: n * k // 2 + n * k // bs * 4
+        self.bytes = dict(
+            qkv=nf4(self.nqkv, H) + 3 * r * H * 2 + self.nqkv * r * 2 + self.nqkv * 2
+            + B * H * 2 + B * self.nqkv * 2,
+            o=nf4(H, Hq * D) + (r * Hq * D + H * r) * 2 + B * Hq * D * 2 + B * H * 2,
+            gate_up=nf4(2 * I, H) + B * H * 2 + B * 2 * I * 2,
+            down=nf4(H, I) + B * I * 2 + B * H * 2,
+        )
+
+    # -------------------------------------------------------------- launch --
+    def _tick(self, kind: str, nbytes: int):
+        if not self.timing:
+            return None
+        e0 = torch.cuda.Event(enable_timing=True, external=True)
+        e1 = torch.cuda.Event(enable_timing=True, external=True)
+        e0.record()
+        self._events.append((kind, nbytes, e0, e1))
+        return e1
+
+    @staticmethod
+    def _tock(e1):
+        if e1 is not None:
+            e1.record()
+
+    def attention_bytes(self) -> int:
+        """Algorithmic bytes of one attention launch at the current lengths (host sync)."""
+        n = int(self.attn_len.sum().item())
+        nblk = int(((self.attn_len + self.pool.block_size - 1) // self.pool.block_size).sum())
+        return (n * self.Hkv * self.D * 2 * 2 + self.B * self.Hq * self.D * 2 * 2 + nblk * 4)
+
+    def _forward(self):
+        """Embedding -> layers -> final norm -> lm_head -> argmax (device only)."""
+        lib, st = self.lib, _lib.stream_handle(self.device)
+        B, H, D, Hq, Hkv, I = self.B, self.H, self.D, self.Hq, self.Hkv, self.I
+        chk = _lib.check
+        wsa, wsa_n = self.ws_attn.data_ptr(), self.ws_attn.numel()
+        pool = self.pool
+        chk(lib.grpo_embedding(self.tokens.data_ptr(), self.embed.data_ptr(), self.V, H,
+                               self.h.data_ptr(), B, st), "embedding")
+        for li, L in enumerate(self.layers):
+            kc, vc = pool.layer(li)
+            if li == 0:
+                chk(lib.grpo_add_rmsnorm(self.h.data_ptr(), None, None, L["in_norm"].data_ptr(),
+                                         self.x.data_ptr(), B, H, L["eps"], st), "rmsnorm")
+            else:
+                chk(lib.grpo_add_rmsnorm(self.down.data_ptr(), self.h.data_ptr(),
+                                         self.h.data_ptr(), L["in_norm"].data_ptr(),
+                                         self.x.data_ptr(), B, H, L["eps"], st), "add_rmsnorm")
+            q = L["qkv"]
+            e = self._tick("nf4_linear", self.bytes["qkv"])
+            chk(lib.grpo_nf4_lora_linear_grouped(
+                self.x.data_ptr(), H, q.packed.data_ptr(), q.absmax.data_ptr(), q.code.data_ptr(),
+                self.bs, 3, L["seg_rows"], L["biases"], L["la"], L["lb"], L["r"], L["scaling"],
+                self.qkv.data_ptr(), self.nqkv, B, H, st), "qkv")
+            self._tock(e)
+            chk(lib.grpo_rope_append(
+                self.qkv.data_ptr(), self.nqkv, Hq, Hkv, D, self.cos.data_ptr(),
+                self.sin.data_ptr(), self.max_pos, self.append_pos.data_ptr(),
+                self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), pool.num_blocks,
+                self.block_tables.data_ptr(), self.max_blocks, pool.block_size, self.max_blocks,
+                B, st), "rope_append")
+            e = self._tick("paged_attention", 0)
+            chk(lib.grpo_paged_attn_decode(
+                self.q.data_ptr(), Hq * D, D, kc.data_ptr(), vc.data_ptr(), pool.num_blocks,
+                self.block_tables.data_ptr(), self.max_blocks, self.attn_len.data_ptr(),
+                self.attn.data_ptr(), 1, B, Hq, Hkv, D, pool.block_size, self.max_blocks,
+                1.0 / math.sqrt(D), wsa, wsa_n, st), "attention")
+            self._tock(e)
+            e = self._tick("nf4_linear", self.bytes["o"])
+            chk(lib.grpo_nf4_lora_linear(
+                self.attn.data_ptr(), Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
+                L["o_code"].data_ptr(), self.bs, None, L["o_la"].data_ptr(), L["o_lb"].data_ptr(),
+                L["o_r"], L["o_scaling"], self.o.data_ptr(), H, B, H, Hq * D, st),
+                "o_proj")
+            self._tock(e)
+            chk(lib.grpo_add_rmsnorm(self.o.data_ptr(), self.h.data_ptr(), self.h.data_ptr(),
+                                     L["post_norm"].data_ptr(), self.x.data_ptr(), B, H,
+                                     L["eps"], st), "post_norm")
+            g = L["gu"]
+            e = self._tick("nf4_linear", self.bytes["gate_up"])
+            chk(lib.grpo_nf4_lora_linear(
+                self.x.data_ptr(), H, g.packed.data_ptr(), g.absmax.data_ptr(),
+                g.code.data_ptr(), self.bs, None, None, None, 0, 1.0, self.gu.data_ptr(), 2 * I,
+                B, 2 * I, H, st), "gate_up")
+            self._tock(e)
+            chk(lib.grpo_silu_mul(self.gu.data_ptr(), 2 * I, I, self.act.data_ptr(), I, B, st),
+                "silu_mul")
+            e = self._tick("nf4_linear", self.bytes["down"])
+            chk(lib.grpo_nf4_lora_linear(
+                self.act.data_ptr(), I, L["down_w"].data_ptr(), L["down_absmax"].data_ptr(),
+                L["down_code"].data_ptr(), self.bs, None, None, None, 0, 1.0,
+                self.down.data_ptr(), H, B, H, I, st), "down")
+            self._tock(e)
+        chk(lib.grpo_add_rmsnorm(self.down.data_ptr(), self.h.data_ptr(), self.h.data_ptr(),
+                                 self.final_norm.data_ptr(), self.x.data_ptr(), B, H,
+                                 self.final_eps, st), "final_norm")
+        e = self._tick("lm_head", self.lm_head.numel() * 2 + self.B * (self.H + self.V) * 2)
+        torch.matmul(self.x, self.lm_head.t(), out=self.logits)
+        self._tock(e)
+        chk(lib.grpo_argmax_bf16(self.logits.data_ptr(), self.V, self.V, B,
+                                 self.next.data_ptr(), st), "argmax")
+
+    def _advance(self, greedy_tokens: torch.Tensor):
+        """Record the step's tokens and move the per-row state (device only)."""
+        out = torch.where(self.active, greedy_tokens, self.pad)
+        if self.generated is not None:
+            self.generated.scatter_(1, self.step_idx.view(1, 1).expand(self.B, 1), out.view(-1, 1))
+        self.step_idx.add_(1)
+        act = self.active.to(torch.int32)
+        self.pos.add_(act)
+        self.count.add_(act)
+        still = self.active & (self.count < self.limit) & (greedy_tokens != self.eos)
+        self.active.copy_(still)
+        self.tokens.copy_(greedy_tokens)
+        self._masks()
+
+    def _masks(self):
+        self.append_pos.copy_(torch.where(self.active, self.pos, torch.full_like(self.pos, -1)))
+        self.attn_len.copy_(torch.where(self.active, self.pos + 1, torch.zeros_like(self.pos)))
+
+    def _step(self):
+        self._forward()
+        self._advance(self.next)
+
+    # ------------------------------------------------------------ control --
+    def start(self, tokens: torch.Tensor, positions: torch.Tensor, block_tables: torch.Tensor,
+              limits: torch.Tensor, max_new_tokens: int, eos_token_id: Optional[int] = None,
+              pad_token_id: int = 0, record: bool = True):
+        """Load a new batch: input tokens at ``positions`` (tokens already cached)."""
+        B = self.B
+        self.tokens.copy_(tokens.view(B))
+        self.pos.copy_(positions.view(B).to(torch.int32))
+        self.count.zero_()
+        self.limit.copy_(limits.view(B).to(torch.int32))
+        self.active.copy_(self.limit > 0)
+        self.step_idx.zero_()
+        self.eos.fill_(-1 if eos_token_id is None else int(eos_token_id))
+        self.pad.fill_(int(pad_token_id))
+        w = block_tables.shape[1]
+        self.block_tables.fill_(-1)
+        self.block_tables[:, :w].copy_(block_tables)
+        if record:
+            if self.generated is None or self.generated.shape[1] != max_new_tokens:
+                self.generated = torch.full((B, max_new_tokens), pad_token_id, dtype=torch.int64,
+                                            device=self.device)
+                self.graph = None  # the recorded step writes into this buffer
+            self.generated.fill_(pad_token_id)
+        self._masks()
+
+    def capture(self, timing: bool = False):
+        """Record one step into a HIP graph (after two warm-up steps on a side stream).
+
+        ``timing=True`` adds event-record nodes around every NF4-linear, attention
+        and lm_head launch; ``kernel_times()`` reads them after a replay.
+        """
+        # A warm-up step writes K/V only at each active row's slot pos[b], which
+        # is not yet valid cache content: the first real step rewrites it before
+        # attention reads it.  Row state is saved and restored around them.
+        saved = [t.clone() for t in (self.tokens, self.pos, self.count, self.active,
+                                     self.step_idx)]
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            for _ in range(2):
+                self._step()
+                self._restore(saved)
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        self._events = []
+        self.timing = timing
+        try:
+            with torch.cuda.graph(g, stream=s):
+                self._step()
+        finally:
+            self.timing = False
+        self._restore(saved)
+        self.graph = g
+
+    def _restore(self, saved):
+        for t, v in zip((self.tokens, self.pos, self.count, self.active, self.step_idx), saved):
+            t.copy_(v)
+        if self.generated is not None:
+            self.generated.fill_(int(self.pad.item()))
+        self._masks()
+
+    def kernel_times(self) -> dict:
+        """{kind: (total ms, total algorithmic bytes, launches)} of the last replay."""
+        out: dict[str, list] = {}
+        for kind, nbytes, e0, e1 in self._events:
+            t = out.setdefault(kind, [0.0, 0, 0])
+            t[0] += e0.elapsed_time(e1)
+            t[1] += nbytes
+            t[2] += 1
+        return {k: tuple(v) for k, v in out.items()}
+
+    def step(self):
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self._step()
+
+    def run(self, steps: int):
+        for _ in range(steps):
+            self.step()
+
+
+# ------------------------------------------------------------- drop-in ---
+
+def _prompt_rows(input_ids: torch.Tensor, attention_mask: Optional[torch.Tensor]):
+    ids = input_ids.detach().cpu()
+    mask = None if attention_mask is None else attention_mask.detach().cpu()
+    rows = []
+    for b in range(ids.shape[0]):
+        r = ids[b] if mask is None else ids[b][mask[b].bool()]
+        rows.append(tuple(int(t) for t in r.tolist()))
+    return rows
+
+
+@torch.no_grad()
+def prefill(engine1: DecodeEngine, pool: PagedKVPool, prompt: tuple, width: int) -> int:
+    """Teacher-forced prefill of ``prompt[:-1]`` into a new pool sequence (B = 1 engine)."""
+    sid = pool.allocate(len(prompt))
+    n = len(prompt) - 1
+    if n > 0:
+        dev = engine1.device
+        tbl = pool.block_table([sid], width, device=dev)
+        engine1.start(torch.tensor([prompt[0]], device=dev), torch.zeros(1, device=dev), tbl,
+                      torch.tensor([n], device=dev), n, record=False)
+        prompt_t = torch.tensor(prompt, dtype=torch.int64, device=dev)
+        for t in range(n):
+            engine1.tokens.copy_(prompt_t[t:t + 1])  # teacher forcing
+            engine1.step()
+    pool.set_length(sid, n)
+    return sid
+
+
+@torch.no_grad()
+def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
+                          attention_mask: Optional[torch.Tensor] = None,
+                          max_new_tokens: int = 128, do_sample: bool = False,
+                          temperature: float = 1.0, top_p: float = 1.0,
+                          pad_token_id: int = 0, eos_token_id: Optional[int] = None,
+                          seed: Optional[int] = None, block_size: int = 16,
+                          use_cache: Optional[bool] = None,
+                          stop_lengths: Optional[list[int]] = None) -> torch.Tensor:
+    """Drop-in for ``paged_kv.paged_kv_decode_model``: returns ``[B, max_new_tokens]``.
+
+    Rows with identical (unpadded) prompts share one prefill; their full prompt
+    blocks are shared through the pool and the partial last block is copied
+    per row.  ``stop_lengths`` (an extension) caps each row's generated length.
+    Greedy decoding runs entirely in the captured graph.
+    """
+    if max_new_tokens <= 0:
+        raise ValueError(f"max_new_tokens must be > 0, got {max_new_tokens}.")
+    if input_ids.ndim != 2 or input_ids.shape[1] == 0:
+        raise ValueError("input_ids must be [batch, seq_len] with at least 1 token.")
+    if do_sample and temperature > 0.0:
+        raise ValueError("sampling (do_sample=True) is not implemented on the HIP decode "
+                         "graph yet; use greedy decoding")
+    cfg = model.config
+    dev = input_ids.device
+    rows = _prompt_rows(input_ids, attention_mask)
+    B = len(rows)
+    max_ctx = max(len(r) for r in rows) + max_new_tokens
+    width = -(-max_ctx // block_size)
+    uniq = sorted(set(rows), key=rows.index)
+    nblocks = len(uniq) * width + B * (width + 1)
+    pool = PagedKVPool(cfg.num_hidden_layers, nblocks, cfg.num_key_value_heads, cfg.head_dim,
+                       block_size, device=dev)
+    eng1 = DecodeEngine(model, pool, 1, width)
+    eng1.capture()
+    parents = {p: prefill(eng1, pool, p, width) for p in uniq}
+    sids = []
+    for r in rows:
+        (cid,) = pool.fork(parents[r], 1, reserve_tokens=len(r) - 1 + max_new_tokens + 1)
+        sids.append(cid)
+    for p in parents.values():
+        pool.free(p)
+    pool.check_invariants()
+    eng = DecodeEngine(model, pool, B, width)
+    limits = torch.tensor(stop_lengths if stop_lengths is not None else [max_new_tokens] * B,
+                          dtype=torch.int32, device=dev).clamp(max=max_new_tokens)
+    eng.start(torch.tensor([r[-1] for r in rows], device=dev),
+              torch.tensor([len(r) - 1 for r in rows], device=dev),
+              pool.block_table(sids, width, device=dev), limits, max_new_tokens,
+              eos_token_id=eos_token_id, pad_token_id=pad_token_id)
+    eng.capture()
+    eng.start(torch.tensor([r[-1] for r in rows], device=dev),
+              torch.tensor([len(r) - 1 for r in rows], device=dev),
+              pool.block_table(sids, width, device=dev), limits, max_new_tokens,
+              eos_token_id=eos_token_id, pad_token_id=pad_token_id)
+    eng.run(max_new_tokens)
+    return eng.generated.clone()
+
+
+__all__ = ["DecodeEngine", "paged_kv_decode_model", "prefill"]

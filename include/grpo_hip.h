@@ -56,14 +56,6 @@ const char* grpo_last_error(void);
 int grpo_nf4_dequant(const uint8_t* w, const float* absmax, const float* code16, void* out,
                      int64_t numel, int blocksize, grpo_stream_t stream);
 
-/* Workspace bytes grpo_nf4_lora_linear needs for this shape (0 if none).
- * Layout: the first 64 KiB hold split-K group counters, the rest partial sums.
- * The counters must be zero before the first use (zero-fill a new workspace
- * once); every call leaves them at zero, so one workspace can serve calls of
- * any shape in stream order.  Calls that may run concurrently must not share a
- * workspace, and the workspace must not be used for anything else. */
-size_t grpo_nf4_lora_linear_workspace_bytes(int M, int N, int K, int r);
-
 /* y[M,N] = bf16(bf16(bf16(x W^T) + bias) + bf16(bf16(bf16(x A^T) B^T) * bf16(scaling)))
  * -- the fused NF4 + LoRA forward of FusedLoRAFunction.forward /
  * _lora_forward_kernel (src/triton_kernels/lora_forward.py:653-759, 107-260).
@@ -73,12 +65,28 @@ size_t grpo_nf4_lora_linear_workspace_bytes(int M, int N, int K, int r);
  *   lora_a  : bf16 [r, K] (row-major), lora_b: bf16 [N, r]; r == 0 drops the
  *             LoRA term (plain NF4 linear; lora_a/lora_b may be NULL)
  *   y       : bf16 [M, N], row stride ldy
- */
+ * Needs no workspace: any split of K is reduced inside one workgroup, so the
+ * result is deterministic (independent of scheduling). */
 int grpo_nf4_lora_linear(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
                          const float* code16, int blocksize, const void* bias, const void* lora_a,
                          const void* lora_b, int r, float scaling, void* y, int64_t ldy, int M,
-                         int N, int K, void* workspace, size_t workspace_bytes,
-                         grpo_stream_t stream);
+                         int N, int K, grpo_stream_t stream);
+
+/* Grouped form: the output rows are split into nseg (1..4) consecutive
+ * segments of seg_rows[s] rows, stacked in ONE NF4 weight (w/absmax cover all
+ * rows) and one output y[M, sum(seg_rows)].  Segment s has its own bias[s]
+ * (or NULL), lora_a[s] [r, K] and lora_b[s] [seg_rows[s], r]; bias, lora_a
+ * and lora_b are HOST arrays of nseg device pointers (bias itself may be
+ * NULL).  One launch computes what the reference computes with one
+ * lora_fused_forward per projection -- the q/k/v projections of
+ * fused_qkv_rope (src/triton_kernels/fused_ops.py:198-219) or gate/up of
+ * fused_mlp (fused_ops.py:184-193). */
+int grpo_nf4_lora_linear_grouped(const void* x, int64_t ldx, const uint8_t* w,
+                                 const float* absmax, const float* code16, int blocksize, int nseg,
+                                 const int* seg_rows, const void* const* bias,
+                                 const void* const* lora_a, const void* const* lora_b, int r,
+                                 float scaling, void* y, int64_t ldy, int M, int K,
+                                 grpo_stream_t stream);
 
 /* ------------------------------------------------------------ paged KV --
  * Cache layout: k_cache, v_cache bf16 [num_blocks, Hkv, block_size, D],
@@ -117,6 +125,46 @@ int grpo_paged_attn_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h
                            const int32_t* context_lens, void* out, int out_bf16, int B, int Hq,
                            int Hkv, int D, int block_size, int max_blocks, float scale,
                            void* workspace, size_t workspace_bytes, grpo_stream_t stream);
+
+/* ------------------------------------------------------- decode step --
+ * Ops of the model-level decode step around the two hot-path kernels
+ * (src/triton_kernels/paged_kv.py:690-820).  bf16 tensors are row-major. */
+
+/* out[b,:] = table[ids[b],:] (table bf16 [V, H]; ids int64 [B]; ids outside
+ * [0, V) give zeros).  Replaces embeddings(last_tokens) (paged_kv.py:691). */
+int grpo_embedding(const int64_t* ids, const void* table, int64_t V, int H, void* out, int B,
+                   grpo_stream_t stream);
+
+/* h = residual ? bf16(x + residual) : x  (written to h_out when residual and
+ * h_out are given; h_out may alias residual); y = bf16(bf16(h * rsqrt(mean(h^2)
+ * + eps)) * weight).  x, residual, h_out, y: [M, H]; weight [H].  Replaces the
+ * residual add + fused_rmsnorm pair (paged_kv.py:706-711, 791-798;
+ * fused_ops.py:34-77). */
+int grpo_add_rmsnorm(const void* x, const void* residual, void* h_out, const void* weight,
+                     void* y, int M, int H, float eps, grpo_stream_t stream);
+
+/* RoPE on q and k of one token per sequence (position context_lens[b], cos/sin
+ * tables bf16 [max_pos, D]), q -> q_out [B, Hq, D], rotated k and v appended to
+ * the paged cache at slot context_lens[b] (same skip rules as
+ * grpo_paged_kv_append).  qkv: [B, ld] rows laid out [q | k | v].  Replaces
+ * fused_qkv_rope's RoPE (fused_ops.py:212-218) + repeat_kv + the KV update
+ * kernel (paged_kv.py:723-752). */
+int grpo_rope_append(const void* qkv, int64_t ld, int Hq, int Hkv, int D, const void* cos_table,
+                     const void* sin_table, int max_pos, const int32_t* context_lens, void* q_out,
+                     void* k_cache, void* v_cache, int64_t num_blocks,
+                     const int32_t* block_tables, int64_t bt_stride, int block_size,
+                     int max_blocks, int B, grpo_stream_t stream);
+
+/* out[m, :N] = bf16(bf16(silu(g)) * u) with g = gate_up[m, :N], u = gate_up[m, N:2N]
+ * (fused_silu_mul, fused_ops.py:79-112, 151-181). */
+int grpo_silu_mul(const void* gate_up, int64_t ld, int N, void* out, int64_t ldo, int M,
+                  grpo_stream_t stream);
+
+/* out[m] = first index of the maximum of logits[m, :V] (bf16, row stride ld);
+ * greedy sampling of _sample_tokens / fused_logits_sampling (paged_kv.py:444-445,
+ * fused_ops.py:232-234). */
+int grpo_argmax_bf16(const void* logits, int64_t ld, int V, int M, int64_t* out,
+                     grpo_stream_t stream);
 
 #ifdef __cplusplus
 }

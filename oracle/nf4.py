@@ -124,8 +124,27 @@ def dequantize_nf4(packed, absmax, numel: int, blocksize: int,
     ``w = bf16_rne(float32(code[q]) * float32(a))`` per element
     (``lora_forward.py:183-206``).
     """
+    if nested is None and numel % blocksize == 0 and blocksize % 2 == 0:
+        return _dequantize_blocked(packed, absmax, numel, blocksize, code)
     q = nibbles(packed, numel)
     c = np.asarray(code, dtype=np.float32)[q]
     a = block_scales(absmax, numel, blocksize, nested)
     w = (c * a).astype(np.float32)
     return f32_to_bf16_bits(w)
+
+
+def _dequantize_blocked(packed, absmax, numel: int, blocksize: int, code) -> np.ndarray:
+    """Same values as the element-wise path, computed per whole block.
+
+    A 256-entry table gives (code[hi], code[lo]) per byte; each block of
+    ``blocksize`` elements (``blocksize/2`` bytes) is multiplied by its absmax;
+    identical float32 products, identical rounding.  Used to keep the CPU
+    baseline of a full-model step within seconds.
+    """
+    c = np.asarray(code, dtype=np.float32)
+    lut = np.stack([c[np.arange(256) >> 4], c[np.arange(256) & 15]], axis=1)  # [256, 2]
+    nblk = numel // blocksize
+    by = np.asarray(packed, dtype=np.uint8).reshape(-1)[: numel // 2].reshape(nblk, blocksize // 2)
+    a = np.asarray(absmax, dtype=np.float32).reshape(-1)[:nblk]
+    w = lut[by] * a[:, None, None]  # [nblk, bs/2, 2] float32
+    return f32_to_bf16_bits(w.reshape(-1))

@@ -47,9 +47,6 @@ def test_python_signatures_cover_the_header():
 
 def test_version_and_workspace_sizes(lib):
     assert lib.grpo_version() == 100
-    # split-K needs a workspace at the down_proj shape; not when one split suffices
-    assert lib.grpo_nf4_lora_linear_workspace_bytes(8, 1536, 8960, 0) > 0
-    assert lib.grpo_nf4_lora_linear_workspace_bytes(8, 16, 16, 4) == 0  # generic path
     assert lib.grpo_paged_attn_workspace_bytes(8, 12, 2, 128, 16, 64) > 0
     assert lib.grpo_paged_attn_workspace_bytes(8, 12, 2, 8, 4, 64) == 0  # generic path
 
@@ -58,7 +55,7 @@ def test_argument_errors_return_negative_codes(lib):
     rc = lib.grpo_nf4_dequant(None, None, None, None, -1, 64, None)
     assert rc < 0 and b"numel" in lib.grpo_last_error()
     rc = lib.grpo_nf4_lora_linear(None, 0, None, None, None, 64, None, None, None, 0, 1.0, None,
-                                  0, 1, 1, 1, None, 0, None)
+                                  0, 1, 1, 1, None)
     assert rc < 0 and b"null" in lib.grpo_last_error()
     rc = lib.grpo_paged_attn_decode(None, 0, 0, None, None, 1, None, 0, None, None, 0, 1, 12, 5,
                                     128, 16, 4, 1.0, None, 0, None)

@@ -95,6 +95,8 @@ FAST = [
     (64, 512, 512, 16, True),
     (32, 3584, 3584, 16, True),   # 7B q_proj at G = 32
     (64, 512, 3584, 16, True),    # 7B k/v_proj at G = 64
+    (8, 3584, 18944, 0, False),   # 7B down_proj (deepest k-split)
+    (64, 256, 4096, 16, True),    # LoRA with two k-steps per wave
 ]
 
 
@@ -132,21 +134,15 @@ def test_linear_blocksize_128(dev):
     assert rel_err(bf16_bits_to_f32(got), bf16_bits_to_f32(oracle_linear(c))) <= TOL
 
 
-def test_linear_split_k_is_deterministic_and_resets(dev):
-    """Repeated and interleaved split-K calls give bit-identical results."""
-    from grpo_mi355x.kernels import ops
-
+def test_linear_is_deterministic_across_calls(dev):
+    """Repeated and interleaved calls of different shapes give bit-identical results."""
     big = make_linear_case(5, 8, 1536, 8960, 0, False)
     small = make_linear_case(6, 8, 256, 1536, 16, True)
-    assert ops.nf4_lora_linear_workspace_bytes(8, 1536, 8960, 0) > 0
     y1 = run_linear(dev, big)
     ys = run_linear(dev, small)
     y2 = run_linear(dev, big)
     ys2 = run_linear(dev, small)
     assert np.array_equal(y1, y2) and np.array_equal(ys, ys2)
-    ws = ops._workspaces.get(("nf4_linear", dev.index or 0))
-    # the first 64 KiB hold the split-K group counters; they must be back at zero
-    assert torch.all(ws[:65536] == 0)
 
 
 def test_linear_scaling_and_zero_lora(dev):

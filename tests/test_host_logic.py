@@ -1,0 +1,142 @@
+"""CPU tests of host-side logic: the paged KV block pool and argument validation."""
+
+import pytest
+import torch
+
+from grpo_mi355x.core.kv_pool import PagedKVPool
+
+
+def test_pool_allocate_reserve_free():
+    pool = PagedKVPool(2, 10, 2, 8, block_size=4)
+    a = pool.allocate(9)  # 3 blocks
+    assert len(pool.blocks[a]) == 3 and pool.num_free == 7
+    pool.reserve(a, 12)  # still 3 blocks
+    assert len(pool.blocks[a]) == 3
+    pool.reserve(a, 13)
+    assert len(pool.blocks[a]) == 4
+    pool.check_invariants()
+    pool.free(a)
+    assert pool.num_free == 10
+    pool.check_invariants()
+
+
+def test_pool_out_of_blocks_raises():
+    pool = PagedKVPool(1, 2, 1, 4, block_size=4)
+    pool.allocate(8)
+    with pytest.raises(RuntimeError, match="out of memory"):
+        pool.allocate(1)
+
+
+def test_fork_shares_full_blocks_and_copies_partial():
+    pool = PagedKVPool(2, 32, 2, 8, block_size=4)
+    p = pool.allocate(10)
+    pool.set_length(p, 10)  # 2 full blocks + 2 tokens in the third
+    pool.k[:, pool.blocks[p][2]] = 7.0
+    kids = pool.fork(p, 3, reserve_tokens=20)
+    for c in kids:
+        assert pool.blocks[c][:2] == pool.blocks[p][:2]           # shared prefix
+        assert pool.blocks[c][2] != pool.blocks[p][2]             # private copy of the tail
+        assert torch.all(pool.k[:, pool.blocks[c][2]] == 7.0)     # copied content
+        assert len(pool.blocks[c]) == 5
+    assert pool.refcount[pool.blocks[p][0]] == 4
+    pool.check_invariants()
+    pool.free(p)
+    pool.check_invariants()
+    assert pool.refcount[pool.blocks[kids[0]][0]] == 3
+    for c in kids:
+        pool.free(c)
+    assert pool.num_free == 32
+    pool.check_invariants()
+
+
+def test_fork_at_block_boundary_shares_everything():
+    pool = PagedKVPool(1, 16, 1, 4, block_size=4)
+    p = pool.allocate(8)
+    pool.set_length(p, 8)
+    (c,) = pool.fork(p, 1, reserve_tokens=12)
+    assert pool.blocks[c][:2] == pool.blocks[p][:2] and len(pool.blocks[c]) == 3
+    pool.check_invariants()
+
+
+def test_invariant_checker_catches_shared_writable_block():
+    pool = PagedKVPool(1, 8, 1, 4, block_size=4)
+    a = pool.allocate(8)
+    pool.set_length(a, 5)
+    b = pool.allocate(0)
+    pool.blocks[b] = [pool.blocks[a][1]]  # b aliases a's writable block
+    pool.refcount[pool.blocks[a][1]] += 1
+    with pytest.raises(AssertionError, match="shared block"):
+        pool.check_invariants()
+
+
+def test_block_table_padding():
+    pool = PagedKVPool(1, 8, 1, 4, block_size=4)
+    a, b = pool.allocate(8), pool.allocate(3)
+    t = pool.block_table([a, b], 4)
+    assert t.dtype == torch.int32 and t.shape == (2, 4)
+    assert t[1, 1:].tolist() == [-1, -1, -1]
+    with pytest.raises(ValueError):
+        pool.block_table([a], 1)
+
+
+def test_lora_validation_messages_match_reference():
+    from grpo_mi355x.kernels.lora_forward import _validate_inputs
+
+    class QS:
+        shape = (8, 16)
+
+    x = torch.zeros(2, 16)
+    with pytest.raises(ValueError, match=r"x must be \[batch, seq_len, hidden\]"):
+        _validate_inputs(x, torch.zeros(1), QS(), torch.zeros(4, 16), torch.zeros(8, 4))
+    with pytest.raises(ValueError, match="must be on CUDA"):
+        _validate_inputs(torch.zeros(1, 2, 16), torch.zeros(1), QS(), torch.zeros(4, 16),
+                         torch.zeros(8, 4))
+
+
+def test_lora_dropout_rejected_before_any_kernel():
+    from grpo_mi355x.kernels.lora_forward import lora_fused_forward
+
+    with pytest.raises(ValueError, match="Dropout"):
+        lora_fused_forward(torch.zeros(1, 1, 4), base_layer=object(), lora_A=object(),
+                           lora_B=object(), scaling=2.0, dropout=torch.nn.Dropout(0.1))
+
+
+def test_paged_validation_messages_match_reference():
+    from grpo_mi355x.kernels.paged_kv import _validate_inputs
+
+    ids = torch.zeros(2, 3, dtype=torch.long)
+    kc = torch.zeros(4, 2, 16, 8, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="input_ids must be"):
+        _validate_inputs(torch.zeros(3, dtype=torch.long), kc, kc, torch.zeros(2, 4), torch.zeros(2))
+    with pytest.raises(ValueError, match="identical shapes"):
+        _validate_inputs(ids, kc, kc[:2], torch.zeros(2, 4), torch.zeros(2))
+    with pytest.raises(ValueError, match="batch dimension"):
+        _validate_inputs(ids, kc, kc, torch.zeros(3, 4), torch.zeros(2))
+    with pytest.raises(ValueError, match="CUDA"):
+        _validate_inputs(ids, kc, kc, torch.zeros(2, 4), torch.zeros(2))
+
+
+def test_manual_lora_layer_surface():
+    from grpo_mi355x.core.lora import ManualLoRALayer, get_lora_parameters, inject_lora_layers
+    from grpo_mi355x.core.nf4 import Linear4bitNF4
+
+    base = Linear4bitNF4.from_weight(torch.randn(16, 32) * 0.02, torch.zeros(16))
+    layer = ManualLoRALayer(base, rank=4, alpha=8)
+    assert layer.scaling == 2.0 and layer.rank == 4 and layer.alpha == 8
+    assert torch.all(layer.lora_B.weight == 0)
+    assert not layer.base_layer.weight.requires_grad
+    assert layer.base_layer.weight.quant_state.shape == (16, 32)
+
+    class Tiny(torch.nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.q_proj = Linear4bitNF4.from_weight(torch.randn(16, 32))
+            self.k_proj = Linear4bitNF4.from_weight(torch.randn(16, 32))
+            self.other = torch.nn.Linear(32, 16)
+
+    m = Tiny()
+    assert inject_lora_layers(m, ["q_proj", "other"], rank=4, alpha=8) == 1
+    assert isinstance(m.q_proj, ManualLoRALayer) and isinstance(m.k_proj, Linear4bitNF4)
+    assert len(get_lora_parameters(m)) == 2
+    # the quant state survives the dtype cast of inject_lora_layers
+    assert m.q_proj.base_layer.weight.quant_state.absmax.dtype == torch.float32

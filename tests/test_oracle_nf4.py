@@ -122,3 +122,16 @@ def test_dequant_shapes(numel):
     absmax = g.random(-(-numel // 64)).astype(np.float32)
     out = dequantize_nf4(packed, absmax, numel, 64)
     assert out.shape == (numel,) and out.dtype == np.uint16
+
+
+def test_blocked_dequant_equals_elementwise():
+    from oracle.nf4 import _dequantize_blocked
+
+    g = rng(9)
+    for numel, bs in [(64 * 37, 64), (128 * 5, 128), (256 * 3, 256)]:
+        packed = g.integers(0, 256, numel // 2).astype(np.uint8)
+        absmax = (g.random(numel // bs) * 3).astype(np.float32)
+        q = nibbles(packed, numel)
+        ref = f32_to_bf16_bits(NF4_CODE[q] * np.repeat(absmax, bs))
+        assert np.array_equal(_dequantize_blocked(packed, absmax, numel, bs, NF4_CODE), ref)
+        assert np.array_equal(dequantize_nf4(packed, absmax, numel, bs), ref)
