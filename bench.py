@@ -13,9 +13,10 @@ the 8 rows through the block pool, and excluded from the metric).  The metric is
 generated tokens of active rows / wall time of the decode loop.
 
 The JSON line also carries:
-* ``roofline`` -- the dominant kernel (the NF4 linear: q|k|v, o, gate|up, down)
-  over one rollout replayed with graph event-record nodes around each launch:
-  achieved = algorithmic bytes / summed launch durations, peak 8 TB/s;
+* ``roofline`` -- the dominant kernel, the NF4 split-K linear (q|k|v, o,
+  gate|up, down): each kind's 28 per-layer launches of the decode step are
+  replayed as a HIP graph between HIP events on their stream; achieved =
+  algorithmic bytes per launch / average launch duration, peak 8 TB/s;
 * ``cpu_baseline`` -- the numpy oracle (a restatement of the reference's
   PyTorch semantics) running one decode step of the same model on the host.
 """
@@ -82,6 +83,43 @@ def rollout_bytes(cfg, model, stops, prompt_len, group, block_size=16):
                 steps=steps, weight_per_step=per_step_weights)
 
 
+def nf4_kernel_timing(eng, dev, reps: int = 20) -> dict:
+    """Average launch duration of the NF4 split-K linear, per projection kind.
+
+    The step's own NF4 launches of one kind (one per layer, the decode step's
+    arguments) are captured into a HIP graph; the graph is replayed ``reps``
+    times between two HIP events on the stream it runs on, so the average
+    covers back-to-back launches (including the short gap between graph
+    nodes) with every layer's weights streamed from HBM.
+    """
+    import torch
+
+    out = {}
+    side = torch.cuda.Stream(device=dev)
+    for kind in ("qkv", "o", "gate_up", "down"):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=side):
+            launches = [(nb, fn) for k, nb, fn in eng.nf4_launches() if k == kind]
+            for _, fn in launches:
+                fn()
+        g.replay()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (reps * len(launches))
+        nb = launches[0][0]
+        out[kind] = dict(launches=len(launches), avg_us=round(us, 3), bytes_per_launch=nb,
+                         achieved_GBs=round(nb / (us * 1e-6) / 1e9, 1),
+                         splits=eng.plans[kind][0])
+        del g
+    return out
+
+
 def cpu_baseline(model, cfg, group, ctx, seed):
     """One decode step of the numpy oracle on the host (bounded sample)."""
     import numpy as np
@@ -132,7 +170,13 @@ def cpu_baseline(model, cfg, group, ctx, seed):
     t0 = time.perf_counter()
     oracle.step(toks, kcs, vcs, tables, pos)
     dt = time.perf_counter() - t0
-    return dict(value=round(group / dt, 4), unit="tok/s", cores=os.cpu_count(), kind="port",
+    try:
+        from threadpoolctl import threadpool_info
+
+        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:  # pragma: no cover - threadpoolctl is optional
+        cores = os.cpu_count()
+    return dict(value=round(group / dt, 4), unit="tok/s", cores=cores, kind="port",
                 sample=(f"1 decode step of the numpy oracle, G={group} rows at context {ctx + 1}, "
                         f"all 28 layers + lm_head, NF4 dequantized per call; {dt:.2f} s "
                         "(numpy: elementwise single-threaded, BLAS matmuls multi-threaded)"))
@@ -217,36 +261,16 @@ def main():
     roofline = None
     kernels = {}
     if not args.no_kernel_timing:
-        # Same rollout, graph re-captured with event-record nodes around each launch.
-        eng.start(**start)
-        eng.capture(timing=True)
-        eng.start(**start)
-        acc: dict[str, list] = {}
-        attn_bytes = 0
-        for s in range(nsteps):
-            attn_bytes += eng.attention_bytes()
-            eng.step()
-            torch.cuda.synchronize()
-            for k, (ms, nb, n) in eng.kernel_times().items():
-                a = acc.setdefault(k, [0.0, 0, 0])
-                a[0] += ms
-                a[1] += nb
-                a[2] += n
-        acc.setdefault("paged_attention", [0.0, 0, 0])[1] = attn_bytes
-        for k, (ms, nb, n) in acc.items():
-            kernels[k] = dict(launches=n, avg_us=round(ms * 1e3 / max(n, 1), 3),
-                              achieved_GBs=round(nb / (ms * 1e-3) / 1e9, 1) if ms > 0 else None,
-                              bytes_per_launch=nb // max(n, 1))
-        lin = acc["nf4_linear"]
-        achieved = lin[1] / (lin[0] * 1e-3) / 1e9
+        kernels = nf4_kernel_timing(eng, dev)
+        tot_us = sum(k["avg_us"] * k["launches"] for k in kernels.values())
+        tot_b = sum(k["bytes_per_launch"] * k["launches"] for k in kernels.values())
+        n = sum(k["launches"] for k in kernels.values())
+        achieved = tot_b / (tot_us * 1e-6) / 1e9
         roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
                         frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None,
-                        kernel="nf4_linear_mfma (q|k|v, o, gate|up, down)",
-                        avg_launch_us=kernels["nf4_linear"]["avg_us"],
-                        bytes_per_launch=kernels["nf4_linear"]["bytes_per_launch"])
+                        kernel="nf4_part_mfma (q|k|v, o, gate|up, down of one decode step)",
+                        avg_launch_us=round(tot_us / n, 3), bytes_per_launch=tot_b // n)
         log(f"kernel timing: {kernels}")
-        eng.start(**start)
-        eng.capture()  # back to the untimed graph
 
     cpu = None
     if not args.no_cpu_baseline:

@@ -34,6 +34,10 @@ inline hipStream_t as_stream(grpo_stream_t s) { return reinterpret_cast<hipStrea
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+__host__ __device__ inline bool aligned16(const void* ptr) {
+  return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0;
+}
+
 // ---------------------------------------------------------------- bf16 ---
 // float -> bf16 round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
 __device__ __forceinline__ uint16_t f2bf(float f) {
@@ -44,9 +48,12 @@ __device__ __forceinline__ float bf2f(uint16_t b) {
 }
 // Round a float to the nearest bf16 value, returned as float.
 __device__ __forceinline__ float round_bf(float f) { return bf2f(f2bf(f)); }
-// Two floats -> packed bf16 pair (lo in bits 0..15).
+// Two floats -> packed bf16 pair (lo in bits 0..15): one v_cvt_pk_bf16_f32.
+typedef float float2_v __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_v __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
-  return (uint32_t)f2bf(lo) | ((uint32_t)f2bf(hi) << 16);
+  const float2_v v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_v));
 }
 __device__ __forceinline__ float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }

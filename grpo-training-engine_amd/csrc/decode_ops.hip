@@ -2,16 +2,21 @@
 // (src/triton_kernels/paged_kv.py:690-820 and fused_ops.py:34-251):
 // embedding gather, residual add + RMSNorm, RoPE fused with the KV append,
 // SiLU*mul, and greedy argmax.  All bf16 in / bf16 out with the reference's
-// rounding points; memory-bound, one workgroup per row.
+// rounding points; memory-bound, one workgroup per row.  The *_parts forms
+// take the split-K partial sums of the NF4 linear that feeds them and first
+// rebuild its bf16 output (reduction over K slices + LoRA epilogue,
+// linear_parts.hpp), so that linear needs no epilogue launch of its own.
 #include <math.h>
 
-#include "common.hpp"
+#include "linear_parts.hpp"
 
 using namespace grpo;
 
 namespace {
 
 constexpr int ROW_T = 256;
+
+constexpr int PARTS_T = 512;  // consumers of partial sums: more loads in flight per row
 
 __device__ __forceinline__ float block_sum(float v, float* red) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
@@ -159,6 +164,120 @@ __global__ void __launch_bounds__(AMAX_T) argmax_kernel(const uint16_t* __restri
   }
 }
 
+// add_rmsnorm_kernel with x = the finished linear output of row m (a thread
+// finishes four columns at a time).
+__global__ void __launch_bounds__(PARTS_T) add_rmsnorm_parts_kernel(
+    LinParts o, const uint16_t* residual, uint16_t* h_out, const uint16_t* __restrict__ w,
+    uint16_t* __restrict__ y, float eps) {
+  __shared__ float red[PARTS_T / 64];
+  __shared__ float ts[MAXSEG * 16];
+  extern __shared__ float hs[];  // H floats
+  const int m = blockIdx.x, H = o.N;
+  const int64_t row = (int64_t)m * H;
+  lin_load_t(o, m, ts);
+  __syncthreads();
+  float ss = 0.f;
+  for (int i4 = threadIdx.x; i4 < H / 4; i4 += PARTS_T) {
+    float v[4];
+    lin_values4(o, ts, m, 4 * i4, v);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float h = v[c];
+      if (residual) h = round_bf(h + bf2f(residual[row + 4 * i4 + c]));
+      hs[4 * i4 + c] = h;
+      ss += h * h;
+    }
+  }
+  const float total = block_sum(ss, red);
+  const float inv = 1.f / sqrtf(total / (float)H + eps);
+  for (int i = threadIdx.x; i < H; i += PARTS_T) {
+    const float h = hs[i];
+    if (residual && h_out) h_out[row + i] = f2bf(h);
+    y[row + i] = f2bf(round_bf(h * inv) * bf2f(w[i]));
+  }
+}
+
+// rope_append_kernel with qkv = the finished q|k|v output of row b; one
+// workgroup per (row, head): q and k heads rotate column pairs (d, d + D/2),
+// v heads are copied to the cache.
+constexpr int ROPE_T = 64;
+__global__ void __launch_bounds__(ROPE_T) qkv_rope_append_parts_kernel(
+    LinParts o, int Hq, int Hkv, int D, const uint16_t* __restrict__ cos_t,
+    const uint16_t* __restrict__ sin_t, int max_pos, const int32_t* __restrict__ context_lens,
+    uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc,
+    int64_t num_blocks, const int32_t* __restrict__ bt, int64_t bts, int BS, int max_blocks) {
+  __shared__ float ts[MAXSEG * 16];
+  const int b = blockIdx.x, h = blockIdx.y;
+  lin_load_t(o, b, ts);
+  __syncthreads();
+  const int pos = context_lens[b];
+  const int cpos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
+  const int half = D / 2;
+  bool slot_ok = pos >= 0 && pos < max_blocks * BS;
+  int64_t slot_base = 0;
+  if (slot_ok) {
+    const int phys = bt[(int64_t)b * bts + pos / BS];
+    slot_ok = phys >= 0 && phys < num_blocks;
+    slot_base = ((int64_t)phys * Hkv * BS + (pos % BS)) * D;  // + head * BS * D + d
+  }
+  if (h < Hq + Hkv) {
+    uint16_t* dst = nullptr;
+    if (h < Hq)
+      dst = q_out + ((int64_t)b * Hq + h) * D;
+    else if (slot_ok)
+      dst = kc + slot_base + (int64_t)(h - Hq) * BS * D;
+    if (!dst) return;
+    const uint16_t* cr = cos_t + (int64_t)cpos * D;
+    const uint16_t* sr = sin_t + (int64_t)cpos * D;
+    for (int t = threadIdx.x; t < half / 4; t += ROPE_T) {
+      const int d = 4 * t;
+      float x1[4], x2[4];
+      lin_values4(o, ts, b, h * D + d, x1);
+      lin_values4(o, ts, b, h * D + d + half, x2);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int dd = d + c;
+        const float o1 =
+            round_bf(round_bf(x1[c] * bf2f(cr[dd])) + round_bf(-x2[c] * bf2f(sr[dd])));
+        const float o2 = round_bf(round_bf(x2[c] * bf2f(cr[dd + half])) +
+                                  round_bf(x1[c] * bf2f(sr[dd + half])));
+        dst[dd] = f2bf(o1);
+        dst[dd + half] = f2bf(o2);
+      }
+    }
+  } else if (slot_ok) {
+    const int hv = h - Hq - Hkv;
+    uint16_t* dst = vc + slot_base + (int64_t)hv * BS * D;
+    for (int t = threadIdx.x; t < D / 4; t += ROPE_T) {
+      float v[4];
+      lin_values4(o, ts, b, (Hq + Hkv + hv) * D + 4 * t, v);
+#pragma unroll
+      for (int c = 0; c < 4; ++c) dst[4 * t + c] = f2bf(v[c]);
+    }
+  }
+}
+
+// silu_mul_kernel with gate|up = the finished linear output of row m (four
+// columns per thread).
+__global__ void __launch_bounds__(ROW_T) silu_mul_parts_kernel(LinParts o,
+                                                               uint16_t* __restrict__ out,
+                                                               int64_t ldo) {
+  __shared__ float ts[MAXSEG * 16];
+  const int m = blockIdx.y, I = o.N / 2;
+  lin_load_t(o, m, ts);
+  __syncthreads();
+  const int i = (blockIdx.x * ROW_T + threadIdx.x) * 4;
+  if (i >= I) return;
+  float g[4], u[4];
+  lin_values4(o, ts, m, i, g);
+  lin_values4(o, ts, m, I + i, u);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    const float s = round_bf(g[c] * (1.f / (1.f + expf(-g[c]))));
+    out[(int64_t)m * ldo + i + c] = f2bf(s * u[c]);
+  }
+}
+
 }  // namespace
 
 extern "C" int grpo_embedding(const int64_t* ids, const void* table, int64_t V, int H, void* out,
@@ -224,4 +343,51 @@ extern "C" int grpo_argmax_bf16(const void* logits, int64_t ld, int V, int M, in
   argmax_kernel<<<dim3(M), AMAX_T, 0, as_stream(stream)>>>(static_cast<const uint16_t*>(logits),
                                                            ld, V, out);
   return launch_check("argmax");
+}
+
+extern "C" int grpo_add_rmsnorm_parts(const grpo_linear_parts_t* x, const void* residual,
+                                      void* h_out, const void* weight, void* y, float eps,
+                                      grpo_stream_t stream) {
+  LinParts o;
+  if (int rc = make_parts(x, &o)) return rc;
+  if (o.N > 16384) return einval("rmsnorm width must be <= 16384");
+  if (!weight || !y) return einval("null pointer");
+  add_rmsnorm_parts_kernel<<<dim3(o.M), PARTS_T, o.N * sizeof(float), as_stream(stream)>>>(
+      o, static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(h_out),
+      static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(y), eps);
+  return launch_check("add_rmsnorm_parts");
+}
+
+extern "C" int grpo_qkv_rope_append_parts(const grpo_linear_parts_t* qkv, int Hq, int Hkv, int D,
+                                          const void* cos_table, const void* sin_table,
+                                          int max_pos, const int32_t* context_lens, void* q_out,
+                                          void* k_cache, void* v_cache, int64_t num_blocks,
+                                          const int32_t* block_tables, int64_t bt_stride,
+                                          int block_size, int max_blocks, grpo_stream_t stream) {
+  LinParts o;
+  if (int rc = make_parts(qkv, &o)) return rc;
+  if (Hq <= 0 || Hkv <= 0 || D <= 0 || D % 8 || block_size <= 0 || max_pos <= 0)
+    return einval("bad rope/append dimensions (head_dim must be a multiple of 8)");
+  if (o.N != (Hq + 2 * Hkv) * D) return einval("qkv width must be (Hq + 2 Hkv) * D");
+  if (!cos_table || !sin_table || !context_lens || !q_out || !k_cache || !v_cache ||
+      !block_tables)
+    return einval("null pointer");
+  qkv_rope_append_parts_kernel<<<dim3(o.M, Hq + 2 * Hkv), ROPE_T, 0, as_stream(stream)>>>(
+      o, Hq, Hkv, D, static_cast<const uint16_t*>(cos_table),
+      static_cast<const uint16_t*>(sin_table), max_pos, context_lens,
+      static_cast<uint16_t*>(q_out), static_cast<uint16_t*>(k_cache),
+      static_cast<uint16_t*>(v_cache), num_blocks, block_tables, bt_stride, block_size,
+      max_blocks);
+  return launch_check("qkv_rope_append_parts");
+}
+
+extern "C" int grpo_silu_mul_parts(const grpo_linear_parts_t* gate_up, void* out, int64_t ldo,
+                                   grpo_stream_t stream) {
+  LinParts o;
+  if (int rc = make_parts(gate_up, &o)) return rc;
+  if (o.N % 2 || ldo < o.N / 2) return einval("bad silu_mul dimensions");
+  if (!out) return einval("null pointer");
+  silu_mul_parts_kernel<<<dim3((unsigned)cdiv(o.N / 8, ROW_T), o.M), ROW_T, 0,
+                          as_stream(stream)>>>(o, static_cast<uint16_t*>(out), ldo);
+  return launch_check("silu_mul_parts");
 }

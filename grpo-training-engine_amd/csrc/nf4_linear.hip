@@ -1,46 +1,46 @@
-// NF4 dequantization and the fused NF4 + LoRA linear for gfx950.
+// NF4 dequantization and the split-K NF4 + LoRA linear for gfx950.
 //
 // Weight format (bitsandbytes Params4bit, read by the reference in
 // src/triton_kernels/lora_forward.py:171-206): W[N,K] flattened row-major,
 // element e = n*K + k, byte e/2, even e = high nibble; one float32 absmax per
 // `blocksize` flat elements; value = bf16_rne(code[q] * absmax).
 //
-// Fast linear path (M <= 64, K % 256 == 0, K <= 32768, N % 16 == 0,
-// blocksize % 64 == 0, r <= 16): D = A*B on v_mfma_f32_16x16x32_bf16 with
-// A = x (rows m) and B = W^T (columns n).
+// Split-K linear (M <= 64, K % 256 == 0, N % 16 == 0, r <= 16, power-of-two
+// blocksize >= 64): D = A*B on v_mfma_f32_16x16x32_bf16 with A = x (rows m)
+// and B = W^T (columns n).
 //
-//  * Work unit: one wave = one 16-row n-tile x up to 4 k-steps of 256.  Lane
-//    (n = lane%16, group g = lane/16) owns the 64-element chunk
+//  * Work unit: one wave = one 16-row n-tile x one slice of KPW k-steps of
+//    256.  A workgroup is 4 waves = 4 consecutive n-tiles of one slice; the
+//    grid is (tile groups, slices), sized for >= ~2048 waves when the shape
+//    allows it.  Decode shapes have only 96..1120 n-tiles: without the K split
+//    most CUs would idle while a few run the VALU-heavy nibble decode.
+//  * Lane (n = lane%16, group g = lane/16) owns the 64-element chunk
 //    [kstep*256 + 64g, +64) of row n: two 16-byte loads per k-step.  A wave
-//    issues ALL its weight and absmax loads before decoding anything, so the
-//    memory latency is paid once per wave, not once per k-step.
-//  * Decode: per chunk a 16-entry bf16 codebook of bf16(code[j] * absmax) is
-//    built in registers and nibbles are expanded with v_perm byte lookups, so
-//    every product is exactly the reference's bf16(code*absmax) * x.  decode8
-//    emits a dword's eight elements in the order [0,2,4,6,1,3,5,7]; x is
-//    permuted the same way, so MFMA sums matching pairs.
-//  * Split-K stays inside one workgroup: a workgroup has ntw n-tiles x kw
-//    k-groups of waves (<= 16 waves); the kw partial sums are added through
-//    LDS in fixed order, so results are deterministic and no cross-workgroup
-//    synchronisation (device-scope fences) is ever needed.
-//  * x is staged in LDS once per workgroup when it fits (gfx950 allows 160 KiB
-//    per workgroup), otherwise each wave reads its own x fragments from L2.
-//  * LoRA: x A^T is one more 16-column MFMA tile (A is bf16); the tile of
-//    k-group kg is computed by the wave of n-tile kg % ntw, so the extra work
-//    is spread over the workgroup; the epilogue applies the reference's
-//    rounding points (lora_forward.py:243-257).
-#include "common.hpp"
+//    issues all its weight and absmax loads before it decodes anything.
+//  * Decode: per chunk a 16-entry bf16 codebook bf16(code[j] * absmax) is built
+//    in registers and nibbles are expanded with v_perm byte lookups, so every
+//    product is exactly the reference's bf16(code*absmax) * x.  decode8 emits a
+//    dword's eight elements in the order [0,2,4,6,1,3,5,7]; the workgroup
+//    stages its slice of x in LDS permuted the same way.
+//  * x rows >= M: those lanes read row M-1 instead (no masking); the MFMA
+//    output rows they produce are never stored.
+//  * LoRA: x A_s^T is one more 16-column tile per segment (A is bf16: no
+//    decode), computed by extra waves of every slice.
+//  * Output: float32 partial sums part[slice][m][n] and tpart[slice][seg][m][16].
+//    There is no cross-workgroup synchronisation; the sum over slices (fixed
+//    order) and the reference epilogue run in the consuming kernel
+//    (linear_parts.hpp): nf4_finish here, or a fused decode-step op.
+#include "linear_parts.hpp"
 
 using namespace grpo;
 
 namespace {
 
-constexpr int KSTEP = 256;         // k elements per step: 4 lane groups x 64
-constexpr int KPW_MAX = 8;         // k-steps per wave (all loads in flight at once)
-constexpr int MAX_WAVES = 16;      // waves per workgroup (1024 threads)
-constexpr int LDS_BYTES = 163840;  // gfx950: 160 KiB of LDS per workgroup
-constexpr int TARGET_WAVES = 4096; // launch-shape heuristic (4 per SIMD on 256 CUs)
-constexpr int MAXSEG = 4;
+constexpr int KSTEP = 256;          // k elements per step: 4 lane groups x 64
+constexpr int PART_WAVES = 4;       // n-tiles (waves) per workgroup
+constexpr int PART_LDS_MAX = 65536; // bytes of the staged x slice per workgroup
+constexpr int KPW_MAX = 8;          // k-steps per wave (all loads in flight at once)
+int g_target_waves = 2048;          // launch-shape target: 8 waves per CU on 256 CUs
 
 // ------------------------------------------------------------- dequant --
 
@@ -131,319 +131,298 @@ __device__ __forceinline__ uint32_t word(const uint4& v, int i) {
   return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
-// ---------------------------------------------------------- arguments --
+// ---------------------------------------------------- split-K linear --
 
-// Output rows [seg_end[s-1], seg_end[s]) form segment s, with its own bias,
-// LoRA A [r, K] and LoRA B [rows_s, r] (one segment for a plain projection;
-// q|k|v or gate|up stacked into one weight for a grouped launch).
-struct LinearArgs {
+struct PartArgs {
   const uint16_t* x;
   int64_t ldx;
   const uint8_t* w;
   const float* absmax;
   const float* code16;
-  int blocksize;
-  int nseg;
-  int seg_end[MAXSEG];
-  const uint16_t* bias[MAXSEG];
-  const uint16_t* la[MAXSEG];  // lora A [r, K] per segment
-  const uint16_t* lb[MAXSEG];  // lora B [rows_s, r] per segment
-  int r;
-  float scaling;
-  uint16_t* y;
-  int64_t ldy;
-  int M, N, K;
-  int ntw, kw, kpw;  // n-tiles per workgroup, k-groups per workgroup, k-steps per wave
-  int bs_shift;      // log2(blocksize) (power-of-two blocksizes on the fast path)
-  int xstride;       // LDS row stride of staged x (elements)
-  int off_red, off_redt, off_tsum;  // LDS byte offsets of the reduction areas
+  int bs_shift;  // log2(blocksize)
+  const uint16_t* la[MAXSEG];
+  float* part;
+  float* tpart;
+  int M, N, K, NT, ntiles, nseg, r;
+  int xstride;  // LDS row stride of the staged x slice (elements)
 };
 
-struct LinearPlan {
-  int MT, KS, NT, ntw, kw, kpw, grid;
-  bool xlds;
-  int xstride, off_red, off_redt, off_tsum;
-  size_t lds;
-};
-
-__host__ __device__ inline bool aligned16(const void* ptr) {
-  return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0;
-}
-
-bool segments_aligned(const LinearArgs& a, int rows) {
-  for (int s = 0; s + 1 < a.nseg; ++s)
-    if (a.seg_end[s] % rows != 0) return false;
-  return true;
-}
-
-LinearPlan plan_linear(const LinearArgs& a) {
-  LinearPlan p{};
-  p.MT = (a.M + 15) / 16;
-  if (p.MT == 3) p.MT = 4;  // launched as the MT = 4 kernel (sizes below must match)
-  p.KS = a.K / KSTEP;
-  p.NT = a.N / 16;
-  int kw = (TARGET_WAVES + p.NT - 1) / p.NT;
-  if (kw > p.KS) kw = p.KS;
-  if (kw < 1) kw = 1;
-  int kpw = (p.KS + kw - 1) / kw;
-  const int kpw_min = (p.KS + MAX_WAVES - 1) / MAX_WAVES;  // at most 16 k-groups
-  if (kpw < kpw_min) kpw = kpw_min;
-  // LoRA waves also hold a LoRA-A chunk: keep their prefetch depth at <= 2
-  // k-steps so 16-wave workgroups fit in 128 registers per lane.
-  const int kpw_max = a.r > 0 ? 2 : KPW_MAX;
-  if (kpw > kpw_max) kpw = kpw_max;
-  kw = (p.KS + kpw - 1) / kpw;
-  int ntw = MAX_WAVES / kw;
-  ntw = ntw >= 4 ? 4 : (ntw >= 2 ? 2 : 1);
-  while (ntw > 1 && !segments_aligned(a, 16 * ntw)) ntw /= 2;
-  p.kw = kw;
-  p.kpw = kpw;
-  p.ntw = ntw;
-  p.grid = (p.NT + ntw - 1) / ntw;
-  const int red = (kw - 1) * ntw * p.MT * 256 * 4;
-  const int redt = a.r > 0 ? kw * p.MT * 256 * 4 : 0;
-  const int tsum = a.r > 0 ? p.MT * 16 * 16 * 4 : 0;
-  const int xbytes = ((a.M * (a.K + 8) * 2) + 15) & ~15;
-  p.xlds = xbytes + red + redt + tsum <= LDS_BYTES;
-  p.xstride = a.K + 8;
-  const int xb = p.xlds ? xbytes : 0;
-  p.off_red = xb;
-  p.off_redt = xb + red;
-  p.off_tsum = xb + red + redt;
-  p.lds = (size_t)xb + red + redt + tsum;
-  return p;
-}
-
-// x fragment for MFMA: lane (m = mt*16 + lane%16) holds x[m][kcol .. kcol+8) in
-// decode8 order; rows >= M are zero.
-template <bool XLDS>
-__device__ __forceinline__ uint4 xfrag(const LinearArgs& p, const uint16_t* xs, int m, int kcol) {
-  if (m >= p.M) return make_uint4(0, 0, 0, 0);
-  if (XLDS) return *reinterpret_cast<const uint4*>(xs + m * p.xstride + kcol);
-  return deinterleave8(*reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kcol));
-}
-
-// ------------------------------------------------------ fast linear --
-
-template <int MT, bool LORA, bool XLDS, int KPW>
-__global__ void __launch_bounds__(1024) nf4_linear_mfma(LinearArgs p) {
-  extern __shared__ __align__(16) uint8_t smem[];
+template <int MT, int KPW>
+__global__ void __launch_bounds__(256) nf4_part_mfma(PartArgs p) {
+  extern __shared__ __align__(16) uint16_t xs[];  // [M][xstride], decode8 order
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
-  const int nt_local = wave % p.ntw, kg = wave / p.ntw;
-  const int ntile = blockIdx.x * p.ntw + nt_local;
-  const int KS = p.K / KSTEP;
-  const int ks0 = kg * p.kpw;
-  const int nk = max(0, min(p.kpw, KS - ks0));
-  const int n_row = ntile * 16 + ln;
-  const bool row_ok = n_row < p.N;
+  const int tile = blockIdx.x * PART_WAVES + wave;
+  const int slice = blockIdx.y;
+  const int ks0 = slice * KPW;
+  const int nk = min(KPW, p.K / KSTEP - ks0);  // >= 1: the host sizes the grid
+  const int kbase = ks0 * KSTEP;
+  const bool wtile = tile < p.NT;
+  const int n_row = tile * 16 + ln;
 
-  // Segment of this workgroup (the host keeps workgroups inside one segment).
-  const int wg_row0 = blockIdx.x * p.ntw * 16;
-  int seg = 0;
-  while (seg + 1 < p.nseg && wg_row0 >= p.seg_end[seg]) ++seg;
-  const int seg_begin = seg > 0 ? p.seg_end[seg - 1] : 0;
-
-  // The LoRA-A tile of k-group kg is computed once, by the wave of n-tile kg % ntw.
-  const bool do_t = LORA && nt_local == kg % p.ntw;
-  const uint16_t* seg_la = p.la[seg];
-  const bool r_ok = ln < p.r;
-  const bool epi = kg == 0 && row_ok;  // waves of k-group 0 write the outputs
-  const int n_loc = n_row - seg_begin;
-
-  // 1. Every global load of the wave is issued before anything waits on one
-  //    (one memory round trip): weights + absmax of all its k-steps, the
-  //    LoRA-A chunk of its first k-step, the epilogue's bias and LoRA-B row,
-  //    and then the x staging loads.
+  // 1. Weight and absmax loads of every k-step, issued before any use.
   uint4 wv[2 * KPW];
   float av[KPW];
   {
-    const uint8_t* wrow = p.w + (int64_t)(row_ok ? n_row : 0) * (p.K / 2);
+    const uint8_t* wrow = p.w + (int64_t)(wtile ? n_row : 0) * (p.K / 2);
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
-      wv[2 * i] = make_uint4(0, 0, 0, 0);
-      wv[2 * i + 1] = make_uint4(0, 0, 0, 0);
-      av[i] = 0.f;
-      if (i < nk && row_ok) {
-        const int kc = (ks0 + i) * KSTEP + 64 * lg;
+      if (wtile && i < nk) {
+        const int kc = kbase + i * KSTEP + 64 * lg;
         const uint4* wp = reinterpret_cast<const uint4*>(wrow + kc / 2);
         wv[2 * i] = wp[0];
         wv[2 * i + 1] = wp[1];
         av[i] = p.absmax[((int64_t)n_row * p.K + kc) >> p.bs_shift];
+      } else {
+        wv[2 * i] = wv[2 * i + 1] = make_uint4(0, 0, 0, 0);
+        av[i] = 0.f;
       }
-    }
-  }
-  uint4 av4[8];  // LoRA-A chunk of the current k-step
-  if (do_t && nk > 0) {
-    const uint16_t* arow = seg_la + (int64_t)(r_ok ? ln : 0) * p.K + ks0 * KSTEP + 64 * lg;
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      av4[j] = r_ok ? *reinterpret_cast<const uint4*>(arow + 8 * j) : make_uint4(0, 0, 0, 0);
-  }
-  const uint16_t* seg_bias = p.bias[seg];
-  const float bias = epi && seg_bias ? bf2f(seg_bias[n_loc]) : 0.f;
-  float bl[16];
-  if (LORA) {
-    const uint16_t* brow = p.lb[seg] + (int64_t)n_loc * p.r;
-    if (epi && p.r == 16 && aligned16(brow)) {
-      const uint4 b0 = reinterpret_cast<const uint4*>(brow)[0];
-      const uint4 b1 = reinterpret_cast<const uint4*>(brow)[1];
-      const uint32_t bw8[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        bl[2 * q] = bf_lo(bw8[q]);
-        bl[2 * q + 1] = bf_hi(bw8[q]);
-      }
-    } else {
-#pragma unroll
-      for (int q = 0; q < 16; ++q) bl[q] = epi && q < p.r ? bf2f(brow[q]) : 0.f;
     }
   }
 
-  // 2. Stage x (all K) in LDS in decode8 order: loads batched 4 per thread.
-  const uint16_t* xs = reinterpret_cast<const uint16_t*>(smem);
-  if (XLDS) {
-    uint16_t* xw = reinterpret_cast<uint16_t*>(smem);
-    const int chunks = p.K / 8;
+  // 2. Stage x[:, kbase : kbase + nk*256] in LDS, four 16-byte loads per thread in flight.
+  {
+    const int chunks = nk * (KSTEP / 8);
     const int total = p.M * chunks;
-    for (int base = 0; base < total; base += 4 * (int)blockDim.x) {
+    for (int base = 0; base < total; base += 4 * 256) {
       uint4 v[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int i = base + u * (int)blockDim.x + tid;
+        const int i = base + u * 256 + tid;
         if (i < total) {
           const int m = i / chunks, c = i - m * chunks;
-          v[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + c * 8);
+          v[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase + 8 * c);
         }
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int i = base + u * (int)blockDim.x + tid;
+        const int i = base + u * 256 + tid;
         if (i < total) {
           const int m = i / chunks, c = i - m * chunks;
-          *reinterpret_cast<uint4*>(xw + m * p.xstride + c * 8) = deinterleave8(v[u]);
+          *reinterpret_cast<uint4*>(xs + m * p.xstride + 8 * c) = deinterleave8(v[u]);
         }
       }
     }
-    __syncthreads();
   }
-  float code[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
+  __syncthreads();
+  if (tile >= p.ntiles) return;
 
   f32x4_t acc[MT];
-  f32x4_t tacc[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
-    acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    tacc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xrow[mt] = xs + min(mt * 16 + ln, p.M - 1) * p.xstride + 64 * lg;
 
-  // 3. Decode + MFMA, one k-step at a time.
+  if (wtile) {
+    float code[16];
 #pragma unroll
-  for (int i = 0; i < KPW; ++i) {
-    if (i >= nk) break;
-    const int kc = (ks0 + i) * KSTEP + 64 * lg;
-    if (do_t && i > 0) {  // later LoRA-A chunks; latency overlaps the decode below
-      const uint16_t* arow = seg_la + (int64_t)(r_ok ? ln : 0) * p.K + kc;
+    for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        av4[j] = r_ok ? *reinterpret_cast<const uint4*>(arow + 8 * j) : make_uint4(0, 0, 0, 0);
-    }
-    // x fragments of this k-step, read ahead of the decode (one m-tile).
-    uint4 xf[8];
-    constexpr bool PRE = MT == 1 && KPW <= 4;
-    if (PRE) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) xf[j] = xfrag<XLDS>(p, xs, ln, kc + 8 * j);
-    }
-    const Lut t = make_lut(code, av[i]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const uint4 bw = decode8(word(wv[2 * i + (j >> 2)], j & 3), t);
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        acc[mt] = mfma16x16x32(PRE ? xf[j] : xfrag<XLDS>(p, xs, mt * 16 + ln, kc + 8 * j), bw,
-                               acc[mt]);
-    }
-    if (do_t) {
+    for (int i = 0; i < KPW; ++i) {
+      if (i >= nk) break;
+      const Lut t = make_lut(code, av[i]);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        const uint4 bv = deinterleave8(av4[j]);
+        const uint4 bw = decode8(word(wv[2 * i + (j >> 2)], j & 3), t);
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
-          tacc[mt] = mfma16x16x32(PRE ? xf[j] : xfrag<XLDS>(p, xs, mt * 16 + ln, kc + 8 * j),
-                                  bv, tacc[mt]);
+          acc[mt] = mfma16x16x32(
+              *reinterpret_cast<const uint4*>(xrow[mt] + i * KSTEP + 8 * j), bw, acc[mt]);
       }
     }
-  }
-
-  // 4. Reduce the kw k-groups (fixed order) and the LoRA-A partials.
-  float* red = reinterpret_cast<float*>(smem + p.off_red);    // [kw-1][ntw][MT][256]
-  float* redt = reinterpret_cast<float*>(smem + p.off_redt);  // [kw][MT][256]
-  float* tsum = reinterpret_cast<float*>(smem + p.off_tsum);  // [MT*16][16]
-  if (p.kw > 1 && kg > 0) {
+    float* out = p.part + (int64_t)slice * p.M * p.N + n_row;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
-      *reinterpret_cast<float4*>(red + (((kg - 1) * p.ntw + nt_local) * MT + mt) * 256 + lane * 4) =
-          make_float4(acc[mt][0], acc[mt][1], acc[mt][2], acc[mt][3]);
-  }
-  if (do_t) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      *reinterpret_cast<float4*>(redt + (kg * MT + mt) * 256 + lane * 4) =
-          make_float4(tacc[mt][0], tacc[mt][1], tacc[mt][2], tacc[mt][3]);
-  }
-  if (p.kw > 1 || LORA) __syncthreads();
-  if (LORA) {
-    // tacc lane (r = lane%16, g) slot q holds T[m = mt*16 + 4g + q][r]
-    for (int i = tid; i < MT * 256; i += blockDim.x) {
-      const int mt = i >> 8, idx = i & 255, l = idx >> 2, q = idx & 3;
-      float s = 0.f;
-      for (int k = 0; k < p.kw; ++k) s += redt[(k * MT + mt) * 256 + idx];
-      tsum[(mt * 16 + 4 * (l >> 4) + q) * 16 + (l & 15)] = round_bf(s);
-    }
-    __syncthreads();
-  }
-  if (kg != 0 || !row_ok) return;
-  for (int k = 1; k < p.kw; ++k) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const float4 v = *reinterpret_cast<const float4*>(
-          red + (((k - 1) * p.ntw + nt_local) * MT + mt) * 256 + lane * 4);
-      acc[mt][0] += v.x;
-      acc[mt][1] += v.y;
-      acc[mt][2] += v.z;
-      acc[mt][3] += v.w;
-    }
-  }
-
-  // 5. Epilogue: y = bf16(bf16(bf16(acc) + bias) + bf16(bf16(bf16(T) B^T) * bf16(s))).
-  const float sc = round_bf(p.scaling);
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int m = mt * 16 + 4 * lg + q;
-      if (m >= p.M) continue;
-      float v = round_bf(acc[mt][q]);
-      if (seg_bias) v = round_bf(v + bias);
-      if (LORA) {
-        const float* tr = tsum + m * 16;
-        float u = 0.f;
-#pragma unroll
-        for (int rr = 0; rr < 16; ++rr) u += tr[rr] * bl[rr];
-        u = round_bf(round_bf(u) * sc);
-        v = round_bf(v + u);
+      for (int q = 0; q < 4; ++q) {
+        const int m = mt * 16 + 4 * lg + q;
+        if (m < p.M) out[(int64_t)m * p.N] = acc[mt][q];
       }
-      p.y[(int64_t)m * p.ldy + n_row] = f2bf(v);
+  } else {
+    // LoRA-A tile of segment seg: lane n = rank index, A is read as bf16.
+    const int seg = tile - p.NT;
+    const bool r_ok = ln < p.r;
+    const uint16_t* arow = p.la[seg] + (int64_t)(r_ok ? ln : 0) * p.K + kbase + 64 * lg;
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      if (i >= nk) break;
+      uint4 a8[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        a8[j] = r_ok ? *reinterpret_cast<const uint4*>(arow + i * KSTEP + 8 * j)
+                     : make_uint4(0, 0, 0, 0);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint4 bv = deinterleave8(a8[j]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          acc[mt] = mfma16x16x32(
+              *reinterpret_cast<const uint4*>(xrow[mt] + i * KSTEP + 8 * j), bv, acc[mt]);
+      }
     }
+    float* out = p.tpart + ((int64_t)slice * p.nseg + seg) * p.M * 16 + ln;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int m = mt * 16 + 4 * lg + q;
+        if (m < p.M) out[m * 16] = acc[mt][q];
+      }
+  }
+}
+
+// y[m, n] from partial sums: a thread finishes four columns of row m.
+__global__ void __launch_bounds__(256) nf4_finish(LinParts o, uint16_t* __restrict__ y,
+                                                  int64_t ldy) {
+  __shared__ float ts[MAXSEG * 16];
+  const int m = blockIdx.y;
+  lin_load_t(o, m, ts);
+  __syncthreads();
+  const int n = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (n >= o.N) return;
+  float v[4];
+  lin_values4(o, ts, m, n, v);
+  uint16_t* yr = y + (int64_t)m * ldy + n;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) yr[c] = f2bf(v[c]);
+}
+
+struct PartPlan {
+  int MT, NT, ntiles, kpw, S, xstride;
+  size_t lds, part_bytes, tpart_bytes;
+};
+
+bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+// Shape-level support of the split-K path (alignment is checked per call).
+bool part_shape_ok(int M, int N, int K, int r, int nseg, int blocksize, const int* seg_end) {
+  if (!(M >= 1 && M <= 64 && N > 0 && N % 16 == 0 && K > 0 && K % KSTEP == 0)) return false;
+  if (!(r >= 0 && r <= 16 && nseg >= 1 && nseg <= MAXSEG)) return false;
+  if (!pow2(blocksize) || blocksize < 64) return false;
+  for (int s = 0; seg_end && s < nseg; ++s)
+    if (seg_end[s] % 16 != 0) return false;
+  return true;
+}
+
+PartPlan plan_part(int M, int N, int K, int r, int nseg) {
+  PartPlan p{};
+  p.MT = (M + 15) / 16;
+  if (p.MT == 3) p.MT = 4;  // launched as the MT = 4 kernel
+  const int KS = K / KSTEP;
+  p.NT = N / 16;
+  p.ntiles = p.NT + (r > 0 ? nseg : 0);
+  const int s_target = (g_target_waves + p.ntiles - 1) / p.ntiles;
+  int kpw = (KS + s_target - 1) / s_target;
+  static const int choices[] = {1, 2, 3, 4, 6, 8};
+  int pick = KPW_MAX;
+  for (int c : choices)
+    if (c >= kpw) {
+      pick = c;
+      break;
+    }
+  while (pick > 1 && (size_t)M * (pick * KSTEP + 8) * 2 > PART_LDS_MAX) {
+    int lower = 1;
+    for (int c : choices)
+      if (c < pick) lower = c;
+    pick = lower;
+  }
+  p.kpw = pick;
+  p.S = (KS + pick - 1) / pick;
+  p.xstride = pick * KSTEP + 8;
+  p.lds = (size_t)M * p.xstride * 2;
+  p.part_bytes = (size_t)p.S * M * N * 4;
+  p.tpart_bytes = r > 0 ? (size_t)p.S * nseg * M * 16 * 4 : 0;
+  return p;
+}
+
+template <int MT>
+int launch_part(const PartArgs& a, const PartPlan& pl, hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(pl.ntiles, PART_WAVES), (unsigned)pl.S), block(256);
+  switch (pl.kpw) {
+    case 1: nf4_part_mfma<MT, 1><<<grid, block, pl.lds, st>>>(a); break;
+    case 2: nf4_part_mfma<MT, 2><<<grid, block, pl.lds, st>>>(a); break;
+    case 3: nf4_part_mfma<MT, 3><<<grid, block, pl.lds, st>>>(a); break;
+    case 4: nf4_part_mfma<MT, 4><<<grid, block, pl.lds, st>>>(a); break;
+    case 6: nf4_part_mfma<MT, 6><<<grid, block, pl.lds, st>>>(a); break;
+    default: nf4_part_mfma<MT, 8><<<grid, block, pl.lds, st>>>(a); break;
+  }
+  return launch_check("nf4_part_mfma");
+}
+
+int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                 const float* code16, int blocksize, const uint16_t* const* la,
+                 const grpo_linear_parts_t& h, hipStream_t st) {
+  if (!part_shape_ok(h.M, h.N, h.K, h.r, h.nseg, blocksize, h.seg_end)) {
+    set_error("shape not supported by the split-K NF4 linear");
+    return GRPO_EUNSUPPORTED;
+  }
+  const PartPlan pl = plan_part(h.M, h.N, h.K, h.r, h.nseg);
+  if (h.splits != pl.S) return einval("parts.splits differs from grpo_nf4_linear_plan");
+  if (!x || !w || !absmax || !code16 || !h.part) return einval("null pointer");
+  if (h.r > 0 && !h.tpart) return einval("r > 0 needs tpart");
+  if (ldx < h.K || ldx % 8 != 0) return einval("ldx must be >= K and a multiple of 8");
+  if (!aligned16(x) || !aligned16(w)) return einval("x and w must be 16-byte aligned");
+  PartArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.w = w;
+  a.absmax = absmax;
+  a.code16 = code16;
+  a.bs_shift = __builtin_ctz((unsigned)blocksize);
+  for (int s = 0; s < h.nseg; ++s) {
+    a.la[s] = h.r > 0 ? la[s] : nullptr;
+    if (h.r > 0 && (!a.la[s] || !aligned16(a.la[s])))
+      return einval("lora_a must be non-null and 16-byte aligned");
+  }
+  a.part = h.part;
+  a.tpart = h.tpart;
+  a.M = h.M;
+  a.N = h.N;
+  a.K = h.K;
+  a.NT = pl.NT;
+  a.ntiles = pl.ntiles;
+  a.nseg = h.nseg;
+  a.r = h.r;
+  a.xstride = pl.xstride;
+  switch (pl.MT) {
+    case 1: return launch_part<1>(a, pl, st);
+    case 2: return launch_part<2>(a, pl, st);
+    default: return launch_part<4>(a, pl, st);
+  }
+}
+
+int run_finish(const grpo_linear_parts_t* h, uint16_t* y, int64_t ldy, hipStream_t st) {
+  LinParts o;
+  if (int rc = make_parts(h, &o)) return rc;
+  if (!y) return einval("null y");
+  if (ldy < o.N) return einval("ldy smaller than N");
+  nf4_finish<<<dim3((unsigned)cdiv(o.N / 4, 256), (unsigned)o.M), 256, 0, st>>>(o, y, ldy);
+  return launch_check("nf4_finish");
 }
 
 // ---------------------------------------------------- generic linear --
+
+struct GenArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint8_t* w;
+  const float* absmax;
+  const float* code16;
+  int blocksize, nseg, r;
+  int seg_end[MAXSEG];
+  const uint16_t* bias[MAXSEG];
+  const uint16_t* la[MAXSEG];
+  const uint16_t* lb[MAXSEG];
+  float scaling;
+  uint16_t* y;
+  int64_t ldy;
+  int M, N, K;
+};
+
 // Any shape: one thread per output; the reference arithmetic spelled out.
-__global__ void __launch_bounds__(256) nf4_linear_generic(LinearArgs p) {
+__global__ void __launch_bounds__(256) nf4_linear_generic(GenArgs p) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)p.M * p.N) return;
   const int m = (int)(idx / p.N), n = (int)(idx % p.N);
@@ -475,73 +454,53 @@ __global__ void __launch_bounds__(256) nf4_linear_generic(LinearArgs p) {
   p.y[(int64_t)m * p.ldy + n] = f2bf(v);
 }
 
-bool use_fast_linear(const LinearArgs& a) {
-  if ((a.blocksize & (a.blocksize - 1)) != 0) return false;
-  if (!(a.M >= 1 && a.M <= 64 && a.K > 0 && a.K % KSTEP == 0 &&
-        a.K <= MAX_WAVES * (a.r > 0 ? 2 : KPW_MAX) * KSTEP && a.N % 16 == 0 && a.blocksize % 64 == 0 &&
-        a.r <= 16 && a.ldx % 8 == 0 && aligned16(a.x) && aligned16(a.w) &&
-        segments_aligned(a, 16)))
-    return false;
-  for (int s = 0; s < a.nseg; ++s)
-    if (a.r > 0 && !aligned16(a.la[s])) return false;
-  return true;
-}
+// ------------------------------------------------------ linear driver --
 
-// Allows a kernel more than the default dynamic LDS (once per instantiation).
-template <typename K>
-int allow_lds(K kernel) {
-  static int rc = -1;
-  if (rc < 0)
-    rc = hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, LDS_BYTES),
-                   "hipFuncSetAttribute");
-  return rc;
-}
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-template <int MT, bool LORA, int KPW>
-int launch_kpw(LinearArgs& a, const LinearPlan& plan, hipStream_t st) {
-  dim3 grid(plan.grid), block(64 * plan.ntw * plan.kw);
-  if (plan.xlds) {
-    if (int rc = allow_lds(nf4_linear_mfma<MT, LORA, true, KPW>)) return rc;
-    nf4_linear_mfma<MT, LORA, true, KPW><<<grid, block, plan.lds, st>>>(a);
-  } else {
-    if (int rc = allow_lds(nf4_linear_mfma<MT, LORA, false, KPW>)) return rc;
-    nf4_linear_mfma<MT, LORA, false, KPW><<<grid, block, plan.lds, st>>>(a);
-  }
-  return launch_check("nf4_linear_mfma");
-}
-
-template <int MT>
-int launch_fast(LinearArgs& a, const LinearPlan& plan, hipStream_t st) {
-  if (a.r > 0)
-    return plan.kpw <= 1 ? launch_kpw<MT, true, 1>(a, plan, st)
-                         : launch_kpw<MT, true, 2>(a, plan, st);
-  if (plan.kpw <= 1) return launch_kpw<MT, false, 1>(a, plan, st);
-  if (plan.kpw <= 2) return launch_kpw<MT, false, 2>(a, plan, st);
-  if (plan.kpw <= 4) return launch_kpw<MT, false, 4>(a, plan, st);
-  return launch_kpw<MT, false, 8>(a, plan, st);
-}
-
-int run_linear(LinearArgs& a, hipStream_t st) {
-  if (use_fast_linear(a)) {
-    const LinearPlan plan = plan_linear(a);
-    a.ntw = plan.ntw;
-    a.kw = plan.kw;
-    a.kpw = plan.kpw;
-    a.bs_shift = __builtin_ctz((unsigned)a.blocksize);
-    a.xstride = plan.xstride;
-    a.off_red = plan.off_red;
-    a.off_redt = plan.off_redt;
-    a.off_tsum = plan.off_tsum;
-    switch (plan.MT) {
-      case 1: return launch_fast<1>(a, plan, st);
-      case 2: return launch_fast<2>(a, plan, st);
-      default: return launch_fast<4>(a, plan, st);  // M in (32, 64]: one zero m-tile at most
+// One NF4 (+ LoRA) linear into y: split-K partials + finish when the shape,
+// alignment and workspace allow it, the generic kernel otherwise.
+int run_linear(const GenArgs& g, void* workspace, size_t workspace_bytes, hipStream_t st) {
+  bool fast = part_shape_ok(g.M, g.N, g.K, g.r, g.nseg, g.blocksize, g.seg_end) &&
+              g.ldx % 8 == 0 && aligned16(g.x) && aligned16(g.w);
+  for (int s = 0; fast && s < g.nseg && g.r > 0; ++s) fast = aligned16(g.la[s]);
+  if (fast) {
+    const PartPlan pl = plan_part(g.M, g.N, g.K, g.r, g.nseg);
+    const size_t need = align256(pl.part_bytes) + pl.tpart_bytes;
+    if (!workspace || workspace_bytes < need) {
+      set_error("workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+      return GRPO_EWORKSPACE;
     }
+    grpo_linear_parts_t h{};
+    h.part = static_cast<float*>(workspace);
+    h.tpart = g.r > 0 ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
+                                                 align256(pl.part_bytes))
+                      : nullptr;
+    h.splits = pl.S;
+    h.M = g.M;
+    h.N = g.N;
+    h.K = g.K;
+    h.nseg = g.nseg;
+    h.r = g.r;
+    for (int s = 0; s < g.nseg; ++s) {
+      h.seg_end[s] = g.seg_end[s];
+      h.bias[s] = g.bias[s];
+      h.lora_b[s] = g.lb[s];
+    }
+    h.scaling = g.scaling;
+    if (int rc = run_partials(g.x, g.ldx, g.w, g.absmax, g.code16, g.blocksize, g.la, h, st))
+      return rc;
+    return run_finish(&h, g.y, g.ldy, st);
   }
-  const int64_t total = (int64_t)a.M * a.N;
-  nf4_linear_generic<<<dim3((unsigned)cdiv(total, 256)), 256, 0, st>>>(a);
+  const int64_t total = (int64_t)g.M * g.N;
+  nf4_linear_generic<<<dim3((unsigned)cdiv(total, 256)), 256, 0, st>>>(g);
   return launch_check("nf4_linear_generic");
+}
+
+size_t workspace_bytes_for(int M, int N, int K, int r, int nseg, int blocksize) {
+  if (!part_shape_ok(M, N, K, r, nseg, blocksize, nullptr)) return 0;
+  const PartPlan pl = plan_part(M, N, K, r, nseg);
+  return align256(pl.part_bytes) + pl.tpart_bytes;
 }
 
 int check_common(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
@@ -557,6 +516,51 @@ int check_common(const void* x, int64_t ldx, const uint8_t* w, const float* absm
 }
 
 }  // namespace
+
+namespace grpo {
+
+int make_parts(const grpo_linear_parts_t* h, LinParts* d) {
+  if (!h) return einval("null parts descriptor");
+  if (h->splits < 1 || h->M < 1 || h->N < 1 || h->K < 1) return einval("bad parts dimensions");
+  if (h->nseg < 1 || h->nseg > MAXSEG) return einval("nseg must be in [1, 4]");
+  if (h->r < 0 || h->r > 16) return einval("parts: r must be in [0, 16]");
+  if (!h->part || (h->r > 0 && !h->tpart)) return einval("parts: null partial-sum buffer");
+  int prev = 0;
+  for (int s = 0; s < h->nseg; ++s) {
+    if (h->seg_end[s] <= prev) return einval("parts: segment ends must increase");
+    prev = h->seg_end[s];
+    if (h->r > 0 && !h->lora_b[s]) return einval("parts: r > 0 needs lora_b per segment");
+  }
+  if (prev != h->N) return einval("parts: last segment end must equal N");
+  d->part = h->part;
+  d->tpart = h->tpart;
+  d->S = h->splits;
+  d->M = h->M;
+  d->N = h->N;
+  d->K = h->K;
+  d->nseg = h->nseg;
+  d->r = h->r;
+  d->lb_vec = h->r == 16;
+  d->bias_vec = true;
+  for (int s = 0; s < MAXSEG; ++s) {
+    const bool on = s < h->nseg;
+    d->seg_end[s] = on ? h->seg_end[s] : h->N;
+    d->bias[s] = on ? static_cast<const uint16_t*>(h->bias[s]) : nullptr;
+    d->lb[s] = on && h->r > 0 ? static_cast<const uint16_t*>(h->lora_b[s]) : nullptr;
+    if (on && h->r > 0) d->lb_vec = d->lb_vec && aligned16(h->lora_b[s]);
+    if (d->bias[s]) d->bias_vec = d->bias_vec && (reinterpret_cast<uintptr_t>(d->bias[s]) & 7u) == 0;
+  }
+  if (h->N % 16 != 0) return einval("parts: N must be a multiple of 16");
+  for (int s = 0; s < h->nseg; ++s)
+    if (h->seg_end[s] % 16 != 0) return einval("parts: segment ends must be multiples of 16");
+  if ((reinterpret_cast<uintptr_t>(h->part) & 15u) != 0 ||
+      (h->tpart && (reinterpret_cast<uintptr_t>(h->tpart) & 15u) != 0))
+    return einval("parts: partial-sum buffers must be 16-byte aligned");
+  d->scaling = h->scaling;
+  return GRPO_OK;
+}
+
+}  // namespace grpo
 
 extern "C" int grpo_nf4_dequant(const uint8_t* w, const float* absmax, const float* code16,
                                 void* out, int64_t numel, int blocksize, grpo_stream_t stream) {
@@ -580,34 +584,75 @@ extern "C" int grpo_nf4_dequant(const uint8_t* w, const float* absmax, const flo
   return launch_check("nf4_dequant");
 }
 
+extern "C" int grpo_nf4_linear_plan(int M, int N, int K, int r, int nseg, int blocksize,
+                                    int* splits, size_t* part_bytes, size_t* tpart_bytes) {
+  if (!part_shape_ok(M, N, K, r, nseg, blocksize, nullptr)) {
+    set_error("shape not supported by the split-K NF4 linear");
+    return GRPO_EUNSUPPORTED;
+  }
+  const PartPlan pl = plan_part(M, N, K, r, nseg);
+  if (splits) *splits = pl.S;
+  if (part_bytes) *part_bytes = pl.part_bytes;
+  if (tpart_bytes) *tpart_bytes = pl.tpart_bytes;
+  return GRPO_OK;
+}
+
+extern "C" int grpo_nf4_linear_partials(const void* x, int64_t ldx, const uint8_t* w,
+                                        const float* absmax, const float* code16, int blocksize,
+                                        const void* const* lora_a,
+                                        const grpo_linear_parts_t* parts, grpo_stream_t stream) {
+  if (!parts) return einval("null parts descriptor");
+  if (blocksize <= 0) return einval("blocksize must be > 0");
+  LinParts check;
+  if (int rc = make_parts(parts, &check)) return rc;
+  const uint16_t* la[MAXSEG] = {nullptr, nullptr, nullptr, nullptr};
+  if (parts->r > 0) {
+    if (!lora_a) return einval("r > 0 needs lora_a");
+    for (int s = 0; s < parts->nseg; ++s) la[s] = static_cast<const uint16_t*>(lora_a[s]);
+  }
+  return run_partials(static_cast<const uint16_t*>(x), ldx, w, absmax, code16, blocksize, la,
+                      *parts, as_stream(stream));
+}
+
+extern "C" int grpo_nf4_linear_finish(const grpo_linear_parts_t* parts, void* y, int64_t ldy,
+                                      grpo_stream_t stream) {
+  return run_finish(parts, static_cast<uint16_t*>(y), ldy, as_stream(stream));
+}
+
+extern "C" size_t grpo_nf4_lora_linear_workspace_bytes(int M, int N, int K, int r, int nseg,
+                                                       int blocksize) {
+  return workspace_bytes_for(M, N, K, r, nseg, blocksize);
+}
+
 extern "C" int grpo_nf4_lora_linear(const void* x, int64_t ldx, const uint8_t* w,
                                     const float* absmax, const float* code16, int blocksize,
                                     const void* bias, const void* lora_a, const void* lora_b, int r,
                                     float scaling, void* y, int64_t ldy, int M, int N, int K,
+                                    void* workspace, size_t workspace_bytes,
                                     grpo_stream_t stream) {
   if (int rc = check_common(x, ldx, w, absmax, code16, blocksize, r, y, ldy, M, N, K)) return rc;
   if (M == 0 || N == 0) return GRPO_OK;
   if (r > 0 && (!lora_a || !lora_b)) return einval("r > 0 needs lora_a and lora_b");
-  LinearArgs a{};
-  a.x = static_cast<const uint16_t*>(x);
-  a.ldx = ldx;
-  a.w = w;
-  a.absmax = absmax;
-  a.code16 = code16;
-  a.blocksize = blocksize;
-  a.nseg = 1;
-  a.seg_end[0] = N;
-  a.bias[0] = static_cast<const uint16_t*>(bias);
-  a.la[0] = static_cast<const uint16_t*>(lora_a);
-  a.lb[0] = static_cast<const uint16_t*>(lora_b);
-  a.r = r;
-  a.scaling = scaling;
-  a.y = static_cast<uint16_t*>(y);
-  a.ldy = ldy;
-  a.M = M;
-  a.N = N;
-  a.K = K;
-  return run_linear(a, as_stream(stream));
+  GenArgs g{};
+  g.x = static_cast<const uint16_t*>(x);
+  g.ldx = ldx;
+  g.w = w;
+  g.absmax = absmax;
+  g.code16 = code16;
+  g.blocksize = blocksize;
+  g.nseg = 1;
+  g.seg_end[0] = N;
+  g.bias[0] = static_cast<const uint16_t*>(bias);
+  g.la[0] = r > 0 ? static_cast<const uint16_t*>(lora_a) : nullptr;
+  g.lb[0] = r > 0 ? static_cast<const uint16_t*>(lora_b) : nullptr;
+  g.r = r;
+  g.scaling = scaling;
+  g.y = static_cast<uint16_t*>(y);
+  g.ldy = ldy;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  return run_linear(g, workspace, workspace_bytes, as_stream(stream));
 }
 
 extern "C" int grpo_nf4_lora_linear_grouped(const void* x, int64_t ldx, const uint8_t* w,
@@ -615,8 +660,8 @@ extern "C" int grpo_nf4_lora_linear_grouped(const void* x, int64_t ldx, const ui
                                             int blocksize, int nseg, const int* seg_rows,
                                             const void* const* bias, const void* const* lora_a,
                                             const void* const* lora_b, int r, float scaling,
-                                            void* y, int64_t ldy, int M, int K,
-                                            grpo_stream_t stream) {
+                                            void* y, int64_t ldy, int M, int K, void* workspace,
+                                            size_t workspace_bytes, grpo_stream_t stream) {
   if (nseg < 1 || nseg > MAXSEG) return einval("nseg must be in [1, 4]");
   if (!seg_rows) return einval("null seg_rows");
   int N = 0;
@@ -626,31 +671,31 @@ extern "C" int grpo_nf4_lora_linear_grouped(const void* x, int64_t ldx, const ui
   }
   if (int rc = check_common(x, ldx, w, absmax, code16, blocksize, r, y, ldy, M, N, K)) return rc;
   if (M == 0) return GRPO_OK;
-  LinearArgs a{};
-  a.x = static_cast<const uint16_t*>(x);
-  a.ldx = ldx;
-  a.w = w;
-  a.absmax = absmax;
-  a.code16 = code16;
-  a.blocksize = blocksize;
-  a.nseg = nseg;
+  GenArgs g{};
+  g.x = static_cast<const uint16_t*>(x);
+  g.ldx = ldx;
+  g.w = w;
+  g.absmax = absmax;
+  g.code16 = code16;
+  g.blocksize = blocksize;
+  g.nseg = nseg;
   int end = 0;
   for (int s = 0; s < nseg; ++s) {
     end += seg_rows[s];
-    a.seg_end[s] = end;
-    a.bias[s] = bias ? static_cast<const uint16_t*>(bias[s]) : nullptr;
-    a.la[s] = r > 0 && lora_a ? static_cast<const uint16_t*>(lora_a[s]) : nullptr;
-    a.lb[s] = r > 0 && lora_b ? static_cast<const uint16_t*>(lora_b[s]) : nullptr;
-    if (r > 0 && (!a.la[s] || !a.lb[s])) return einval("r > 0 needs lora_a and lora_b per segment");
+    g.seg_end[s] = end;
+    g.bias[s] = bias ? static_cast<const uint16_t*>(bias[s]) : nullptr;
+    g.la[s] = r > 0 && lora_a ? static_cast<const uint16_t*>(lora_a[s]) : nullptr;
+    g.lb[s] = r > 0 && lora_b ? static_cast<const uint16_t*>(lora_b[s]) : nullptr;
+    if (r > 0 && (!g.la[s] || !g.lb[s])) return einval("r > 0 needs lora_a and lora_b per segment");
     if (nseg > 1 && (int64_t)seg_rows[s] * K % blocksize != 0)
       return einval("every segment must hold whole absmax blocks");
   }
-  a.r = r;
-  a.scaling = scaling;
-  a.y = static_cast<uint16_t*>(y);
-  a.ldy = ldy;
-  a.M = M;
-  a.N = N;
-  a.K = K;
-  return run_linear(a, as_stream(stream));
+  g.r = r;
+  g.scaling = scaling;
+  g.y = static_cast<uint16_t*>(y);
+  g.ldy = ldy;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  return run_linear(g, workspace, workspace_bytes, as_stream(stream));
 }

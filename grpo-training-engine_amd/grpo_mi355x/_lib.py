@@ -19,6 +19,30 @@ from ._build import LIB_PATH
 
 _c = ctypes
 _VP, _I64, _I32, _F32, _SZ = _c.c_void_p, _c.c_int64, _c.c_int, _c.c_float, _c.c_size_t
+MAX_SEGMENTS = 4
+
+
+class LinearParts(ctypes.Structure):
+    """``grpo_linear_parts_t``: split-K partial sums of one NF4 (+ LoRA) linear
+    and the epilogue parameters its consumer applies."""
+
+    _fields_ = [
+        ("part", _VP),
+        ("tpart", _VP),
+        ("splits", _I32),
+        ("M", _I32),
+        ("N", _I32),
+        ("K", _I32),
+        ("nseg", _I32),
+        ("r", _I32),
+        ("seg_end", _I32 * MAX_SEGMENTS),
+        ("bias", _VP * MAX_SEGMENTS),
+        ("lora_b", _VP * MAX_SEGMENTS),
+        ("scaling", _F32),
+    ]
+
+
+_PARTS = ctypes.POINTER(LinearParts)
 
 # name -> (restype, argtypes); mirrors include/grpo_hip.h one to one.
 SIGNATURES = {
@@ -26,15 +50,23 @@ SIGNATURES = {
     "grpo_init": (_I32, []),
     "grpo_last_error": (_c.c_char_p, []),
     "grpo_nf4_dequant": (_I32, [_VP, _VP, _VP, _VP, _I64, _I32, _VP]),
+    "grpo_nf4_linear_plan": (
+        _I32,
+        [_I32, _I32, _I32, _I32, _I32, _I32, _c.POINTER(_I32), _c.POINTER(_SZ),
+         _c.POINTER(_SZ)],
+    ),
+    "grpo_nf4_linear_partials": (_I32, [_VP, _I64, _VP, _VP, _VP, _I32, _VP, _PARTS, _VP]),
+    "grpo_nf4_linear_finish": (_I32, [_PARTS, _VP, _I64, _VP]),
+    "grpo_nf4_lora_linear_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
     "grpo_nf4_lora_linear": (
         _I32,
         [_VP, _I64, _VP, _VP, _VP, _I32, _VP, _VP, _VP, _I32, _F32, _VP, _I64, _I32, _I32, _I32,
-         _VP],
+         _VP, _SZ, _VP],
     ),
     "grpo_nf4_lora_linear_grouped": (
         _I32,
         [_VP, _I64, _VP, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _I32, _F32, _VP, _I64, _I32,
-         _I32, _VP],
+         _I32, _VP, _SZ, _VP],
     ),
     "grpo_embedding": (_I32, [_VP, _VP, _I64, _I32, _VP, _I32, _VP]),
     "grpo_add_rmsnorm": (_I32, [_VP, _VP, _VP, _VP, _VP, _I32, _I32, _F32, _VP]),
@@ -44,6 +76,13 @@ SIGNATURES = {
          _I32, _I32, _VP],
     ),
     "grpo_silu_mul": (_I32, [_VP, _I64, _I32, _VP, _I64, _I32, _VP]),
+    "grpo_add_rmsnorm_parts": (_I32, [_PARTS, _VP, _VP, _VP, _VP, _F32, _VP]),
+    "grpo_qkv_rope_append_parts": (
+        _I32,
+        [_PARTS, _I32, _I32, _I32, _VP, _VP, _I32, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I32,
+         _I32, _VP],
+    ),
+    "grpo_silu_mul_parts": (_I32, [_PARTS, _VP, _I64, _VP]),
     "grpo_argmax_bf16": (_I32, [_VP, _I64, _I32, _I32, _VP, _VP]),
     "grpo_paged_kv_append": (
         _I32,

@@ -19,9 +19,9 @@ _workspaces: dict[tuple[str, int], torch.Tensor] = {}
 def workspace(kind: str, nbytes: int, device: torch.device) -> torch.Tensor | None:
     """A zero-initialised uint8 scratch tensor of at least ``nbytes`` per (kind, device).
 
-    Used for the attention's split-context partials (no initialisation
-    needed).  Calls on different streams must not run concurrently with the
-    same workspace.
+    Used for the attention's split-context partials and the NF4 linear's
+    split-K partial sums (no initialisation needed).  Calls on different
+    streams must not run concurrently with the same workspace.
     """
     if nbytes <= 0:
         return None
@@ -82,7 +82,11 @@ def nf4_lora_linear(x2d: torch.Tensor, packed: torch.Tensor, absmax: torch.Tenso
                     code: torch.Tensor, blocksize: int, n: int, bias: torch.Tensor | None = None,
                     lora_a: torch.Tensor | None = None, lora_b: torch.Tensor | None = None,
                     scaling: float = 1.0, out: torch.Tensor | None = None) -> torch.Tensor:
-    """``y[M, N] = W_nf4(x) + bias + B(A(x)) * scaling`` (bf16) -- one fused launch."""
+    """``y[M, N] = W_nf4(x) + bias + B(A(x)) * scaling`` (bf16).
+
+    Split-K partial sums + finish (two launches) on the fast path, one generic
+    launch otherwise.
+    """
     lib = _lib.device_library()
     _need_cuda(x2d, packed, absmax, code, bias, lora_a, lora_b)
     if x2d.ndim != 2:
@@ -109,12 +113,29 @@ def nf4_lora_linear(x2d: torch.Tensor, packed: torch.Tensor, absmax: torch.Tenso
         out = torch.empty((m, n), dtype=torch.bfloat16, device=x2d.device)
     elif out.shape != (m, n) or out.stride(1) != 1 or out.dtype != torch.bfloat16:
         raise ValueError("out must be a bf16 [M, N] tensor with unit column stride.")
+    nbytes = int(lib.grpo_nf4_lora_linear_workspace_bytes(m, n, k, r, 1, int(blocksize)))
+    ws = workspace("nf4_linear", nbytes, x2d.device)
     rc = lib.grpo_nf4_lora_linear(
         x2d.data_ptr(), x2d.stride(0), packed.data_ptr(), absmax.data_ptr(), code.data_ptr(),
         int(blocksize), _lib.ptr(bias), _lib.ptr(lora_a), _lib.ptr(lora_b), r, float(scaling),
-        out.data_ptr(), out.stride(0), m, n, k, _lib.stream_handle(x2d.device))
+        out.data_ptr(), out.stride(0), m, n, k, _lib.ptr(ws), 0 if ws is None else ws.numel(),
+        _lib.stream_handle(x2d.device))
     _lib.check(rc, "grpo_nf4_lora_linear")
     return out
+
+
+def nf4_linear_plan(m: int, n: int, k: int, r: int, nseg: int,
+                    blocksize: int) -> tuple[int, int, int] | None:
+    """(splits, part_bytes, tpart_bytes) of the split-K path, or None if the
+    shape takes the generic kernel."""
+    import ctypes
+
+    s, pb, tb = ctypes.c_int(0), ctypes.c_size_t(0), ctypes.c_size_t(0)
+    rc = _lib.library().grpo_nf4_linear_plan(m, n, k, r, nseg, blocksize, ctypes.byref(s),
+                                             ctypes.byref(pb), ctypes.byref(tb))
+    if rc != 0:
+        return None
+    return s.value, pb.value, tb.value
 
 
 # ----------------------------------------------------------- paged KV ---

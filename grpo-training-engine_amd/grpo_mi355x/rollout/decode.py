@@ -5,13 +5,18 @@ a fixed batch of sequences on a ``PagedKVPool``: the reference's ``_step``
 (``src/triton_kernels/paged_kv.py:690-820``) as a fixed list of C-ABI launches
 per layer --
 
-  add+RMSNorm -> q|k|v NF4+LoRA (one grouped launch) -> RoPE + KV append ->
-  paged GQA attention (bf16 out) -> o_proj NF4+LoRA -> add+RMSNorm ->
-  gate|up NF4 (one launch) -> SiLU*mul -> down NF4
+  add+RMSNorm(down partials) -> q|k|v NF4+LoRA partials (one launch) ->
+  RoPE + KV append (finishes q|k|v) -> paged GQA attention (bf16 out) ->
+  o_proj NF4+LoRA partials -> add+RMSNorm (finishes o_proj) ->
+  gate|up NF4 partials (one launch) -> SiLU*mul (finishes gate|up) ->
+  down NF4 partials
 
--- then the final norm, the bf16 lm_head and greedy argmax.  Lengths, block
-tables and the token buffer live on the device, so the whole step (including
-the per-row bookkeeping) is captured once into a HIP graph and replayed with no
+-- then the final norm, the bf16 lm_head and greedy argmax.  Each NF4 linear
+is a split-K launch that writes float32 partial sums; the op that consumes its
+output sums them and applies the linear's epilogue (bias, LoRA, bf16 rounding)
+itself, so no launch is spent on finishing a linear.  Lengths, block tables
+and the token buffer live on the device, so the whole step (including the
+per-row bookkeeping) is captured once into a HIP graph and replayed with no
 host synchronisation.  Rows stop at EOS or at a per-row length cap; a stopped
 row is masked out of the append (slot -1) and of attention (length 0).
 
@@ -76,27 +81,54 @@ class DecodeEngine:
         # activations
         self.h = torch.zeros(B, H, **bf)
         self.x = torch.zeros(B, H, **bf)
-        self.qkv = torch.zeros(B, self.nqkv, **bf)
         self.q = torch.zeros(B, self.Hq, D, **bf)
         self.attn = torch.zeros(B, self.Hq * D, **bf)
-        self.o = torch.zeros(B, H, **bf)
-        self.gu = torch.zeros(B, 2 * self.I, **bf)
         self.act = torch.zeros(B, self.I, **bf)
-        self.down = torch.zeros(B, H, **bf)
         self.logits = torch.zeros(B, self.V, **bf)
         self.next = torch.zeros(B, dtype=torch.int64, device=dev)
         self._prepare_layers()
         self.graph: Optional[torch.cuda.CUDAGraph] = None
-        # Optional timing: (kind, algorithmic bytes, start event, end event) per
-        # timed launch; events are graph event-record nodes when captured.
-        self.timing = False
-        self._events: list[tuple[str, int, torch.cuda.Event, torch.cuda.Event]] = []
 
     # ------------------------------------------------------------- set-up --
     def _prepare_layers(self):
         cfg, B, dev = self.cfg, self.B, self.device
+        H, I, Hq, D = self.H, self.I, self.Hq, self.D
+        bs = cfg.nf4_blocksize
+        self.bs = bs
         self.layers = []
-        self._keep = []  # ctypes arrays referenced by the launches
+        self._keep = []  # ctypes objects referenced by the launches
+        r = self.model.model.layers[0].self_attn.q_proj.rank
+        shapes = dict(qkv=(self.nqkv, H, r, 3), o=(H, Hq * D, r, 1), gate_up=(2 * I, H, 0, 1),
+                      down=(H, I, 0, 1))
+        plans = {}
+        for kind, (n, k, rr, nseg) in shapes.items():
+            plan = ops.nf4_linear_plan(B, n, k, rr, nseg, bs)
+            if plan is None:
+                raise ValueError(f"{kind} shape [{n}, {k}] (B={B}) is outside the split-K "
+                                 "NF4 path")
+            plans[kind] = plan
+        # One partial-sum buffer serves every linear: each is consumed before
+        # the next linear of the step writes it.
+        self.part = torch.empty(max(p[1] for p in plans.values()) // 4, dtype=torch.float32,
+                                device=dev)
+        self.tpart = torch.empty(max(max(p[2] for p in plans.values()) // 4, 1),
+                                 dtype=torch.float32, device=dev)
+
+        def parts(kind, seg_rows, biases=None, lbs=None, rank=0, scaling=1.0):
+            n, k, _, nseg = shapes[kind]
+            d = _lib.LinearParts()
+            d.part, d.tpart = self.part.data_ptr(), self.tpart.data_ptr()
+            d.splits, d.M, d.N, d.K, d.nseg, d.r = plans[kind][0], B, n, k, nseg, rank
+            end = 0
+            for i, rows in enumerate(seg_rows):
+                end += rows
+                d.seg_end[i] = end
+                d.bias[i] = None if biases is None else biases[i]
+                d.lora_b[i] = None if lbs is None else lbs[i]
+            d.scaling = scaling
+            self._keep.append(d)
+            return ctypes.byref(d)
+
         for layer in self.model.model.layers:
             at, mlp = layer.self_attn, layer.mlp
             qkv = at.qkv
@@ -105,64 +137,76 @@ class DecodeEngine:
                 if p.base_layer.weight.data_ptr() < qkv.packed.data_ptr() or \
                         p.base_layer.weight.data_ptr() >= qkv.packed.data_ptr() + qkv.packed.numel():
                     raise ValueError("q/k/v weights are not views of the stacked buffer")
-            r = projs[0].rank
-            seg_rows = (ctypes.c_int * 3)(*qkv.seg_rows)
-            biases = (ctypes.c_void_p * 3)(*[p.base_layer.bias.data_ptr() for p in projs])
             la = (ctypes.c_void_p * 3)(*[p.lora_A.weight.data_ptr() for p in projs])
-            lb = (ctypes.c_void_p * 3)(*[p.lora_B.weight.data_ptr() for p in projs])
-            self._keep += [seg_rows, biases, la, lb]
             o = at.o_proj
+            o_la = (ctypes.c_void_p * 1)(o.lora_A.weight.data_ptr())
+            self._keep += [la, o_la]
             oq = o.base_layer.weight.quant_state
             dq = mlp.down_proj.weight.quant_state
             self.layers.append(dict(
                 in_norm=layer.input_layernorm.weight, post_norm=layer.post_attention_layernorm.weight,
                 eps=float(layer.input_layernorm.variance_epsilon),
-                qkv=qkv, seg_rows=seg_rows, biases=biases, la=la, lb=lb, r=r,
-                scaling=float(projs[0].scaling),
-                o_w=o.base_layer.weight, o_absmax=oq.absmax, o_code=oq.code,
-                o_la=o.lora_A.weight, o_lb=o.lora_B.weight, o_r=o.rank, o_scaling=float(o.scaling),
-                gu=mlp.gate_up, down_w=mlp.down_proj.weight, down_absmax=dq.absmax,
-                down_code=dq.code))
+                qkv=qkv, la=la,
+                qkv_parts=parts("qkv", qkv.seg_rows,
+                                [p.base_layer.bias.data_ptr() for p in projs],
+                                [p.lora_B.weight.data_ptr() for p in projs], projs[0].rank,
+                                float(projs[0].scaling)),
+                o_w=o.base_layer.weight, o_absmax=oq.absmax, o_code=oq.code, o_la=o_la,
+                o_parts=parts("o", [H], None, [o.lora_B.weight.data_ptr()], o.rank,
+                              float(o.scaling)),
+                gu=mlp.gate_up, gu_parts=parts("gate_up", [2 * I]),
+                down_w=mlp.down_proj.weight, down_absmax=dq.absmax, down_code=dq.code,
+                down_parts=parts("down", [H])))
         self.final_norm = self.model.model.norm.weight
         self.final_eps = float(self.model.model.norm.variance_epsilon)
         self.embed = self.model.model.embed_tokens.weight
         self.lm_head = self.model.lm_head.weight
-        bs = cfg.nf4_blocksize
-        H, I, Hq, D = self.H, self.I, self.Hq, self.D
         # workspaces sized before any graph capture
         self.ws_attn = ops.workspace("paged_attn", max(ops.paged_attention_workspace_bytes(
             B, Hq, self.Hkv, D, self.pool.block_size, self.max_blocks), 1), dev)
-        self.bs = bs
-        r = 16
+        self.plans = plans
         nf4 = lambda n, k: n * k // 2 + n * k // bs * 4
-        self.bytes = dict(
-            qkv=nf4(self.nqkv, H) + 3 * r * H * 2 + self.nqkv * r * 2 + self.nqkv * 2
-            + B * H * 2 + B * self.nqkv * 2,
-            o=nf4(H, Hq * D) + (r * Hq * D + H * r) * 2 + B * Hq * D * 2 + B * H * 2,
-            gate_up=nf4(2 * I, H) + B * H * 2 + B * 2 * I * 2,
-            down=nf4(H, I) + B * I * 2 + B * H * 2,
-        )
+        # Algorithmic HBM bytes of each NF4 partials launch: packed weight +
+        # absmax + LoRA A + x + the float32 partial sums written.
+        self.bytes = {kind: nf4(n, k) + nseg * rr * k * 2 + B * k * 2 + plans[kind][1]
+                      + plans[kind][2] for kind, (n, k, rr, nseg) in shapes.items()}
 
     # -------------------------------------------------------------- launch --
-    def _tick(self, kind: str, nbytes: int):
-        if not self.timing:
-            return None
-        e0 = torch.cuda.Event(enable_timing=True, external=True)
-        e1 = torch.cuda.Event(enable_timing=True, external=True)
-        e0.record()
-        self._events.append((kind, nbytes, e0, e1))
-        return e1
-
-    @staticmethod
-    def _tock(e1):
-        if e1 is not None:
-            e1.record()
-
     def attention_bytes(self) -> int:
         """Algorithmic bytes of one attention launch at the current lengths (host sync)."""
         n = int(self.attn_len.sum().item())
         nblk = int(((self.attn_len + self.pool.block_size - 1) // self.pool.block_size).sum())
         return (n * self.Hkv * self.D * 2 * 2 + self.B * self.Hq * self.D * 2 * 2 + nblk * 4)
+
+    def nf4_launches(self) -> list:
+        """[(kind, algorithmic bytes, launch())] of every NF4 linear of one step,
+        in step order, with the step's own arguments (for kernel timing)."""
+        lib, st = self.lib, _lib.stream_handle(self.device)
+        H, I = self.H, self.I
+        chk = _lib.check
+        out = []
+        for L in self.layers:
+            q = L["qkv"]
+            out.append(("qkv", self.bytes["qkv"], lambda q=q, L=L: chk(
+                lib.grpo_nf4_linear_partials(self.x.data_ptr(), H, q.packed.data_ptr(),
+                                             q.absmax.data_ptr(), q.code.data_ptr(), self.bs,
+                                             L["la"], L["qkv_parts"], st), "qkv")))
+            out.append(("o", self.bytes["o"], lambda L=L: chk(
+                lib.grpo_nf4_linear_partials(self.attn.data_ptr(), self.Hq * self.D,
+                                             L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
+                                             L["o_code"].data_ptr(), self.bs, L["o_la"],
+                                             L["o_parts"], st), "o_proj")))
+            g = L["gu"]
+            out.append(("gate_up", self.bytes["gate_up"], lambda g=g, L=L: chk(
+                lib.grpo_nf4_linear_partials(self.x.data_ptr(), H, g.packed.data_ptr(),
+                                             g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
+                                             None, L["gu_parts"], st), "gate_up")))
+            out.append(("down", self.bytes["down"], lambda L=L: chk(
+                lib.grpo_nf4_linear_partials(self.act.data_ptr(), I, L["down_w"].data_ptr(),
+                                             L["down_absmax"].data_ptr(),
+                                             L["down_code"].data_ptr(), self.bs, None,
+                                             L["down_parts"], st), "down")))
+        return out
 
     def _forward(self):
         """Embedding -> layers -> final norm -> lm_head -> argmax (device only)."""
@@ -173,66 +217,50 @@ class DecodeEngine:
         pool = self.pool
         chk(lib.grpo_embedding(self.tokens.data_ptr(), self.embed.data_ptr(), self.V, H,
                                self.h.data_ptr(), B, st), "embedding")
+        prev = None
         for li, L in enumerate(self.layers):
             kc, vc = pool.layer(li)
-            if li == 0:
+            if prev is None:
                 chk(lib.grpo_add_rmsnorm(self.h.data_ptr(), None, None, L["in_norm"].data_ptr(),
                                          self.x.data_ptr(), B, H, L["eps"], st), "rmsnorm")
             else:
-                chk(lib.grpo_add_rmsnorm(self.down.data_ptr(), self.h.data_ptr(),
-                                         self.h.data_ptr(), L["in_norm"].data_ptr(),
-                                         self.x.data_ptr(), B, H, L["eps"], st), "add_rmsnorm")
+                chk(lib.grpo_add_rmsnorm_parts(prev["down_parts"], self.h.data_ptr(),
+                                               self.h.data_ptr(), L["in_norm"].data_ptr(),
+                                               self.x.data_ptr(), L["eps"], st), "add_rmsnorm")
             q = L["qkv"]
-            e = self._tick("nf4_linear", self.bytes["qkv"])
-            chk(lib.grpo_nf4_lora_linear_grouped(
-                self.x.data_ptr(), H, q.packed.data_ptr(), q.absmax.data_ptr(), q.code.data_ptr(),
-                self.bs, 3, L["seg_rows"], L["biases"], L["la"], L["lb"], L["r"], L["scaling"],
-                self.qkv.data_ptr(), self.nqkv, B, H, st), "qkv")
-            self._tock(e)
-            chk(lib.grpo_rope_append(
-                self.qkv.data_ptr(), self.nqkv, Hq, Hkv, D, self.cos.data_ptr(),
-                self.sin.data_ptr(), self.max_pos, self.append_pos.data_ptr(),
-                self.q.data_ptr(), kc.data_ptr(), vc.data_ptr(), pool.num_blocks,
-                self.block_tables.data_ptr(), self.max_blocks, pool.block_size, self.max_blocks,
-                B, st), "rope_append")
-            e = self._tick("paged_attention", 0)
+            chk(lib.grpo_nf4_linear_partials(self.x.data_ptr(), H, q.packed.data_ptr(),
+                                             q.absmax.data_ptr(), q.code.data_ptr(), self.bs,
+                                             L["la"], L["qkv_parts"], st), "qkv")
+            chk(lib.grpo_qkv_rope_append_parts(
+                L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
+                self.max_pos, self.append_pos.data_ptr(), self.q.data_ptr(), kc.data_ptr(),
+                vc.data_ptr(), pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
+                pool.block_size, self.max_blocks, st), "rope_append")
             chk(lib.grpo_paged_attn_decode(
                 self.q.data_ptr(), Hq * D, D, kc.data_ptr(), vc.data_ptr(), pool.num_blocks,
                 self.block_tables.data_ptr(), self.max_blocks, self.attn_len.data_ptr(),
                 self.attn.data_ptr(), 1, B, Hq, Hkv, D, pool.block_size, self.max_blocks,
                 1.0 / math.sqrt(D), wsa, wsa_n, st), "attention")
-            self._tock(e)
-            e = self._tick("nf4_linear", self.bytes["o"])
-            chk(lib.grpo_nf4_lora_linear(
-                self.attn.data_ptr(), Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
-                L["o_code"].data_ptr(), self.bs, None, L["o_la"].data_ptr(), L["o_lb"].data_ptr(),
-                L["o_r"], L["o_scaling"], self.o.data_ptr(), H, B, H, Hq * D, st),
-                "o_proj")
-            self._tock(e)
-            chk(lib.grpo_add_rmsnorm(self.o.data_ptr(), self.h.data_ptr(), self.h.data_ptr(),
-                                     L["post_norm"].data_ptr(), self.x.data_ptr(), B, H,
-                                     L["eps"], st), "post_norm")
+            chk(lib.grpo_nf4_linear_partials(self.attn.data_ptr(), Hq * D, L["o_w"].data_ptr(),
+                                             L["o_absmax"].data_ptr(), L["o_code"].data_ptr(),
+                                             self.bs, L["o_la"], L["o_parts"], st), "o_proj")
+            chk(lib.grpo_add_rmsnorm_parts(L["o_parts"], self.h.data_ptr(), self.h.data_ptr(),
+                                           L["post_norm"].data_ptr(), self.x.data_ptr(),
+                                           L["eps"], st), "post_norm")
             g = L["gu"]
-            e = self._tick("nf4_linear", self.bytes["gate_up"])
-            chk(lib.grpo_nf4_lora_linear(
-                self.x.data_ptr(), H, g.packed.data_ptr(), g.absmax.data_ptr(),
-                g.code.data_ptr(), self.bs, None, None, None, 0, 1.0, self.gu.data_ptr(), 2 * I,
-                B, 2 * I, H, st), "gate_up")
-            self._tock(e)
-            chk(lib.grpo_silu_mul(self.gu.data_ptr(), 2 * I, I, self.act.data_ptr(), I, B, st),
-                "silu_mul")
-            e = self._tick("nf4_linear", self.bytes["down"])
-            chk(lib.grpo_nf4_lora_linear(
-                self.act.data_ptr(), I, L["down_w"].data_ptr(), L["down_absmax"].data_ptr(),
-                L["down_code"].data_ptr(), self.bs, None, None, None, 0, 1.0,
-                self.down.data_ptr(), H, B, H, I, st), "down")
-            self._tock(e)
-        chk(lib.grpo_add_rmsnorm(self.down.data_ptr(), self.h.data_ptr(), self.h.data_ptr(),
-                                 self.final_norm.data_ptr(), self.x.data_ptr(), B, H,
-                                 self.final_eps, st), "final_norm")
-        e = self._tick("lm_head", self.lm_head.numel() * 2 + self.B * (self.H + self.V) * 2)
+            chk(lib.grpo_nf4_linear_partials(self.x.data_ptr(), H, g.packed.data_ptr(),
+                                             g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
+                                             None, L["gu_parts"], st), "gate_up")
+            chk(lib.grpo_silu_mul_parts(L["gu_parts"], self.act.data_ptr(), I, st), "silu_mul")
+            chk(lib.grpo_nf4_linear_partials(self.act.data_ptr(), I, L["down_w"].data_ptr(),
+                                             L["down_absmax"].data_ptr(),
+                                             L["down_code"].data_ptr(), self.bs, None,
+                                             L["down_parts"], st), "down")
+            prev = L
+        chk(lib.grpo_add_rmsnorm_parts(prev["down_parts"], self.h.data_ptr(), self.h.data_ptr(),
+                                       self.final_norm.data_ptr(), self.x.data_ptr(),
+                                       self.final_eps, st), "final_norm")
         torch.matmul(self.x, self.lm_head.t(), out=self.logits)
-        self._tock(e)
         chk(lib.grpo_argmax_bf16(self.logits.data_ptr(), self.V, self.V, B,
                                  self.next.data_ptr(), st), "argmax")
 
@@ -283,12 +311,8 @@ class DecodeEngine:
             self.generated.fill_(pad_token_id)
         self._masks()
 
-    def capture(self, timing: bool = False):
-        """Record one step into a HIP graph (after two warm-up steps on a side stream).
-
-        ``timing=True`` adds event-record nodes around every NF4-linear, attention
-        and lm_head launch; ``kernel_times()`` reads them after a replay.
-        """
+    def capture(self):
+        """Record one step into a HIP graph (after two warm-up steps on a side stream)."""
         # A warm-up step writes K/V only at each active row's slot pos[b], which
         # is not yet valid cache content: the first real step rewrites it before
         # attention reads it.  Row state is saved and restored around them.
@@ -302,13 +326,8 @@ class DecodeEngine:
                 self._restore(saved)
         torch.cuda.current_stream(self.device).wait_stream(s)
         g = torch.cuda.CUDAGraph()
-        self._events = []
-        self.timing = timing
-        try:
-            with torch.cuda.graph(g, stream=s):
-                self._step()
-        finally:
-            self.timing = False
+        with torch.cuda.graph(g, stream=s):
+            self._step()
         self._restore(saved)
         self.graph = g
 
@@ -318,16 +337,6 @@ class DecodeEngine:
         if self.generated is not None:
             self.generated.fill_(int(self.pad.item()))
         self._masks()
-
-    def kernel_times(self) -> dict:
-        """{kind: (total ms, total algorithmic bytes, launches)} of the last replay."""
-        out: dict[str, list] = {}
-        for kind, nbytes, e0, e1 in self._events:
-            t = out.setdefault(kind, [0.0, 0, 0])
-            t[0] += e0.elapsed_time(e1)
-            t[1] += nbytes
-            t[2] += 1
-        return {k: tuple(v) for k, v in out.items()}
 
     def step(self):
         if self.graph is not None:

@@ -4,10 +4,10 @@
  *
  * Every pointer argument is a DEVICE pointer owned by the caller (torch); the
  * library never allocates device memory.  Scratch space is passed in
- * explicitly ("workspace").  Every entry point is asynchronous on the given
- * stream (a hipStream_t passed as void*; NULL = the default stream) and makes
- * no host synchronisation.  bf16 tensors are passed as void* (2-byte
- * bfloat16 elements).
+ * explicitly ("workspace" arguments, grpo_linear_parts_t buffers).  Every
+ * entry point is asynchronous on the given stream (a hipStream_t passed as
+ * void*; NULL = the default stream) and makes no host synchronisation.  bf16
+ * tensors are passed as void* (2-byte bfloat16 elements).
  *
  * Return codes: 0 = success; < 0 = invalid argument (the Python layer raises
  * ValueError, matching the reference's shape/dtype checks); > 0 = a HIP
@@ -56,6 +56,59 @@ const char* grpo_last_error(void);
 int grpo_nf4_dequant(const uint8_t* w, const float* absmax, const float* code16, void* out,
                      int64_t numel, int blocksize, grpo_stream_t stream);
 
+/* ------------------------------------------------ split-K NF4 linear --
+ * The fast NF4 (+ LoRA) linear runs as a split-K kernel: workgroups own a
+ * 16-row tile of W and one slice of K, so every CU gets work even when N/16
+ * is small, and they write float32 partial sums.  The reduction over slices
+ * (fixed order, deterministic) and the reference's rounding points
+ * (lora_forward.py:243-257) are applied by the kernel that consumes the
+ * result: grpo_nf4_linear_finish for a bf16 output, or the fused consumers of
+ * the decode step (grpo_add_rmsnorm_parts, grpo_qkv_rope_append_parts,
+ * grpo_silu_mul_parts).
+ *
+ * Output rows [seg_end[s-1], seg_end[s]) form segment s (one segment for a
+ * plain projection; q|k|v or gate|up stacked in one weight), each with its own
+ * bias, LoRA A [r, K] and LoRA B [rows_s, r]. */
+#define GRPO_MAX_SEGMENTS 4
+
+typedef struct grpo_linear_parts {
+  float* part;   /* float32 [splits][M][N]: per-slice partial sums of x W^T   */
+  float* tpart;  /* float32 [splits][nseg][M][16]: partial sums of x A_s^T, r > 0 */
+  int splits;    /* slices of K, from grpo_nf4_linear_plan                     */
+  int M, N, K, nseg, r;
+  int seg_end[GRPO_MAX_SEGMENTS];         /* exclusive end row of each segment */
+  const void* bias[GRPO_MAX_SEGMENTS];    /* bf16 [rows_s] or NULL             */
+  const void* lora_b[GRPO_MAX_SEGMENTS];  /* bf16 [rows_s, r] when r > 0       */
+  float scaling;                          /* LoRA alpha / r                    */
+} grpo_linear_parts_t;
+
+/* Launch plan of the split-K path for this shape: number of K slices and the
+ * bytes of part/tpart.  GRPO_OK if the path supports the shape (M <= 64,
+ * K % 256 == 0, N % 16 == 0, segment ends % 16 == 0, r <= 16, power-of-two
+ * blocksize >= 64), GRPO_EUNSUPPORTED otherwise. */
+int grpo_nf4_linear_plan(int M, int N, int K, int r, int nseg, int blocksize, int* splits,
+                         size_t* part_bytes, size_t* tpart_bytes);
+
+/* Partial sums of one NF4 (+ LoRA) linear into parts->part / parts->tpart
+ * (parts->splits must be the planned value).  x: bf16 [M, K], row stride ldx
+ * (a multiple of 8); w/absmax/code16/blocksize: non-nested NF4 weight of
+ * logical shape [N, K]; lora_a: HOST array of nseg device pointers to bf16
+ * [r, K] (ignored when r == 0).  The dequant-matmul half of
+ * _lora_forward_kernel (lora_forward.py:107-241). */
+int grpo_nf4_linear_partials(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                             const float* code16, int blocksize, const void* const* lora_a,
+                             const grpo_linear_parts_t* parts, grpo_stream_t stream);
+
+/* y[M, N] (bf16, row stride ldy) from partial sums: the epilogue of
+ * _lora_forward_kernel, y = bf16(bf16(bf16(acc) + bias) + bf16(bf16(bf16(t) B^T)
+ * * bf16(scaling))) with acc, t summed over slices in slice order. */
+int grpo_nf4_linear_finish(const grpo_linear_parts_t* parts, void* y, int64_t ldy,
+                           grpo_stream_t stream);
+
+/* Workspace bytes of grpo_nf4_lora_linear[_grouped] for this shape (0 when
+ * the shape takes the workspace-free generic kernel). */
+size_t grpo_nf4_lora_linear_workspace_bytes(int M, int N, int K, int r, int nseg, int blocksize);
+
 /* y[M,N] = bf16(bf16(bf16(x W^T) + bias) + bf16(bf16(bf16(x A^T) B^T) * bf16(scaling)))
  * -- the fused NF4 + LoRA forward of FusedLoRAFunction.forward /
  * _lora_forward_kernel (src/triton_kernels/lora_forward.py:653-759, 107-260).
@@ -65,19 +118,22 @@ int grpo_nf4_dequant(const uint8_t* w, const float* absmax, const float* code16,
  *   lora_a  : bf16 [r, K] (row-major), lora_b: bf16 [N, r]; r == 0 drops the
  *             LoRA term (plain NF4 linear; lora_a/lora_b may be NULL)
  *   y       : bf16 [M, N], row stride ldy
- * Needs no workspace: any split of K is reduced inside one workgroup, so the
- * result is deterministic (independent of scheduling). */
+ *   workspace: grpo_nf4_lora_linear_workspace_bytes(...) bytes (no
+ *             initialisation needed); two launches (partials + finish).
+ * Shapes outside the split-K path take a one-thread-per-output kernel with
+ * the same arithmetic and need no workspace. */
 int grpo_nf4_lora_linear(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
                          const float* code16, int blocksize, const void* bias, const void* lora_a,
                          const void* lora_b, int r, float scaling, void* y, int64_t ldy, int M,
-                         int N, int K, grpo_stream_t stream);
+                         int N, int K, void* workspace, size_t workspace_bytes,
+                         grpo_stream_t stream);
 
 /* Grouped form: the output rows are split into nseg (1..4) consecutive
  * segments of seg_rows[s] rows, stacked in ONE NF4 weight (w/absmax cover all
  * rows) and one output y[M, sum(seg_rows)].  Segment s has its own bias[s]
  * (or NULL), lora_a[s] [r, K] and lora_b[s] [seg_rows[s], r]; bias, lora_a
  * and lora_b are HOST arrays of nseg device pointers (bias itself may be
- * NULL).  One launch computes what the reference computes with one
+ * NULL).  One call computes what the reference computes with one
  * lora_fused_forward per projection -- the q/k/v projections of
  * fused_qkv_rope (src/triton_kernels/fused_ops.py:198-219) or gate/up of
  * fused_mlp (fused_ops.py:184-193). */
@@ -86,7 +142,7 @@ int grpo_nf4_lora_linear_grouped(const void* x, int64_t ldx, const uint8_t* w,
                                  const int* seg_rows, const void* const* bias,
                                  const void* const* lora_a, const void* const* lora_b, int r,
                                  float scaling, void* y, int64_t ldy, int M, int K,
-                                 grpo_stream_t stream);
+                                 void* workspace, size_t workspace_bytes, grpo_stream_t stream);
 
 /* ------------------------------------------------------------ paged KV --
  * Cache layout: k_cache, v_cache bf16 [num_blocks, Hkv, block_size, D],
@@ -159,6 +215,29 @@ int grpo_rope_append(const void* qkv, int64_t ld, int Hq, int Hkv, int D, const 
  * (fused_silu_mul, fused_ops.py:79-112, 151-181). */
 int grpo_silu_mul(const void* gate_up, int64_t ld, int N, void* out, int64_t ldo, int M,
                   grpo_stream_t stream);
+
+/* Fused consumers of split-K partial sums (grpo_linear_parts_t above): each
+ * first reconstructs the linear's bf16 output exactly as
+ * grpo_nf4_linear_finish would, then applies its own op. */
+
+/* grpo_add_rmsnorm with x = the finished [M, H = parts->N] linear output
+ * (o_proj or down_proj). */
+int grpo_add_rmsnorm_parts(const grpo_linear_parts_t* x, const void* residual, void* h_out,
+                           const void* weight, void* y, float eps, grpo_stream_t stream);
+
+/* grpo_rope_append with qkv = the finished [B = parts->M, (Hq + 2 Hkv) D]
+ * q|k|v projection output. */
+int grpo_qkv_rope_append_parts(const grpo_linear_parts_t* qkv, int Hq, int Hkv, int D,
+                               const void* cos_table, const void* sin_table, int max_pos,
+                               const int32_t* context_lens, void* q_out, void* k_cache,
+                               void* v_cache, int64_t num_blocks, const int32_t* block_tables,
+                               int64_t bt_stride, int block_size, int max_blocks,
+                               grpo_stream_t stream);
+
+/* grpo_silu_mul with gate_up = the finished [M, 2I] gate|up output
+ * (I = parts->N / 2); out [M, I], row stride ldo. */
+int grpo_silu_mul_parts(const grpo_linear_parts_t* gate_up, void* out, int64_t ldo,
+                        grpo_stream_t stream);
 
 /* out[m] = first index of the maximum of logits[m, :V] (bf16, row stride ld);
  * greedy sampling of _sample_tokens / fused_logits_sampling (paged_kv.py:444-445,

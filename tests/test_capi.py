@@ -49,19 +49,54 @@ def test_version_and_workspace_sizes(lib):
     assert lib.grpo_version() == 100
     assert lib.grpo_paged_attn_workspace_bytes(8, 12, 2, 128, 16, 64) > 0
     assert lib.grpo_paged_attn_workspace_bytes(8, 12, 2, 8, 4, 64) == 0  # generic path
+    # split-K linear: partial sums [splits, M, N] float32 (+ LoRA [splits, nseg, M, 16])
+    assert lib.grpo_nf4_lora_linear_workspace_bytes(8, 1536, 8960, 0, 1, 64) >= 8 * 1536 * 4
+    assert lib.grpo_nf4_lora_linear_workspace_bytes(8, 48, 100, 4, 1, 64) == 0  # generic
+    assert lib.grpo_nf4_lora_linear_workspace_bytes(8, 256, 512, 16, 1, 96) == 0  # blocksize
+
+
+def test_split_k_plan_covers_k_exactly():
+    """Every plan's slices cover K: splits * kpw >= K/256 > (splits - 1) * kpw for a
+    k-steps-per-slice value kpw in {1, 2, 3, 4, 6, 8}; partial bytes match the layout."""
+    from grpo_mi355x.kernels import ops
+
+    for m, n, k, r, nseg in [(8, 2048, 1536, 16, 3), (8, 1536, 1536, 16, 1), (8, 17920, 1536, 0, 1),
+                             (8, 1536, 8960, 0, 1), (64, 512, 3584, 16, 3), (1, 256, 512, 16, 1),
+                             (33, 256, 768, 16, 1), (8, 3584, 18944, 0, 1)]:
+        splits, pb, tb = ops.nf4_linear_plan(m, n, k, r, nseg, 64)
+        ks = k // 256
+        assert any(splits * kpw >= ks > (splits - 1) * kpw for kpw in (1, 2, 3, 4, 6, 8))
+        assert pb == splits * m * n * 4
+        assert tb == (splits * nseg * m * 16 * 4 if r else 0)
+    assert ops.nf4_linear_plan(8, 40, 512, 0, 1, 64) is None  # N % 16
+    assert ops.nf4_linear_plan(65, 256, 512, 0, 1, 64) is None  # M > 64
 
 
 def test_argument_errors_return_negative_codes(lib):
     rc = lib.grpo_nf4_dequant(None, None, None, None, -1, 64, None)
     assert rc < 0 and b"numel" in lib.grpo_last_error()
     rc = lib.grpo_nf4_lora_linear(None, 0, None, None, None, 64, None, None, None, 0, 1.0, None,
-                                  0, 1, 1, 1, None)
+                                  0, 1, 1, 1, None, 0, None)
     assert rc < 0 and b"null" in lib.grpo_last_error()
     rc = lib.grpo_paged_attn_decode(None, 0, 0, None, None, 1, None, 0, None, None, 0, 1, 12, 5,
                                     128, 16, 4, 1.0, None, 0, None)
     assert rc < 0 and b"multiple" in lib.grpo_last_error()
     # empty problems are no-ops
     assert lib.grpo_nf4_dequant(None, None, None, None, 0, 64, None) == 0
+    # split-K descriptors are validated before anything is launched
+    from grpo_mi355x import _lib
+
+    d = _lib.LinearParts()
+    d.splits, d.M, d.N, d.K, d.nseg = 1, 8, 256, 512, 1
+    d.seg_end[0] = 256
+    assert lib.grpo_nf4_linear_finish(d, None, 256, None) < 0  # null part buffer
+    d.part = 16
+    d.seg_end[0] = 128
+    assert lib.grpo_nf4_linear_finish(d, None, 256, None) < 0
+    assert b"segment" in lib.grpo_last_error()
+    d.seg_end[0] = 256
+    d.r = 16
+    assert lib.grpo_add_rmsnorm_parts(d, None, None, None, None, 1e-6, None) < 0  # no tpart
 
 
 def test_check_maps_codes_to_reference_exceptions(lib):
