@@ -55,6 +55,12 @@ def parse():
     ap.add_argument("--layers", type=int, default=28, help="(smaller only for debugging)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-kernel-timing", action="store_true")
+    ap.add_argument("--eager", action="store_true",
+                    help="launch every decode step directly instead of replaying a HIP graph "
+                         "(for profilers that cannot follow graph launches)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first stream a 256 MiB buffer through a copy-like kernel 3 times "
+                         "(scale reference for the HBM FETCH_SIZE/WRITE_SIZE counters)")
     return ap.parse_args()
 
 
@@ -83,24 +89,44 @@ def rollout_bytes(cfg, model, stops, prompt_len, group, block_size=16):
                 steps=steps, weight_per_step=per_step_weights)
 
 
-def nf4_kernel_timing(eng, dev, reps: int = 20) -> dict:
-    """Average launch duration of the NF4 split-K linear, per projection kind.
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "nf4_part_mfma_traffic_cfg3.md")
 
-    The step's own NF4 launches of one kind (one per layer, the decode step's
-    arguments) are captured into a HIP graph; the graph is replayed ``reps``
-    times between two HIP events on the stream it runs on, so the average
-    covers back-to-back launches (including the short gap between graph
-    nodes) with every layer's weights streamed from HBM.
+
+def measured_traffic():
+    """HBM bytes per NF4 launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
+    summary (two counter passes, scaled by a copy kernel of known size), or None."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            for line in fh:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def kernel_timing(eng, dev, reps: int = 20) -> dict:
+    """Average launch duration of every op kind of the decode step.
+
+    The step's own launches of one kind (e.g. the 28 per-layer q|k|v NF4
+    launches, with the step's arguments) are captured into a HIP graph; the
+    graph is replayed ``reps`` times between two HIP events on the stream it
+    runs on, so the average covers back-to-back launches (including the short
+    gap between graph nodes) with every layer's weights streamed from HBM.
     """
     import torch
 
     out = {}
     side = torch.cuda.Stream(device=dev)
-    for kind in ("qkv", "o", "gate_up", "down"):
+    kinds = []
+    for k, _ in eng.launches():
+        if k not in kinds:
+            kinds.append(k)
+    for kind in kinds:
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g, stream=side):
-            launches = [(nb, fn) for k, nb, fn in eng.nf4_launches() if k == kind]
-            for _, fn in launches:
+            fns = [fn for k, fn in eng.launches() if k == kind]
+            for fn in fns:
                 fn()
         g.replay()
         torch.cuda.synchronize()
@@ -111,11 +137,13 @@ def nf4_kernel_timing(eng, dev, reps: int = 20) -> dict:
             g.replay()
         e1.record()
         e1.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (reps * len(launches))
-        nb = launches[0][0]
-        out[kind] = dict(launches=len(launches), avg_us=round(us, 3), bytes_per_launch=nb,
-                         achieved_GBs=round(nb / (us * 1e-6) / 1e9, 1),
-                         splits=eng.plans[kind][0])
+        us = e0.elapsed_time(e1) * 1e3 / (reps * len(fns))
+        rec = dict(launches=len(fns), avg_us=round(us, 3))
+        if kind in eng.NF4_KINDS:
+            nb = eng.bytes[kind]
+            rec.update(bytes_per_launch=nb, achieved_GBs=round(nb / (us * 1e-6) / 1e9, 1),
+                       splits=eng.plans[kind][0])
+        out[kind] = rec
         del g
     return out
 
@@ -199,11 +227,19 @@ def main():
 
     _lib.device_library()
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):  # a float32 multiply kernel: reads 256 MiB, writes 256 MiB
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x (read 268435456 B, write 268435456 B) elementwise kernels")
+        del src, dst
     cfg = Qwen2Config.qwen2_1_5b()
     cfg.num_hidden_layers = args.layers
     G, P, NEW, BS = args.group, args.prompt_len, args.max_new, 16
     rng = np.random.default_rng(args.seed)
-    stops = rng.integers(64, NEW + 1, G).tolist()
+    stops = rng.integers(min(64, NEW), NEW + 1, G).tolist()
     prompt = rng.integers(0, cfg.vocab_size, P).tolist()
     log(f"building model (layers={cfg.num_hidden_layers}) ...")
     t = time.time()
@@ -214,7 +250,8 @@ def main():
     pool = PagedKVPool(cfg.num_hidden_layers, width * (G + 2), cfg.num_key_value_heads,
                        cfg.head_dim, BS, device=dev)
     eng1 = DecodeEngine(model, pool, 1, width)
-    eng1.capture()
+    if not args.eager:
+        eng1.capture()
     t = time.time()
     parent = prefill(eng1, pool, tuple(prompt), width)
     torch.cuda.synchronize()
@@ -229,7 +266,8 @@ def main():
                  positions=torch.full((G,), P - 1, device=dev), block_tables=tables,
                  limits=torch.tensor(stops, device=dev), max_new_tokens=NEW)
     eng.start(**start)
-    eng.capture()
+    if not args.eager:
+        eng.capture()
     nsteps = max(stops)
 
     def rollout():
@@ -249,7 +287,8 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     elapsed = t1 - t0
-    assert torch.equal(eng.generated, gen), "rollouts are not deterministic"
+    if args.warmup > 0:
+        assert torch.equal(eng.generated, gen), "rollouts are not deterministic"
     tokens = sum(stops) * args.steps
     value = tokens / elapsed
     ms_rollout = elapsed / args.steps * 1e3
@@ -261,13 +300,19 @@ def main():
     roofline = None
     kernels = {}
     if not args.no_kernel_timing:
-        kernels = nf4_kernel_timing(eng, dev)
-        tot_us = sum(k["avg_us"] * k["launches"] for k in kernels.values())
-        tot_b = sum(k["bytes_per_launch"] * k["launches"] for k in kernels.values())
-        n = sum(k["launches"] for k in kernels.values())
+        # time the ops at a representative point of the rollout: every row
+        # active, context = prompt + 64 generated tokens
+        eng.start(**start)
+        eng.run(min(64, nsteps))
+        torch.cuda.synchronize()
+        kernels = kernel_timing(eng, dev)
+        nf4 = [kernels[k] for k in eng.NF4_KINDS]
+        tot_us = sum(k["avg_us"] * k["launches"] for k in nf4)
+        tot_b = sum(k["bytes_per_launch"] * k["launches"] for k in nf4)
+        n = sum(k["launches"] for k in nf4)
         achieved = tot_b / (tot_us * 1e-6) / 1e9
         roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                        frac=round(achieved / PEAK_HBM_GBS, 4), traffic=None,
+                        frac=round(achieved / PEAK_HBM_GBS, 4), traffic=measured_traffic(),
                         kernel="nf4_part_mfma (q|k|v, o, gate|up, down of one decode step)",
                         avg_launch_us=round(tot_us / n, 3), bytes_per_launch=tot_b // n)
         log(f"kernel timing: {kernels}")

@@ -150,6 +150,8 @@ struct PartArgs {
 template <int MT, int KPW>
 __global__ void __launch_bounds__(256) nf4_part_mfma(PartArgs p) {
   extern __shared__ __align__(16) uint16_t xs[];  // [M][xstride], decode8 order
+  // Padding workgroups of the XCD-aligned grid have no tile at all.
+  if ((int)blockIdx.x * PART_WAVES >= p.ntiles) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
@@ -337,9 +339,16 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg) {
   return p;
 }
 
+// Workgroups are dispatched round-robin over the 8 XCDs by linear id
+// x + y * gridDim.x.  With gridDim.x a multiple of 8, every K slice of a tile
+// group runs on the same XCD, so the absmax lines that the slices of a row
+// share are fetched from HBM into one L2 only.
+constexpr int NUM_XCD = 8;
+
 template <int MT>
 int launch_part(const PartArgs& a, const PartPlan& pl, hipStream_t st) {
-  const dim3 grid((unsigned)cdiv(pl.ntiles, PART_WAVES), (unsigned)pl.S), block(256);
+  const int groups = (int)cdiv(pl.ntiles, PART_WAVES);
+  const dim3 grid((unsigned)(cdiv(groups, NUM_XCD) * NUM_XCD), (unsigned)pl.S), block(256);
   switch (pl.kpw) {
     case 1: nf4_part_mfma<MT, 1><<<grid, block, pl.lds, st>>>(a); break;
     case 2: nf4_part_mfma<MT, 2><<<grid, block, pl.lds, st>>>(a); break;

@@ -178,91 +178,75 @@ class DecodeEngine:
         nblk = int(((self.attn_len + self.pool.block_size - 1) // self.pool.block_size).sum())
         return (n * self.Hkv * self.D * 2 * 2 + self.B * self.Hq * self.D * 2 * 2 + nblk * 4)
 
-    def nf4_launches(self) -> list:
-        """[(kind, algorithmic bytes, launch())] of every NF4 linear of one step,
-        in step order, with the step's own arguments (for kernel timing)."""
-        lib, st = self.lib, _lib.stream_handle(self.device)
-        H, I = self.H, self.I
-        chk = _lib.check
-        out = []
-        for L in self.layers:
-            q = L["qkv"]
-            out.append(("qkv", self.bytes["qkv"], lambda q=q, L=L: chk(
-                lib.grpo_nf4_linear_partials(self.x.data_ptr(), H, q.packed.data_ptr(),
-                                             q.absmax.data_ptr(), q.code.data_ptr(), self.bs,
-                                             L["la"], L["qkv_parts"], st), "qkv")))
-            out.append(("o", self.bytes["o"], lambda L=L: chk(
-                lib.grpo_nf4_linear_partials(self.attn.data_ptr(), self.Hq * self.D,
-                                             L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
-                                             L["o_code"].data_ptr(), self.bs, L["o_la"],
-                                             L["o_parts"], st), "o_proj")))
-            g = L["gu"]
-            out.append(("gate_up", self.bytes["gate_up"], lambda g=g, L=L: chk(
-                lib.grpo_nf4_linear_partials(self.x.data_ptr(), H, g.packed.data_ptr(),
-                                             g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
-                                             None, L["gu_parts"], st), "gate_up")))
-            out.append(("down", self.bytes["down"], lambda L=L: chk(
-                lib.grpo_nf4_linear_partials(self.act.data_ptr(), I, L["down_w"].data_ptr(),
-                                             L["down_absmax"].data_ptr(),
-                                             L["down_code"].data_ptr(), self.bs, None,
-                                             L["down_parts"], st), "down")))
-        return out
+    NF4_KINDS = ("qkv", "o", "gate_up", "down")
 
-    def _forward(self):
-        """Embedding -> layers -> final norm -> lm_head -> argmax (device only)."""
+    def launches(self) -> list:
+        """[(kind, launch())] of one forward pass, in order, bound to torch's
+        current stream (call inside the stream/graph context they run in)."""
         lib, st = self.lib, _lib.stream_handle(self.device)
         B, H, D, Hq, Hkv, I = self.B, self.H, self.D, self.Hq, self.Hkv, self.I
         chk = _lib.check
         wsa, wsa_n = self.ws_attn.data_ptr(), self.ws_attn.numel()
         pool = self.pool
-        chk(lib.grpo_embedding(self.tokens.data_ptr(), self.embed.data_ptr(), self.V, H,
-                               self.h.data_ptr(), B, st), "embedding")
+        h, x = self.h.data_ptr(), self.x.data_ptr()
+        out = [("embedding", lambda: chk(lib.grpo_embedding(
+            self.tokens.data_ptr(), self.embed.data_ptr(), self.V, H, h, B, st), "embedding"))]
         prev = None
         for li, L in enumerate(self.layers):
-            kc, vc = pool.layer(li)
+            kc, vc = (t.data_ptr() for t in pool.layer(li))
             if prev is None:
-                chk(lib.grpo_add_rmsnorm(self.h.data_ptr(), None, None, L["in_norm"].data_ptr(),
-                                         self.x.data_ptr(), B, H, L["eps"], st), "rmsnorm")
+                out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm(
+                    h, None, None, L["in_norm"].data_ptr(), x, B, H, L["eps"], st), "rmsnorm")))
             else:
-                chk(lib.grpo_add_rmsnorm_parts(prev["down_parts"], self.h.data_ptr(),
-                                               self.h.data_ptr(), L["in_norm"].data_ptr(),
-                                               self.x.data_ptr(), L["eps"], st), "add_rmsnorm")
+                out.append(("rmsnorm", lambda L=L, P=prev: chk(lib.grpo_add_rmsnorm_parts(
+                    P["down_parts"], h, h, L["in_norm"].data_ptr(), x, L["eps"], st),
+                    "add_rmsnorm")))
             q = L["qkv"]
-            chk(lib.grpo_nf4_linear_partials(self.x.data_ptr(), H, q.packed.data_ptr(),
-                                             q.absmax.data_ptr(), q.code.data_ptr(), self.bs,
-                                             L["la"], L["qkv_parts"], st), "qkv")
-            chk(lib.grpo_qkv_rope_append_parts(
-                L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
-                self.max_pos, self.append_pos.data_ptr(), self.q.data_ptr(), kc.data_ptr(),
-                vc.data_ptr(), pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
-                pool.block_size, self.max_blocks, st), "rope_append")
-            chk(lib.grpo_paged_attn_decode(
-                self.q.data_ptr(), Hq * D, D, kc.data_ptr(), vc.data_ptr(), pool.num_blocks,
+            out.append(("qkv", lambda q=q, L=L: chk(lib.grpo_nf4_linear_partials(
+                x, H, q.packed.data_ptr(), q.absmax.data_ptr(), q.code.data_ptr(), self.bs,
+                L["la"], L["qkv_parts"], st), "qkv")))
+            out.append(("rope_append", lambda L=L, kc=kc, vc=vc: chk(
+                lib.grpo_qkv_rope_append_parts(
+                    L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
+                    self.max_pos, self.append_pos.data_ptr(), self.q.data_ptr(), kc, vc,
+                    pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
+                    pool.block_size, self.max_blocks, st), "rope_append")))
+            out.append(("attention", lambda kc=kc, vc=vc: chk(lib.grpo_paged_attn_decode(
+                self.q.data_ptr(), Hq * D, D, kc, vc, pool.num_blocks,
                 self.block_tables.data_ptr(), self.max_blocks, self.attn_len.data_ptr(),
                 self.attn.data_ptr(), 1, B, Hq, Hkv, D, pool.block_size, self.max_blocks,
-                1.0 / math.sqrt(D), wsa, wsa_n, st), "attention")
-            chk(lib.grpo_nf4_linear_partials(self.attn.data_ptr(), Hq * D, L["o_w"].data_ptr(),
-                                             L["o_absmax"].data_ptr(), L["o_code"].data_ptr(),
-                                             self.bs, L["o_la"], L["o_parts"], st), "o_proj")
-            chk(lib.grpo_add_rmsnorm_parts(L["o_parts"], self.h.data_ptr(), self.h.data_ptr(),
-                                           L["post_norm"].data_ptr(), self.x.data_ptr(),
-                                           L["eps"], st), "post_norm")
+                1.0 / math.sqrt(D), wsa, wsa_n, st), "attention")))
+            out.append(("o", lambda L=L: chk(lib.grpo_nf4_linear_partials(
+                self.attn.data_ptr(), Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
+                L["o_code"].data_ptr(), self.bs, L["o_la"], L["o_parts"], st), "o_proj")))
+            out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm_parts(
+                L["o_parts"], h, h, L["post_norm"].data_ptr(), x, L["eps"], st), "post_norm")))
             g = L["gu"]
-            chk(lib.grpo_nf4_linear_partials(self.x.data_ptr(), H, g.packed.data_ptr(),
-                                             g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
-                                             None, L["gu_parts"], st), "gate_up")
-            chk(lib.grpo_silu_mul_parts(L["gu_parts"], self.act.data_ptr(), I, st), "silu_mul")
-            chk(lib.grpo_nf4_linear_partials(self.act.data_ptr(), I, L["down_w"].data_ptr(),
-                                             L["down_absmax"].data_ptr(),
-                                             L["down_code"].data_ptr(), self.bs, None,
-                                             L["down_parts"], st), "down")
+            out.append(("gate_up", lambda g=g, L=L: chk(lib.grpo_nf4_linear_partials(
+                x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
+                None, L["gu_parts"], st), "gate_up")))
+            out.append(("silu_mul", lambda L=L: chk(lib.grpo_silu_mul_parts(
+                L["gu_parts"], self.act.data_ptr(), I, st), "silu_mul")))
+            out.append(("down", lambda L=L: chk(lib.grpo_nf4_linear_partials(
+                self.act.data_ptr(), I, L["down_w"].data_ptr(), L["down_absmax"].data_ptr(),
+                L["down_code"].data_ptr(), self.bs, None, L["down_parts"], st), "down")))
             prev = L
-        chk(lib.grpo_add_rmsnorm_parts(prev["down_parts"], self.h.data_ptr(), self.h.data_ptr(),
-                                       self.final_norm.data_ptr(), self.x.data_ptr(),
-                                       self.final_eps, st), "final_norm")
-        torch.matmul(self.x, self.lm_head.t(), out=self.logits)
-        chk(lib.grpo_argmax_bf16(self.logits.data_ptr(), self.V, self.V, B,
-                                 self.next.data_ptr(), st), "argmax")
+        out.append(("rmsnorm", lambda P=prev: chk(lib.grpo_add_rmsnorm_parts(
+            P["down_parts"], h, h, self.final_norm.data_ptr(), x, self.final_eps, st),
+            "final_norm")))
+        out.append(("lm_head", lambda: torch.matmul(self.x, self.lm_head.t(), out=self.logits)))
+        out.append(("argmax", lambda: chk(lib.grpo_argmax_bf16(
+            self.logits.data_ptr(), self.V, self.V, B, self.next.data_ptr(), st), "argmax")))
+        return out
+
+    def nf4_launches(self) -> list:
+        """[(kind, algorithmic bytes, launch())] of every NF4 linear of one step."""
+        return [(k, self.bytes[k], fn) for k, fn in self.launches() if k in self.NF4_KINDS]
+
+    def _forward(self):
+        """Embedding -> layers -> final norm -> lm_head -> argmax (device only)."""
+        for _, fn in self.launches():
+            fn()
 
     def _advance(self, greedy_tokens: torch.Tensor):
         """Record the step's tokens and move the per-row state (device only)."""
