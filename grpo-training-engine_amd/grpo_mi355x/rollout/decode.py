@@ -37,6 +37,7 @@ import torch
 from .. import _lib
 from ..core.kv_pool import PagedKVPool
 from ..kernels import ops
+from .adapt import decode_model_from
 from .qwen2 import Qwen2ForCausalLM
 
 
@@ -374,6 +375,10 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
                           stop_lengths: Optional[list[int]] = None) -> torch.Tensor:
     """Drop-in for ``paged_kv.paged_kv_decode_model``: returns ``[B, max_new_tokens]``.
 
+    ``model`` is either this package's ``Qwen2ForCausalLM`` or a transformers
+    Qwen2 model in the reference's training layout (NF4 linears, LoRA on
+    q/k/v/o), adapted once by ``rollout.adapt.decode_model_from``.
+
     Rows with identical (unpadded) prompts share one prefill; their full prompt
     blocks are shared through the pool and the partial last block is copied
     per row.  ``stop_lengths`` (an extension) caps each row's generated length.
@@ -386,6 +391,7 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
     if do_sample and temperature > 0.0:
         raise ValueError("sampling (do_sample=True) is not implemented on the HIP decode "
                          "graph yet; use greedy decoding")
+    model = decode_model_from(model)
     cfg = model.config
     dev = input_ids.device
     rows = _prompt_rows(input_ids, attention_mask)

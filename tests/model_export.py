@@ -22,8 +22,10 @@ def _nf4(lin, bias=None, a=None, b=None):
     return d
 
 
-def export(model) -> tuple[dict, dict]:
-    cfg = model.config
+def export(model, cfg=None) -> tuple[dict, dict]:
+    """Oracle weights/config of ``model``; ``cfg`` overrides ``model.config`` (a
+    transformers config lacks the NF4 blocksize and LoRA fields)."""
+    cfg = cfg or model.config
     layers = []
     for L in model.model.layers:
         at, mlp = L.self_attn, L.mlp

@@ -150,3 +150,36 @@ def test_paged_kv_decode_model_greedy_matches_oracle(dev):
     for row, stop in enumerate([8, 3, 5]):
         assert np.array_equal(got[row, :stop], ref[:stop])
         assert np.all(got[row, stop:] == 0)
+
+
+def test_paged_kv_decode_accepts_transformers_model(dev):
+    """The trainer's call (trainer.py:389-400) with a transformers Qwen2 model whose
+    linears are NF4 and whose q/k/v/o carry ManualLoRALayer adapters."""
+    from hf_model import build_hf_nf4_lora_model
+
+    from grpo_mi355x.kernels import paged_kv_decode
+    from grpo_mi355x.rollout.adapt import decode_model_from
+
+    hf = build_hf_nf4_lora_model(seed=4, layers=2, device=dev)
+    w, c = export(hf, decode_model_from(hf).config)
+    oracle = Qwen2DecodeOracle(w, c)
+    g = np.random.default_rng(7)
+    prompt = g.integers(0, 1000, 19).tolist()
+    G, new = 4, 6
+    ids = torch.tensor([prompt] * G, device=dev)
+    got = paged_kv_decode(hf, input_ids=ids, attention_mask=torch.ones_like(ids),
+                          max_new_tokens=new, do_sample=False, pad_token_id=0,
+                          eos_token_id=None, use_cache=True).cpu().numpy()
+    width = 2
+    kcs = [np.zeros((width, 2, 16, 128), np.uint16) for _ in range(2)]
+    vcs = [np.zeros_like(k) for k in kcs]
+    tab = np.arange(width, dtype=np.int32)[None]
+    tok, ref = prompt[0], []
+    for t in range(len(prompt) - 1 + new):
+        tok_in = prompt[t] if t < len(prompt) else tok
+        _, nxt = oracle.step(np.array([tok_in]), kcs, vcs, tab, np.array([t]))
+        if t >= len(prompt) - 1:
+            ref.append(int(nxt[0]))
+            tok = int(nxt[0])
+    for row in range(G):
+        assert np.array_equal(got[row], np.array(ref))
