@@ -165,7 +165,8 @@ __global__ void __launch_bounds__(AMAX_T) argmax_kernel(const uint16_t* __restri
 }
 
 // add_rmsnorm_kernel with x = the finished linear output of row m (a thread
-// finishes four columns at a time).
+// finishes four columns at a time; the first four columns of every thread are
+// fetched before the LoRA-t barrier, so most rows need one memory round trip).
 __global__ void __launch_bounds__(PARTS_T) add_rmsnorm_parts_kernel(
     LinParts o, const uint16_t* residual, uint16_t* h_out, const uint16_t* __restrict__ w,
     uint16_t* __restrict__ y, float eps) {
@@ -174,23 +175,41 @@ __global__ void __launch_bounds__(PARTS_T) add_rmsnorm_parts_kernel(
   extern __shared__ float hs[];  // H floats
   const int m = blockIdx.x, H = o.N;
   const int64_t row = (int64_t)m * H;
+  const int tid = threadIdx.x;
+  const bool first = tid < H / 4;
+  Fetch4<> f;
+  uint2 res0 = make_uint2(0, 0);
+  if (first) {
+    lin_fetch4(o, m, 4 * tid, f);
+    if (residual) res0 = *reinterpret_cast<const uint2*>(residual + row + 4 * tid);
+  }
   lin_load_t(o, m, ts);
   __syncthreads();
   float ss = 0.f;
-  for (int i4 = threadIdx.x; i4 < H / 4; i4 += PARTS_T) {
-    float v[4];
-    lin_values4(o, ts, m, 4 * i4, v);
+  auto take = [&](int i4, const float (&v)[4], uint2 rr) {
+    const float rv[4] = {bf_lo(rr.x), bf_hi(rr.x), bf_lo(rr.y), bf_hi(rr.y)};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float h = v[c];
-      if (residual) h = round_bf(h + bf2f(residual[row + 4 * i4 + c]));
+      if (residual) h = round_bf(h + rv[c]);
       hs[4 * i4 + c] = h;
       ss += h * h;
     }
+  };
+  if (first) {
+    float v[4];
+    lin_finish4(o, ts, f, v);
+    take(tid, v, res0);
+  }
+  for (int i4 = tid + PARTS_T; i4 < H / 4; i4 += PARTS_T) {  // rows wider than 4 * PARTS_T
+    float v[4];
+    lin_values4(o, ts, m, 4 * i4, v);
+    take(i4, v,
+         residual ? *reinterpret_cast<const uint2*>(residual + row + 4 * i4) : make_uint2(0, 0));
   }
   const float total = block_sum(ss, red);
   const float inv = 1.f / sqrtf(total / (float)H + eps);
-  for (int i = threadIdx.x; i < H; i += PARTS_T) {
+  for (int i = tid; i < H; i += PARTS_T) {
     const float h = hs[i];
     if (residual && h_out) h_out[row + i] = f2bf(h);
     y[row + i] = f2bf(round_bf(h * inv) * bf2f(w[i]));
@@ -352,6 +371,8 @@ extern "C" int grpo_add_rmsnorm_parts(const grpo_linear_parts_t* x, const void* 
   if (int rc = make_parts(x, &o)) return rc;
   if (o.N > 16384) return einval("rmsnorm width must be <= 16384");
   if (!weight || !y) return einval("null pointer");
+  if (residual && (reinterpret_cast<uintptr_t>(residual) & 7u) != 0)
+    return einval("residual must be 8-byte aligned");
   add_rmsnorm_parts_kernel<<<dim3(o.M), PARTS_T, o.N * sizeof(float), as_stream(stream)>>>(
       o, static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(h_out),
       static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(y), eps);

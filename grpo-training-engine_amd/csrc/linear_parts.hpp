@@ -12,6 +12,12 @@
 namespace grpo {
 
 constexpr int MAXSEG = GRPO_MAX_SEGMENTS;
+constexpr int ATTN_MAX_SPLITS = 8;  // context splits of the decode attention
+
+// Host: bps (blocks per split) and number of splits of the split decode
+// attention for this shape; GRPO_EUNSUPPORTED outside its fast path.
+int attn_plan_geometry(int B, int Hq, int Hkv, int D, int block_size, int max_blocks, int* bps,
+                       int* splits);
 
 // Device copy of grpo_linear_parts_t (passed to kernels by value).
 struct LinParts {
@@ -35,81 +41,107 @@ __device__ __forceinline__ int lin_seg(const LinParts& o, int n) {
   return s;
 }
 
-// Sum over the S slices of float4 partials at p (slice stride `stride` float4s),
-// in slice order.  Loads are issued 8 slices at a time so that they are in
-// flight together (the kernels consuming partials are latency-bound).
-__device__ __forceinline__ float4 slice_sum4(const float4* p, int S, int64_t stride) {
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int k0 = 0; k0 < S; k0 += 8) {
-    float4 v[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (k0 + j < S) v[j] = p[(k0 + j) * stride];
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-      if (k0 + j < S) {
-        acc.x += v[j].x;
-        acc.y += v[j].y;
-        acc.z += v[j].z;
-        acc.w += v[j].w;
-      }
-  }
-  return acc;
-}
+constexpr int MAX_SLICES = 16;  // K slices of a split-K linear (the plan keeps S <= 16)
 
 // LoRA t of row m rounded to bf16, ts[seg*16 + j], computed by the whole
-// workgroup (the caller synchronises before reading ts).
+// workgroup (the caller synchronises before reading ts).  The S slices of a
+// float4 are loaded together (predicated, no loop), so this is one round trip.
 __device__ __forceinline__ void lin_load_t(const LinParts& o, int m, float* ts) {
   if (o.r <= 0) return;
   for (int i = threadIdx.x; i < o.nseg * 4; i += blockDim.x) {
     const int seg = i >> 2, q = i & 3;
     const float4* p = reinterpret_cast<const float4*>(o.tpart + ((int64_t)seg * o.M + m) * 16) + q;
-    const float4 s = slice_sum4(p, o.S, (int64_t)o.nseg * o.M * 4);
+    const int64_t stride = (int64_t)o.nseg * o.M * 4;
+    float4 v[MAX_SLICES];
+#pragma unroll
+    for (int k = 0; k < MAX_SLICES; ++k)
+      if (k < o.S) v[k] = p[k * stride];
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < MAX_SLICES; ++k)
+      if (k < o.S) {
+        acc.x += v[k].x;
+        acc.y += v[k].y;
+        acc.z += v[k].z;
+        acc.w += v[k].w;
+      }
     float* t = ts + seg * 16 + 4 * q;
-    t[0] = round_bf(s.x);
-    t[1] = round_bf(s.y);
-    t[2] = round_bf(s.z);
-    t[3] = round_bf(s.w);
+    t[0] = round_bf(acc.x);
+    t[1] = round_bf(acc.y);
+    t[2] = round_bf(acc.z);
+    t[3] = round_bf(acc.w);
   }
 }
 
-// Outputs (m, n..n+3) of the linear as the reference's bf16 values (as floats);
-// n % 4 == 0, so the four columns lie in one segment.
-__device__ __forceinline__ void lin_values4(const LinParts& o, const float* ts, int m, int n,
-                                            float v[4]) {
-  const float4 acc = slice_sum4(
-      reinterpret_cast<const float4*>(o.part + (int64_t)m * o.N + n), o.S, (int64_t)o.M * o.N / 4);
+// Inputs of four consecutive outputs (m, n..n+3) of a linear, loaded by
+// lin_fetch4 (all loads issued at once) and combined by lin_finish4, so a
+// consumer can put a barrier (e.g. for lin_load_t) between the two without a
+// second memory round trip.  n % 4 == 0: the four columns lie in one segment.
+template <int MS = MAX_SLICES>
+struct Fetch4 {
+  float4 part[MS];  // requires S <= MS
+  uint4 lb[8];  // LoRA B rows (r == 16, aligned): two 16-byte halves per column
+  uint2 bias;   // four bf16 biases (aligned)
+  int seg, nl;
+};
+
+template <int MS>
+__device__ __forceinline__ void lin_fetch4(const LinParts& o, int m, int n, Fetch4<MS>& f) {
+  const float4* p = reinterpret_cast<const float4*>(o.part + (int64_t)m * o.N + n);
+  const int64_t stride = (int64_t)o.M * o.N / 4;
+#pragma unroll
+  for (int k = 0; k < MS; ++k)
+    if (k < o.S) f.part[k] = p[k * stride];
+  f.seg = lin_seg(o, n);
+  f.nl = n - (f.seg > 0 ? o.seg_end[f.seg - 1] : 0);
+  if (o.bias[f.seg] && o.bias_vec) f.bias = *reinterpret_cast<const uint2*>(o.bias[f.seg] + f.nl);
+  if (o.r > 0 && o.lb_vec) {
+    const uint4* br = reinterpret_cast<const uint4*>(o.lb[f.seg] + (int64_t)f.nl * 16);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f.lb[j] = br[j];
+  }
+}
+
+// The reference's bf16 values (as floats) of the four outputs; ts holds the
+// row's LoRA t (lin_load_t) when r > 0.
+template <int MS>
+__device__ __forceinline__ void lin_finish4(const LinParts& o, const float* ts,
+                                            const Fetch4<MS>& f, float v[4]) {
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int k = 0; k < MS; ++k)
+    if (k < o.S) {
+      acc.x += f.part[k].x;
+      acc.y += f.part[k].y;
+      acc.z += f.part[k].z;
+      acc.w += f.part[k].w;
+    }
   v[0] = round_bf(acc.x);
   v[1] = round_bf(acc.y);
   v[2] = round_bf(acc.z);
   v[3] = round_bf(acc.w);
-  const int seg = lin_seg(o, n);
-  const int nl = n - (seg > 0 ? o.seg_end[seg - 1] : 0);
-  if (o.bias[seg]) {
+  if (o.bias[f.seg]) {
     float b[4];
     if (o.bias_vec) {
-      const uint2 bb = *reinterpret_cast<const uint2*>(o.bias[seg] + nl);
-      b[0] = bf_lo(bb.x);
-      b[1] = bf_hi(bb.x);
-      b[2] = bf_lo(bb.y);
-      b[3] = bf_hi(bb.y);
+      b[0] = bf_lo(f.bias.x);
+      b[1] = bf_hi(f.bias.x);
+      b[2] = bf_lo(f.bias.y);
+      b[3] = bf_hi(f.bias.y);
     } else {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) b[c] = bf2f(o.bias[seg][nl + c]);
+      for (int c = 0; c < 4; ++c) b[c] = bf2f(o.bias[f.seg][f.nl + c]);
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) v[c] = round_bf(v[c] + b[c]);
   }
   if (o.r > 0) {
-    const float* t = ts + seg * 16;
+    const float* t = ts + f.seg * 16;
     const float sc = round_bf(o.scaling);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const uint16_t* br = o.lb[seg] + (int64_t)(nl + c) * o.r;
       float u = 0.f;
       if (o.lb_vec) {
-        const uint4 b0 = reinterpret_cast<const uint4*>(br)[0];
-        const uint4 b1 = reinterpret_cast<const uint4*>(br)[1];
+        const uint4 b0 = f.lb[2 * c], b1 = f.lb[2 * c + 1];
         const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
@@ -117,12 +149,21 @@ __device__ __forceinline__ void lin_values4(const LinParts& o, const float* ts, 
           u += t[2 * j + 1] * bf_hi(bw[j]);
         }
       } else {
+        const uint16_t* br = o.lb[f.seg] + (int64_t)(f.nl + c) * o.r;
         for (int j = 0; j < o.r; ++j) u += t[j] * bf2f(br[j]);
       }
       u = round_bf(round_bf(u) * sc);
       v[c] = round_bf(v[c] + u);
     }
   }
+}
+
+// Outputs (m, n..n+3) as the reference's bf16 values (fetch + finish).
+__device__ __forceinline__ void lin_values4(const LinParts& o, const float* ts, int m, int n,
+                                            float v[4]) {
+  Fetch4<> f;
+  lin_fetch4(o, m, n, f);
+  lin_finish4(o, ts, f, v);
 }
 
 }  // namespace grpo

@@ -145,9 +145,64 @@ struct PartArgs {
   float* tpart;
   int M, N, K, NT, ntiles, nseg, r;
   int xstride;  // LDS row stride of the staged x slice (elements)
+  // x = decode attention output given as split partials (o_proj of the decode step)
+  const float* att_o;    // [M][Hq][S][128] unnormalised O
+  const float* att_ml;   // [M][Hq][S][2]: max (log2 domain), sum
+  const int32_t* att_len;
+  int att_S, att_bps, att_Hq, att_cap;
 };
 
-template <int MT, int KPW>
+// Eight consecutive columns k..k+7 (one head, d0 = k % 128) of row m of the
+// attention output, merged over its context splits:
+// O = sum_s 2^(m_s - M) O_s / max(sum_s 2^(m_s - M) l_s, 1e-6), rounded to bf16
+// (the reference's float32 attention output cast to the model dtype).
+__device__ __forceinline__ uint4 attn_chunk(const PartArgs& p, int m, int k) {
+  const int hq = k >> 7, d0 = k & 127;
+  int ctx = p.att_len[m];
+  ctx = ctx < 0 ? 0 : (ctx > p.att_cap ? p.att_cap : ctx);
+  const int nblk = (ctx + 15) / 16;
+  const int ns = nblk > 0 ? (nblk + p.att_bps - 1) / p.att_bps : 1;
+  const int64_t base = ((int64_t)m * p.att_Hq + hq) * p.att_S;
+  float ms[ATTN_MAX_SPLITS], ls[ATTN_MAX_SPLITS];
+  float4 o0[ATTN_MAX_SPLITS], o1[ATTN_MAX_SPLITS];
+#pragma unroll
+  for (int s = 0; s < ATTN_MAX_SPLITS; ++s) {
+    if (s < ns) {
+      const float2 ml = *reinterpret_cast<const float2*>(p.att_ml + (base + s) * 2);
+      ms[s] = ml.x;
+      ls[s] = ml.y;
+      const float4* op = reinterpret_cast<const float4*>(p.att_o + (base + s) * 128 + d0);
+      o0[s] = op[0];
+      o1[s] = op[1];
+    }
+  }
+  float M = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < ATTN_MAX_SPLITS; ++s)
+    if (s < ns) M = fmaxf(M, ms[s]);
+  float L = 0.f, O[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (M != -INFINITY) {
+#pragma unroll
+    for (int s = 0; s < ATTN_MAX_SPLITS; ++s)
+      if (s < ns) {
+        const float f = exp2f(ms[s] - M);
+        L += f * ls[s];
+        O[0] += f * o0[s].x;
+        O[1] += f * o0[s].y;
+        O[2] += f * o0[s].z;
+        O[3] += f * o0[s].w;
+        O[4] += f * o1[s].x;
+        O[5] += f * o1[s].y;
+        O[6] += f * o1[s].z;
+        O[7] += f * o1[s].w;
+      }
+  }
+  const float den = fmaxf(L, 1e-6f);
+  return make_uint4(pack_bf2(O[0] / den, O[1] / den), pack_bf2(O[2] / den, O[3] / den),
+                    pack_bf2(O[4] / den, O[5] / den), pack_bf2(O[6] / den, O[7] / den));
+}
+
+template <int MT, int KPW, bool XATT>
 __global__ void __launch_bounds__(256) nf4_part_mfma(PartArgs p) {
   extern __shared__ __align__(16) uint16_t xs[];  // [M][xstride], decode8 order
   // Padding workgroups of the XCD-aligned grid have no tile at all.
@@ -194,7 +249,8 @@ __global__ void __launch_bounds__(256) nf4_part_mfma(PartArgs p) {
         const int i = base + u * 256 + tid;
         if (i < total) {
           const int m = i / chunks, c = i - m * chunks;
-          v[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase + 8 * c);
+          v[u] = XATT ? attn_chunk(p, m, kbase + 8 * c)
+                      : *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase + 8 * c);
         }
       }
 #pragma unroll
@@ -301,6 +357,7 @@ bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 // Shape-level support of the split-K path (alignment is checked per call).
 bool part_shape_ok(int M, int N, int K, int r, int nseg, int blocksize, const int* seg_end) {
   if (!(M >= 1 && M <= 64 && N > 0 && N % 16 == 0 && K > 0 && K % KSTEP == 0)) return false;
+  if (K > MAX_SLICES * KPW_MAX * KSTEP) return false;  // K <= 32768
   if (!(r >= 0 && r <= 16 && nseg >= 1 && nseg <= MAXSEG)) return false;
   if (!pow2(blocksize) || blocksize < 64) return false;
   for (int s = 0; seg_end && s < nseg; ++s)
@@ -330,6 +387,14 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg) {
       if (c < pick) lower = c;
     pick = lower;
   }
+  // consumers read at most MAX_SLICES partial sums per output
+  while ((KS + pick - 1) / pick > MAX_SLICES && pick < KPW_MAX) {
+    for (int c : choices)
+      if (c > pick) {
+        pick = c;
+        break;
+      }
+  }
   p.kpw = pick;
   p.S = (KS + pick - 1) / pick;
   p.xstride = pick * KSTEP + 8;
@@ -345,34 +410,42 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg) {
 // share are fetched from HBM into one L2 only.
 constexpr int NUM_XCD = 8;
 
-template <int MT>
+template <int MT, bool XATT>
 int launch_part(const PartArgs& a, const PartPlan& pl, hipStream_t st) {
   const int groups = (int)cdiv(pl.ntiles, PART_WAVES);
   const dim3 grid((unsigned)(cdiv(groups, NUM_XCD) * NUM_XCD), (unsigned)pl.S), block(256);
   switch (pl.kpw) {
-    case 1: nf4_part_mfma<MT, 1><<<grid, block, pl.lds, st>>>(a); break;
-    case 2: nf4_part_mfma<MT, 2><<<grid, block, pl.lds, st>>>(a); break;
-    case 3: nf4_part_mfma<MT, 3><<<grid, block, pl.lds, st>>>(a); break;
-    case 4: nf4_part_mfma<MT, 4><<<grid, block, pl.lds, st>>>(a); break;
-    case 6: nf4_part_mfma<MT, 6><<<grid, block, pl.lds, st>>>(a); break;
-    default: nf4_part_mfma<MT, 8><<<grid, block, pl.lds, st>>>(a); break;
+    case 1: nf4_part_mfma<MT, 1, XATT><<<grid, block, pl.lds, st>>>(a); break;
+    case 2: nf4_part_mfma<MT, 2, XATT><<<grid, block, pl.lds, st>>>(a); break;
+    case 3: nf4_part_mfma<MT, 3, XATT><<<grid, block, pl.lds, st>>>(a); break;
+    case 4: nf4_part_mfma<MT, 4, XATT><<<grid, block, pl.lds, st>>>(a); break;
+    case 6: nf4_part_mfma<MT, 6, XATT><<<grid, block, pl.lds, st>>>(a); break;
+    default: nf4_part_mfma<MT, 8, XATT><<<grid, block, pl.lds, st>>>(a); break;
   }
   return launch_check("nf4_part_mfma");
 }
 
+// Attention-output source of x (o_proj of the decode step), or all-null.
+struct AttnSource {
+  const float* o = nullptr;
+  const float* ml = nullptr;
+  const int32_t* len = nullptr;
+  int S = 0, bps = 0, Hq = 0, cap = 0;
+};
+
 int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* absmax,
                  const float* code16, int blocksize, const uint16_t* const* la,
-                 const grpo_linear_parts_t& h, hipStream_t st) {
+                 const grpo_linear_parts_t& h, hipStream_t st, const AttnSource* att = nullptr) {
   if (!part_shape_ok(h.M, h.N, h.K, h.r, h.nseg, blocksize, h.seg_end)) {
     set_error("shape not supported by the split-K NF4 linear");
     return GRPO_EUNSUPPORTED;
   }
   const PartPlan pl = plan_part(h.M, h.N, h.K, h.r, h.nseg);
   if (h.splits != pl.S) return einval("parts.splits differs from grpo_nf4_linear_plan");
-  if (!x || !w || !absmax || !code16 || !h.part) return einval("null pointer");
+  if ((!x && !att) || !w || !absmax || !code16 || !h.part) return einval("null pointer");
   if (h.r > 0 && !h.tpart) return einval("r > 0 needs tpart");
-  if (ldx < h.K || ldx % 8 != 0) return einval("ldx must be >= K and a multiple of 8");
-  if (!aligned16(x) || !aligned16(w)) return einval("x and w must be 16-byte aligned");
+  if (!att && (ldx < h.K || ldx % 8 != 0)) return einval("ldx must be >= K and a multiple of 8");
+  if ((!att && !aligned16(x)) || !aligned16(w)) return einval("x and w must be 16-byte aligned");
   PartArgs a{};
   a.x = x;
   a.ldx = ldx;
@@ -395,10 +468,24 @@ int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* 
   a.nseg = h.nseg;
   a.r = h.r;
   a.xstride = pl.xstride;
+  if (att) {
+    a.att_o = att->o;
+    a.att_ml = att->ml;
+    a.att_len = att->len;
+    a.att_S = att->S;
+    a.att_bps = att->bps;
+    a.att_Hq = att->Hq;
+    a.att_cap = att->cap;
+    switch (pl.MT) {
+      case 1: return launch_part<1, true>(a, pl, st);
+      case 2: return launch_part<2, true>(a, pl, st);
+      default: return launch_part<4, true>(a, pl, st);
+    }
+  }
   switch (pl.MT) {
-    case 1: return launch_part<1>(a, pl, st);
-    case 2: return launch_part<2>(a, pl, st);
-    default: return launch_part<4>(a, pl, st);
+    case 1: return launch_part<1, false>(a, pl, st);
+    case 2: return launch_part<2, false>(a, pl, st);
+    default: return launch_part<4, false>(a, pl, st);
   }
 }
 
@@ -531,6 +618,7 @@ namespace grpo {
 int make_parts(const grpo_linear_parts_t* h, LinParts* d) {
   if (!h) return einval("null parts descriptor");
   if (h->splits < 1 || h->M < 1 || h->N < 1 || h->K < 1) return einval("bad parts dimensions");
+  if (h->splits > MAX_SLICES) return einval("parts: at most 16 K slices");
   if (h->nseg < 1 || h->nseg > MAXSEG) return einval("nseg must be in [1, 4]");
   if (h->r < 0 || h->r > 16) return einval("parts: r must be in [0, 16]");
   if (!h->part || (h->r > 0 && !h->tpart)) return einval("parts: null partial-sum buffer");
@@ -707,4 +795,40 @@ extern "C" int grpo_nf4_lora_linear_grouped(const void* x, int64_t ldx, const ui
   g.N = N;
   g.K = K;
   return run_linear(g, workspace, workspace_bytes, as_stream(stream));
+}
+
+extern "C" int grpo_nf4_linear_partials_attn(const void* attn_workspace,
+                                             const int32_t* context_lens, int Hq, int Hkv,
+                                             int D, int block_size, int max_blocks,
+                                             const uint8_t* w, const float* absmax,
+                                             const float* code16, int blocksize,
+                                             const void* const* lora_a,
+                                             const grpo_linear_parts_t* parts,
+                                             grpo_stream_t stream) {
+  if (!parts) return einval("null parts descriptor");
+  if (blocksize <= 0) return einval("blocksize must be > 0");
+  LinParts check;
+  if (int rc = make_parts(parts, &check)) return rc;
+  if (!attn_workspace || !context_lens) return einval("null pointer");
+  if (!aligned16(attn_workspace)) return einval("attention workspace must be 16-byte aligned");
+  if (Hkv <= 0 || Hq <= 0 || D != 128 || parts->K != Hq * D)
+    return einval("attention input needs head_dim 128 and K == Hq * 128");
+  AttnSource att;
+  if (attn_plan_geometry(parts->M, Hq, Hkv, D, block_size, max_blocks, &att.bps, &att.S) != 0) {
+    set_error("attention geometry not supported by the split attention kernel");
+    return GRPO_EUNSUPPORTED;
+  }
+  if (att.S > ATTN_MAX_SPLITS) return einval("too many attention splits");
+  att.o = static_cast<const float*>(attn_workspace);
+  att.ml = att.o + (size_t)parts->M * Hq * att.S * D;
+  att.len = context_lens;
+  att.Hq = Hq;
+  att.cap = max_blocks * block_size;
+  const uint16_t* la[MAXSEG] = {nullptr, nullptr, nullptr, nullptr};
+  if (parts->r > 0) {
+    if (!lora_a) return einval("r > 0 needs lora_a");
+    for (int s = 0; s < parts->nseg; ++s) la[s] = static_cast<const uint16_t*>(lora_a[s]);
+  }
+  return run_partials(nullptr, 0, w, absmax, code16, blocksize, la, *parts, as_stream(stream),
+                      &att);
 }

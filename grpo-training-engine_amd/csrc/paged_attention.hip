@@ -4,35 +4,44 @@
 // context_lens int32 [B] (device-resident, read-only here).
 //
 // Fast decode path (D == 128, block_size == 16, Hq/Hkv <= 8): grid
-// (context split, KV head, sequence), 4 waves per workgroup; every wave walks
-// its share of the split's 16-token blocks.  Per block the 4 KB K tile is read
-// with 16-byte loads straight into the A operand of v_mfma_f32_16x16x32_bf16
-// (rows = tokens) against the B operand Q^T of all query heads of the GQA group
-// (columns = heads), giving S^T[token][head] in 4 MFMAs.  The online softmax
-// runs in the exp2 domain; P and the per-head rescale go through a per-wave LDS
-// slot; P.V runs on VALU with every V element loaded once and applied to all
-// heads of the group.  Waves merge through LDS; sequences needing several
-// splits write (max, sum, unnormalised O) partials that a second kernel merges
-// with log-sum-exp weights.  K and V of a KV head are therefore read once per
-// step, not once per query head.
+// (context split, KV head, sequence) with at most 8 splits; 8 waves per
+// workgroup, each wave walking every 8th 16-token block of its split (the next
+// block's K/V loads are issued before the current block is processed).  Per
+// block the 4 KB K tile is read with 16-byte loads straight into the A operand
+// of v_mfma_f32_16x16x32_bf16 (rows = tokens) against the B operand Q^T of all
+// query heads of the GQA group (columns = heads), giving S^T[token][head] in 4
+// MFMAs.  The online softmax runs in the exp2 domain; P and the per-head
+// rescale go through a per-wave LDS slot; P.V runs on VALU with every V
+// element loaded once and applied to all heads of the group.  The 8 waves
+// merge through LDS and every split writes (max, sum, unnormalised O): the
+// standalone entry point merges them in a second kernel, the decode step merges
+// them while the o_proj kernel stages its input (linear_parts.hpp, nf4_linear.hip).
+// K and V of a KV head are read once per step, not once per query head.
+//
+// The decode step's variant also finishes the q|k|v projection from its split-K
+// partial sums, applies RoPE to q and k, and appends the new token's K/V to the
+// cache (the split holding the slot does it before it reads the cache), so
+// neither q nor the RoPE + append needs a launch of its own.
 #include <math.h>
 
-#include "common.hpp"
+#include "linear_parts.hpp"
 
 using namespace grpo;
 
 namespace {
 
-constexpr int FD = 128;  // fast-path head dim
-constexpr int FBS = 16;  // fast-path block size
-constexpr int TARGET_WAVES = 1024;
+constexpr int FD = 128;        // fast-path head dim
+constexpr int FBS = 16;        // fast-path block size
+constexpr int AW = 8;          // waves per workgroup
+constexpr int AT = 64 * AW;    // threads per workgroup
+constexpr int MAX_SPLITS = ATTN_MAX_SPLITS;  // context splits per (sequence, KV head)
 constexpr float LOG2E = 1.4426950408889634f;
 
 struct AttnArgs {
   const uint16_t* q;
   int64_t qsb, qsh;
-  const uint16_t* kc;
-  const uint16_t* vc;
+  uint16_t* kc;
+  uint16_t* vc;
   int64_t num_blocks;
   const int32_t* bt;
   int64_t bts;
@@ -44,7 +53,13 @@ struct AttnArgs {
   int bps;       // blocks per split
   int S;         // splits allocated in the workspace
   float* ws_o;   // [B][Hq][S][D]
-  float* ws_ml;  // [B][Hq][S][2]
+  float* ws_ml;  // [B][Hq][S][2]: max (log2 domain), sum
+  // fused q|k|v finish + RoPE + append (decode step)
+  LinParts qkv;
+  const uint16_t* cos_t;
+  const uint16_t* sin_t;
+  int max_pos;
+  const int32_t* append_pos;
 };
 
 struct AttnPlan {
@@ -61,12 +76,11 @@ AttnPlan plan_attn(int B, int Hq, int Hkv, int D, int BS, int max_blocks) {
     p.S = 1;
     return p;
   }
-  const int64_t total = (int64_t)B * Hkv * max_blocks;
-  int64_t bpw = total / TARGET_WAVES;
-  if (bpw < 1) bpw = 1;
-  p.bps = (int)(4 * bpw);
-  p.S = max_blocks > 0 ? (int)cdiv(max_blocks, p.bps) : 1;
-  if (p.S > 1) p.bytes = (size_t)B * Hq * p.S * (D + 2) * 4;
+  const int mb = max_blocks > 0 ? max_blocks : 1;
+  const int bpw = (int)cdiv(mb, (int64_t)AW * MAX_SPLITS);
+  p.bps = AW * bpw;
+  p.S = (int)cdiv(mb, p.bps);
+  p.bytes = (size_t)B * Hq * p.S * (D + 2) * 4;
   return p;
 }
 
@@ -83,14 +97,24 @@ __device__ __forceinline__ void store_out(const AttnArgs& p, int64_t idx, float 
     static_cast<float*>(p.out)[idx] = v;
 }
 
+// Orders a wave's LDS writes before its lanes read each other's values: wait
+// for the wave's outstanding LDS operations only (lgkmcnt), with a compiler
+// memory barrier.  A memory-model fence would also wait for the wave's
+// outstanding global loads, i.e. for the next block's prefetch.
 __device__ __forceinline__ void wave_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int GQ>
-__global__ void __launch_bounds__(256) paged_attn_mfma(AttnArgs p) {
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
+  return (uint32_t)lo | ((uint32_t)hi << 16);
+}
+
+constexpr int QKV_MAX_SLICES = 8;  // K slices of the q|k|v projection read here
+typedef Fetch4<QKV_MAX_SLICES> QkvFetch;
+
+template <int GQ, bool FUSED>
+__global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
@@ -101,23 +125,113 @@ __global__ void __launch_bounds__(256) paged_attn_mfma(AttnArgs p) {
   const int blk0 = s * p.bps;
   const int blk1 = min(blk0 + p.bps, nblk);
 
-  __shared__ __align__(16) float sP[4][16][16];
-  __shared__ float sC[4][16];
-  __shared__ float sM[4][16];
-  __shared__ float sL[4][16];
-  __shared__ __align__(16) float sO[4][GQ][FD];
+  extern __shared__ __align__(16) float sO[];  // [AW][GQ][FD]
+  __shared__ __align__(16) uint16_t sQ[GQ][FD];
+  __shared__ float sTs[MAXSEG * 16];
+  __shared__ __align__(16) float sP[AW][16][16];
+  __shared__ float sC[AW][16];
+  __shared__ float sM[AW][16];
+  __shared__ float sL[AW][16];
+
+  const int64_t head_stride = (int64_t)FBS * FD;
+  // K/V fragments of physical block phys (zeros for an invalid id, then skipped).
+  auto load_kv = [&](int phys, uint4 (&kf)[4], uint4 (&vf)[4]) -> bool {
+    const bool ok = phys >= 0 && phys < p.num_blocks;
+    const uint16_t* kb = p.kc + ((int64_t)(ok ? phys : 0) * p.Hkv + kvh) * head_stride;
+    const uint16_t* vb = p.vc + ((int64_t)(ok ? phys : 0) * p.Hkv + kvh) * head_stride;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kf[i] = ok ? *reinterpret_cast<const uint4*>(kb + ln * FD + 8 * lg + 32 * i)
+                 : make_uint4(0, 0, 0, 0);
+      vf[i] = ok ? *reinterpret_cast<const uint4*>(vb + (4 * lg + i) * FD + 8 * ln)
+                 : make_uint4(0, 0, 0, 0);
+    }
+    return ok;
+  };
+  // The split's slice of the block table, in LDS after the prologue.
+  int* sBT = reinterpret_cast<int*>(sO + (size_t)AW * GQ * FD);
+  for (int i = tid; i < blk1 - blk0; i += AT) sBT[i] = p.bt[(int64_t)b * p.bts + blk0 + i];
+
+  // 1. Q of the GQA group in LDS (and, fused, the new token's K/V in the cache).
+  // The first block's K/V loads go out first, unless it is the block this split
+  // appends to (that one is loaded after the append).
+  const int pos = FUSED ? p.append_pos[b] : -1;
+  const int first = blk0 + wave;
+  const bool late = FUSED && pos >= 0 && first == pos / FBS;
+  uint4 kn[4], vn[4];
+  bool ok_next = false;
+  if (!late && first < blk1) ok_next = load_kv(p.bt[(int64_t)b * p.bts + first], kn, vn);
+  if (FUSED) {
+    // Phase A (one memory round trip): every column group of q (GQ heads), of k
+    // and of v of this KV head is fetched by one thread, then finished (bias,
+    // LoRA, bf16) into LDS.  Phase B: RoPE from LDS; the split that holds the
+    // slot writes K (rotated) and V of the new token into the cache.
+    const int pblk = pos >= 0 ? pos / FBS : -1;
+    const bool app = pos >= 0 && pos < p.max_blocks * FBS && pblk >= blk0 && pblk < blk1;
+    const int nrow = GQ + (app ? 2 : 0);  // q heads, then k, then v
+    float* sRaw = sO;                     // [GQ + 2][FD], reused by the wave merge later
+    QkvFetch f;
+    const bool fetch = tid < nrow * (FD / 4);
+    const int row = tid / (FD / 4), d4 = 4 * (tid % (FD / 4));
+    if (fetch) {
+      const int n0 = row < GQ ? (kvh * GQ + row) * FD
+                              : (row == GQ ? (p.Hq + kvh) * FD : (p.Hq + p.Hkv + kvh) * FD);
+      lin_fetch4(p.qkv, b, n0 + d4, f);
+    }
+    lin_load_t(p.qkv, b, sTs);
+    __syncthreads();
+    if (fetch) {
+      float v[4];
+      lin_finish4(p.qkv, sTs, f, v);
+      *reinterpret_cast<float4*>(sRaw + row * FD + d4) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    __syncthreads();
+    const int cpos = pos < 0 ? 0 : (pos >= p.max_pos ? p.max_pos - 1 : pos);
+    const uint16_t* cr = p.cos_t + (int64_t)cpos * FD;
+    const uint16_t* sr = p.sin_t + (int64_t)cpos * FD;
+    int64_t slot = -1;
+    if (app) {
+      const int phys = p.bt[(int64_t)b * p.bts + pblk];
+      if (phys >= 0 && phys < p.num_blocks)
+        slot = (((int64_t)phys * p.Hkv + kvh) * FBS + pos % FBS) * FD;
+    }
+    // RoPE pairs (d, d + D/2): GQ q rows (+ the k row when appending).
+    const int npair = (GQ + (app ? 1 : 0)) * (FD / 2);
+    for (int i = tid; i < npair; i += AT) {
+      const int r = i / (FD / 2), d = i % (FD / 2);
+      const float x1 = sRaw[r * FD + d], x2 = sRaw[r * FD + d + FD / 2];
+      const uint16_t lo = f2bf(round_bf(round_bf(x1 * bf2f(cr[d])) + round_bf(-x2 * bf2f(sr[d]))));
+      const uint16_t hi = f2bf(round_bf(round_bf(x2 * bf2f(cr[d + FD / 2])) +
+                                        round_bf(x1 * bf2f(sr[d + FD / 2]))));
+      if (r < GQ) {
+        sQ[r][d] = lo;
+        sQ[r][d + FD / 2] = hi;
+      } else if (slot >= 0) {
+        p.kc[slot + d] = lo;
+        p.kc[slot + d + FD / 2] = hi;
+      }
+    }
+    if (app && slot >= 0)
+      for (int d = tid; d < FD; d += AT) p.vc[slot + d] = f2bf(sRaw[(GQ + 1) * FD + d]);
+  } else {
+    for (int i = tid; i < GQ * (FD / 8); i += AT) {
+      const int h = i / (FD / 8), c = i - h * (FD / 8);
+      *reinterpret_cast<uint4*>(&sQ[h][8 * c]) = *reinterpret_cast<const uint4*>(
+          p.q + (int64_t)b * p.qsb + (int64_t)(kvh * GQ + h) * p.qsh + 8 * c);
+    }
+  }
+  // Orders the appended K/V (global), sQ and the reuse of sO before any wave
+  // reads them.
+  __syncthreads();
+  if (late) ok_next = load_kv(sBT[first - blk0], kn, vn);
 
   // Q^T as the MFMA B operand: lane (head ln, group lg) holds
   // Q[head][8*lg + 32*i + 0..7] for MFMA i.
   uint4 qf[4];
-  {
-    const bool hv = ln < GQ;
-    const uint16_t* qrow =
-        p.q + (int64_t)b * p.qsb + (int64_t)(kvh * GQ + (hv ? ln : 0)) * p.qsh;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      qf[i] = hv ? *reinterpret_cast<const uint4*>(qrow + 8 * lg + 32 * i) : make_uint4(0, 0, 0, 0);
-  }
+  for (int i = 0; i < 4; ++i)
+    qf[i] = ln < GQ ? *reinterpret_cast<const uint4*>(&sQ[ln][8 * lg + 32 * i])
+                    : make_uint4(0, 0, 0, 0);
   const float sl2 = p.scale * LOG2E;
   float m_run = -INFINITY, l_run = 0.f;  // softmax state of head ln
   float o[GQ][8];
@@ -126,18 +240,17 @@ __global__ void __launch_bounds__(256) paged_attn_mfma(AttnArgs p) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[h][j] = 0.f;
 
-  const int64_t head_stride = (int64_t)FBS * FD;
-  for (int blk = blk0 + wave; blk < blk1; blk += 4) {
-    const int phys = p.bt[(int64_t)b * p.bts + blk];
-    if (phys < 0 || phys >= p.num_blocks) continue;
-    const uint16_t* kb = p.kc + ((int64_t)phys * p.Hkv + kvh) * head_stride;
-    const uint16_t* vb = p.vc + ((int64_t)phys * p.Hkv + kvh) * head_stride;
+  for (int blk = blk0 + wave; blk < blk1; blk += AW) {
     uint4 kf[4], vf[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kf[i] = *reinterpret_cast<const uint4*>(kb + ln * FD + 8 * lg + 32 * i);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) vf[i] = *reinterpret_cast<const uint4*>(vb + (4 * lg + i) * FD + 8 * ln);
-
+    for (int i = 0; i < 4; ++i) {
+      kf[i] = kn[i];
+      vf[i] = vn[i];
+    }
+    const bool ok = ok_next;
+    const int nxt = blk + AW;
+    ok_next = nxt < blk1 ? load_kv(sBT[nxt - blk0], kn, vn) : false;
+    if (!ok) continue;
     f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) sacc = mfma16x16x32(kf[i], qf[i], sacc);
@@ -150,8 +263,7 @@ __global__ void __launch_bounds__(256) paged_attn_mfma(AttnArgs p) {
       sv[r] = t < ctx ? sacc[r] * sl2 : -INFINITY;
       bmax = fmaxf(bmax, sv[r]);
     }
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 16));
-    bmax = fmaxf(bmax, __shfl_xor(bmax, 32));
+    bmax = pair32_max(pair16_max(bmax));
     const float m_new = fmaxf(m_run, bmax);  // finite: token blk*16 < ctx
     const float corr = exp2f(m_run - m_new);
     float pv[4];
@@ -161,8 +273,7 @@ __global__ void __launch_bounds__(256) paged_attn_mfma(AttnArgs p) {
       pv[r] = exp2f(sv[r] - m_new);
       ps += pv[r];
     }
-    ps += __shfl_xor(ps, 16);
-    ps += __shfl_xor(ps, 32);
+    ps = pair32_sum(pair16_sum(ps));
     l_run = l_run * corr + ps;
     m_run = m_new;
     *reinterpret_cast<float4*>(&sP[wave][ln][4 * lg]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
@@ -189,50 +300,43 @@ __global__ void __launch_bounds__(256) paged_attn_mfma(AttnArgs p) {
     wave_sync();
   }
 
-  // Sum the four token groups of the wave, then merge the four waves.
+  // Sum the four token groups of the wave, then merge the AW waves.
 #pragma unroll
   for (int h = 0; h < GQ; ++h)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      o[h][j] += __shfl_xor(o[h][j], 16);
-      o[h][j] += __shfl_xor(o[h][j], 32);
+      o[h][j] = pair32_sum(pair16_sum(o[h][j]));
     }
   if (lg == 0) {
     sM[wave][ln] = m_run;
     sL[wave][ln] = l_run;
 #pragma unroll
     for (int h = 0; h < GQ; ++h) {
-      *reinterpret_cast<float4*>(&sO[wave][h][8 * ln]) =
-          make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
-      *reinterpret_cast<float4*>(&sO[wave][h][8 * ln + 4]) =
-          make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+      float* dst = sO + ((size_t)wave * GQ + h) * FD + 8 * ln;
+      *reinterpret_cast<float4*>(dst) = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
+      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
     }
   }
   __syncthreads();
-  for (int i = tid; i < GQ * FD; i += 256) {
+  for (int i = tid; i < GQ * FD; i += AT) {
     const int h = i / FD, d = i - h * FD;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, sM[w][h]);
+    for (int w = 0; w < AW; ++w) M = fmaxf(M, sM[w][h]);
     float L = 0.f, O = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
+      for (int w = 0; w < AW; ++w) {
         const float f = exp2f(sM[w][h] - M);
         L += f * sL[w][h];
-        O += f * sO[w][h][d];
+        O += f * sO[((size_t)w * GQ + h) * FD + d];
       }
     }
-    const int hq = kvh * GQ + h;
-    if (nsplit == 1) {
-      store_out(p, ((int64_t)b * p.Hq + hq) * FD + d, O / fmaxf(L, 1e-6f));
-    } else {
-      const int64_t slot = ((int64_t)b * p.Hq + hq) * p.S + s;
-      p.ws_o[slot * FD + d] = O;
-      if (d == 0) {
-        p.ws_ml[slot * 2] = M;
-        p.ws_ml[slot * 2 + 1] = L;
-      }
+    const int64_t slot = ((int64_t)b * p.Hq + kvh * GQ + h) * p.S + s;
+    p.ws_o[slot * FD + d] = O;
+    if (d == 0) {
+      p.ws_ml[slot * 2] = M;
+      p.ws_ml[slot * 2 + 1] = L;
     }
   }
 }
@@ -243,7 +347,6 @@ __global__ void __launch_bounds__(128) paged_attn_merge(AttnArgs p) {
   const int ctx = seq_ctx(p, b);
   const int nblk = (ctx + p.BS - 1) / p.BS;
   const int nsplit = nblk > 0 ? (nblk + p.bps - 1) / p.bps : 1;
-  if (nsplit <= 1) return;
   const int64_t base = ((int64_t)b * p.Hq + hq) * p.S;
   float M = -INFINITY;
   for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p.ws_ml[(base + s) * 2]);
@@ -252,13 +355,13 @@ __global__ void __launch_bounds__(128) paged_attn_merge(AttnArgs p) {
   if (any)
     for (int s = 0; s < nsplit; ++s)
       L += exp2f(p.ws_ml[(base + s) * 2] - M) * p.ws_ml[(base + s) * 2 + 1];
-  const float inv = 1.f / fmaxf(L, 1e-6f);
+  const float den = fmaxf(L, 1e-6f);
   for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
     float O = 0.f;
     if (any)
       for (int s = 0; s < nsplit; ++s)
         O += exp2f(p.ws_ml[(base + s) * 2] - M) * p.ws_o[(base + s) * p.D + d];
-    store_out(p, ((int64_t)b * p.Hq + hq) * p.D + d, O * inv);
+    store_out(p, ((int64_t)b * p.Hq + hq) * p.D + d, O / den);
   }
 }
 
@@ -367,11 +470,43 @@ __global__ void __launch_bounds__(128) paged_kv_append_kernel(
   }
 }
 
-template <int GQ>
-int launch_fast_attn(const AttnArgs& a, hipStream_t st) {
-  dim3 grid(a.S, a.Hkv, a.B);
-  paged_attn_mfma<GQ><<<grid, 256, 0, st>>>(a);
-  return launch_check("paged_attn_mfma");
+template <int GQ, bool FUSED>
+int launch_split(const AttnArgs& a, hipStream_t st) {
+  // wave merge [AW][GQ][FD] floats (the fused prologue reuses it as [GQ + 2][FD]),
+  // then the split's block-table slice
+  const size_t lds = (size_t)AW * GQ * FD * sizeof(float) + (size_t)a.bps * sizeof(int);
+  if (lds > 65536) return einval("context too long for the split attention kernel");
+  paged_attn_split<GQ, FUSED><<<dim3(a.S, a.Hkv, a.B), AT, lds, st>>>(a);
+  return launch_check("paged_attn_split");
+}
+
+template <bool FUSED>
+int launch_split_gq(const AttnArgs& a, hipStream_t st) {
+  switch (a.Hq / a.Hkv) {
+    case 1: return launch_split<1, FUSED>(a, st);
+    case 2: return launch_split<2, FUSED>(a, st);
+    case 3: return launch_split<3, FUSED>(a, st);
+    case 4: return launch_split<4, FUSED>(a, st);
+    case 5: return launch_split<5, FUSED>(a, st);
+    case 6: return launch_split<6, FUSED>(a, st);
+    case 7: return launch_split<7, FUSED>(a, st);
+    default: return launch_split<8, FUSED>(a, st);
+  }
+}
+
+int use_workspace(AttnArgs& a, const AttnPlan& plan, void* workspace, size_t workspace_bytes) {
+  if (!workspace || workspace_bytes < plan.bytes) {
+    set_error("invalid argument: workspace of %zu bytes needed, %zu given", plan.bytes,
+              workspace_bytes);
+    return GRPO_EWORKSPACE;
+  }
+  if ((reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
+    return einval("attention workspace must be 16-byte aligned");
+  a.bps = plan.bps;
+  a.S = plan.S;
+  a.ws_o = static_cast<float*>(workspace);
+  a.ws_ml = a.ws_o + (size_t)a.B * a.Hq * plan.S * a.D;
+  return GRPO_OK;
 }
 
 }  // namespace
@@ -418,8 +553,8 @@ extern "C" int grpo_paged_attn_decode(const void* q, int64_t q_stride_b, int64_t
   a.q = static_cast<const uint16_t*>(q);
   a.qsb = q_stride_b;
   a.qsh = q_stride_h;
-  a.kc = static_cast<const uint16_t*>(k_cache);
-  a.vc = static_cast<const uint16_t*>(v_cache);
+  a.kc = static_cast<uint16_t*>(const_cast<void*>(k_cache));
+  a.vc = static_cast<uint16_t*>(const_cast<void*>(v_cache));
   a.num_blocks = num_blocks;
   a.bt = block_tables;
   a.bts = bt_stride;
@@ -439,29 +574,8 @@ extern "C" int grpo_paged_attn_decode(const void* q, int64_t q_stride_b, int64_t
                        q_stride_h % 8 == 0 && (reinterpret_cast<uintptr_t>(k_cache) & 15u) == 0 &&
                        (reinterpret_cast<uintptr_t>(v_cache) & 15u) == 0;
   if (plan.fast && aligned && max_blocks > 0) {
-    a.bps = plan.bps;
-    a.S = plan.S;
-    if (plan.S > 1) {
-      if (!workspace || workspace_bytes < plan.bytes) {
-        set_error("invalid argument: workspace of %zu bytes needed, %zu given", plan.bytes,
-                  workspace_bytes);
-        return GRPO_EWORKSPACE;
-      }
-      a.ws_o = static_cast<float*>(workspace);
-      a.ws_ml = a.ws_o + (size_t)B * Hq * plan.S * D;
-    }
-    int rc = GRPO_OK;
-    switch (Hq / Hkv) {
-      case 1: rc = launch_fast_attn<1>(a, st); break;
-      case 2: rc = launch_fast_attn<2>(a, st); break;
-      case 3: rc = launch_fast_attn<3>(a, st); break;
-      case 4: rc = launch_fast_attn<4>(a, st); break;
-      case 5: rc = launch_fast_attn<5>(a, st); break;
-      case 6: rc = launch_fast_attn<6>(a, st); break;
-      case 7: rc = launch_fast_attn<7>(a, st); break;
-      default: rc = launch_fast_attn<8>(a, st); break;
-    }
-    if (rc != GRPO_OK || plan.S <= 1) return rc;
+    if (int rc = use_workspace(a, plan, workspace, workspace_bytes)) return rc;
+    if (int rc = launch_split_gq<false>(a, st)) return rc;
     paged_attn_merge<<<dim3(Hq, B), 128, 0, st>>>(a);
     return launch_check("paged_attn_merge");
   }
@@ -470,3 +584,65 @@ extern "C" int grpo_paged_attn_decode(const void* q, int64_t q_stride_b, int64_t
   paged_attn_generic<<<dim3(Hq, B), GEN_T, 0, st>>>(a);
   return launch_check("paged_attn_generic");
 }
+
+extern "C" int grpo_paged_attn_decode_qkv(const grpo_linear_parts_t* qkv, int Hq, int Hkv, int D,
+                                          const void* cos_table, const void* sin_table,
+                                          int max_pos, const int32_t* append_pos,
+                                          const int32_t* context_lens, void* k_cache,
+                                          void* v_cache, int64_t num_blocks,
+                                          const int32_t* block_tables, int64_t bt_stride,
+                                          int block_size, int max_blocks, float scale,
+                                          void* workspace, size_t workspace_bytes,
+                                          grpo_stream_t stream) {
+  AttnArgs a{};
+  if (int rc = make_parts(qkv, &a.qkv)) return rc;
+  if (Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || max_blocks <= 0 || num_blocks < 0 || max_pos <= 0)
+    return einval("bad attention dimensions");
+  const AttnPlan plan = plan_attn(a.qkv.M, Hq, Hkv, D, block_size, max_blocks);
+  if (!plan.fast) {
+    set_error("fused q|k|v attention needs head_dim 128, block size 16, Hq/Hkv <= 8");
+    return GRPO_EUNSUPPORTED;
+  }
+  if (a.qkv.N != (Hq + 2 * Hkv) * D) return einval("qkv width must be (Hq + 2 Hkv) * D");
+  if (a.qkv.S > QKV_MAX_SLICES) {
+    set_error("fused q|k|v attention reads at most 8 K slices of the projection");
+    return GRPO_EUNSUPPORTED;
+  }
+  if (!cos_table || !sin_table || !append_pos || !context_lens || !k_cache || !v_cache ||
+      !block_tables)
+    return einval("null pointer");
+  if ((reinterpret_cast<uintptr_t>(k_cache) & 15u) || (reinterpret_cast<uintptr_t>(v_cache) & 15u))
+    return einval("caches must be 16-byte aligned");
+  a.kc = static_cast<uint16_t*>(k_cache);
+  a.vc = static_cast<uint16_t*>(v_cache);
+  a.num_blocks = num_blocks;
+  a.bt = block_tables;
+  a.bts = bt_stride;
+  a.cl = context_lens;
+  a.B = a.qkv.M;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.D = D;
+  a.BS = block_size;
+  a.max_blocks = max_blocks;
+  a.scale = scale;
+  a.cos_t = static_cast<const uint16_t*>(cos_table);
+  a.sin_t = static_cast<const uint16_t*>(sin_table);
+  a.max_pos = max_pos;
+  a.append_pos = append_pos;
+  if (int rc = use_workspace(a, plan, workspace, workspace_bytes)) return rc;
+  return launch_split_gq<true>(a, as_stream(stream));
+}
+
+namespace grpo {
+
+int attn_plan_geometry(int B, int Hq, int Hkv, int D, int block_size, int max_blocks, int* bps,
+                       int* splits) {
+  const AttnPlan plan = plan_attn(B, Hq, Hkv, D, block_size, max_blocks);
+  if (!plan.fast || max_blocks <= 0) return GRPO_EUNSUPPORTED;
+  *bps = plan.bps;
+  *splits = plan.S;
+  return GRPO_OK;
+}
+
+}  // namespace grpo

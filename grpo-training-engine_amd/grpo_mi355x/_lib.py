@@ -89,6 +89,15 @@ SIGNATURES = {
         [_VP, _VP, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _I32, _I32, _I32, _I32, _I32, _VP],
     ),
     "grpo_paged_attn_workspace_bytes": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "grpo_paged_attn_decode_qkv": (
+        _I32,
+        [_PARTS, _I32, _I32, _I32, _VP, _VP, _I32, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I32,
+         _I32, _F32, _VP, _SZ, _VP],
+    ),
+    "grpo_nf4_linear_partials_attn": (
+        _I32,
+        [_VP, _VP, _I32, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _I32, _VP, _PARTS, _VP],
+    ),
     "grpo_paged_attn_decode": (
         _I32,
         [_VP, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32,

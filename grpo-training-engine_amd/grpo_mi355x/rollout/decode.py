@@ -6,10 +6,10 @@ a fixed batch of sequences on a ``PagedKVPool``: the reference's ``_step``
 per layer --
 
   add+RMSNorm(down partials) -> q|k|v NF4+LoRA partials (one launch) ->
-  RoPE + KV append (finishes q|k|v) -> paged GQA attention (bf16 out) ->
-  o_proj NF4+LoRA partials -> add+RMSNorm (finishes o_proj) ->
-  gate|up NF4 partials (one launch) -> SiLU*mul (finishes gate|up) ->
-  down NF4 partials
+  paged GQA attention (finishes q|k|v, RoPE, KV append; split partials) ->
+  o_proj NF4+LoRA partials (merges the attention splits while staging x) ->
+  add+RMSNorm (finishes o_proj) -> gate|up NF4 partials (one launch) ->
+  SiLU*mul (finishes gate|up) -> down NF4 partials
 
 -- then the final norm, the bf16 lm_head and greedy argmax.  Each NF4 linear
 is a split-K launch that writes float32 partial sums; the op that consumes its
@@ -82,8 +82,6 @@ class DecodeEngine:
         # activations
         self.h = torch.zeros(B, H, **bf)
         self.x = torch.zeros(B, H, **bf)
-        self.q = torch.zeros(B, self.Hq, D, **bf)
-        self.attn = torch.zeros(B, self.Hq * D, **bf)
         self.act = torch.zeros(B, self.I, **bf)
         self.logits = torch.zeros(B, self.V, **bf)
         self.next = torch.zeros(B, dtype=torch.int64, device=dev)
@@ -206,20 +204,17 @@ class DecodeEngine:
             out.append(("qkv", lambda q=q, L=L: chk(lib.grpo_nf4_linear_partials(
                 x, H, q.packed.data_ptr(), q.absmax.data_ptr(), q.code.data_ptr(), self.bs,
                 L["la"], L["qkv_parts"], st), "qkv")))
-            out.append(("rope_append", lambda L=L, kc=kc, vc=vc: chk(
-                lib.grpo_qkv_rope_append_parts(
+            out.append(("attention", lambda L=L, kc=kc, vc=vc: chk(
+                lib.grpo_paged_attn_decode_qkv(
                     L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
-                    self.max_pos, self.append_pos.data_ptr(), self.q.data_ptr(), kc, vc,
+                    self.max_pos, self.append_pos.data_ptr(), self.attn_len.data_ptr(), kc, vc,
                     pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
-                    pool.block_size, self.max_blocks, st), "rope_append")))
-            out.append(("attention", lambda kc=kc, vc=vc: chk(lib.grpo_paged_attn_decode(
-                self.q.data_ptr(), Hq * D, D, kc, vc, pool.num_blocks,
-                self.block_tables.data_ptr(), self.max_blocks, self.attn_len.data_ptr(),
-                self.attn.data_ptr(), 1, B, Hq, Hkv, D, pool.block_size, self.max_blocks,
-                1.0 / math.sqrt(D), wsa, wsa_n, st), "attention")))
-            out.append(("o", lambda L=L: chk(lib.grpo_nf4_linear_partials(
-                self.attn.data_ptr(), Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
-                L["o_code"].data_ptr(), self.bs, L["o_la"], L["o_parts"], st), "o_proj")))
+                    pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n, st),
+                "attention")))
+            out.append(("o", lambda L=L: chk(lib.grpo_nf4_linear_partials_attn(
+                wsa, self.attn_len.data_ptr(), Hq, Hkv, D, pool.block_size, self.max_blocks,
+                L["o_w"].data_ptr(), L["o_absmax"].data_ptr(), L["o_code"].data_ptr(), self.bs,
+                L["o_la"], L["o_parts"], st), "o_proj")))
             out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm_parts(
                 L["o_parts"], h, h, L["post_norm"].data_ptr(), x, L["eps"], st), "post_norm")))
             g = L["gu"]

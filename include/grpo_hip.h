@@ -182,6 +182,36 @@ int grpo_paged_attn_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h
                            int Hkv, int D, int block_size, int max_blocks, float scale,
                            void* workspace, size_t workspace_bytes, grpo_stream_t stream);
 
+/* Decode-step attention: grpo_paged_attn_decode with q, k and v taken from the
+ * split-K partial sums of the q|k|v projection (finished here with its bias and
+ * LoRA epilogue), RoPE applied to q and k at position append_pos[b] (cos/sin
+ * tables bf16 [max_pos, D]), and the new token's K/V appended at slot
+ * append_pos[b] (skipped when < 0) before attention reads the cache.
+ * context_lens[b] is the attention length (0 = inactive row).  Writes split
+ * partials to the workspace (grpo_paged_attn_workspace_bytes(B = qkv->M, ...))
+ * for grpo_nf4_linear_partials_attn, which merges them.  Fuses fused_qkv_rope
+ * (fused_ops.py:198-219), the KV update (paged_kv.py:253-319) and the
+ * attention kernel (paged_kv.py:63-251) of one layer of _step
+ * (paged_kv.py:712-761).  Needs D = 128, block size 16, Hq/Hkv <= 8. */
+int grpo_paged_attn_decode_qkv(const grpo_linear_parts_t* qkv, int Hq, int Hkv, int D,
+                               const void* cos_table, const void* sin_table, int max_pos,
+                               const int32_t* append_pos, const int32_t* context_lens,
+                               void* k_cache, void* v_cache, int64_t num_blocks,
+                               const int32_t* block_tables, int64_t bt_stride, int block_size,
+                               int max_blocks, float scale, void* workspace,
+                               size_t workspace_bytes, grpo_stream_t stream);
+
+/* grpo_nf4_linear_partials with x = the attention output left by
+ * grpo_paged_attn_decode_qkv in attn_workspace (x[b, h*D + d], merged over
+ * context splits and rounded to bf16 while the kernel stages it): the o_proj
+ * of _step (paged_kv.py:762-775).  Hq, Hkv, D, block_size, max_blocks and
+ * context_lens must be those of the attention call; parts->K = Hq * D. */
+int grpo_nf4_linear_partials_attn(const void* attn_workspace, const int32_t* context_lens,
+                                  int Hq, int Hkv, int D, int block_size, int max_blocks,
+                                  const uint8_t* w, const float* absmax, const float* code16,
+                                  int blocksize, const void* const* lora_a,
+                                  const grpo_linear_parts_t* parts, grpo_stream_t stream);
+
 /* ------------------------------------------------------- decode step --
  * Ops of the model-level decode step around the two hot-path kernels
  * (src/triton_kernels/paged_kv.py:690-820).  bf16 tensors are row-major. */
