@@ -37,7 +37,7 @@ using namespace grpo;
 namespace {
 
 constexpr int KSTEP = 256;          // k elements per step: 4 lane groups x 64
-constexpr int PART_WAVES = 4;       // n-tiles (waves) per workgroup
+constexpr int PART_WAVES = 4;       // n-tiles (waves) per workgroup, x given in bf16
 constexpr int PART_LDS_MAX = 65536; // bytes of the staged x slice per workgroup
 constexpr int KPW_MAX = 8;          // k-steps per wave (all loads in flight at once)
 int g_target_waves = 2048;          // launch-shape target: 8 waves per CU on 256 CUs
@@ -150,7 +150,65 @@ struct PartArgs {
   const float* att_ml;   // [M][Hq][S][2]: max (log2 domain), sum
   const int32_t* att_len;
   int att_S, att_bps, att_Hq, att_cap;
+  // x = SiLU(gate) * up from the gate|up projection's partial sums (down_proj)
+  const float* gu_part;  // [gu_S][M][2 * K]
+  int gu_S;
 };
+
+enum XSource { X_BF16 = 0, X_ATTN = 1, X_SILU = 2 };
+
+// n-tiles (waves) per workgroup.  Every workgroup of a K slice rebuilds the x
+// slice it stages; the SiLU source reads 16 bytes of partial sums per element,
+// so its workgroups are larger (fewer rebuilds).  Measured at decode shapes:
+// the attention-merge source is fastest with the default 4.
+__host__ __device__ constexpr int waves_per_group(int xsrc) {
+  return xsrc == X_SILU ? 8 : PART_WAVES;
+}
+constexpr int GU_MAX_SLICES = 2;  // K slices of the gate|up partial sums read while staging
+
+// Columns k..k+7 of row m of bf16(bf16(silu(g)) * u), with g = bf16(sum of the
+// gate partials), u = bf16(sum of the up partials) (fused_ops.py:79-112 applied
+// to the finished gate|up output).
+__device__ __forceinline__ uint4 silu_chunk(const PartArgs& p, int m, int k) {
+  const int64_t row = (int64_t)m * 2 * p.K;
+  const int64_t stride = (int64_t)p.M * 2 * p.K / 4;
+  const float4* pg = reinterpret_cast<const float4*>(p.gu_part + row + k);
+  const float4* pu = reinterpret_cast<const float4*>(p.gu_part + row + p.K + k);
+  float4 g[GU_MAX_SLICES][2], u[GU_MAX_SLICES][2];
+#pragma unroll
+  for (int s = 0; s < GU_MAX_SLICES; ++s)
+    if (s < p.gu_S) {
+      g[s][0] = pg[s * stride];
+      g[s][1] = pg[s * stride + 1];
+      u[s][0] = pu[s * stride];
+      u[s][1] = pu[s * stride + 1];
+    }
+  float gs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float us[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < GU_MAX_SLICES; ++s)
+    if (s < p.gu_S) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        gs[4 * h + 0] += g[s][h].x;
+        gs[4 * h + 1] += g[s][h].y;
+        gs[4 * h + 2] += g[s][h].z;
+        gs[4 * h + 3] += g[s][h].w;
+        us[4 * h + 0] += u[s][h].x;
+        us[4 * h + 1] += u[s][h].y;
+        us[4 * h + 2] += u[s][h].z;
+        us[4 * h + 3] += u[s][h].w;
+      }
+    }
+  float o[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float gv = round_bf(gs[j]);
+    o[j] = round_bf(gv * (1.f / (1.f + expf(-gv)))) * round_bf(us[j]);
+  }
+  return make_uint4(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]), pack_bf2(o[4], o[5]),
+                    pack_bf2(o[6], o[7]));
+}
 
 // Eight consecutive columns k..k+7 (one head, d0 = k % 128) of row m of the
 // attention output, merged over its context splits:
@@ -202,15 +260,16 @@ __device__ __forceinline__ uint4 attn_chunk(const PartArgs& p, int m, int k) {
                     pack_bf2(O[4] / den, O[5] / den), pack_bf2(O[6] / den, O[7] / den));
 }
 
-template <int MT, int KPW, bool XATT>
-__global__ void __launch_bounds__(256) nf4_part_mfma(PartArgs p) {
+template <int MT, int KPW, int XSRC>
+__global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(PartArgs p) {
+  constexpr int WPG = waves_per_group(XSRC), NT = 64 * WPG;
   extern __shared__ __align__(16) uint16_t xs[];  // [M][xstride], decode8 order
   // Padding workgroups of the XCD-aligned grid have no tile at all.
-  if ((int)blockIdx.x * PART_WAVES >= p.ntiles) return;
+  if ((int)blockIdx.x * WPG >= p.ntiles) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
-  const int tile = blockIdx.x * PART_WAVES + wave;
+  const int tile = blockIdx.x * WPG + wave;
   const int slice = blockIdx.y;
   const int ks0 = slice * KPW;
   const int nk = min(KPW, p.K / KSTEP - ks0);  // >= 1: the host sizes the grid
@@ -242,20 +301,24 @@ __global__ void __launch_bounds__(256) nf4_part_mfma(PartArgs p) {
   {
     const int chunks = nk * (KSTEP / 8);
     const int total = p.M * chunks;
-    for (int base = 0; base < total; base += 4 * 256) {
+    for (int base = 0; base < total; base += 4 * NT) {
       uint4 v[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int i = base + u * 256 + tid;
+        const int i = base + u * NT + tid;
         if (i < total) {
           const int m = i / chunks, c = i - m * chunks;
-          v[u] = XATT ? attn_chunk(p, m, kbase + 8 * c)
-                      : *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase + 8 * c);
+          if (XSRC == X_ATTN)
+            v[u] = attn_chunk(p, m, kbase + 8 * c);
+          else if (XSRC == X_SILU)
+            v[u] = silu_chunk(p, m, kbase + 8 * c);
+          else
+            v[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase + 8 * c);
         }
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int i = base + u * 256 + tid;
+        const int i = base + u * NT + tid;
         if (i < total) {
           const int m = i / chunks, c = i - m * chunks;
           *reinterpret_cast<uint4*>(xs + m * p.xstride + 8 * c) = deinterleave8(v[u]);
@@ -410,17 +473,18 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg) {
 // share are fetched from HBM into one L2 only.
 constexpr int NUM_XCD = 8;
 
-template <int MT, bool XATT>
+template <int MT, int XSRC>
 int launch_part(const PartArgs& a, const PartPlan& pl, hipStream_t st) {
-  const int groups = (int)cdiv(pl.ntiles, PART_WAVES);
-  const dim3 grid((unsigned)(cdiv(groups, NUM_XCD) * NUM_XCD), (unsigned)pl.S), block(256);
+  constexpr int WPG = waves_per_group(XSRC);
+  const int groups = (int)cdiv(pl.ntiles, WPG);
+  const dim3 grid((unsigned)(cdiv(groups, NUM_XCD) * NUM_XCD), (unsigned)pl.S), block(64 * WPG);
   switch (pl.kpw) {
-    case 1: nf4_part_mfma<MT, 1, XATT><<<grid, block, pl.lds, st>>>(a); break;
-    case 2: nf4_part_mfma<MT, 2, XATT><<<grid, block, pl.lds, st>>>(a); break;
-    case 3: nf4_part_mfma<MT, 3, XATT><<<grid, block, pl.lds, st>>>(a); break;
-    case 4: nf4_part_mfma<MT, 4, XATT><<<grid, block, pl.lds, st>>>(a); break;
-    case 6: nf4_part_mfma<MT, 6, XATT><<<grid, block, pl.lds, st>>>(a); break;
-    default: nf4_part_mfma<MT, 8, XATT><<<grid, block, pl.lds, st>>>(a); break;
+    case 1: nf4_part_mfma<MT, 1, XSRC><<<grid, block, pl.lds, st>>>(a); break;
+    case 2: nf4_part_mfma<MT, 2, XSRC><<<grid, block, pl.lds, st>>>(a); break;
+    case 3: nf4_part_mfma<MT, 3, XSRC><<<grid, block, pl.lds, st>>>(a); break;
+    case 4: nf4_part_mfma<MT, 4, XSRC><<<grid, block, pl.lds, st>>>(a); break;
+    case 6: nf4_part_mfma<MT, 6, XSRC><<<grid, block, pl.lds, st>>>(a); break;
+    default: nf4_part_mfma<MT, 8, XSRC><<<grid, block, pl.lds, st>>>(a); break;
   }
   return launch_check("nf4_part_mfma");
 }
@@ -433,19 +497,27 @@ struct AttnSource {
   int S = 0, bps = 0, Hq = 0, cap = 0;
 };
 
+// gate|up partial-sum source of x (down_proj of the decode step), or null.
+struct SiluSource {
+  const float* part = nullptr;
+  int S = 0;
+};
+
 int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* absmax,
                  const float* code16, int blocksize, const uint16_t* const* la,
-                 const grpo_linear_parts_t& h, hipStream_t st, const AttnSource* att = nullptr) {
+                 const grpo_linear_parts_t& h, hipStream_t st, const AttnSource* att = nullptr,
+                 const SiluSource* silu = nullptr) {
+  const bool xsrc = att || silu;
   if (!part_shape_ok(h.M, h.N, h.K, h.r, h.nseg, blocksize, h.seg_end)) {
     set_error("shape not supported by the split-K NF4 linear");
     return GRPO_EUNSUPPORTED;
   }
   const PartPlan pl = plan_part(h.M, h.N, h.K, h.r, h.nseg);
   if (h.splits != pl.S) return einval("parts.splits differs from grpo_nf4_linear_plan");
-  if ((!x && !att) || !w || !absmax || !code16 || !h.part) return einval("null pointer");
+  if ((!x && !xsrc) || !w || !absmax || !code16 || !h.part) return einval("null pointer");
   if (h.r > 0 && !h.tpart) return einval("r > 0 needs tpart");
-  if (!att && (ldx < h.K || ldx % 8 != 0)) return einval("ldx must be >= K and a multiple of 8");
-  if ((!att && !aligned16(x)) || !aligned16(w)) return einval("x and w must be 16-byte aligned");
+  if (!xsrc && (ldx < h.K || ldx % 8 != 0)) return einval("ldx must be >= K and a multiple of 8");
+  if ((!xsrc && !aligned16(x)) || !aligned16(w)) return einval("x and w must be 16-byte aligned");
   PartArgs a{};
   a.x = x;
   a.ldx = ldx;
@@ -477,15 +549,24 @@ int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* 
     a.att_Hq = att->Hq;
     a.att_cap = att->cap;
     switch (pl.MT) {
-      case 1: return launch_part<1, true>(a, pl, st);
-      case 2: return launch_part<2, true>(a, pl, st);
-      default: return launch_part<4, true>(a, pl, st);
+      case 1: return launch_part<1, X_ATTN>(a, pl, st);
+      case 2: return launch_part<2, X_ATTN>(a, pl, st);
+      default: return launch_part<4, X_ATTN>(a, pl, st);
+    }
+  }
+  if (silu) {
+    a.gu_part = silu->part;
+    a.gu_S = silu->S;
+    switch (pl.MT) {
+      case 1: return launch_part<1, X_SILU>(a, pl, st);
+      case 2: return launch_part<2, X_SILU>(a, pl, st);
+      default: return launch_part<4, X_SILU>(a, pl, st);
     }
   }
   switch (pl.MT) {
-    case 1: return launch_part<1, false>(a, pl, st);
-    case 2: return launch_part<2, false>(a, pl, st);
-    default: return launch_part<4, false>(a, pl, st);
+    case 1: return launch_part<1, X_BF16>(a, pl, st);
+    case 2: return launch_part<2, X_BF16>(a, pl, st);
+    default: return launch_part<4, X_BF16>(a, pl, st);
   }
 }
 
@@ -831,4 +912,31 @@ extern "C" int grpo_nf4_linear_partials_attn(const void* attn_workspace,
   }
   return run_partials(nullptr, 0, w, absmax, code16, blocksize, la, *parts, as_stream(stream),
                       &att);
+}
+
+extern "C" int grpo_nf4_linear_partials_silu(const grpo_linear_parts_t* gate_up, const uint8_t* w,
+                                             const float* absmax, const float* code16,
+                                             int blocksize, const grpo_linear_parts_t* parts,
+                                             grpo_stream_t stream) {
+  if (!parts || !gate_up) return einval("null parts descriptor");
+  if (blocksize <= 0) return einval("blocksize must be > 0");
+  LinParts check, gu;
+  if (int rc = make_parts(parts, &check)) return rc;
+  if (int rc = make_parts(gate_up, &gu)) return rc;
+  if (gu.r != 0) return einval("gate|up source must have no LoRA term");
+  for (int s = 0; s < gu.nseg; ++s)
+    if (gu.bias[s]) return einval("gate|up source must have no bias");
+  if (gu.M != parts->M || gu.N != 2 * parts->K)
+    return einval("gate|up source must be [M, 2K] for a down projection of input width K");
+  if (gu.S > GU_MAX_SLICES) {
+    set_error("gate|up source has more than 2 K slices");
+    return GRPO_EUNSUPPORTED;
+  }
+  SiluSource src;
+  src.part = gu.part;
+  src.S = gu.S;
+  const uint16_t* la[MAXSEG] = {nullptr, nullptr, nullptr, nullptr};
+  if (parts->r > 0) return einval("down projection with LoRA is not supported here");
+  return run_partials(nullptr, 0, w, absmax, code16, blocksize, la, *parts, as_stream(stream),
+                      nullptr, &src);
 }

@@ -9,7 +9,7 @@ per layer --
   paged GQA attention (finishes q|k|v, RoPE, KV append; split partials) ->
   o_proj NF4+LoRA partials (merges the attention splits while staging x) ->
   add+RMSNorm (finishes o_proj) -> gate|up NF4 partials (one launch) ->
-  SiLU*mul (finishes gate|up) -> down NF4 partials
+  down NF4 partials (finishes gate|up and applies SiLU*mul while staging x)
 
 -- then the final norm, the bf16 lm_head and greedy argmax.  Each NF4 linear
 is a split-K launch that writes float32 partial sums; the op that consumes its
@@ -106,17 +106,20 @@ class DecodeEngine:
                 raise ValueError(f"{kind} shape [{n}, {k}] (B={B}) is outside the split-K "
                                  "NF4 path")
             plans[kind] = plan
-        # One partial-sum buffer serves every linear: each is consumed before
-        # the next linear of the step writes it.
+        # Partial-sum buffers: q|k|v, o and down share one (each is consumed by
+        # the next kernel before another linear writes it); gate|up has its own,
+        # because down_proj reads it while writing its own partial sums.
         self.part = torch.empty(max(p[1] for p in plans.values()) // 4, dtype=torch.float32,
                                 device=dev)
+        self.part_gu = torch.empty(plans["gate_up"][1] // 4, dtype=torch.float32, device=dev)
         self.tpart = torch.empty(max(max(p[2] for p in plans.values()) // 4, 1),
                                  dtype=torch.float32, device=dev)
 
         def parts(kind, seg_rows, biases=None, lbs=None, rank=0, scaling=1.0):
             n, k, _, nseg = shapes[kind]
             d = _lib.LinearParts()
-            d.part, d.tpart = self.part.data_ptr(), self.tpart.data_ptr()
+            buf = self.part_gu if kind == "gate_up" else self.part
+            d.part, d.tpart = buf.data_ptr(), self.tpart.data_ptr()
             d.splits, d.M, d.N, d.K, d.nseg, d.r = plans[kind][0], B, n, k, nseg, rank
             end = 0
             for i, rows in enumerate(seg_rows):
@@ -164,6 +167,9 @@ class DecodeEngine:
         self.ws_attn = ops.workspace("paged_attn", max(ops.paged_attention_workspace_bytes(
             B, Hq, self.Hkv, D, self.pool.block_size, self.max_blocks), 1), dev)
         self.plans = plans
+        # down_proj stages SiLU(gate) * up straight from the gate|up partial
+        # sums when they have at most 2 K slices (the fused kernel's limit)
+        self.fuse_silu = plans["gate_up"][0] <= 2
         nf4 = lambda n, k: n * k // 2 + n * k // bs * 4
         # Algorithmic HBM bytes of each NF4 partials launch: packed weight +
         # absmax + LoRA A + x + the float32 partial sums written.
@@ -221,11 +227,17 @@ class DecodeEngine:
             out.append(("gate_up", lambda g=g, L=L: chk(lib.grpo_nf4_linear_partials(
                 x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
                 None, L["gu_parts"], st), "gate_up")))
-            out.append(("silu_mul", lambda L=L: chk(lib.grpo_silu_mul_parts(
-                L["gu_parts"], self.act.data_ptr(), I, st), "silu_mul")))
-            out.append(("down", lambda L=L: chk(lib.grpo_nf4_linear_partials(
-                self.act.data_ptr(), I, L["down_w"].data_ptr(), L["down_absmax"].data_ptr(),
-                L["down_code"].data_ptr(), self.bs, None, L["down_parts"], st), "down")))
+            if self.fuse_silu:
+                out.append(("down", lambda L=L: chk(lib.grpo_nf4_linear_partials_silu(
+                    L["gu_parts"], L["down_w"].data_ptr(), L["down_absmax"].data_ptr(),
+                    L["down_code"].data_ptr(), self.bs, L["down_parts"], st), "down")))
+            else:
+                out.append(("silu_mul", lambda L=L: chk(lib.grpo_silu_mul_parts(
+                    L["gu_parts"], self.act.data_ptr(), I, st), "silu_mul")))
+                out.append(("down", lambda L=L: chk(lib.grpo_nf4_linear_partials(
+                    self.act.data_ptr(), I, L["down_w"].data_ptr(),
+                    L["down_absmax"].data_ptr(), L["down_code"].data_ptr(), self.bs, None,
+                    L["down_parts"], st), "down")))
             prev = L
         out.append(("rmsnorm", lambda P=prev: chk(lib.grpo_add_rmsnorm_parts(
             P["down_parts"], h, h, self.final_norm.data_ptr(), x, self.final_eps, st),

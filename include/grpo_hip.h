@@ -212,6 +212,15 @@ int grpo_nf4_linear_partials_attn(const void* attn_workspace, const int32_t* con
                                   int blocksize, const void* const* lora_a,
                                   const grpo_linear_parts_t* parts, grpo_stream_t stream);
 
+/* grpo_nf4_linear_partials with x = bf16(bf16(silu(g)) * u), g and u the
+ * finished gate and up halves of the gate|up projection given by its partial
+ * sums (no bias or LoRA, at most 2 K slices; gate_up->N = 2 * parts->K),
+ * computed while the kernel stages x: fused_silu_mul (fused_ops.py:79-112)
+ * feeding down_proj in fused_mlp (fused_ops.py:184-193). */
+int grpo_nf4_linear_partials_silu(const grpo_linear_parts_t* gate_up, const uint8_t* w,
+                                  const float* absmax, const float* code16, int blocksize,
+                                  const grpo_linear_parts_t* parts, grpo_stream_t stream);
+
 /* ------------------------------------------------------- decode step --
  * Ops of the model-level decode step around the two hot-path kernels
  * (src/triton_kernels/paged_kv.py:690-820).  bf16 tensors are row-major. */
