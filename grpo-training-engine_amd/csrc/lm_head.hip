@@ -1,0 +1,278 @@
+// bf16 lm_head GEMV with fused per-tile argmax, and the device-side greedy
+// advance of the decode step (src/triton_kernels/paged_kv.py:800-820 and
+// :418-450 greedy branch; the row bookkeeping of :938, :978).
+//
+// lm_head: logits[m, v] = bf16(x[m, :] . W[v, :]) for the M rows of a decode
+// step, W bf16 [V, K] (467 MB for Qwen2-1.5B: the largest single read of the
+// step).  One wave = 16 vocabulary rows over all of K on
+// v_mfma_f32_16x16x32_bf16 (A = x staged in LDS, B = W^T); W is streamed with
+// 16-byte loads, the next k-step's loads issued before the current one is
+// multiplied.  Each wave also reduces its 16 logits per row to (max, first
+// index) and writes that pair, so the argmax over V needs only a small second
+// pass instead of re-reading the logits.
+#include <math.h>
+
+#include "common.hpp"
+
+using namespace grpo;
+
+namespace {
+
+constexpr int LM_KSTEP = 256;
+constexpr int LM_WAVES = 16;  // vocabulary tiles per workgroup (x staged once per workgroup)
+constexpr int ADV_T = 1024;
+constexpr size_t LM_LDS_MAX = 163840;  // gfx950: 160 KiB of LDS per workgroup
+
+// Lets a kernel use more than 64 KiB of dynamic LDS (once per instantiation).
+template <typename K>
+int allow_lds(K kernel) {
+  static const int rc = hip_check(
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)LM_LDS_MAX),
+      "hipFuncSetAttribute");
+  return rc;
+}
+
+struct LmArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint16_t* w;
+  int V, K, M, NT;
+  uint16_t* logits;  // [M][ldl] or null
+  int64_t ldl;
+  float* pval;       // [M][NT]
+  int* pidx;         // [M][NT]
+};
+
+// Strictly better in the argmax order: larger value, or equal value at a
+// smaller index (the first maximum).  NaN never wins.
+__device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
+  return v > bv || (v == bv && i < bi);
+}
+
+template <int MT>
+__global__ void __launch_bounds__(64 * LM_WAVES) lm_head_argmax_kernel(LmArgs p) {
+  extern __shared__ __align__(16) uint16_t xs[];  // [M][K + 8]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  const int tile = blockIdx.x * LM_WAVES + wave;
+  const int xstride = p.K + 8;
+  const int KS = p.K / LM_KSTEP;
+
+  // First k-step of W, then x into LDS.
+  const bool live = tile < p.NT;
+  const uint16_t* wrow = p.w + (int64_t)(live ? tile * 16 + ln : 0) * p.K + 64 * lg;
+  uint4 wa[8], wb[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) wa[j] = live ? *reinterpret_cast<const uint4*>(wrow + 8 * j)
+                                           : make_uint4(0, 0, 0, 0);
+  {
+    const int chunks = p.K / 8, total = p.M * chunks;
+    for (int i = tid; i < total; i += 64 * LM_WAVES) {
+      const int m = i / chunks, c = i - m * chunks;
+      *reinterpret_cast<uint4*>(xs + m * xstride + 8 * c) =
+          *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + 8 * c);
+    }
+  }
+  __syncthreads();
+  if (!live) return;
+
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xrow[mt] = xs + min(mt * 16 + ln, p.M - 1) * xstride + 64 * lg;
+
+  for (int ks = 0; ks < KS; ks += 2) {
+    if (ks + 1 < KS) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        wb[j] = *reinterpret_cast<const uint4*>(wrow + (ks + 1) * LM_KSTEP + 8 * j);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = mfma16x16x32(
+            *reinterpret_cast<const uint4*>(xrow[mt] + ks * LM_KSTEP + 8 * j), wa[j], acc[mt]);
+    if (ks + 1 >= KS) break;
+    if (ks + 2 < KS) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        wa[j] = *reinterpret_cast<const uint4*>(wrow + (ks + 2) * LM_KSTEP + 8 * j);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = mfma16x16x32(
+            *reinterpret_cast<const uint4*>(xrow[mt] + (ks + 1) * LM_KSTEP + 8 * j), wb[j],
+            acc[mt]);
+  }
+
+  // lane (n = ln, group lg) holds logits[m = mt*16 + 4*lg + q][tile*16 + ln].
+  const int v = tile * 16 + ln;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int m = mt * 16 + 4 * lg + q;
+      const uint16_t b = f2bf(acc[mt][q]);
+      float bv = bf2f(b);
+      int bi = v;
+      if (bv != bv) {  // NaN never wins
+        bv = -INFINITY;
+        bi = 0x7fffffff;
+      }
+      // (max, first index) over the 16 lanes of this lane group
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (better(ov, oi, bv, bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (m < p.M) {
+        if (p.logits) p.logits[(int64_t)m * p.ldl + v] = b;
+        if (ln == 0) {
+          p.pval[(int64_t)m * p.NT + tile] = bv;
+          p.pidx[(int64_t)m * p.NT + tile] = bi;
+        }
+      }
+    }
+}
+
+// Greedy token of row m from the per-tile (max, index) pairs, then the row's
+// decode bookkeeping: record the token, advance the lengths, stop at EOS or the
+// row's limit, and set the next step's append slot / attention length.
+__global__ void __launch_bounds__(ADV_T) decode_advance_kernel(
+    const float* __restrict__ pval, const int* __restrict__ pidx, int NT, int64_t* next_out,
+    int64_t* tokens, int32_t* pos, int32_t* count, const int32_t* limit, uint8_t* active,
+    const int64_t* eos, int64_t* generated, int64_t gen_ld, int32_t* append_pos,
+    int32_t* attn_len) {
+  __shared__ float sv[ADV_T / 64];
+  __shared__ int si[ADV_T / 64];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  float bv = -INFINITY;
+  int bi = 0x7fffffff;
+  for (int t = tid; t < NT; t += ADV_T) {
+    const float v = pval[(int64_t)m * NT + t];
+    const int i = pidx[(int64_t)m * NT + t];
+    if (better(v, i, bv, bi)) {
+      bv = v;
+      bi = i;
+    }
+  }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const float ov = __shfl_xor(bv, o);
+    const int oi = __shfl_xor(bi, o);
+    if (better(ov, oi, bv, bi)) {
+      bv = ov;
+      bi = oi;
+    }
+  }
+  if ((tid & 63) == 0) {
+    sv[tid >> 6] = bv;
+    si[tid >> 6] = bi;
+  }
+  __syncthreads();
+  if (tid != 0) return;
+  for (int w = 1; w < ADV_T / 64; ++w)
+    if (better(sv[w], si[w], bv, bi)) {
+      bv = sv[w];
+      bi = si[w];
+    }
+  const int64_t g = bi == 0x7fffffff ? 0 : bi;
+  if (next_out) next_out[m] = g;
+  if (!tokens) return;
+  const bool a = active[m] != 0;
+  if (a) {
+    const int c = count[m];
+    if (generated && c >= 0 && c < gen_ld) generated[(int64_t)m * gen_ld + c] = g;
+    pos[m] += 1;
+    count[m] = c + 1;
+  }
+  const bool still = a && count[m] < limit[m] && g != eos[0];
+  active[m] = still ? 1 : 0;
+  tokens[m] = g;
+  append_pos[m] = still ? pos[m] : -1;
+  attn_len[m] = still ? pos[m] + 1 : 0;
+}
+
+}  // namespace
+
+extern "C" size_t grpo_lm_head_workspace_bytes(int M, int V) {
+  if (M <= 0 || V <= 0) return 0;
+  return (size_t)M * cdiv(V, 16) * 8;
+}
+
+extern "C" int grpo_lm_head_argmax(const void* x, int64_t ldx, const void* w, int V, int K, int M,
+                                   void* logits, int64_t ld_logits, void* workspace,
+                                   size_t workspace_bytes, grpo_stream_t stream) {
+  if (M <= 0 || V <= 0 || K <= 0) return einval("bad lm_head dimensions");
+  if (M > 64) return einval("lm_head argmax supports M <= 64 rows");
+  if (V % 16 || K % LM_KSTEP) return einval("lm_head needs V % 16 == 0 and K % 256 == 0");
+  if (!x || !w || !workspace) return einval("null pointer");
+  if (ldx < K || ldx % 8 || !aligned16(x) || !aligned16(w))
+    return einval("x and W must be 16-byte aligned with ldx >= K, ldx % 8 == 0");
+  if (logits && ld_logits < V) return einval("ld_logits smaller than V");
+  const size_t need = grpo_lm_head_workspace_bytes(M, V);
+  if (workspace_bytes < need) {
+    set_error("invalid argument: workspace of %zu bytes needed, %zu given", need,
+              workspace_bytes);
+    return GRPO_EWORKSPACE;
+  }
+  const size_t lds = (size_t)M * (K + 8) * 2;
+  if (lds > LM_LDS_MAX) {
+    set_error("lm_head: x [M, K] does not fit in LDS (M * (K + 8) * 2 > 160 KiB)");
+    return GRPO_EUNSUPPORTED;
+  }
+  LmArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.w = static_cast<const uint16_t*>(w);
+  a.V = V;
+  a.K = K;
+  a.M = M;
+  a.NT = V / 16;
+  a.logits = static_cast<uint16_t*>(logits);
+  a.ldl = ld_logits;
+  a.pval = static_cast<float*>(workspace);
+  a.pidx = reinterpret_cast<int*>(a.pval + (size_t)M * a.NT);
+  const dim3 grid((unsigned)cdiv(a.NT, LM_WAVES)), block(64 * LM_WAVES);
+  hipStream_t st = as_stream(stream);
+  if (M <= 16) {
+    if (int rc = allow_lds(lm_head_argmax_kernel<1>)) return rc;
+    lm_head_argmax_kernel<1><<<grid, block, lds, st>>>(a);
+  } else if (M <= 32) {
+    if (int rc = allow_lds(lm_head_argmax_kernel<2>)) return rc;
+    lm_head_argmax_kernel<2><<<grid, block, lds, st>>>(a);
+  } else {
+    if (int rc = allow_lds(lm_head_argmax_kernel<4>)) return rc;
+    lm_head_argmax_kernel<4><<<grid, block, lds, st>>>(a);
+  }
+  return launch_check("lm_head_argmax");
+}
+
+extern "C" int grpo_decode_advance(const void* lm_workspace, int M, int V, int64_t* next_tokens,
+                                   int64_t* tokens, int32_t* pos, int32_t* count,
+                                   const int32_t* limit, uint8_t* active, const int64_t* eos,
+                                   int64_t* generated, int64_t gen_ld, int32_t* append_pos,
+                                   int32_t* attn_len, grpo_stream_t stream) {
+  if (M <= 0 || V <= 0 || V % 16) return einval("bad advance dimensions");
+  if (!lm_workspace) return einval("null workspace");
+  if (tokens && (!pos || !count || !limit || !active || !eos || !append_pos || !attn_len))
+    return einval("null row state");
+  if (generated && gen_ld <= 0) return einval("gen_ld must be > 0");
+  const int NT = V / 16;
+  const float* pval = static_cast<const float*>(lm_workspace);
+  const int* pidx = reinterpret_cast<const int*>(pval + (size_t)M * NT);
+  decode_advance_kernel<<<dim3(M), ADV_T, 0, as_stream(stream)>>>(
+      pval, pidx, NT, next_tokens, tokens, pos, count, limit, active, eos, generated, gen_ld,
+      append_pos, attn_len);
+  return launch_check("decode_advance");
+}

@@ -21,7 +21,7 @@ NATIVE_DIR = PKG_DIR / "_native"
 LIB_PATH = NATIVE_DIR / "libgrpo_hip.so"
 ARCH = "gfx950"
 
-SOURCES = ("capi.hip", "nf4_linear.hip", "paged_attention.hip", "decode_ops.hip")
+SOURCES = ("capi.hip", "nf4_linear.hip", "paged_attention.hip", "decode_ops.hip", "lm_head.hip")
 
 
 def hipcc() -> str:

@@ -84,6 +84,13 @@ SIGNATURES = {
     ),
     "grpo_silu_mul_parts": (_I32, [_PARTS, _VP, _I64, _VP]),
     "grpo_argmax_bf16": (_I32, [_VP, _I64, _I32, _I32, _VP, _VP]),
+    "grpo_lm_head_workspace_bytes": (_SZ, [_I32, _I32]),
+    "grpo_lm_head_argmax": (
+        _I32, [_VP, _I64, _VP, _I32, _I32, _I32, _VP, _I64, _VP, _SZ, _VP]),
+    "grpo_decode_advance": (
+        _I32,
+        [_VP, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _VP, _VP, _VP],
+    ),
     "grpo_paged_kv_append": (
         _I32,
         [_VP, _VP, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _I32, _I32, _I32, _I32, _I32, _VP],

@@ -11,7 +11,8 @@ per layer --
   add+RMSNorm (finishes o_proj) -> gate|up NF4 partials (one launch) ->
   down NF4 partials (finishes gate|up and applies SiLU*mul while staging x)
 
--- then the final norm, the bf16 lm_head and greedy argmax.  Each NF4 linear
+-- then the final norm, the bf16 lm_head GEMV with the first argmax pass, and
+one kernel that finishes the argmax and advances every row's state.  Each NF4 linear
 is a split-K launch that writes float32 partial sums; the op that consumes its
 output sums them and applies the linear's epilogue (bias, LoRA, bf16 rounding)
 itself, so no launch is spent on finishing a linear.  Lengths, block tables
@@ -167,6 +168,12 @@ class DecodeEngine:
         self.ws_attn = ops.workspace("paged_attn", max(ops.paged_attention_workspace_bytes(
             B, Hq, self.Hkv, D, self.pool.block_size, self.max_blocks), 1), dev)
         self.plans = plans
+        # bf16 lm_head GEMV with fused argmax + device-side row advance, when
+        # x [B, H] fits the kernel's LDS; otherwise hipBLASLt + argmax + torch ops.
+        lm_bytes = int(self.lib.grpo_lm_head_workspace_bytes(B, self.V))
+        self.lm_fused = (self.V % 16 == 0 and H % 256 == 0 and B <= 64
+                         and B * (H + 8) * 2 <= 160 * 1024)
+        self.ws_lm = torch.empty(max(lm_bytes, 16), dtype=torch.uint8, device=dev)
         # down_proj stages SiLU(gate) * up straight from the gate|up partial
         # sums when they have at most 2 K slices (the fused kernel's limit)
         self.fuse_silu = plans["gate_up"][0] <= 2
@@ -242,9 +249,23 @@ class DecodeEngine:
         out.append(("rmsnorm", lambda P=prev: chk(lib.grpo_add_rmsnorm_parts(
             P["down_parts"], h, h, self.final_norm.data_ptr(), x, self.final_eps, st),
             "final_norm")))
-        out.append(("lm_head", lambda: torch.matmul(self.x, self.lm_head.t(), out=self.logits)))
-        out.append(("argmax", lambda: chk(lib.grpo_argmax_bf16(
-            self.logits.data_ptr(), self.V, self.V, B, self.next.data_ptr(), st), "argmax")))
+        if self.lm_fused:
+            gen = self.generated
+            out.append(("lm_head", lambda: chk(lib.grpo_lm_head_argmax(
+                x, H, self.lm_head.data_ptr(), self.V, H, B, self.logits.data_ptr(), self.V,
+                self.ws_lm.data_ptr(), self.ws_lm.numel(), st), "lm_head")))
+            out.append(("advance", lambda: chk(lib.grpo_decode_advance(
+                self.ws_lm.data_ptr(), B, self.V, self.next.data_ptr(), self.tokens.data_ptr(),
+                self.pos.data_ptr(), self.count.data_ptr(), self.limit.data_ptr(),
+                self.active.data_ptr(), self.eos.data_ptr(),
+                None if gen is None else gen.data_ptr(), 0 if gen is None else gen.shape[1],
+                self.append_pos.data_ptr(), self.attn_len.data_ptr(), st), "advance")))
+        else:
+            out.append(("lm_head",
+                        lambda: torch.matmul(self.x, self.lm_head.t(), out=self.logits)))
+            out.append(("argmax", lambda: chk(lib.grpo_argmax_bf16(
+                self.logits.data_ptr(), self.V, self.V, B, self.next.data_ptr(), st),
+                "argmax")))
         return out
 
     def nf4_launches(self) -> list:
@@ -276,7 +297,8 @@ class DecodeEngine:
 
     def _step(self):
         self._forward()
-        self._advance(self.next)
+        if not self.lm_fused:  # the fused path advanced the rows on the device
+            self._advance(self.next)
 
     # ------------------------------------------------------------ control --
     def start(self, tokens: torch.Tensor, positions: torch.Tensor, block_tables: torch.Tensor,

@@ -278,6 +278,32 @@ int grpo_qkv_rope_append_parts(const grpo_linear_parts_t* qkv, int Hq, int Hkv, 
 int grpo_silu_mul_parts(const grpo_linear_parts_t* gate_up, void* out, int64_t ldo,
                         grpo_stream_t stream);
 
+/* Workspace bytes of grpo_lm_head_argmax (per-tile maxima) for M rows, vocab V. */
+size_t grpo_lm_head_workspace_bytes(int M, int V);
+
+/* logits[m, v] = bf16(x[m, :] . W[v, :]) (x bf16 [M, K] row stride ldx, W bf16
+ * [V, K]; logits bf16 row stride ld_logits, or NULL to skip storing them) and,
+ * in the workspace, the (max, first index) of every 16-column tile of every
+ * row for grpo_decode_advance.  The bf16 lm_head of _step
+ * (paged_kv.py:800-806) followed by the first pass of the greedy argmax
+ * (paged_kv.py:444-445).  Needs V % 16 == 0, K % 256 == 0, M <= 64 and
+ * M * (K + 8) * 2 <= 160 KiB (GRPO_EUNSUPPORTED otherwise). */
+int grpo_lm_head_argmax(const void* x, int64_t ldx, const void* w, int V, int K, int M,
+                        void* logits, int64_t ld_logits, void* workspace, size_t workspace_bytes,
+                        grpo_stream_t stream);
+
+/* Greedy token of every row from grpo_lm_head_argmax's workspace (first index
+ * of the maximum), written to next_tokens (may be NULL), and the decode loop's
+ * per-row bookkeeping (paged_kv.py:903-980, with per-row stop lengths): for an
+ * active row, generated[m, count[m]] = token (generated may be NULL), pos and
+ * count advance; the row stays active while count < limit and token != eos[0];
+ * tokens[m] = token; append_pos[m] = active ? pos : -1; attn_len[m] = active ?
+ * pos + 1 : 0.  tokens == NULL computes next_tokens only.  active is uint8 (0/1). */
+int grpo_decode_advance(const void* lm_workspace, int M, int V, int64_t* next_tokens,
+                        int64_t* tokens, int32_t* pos, int32_t* count, const int32_t* limit,
+                        uint8_t* active, const int64_t* eos, int64_t* generated, int64_t gen_ld,
+                        int32_t* append_pos, int32_t* attn_len, grpo_stream_t stream);
+
 /* out[m] = first index of the maximum of logits[m, :V] (bf16, row stride ld);
  * greedy sampling of _sample_tokens / fused_logits_sampling (paged_kv.py:444-445,
  * fused_ops.py:232-234). */

@@ -25,7 +25,7 @@ def _model(dev, layers=2, seed=3):
     from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
 
     cfg = Qwen2Config.tiny(layers=layers, heads=4, kv_heads=2, head_dim=128, inter=1024,
-                           vocab=1000)
+                           vocab=1024)  # V % 16 == 0: the fused lm_head + advance path
     return build_random_model(cfg, dev, seed=seed)
 
 
@@ -160,7 +160,7 @@ def test_paged_kv_decode_accepts_transformers_model(dev):
     from grpo_mi355x.kernels import paged_kv_decode
     from grpo_mi355x.rollout.adapt import decode_model_from
 
-    hf = build_hf_nf4_lora_model(seed=4, layers=2, device=dev)
+    hf = build_hf_nf4_lora_model(seed=4, layers=2, device=dev)  # vocab 1000: hipBLASLt path
     w, c = export(hf, decode_model_from(hf).config)
     oracle = Qwen2DecodeOracle(w, c)
     g = np.random.default_rng(7)
@@ -183,3 +183,55 @@ def test_paged_kv_decode_accepts_transformers_model(dev):
             tok = int(nxt[0])
     for row in range(G):
         assert np.array_equal(got[row], np.array(ref))
+
+
+def test_lm_head_argmax_and_advance(dev):
+    """bf16 lm_head GEMV + first-index argmax + the row bookkeeping, vs torch."""
+    from grpo_mi355x import _lib
+
+    lib = _lib.device_library()
+    st = _lib.stream_handle(dev)
+    g = torch.Generator().manual_seed(11)
+    M, V, K = 8, 4096, 512
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(V, K, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    w[100:104] = w[5]  # exact ties: the first index must win
+    x[3] = 0.0         # an all-zero row: every logit ties at 0 -> index 0
+    logits = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(int(lib.grpo_lm_head_workspace_bytes(M, V)), dtype=torch.uint8, device=dev)
+    _lib.check(lib.grpo_lm_head_argmax(x.data_ptr(), K, w.data_ptr(), V, K, M, logits.data_ptr(),
+                                       V, ws.data_ptr(), ws.numel(), st), "lm_head")
+    ref = (x.float() @ w.float().t())
+    assert rel_err(logits.float().cpu().numpy(), ref.cpu().numpy()) <= 1e-2
+    # row state: rows 0..7 with different activity / limits / eos hits
+    nxt = torch.full((M,), -5, dtype=torch.int64, device=dev)
+    tokens = torch.zeros(M, dtype=torch.int64, device=dev)
+    pos = torch.arange(10, 10 + M, dtype=torch.int32, device=dev)
+    count = torch.tensor([0, 1, 2, 3, 4, 5, 6, 7], dtype=torch.int32, device=dev)
+    limit = torch.tensor([9, 2, 9, 9, 9, 9, 9, 9], dtype=torch.int32, device=dev)
+    active = torch.tensor([1, 1, 0, 1, 1, 1, 1, 1], dtype=torch.uint8, device=dev)
+    gen = torch.full((M, 9), -1, dtype=torch.int64, device=dev)
+    greedy_ref = logits.float().argmax(dim=1)  # torch: first index of the maximum
+    eos = torch.tensor([int(greedy_ref[4])], dtype=torch.int64, device=dev)
+    app = torch.zeros(M, dtype=torch.int32, device=dev)
+    alen = torch.zeros(M, dtype=torch.int32, device=dev)
+    _lib.check(lib.grpo_decode_advance(ws.data_ptr(), M, V, nxt.data_ptr(), tokens.data_ptr(),
+                                       pos.data_ptr(), count.data_ptr(), limit.data_ptr(),
+                                       active.data_ptr(), eos.data_ptr(), gen.data_ptr(), 9,
+                                       app.data_ptr(), alen.data_ptr(), st), "advance")
+    torch.cuda.synchronize()
+    assert torch.equal(nxt, greedy_ref) and int(nxt[3]) == 0
+    assert torch.equal(tokens, nxt)
+    was = [1, 1, 0, 1, 1, 1, 1, 1]
+    for m in range(M):
+        c0 = [0, 1, 2, 3, 4, 5, 6, 7][m]
+        if was[m]:
+            assert int(gen[m, c0]) == int(nxt[m]) and int(count[m]) == c0 + 1
+            assert int(pos[m]) == 10 + m + 1
+        else:
+            assert torch.all(gen[m] == -1) and int(count[m]) == c0 and int(pos[m]) == 10 + m
+        still = bool(was[m]) and int(count[m]) < int(limit[m]) and int(nxt[m]) != int(eos[0])
+        assert bool(active[m]) == still
+        assert int(app[m]) == (int(pos[m]) if still else -1)
+        assert int(alen[m]) == (int(pos[m]) + 1 if still else 0)
+    assert not bool(active[1]) and not bool(active[4])  # limit reached / EOS
