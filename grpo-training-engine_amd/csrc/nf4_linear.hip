@@ -168,21 +168,28 @@ constexpr int GU_MAX_SLICES = 2;  // K slices of the gate|up partial sums read w
 
 // Columns k..k+7 of row m of bf16(bf16(silu(g)) * u), with g = bf16(sum of the
 // gate partials), u = bf16(sum of the up partials) (fused_ops.py:79-112 applied
-// to the finished gate|up output).
-__device__ __forceinline__ uint4 silu_chunk(const PartArgs& p, int m, int k) {
+// to the finished gate|up output).  silu_fetch issues the loads, silu_finish
+// combines them, so the loads can go out before the kernel's weight loads.
+struct SiluFetch {
+  float4 g[GU_MAX_SLICES][2], u[GU_MAX_SLICES][2];
+};
+
+__device__ __forceinline__ void silu_fetch(const PartArgs& p, int m, int k, SiluFetch& f) {
   const int64_t row = (int64_t)m * 2 * p.K;
   const int64_t stride = (int64_t)p.M * 2 * p.K / 4;
   const float4* pg = reinterpret_cast<const float4*>(p.gu_part + row + k);
   const float4* pu = reinterpret_cast<const float4*>(p.gu_part + row + p.K + k);
-  float4 g[GU_MAX_SLICES][2], u[GU_MAX_SLICES][2];
 #pragma unroll
   for (int s = 0; s < GU_MAX_SLICES; ++s)
     if (s < p.gu_S) {
-      g[s][0] = pg[s * stride];
-      g[s][1] = pg[s * stride + 1];
-      u[s][0] = pu[s * stride];
-      u[s][1] = pu[s * stride + 1];
+      f.g[s][0] = pg[s * stride];
+      f.g[s][1] = pg[s * stride + 1];
+      f.u[s][0] = pu[s * stride];
+      f.u[s][1] = pu[s * stride + 1];
     }
+}
+
+__device__ __forceinline__ uint4 silu_finish(const PartArgs& p, const SiluFetch& f) {
   float gs[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float us[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -190,14 +197,14 @@ __device__ __forceinline__ uint4 silu_chunk(const PartArgs& p, int m, int k) {
     if (s < p.gu_S) {
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        gs[4 * h + 0] += g[s][h].x;
-        gs[4 * h + 1] += g[s][h].y;
-        gs[4 * h + 2] += g[s][h].z;
-        gs[4 * h + 3] += g[s][h].w;
-        us[4 * h + 0] += u[s][h].x;
-        us[4 * h + 1] += u[s][h].y;
-        us[4 * h + 2] += u[s][h].z;
-        us[4 * h + 3] += u[s][h].w;
+        gs[4 * h + 0] += f.g[s][h].x;
+        gs[4 * h + 1] += f.g[s][h].y;
+        gs[4 * h + 2] += f.g[s][h].z;
+        gs[4 * h + 3] += f.g[s][h].w;
+        us[4 * h + 0] += f.u[s][h].x;
+        us[4 * h + 1] += f.u[s][h].y;
+        us[4 * h + 2] += f.u[s][h].z;
+        us[4 * h + 3] += f.u[s][h].w;
       }
     }
   float o[8];
@@ -208,6 +215,12 @@ __device__ __forceinline__ uint4 silu_chunk(const PartArgs& p, int m, int k) {
   }
   return make_uint4(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]), pack_bf2(o[4], o[5]),
                     pack_bf2(o[6], o[7]));
+}
+
+__device__ __forceinline__ uint4 silu_chunk(const PartArgs& p, int m, int k) {
+  SiluFetch f;
+  silu_fetch(p, m, k, f);
+  return silu_finish(p, f);
 }
 
 // Eight consecutive columns k..k+7 (one head, d0 = k % 128) of row m of the
@@ -277,6 +290,36 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   const bool wtile = tile < p.NT;
   const int n_row = tile * 16 + ln;
 
+  // Vector loads retire in issue order, so whatever the staging must wait for
+  // is issued BEFORE the weight loads: the first batch of x (bf16 source) or
+  // of the gate|up partial sums (SiLU source).  Otherwise the staging barrier
+  // would wait for the whole workgroup's weights and no decode could overlap
+  // the weight stream.
+  const int chunks = nk * (KSTEP / 8);
+  const int total = p.M * chunks;
+  uint4 xv[4];
+  constexpr int SF = 2;  // SiLU chunks per thread fetched ahead
+  SiluFetch sf[SF];
+  if (XSRC == X_BF16) {
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = u * NT + tid;
+      if (i < total) {
+        const int m = i / chunks, c = i - m * chunks;
+        xv[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase + 8 * c);
+      }
+    }
+  } else if (XSRC == X_SILU) {
+#pragma unroll
+    for (int u = 0; u < SF; ++u) {
+      const int i = u * NT + tid;
+      if (i < total) {
+        const int m = i / chunks, c = i - m * chunks;
+        silu_fetch(p, m, kbase + 8 * c, sf[u]);
+      }
+    }
+  }
+
   // 1. Weight and absmax loads of every k-step, issued before any use.
   uint4 wv[2 * KPW];
   float av[KPW];
@@ -297,32 +340,31 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
     }
   }
 
-  // 2. Stage x[:, kbase : kbase + nk*256] in LDS, four 16-byte loads per thread in flight.
-  {
-    const int chunks = nk * (KSTEP / 8);
-    const int total = p.M * chunks;
-    for (int base = 0; base < total; base += 4 * NT) {
-      uint4 v[4];
+  // 2. Stage x[:, kbase : kbase + nk*256] in LDS (decode8 order), four chunks
+  //    per thread per batch.
+  for (int base = 0; base < total; base += 4 * NT) {
+    uint4 v[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = base + u * NT + tid;
-        if (i < total) {
-          const int m = i / chunks, c = i - m * chunks;
-          if (XSRC == X_ATTN)
-            v[u] = attn_chunk(p, m, kbase + 8 * c);
-          else if (XSRC == X_SILU)
-            v[u] = silu_chunk(p, m, kbase + 8 * c);
-          else
-            v[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase + 8 * c);
-        }
+    for (int u = 0; u < 4; ++u) {
+      const int i = base + u * NT + tid;
+      if (i < total) {
+        const int m = i / chunks, c = i - m * chunks;
+        if (XSRC == X_ATTN)
+          v[u] = attn_chunk(p, m, kbase + 8 * c);
+        else if (XSRC == X_SILU)
+          v[u] = base == 0 && u < SF ? silu_finish(p, sf[u]) : silu_chunk(p, m, kbase + 8 * c);
+        else
+          v[u] = base == 0 ? xv[u]
+                           : *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase +
+                                                             8 * c);
       }
+    }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int i = base + u * NT + tid;
-        if (i < total) {
-          const int m = i / chunks, c = i - m * chunks;
-          *reinterpret_cast<uint4*>(xs + m * p.xstride + 8 * c) = deinterleave8(v[u]);
-        }
+    for (int u = 0; u < 4; ++u) {
+      const int i = base + u * NT + tid;
+      if (i < total) {
+        const int m = i / chunks, c = i - m * chunks;
+        *reinterpret_cast<uint4*>(xs + m * p.xstride + 8 * c) = deinterleave8(v[u]);
       }
     }
   }
