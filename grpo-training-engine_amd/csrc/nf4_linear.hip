@@ -174,19 +174,21 @@ struct SiluFetch {
   float4 g[GU_MAX_SLICES][2], u[GU_MAX_SLICES][2];
 };
 
+// Loads are unconditional (slices >= gu_S re-read the last slice and are not
+// summed), so the compiler can count them: see nf4_part_mfma.
 __device__ __forceinline__ void silu_fetch(const PartArgs& p, int m, int k, SiluFetch& f) {
   const int64_t row = (int64_t)m * 2 * p.K;
   const int64_t stride = (int64_t)p.M * 2 * p.K / 4;
   const float4* pg = reinterpret_cast<const float4*>(p.gu_part + row + k);
   const float4* pu = reinterpret_cast<const float4*>(p.gu_part + row + p.K + k);
 #pragma unroll
-  for (int s = 0; s < GU_MAX_SLICES; ++s)
-    if (s < p.gu_S) {
-      f.g[s][0] = pg[s * stride];
-      f.g[s][1] = pg[s * stride + 1];
-      f.u[s][0] = pu[s * stride];
-      f.u[s][1] = pu[s * stride + 1];
-    }
+  for (int s = 0; s < GU_MAX_SLICES; ++s) {
+    const int64_t o = (int64_t)min(s, p.gu_S - 1) * stride;
+    f.g[s][0] = pg[o];
+    f.g[s][1] = pg[o + 1];
+    f.u[s][0] = pu[o];
+    f.u[s][1] = pu[o + 1];
+  }
 }
 
 __device__ __forceinline__ uint4 silu_finish(const PartArgs& p, const SiluFetch& f) {
@@ -227,50 +229,64 @@ __device__ __forceinline__ uint4 silu_chunk(const PartArgs& p, int m, int k) {
 // attention output, merged over its context splits:
 // O = sum_s 2^(m_s - M) O_s / max(sum_s 2^(m_s - M) l_s, 1e-6), rounded to bf16
 // (the reference's float32 attention output cast to the model dtype).
-__device__ __forceinline__ uint4 attn_chunk(const PartArgs& p, int m, int k) {
+// attn_fetch loads every split slot (slots >= att_S re-read the last one; only
+// the row's ns <= att_S used splits are merged): the addresses do not depend
+// on the context length, so these loads can be issued before the weights.
+struct AttnFetch {
+  float4 o0[ATTN_MAX_SPLITS], o1[ATTN_MAX_SPLITS];
+  float2 ml[ATTN_MAX_SPLITS];
+  int len;
+};
+
+__device__ __forceinline__ void attn_fetch(const PartArgs& p, int m, int k, AttnFetch& f) {
   const int hq = k >> 7, d0 = k & 127;
-  int ctx = p.att_len[m];
+  f.len = p.att_len[m];
+  const int64_t base = ((int64_t)m * p.att_Hq + hq) * p.att_S;
+#pragma unroll
+  for (int s = 0; s < ATTN_MAX_SPLITS; ++s) {
+    const int64_t sl = base + min(s, p.att_S - 1);
+    f.ml[s] = *reinterpret_cast<const float2*>(p.att_ml + sl * 2);
+    const float4* op = reinterpret_cast<const float4*>(p.att_o + sl * 128 + d0);
+    f.o0[s] = op[0];
+    f.o1[s] = op[1];
+  }
+}
+
+__device__ __forceinline__ uint4 attn_finish(const PartArgs& p, const AttnFetch& f) {
+  int ctx = f.len;
   ctx = ctx < 0 ? 0 : (ctx > p.att_cap ? p.att_cap : ctx);
   const int nblk = (ctx + 15) / 16;
   const int ns = nblk > 0 ? (nblk + p.att_bps - 1) / p.att_bps : 1;
-  const int64_t base = ((int64_t)m * p.att_Hq + hq) * p.att_S;
-  float ms[ATTN_MAX_SPLITS], ls[ATTN_MAX_SPLITS];
-  float4 o0[ATTN_MAX_SPLITS], o1[ATTN_MAX_SPLITS];
-#pragma unroll
-  for (int s = 0; s < ATTN_MAX_SPLITS; ++s) {
-    if (s < ns) {
-      const float2 ml = *reinterpret_cast<const float2*>(p.att_ml + (base + s) * 2);
-      ms[s] = ml.x;
-      ls[s] = ml.y;
-      const float4* op = reinterpret_cast<const float4*>(p.att_o + (base + s) * 128 + d0);
-      o0[s] = op[0];
-      o1[s] = op[1];
-    }
-  }
   float M = -INFINITY;
 #pragma unroll
   for (int s = 0; s < ATTN_MAX_SPLITS; ++s)
-    if (s < ns) M = fmaxf(M, ms[s]);
+    if (s < ns) M = fmaxf(M, f.ml[s].x);
   float L = 0.f, O[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   if (M != -INFINITY) {
 #pragma unroll
     for (int s = 0; s < ATTN_MAX_SPLITS; ++s)
       if (s < ns) {
-        const float f = exp2f(ms[s] - M);
-        L += f * ls[s];
-        O[0] += f * o0[s].x;
-        O[1] += f * o0[s].y;
-        O[2] += f * o0[s].z;
-        O[3] += f * o0[s].w;
-        O[4] += f * o1[s].x;
-        O[5] += f * o1[s].y;
-        O[6] += f * o1[s].z;
-        O[7] += f * o1[s].w;
+        const float w = exp2f(f.ml[s].x - M);
+        L += w * f.ml[s].y;
+        O[0] += w * f.o0[s].x;
+        O[1] += w * f.o0[s].y;
+        O[2] += w * f.o0[s].z;
+        O[3] += w * f.o0[s].w;
+        O[4] += w * f.o1[s].x;
+        O[5] += w * f.o1[s].y;
+        O[6] += w * f.o1[s].z;
+        O[7] += w * f.o1[s].w;
       }
   }
   const float den = fmaxf(L, 1e-6f);
   return make_uint4(pack_bf2(O[0] / den, O[1] / den), pack_bf2(O[2] / den, O[3] / den),
                     pack_bf2(O[4] / den, O[5] / den), pack_bf2(O[6] / den, O[7] / den));
+}
+
+__device__ __forceinline__ uint4 attn_chunk(const PartArgs& p, int m, int k) {
+  AttnFetch f;
+  attn_fetch(p, m, k, f);
+  return attn_finish(p, f);
 }
 
 template <int MT, int KPW, int XSRC>
@@ -290,82 +306,93 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   const bool wtile = tile < p.NT;
   const int n_row = tile * 16 + ln;
 
-  // Vector loads retire in issue order, so whatever the staging must wait for
-  // is issued BEFORE the weight loads: the first batch of x (bf16 source) or
-  // of the gate|up partial sums (SiLU source).  Otherwise the staging barrier
-  // would wait for the whole workgroup's weights and no decode could overlap
-  // the weight stream.
+  // Load order.  Vector loads retire in issue order and the compiler waits for
+  // a load with s_waitcnt vmcnt(N), N = loads issued after it.  Every global
+  // load below is therefore unconditional (indexes clamped into range, extra
+  // values discarded) so that N is exact, and loads are issued in the order
+  // their data is needed: codebook, the first batch of the x source, then the
+  // weights k-step by k-step.  The staging then waits only for x, and decoding
+  // k-step i only for that step's weights while later steps are in flight.
+  // (With a conditional load anywhere in between, the compiler has to wait
+  // with vmcnt(0), i.e. for the whole workgroup's weights, before staging.)
+  float code[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
+
   const int chunks = nk * (KSTEP / 8);
   const int total = p.M * chunks;
   uint4 xv[4];
   constexpr int SF = 2;  // SiLU chunks per thread fetched ahead
   SiluFetch sf[SF];
+  AttnFetch af;  // one attention chunk per thread fetched ahead
   if (XSRC == X_BF16) {
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int i = u * NT + tid;
-      if (i < total) {
-        const int m = i / chunks, c = i - m * chunks;
-        xv[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase + 8 * c);
-      }
+      const int i = min(u * NT + tid, total - 1);
+      const int m = i / chunks, c = i - m * chunks;
+      xv[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase + 8 * c);
     }
   } else if (XSRC == X_SILU) {
 #pragma unroll
     for (int u = 0; u < SF; ++u) {
-      const int i = u * NT + tid;
-      if (i < total) {
-        const int m = i / chunks, c = i - m * chunks;
-        silu_fetch(p, m, kbase + 8 * c, sf[u]);
-      }
+      const int i = min(u * NT + tid, total - 1);
+      const int m = i / chunks, c = i - m * chunks;
+      silu_fetch(p, m, kbase + 8 * c, sf[u]);
     }
+  } else {
+    const int i = min(tid, total - 1);
+    const int m = i / chunks, c = i - m * chunks;
+    attn_fetch(p, m, kbase + 8 * c, af);
   }
+  // Keep the scheduler from hoisting the (cheaper to address) weight loads
+  // above the x loads.
+  __builtin_amdgcn_sched_barrier(0);
 
-  // 1. Weight and absmax loads of every k-step, issued before any use.
+  // Weight and absmax loads of every k-step.  LoRA and padding waves read row
+  // 0 and the last k-step is re-read past nk; those values are never used.
   uint4 wv[2 * KPW];
   float av[KPW];
   {
-    const uint8_t* wrow = p.w + (int64_t)(wtile ? n_row : 0) * (p.K / 2);
+    const int wr = wtile ? n_row : 0;
+    const uint8_t* wrow = p.w + (int64_t)wr * (p.K / 2);
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
-      if (wtile && i < nk) {
-        const int kc = kbase + i * KSTEP + 64 * lg;
-        const uint4* wp = reinterpret_cast<const uint4*>(wrow + kc / 2);
-        wv[2 * i] = wp[0];
-        wv[2 * i + 1] = wp[1];
-        av[i] = p.absmax[((int64_t)n_row * p.K + kc) >> p.bs_shift];
-      } else {
-        wv[2 * i] = wv[2 * i + 1] = make_uint4(0, 0, 0, 0);
-        av[i] = 0.f;
-      }
+      const int kc = kbase + min(i, nk - 1) * KSTEP + 64 * lg;
+      const uint4* wp = reinterpret_cast<const uint4*>(wrow + kc / 2);
+      wv[2 * i] = wp[0];
+      wv[2 * i + 1] = wp[1];
+      av[i] = p.absmax[((int64_t)wr * p.K + kc) >> p.bs_shift];
     }
   }
 
-  // 2. Stage x[:, kbase : kbase + nk*256] in LDS (decode8 order), four chunks
-  //    per thread per batch.
+  // Stage x[:, kbase : kbase + nk*256] in LDS (decode8 order), four chunks per
+  // thread per batch.  A batch entry that starts past the end is skipped by
+  // the whole workgroup (it would otherwise issue loads behind the weights);
+  // within a partial entry, indexes are clamped to the last chunk, which is
+  // then written twice with the same value.  At decode shapes every chunk
+  // comes from the loads issued above.
   for (int base = 0; base < total; base += 4 * NT) {
     uint4 v[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int i = base + u * NT + tid;
-      if (i < total) {
-        const int m = i / chunks, c = i - m * chunks;
-        if (XSRC == X_ATTN)
-          v[u] = attn_chunk(p, m, kbase + 8 * c);
-        else if (XSRC == X_SILU)
-          v[u] = base == 0 && u < SF ? silu_finish(p, sf[u]) : silu_chunk(p, m, kbase + 8 * c);
-        else
-          v[u] = base == 0 ? xv[u]
-                           : *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase +
-                                                             8 * c);
-      }
+      if (base + u * NT >= total) break;
+      const int i = min(base + u * NT + tid, total - 1);
+      const int m = i / chunks, c = i - m * chunks;
+      if (XSRC == X_ATTN)
+        v[u] = base == 0 && u == 0 ? attn_finish(p, af) : attn_chunk(p, m, kbase + 8 * c);
+      else if (XSRC == X_SILU)
+        v[u] = base == 0 && u < SF ? silu_finish(p, sf[u]) : silu_chunk(p, m, kbase + 8 * c);
+      else
+        v[u] = base == 0 ? xv[u]
+                         : *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase +
+                                                           8 * c);
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
-      const int i = base + u * NT + tid;
-      if (i < total) {
-        const int m = i / chunks, c = i - m * chunks;
-        *reinterpret_cast<uint4*>(xs + m * p.xstride + 8 * c) = deinterleave8(v[u]);
-      }
+      if (base + u * NT >= total) break;
+      const int i = min(base + u * NT + tid, total - 1);
+      const int m = i / chunks, c = i - m * chunks;
+      *reinterpret_cast<uint4*>(xs + m * p.xstride + 8 * c) = deinterleave8(v[u]);
     }
   }
   __syncthreads();
@@ -379,9 +406,6 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   for (int mt = 0; mt < MT; ++mt) xrow[mt] = xs + min(mt * 16 + ln, p.M - 1) * p.xstride + 64 * lg;
 
   if (wtile) {
-    float code[16];
-#pragma unroll
-    for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
       if (i >= nk) break;
