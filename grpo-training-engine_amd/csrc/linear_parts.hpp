@@ -41,6 +41,16 @@ __device__ __forceinline__ int lin_seg(const LinParts& o, int n) {
   return s;
 }
 
+// a[i] of a kernel-argument array for a per-lane i < MAXSEG, by selects over
+// the four uniform entries: indexing the argument array with a per-lane index
+// would read it with a dependent vector load instead of scalar loads.
+template <typename T>
+__device__ __forceinline__ T sel4(T a0, T a1, T a2, T a3, int i) {
+  return i == 0 ? a0 : (i == 1 ? a1 : (i == 2 ? a2 : a3));
+}
+static_assert(MAXSEG == 4, "sel_seg selects among four entries");
+#define sel_seg(a, i) sel4((a)[0], (a)[1], (a)[2], (a)[3], (i))
+
 constexpr int MAX_SLICES = 16;  // K slices of a split-K linear (the plan keeps S <= 16)
 
 // LoRA t of row m rounded to bf16, ts[seg*16 + j], computed by the whole
@@ -93,13 +103,48 @@ __device__ __forceinline__ void lin_fetch4(const LinParts& o, int m, int n, Fetc
   for (int k = 0; k < MS; ++k)
     if (k < o.S) f.part[k] = p[k * stride];
   f.seg = lin_seg(o, n);
-  f.nl = n - (f.seg > 0 ? o.seg_end[f.seg - 1] : 0);
-  if (o.bias[f.seg] && o.bias_vec) f.bias = *reinterpret_cast<const uint2*>(o.bias[f.seg] + f.nl);
+  f.nl = n - (f.seg > 0 ? sel_seg(o.seg_end, f.seg - 1) : 0);
+  const uint16_t* bias = sel_seg(o.bias, f.seg);
+  if (bias && o.bias_vec) f.bias = *reinterpret_cast<const uint2*>(bias + f.nl);
   if (o.r > 0 && o.lb_vec) {
-    const uint4* br = reinterpret_cast<const uint4*>(o.lb[f.seg] + (int64_t)f.nl * 16);
+    const uint4* br = reinterpret_cast<const uint4*>(sel_seg(o.lb, f.seg) + (int64_t)f.nl * 16);
 #pragma unroll
     for (int j = 0; j < 8; ++j) f.lb[j] = br[j];
   }
+}
+
+// LoRA t of row m in two steps, so a caller can issue other loads between
+// them: lin_fetch_t loads item i (one float4 of ranks of one segment, all
+// slices; i is clamped into range and slices >= S re-read the last one),
+// lin_store_t sums and stores the items i < nseg*4.
+template <int MS>
+__device__ __forceinline__ void lin_fetch_t(const LinParts& o, int m, int i, float4 (&v)[MS]) {
+  const int ic = max(0, min(i, o.nseg * 4 - 1));
+  const float* base = o.r > 0 ? o.tpart + ((int64_t)(ic >> 2) * o.M + m) * 16 : o.part;
+  const float4* p = reinterpret_cast<const float4*>(base) + (o.r > 0 ? (ic & 3) : 0);
+  const int64_t stride = o.r > 0 ? (int64_t)o.nseg * o.M * 4 : 0;
+#pragma unroll
+  for (int k = 0; k < MS; ++k) v[k] = p[min(k, o.S - 1) * stride];
+}
+
+template <int MS>
+__device__ __forceinline__ void lin_store_t(const LinParts& o, const float4 (&v)[MS], int i,
+                                            float* ts) {
+  if (o.r <= 0 || i >= o.nseg * 4) return;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int k = 0; k < MS; ++k)
+    if (k < o.S) {
+      acc.x += v[k].x;
+      acc.y += v[k].y;
+      acc.z += v[k].z;
+      acc.w += v[k].w;
+    }
+  float* t = ts + (i >> 2) * 16 + 4 * (i & 3);
+  t[0] = round_bf(acc.x);
+  t[1] = round_bf(acc.y);
+  t[2] = round_bf(acc.z);
+  t[3] = round_bf(acc.w);
 }
 
 // The reference's bf16 values (as floats) of the four outputs; ts holds the
@@ -120,7 +165,8 @@ __device__ __forceinline__ void lin_finish4(const LinParts& o, const float* ts,
   v[1] = round_bf(acc.y);
   v[2] = round_bf(acc.z);
   v[3] = round_bf(acc.w);
-  if (o.bias[f.seg]) {
+  const uint16_t* bias = sel_seg(o.bias, f.seg);
+  if (bias) {
     float b[4];
     if (o.bias_vec) {
       b[0] = bf_lo(f.bias.x);
@@ -129,7 +175,7 @@ __device__ __forceinline__ void lin_finish4(const LinParts& o, const float* ts,
       b[3] = bf_hi(f.bias.y);
     } else {
 #pragma unroll
-      for (int c = 0; c < 4; ++c) b[c] = bf2f(o.bias[f.seg][f.nl + c]);
+      for (int c = 0; c < 4; ++c) b[c] = bf2f(bias[f.nl + c]);
     }
 #pragma unroll
     for (int c = 0; c < 4; ++c) v[c] = round_bf(v[c] + b[c]);
@@ -149,7 +195,7 @@ __device__ __forceinline__ void lin_finish4(const LinParts& o, const float* ts,
           u += t[2 * j + 1] * bf_hi(bw[j]);
         }
       } else {
-        const uint16_t* br = o.lb[f.seg] + (int64_t)(f.nl + c) * o.r;
+        const uint16_t* br = sel_seg(o.lb, f.seg) + (int64_t)(f.nl + c) * o.r;
         for (int j = 0; j < o.r; ++j) u += t[j] * bf2f(br[j]);
       }
       u = round_bf(round_bf(u) * sc);

@@ -174,21 +174,19 @@ struct SiluFetch {
   float4 g[GU_MAX_SLICES][2], u[GU_MAX_SLICES][2];
 };
 
-// Loads are unconditional (slices >= gu_S re-read the last slice and are not
-// summed), so the compiler can count them: see nf4_part_mfma.
 __device__ __forceinline__ void silu_fetch(const PartArgs& p, int m, int k, SiluFetch& f) {
   const int64_t row = (int64_t)m * 2 * p.K;
   const int64_t stride = (int64_t)p.M * 2 * p.K / 4;
   const float4* pg = reinterpret_cast<const float4*>(p.gu_part + row + k);
   const float4* pu = reinterpret_cast<const float4*>(p.gu_part + row + p.K + k);
 #pragma unroll
-  for (int s = 0; s < GU_MAX_SLICES; ++s) {
-    const int64_t o = (int64_t)min(s, p.gu_S - 1) * stride;
-    f.g[s][0] = pg[o];
-    f.g[s][1] = pg[o + 1];
-    f.u[s][0] = pu[o];
-    f.u[s][1] = pu[o + 1];
-  }
+  for (int s = 0; s < GU_MAX_SLICES; ++s)
+    if (s < p.gu_S) {
+      f.g[s][0] = pg[s * stride];
+      f.g[s][1] = pg[s * stride + 1];
+      f.u[s][0] = pu[s * stride];
+      f.u[s][1] = pu[s * stride + 1];
+    }
 }
 
 __device__ __forceinline__ uint4 silu_finish(const PartArgs& p, const SiluFetch& f) {
@@ -229,9 +227,9 @@ __device__ __forceinline__ uint4 silu_chunk(const PartArgs& p, int m, int k) {
 // attention output, merged over its context splits:
 // O = sum_s 2^(m_s - M) O_s / max(sum_s 2^(m_s - M) l_s, 1e-6), rounded to bf16
 // (the reference's float32 attention output cast to the model dtype).
-// attn_fetch loads every split slot (slots >= att_S re-read the last one; only
-// the row's ns <= att_S used splits are merged): the addresses do not depend
-// on the context length, so these loads can be issued before the weights.
+// attn_fetch loads every allocated split slot (only the row's ns <= att_S used
+// splits are merged): the addresses do not depend on the context length, so
+// these loads can be issued before the weights.
 struct AttnFetch {
   float4 o0[ATTN_MAX_SPLITS], o1[ATTN_MAX_SPLITS];
   float2 ml[ATTN_MAX_SPLITS];
@@ -243,13 +241,14 @@ __device__ __forceinline__ void attn_fetch(const PartArgs& p, int m, int k, Attn
   f.len = p.att_len[m];
   const int64_t base = ((int64_t)m * p.att_Hq + hq) * p.att_S;
 #pragma unroll
-  for (int s = 0; s < ATTN_MAX_SPLITS; ++s) {
-    const int64_t sl = base + min(s, p.att_S - 1);
-    f.ml[s] = *reinterpret_cast<const float2*>(p.att_ml + sl * 2);
-    const float4* op = reinterpret_cast<const float4*>(p.att_o + sl * 128 + d0);
-    f.o0[s] = op[0];
-    f.o1[s] = op[1];
-  }
+  for (int s = 0; s < ATTN_MAX_SPLITS; ++s)
+    if (s < p.att_S) {
+      const int64_t sl = base + s;
+      f.ml[s] = *reinterpret_cast<const float2*>(p.att_ml + sl * 2);
+      const float4* op = reinterpret_cast<const float4*>(p.att_o + sl * 128 + d0);
+      f.o0[s] = op[0];
+      f.o1[s] = op[1];
+    }
 }
 
 __device__ __forceinline__ uint4 attn_finish(const PartArgs& p, const AttnFetch& f) {
@@ -307,14 +306,16 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   const int n_row = tile * 16 + ln;
 
   // Load order.  Vector loads retire in issue order and the compiler waits for
-  // a load with s_waitcnt vmcnt(N), N = loads issued after it.  Every global
-  // load below is therefore unconditional (indexes clamped into range, extra
-  // values discarded) so that N is exact, and loads are issued in the order
-  // their data is needed: codebook, the first batch of the x source, then the
-  // weights k-step by k-step.  The staging then waits only for x, and decoding
-  // k-step i only for that step's weights while later steps are in flight.
-  // (With a conditional load anywhere in between, the compiler has to wait
-  // with vmcnt(0), i.e. for the whole workgroup's weights, before staging.)
+  // a load with s_waitcnt vmcnt(N), N = loads issued after it; after a
+  // conditional load it can only assume the fewest loads, so a conditional
+  // load makes the waits of the loads issued BEFORE it conservative, never of
+  // those after it.  Hence: the codebook (scalar loads), then the first batch
+  // of the x source (predicated: only the chunks that exist), then the weights
+  // k-step by k-step, unconditional (indexes clamped into range, extra values
+  // discarded).  The staging then waits only for x, and decoding k-step i only
+  // for that step's weights while later steps are in flight.  (With the
+  // weight loads conditional, the staging had to wait with vmcnt(0), i.e. for
+  // the whole workgroup's weights.)
   float code[16];
 #pragma unroll
   for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
@@ -326,8 +327,12 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   SiluFetch sf[SF];
   AttnFetch af;  // one attention chunk per thread fetched ahead
   if (XSRC == X_BF16) {
+    // bf16 x: whole batch entries past the end are skipped (uniform), a partial
+    // one re-reads the last chunk (clamped), so no load is predicated.  (The
+    // predicated form makes the compiler wait for every weight after staging.)
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
+      if (u * NT >= total) break;
       const int i = min(u * NT + tid, total - 1);
       const int m = i / chunks, c = i - m * chunks;
       xv[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase + 8 * c);
@@ -335,13 +340,14 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   } else if (XSRC == X_SILU) {
 #pragma unroll
     for (int u = 0; u < SF; ++u) {
-      const int i = min(u * NT + tid, total - 1);
-      const int m = i / chunks, c = i - m * chunks;
-      silu_fetch(p, m, kbase + 8 * c, sf[u]);
+      const int i = u * NT + tid;
+      if (i < total) {
+        const int m = i / chunks, c = i - m * chunks;
+        silu_fetch(p, m, kbase + 8 * c, sf[u]);
+      }
     }
-  } else {
-    const int i = min(tid, total - 1);
-    const int m = i / chunks, c = i - m * chunks;
+  } else if (tid < total) {
+    const int m = tid / chunks, c = tid - m * chunks;
     attn_fetch(p, m, kbase + 8 * c, af);
   }
   // Keep the scheduler from hoisting the (cheaper to address) weight loads
@@ -367,32 +373,37 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
 
   // Stage x[:, kbase : kbase + nk*256] in LDS (decode8 order), four chunks per
   // thread per batch.  A batch entry that starts past the end is skipped by
-  // the whole workgroup (it would otherwise issue loads behind the weights);
-  // within a partial entry, indexes are clamped to the last chunk, which is
-  // then written twice with the same value.  At decode shapes every chunk
-  // comes from the loads issued above.
+  // the whole workgroup.  The bf16 source clamps the chunk index (the last
+  // chunk is then written twice with the same value); the other sources
+  // predicate.  At decode shapes every chunk comes from the loads issued
+  // above; larger M stages the rest here, behind the weights.
+  constexpr bool CLAMP = XSRC == X_BF16;
   for (int base = 0; base < total; base += 4 * NT) {
     uint4 v[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       if (base + u * NT >= total) break;
-      const int i = min(base + u * NT + tid, total - 1);
-      const int m = i / chunks, c = i - m * chunks;
-      if (XSRC == X_ATTN)
-        v[u] = base == 0 && u == 0 ? attn_finish(p, af) : attn_chunk(p, m, kbase + 8 * c);
-      else if (XSRC == X_SILU)
-        v[u] = base == 0 && u < SF ? silu_finish(p, sf[u]) : silu_chunk(p, m, kbase + 8 * c);
-      else
-        v[u] = base == 0 ? xv[u]
-                         : *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase +
-                                                           8 * c);
+      const int i = CLAMP ? min(base + u * NT + tid, total - 1) : base + u * NT + tid;
+      if (CLAMP || i < total) {
+        const int m = i / chunks, c = i - m * chunks;
+        if (XSRC == X_ATTN)
+          v[u] = base == 0 && u == 0 ? attn_finish(p, af) : attn_chunk(p, m, kbase + 8 * c);
+        else if (XSRC == X_SILU)
+          v[u] = base == 0 && u < SF ? silu_finish(p, sf[u]) : silu_chunk(p, m, kbase + 8 * c);
+        else
+          v[u] = base == 0 ? xv[u]
+                           : *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase +
+                                                             8 * c);
+      }
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
       if (base + u * NT >= total) break;
-      const int i = min(base + u * NT + tid, total - 1);
-      const int m = i / chunks, c = i - m * chunks;
-      *reinterpret_cast<uint4*>(xs + m * p.xstride + 8 * c) = deinterleave8(v[u]);
+      const int i = CLAMP ? min(base + u * NT + tid, total - 1) : base + u * NT + tid;
+      if (CLAMP || i < total) {
+        const int m = i / chunks, c = i - m * chunks;
+        *reinterpret_cast<uint4*>(xs + m * p.xstride + 8 * c) = deinterleave8(v[u]);
+      }
     }
   }
   __syncthreads();
@@ -431,7 +442,7 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
     // LoRA-A tile of segment seg: lane n = rank index, A is read as bf16.
     const int seg = tile - p.NT;
     const bool r_ok = ln < p.r;
-    const uint16_t* arow = p.la[seg] + (int64_t)(r_ok ? ln : 0) * p.K + kbase + 64 * lg;
+    const uint16_t* arow = sel_seg(p.la, seg) + (int64_t)(r_ok ? ln : 0) * p.K + kbase + 64 * lg;
 #pragma unroll
     for (int i = 0; i < KPW; ++i) {
       if (i >= nk) break;

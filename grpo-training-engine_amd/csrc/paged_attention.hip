@@ -78,6 +78,13 @@ AttnPlan plan_attn(int B, int Hq, int Hkv, int D, int BS, int max_blocks) {
   }
   const int mb = max_blocks > 0 ? max_blocks : 1;
   const int bpw = (int)cdiv(mb, (int64_t)AW * MAX_SPLITS);
+  // one thread per block-table entry of a split: bps <= AT (contexts <= 64K)
+  if (AW * bpw > AT) {
+    p.fast = false;
+    p.bps = mb;
+    p.S = 1;
+    return p;
+  }
   p.bps = AW * bpw;
   p.S = (int)cdiv(mb, p.bps);
   p.bytes = (size_t)B * Hq * p.S * (D + 2) * 4;
@@ -116,114 +123,172 @@ typedef Fetch4<QKV_MAX_SLICES> QkvFetch;
 template <int GQ, bool FUSED>
 __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 15, lg = lane >> 4;
-  const int ctx = seq_ctx(p, b);
-  const int nblk = (ctx + FBS - 1) / FBS;
-  const int nsplit = nblk > 0 ? (nblk + p.bps - 1) / p.bps : 1;
-  if (s >= nsplit) return;
-  const int blk0 = s * p.bps;
-  const int blk1 = min(blk0 + p.bps, nblk);
+  const int blk0 = s * p.bps;  // < max_blocks for every launched split
 
   extern __shared__ __align__(16) float sO[];  // [AW][GQ][FD]
   __shared__ __align__(16) uint16_t sQ[GQ][FD];
+  __shared__ __align__(16) uint16_t sNew[2][FD];  // appended token: rotated K, V
   __shared__ float sTs[MAXSEG * 16];
   __shared__ __align__(16) float sP[AW][16][16];
   __shared__ float sC[AW][16];
   __shared__ float sM[AW][16];
   __shared__ float sL[AW][16];
+  int* sBT = reinterpret_cast<int*>(sO + (size_t)AW * GQ * FD);  // the split's table slice
 
   const int64_t head_stride = (int64_t)FBS * FD;
-  // K/V fragments of physical block phys (zeros for an invalid id, then skipped).
-  auto load_kv = [&](int phys, uint4 (&kf)[4], uint4 (&vf)[4]) -> bool {
+  // K/V fragments of physical block phys; an invalid id reads block 0 and the
+  // block is then skipped.  The loads are unconditional (see below).
+  auto load_kv = [&](int phys, uint4 (&kf)[4], uint4 (&vf)[4])
+                     __attribute__((always_inline)) -> bool {
     const bool ok = phys >= 0 && phys < p.num_blocks;
-    const uint16_t* kb = p.kc + ((int64_t)(ok ? phys : 0) * p.Hkv + kvh) * head_stride;
-    const uint16_t* vb = p.vc + ((int64_t)(ok ? phys : 0) * p.Hkv + kvh) * head_stride;
+    const int64_t ph = ok ? phys : 0;
+    const uint16_t* kb = p.kc + (ph * p.Hkv + kvh) * head_stride;
+    const uint16_t* vb = p.vc + (ph * p.Hkv + kvh) * head_stride;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      kf[i] = ok ? *reinterpret_cast<const uint4*>(kb + ln * FD + 8 * lg + 32 * i)
-                 : make_uint4(0, 0, 0, 0);
-      vf[i] = ok ? *reinterpret_cast<const uint4*>(vb + (4 * lg + i) * FD + 8 * ln)
-                 : make_uint4(0, 0, 0, 0);
+      kf[i] = *reinterpret_cast<const uint4*>(kb + ln * FD + 8 * lg + 32 * i);
+      vf[i] = *reinterpret_cast<const uint4*>(vb + (4 * lg + i) * FD + 8 * ln);
     }
     return ok;
   };
-  // The split's slice of the block table, in LDS after the prologue.
-  int* sBT = reinterpret_cast<int*>(sO + (size_t)AW * GQ * FD);
-  for (int i = tid; i < blk1 - blk0; i += AT) sBT[i] = p.bt[(int64_t)b * p.bts + blk0 + i];
 
-  // 1. Q of the GQA group in LDS (and, fused, the new token's K/V in the cache).
-  // The first block's K/V loads go out first, unless it is the block this split
-  // appends to (that one is loaded after the append).
-  const int pos = FUSED ? p.append_pos[b] : -1;
+  // Load schedule.  Vector loads retire in issue order and the compiler waits
+  // for one with s_waitcnt vmcnt(N), N = loads issued after it; after a
+  // conditional load it can only assume the fewest loads, so a conditional
+  // load makes the waits of the loads issued BEFORE it conservative, never of
+  // those after it.  Hence: first the loads only some threads need, each
+  // predicated (LoRA t: 12 threads; the q|k|v partial sums of the GQ + 2 rows,
+  // or q; the block-table slice), none depending on a loaded value; meanwhile
+  // one batch of scalar loads brings the context length, the append position
+  // and this wave's first block id; then the loads every thread needs,
+  // unconditional: the RoPE tables and the first block's K/V (HBM).  Each
+  // phase then waits only for its own loads.  The wave whose first block
+  // receives the new token loads it before the append and patches the
+  // token's row from LDS afterwards.
   const int first = blk0 + wave;
-  const bool late = FUSED && pos >= 0 && first == pos / FBS;
-  uint4 kn[4], vn[4];
-  bool ok_next = false;
-  if (!late && first < blk1) ok_next = load_kv(p.bt[(int64_t)b * p.bts + first], kn, vn);
-  if (FUSED) {
-    // Phase A (one memory round trip): every column group of q (GQ heads), of k
-    // and of v of this KV head is fetched by one thread, then finished (bias,
-    // LoRA, bf16) into LDS.  Phase B: RoPE from LDS; the split that holds the
-    // slot writes K (rotated) and V of the new token into the cache.
-    const int pblk = pos >= 0 ? pos / FBS : -1;
-    const bool app = pos >= 0 && pos < p.max_blocks * FBS && pblk >= blk0 && pblk < blk1;
-    const int nrow = GQ + (app ? 2 : 0);  // q heads, then k, then v
-    float* sRaw = sO;                     // [GQ + 2][FD], reused by the wave merge later
-    QkvFetch f;
-    const bool fetch = tid < nrow * (FD / 4);
-    const int row = tid / (FD / 4), d4 = 4 * (tid % (FD / 4));
-    if (fetch) {
+  const int ctx_raw = p.cl[b];
+  const int pos = FUSED ? p.append_pos[b] : -1;
+  const int phys0 = p.bt[(int64_t)b * p.bts + min(first, p.max_blocks - 1)];
+  constexpr int NROW = GQ + 2;  // fused rows: GQ q heads, then k, then v
+  static_assert(NROW * (FD / 4) <= AT - 64, "the last wave fetches no q|k|v row");
+  const int row = tid / (FD / 4), d4 = 4 * (tid % (FD / 4));
+  const int t_item = tid - (AT - 64);  // LoRA t item of a last-wave lane
+  QkvFetch f;
+  float4 tv[QKV_MAX_SLICES];
+  uint4 qv = make_uint4(0, 0, 0, 0);
+  if constexpr (FUSED) {
+    // LoRA t by the last wave (no q|k|v rows; its first K/V is needed only
+    // after the prologue): the compiler starts the sum right after these loads,
+    // which stalls the fetching wave for one round trip.
+    if (t_item >= 0 && t_item < p.qkv.nseg * 4 && p.qkv.r > 0) lin_fetch_t(p.qkv, b, t_item, tv);
+    if (row < NROW) {
       const int n0 = row < GQ ? (kvh * GQ + row) * FD
                               : (row == GQ ? (p.Hq + kvh) * FD : (p.Hq + p.Hkv + kvh) * FD);
       lin_fetch4(p.qkv, b, n0 + d4, f);
     }
-    lin_load_t(p.qkv, b, sTs);
+  } else {
+    if (tid < GQ * (FD / 8)) {
+      const int h = tid / (FD / 8), c = tid - h * (FD / 8);
+      qv = *reinterpret_cast<const uint4*>(p.q + (int64_t)b * p.qsb +
+                                           (int64_t)(kvh * GQ + h) * p.qsh + 8 * c);
+    }
+  }
+  int bt_v = 0;
+  if (tid < p.bps) bt_v = p.bt[(int64_t)b * p.bts + min(blk0 + tid, p.max_blocks - 1)];
+  // Consumed together here, the three scalar loads (issued above, ahead of
+  // the predicated vector loads) are waited for once (otherwise the compiler
+  // sinks the last two below the early exit and waits for each in turn).
+  asm volatile("" ::"s"(ctx_raw), "s"(pos), "s"(phys0));
+  const int ctx = max(0, min(ctx_raw, p.max_blocks * FBS));
+  const int nblk = (ctx + FBS - 1) / FBS;
+  const int nsplit = nblk > 0 ? (nblk + p.bps - 1) / p.bps : 1;
+  if (s >= nsplit) return;
+  const int blk1 = min(blk0 + p.bps, nblk);
+  const int nb = blk1 - blk0;  // 0 only for an empty context
+  const int pblk = pos >= 0 ? pos / FBS : -1;
+  const bool app = FUSED && pos >= 0 && pos < p.max_blocks * FBS && pblk >= blk0 && pblk < blk1;
+  uint16_t rc0 = 0, rc1 = 0, rs0 = 0, rs1 = 0;  // cos/sin of RoPE pair dimension tid % 64
+  if constexpr (FUSED) {
+    const int cpos = pos < 0 ? 0 : (pos >= p.max_pos ? p.max_pos - 1 : pos);
+    const int d = tid % (FD / 2);
+    rc0 = p.cos_t[(int64_t)cpos * FD + d];
+    rc1 = p.cos_t[(int64_t)cpos * FD + d + FD / 2];
+    rs0 = p.sin_t[(int64_t)cpos * FD + d];
+    rs1 = p.sin_t[(int64_t)cpos * FD + d + FD / 2];
+  }
+  uint4 kn[4], vn[4];
+  bool ok_next = load_kv(first < blk1 ? phys0 : -1, kn, vn);
+
+  if constexpr (FUSED) {
+    // Phase A: LoRA t and the q|k|v finish (bias, LoRA, bf16) into LDS.
+    float* sRaw = sO;  // [GQ + 2][FD], reused by the wave merge later
+    if (t_item >= 0) lin_store_t(p.qkv, tv, t_item, sTs);
+    if (tid < nb) sBT[tid] = bt_v;
     __syncthreads();
-    if (fetch) {
+    if (row < NROW) {
       float v[4];
       lin_finish4(p.qkv, sTs, f, v);
       *reinterpret_cast<float4*>(sRaw + row * FD + d4) = make_float4(v[0], v[1], v[2], v[3]);
     }
     __syncthreads();
-    const int cpos = pos < 0 ? 0 : (pos >= p.max_pos ? p.max_pos - 1 : pos);
-    const uint16_t* cr = p.cos_t + (int64_t)cpos * FD;
-    const uint16_t* sr = p.sin_t + (int64_t)cpos * FD;
-    int64_t slot = -1;
-    if (app) {
-      const int phys = p.bt[(int64_t)b * p.bts + pblk];
-      if (phys >= 0 && phys < p.num_blocks)
-        slot = (((int64_t)phys * p.Hkv + kvh) * FBS + pos % FBS) * FD;
-    }
-    // RoPE pairs (d, d + D/2): GQ q rows (+ the k row when appending).
+    // The new token's cache row: its block id comes from the split's table
+    // slice (in LDS since the first barrier).
+    const int physA = app ? sBT[pblk - blk0] : -1;
+    const int64_t slot = app && physA >= 0 && physA < p.num_blocks
+                             ? (((int64_t)physA * p.Hkv + kvh) * FBS + pos % FBS) * FD
+                             : -1;
+    // Phase B: RoPE pairs (d, d + D/2) of the GQ q rows (+ the k row when
+    // appending); the pair index advances by AT, a multiple of D/2, so every
+    // pair of a thread uses dimension tid % 64.
     const int npair = (GQ + (app ? 1 : 0)) * (FD / 2);
+    const float c0 = bf2f(rc0), c1 = bf2f(rc1), s0 = bf2f(rs0), s1 = bf2f(rs1);
     for (int i = tid; i < npair; i += AT) {
       const int r = i / (FD / 2), d = i % (FD / 2);
       const float x1 = sRaw[r * FD + d], x2 = sRaw[r * FD + d + FD / 2];
-      const uint16_t lo = f2bf(round_bf(round_bf(x1 * bf2f(cr[d])) + round_bf(-x2 * bf2f(sr[d]))));
-      const uint16_t hi = f2bf(round_bf(round_bf(x2 * bf2f(cr[d + FD / 2])) +
-                                        round_bf(x1 * bf2f(sr[d + FD / 2]))));
+      const uint16_t lo = f2bf(round_bf(round_bf(x1 * c0) + round_bf(-x2 * s0)));
+      const uint16_t hi = f2bf(round_bf(round_bf(x2 * c1) + round_bf(x1 * s1)));
       if (r < GQ) {
         sQ[r][d] = lo;
         sQ[r][d + FD / 2] = hi;
-      } else if (slot >= 0) {
-        p.kc[slot + d] = lo;
-        p.kc[slot + d + FD / 2] = hi;
+      } else {
+        sNew[0][d] = lo;
+        sNew[0][d + FD / 2] = hi;
+        if (slot >= 0) {
+          p.kc[slot + d] = lo;
+          p.kc[slot + d + FD / 2] = hi;
+        }
       }
     }
-    if (app && slot >= 0)
-      for (int d = tid; d < FD; d += AT) p.vc[slot + d] = f2bf(sRaw[(GQ + 1) * FD + d]);
+    if (app)
+      for (int d = tid; d < FD; d += AT) {
+        const uint16_t v = f2bf(sRaw[(GQ + 1) * FD + d]);
+        sNew[1][d] = v;
+        if (slot >= 0) p.vc[slot + d] = v;
+      }
   } else {
-    for (int i = tid; i < GQ * (FD / 8); i += AT) {
-      const int h = i / (FD / 8), c = i - h * (FD / 8);
-      *reinterpret_cast<uint4*>(&sQ[h][8 * c]) = *reinterpret_cast<const uint4*>(
-          p.q + (int64_t)b * p.qsb + (int64_t)(kvh * GQ + h) * p.qsh + 8 * c);
+    if (tid < GQ * (FD / 8)) {
+      const int h = tid / (FD / 8), c = tid - h * (FD / 8);
+      *reinterpret_cast<uint4*>(&sQ[h][8 * c]) = qv;
+    }
+    if (tid < nb) sBT[tid] = bt_v;
+  }
+  // Orders sQ, sNew, sBT and the reuse of sO before any wave reads them.  (The
+  // cache rows written above are read by no wave of this launch: the block
+  // holding them is this split's, and its wave patches the row from sNew.)
+  __syncthreads();
+
+  if (FUSED && app && first == pblk) {
+    // The first block of this wave received the new token at row t.
+    const int t = pos % FBS;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (ln == t) kn[i] = *reinterpret_cast<const uint4*>(&sNew[0][8 * lg + 32 * i]);
+      if (4 * lg + i == t) vn[i] = *reinterpret_cast<const uint4*>(&sNew[1][8 * ln]);
     }
   }
-  // Orders the appended K/V (global), sQ and the reuse of sO before any wave
-  // reads them.
-  __syncthreads();
-  if (late) ok_next = load_kv(sBT[first - blk0], kn, vn);
 
   // Q^T as the MFMA B operand: lane (head ln, group lg) holds
   // Q[head][8*lg + 32*i + 0..7] for MFMA i.
@@ -240,17 +305,11 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[h][j] = 0.f;
 
-  for (int blk = blk0 + wave; blk < blk1; blk += AW) {
-    uint4 kf[4], vf[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      kf[i] = kn[i];
-      vf[i] = vn[i];
-    }
-    const bool ok = ok_next;
-    const int nxt = blk + AW;
-    ok_next = nxt < blk1 ? load_kv(sBT[nxt - blk0], kn, vn) : false;
-    if (!ok) continue;
+  // One 16-token block: S^T on MFMA, online softmax, P.V on VALU.  (Inlined
+  // at both call sites: a call would pass every captured variable, the kernel
+  // arguments included, through scratch memory.)
+  auto block = [&](int blk, const uint4 (&kf)[4], const uint4 (&vf)[4])
+                   __attribute__((always_inline)) {
     f32x4_t sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int i = 0; i < 4; ++i) sacc = mfma16x16x32(kf[i], qf[i], sacc);
@@ -298,6 +357,27 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
       }
     }
     wave_sync();
+  };
+
+  // The wave's blocks first, first + AW, ...: the next block's loads are issued
+  // before the current one is processed.  The two branches keep the load count
+  // exact (a prefetch issued or not), so the current block waits only for its
+  // own loads.
+  for (int blk = first; blk < blk1; blk += AW) {
+    uint4 kf[4], vf[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      kf[i] = kn[i];
+      vf[i] = vn[i];
+    }
+    const bool ok = ok_next;
+    const int nxt = blk + AW;
+    if (nxt < blk1) {
+      ok_next = load_kv(sBT[nxt - blk0], kn, vn);
+      if (ok) block(blk, kf, vf);
+    } else {
+      if (ok) block(blk, kf, vf);
+    }
   }
 
   // Sum the four token groups of the wave, then merge the AW waves.
