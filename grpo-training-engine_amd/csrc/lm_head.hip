@@ -6,8 +6,8 @@
 // step, W bf16 [V, K] (467 MB for Qwen2-1.5B: the largest single read of the
 // step).  One wave = 16 vocabulary rows over all of K on
 // v_mfma_f32_16x16x32_bf16 (A = x staged in LDS, B = W^T); W is streamed with
-// 16-byte loads, the next k-step's loads issued before the current one is
-// multiplied.  Each wave also reduces its 16 logits per row to (max, first
+// 16-byte loads laid out so each load instruction covers 64 contiguous bytes
+// of every row of the tile.  Each wave also reduces its 16 logits per row to (max, first
 // index) and writes that pair, so the argmax over V needs only a small second
 // pass instead of re-reading the logits.
 #include <math.h>
@@ -19,7 +19,7 @@ using namespace grpo;
 namespace {
 
 constexpr int LM_KSTEP = 256;
-constexpr int LM_WAVES = 16;  // vocabulary tiles per workgroup (x staged once per workgroup)
+constexpr int LM_WAVES = 4;  // vocabulary tiles per workgroup (x staged once per workgroup)
 constexpr int ADV_T = 1024;
 constexpr size_t LM_LDS_MAX = 163840;  // gfx950: 160 KiB of LDS per workgroup
 
@@ -58,14 +58,14 @@ __global__ void __launch_bounds__(64 * LM_WAVES) lm_head_argmax_kernel(LmArgs p)
   const int tile = blockIdx.x * LM_WAVES + wave;
   const int xstride = p.K + 8;
   const int KS = p.K / LM_KSTEP;
-
-  // First k-step of W, then x into LDS.
   const bool live = tile < p.NT;
-  const uint16_t* wrow = p.w + (int64_t)(live ? tile * 16 + ln : 0) * p.K + 64 * lg;
-  uint4 wa[8], wb[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) wa[j] = live ? *reinterpret_cast<const uint4*>(wrow + 8 * j)
-                                           : make_uint4(0, 0, 0, 0);
+
+  // Lane (row ln, group lg) supplies k-slots 8*lg..8*lg+7 of each MFMA j as
+  // elements 32*j + 8*lg + 0..7 of the k-step: one 16-byte load per MFMA, and
+  // each load instruction reads 64 contiguous bytes of each of the wave's 16
+  // rows (16 half-lines; the layout 64*lg + 8*j touched 64 lines, 16 bytes
+  // each, and streamed W ~20 % slower).  x is read from LDS in the same order.
+  const uint16_t* wrow = p.w + (int64_t)(live ? tile * 16 + ln : 0) * p.K + 8 * lg;
   {
     const int chunks = p.K / 8, total = p.M * chunks;
     for (int i = tid; i < total; i += 64 * LM_WAVES) {
@@ -82,33 +82,22 @@ __global__ void __launch_bounds__(64 * LM_WAVES) lm_head_argmax_kernel(LmArgs p)
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   const uint16_t* xrow[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) xrow[mt] = xs + min(mt * 16 + ln, p.M - 1) * xstride + 64 * lg;
+  for (int mt = 0; mt < MT; ++mt) xrow[mt] = xs + min(mt * 16 + ln, p.M - 1) * xstride + 8 * lg;
 
-  for (int ks = 0; ks < KS; ks += 2) {
-    if (ks + 1 < KS) {
+  // One k-step at a time: more loads in flight per wave (double buffering)
+  // measured slower here, the HBM stream already being saturated by the
+  // number of resident waves.
+  for (int ks = 0; ks < KS; ++ks) {
+    uint4 w[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        wb[j] = *reinterpret_cast<const uint4*>(wrow + (ks + 1) * LM_KSTEP + 8 * j);
-    }
+    for (int j = 0; j < 8; ++j)
+      w[j] = *reinterpret_cast<const uint4*>(wrow + ks * LM_KSTEP + 32 * j);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
         acc[mt] = mfma16x16x32(
-            *reinterpret_cast<const uint4*>(xrow[mt] + ks * LM_KSTEP + 8 * j), wa[j], acc[mt]);
-    if (ks + 1 >= KS) break;
-    if (ks + 2 < KS) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        wa[j] = *reinterpret_cast<const uint4*>(wrow + (ks + 2) * LM_KSTEP + 8 * j);
-    }
-#pragma unroll
-    for (int j = 0; j < 8; ++j)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-        acc[mt] = mfma16x16x32(
-            *reinterpret_cast<const uint4*>(xrow[mt] + (ks + 1) * LM_KSTEP + 8 * j), wb[j],
-            acc[mt]);
+            *reinterpret_cast<const uint4*>(xrow[mt] + ks * LM_KSTEP + 32 * j), w[j], acc[mt]);
   }
 
   // lane (n = ln, group lg) holds logits[m = mt*16 + 4*lg + q][tile*16 + ln].

@@ -50,8 +50,11 @@ class DecodeEngine:
     """Static-shape decode step for ``batch`` rows over a KV pool."""
 
     def __init__(self, model: Qwen2ForCausalLM, pool: PagedKVPool, batch: int, max_blocks: int,
-                 max_pos: Optional[int] = None):
+                 max_pos: Optional[int] = None, keep_logits: bool = False):
         self.lib = _lib.device_library()
+        # Greedy decoding needs only each step's argmax; keep_logits also fills
+        # self.logits [B, V] (bf16) every step, for callers that inspect them.
+        self.keep_logits = keep_logits
         cfg = model.config
         self.model, self.pool, self.cfg = model, pool, cfg
         self.B, self.max_blocks = batch, max_blocks
@@ -251,8 +254,9 @@ class DecodeEngine:
             "final_norm")))
         if self.lm_fused:
             gen = self.generated
+            logits = self.logits.data_ptr() if self.keep_logits else None
             out.append(("lm_head", lambda: chk(lib.grpo_lm_head_argmax(
-                x, H, self.lm_head.data_ptr(), self.V, H, B, self.logits.data_ptr(), self.V,
+                x, H, self.lm_head.data_ptr(), self.V, H, B, logits, self.V,
                 self.ws_lm.data_ptr(), self.ws_lm.numel(), st), "lm_head")))
             out.append(("advance", lambda: chk(lib.grpo_decode_advance(
                 self.ws_lm.data_ptr(), B, self.V, self.next.data_ptr(), self.tokens.data_ptr(),

@@ -80,7 +80,7 @@ def test_decode_step_matches_oracle(dev, layers):
     # GPU: private blocks per row (no sharing here), teacher-forced prefill in the B-row engine
     pool = PagedKVPool(layers, B * width, 2, 128, bs, device=dev)
     sids = [pool.allocate(width * bs) for _ in range(B)]
-    eng = DecodeEngine(model, pool, B, width)
+    eng = DecodeEngine(model, pool, B, width, keep_logits=True)
     tbl = pool.block_table(sids, width, device=dev)
     eng.start(torch.zeros(B, dtype=torch.int64, device=dev), torch.zeros(B, device=dev), tbl,
               torch.full((B,), 100, device=dev), 100)
