@@ -18,6 +18,10 @@ constexpr int ROW_T = 256;
 
 constexpr int PARTS_T = 512;  // consumers of partial sums: more loads in flight per row
 
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
+  return (uint32_t)lo | ((uint32_t)hi << 16);
+}
+
 __device__ __forceinline__ float block_sum(float v, float* red) {
   for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -169,47 +173,77 @@ __global__ void __launch_bounds__(AMAX_T) argmax_kernel(const uint16_t* __restri
 // fetched before the LoRA-t barrier, so most rows need one memory round trip).
 __global__ void __launch_bounds__(PARTS_T) add_rmsnorm_parts_kernel(
     LinParts o, const uint16_t* residual, uint16_t* h_out, const uint16_t* __restrict__ w,
-    uint16_t* __restrict__ y, float eps) {
+    uint16_t* __restrict__ y, float eps, bool vec) {
   __shared__ float red[PARTS_T / 64];
   __shared__ float ts[MAXSEG * 16];
-  extern __shared__ float hs[];  // H floats
+  extern __shared__ float hs[];  // H floats (columns past 4 * PARTS_T only)
   const int m = blockIdx.x, H = o.N;
   const int64_t row = (int64_t)m * H;
   const int tid = threadIdx.x;
+  // Thread tid owns columns 4*tid .. 4*tid+3 from the loads to the final
+  // stores, so its h stays in registers; the norm weight is fetched with the
+  // partial sums (a load after the row reduction would be one more memory
+  // round trip at the end of the kernel).  Wider rows (> 4 * PARTS_T) put the
+  // rest through LDS.
   const bool first = tid < H / 4;
   Fetch4<> f;
-  uint2 res0 = make_uint2(0, 0);
+  uint2 res0 = make_uint2(0, 0), w0 = make_uint2(0, 0);
   if (first) {
     lin_fetch4(o, m, 4 * tid, f);
     if (residual) res0 = *reinterpret_cast<const uint2*>(residual + row + 4 * tid);
+    if (vec) {
+      w0 = *reinterpret_cast<const uint2*>(w + 4 * tid);
+    } else {
+      w0.x = pack2(w[4 * tid], w[4 * tid + 1]);
+      w0.y = pack2(w[4 * tid + 2], w[4 * tid + 3]);
+    }
   }
   lin_load_t(o, m, ts);
   __syncthreads();
   float ss = 0.f;
-  auto take = [&](int i4, const float (&v)[4], uint2 rr) {
+  float h0[4] = {0.f, 0.f, 0.f, 0.f};
+  auto add_res = [&](const float (&v)[4], uint2 rr, float (&h)[4]) {
     const float rv[4] = {bf_lo(rr.x), bf_hi(rr.x), bf_lo(rr.y), bf_hi(rr.y)};
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      float h = v[c];
-      if (residual) h = round_bf(h + rv[c]);
-      hs[4 * i4 + c] = h;
-      ss += h * h;
+      h[c] = residual ? round_bf(v[c] + rv[c]) : v[c];
+      ss += h[c] * h[c];
     }
   };
   if (first) {
     float v[4];
     lin_finish4(o, ts, f, v);
-    take(tid, v, res0);
+    add_res(v, res0, h0);
   }
   for (int i4 = tid + PARTS_T; i4 < H / 4; i4 += PARTS_T) {  // rows wider than 4 * PARTS_T
-    float v[4];
+    float v[4], h[4];
     lin_values4(o, ts, m, 4 * i4, v);
-    take(i4, v,
-         residual ? *reinterpret_cast<const uint2*>(residual + row + 4 * i4) : make_uint2(0, 0));
+    add_res(v, residual ? *reinterpret_cast<const uint2*>(residual + row + 4 * i4)
+                        : make_uint2(0, 0), h);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) hs[4 * i4 + c] = h[c];
   }
   const float total = block_sum(ss, red);
   const float inv = 1.f / sqrtf(total / (float)H + eps);
-  for (int i = tid; i < H; i += PARTS_T) {
+  if (first) {
+    const float wv[4] = {bf_lo(w0.x), bf_hi(w0.x), bf_lo(w0.y), bf_hi(w0.y)};
+    float yv[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) yv[c] = round_bf(h0[c] * inv) * wv[c];
+    const uint2 yo = make_uint2(pack_bf2(yv[0], yv[1]), pack_bf2(yv[2], yv[3]));
+    const uint2 ho = make_uint2(pack_bf2(h0[0], h0[1]), pack_bf2(h0[2], h0[3]));
+    if (vec) {
+      *reinterpret_cast<uint2*>(y + row + 4 * tid) = yo;
+      if (residual && h_out) *reinterpret_cast<uint2*>(h_out + row + 4 * tid) = ho;
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        y[row + 4 * tid + c] = f2bf(yv[c]);
+        if (residual && h_out) h_out[row + 4 * tid + c] = f2bf(h0[c]);
+      }
+    }
+  }
+  for (int i = 4 * PARTS_T + tid; i < H; i += PARTS_T) {
     const float h = hs[i];
     if (residual && h_out) h_out[row + i] = f2bf(h);
     y[row + i] = f2bf(round_bf(h * inv) * bf2f(w[i]));
@@ -373,9 +407,11 @@ extern "C" int grpo_add_rmsnorm_parts(const grpo_linear_parts_t* x, const void* 
   if (!weight || !y) return einval("null pointer");
   if (residual && (reinterpret_cast<uintptr_t>(residual) & 7u) != 0)
     return einval("residual must be 8-byte aligned");
+  auto a8 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 7u) == 0; };
+  const bool vec = a8(weight) && a8(y) && (!h_out || a8(h_out));  // rows: N % 16 == 0
   add_rmsnorm_parts_kernel<<<dim3(o.M), PARTS_T, o.N * sizeof(float), as_stream(stream)>>>(
       o, static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(h_out),
-      static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(y), eps);
+      static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(y), eps, vec);
   return launch_check("add_rmsnorm_parts");
 }
 

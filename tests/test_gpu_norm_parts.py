@@ -1,0 +1,101 @@
+"""grpo_add_rmsnorm_parts through the C ABI against the oracle.
+
+The split-K partial sums come from the GPU linear (grpo_nf4_linear_partials)
+on seeded NF4 weights; the reference is the oracle linear
+(oracle.lora_linear.nf4_lora_linear, pinned by the golden fixtures) followed
+by the residual add and the oracle RMSNorm (oracle.decode.rmsnorm, pinned
+against transformers' Qwen2RMSNorm).  Cases cover the register path (rows of
+at most 2048 columns), the LDS path for wider rows (3584: Qwen2-7B's hidden
+size), the LoRA + bias epilogue, and a norm weight and output that are only
+2-byte aligned (the scalar load/store path).
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+from oracle.decode import rmsnorm
+from oracle.lora_linear import nf4_lora_linear
+from oracle.nf4 import NF4_CODE, quantize_nf4
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+
+
+def _bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _dev_bf16(bits, dev, offset=0):
+    """bf16 tensor holding ``bits``; ``offset`` elements of padding in front make
+    the returned view only 2-byte aligned when offset is odd."""
+    flat = np.zeros(bits.size + offset, np.uint16)
+    flat[offset:] = bits.reshape(-1)
+    t = torch.from_numpy(flat.view(np.int16)).view(torch.bfloat16).to(dev)
+    return t[offset:].view(bits.shape)
+
+
+@pytest.mark.parametrize("n,lora,offset", [(1536, False, 0), (1536, True, 1), (3584, True, 0),
+                                           (3584, False, 1)])
+def test_add_rmsnorm_parts_matches_oracle(dev, n, lora, offset):
+    from grpo_mi355x import _lib
+    from grpo_mi355x.kernels import ops
+
+    lib = _lib.device_library()
+    st = _lib.stream_handle(dev)
+    m, k, r, bs, eps = 8, 512, 16, 64, 1e-6
+    g = np.random.default_rng(n + 10 * lora + offset)
+    x = f32_to_bf16_bits(g.standard_normal((m, k)).astype(np.float32))
+    w = (g.standard_normal((n, k)) * 0.05).astype(np.float32)
+    packed, absmax = quantize_nf4(w, bs)
+    bias = f32_to_bf16_bits((g.standard_normal(n) * 0.1).astype(np.float32))
+    a = f32_to_bf16_bits((g.standard_normal((r, k)) * 0.05).astype(np.float32))
+    b = f32_to_bf16_bits((g.standard_normal((n, r)) * 0.05).astype(np.float32))
+    res = f32_to_bf16_bits(g.standard_normal((m, n)).astype(np.float32))
+    nw = f32_to_bf16_bits((1 + 0.1 * g.standard_normal(n)).astype(np.float32))
+
+    # split-K partial sums of the linear on the GPU
+    rr = r if lora else 0
+    plan = ops.nf4_linear_plan(m, n, k, rr, 1, bs)
+    assert plan is not None
+    splits, pbytes, tbytes = plan
+    t = lambda arr: torch.from_numpy(np.ascontiguousarray(arr)).to(dev)
+    x_d, a_d, b_d, bias_d = (_dev_bf16(v, dev) for v in (x, a, b, bias))
+    pk_d, am_d, code_d = t(packed), t(absmax), t(NF4_CODE.astype(np.float32))
+    part = torch.empty(max(pbytes, 16) // 4, dtype=torch.float32, device=dev)
+    tpart = torch.empty(max(tbytes, 16) // 4, dtype=torch.float32, device=dev)
+    d = _lib.LinearParts()
+    d.part, d.tpart = part.data_ptr(), tpart.data_ptr()
+    d.splits, d.M, d.N, d.K, d.nseg, d.r = splits, m, n, k, 1, rr
+    d.seg_end[0] = n
+    d.bias[0] = bias_d.data_ptr()
+    d.lora_b[0] = b_d.data_ptr() if lora else None
+    d.scaling = 2.0
+    la = (ctypes.c_void_p * 1)(a_d.data_ptr() if lora else None)
+    _lib.check(lib.grpo_nf4_linear_partials(x_d.data_ptr(), k, pk_d.data_ptr(), am_d.data_ptr(),
+                                            code_d.data_ptr(), bs, la, ctypes.byref(d), st),
+               "partials")
+
+    # residual add + RMSNorm from the partials, in place on the residual
+    h_d = _dev_bf16(res, dev)  # the residual must be 8-byte aligned
+    nw_d = _dev_bf16(nw, dev, offset)
+    y_d = _dev_bf16(np.zeros((m, n), np.uint16), dev, offset)
+    _lib.check(lib.grpo_add_rmsnorm_parts(ctypes.byref(d), h_d.data_ptr(), h_d.data_ptr(),
+                                          nw_d.data_ptr(), y_d.data_ptr(), eps, st), "norm")
+    torch.cuda.synchronize()
+
+    lin = nf4_lora_linear(x, packed, absmax, n, k, bs, bias_bits=bias,
+                          a_bits=a if lora else None, b_bits=b if lora else None, scaling=2.0)
+    h_ref = f32_to_bf16_bits(bf16_bits_to_f32(lin) + bf16_bits_to_f32(res))
+    y_ref = rmsnorm(h_ref, nw, eps)
+    h_got, y_got = _bits(h_d), _bits(y_d)
+    # the linear's float32 summation order differs from numpy's: a few outputs
+    # differ by an ulp, which the residual add and the norm carry along
+    assert np.mean(h_got == h_ref) >= 0.97
+    assert rel_err(bf16_bits_to_f32(h_got), bf16_bits_to_f32(h_ref)) <= 1e-2
+    assert np.mean(y_got == y_ref) >= 0.95
+    assert rel_err(bf16_bits_to_f32(y_got), bf16_bits_to_f32(y_ref)) <= 1e-2
