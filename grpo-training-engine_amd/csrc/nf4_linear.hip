@@ -30,6 +30,8 @@
 //    There is no cross-workgroup synchronisation; the sum over slices (fixed
 //    order) and the reference epilogue run in the consuming kernel
 //    (linear_parts.hpp): nf4_finish here, or a fused decode-step op.
+#include <algorithm>
+
 #include "linear_parts.hpp"
 
 using namespace grpo;
@@ -656,6 +658,160 @@ int run_finish(const grpo_linear_parts_t* h, uint16_t* y, int64_t ldy, hipStream
   return launch_check("nf4_finish");
 }
 
+// ------------------------------------------ gate|up with SiLU * up --
+//
+// act[m, j] = bf16(bf16(silu(g)) * u) with g = bf16(x . Wg[j, :]) and
+// u = bf16(x . Wu[j, :]): the MLP's gate and up projections of the stacked
+// [2I, K] NF4 weight (rows 0..I-1 gate, I..2I-1 up; bnb Linear4bit, no LoRA,
+// no bias) followed by fused_ops.py:79-112.  One workgroup per 16 columns j
+// (gate tile t and up tile t): waves 0..S-1 take K slices 0..S-1 of the gate
+// tile, waves S..2S-1 those of the up tile; the slices are summed through LDS
+// in slice order (the float32 order of the split-K consumers), so down_proj
+// reads a finished bf16 input instead of float32 partial sums.
+
+struct GuArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint8_t* w;
+  const float* absmax;
+  const float* code16;
+  int bs_shift;
+  uint16_t* act;
+  int64_t lda;
+  int M, I, K;
+};
+
+constexpr int GU_XU = 8;  // x chunks per thread loaded ahead of the weights
+
+// S (slices per tile) is a template parameter: with the thread count known at
+// compile time the x chunks stay in registers (a runtime count sent them to
+// scratch memory).
+template <int KPW, int S>
+__global__ void __launch_bounds__(128 * S) nf4_gate_up_silu(GuArgs p) {
+  constexpr int MT = 1;
+  extern __shared__ __align__(16) uint16_t xs[];  // [M][K + 8] (decode8 order), then sums
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 15, lg = lane >> 4;
+  constexpr int NTH = 128 * S;
+  const int t = blockIdx.x;
+  const bool up = wave >= S;
+  const int slice = up ? wave - S : wave;
+  const int KS = p.K / KSTEP;
+  const int ks0 = slice * KPW;
+  const int nk = min(KPW, KS - ks0);  // >= 1: S = ceil(KS / KPW)
+  const int n_row = (up ? p.I : 0) + t * 16 + ln;
+  const int xstride = p.K + 8;
+  float* red = reinterpret_cast<float*>(xs + p.M * xstride);  // [2S][M][16]
+  static_assert(MT == 1, "M <= 16");
+
+  // Load order as in nf4_part_mfma: codebook (scalar loads), x (whole K, the
+  // first GU_XU chunks per thread; whole entries past the end skipped, a
+  // partial one clamped), then this wave's weights, unconditional.
+  float code[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
+  const int chunks = p.K / 8, total = p.M * chunks;
+  uint4 xv[GU_XU];
+#pragma unroll
+  for (int u = 0; u < GU_XU; ++u) {
+    if (u * NTH >= total) break;
+    const int i = min(u * NTH + tid, total - 1);
+    const int m = i / chunks, c = i - m * chunks;
+    xv[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + 8 * c);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 wv[2 * KPW];
+  float av[KPW];
+  {
+    const uint8_t* wrow = p.w + (int64_t)n_row * (p.K / 2);
+#pragma unroll
+    for (int i = 0; i < KPW; ++i) {
+      const int kc = (ks0 + min(i, nk - 1)) * KSTEP + 64 * lg;
+      const uint4* wp = reinterpret_cast<const uint4*>(wrow + kc / 2);
+      wv[2 * i] = wp[0];
+      wv[2 * i + 1] = wp[1];
+      av[i] = p.absmax[((int64_t)n_row * p.K + kc) >> p.bs_shift];
+    }
+  }
+  for (int base = 0; base < total; base += GU_XU * NTH) {
+#pragma unroll
+    for (int u = 0; u < GU_XU; ++u) {
+      if (base + u * NTH >= total) break;
+      const int i = min(base + u * NTH + tid, total - 1);
+      const int m = i / chunks, c = i - m * chunks;
+      const uint4 v = base == 0 ? xv[u]
+                                : *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + 8 * c);
+      *reinterpret_cast<uint4*>(xs + m * xstride + 8 * c) = deinterleave8(v);
+    }
+  }
+  __syncthreads();
+
+  f32x4_t acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    xrow[mt] = xs + min(mt * 16 + ln, p.M - 1) * xstride + ks0 * KSTEP + 64 * lg;
+#pragma unroll
+  for (int i = 0; i < KPW; ++i) {
+    if (i >= nk) break;
+    const Lut lt = make_lut(code, av[i]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint4 bw = decode8(word(wv[2 * i + (j >> 2)], j & 3), lt);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = mfma16x16x32(*reinterpret_cast<const uint4*>(xrow[mt] + i * KSTEP + 8 * j), bw,
+                               acc[mt]);
+    }
+  }
+  // lane (n = ln, group lg) holds D[m = mt*16 + 4*lg + q][n]
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int m = mt * 16 + 4 * lg + q;
+      if (m < p.M) red[(wave * p.M + m) * 16 + ln] = acc[mt][q];
+    }
+  __syncthreads();
+  for (int i = tid; i < p.M * 16; i += NTH) {
+    const int m = i >> 4, n = i & 15;
+    float g = 0.f, u = 0.f;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      g += red[(s * p.M + m) * 16 + n];
+      u += red[((S + s) * p.M + m) * 16 + n];
+    }
+    const float gv = round_bf(g);
+    const float o = round_bf(gv * (1.f / (1.f + expf(-gv)))) * round_bf(u);
+    p.act[(int64_t)m * p.lda + t * 16 + n] = f2bf(o);
+  }
+}
+
+int g_gu_kpw = 3;  // k-steps per wave of the gate|up kernel (S = ceil(K/256 / kpw) <= 8); measured best
+
+struct GuPlan {
+  int kpw, S, MT;
+  size_t lds;
+};
+
+// Shape support of nf4_gate_up_silu; returns false for shapes it does not take.
+bool plan_gu(int M, int I, int K, int blocksize, GuPlan* pl) {
+  if (M < 1 || M > 16 || I <= 0 || I % 16 || K <= 0 || K % KSTEP) return false;
+  if (!pow2(blocksize) || blocksize < 64) return false;
+  const int KS = K / KSTEP;
+  int kpw = std::min(g_gu_kpw, KS);
+  while ((KS + kpw - 1) / kpw > 8) ++kpw;
+  if (kpw > 3) return false;
+  pl->kpw = kpw;
+  pl->S = (KS + kpw - 1) / kpw;
+  pl->MT = 1;
+  pl->lds = (size_t)M * (K + 8) * 2 + (size_t)2 * pl->S * M * 16 * 4;
+  return pl->lds <= 65536;
+}
+
 // ---------------------------------------------------- generic linear --
 
 struct GenArgs {
@@ -1016,4 +1172,53 @@ extern "C" int grpo_nf4_linear_partials_silu(const grpo_linear_parts_t* gate_up,
   if (parts->r > 0) return einval("down projection with LoRA is not supported here");
   return run_partials(nullptr, 0, w, absmax, code16, blocksize, la, *parts, as_stream(stream),
                       nullptr, &src);
+}
+
+extern "C" int grpo_nf4_gate_up_silu_supported(int M, int I, int K, int blocksize) {
+  GuPlan pl;
+  return plan_gu(M, I, K, blocksize, &pl) ? 1 : 0;
+}
+
+extern "C" int grpo_nf4_gate_up_silu(const void* x, int64_t ldx, const uint8_t* w,
+                                     const float* absmax, const float* code16, int blocksize,
+                                     int I, int K, int M, void* act, int64_t lda,
+                                     grpo_stream_t stream) {
+  GuPlan pl;
+  if (!plan_gu(M, I, K, blocksize, &pl)) {
+    set_error("shape not supported by the fused gate|up SiLU kernel");
+    return GRPO_EUNSUPPORTED;
+  }
+  if (!x || !w || !absmax || !code16 || !act) return einval("null pointer");
+  if (ldx < K || ldx % 8 || !aligned16(x) || !aligned16(w))
+    return einval("x and w must be 16-byte aligned with ldx >= K, ldx % 8 == 0");
+  if (lda < I) return einval("lda smaller than I");
+  GuArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.w = w;
+  a.absmax = absmax;
+  a.code16 = code16;
+  a.bs_shift = __builtin_ctz((unsigned)blocksize);
+  a.act = static_cast<uint16_t*>(act);
+  a.lda = lda;
+  a.M = M;
+  a.I = I;
+  a.K = K;
+  const dim3 grid((unsigned)(I / 16)), block(128 * pl.S);
+  hipStream_t st = as_stream(stream);
+  switch (pl.kpw * 16 + pl.S) {
+#define GU_CASE(KPW, S) \
+  case KPW * 16 + S: nf4_gate_up_silu<KPW, S><<<grid, block, pl.lds, st>>>(a); break;
+    GU_CASE(1, 1) GU_CASE(1, 2) GU_CASE(1, 3) GU_CASE(1, 4)
+    GU_CASE(1, 5) GU_CASE(1, 6) GU_CASE(1, 7) GU_CASE(1, 8)
+    GU_CASE(2, 5) GU_CASE(2, 6) GU_CASE(2, 7) GU_CASE(2, 8)
+    GU_CASE(3, 6) GU_CASE(3, 7) GU_CASE(3, 8)
+    GU_CASE(2, 1) GU_CASE(2, 2) GU_CASE(2, 3) GU_CASE(2, 4)
+    GU_CASE(3, 1) GU_CASE(3, 2) GU_CASE(3, 3) GU_CASE(3, 4) GU_CASE(3, 5)
+#undef GU_CASE
+    default:
+      set_error("gate|up SiLU kernel: no instantiation for %d k-steps x %d slices", pl.kpw, pl.S);
+      return GRPO_EUNSUPPORTED;
+  }
+  return launch_check("nf4_gate_up_silu");
 }

@@ -102,6 +102,9 @@ SIGNATURES = {
          _I32, _F32, _VP, _SZ, _VP],
     ),
     "grpo_nf4_linear_partials_silu": (_I32, [_PARTS, _VP, _VP, _VP, _I32, _PARTS, _VP]),
+    "grpo_nf4_gate_up_silu": (
+        _I32, [_VP, _I64, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _I64, _VP]),
+    "grpo_nf4_gate_up_silu_supported": (_I32, [_I32, _I32, _I32, _I32]),
     "grpo_nf4_linear_partials_attn": (
         _I32,
         [_VP, _VP, _I32, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _I32, _VP, _PARTS, _VP],

@@ -177,14 +177,20 @@ class DecodeEngine:
         self.lm_fused = (self.V % 16 == 0 and H % 256 == 0 and B <= 64
                          and B * (H + 8) * 2 <= 160 * 1024)
         self.ws_lm = torch.empty(max(lm_bytes, 16), dtype=torch.uint8, device=dev)
-        # down_proj stages SiLU(gate) * up straight from the gate|up partial
-        # sums when they have at most 2 K slices (the fused kernel's limit)
-        self.fuse_silu = plans["gate_up"][0] <= 2
+        # MLP: gate|up and SiLU*up in one kernel that writes the bf16 input of
+        # down_proj, when the shape allows; else down_proj stages SiLU(gate)*up
+        # from the gate|up partial sums (at most 2 K slices), else a SiLU*mul
+        # launch of its own.
+        self.gu_fused = bool(self.lib.grpo_nf4_gate_up_silu_supported(B, I, H, bs))
+        self.fuse_silu = not self.gu_fused and plans["gate_up"][0] <= 2
         nf4 = lambda n, k: n * k // 2 + n * k // bs * 4
-        # Algorithmic HBM bytes of each NF4 partials launch: packed weight +
-        # absmax + LoRA A + x + the float32 partial sums written.
+        # Algorithmic HBM bytes of each NF4 launch: packed weight + absmax +
+        # LoRA A + x + the float32 partial sums written (the fused gate|up
+        # writes the bf16 [B, I] activation instead).
         self.bytes = {kind: nf4(n, k) + nseg * rr * k * 2 + B * k * 2 + plans[kind][1]
                       + plans[kind][2] for kind, (n, k, rr, nseg) in shapes.items()}
+        if self.gu_fused:
+            self.bytes["gate_up"] = nf4(2 * I, H) + B * H * 2 + B * I * 2
 
     # -------------------------------------------------------------- launch --
     def attention_bytes(self) -> int:
@@ -234,10 +240,20 @@ class DecodeEngine:
             out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm_parts(
                 L["o_parts"], h, h, L["post_norm"].data_ptr(), x, L["eps"], st), "post_norm")))
             g = L["gu"]
-            out.append(("gate_up", lambda g=g, L=L: chk(lib.grpo_nf4_linear_partials(
-                x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
-                None, L["gu_parts"], st), "gate_up")))
-            if self.fuse_silu:
+            if self.gu_fused:
+                out.append(("gate_up", lambda g=g: chk(lib.grpo_nf4_gate_up_silu(
+                    x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
+                    I, H, B, self.act.data_ptr(), I, st), "gate_up")))
+            else:
+                out.append(("gate_up", lambda g=g, L=L: chk(lib.grpo_nf4_linear_partials(
+                    x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
+                    None, L["gu_parts"], st), "gate_up")))
+            if self.gu_fused:
+                out.append(("down", lambda L=L: chk(lib.grpo_nf4_linear_partials(
+                    self.act.data_ptr(), I, L["down_w"].data_ptr(),
+                    L["down_absmax"].data_ptr(), L["down_code"].data_ptr(), self.bs, None,
+                    L["down_parts"], st), "down")))
+            elif self.fuse_silu:
                 out.append(("down", lambda L=L: chk(lib.grpo_nf4_linear_partials_silu(
                     L["gu_parts"], L["down_w"].data_ptr(), L["down_absmax"].data_ptr(),
                     L["down_code"].data_ptr(), self.bs, L["down_parts"], st), "down")))

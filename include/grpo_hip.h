@@ -221,6 +221,21 @@ int grpo_nf4_linear_partials_silu(const grpo_linear_parts_t* gate_up, const uint
                                   const float* absmax, const float* code16, int blocksize,
                                   const grpo_linear_parts_t* parts, grpo_stream_t stream);
 
+/* act[m, j] = bf16(bf16(silu(g)) * u), g = bf16(x[m] . W[j]), u = bf16(x[m] .
+ * W[I + j]) for j < I: the gate and up NF4 projections of a stacked [2I, K]
+ * weight (bnb Params4bit, non-nested absmax; dequant of lora_forward.py:171-206,
+ * no bias, no LoRA) with fused_silu_mul (fused_ops.py:79-112) applied, as
+ * fused_mlp feeds down_proj (fused_ops.py:184-193).  act is bf16 [M, lda].
+ * Fast path only: M <= 16, I % 16 == 0, K % 256 == 0, K <= 6144, power-of-two
+ * blocksize >= 64, M * (K + 8) * 2 bytes of x plus the slice sums in 64 KiB of
+ * LDS; GRPO_EUNSUPPORTED otherwise (see grpo_nf4_gate_up_silu_supported). */
+int grpo_nf4_gate_up_silu(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                          const float* code16, int blocksize, int I, int K, int M, void* act,
+                          int64_t lda, grpo_stream_t stream);
+
+/* 1 if grpo_nf4_gate_up_silu takes this shape, else 0. */
+int grpo_nf4_gate_up_silu_supported(int M, int I, int K, int blocksize);
+
 /* ------------------------------------------------------- decode step --
  * Ops of the model-level decode step around the two hot-path kernels
  * (src/triton_kernels/paged_kv.py:690-820).  bf16 tensors are row-major. */

@@ -99,3 +99,51 @@ def test_add_rmsnorm_parts_matches_oracle(dev, n, lora, offset):
     assert rel_err(bf16_bits_to_f32(h_got), bf16_bits_to_f32(h_ref)) <= 1e-2
     assert np.mean(y_got == y_ref) >= 0.95
     assert rel_err(bf16_bits_to_f32(y_got), bf16_bits_to_f32(y_ref)) <= 1e-2
+
+
+@pytest.mark.parametrize("m,i,k", [(8, 8960, 1536), (3, 256, 512), (16, 512, 1536),
+                                   (8, 512, 3584)])
+def test_gate_up_silu_matches_oracle(dev, m, i, k):
+    """grpo_nf4_gate_up_silu = oracle NF4 linear of the gate and up halves of a
+    stacked weight, then oracle SiLU*mul (fused_ops.py:79-112)."""
+    from grpo_mi355x import _lib
+
+    from oracle.decode import silu_mul
+
+    lib = _lib.device_library()
+    bs = 64
+    assert lib.grpo_nf4_gate_up_silu_supported(m, i, k, bs) == 1
+    g = np.random.default_rng(m * 7 + i + k)
+    x = f32_to_bf16_bits(g.standard_normal((m, k)).astype(np.float32))
+    w = (g.standard_normal((2 * i, k)) * 0.05).astype(np.float32)
+    packed, absmax = quantize_nf4(w, bs)
+    t = lambda arr: torch.from_numpy(np.ascontiguousarray(arr)).to(dev)
+    # device buffers are kept in names until the kernel has run (a temporary
+    # freed before the asynchronous launch may be reused by the next copy)
+    x_d, pk_d, am_d = _dev_bf16(x, dev), t(packed), t(absmax)
+    code_d = t(NF4_CODE.astype(np.float32))
+    act = torch.zeros(m, i + 8, dtype=torch.bfloat16, device=dev)  # lda > I
+    _lib.check(lib.grpo_nf4_gate_up_silu(x_d.data_ptr(), k, pk_d.data_ptr(), am_d.data_ptr(),
+                                         code_d.data_ptr(), bs, i, k, m, act.data_ptr(), i + 8,
+                                         _lib.stream_handle(dev)), "gu")
+    torch.cuda.synchronize()
+    half = packed.size // 2, absmax.size // 2
+    gate = nf4_lora_linear(x, packed[:half[0]], absmax[:half[1]], i, k, bs)
+    up = nf4_lora_linear(x, packed[half[0]:], absmax[half[1]:], i, k, bs)
+    ref = silu_mul(gate, up)
+    got = _bits(act)[:, :i]
+    assert np.all(_bits(act)[:, i:] == 0)  # columns past I untouched
+    assert np.mean(got == ref) >= 0.97
+    assert rel_err(bf16_bits_to_f32(got), bf16_bits_to_f32(ref)) <= 1e-2
+
+
+def test_gate_up_silu_rejects_unsupported(dev):
+    from grpo_mi355x import _lib
+
+    lib = _lib.device_library()
+    assert lib.grpo_nf4_gate_up_silu_supported(17, 256, 512, 64) == 0  # M > 16
+    assert lib.grpo_nf4_gate_up_silu_supported(8, 250, 512, 64) == 0   # I % 16
+    assert lib.grpo_nf4_gate_up_silu_supported(8, 256, 500, 64) == 0   # K % 256
+    assert lib.grpo_nf4_gate_up_silu_supported(8, 256, 6400, 64) == 0  # K > 6144
+    assert lib.grpo_nf4_gate_up_silu(None, 512, None, None, None, 64, 256, 512, 17, None, 256,
+                                     None) == -2  # GRPO_EUNSUPPORTED
