@@ -514,7 +514,10 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg) {
   const int KS = K / KSTEP;
   p.NT = N / 16;
   p.ntiles = p.NT + (r > 0 ? nseg : 0);
-  const int s_target = (g_target_waves + p.ntiles - 1) / p.ntiles;
+  // Long K (down_proj, K = 8960): fewer, longer K slices measured faster
+  // (fewer partial sums to write and for the consumer to read back).
+  const int target = K >= 4096 ? g_target_waves / 2 : g_target_waves;
+  const int s_target = (target + p.ntiles - 1) / p.ntiles;
   int kpw = (KS + s_target - 1) / s_target;
   static const int choices[] = {1, 2, 3, 4, 6, 8};
   int pick = KPW_MAX;
