@@ -398,26 +398,40 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
     }
   }
   __syncthreads();
-  for (int i = tid; i < GQ * FD; i += AT) {
-    const int h = i / FD, d = i - h * FD;
+  // Per head (one thread each): the split's max M, the waves' weights
+  // 2^(m_w - M) and the split's sum L; then O four columns per thread.
+  __shared__ float sF[AW][GQ];
+  if (tid < GQ) {
+    const int h = tid;
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < AW; ++w) M = fmaxf(M, sM[w][h]);
-    float L = 0.f, O = 0.f;
-    if (M != -INFINITY) {
+    float L = 0.f;
 #pragma unroll
-      for (int w = 0; w < AW; ++w) {
-        const float f = exp2f(sM[w][h] - M);
-        L += f * sL[w][h];
-        O += f * sO[((size_t)w * GQ + h) * FD + d];
-      }
+    for (int w = 0; w < AW; ++w) {
+      const float f = M == -INFINITY ? 0.f : exp2f(sM[w][h] - M);
+      sF[w][h] = f;
+      L += f * sL[w][h];
     }
     const int64_t slot = ((int64_t)b * p.Hq + kvh * GQ + h) * p.S + s;
-    p.ws_o[slot * FD + d] = O;
-    if (d == 0) {
-      p.ws_ml[slot * 2] = M;
-      p.ws_ml[slot * 2 + 1] = L;
+    p.ws_ml[slot * 2] = M;
+    p.ws_ml[slot * 2 + 1] = L;
+  }
+  __syncthreads();
+  for (int i = tid; i < GQ * FD / 4; i += AT) {
+    const int h = i / (FD / 4), d4 = 4 * (i - h * (FD / 4));
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int w = 0; w < AW; ++w) {
+      const float f = sF[w][h];
+      const float4 v = *reinterpret_cast<const float4*>(sO + ((size_t)w * GQ + h) * FD + d4);
+      O.x += f * v.x;
+      O.y += f * v.y;
+      O.z += f * v.z;
+      O.w += f * v.w;
     }
+    const int64_t slot = ((int64_t)b * p.Hq + kvh * GQ + h) * p.S + s;
+    *reinterpret_cast<float4*>(p.ws_o + slot * FD + d4) = O;
   }
 }
 
