@@ -22,14 +22,31 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
   return (uint32_t)lo | ((uint32_t)hi << 16);
 }
 
+// Sum over a wave: DPP within each row of 16 lanes (xor 1, xor 2, half-row
+// mirror, row mirror), then the permlane swaps across rows; every lane gets
+// the total.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(
+      __builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp<0x141>(v);  // row_half_mirror
+  v += dpp<0x140>(v);  // row_mirror
+  return pair32_sum(pair16_sum(v));
+}
+
+// Sum over the workgroup, every thread gets the total.  Uses red[] once:
+// call it once per kernel (there is no trailing barrier).
 __device__ __forceinline__ float block_sum(float v, float* red) {
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o);
+  v = wave_sum(v);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   if (lane == 0) red[wave] = v;
   __syncthreads();
   float t = 0.f;
   for (int w = 0; w < (int)(blockDim.x >> 6); ++w) t += red[w];
-  __syncthreads();
   return t;
 }
 
