@@ -89,7 +89,7 @@ def rollout_bytes(cfg, model, stops, prompt_len, group, block_size=16):
                 steps=steps, weight_per_step=per_step_weights)
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "nf4_part_mfma_traffic_cfg3.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "nf4_linears_traffic_cfg3.md")
 
 
 def measured_traffic():
@@ -317,7 +317,7 @@ def main():
         achieved = tot_b / (tot_us * 1e-6) / 1e9
         roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
                         frac=round(achieved / PEAK_HBM_GBS, 4), traffic=measured_traffic(),
-                        kernel="nf4_part_mfma (q|k|v, o, gate|up, down of one decode step)",
+                        kernel="NF4 linears: nf4_part_mfma (q|k|v, o, down) + nf4_gate_up_silu (gate|up)",
                         avg_launch_us=round(tot_us / n, 3), bytes_per_launch=tot_b // n)
         log(f"kernel timing: {kernels}")
 
