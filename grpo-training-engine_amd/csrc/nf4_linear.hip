@@ -42,7 +42,10 @@ constexpr int KSTEP = 256;          // k elements per step: 4 lane groups x 64
 constexpr int PART_WAVES = 4;       // n-tiles (waves) per workgroup, x given in bf16
 constexpr int PART_LDS_MAX = 65536; // bytes of the staged x slice per workgroup
 constexpr int KPW_MAX = 8;          // k-steps per wave (all loads in flight at once)
-int g_target_waves = 2048;          // launch-shape target: 8 waves per CU on 256 CUs
+#ifndef GRPO_TARGET_WAVES
+#define GRPO_TARGET_WAVES 2048
+#endif
+int g_target_waves = GRPO_TARGET_WAVES;  // launch-shape target: 8 waves per CU on 256 CUs
 
 // ------------------------------------------------------------- dequant --
 
@@ -143,9 +146,10 @@ struct PartArgs {
   const float* code16;
   int bs_shift;  // log2(blocksize)
   const uint16_t* la[MAXSEG];
-  float* part;
-  float* tpart;
+  float* part;   // rows of this launch: part[slice][m][n] at slice stride Mp*N
+  float* tpart;  // tpart[slice][seg][m][16] at seg stride Mp*16
   int M, N, K, NT, ntiles, nseg, r;
+  int Mp;       // rows of the partial-sum layout (M, or more when rows are launched in chunks)
   int xstride;  // LDS row stride of the staged x slice (elements)
   // x = decode attention output given as split partials (o_proj of the decode step)
   const float* att_o;    // [M][Hq][S][128] unnormalised O
@@ -432,7 +436,7 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
               *reinterpret_cast<const uint4*>(xrow[mt] + i * KSTEP + 8 * j), bw, acc[mt]);
       }
     }
-    float* out = p.part + (int64_t)slice * p.M * p.N + n_row;
+    float* out = p.part + (int64_t)slice * p.Mp * p.N + n_row;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -462,7 +466,7 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
               *reinterpret_cast<const uint4*>(xrow[mt] + i * KSTEP + 8 * j), bv, acc[mt]);
       }
     }
-    float* out = p.tpart + ((int64_t)slice * p.nseg + seg) * p.M * 16 + ln;
+    float* out = p.tpart + ((int64_t)slice * p.nseg + seg) * p.Mp * 16 + ln;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -491,12 +495,16 @@ __global__ void __launch_bounds__(256) nf4_finish(LinParts o, uint16_t* __restri
 
 struct PartPlan {
   int MT, NT, ntiles, kpw, S, xstride;
+  int mchunk;  // rows per launch: M, or a multiple of 16 when x of M rows overflows LDS
+  bool ok;     // false: no (k-steps, row chunk) fits both the slice cap and LDS
   size_t lds, part_bytes, tpart_bytes;
 };
 
 bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
 // Shape-level support of the split-K path (alignment is checked per call).
+PartPlan plan_part(int M, int N, int K, int r, int nseg);
+
 bool part_shape_ok(int M, int N, int K, int r, int nseg, int blocksize, const int* seg_end) {
   if (!(M >= 1 && M <= 64 && N > 0 && N % 16 == 0 && K > 0 && K % KSTEP == 0)) return false;
   if (K > MAX_SLICES * KPW_MAX * KSTEP) return false;  // K <= 32768
@@ -504,7 +512,7 @@ bool part_shape_ok(int M, int N, int K, int r, int nseg, int blocksize, const in
   if (!pow2(blocksize) || blocksize < 64) return false;
   for (int s = 0; seg_end && s < nseg; ++s)
     if (seg_end[s] % 16 != 0) return false;
-  return true;
+  return plan_part(M, N, K, r, nseg).ok;
 }
 
 PartPlan plan_part(int M, int N, int K, int r, int nseg) {
@@ -543,7 +551,20 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg) {
   p.kpw = pick;
   p.S = (KS + pick - 1) / pick;
   p.xstride = pick * KSTEP + 8;
-  p.lds = (size_t)M * p.xstride * 2;
+  // Wide batches of long-K linears (M = 64 at K = 18944 needs 6 k-steps per
+  // slice for <= MAX_SLICES slices) stage more x than LDS holds: their rows are
+  // launched in chunks of 16-row multiples, each writing its rows of the same
+  // partial-sum layout.
+  p.mchunk = M;
+  const size_t row_bytes = (size_t)p.xstride * 2;
+  if ((size_t)M * row_bytes > PART_LDS_MAX)
+    p.mchunk = 16 * (int)(PART_LDS_MAX / (16 * row_bytes));
+  p.ok = p.mchunk >= 1 && p.S <= MAX_SLICES;
+  if (p.mchunk < M) {
+    p.MT = p.mchunk / 16;
+    if (p.MT == 3) p.MT = 2, p.mchunk = 32;  // chunks run on the MT = 1, 2 or 4 kernel
+  }
+  p.lds = (size_t)std::min(M, std::max(p.mchunk, 1)) * row_bytes;
   p.part_bytes = (size_t)p.S * M * N * 4;
   p.tpart_bytes = r > 0 ? (size_t)p.S * nseg * M * 16 * 4 : 0;
   return p;
@@ -595,6 +616,14 @@ int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* 
     return GRPO_EUNSUPPORTED;
   }
   const PartPlan pl = plan_part(h.M, h.N, h.K, h.r, h.nseg);
+  if (!pl.ok) {
+    set_error("shape not supported by the split-K NF4 linear");
+    return GRPO_EUNSUPPORTED;
+  }
+  if (xsrc && pl.mchunk < h.M) {
+    set_error("x staged from attention or gate|up partials must fit LDS in one launch");
+    return GRPO_EUNSUPPORTED;
+  }
   if (h.splits != pl.S) return einval("parts.splits differs from grpo_nf4_linear_plan");
   if ((!x && !xsrc) || !w || !absmax || !code16 || !h.part) return einval("null pointer");
   if (h.r > 0 && !h.tpart) return einval("r > 0 needs tpart");
@@ -615,6 +644,7 @@ int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* 
   a.part = h.part;
   a.tpart = h.tpart;
   a.M = h.M;
+  a.Mp = h.M;
   a.N = h.N;
   a.K = h.K;
   a.NT = pl.NT;
@@ -645,11 +675,21 @@ int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* 
       default: return launch_part<4, X_SILU>(a, pl, st);
     }
   }
-  switch (pl.MT) {
-    case 1: return launch_part<1, X_BF16>(a, pl, st);
-    case 2: return launch_part<2, X_BF16>(a, pl, st);
-    default: return launch_part<4, X_BF16>(a, pl, st);
+  for (int m0 = 0; m0 < h.M; m0 += pl.mchunk) {
+    PartArgs c = a;
+    c.M = std::min(pl.mchunk, h.M - m0);
+    c.x = x + (int64_t)m0 * ldx;
+    c.part = h.part + (int64_t)m0 * h.N;
+    c.tpart = h.tpart ? h.tpart + (int64_t)m0 * 16 : nullptr;
+    int rc;
+    switch (pl.MT) {
+      case 1: rc = launch_part<1, X_BF16>(c, pl, st); break;
+      case 2: rc = launch_part<2, X_BF16>(c, pl, st); break;
+      default: rc = launch_part<4, X_BF16>(c, pl, st); break;
+    }
+    if (rc) return rc;
   }
+  return GRPO_OK;
 }
 
 int run_finish(const grpo_linear_parts_t* h, uint16_t* y, int64_t ldy, hipStream_t st) {
@@ -793,7 +833,10 @@ __global__ void __launch_bounds__(128 * S) nf4_gate_up_silu(GuArgs p) {
   }
 }
 
-int g_gu_kpw = 3;  // k-steps per wave of the gate|up kernel (S = ceil(K/256 / kpw) <= 8); measured best
+#ifndef GRPO_GU_KPW
+#define GRPO_GU_KPW 3
+#endif
+int g_gu_kpw = GRPO_GU_KPW;  // k-steps per wave of the gate|up kernel (S = ceil(K/256 / kpw) <= 8); measured best
 
 struct GuPlan {
   int kpw, S, MT;
@@ -1005,6 +1048,10 @@ extern "C" int grpo_nf4_linear_plan(int M, int N, int K, int r, int nseg, int bl
     return GRPO_EUNSUPPORTED;
   }
   const PartPlan pl = plan_part(M, N, K, r, nseg);
+  if (!pl.ok) {
+    set_error("shape not supported by the split-K NF4 linear");
+    return GRPO_EUNSUPPORTED;
+  }
   if (splits) *splits = pl.S;
   if (part_bytes) *part_bytes = pl.part_bytes;
   if (tpart_bytes) *tpart_bytes = pl.tpart_bytes;

@@ -117,10 +117,12 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
   return (uint32_t)lo | ((uint32_t)hi << 16);
 }
 
-constexpr int QKV_MAX_SLICES = 8;  // K slices of the q|k|v projection read here
-typedef Fetch4<QKV_MAX_SLICES> QkvFetch;
+// K slices of the q|k|v projection the fused prologue reads: MS = 8 covers
+// the decode shapes up to M = 16 rows; wide batches of long-K models (M = 64 at
+// hidden 3584: 14 slices) take the MS = 16 instantiation.
+constexpr int QKV_SLICES_SMALL = 8;
 
-template <int GQ, bool FUSED>
+template <int GQ, bool FUSED, int MS = QKV_SLICES_SMALL>
 __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
@@ -176,8 +178,8 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
   static_assert(NROW * (FD / 4) <= AT - 64, "the last wave fetches no q|k|v row");
   const int row = tid / (FD / 4), d4 = 4 * (tid % (FD / 4));
   const int t_item = tid - (AT - 64);  // LoRA t item of a last-wave lane
-  QkvFetch f;
-  float4 tv[QKV_MAX_SLICES];
+  Fetch4<MS> f;
+  float4 tv[MS];
   uint4 qv = make_uint4(0, 0, 0, 0);
   if constexpr (FUSED) {
     // LoRA t by the last wave (no q|k|v rows; its first K/V is needed only
@@ -570,7 +572,11 @@ int launch_split(const AttnArgs& a, hipStream_t st) {
   // then the split's block-table slice
   const size_t lds = (size_t)AW * GQ * FD * sizeof(float) + (size_t)a.bps * sizeof(int);
   if (lds > 65536) return einval("context too long for the split attention kernel");
-  paged_attn_split<GQ, FUSED><<<dim3(a.S, a.Hkv, a.B), AT, lds, st>>>(a);
+  const dim3 grid(a.S, a.Hkv, a.B);
+  if (FUSED && a.qkv.S > QKV_SLICES_SMALL)
+    paged_attn_split<GQ, FUSED, MAX_SLICES><<<grid, AT, lds, st>>>(a);
+  else
+    paged_attn_split<GQ, FUSED><<<grid, AT, lds, st>>>(a);
   return launch_check("paged_attn_split");
 }
 
@@ -698,8 +704,8 @@ extern "C" int grpo_paged_attn_decode_qkv(const grpo_linear_parts_t* qkv, int Hq
     return GRPO_EUNSUPPORTED;
   }
   if (a.qkv.N != (Hq + 2 * Hkv) * D) return einval("qkv width must be (Hq + 2 Hkv) * D");
-  if (a.qkv.S > QKV_MAX_SLICES) {
-    set_error("fused q|k|v attention reads at most 8 K slices of the projection");
+  if (a.qkv.S > MAX_SLICES) {
+    set_error("fused q|k|v attention reads at most %d K slices of the projection", MAX_SLICES);
     return GRPO_EUNSUPPORTED;
   }
   if (!cos_table || !sin_table || !append_pos || !context_lens || !k_cache || !v_cache ||

@@ -382,6 +382,61 @@ class DecodeEngine:
         for _ in range(steps):
             self.step()
 
+    def run_paged(self, sids: list, max_steps: int, chunk: Optional[int] = None,
+                  check_invariants: bool = False) -> dict:
+        """Decode until every row has stopped (or ``max_steps``), allocating each
+        row's KV blocks one chunk ahead and releasing them when the row stops.
+
+        ``sids[b]`` is the pool sequence of row ``b`` (its table row already
+        loaded by ``start``).  Every ``chunk`` steps (default: the block size,
+        so a row needs at most one new block per chunk) the host reads the
+        rows' positions and activity -- the only synchronisation -- then
+        releases the blocks of rows that stopped (``PagedKVPool.free``: shared
+        prompt blocks return to the free list with their last reference),
+        reserves blocks for the next ``chunk`` positions of every active row and
+        writes the new entries into the device block table.  The steps in
+        between are graph replays.  The reference allocates one cache for the
+        whole call instead (``paged_kv.py:626-645``); BASELINE config 4 asks
+        for blocks allocated and freed as sequences finish.
+
+        Returns ``dict(steps, peak_blocks)``: decode steps run and the most
+        blocks in use at once.
+        """
+        pool = self.pool
+        chunk = chunk or pool.block_size
+        live = {b: s for b, s in enumerate(sids)}
+        steps = peak = 0
+        while True:
+            pos = self.pos.cpu().tolist()
+            act = self.active.cpu().tolist()
+            for b in [b for b in live if not act[b]]:
+                pool.free(live.pop(b))
+                self.block_tables[b].fill_(-1)
+            if not live or steps >= max_steps:
+                break
+            n = min(chunk, max_steps - steps)
+            for b, sid in live.items():
+                have = len(pool.blocks[sid])
+                pool.set_length(sid, pos[b])
+                pool.reserve(sid, pos[b] + n)  # slots pos .. pos + n - 1
+                bl = pool.blocks[sid]
+                if len(bl) > self.max_blocks:
+                    raise RuntimeError(f"row {b} needs {len(bl)} blocks; the engine's block "
+                                       f"table holds {self.max_blocks}")
+                if len(bl) > have:
+                    self.block_tables[b, have:len(bl)].copy_(
+                        torch.tensor(bl[have:], dtype=torch.int32))
+            if check_invariants:
+                pool.check_invariants()
+            peak = max(peak, pool.num_blocks - pool.num_free)
+            for _ in range(n):
+                self.step()
+            steps += n
+        for b in list(live):  # rows cut off by max_steps
+            pool.free(live.pop(b))
+            self.block_tables[b].fill_(-1)
+        return dict(steps=steps, peak_blocks=peak)
+
 
 # ------------------------------------------------------------- drop-in ---
 
@@ -431,7 +486,10 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
     Rows with identical (unpadded) prompts share one prefill; their full prompt
     blocks are shared through the pool and the partial last block is copied
     per row.  ``stop_lengths`` (an extension) caps each row's generated length.
-    Greedy decoding runs entirely in the captured graph.
+    Greedy decoding runs in the captured graph; every block-size steps the host
+    gives growing rows their next block and frees the blocks of rows that
+    stopped (``DecodeEngine.run_paged``), and decoding ends once every row has
+    stopped (the reference's ``finished.all()`` exit, ``paged_kv.py:903``).
     """
     if max_new_tokens <= 0:
         raise ValueError(f"max_new_tokens must be > 0, got {max_new_tokens}.")
@@ -456,7 +514,8 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
     parents = {p: prefill(eng1, pool, p, width) for p in uniq}
     sids = []
     for r in rows:
-        (cid,) = pool.fork(parents[r], 1, reserve_tokens=len(r) - 1 + max_new_tokens + 1)
+        # room for the first decode slot; run_paged grows the row from there
+        (cid,) = pool.fork(parents[r], 1, reserve_tokens=len(r))
         sids.append(cid)
     for p in parents.values():
         pool.free(p)
@@ -473,7 +532,7 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
               torch.tensor([len(r) - 1 for r in rows], device=dev),
               pool.block_table(sids, width, device=dev), limits, max_new_tokens,
               eos_token_id=eos_token_id, pad_token_id=pad_token_id)
-    eng.run(max_new_tokens)
+    eng.run_paged(sids, max_new_tokens)
     return eng.generated.clone()
 
 

@@ -62,7 +62,8 @@ def test_split_k_plan_covers_k_exactly():
 
     for m, n, k, r, nseg in [(8, 2048, 1536, 16, 3), (8, 1536, 1536, 16, 1), (8, 17920, 1536, 0, 1),
                              (8, 1536, 8960, 0, 1), (64, 512, 3584, 16, 3), (1, 256, 512, 16, 1),
-                             (33, 256, 768, 16, 1), (8, 3584, 18944, 0, 1)]:
+                             (33, 256, 768, 16, 1), (8, 3584, 18944, 0, 1),
+                             (64, 3584, 18944, 0, 1), (64, 4608, 3584, 16, 3)]:
         splits, pb, tb = ops.nf4_linear_plan(m, n, k, r, nseg, 64)
         ks = k // 256
         assert any(splits * kpw >= ks > (splits - 1) * kpw for kpw in (1, 2, 3, 4, 6, 8))
@@ -70,6 +71,8 @@ def test_split_k_plan_covers_k_exactly():
         assert tb == (splits * nseg * m * 16 * 4 if r else 0)
     assert ops.nf4_linear_plan(8, 40, 512, 0, 1, 64) is None  # N % 16
     assert ops.nf4_linear_plan(65, 256, 512, 0, 1, 64) is None  # M > 64
+    # 16 slices of 8 k-steps: even 16 staged rows of x exceed LDS
+    assert ops.nf4_linear_plan(16, 256, 32768, 0, 1, 64) is None
 
 
 def test_argument_errors_return_negative_codes(lib):

@@ -1,0 +1,134 @@
+"""BASELINE config 4 on the GPU: a ragged group with blocks allocated and freed as rows finish.
+
+G = 32 rows = 4 prompts x 8 samples, prompt lengths uniform in [128, 256] (config 4
+uses [128, 512]; shortened so the oracle's token-by-token prefill stays quick),
+response lengths from a long-tail lognormal (median 20, sigma 0.75, capped at 64;
+config 4: median 200, capped at 1024), block size 16, on a tiny Qwen2-shaped
+NF4+LoRA model.  Greedy decoding makes the 8 samples of a prompt identical up to
+their stops, so the oracle decodes each prompt once.
+
+Checked: every row's tokens equal the oracle's greedy tokens up to its stop
+(compared up to the first step whose oracle top-2 logit margin is inside the
+bf16 tolerance, after which a near-tie may legitimately flip) and pad after it;
+the pool's invariants hold at every chunk; blocks are reserved one chunk ahead
+(peak use below an up-front reservation of every row's maximum); every block
+is back on the free list at the end.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.bf16 import bf16_bits_to_f32
+from oracle.decode import Qwen2DecodeOracle
+
+from model_export import export
+
+pytestmark = pytest.mark.gpu
+
+PAD = 0
+
+
+def _model(dev, seed=9):
+    from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
+
+    cfg = Qwen2Config.tiny(layers=2, heads=4, kv_heads=2, head_dim=128, inter=1024, vocab=1024)
+    return build_random_model(cfg, dev, seed=seed)
+
+
+def _workload(seed=4, prompts=4, samples=8, new=64):
+    g = np.random.default_rng(seed)
+    lens = g.integers(128, 257, prompts)
+    plist = [g.integers(1, 1000, n).tolist() for n in lens]
+    stops = np.minimum(new, np.maximum(1, np.round(g.lognormal(np.log(20.0), 0.75,
+                                                                prompts * samples)))).astype(int)
+    rows = [plist[i // samples] for i in range(prompts * samples)]
+    return plist, rows, stops.tolist(), new
+
+
+def _oracle_greedy(oracle, prompt, new):
+    """Greedy tokens after ``prompt`` and whether each step's top-2 margin is safe."""
+    width = -(-(len(prompt) + new) // 16)
+    kcs = [np.zeros((width, 2, 16, 128), np.uint16) for _ in range(2)]
+    vcs = [np.zeros_like(k) for k in kcs]
+    tab = np.arange(width, dtype=np.int32)[None]
+    tok, out, safe = prompt[0], [], []
+    for t in range(len(prompt) - 1 + new):
+        tok_in = prompt[t] if t < len(prompt) else tok
+        logits, nxt = oracle.step(np.array([tok_in]), kcs, vcs, tab, np.array([t]))
+        if t >= len(prompt) - 1:
+            lr = bf16_bits_to_f32(logits[0])
+            srt = np.sort(lr)
+            safe.append(srt[-1] - srt[-2] > 1e-2 * np.abs(lr).max())
+            out.append(int(nxt[0]))
+            tok = int(nxt[0])
+    return np.array(out), np.array(safe)
+
+
+def test_cfg4_ragged_group_matches_oracle(dev):
+    from grpo_mi355x.kernels import paged_kv_decode
+
+    model = _model(dev)
+    plist, rows, stops, new = _workload()
+    L = max(len(r) for r in rows)
+    ids = torch.full((len(rows), L), PAD, dtype=torch.int64)
+    mask = torch.zeros_like(ids)
+    for b, r in enumerate(rows):  # left padding, as a tokenizer batch would give
+        ids[b, L - len(r):] = torch.tensor(r)
+        mask[b, L - len(r):] = 1
+    got = paged_kv_decode(model, ids.to(dev), attention_mask=mask.to(dev), max_new_tokens=new,
+                          do_sample=False, pad_token_id=PAD, eos_token_id=None,
+                          stop_lengths=stops).cpu().numpy()
+    assert got.shape == (len(rows), new)
+    w, c = export(model)
+    oracle = Qwen2DecodeOracle(w, c)
+    refs = [_oracle_greedy(oracle, p, max(s for r, s in zip(rows, stops) if r is p or r == p))
+            for p in plist]
+    compared = 0
+    for b, (r, stop) in enumerate(zip(rows, stops)):
+        ref, safe = refs[plist.index(r)]
+        unsafe = np.flatnonzero(~safe[:stop])
+        n = int(unsafe[0]) if unsafe.size else stop  # tokens before the first near-tie
+        assert np.array_equal(got[b, :n], ref[:n]), (b, got[b, :n], ref[:n])
+        assert np.all(got[b, stop:] == PAD)
+        compared += n
+    # a random tiny model has small top-2 margins: a near-tie ends the comparison of
+    # its prompt's rows, so at least half of the tokens must be compared
+    assert compared >= 0.5 * sum(stops)
+
+
+def test_cfg4_blocks_allocated_ahead_and_freed(dev):
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine, prefill
+
+    model = _model(dev)
+    plist, rows, stops, new = _workload(seed=5)
+    width = -(-(max(len(p) for p in plist) + new) // 16)
+    B = len(rows)
+    nblocks = len(plist) * width + B * (width + 1)
+    pool = PagedKVPool(2, nblocks, 2, 128, 16, device=dev)
+    eng1 = DecodeEngine(model, pool, 1, width)
+    eng1.capture()
+    parents = [prefill(eng1, pool, tuple(p), width) for p in plist]
+    sids = [pool.fork(parents[plist.index(r)], 1, reserve_tokens=len(r))[0] for r in rows]
+    for p in parents:
+        pool.free(p)
+    pool.check_invariants()
+    upfront = sum(-(-(len(r) + new) // 16) for r in rows)  # private reservation per row
+    eng = DecodeEngine(model, pool, B, width)
+    start = dict(tokens=torch.tensor([r[-1] for r in rows], device=dev),
+                 positions=torch.tensor([len(r) - 1 for r in rows], device=dev),
+                 block_tables=pool.block_table(sids, width, device=dev),
+                 limits=torch.tensor(stops, device=dev), max_new_tokens=new)
+    eng.start(**start)
+    eng.capture()
+    eng.start(**start)
+    stats = eng.run_paged(sids, new, check_invariants=True)
+    torch.cuda.synchronize()
+    assert stats["steps"] <= max(stops) + 16
+    assert stats["peak_blocks"] < upfront
+    assert pool.num_free == pool.num_blocks and not pool.blocks
+    pool.check_invariants()
+    gen = eng.generated.cpu().numpy()
+    for b, s in enumerate(stops):
+        assert np.all(gen[b, s:] == 0) and np.all(gen[b, :s] >= 0)

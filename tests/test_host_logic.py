@@ -140,3 +140,48 @@ def test_manual_lora_layer_surface():
     assert len(get_lora_parameters(m)) == 2
     # the quant state survives the dtype cast of inject_lora_layers
     assert m.q_proj.base_layer.weight.quant_state.absmax.dtype == torch.float32
+
+
+def test_run_paged_reserves_ahead_and_frees_stopped_rows():
+    """DecodeEngine.run_paged's block accounting, with a host stand-in for the
+    graph step: every slot a row writes is mapped and private when written,
+    rows get blocks one chunk ahead, stopped rows release theirs."""
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine
+
+    pool = PagedKVPool(1, 64, 1, 8, block_size=4)
+    parent = pool.allocate(6)
+    pool.set_length(parent, 6)
+    sids = pool.fork(parent, 3, reserve_tokens=7)
+    pool.free(parent)
+    limits = [1, 5, 13]
+
+    class Stand:
+        def __init__(self):
+            self.pool, self.max_blocks = pool, 8
+            self.pos = torch.full((3,), 6, dtype=torch.int32)
+            self.count = torch.zeros(3, dtype=torch.int32)
+            self.active = torch.ones(3, dtype=torch.bool)
+            self.block_tables = pool.block_table(sids, 8)
+            self.in_use = []
+
+        def step(self):
+            self.in_use.append(pool.num_blocks - pool.num_free)
+            for b in range(3):
+                if not self.active[b]:
+                    continue
+                blk = int(self.block_tables[b, int(self.pos[b]) // 4])
+                assert blk >= 0 and pool.refcount[blk] == 1
+                self.pos[b] += 1
+                self.count[b] += 1
+                if int(self.count[b]) >= limits[b]:
+                    self.active[b] = False
+
+    s = Stand()
+    stats = DecodeEngine.run_paged(s, sids, 50, check_invariants=True)
+    assert stats["steps"] == 16  # the longest row stops in the 4th chunk of 4
+    assert s.count.tolist() == limits
+    # 7 private slots for 6 + 13 tokens: at most one chunk ahead of each live row
+    assert stats["peak_blocks"] <= 1 + 3 + 2 + 2 + 5
+    assert pool.num_free == pool.num_blocks and not pool.blocks
+    assert torch.all(s.block_tables == -1)
