@@ -61,6 +61,10 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first stream a 256 MiB buffer through a copy-like kernel 3 times "
                          "(scale reference for the HBM FETCH_SIZE/WRITE_SIZE counters)")
+    ap.add_argument("--config", type=int, default=3, choices=(3, 4, 5),
+                    help="BASELINE config: 3 (default, the headline metric), 4 (G=32 ragged "
+                         "group, blocks freed as rows stop) or 5 (Qwen2-7B shape, G=64, "
+                         "long contexts); 4 and 5 are extra measurements, not the headline")
     return ap.parse_args()
 
 
@@ -214,6 +218,156 @@ def cpu_baseline(model, cfg, group, ctx, seed):
                         "(numpy: elementwise single-threaded, BLAS matmuls multi-threaded)"))
 
 
+def _emit(args, value, unit, ms_step, workload, extra):
+    out = {"metric": METRIC, "value": round(value, 2), "unit": unit, "n_gpus": 1,
+           "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 3),
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+           "data": "synthetic (random-init weights N(0,0.02) -> NF4, LoRA N(0,0.01); random "
+                   "prompts)", "config": dict(workload=workload, parallelism="single GPU")}
+    out.update(extra)
+    print(json.dumps(out), flush=True)
+
+
+def run_cfg4(args):
+    """G = 32 (4 prompts x 8 samples), prompts U[128, 512],
+    responses lognormal (median 200, sigma 0.75) capped at 1024, blocks reserved
+    one block ahead and freed as rows stop (DecodeEngine.run_paged).  One timed
+    step = one rollout: fork the 8 samples of each prefilled prompt, decode until
+    every row stops (blocks released on the way)."""
+    import numpy as np
+    import torch
+
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine, prefill
+    from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
+
+    dev = torch.device("cuda:0")
+    cfg = Qwen2Config.qwen2_1_5b()
+    cfg.num_hidden_layers = args.layers
+    rng = np.random.default_rng(args.seed)
+    P, S, NEW, BS = 4, 8, 1024, 16
+    lens = rng.integers(128, 513, P).tolist()
+    prompts = [rng.integers(0, cfg.vocab_size, n).tolist() for n in lens]
+    stops = np.minimum(NEW, np.maximum(1, np.round(rng.lognormal(np.log(200.0), 0.75, P * S))))
+    stops = stops.astype(int).tolist()
+    model = build_random_model(cfg, dev, seed=args.seed)
+    width = -(-(max(lens) + NEW) // BS)
+    G = P * S
+    pool = PagedKVPool(cfg.num_hidden_layers, P * width + G * (width + 1),
+                       cfg.num_key_value_heads, cfg.head_dim, BS, device=dev)
+    eng1 = DecodeEngine(model, pool, 1, width)
+    eng1.capture()
+    parents = [prefill(eng1, pool, tuple(p), width) for p in prompts]
+    del eng1
+    eng = DecodeEngine(model, pool, G, width)
+    rows = [prompts[i // S] for i in range(G)]
+
+    def rollout():
+        sids = [pool.fork(parents[i // S], 1, reserve_tokens=len(rows[i]))[0] for i in range(G)]
+        eng.start(torch.tensor([r[-1] for r in rows], device=dev),
+                  torch.tensor([len(r) - 1 for r in rows], device=dev),
+                  pool.block_table(sids, width, device=dev), torch.tensor(stops, device=dev),
+                  NEW)
+        return sids
+
+    sids = rollout()
+    eng.capture()
+    peak = 0
+    for _ in range(args.warmup):
+        eng.run_paged(sids, NEW)
+        sids = rollout()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    nsteps = 0
+    for i in range(args.steps):
+        st = eng.run_paged(sids, NEW)
+        nsteps, peak = st["steps"], st["peak_blocks"]
+        if i + 1 < args.steps:
+            sids = rollout()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    assert pool.num_free == pool.num_blocks - sum(len(pool.blocks[p]) for p in parents)
+    value = sum(stops) * args.steps / elapsed
+    log(f"config 4: {value:.1f} tok/s, {nsteps} decode steps per rollout, peak {peak} of "
+        f"{pool.num_blocks} blocks")
+    _emit(args, value, "tok/s", elapsed / args.steps * 1e3,
+          "BASELINE config 4: Qwen2-1.5B-shaped NF4+LoRA decode, G=32 (4 prompts x 8), prompts "
+          "U[128,512], responses lognormal(median 200, sigma 0.75) capped at 1024, blocks "
+          "freed as rows stop; step = one ragged rollout",
+          dict(prompt_lens=lens, response_tokens=sum(stops), decode_steps_per_rollout=nsteps,
+               us_per_decode_step=round(elapsed / args.steps / max(nsteps, 1) * 1e6, 2),
+               peak_blocks=peak, pool_blocks=pool.num_blocks))
+
+
+def run_cfg5(args):
+    """Qwen2-7B shape (28 layers), G = 64, contexts U[1024, 4096]
+    over a KV pool pre-filled with N(0, 1) bf16 (decode-only: no 4k prefill).  One
+    timed step = one decode step of the 64 rows (graph replay)."""
+    import numpy as np
+    import torch
+
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine
+    from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
+
+    dev = torch.device("cuda:0")
+    cfg = Qwen2Config.qwen2_7b()
+    cfg.num_hidden_layers = args.layers
+    rng = np.random.default_rng(args.seed)
+    G, BS = 64, 16
+    steps = args.steps * 16
+    ctx = rng.integers(1024, 4097, G)
+    width = -(-(int(ctx.max()) + steps + (args.warmup + 1) * 16) // BS)
+    need = [-(-(int(c) + steps + (args.warmup + 1) * 16) // BS) for c in ctx]
+    nb = sum(need)
+    model = build_random_model(cfg, dev, seed=args.seed)
+    pool = PagedKVPool(cfg.num_hidden_layers, nb, cfg.num_key_value_heads, cfg.head_dim, BS,
+                       device=dev)
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    for li in range(cfg.num_hidden_layers):
+        pool.k[li].normal_(generator=gen)
+        pool.v[li].normal_(generator=gen)
+    perm = rng.permutation(nb).astype(np.int32)
+    tables = np.full((G, width), -1, np.int32)
+    o = 0
+    for b in range(G):
+        tables[b, :need[b]] = perm[o:o + need[b]]
+        o += need[b]
+    eng = DecodeEngine(model, pool, G, width)
+    start = dict(tokens=torch.from_numpy(rng.integers(0, cfg.vocab_size, G)).to(dev),
+                 positions=torch.from_numpy(ctx).to(dev),
+                 block_tables=torch.from_numpy(tables).to(dev),
+                 limits=torch.full((G,), 1 << 20, device=dev), max_new_tokens=steps + 64)
+    eng.start(**start)
+    eng.capture()
+    eng.start(**start)
+    eng.run(16 * args.warmup)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    eng.run(steps)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    value = G * steps / elapsed
+    kv = int(eng.attn_len.sum().item()) * cfg.num_key_value_heads * cfg.head_dim * 2 * 2 \
+        * cfg.num_hidden_layers
+    wb = sum(model.weight_bytes().values())
+    step_s = elapsed / steps
+    log(f"config 5: {value:.1f} tok/s, {step_s * 1e6:.1f} us/decode step")
+    kernels = {} if args.no_kernel_timing else kernel_timing(eng, dev)
+    if kernels:
+        ab = eng.attention_bytes()
+        kernels["attention"].update(bytes_per_launch=ab, achieved_GBs=round(
+            ab / (kernels["attention"]["avg_us"] * 1e-6) / 1e9, 1))
+    _emit(args, value, "tok/s", step_s * 1e3,
+          "BASELINE config 5: Qwen2-7B-shaped NF4+LoRA decode, G=64, contexts U[1024,4096], KV "
+          "pool pre-filled N(0,1) bf16 (decode only); step = one decode step of 64 rows",
+          dict(us_per_decode_step=round(step_s * 1e6, 2),
+               step_hbm=dict(weight_bytes=wb, kv_bytes=kv,
+                             achieved_GBs=round((wb + kv) / step_s / 1e9, 1),
+                             frac_of_peak=round((wb + kv) / step_s / 1e9 / PEAK_HBM_GBS, 4)),
+               kernels=kernels))
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -221,6 +375,11 @@ def main():
               "multi-GPU path (rollout groups would shard data-parallel, one group per GPU).",
               file=sys.stderr)
         sys.exit(2)
+    if args.config != 3:
+        from grpo_mi355x import _lib
+
+        _lib.device_library()
+        return run_cfg4(args) if args.config == 4 else run_cfg5(args)
     import numpy as np
     import torch
 
