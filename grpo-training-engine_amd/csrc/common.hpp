@@ -89,6 +89,36 @@ __device__ __forceinline__ float pair32_max(float v) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// Kernel arguments are read with scalar loads that the compiler places where a
+// field is first needed; a kernel whose early branches use fields from several
+// 64-byte lines of the argument segment then waits for one scalar-cache miss
+// after another (each a memory round trip at kernel start).  Touching every
+// line of the first BYTES bytes at entry issues those misses together; the
+// later argument loads hit the scalar cache.
+template <int BYTES>
+__device__ __forceinline__ void touch_kernargs() {
+  constexpr int LINES = (BYTES + 63) / 64;
+  static_assert(LINES <= 8, "argument segment larger than 512 bytes");
+  typedef const __attribute__((address_space(4))) uint32_t* kernarg_ptr;
+  const kernarg_ptr k = (kernarg_ptr)__builtin_amdgcn_kernarg_segment_ptr();
+  uint32_t v[8];
+#pragma unroll
+  for (int i = 0; i < LINES; ++i) v[i] = k[i * 16];
+#pragma unroll
+  for (int i = 0; i < LINES; ++i) asm volatile("" ::"s"(v[i]));
+}
+
+// Value from a wave-uniform address that no thread writes during the kernel,
+// read through the constant address space: a scalar load, whose wait
+// (lgkmcnt) does not hold back the wave's vector loads.  (A plain load of a
+// uniform address is a vector load that must be waited for, and moved to a
+// scalar register, before the loads that follow it can be issued.)
+template <typename T>
+__device__ __forceinline__ T load_uniform(const T* ptr) {
+  typedef const __attribute__((address_space(4))) T* cptr;
+  return *(cptr)ptr;
+}
+
 __device__ __forceinline__ f32x4_t mfma16x16x32(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }

@@ -191,6 +191,7 @@ __global__ void __launch_bounds__(AMAX_T) argmax_kernel(const uint16_t* __restri
 __global__ void __launch_bounds__(PARTS_T) add_rmsnorm_parts_kernel(
     LinParts o, const uint16_t* residual, uint16_t* h_out, const uint16_t* __restrict__ w,
     uint16_t* __restrict__ y, float eps, bool vec) {
+  touch_kernargs<sizeof(LinParts) + 4 * sizeof(void*) + 8>();
   __shared__ float red[PARTS_T / 64];
   __shared__ float ts[MAXSEG * 16];
   extern __shared__ float hs[];  // H floats (columns past 4 * PARTS_T only)

@@ -52,6 +52,7 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
 
 template <int MT>
 __global__ void __launch_bounds__(64 * LM_WAVES) lm_head_argmax_kernel(LmArgs p) {
+  touch_kernargs<sizeof(LmArgs)>();
   extern __shared__ __align__(16) uint16_t xs[];  // [M][K + 8]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
@@ -142,6 +143,7 @@ __global__ void __launch_bounds__(ADV_T) decode_advance_kernel(
     int64_t* tokens, int32_t* pos, int32_t* count, const int32_t* limit, uint8_t* active,
     const int64_t* eos, int64_t* generated, int64_t gen_ld, int32_t* append_pos,
     int32_t* attn_len) {
+  touch_kernargs<14 * 8>();
   __shared__ float sv[ADV_T / 64];
   __shared__ int si[ADV_T / 64];
   const int m = blockIdx.x, tid = threadIdx.x;

@@ -296,6 +296,7 @@ __device__ __forceinline__ uint4 attn_chunk(const PartArgs& p, int m, int k) {
 
 template <int MT, int KPW, int XSRC>
 __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(PartArgs p) {
+  touch_kernargs<sizeof(PartArgs)>();
   constexpr int WPG = waves_per_group(XSRC), NT = 64 * WPG;
   extern __shared__ __align__(16) uint16_t xs[];  // [M][xstride], decode8 order
   // Padding workgroups of the XCD-aligned grid have no tile at all.

@@ -124,6 +124,7 @@ constexpr int QKV_SLICES_SMALL = 8;
 
 template <int GQ, bool FUSED, int MS = QKV_SLICES_SMALL>
 __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
+  touch_kernargs<sizeof(AttnArgs)>();
   const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -163,17 +164,20 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
   // load makes the waits of the loads issued BEFORE it conservative, never of
   // those after it.  Hence: first the loads only some threads need, each
   // predicated (LoRA t: 12 threads; the q|k|v partial sums of the GQ + 2 rows,
-  // or q; the block-table slice), none depending on a loaded value; meanwhile
-  // one batch of scalar loads brings the context length, the append position
-  // and this wave's first block id; then the loads every thread needs,
+  // or q; the block-table slice), none depending on a loaded value; then one
+  // batch of scalar loads brings the context length, the append position and
+  // this wave's first block id; then the loads every thread needs,
   // unconditional: the RoPE tables and the first block's K/V (HBM).  Each
   // phase then waits only for its own loads.  The wave whose first block
   // receives the new token loads it before the append and patches the
   // token's row from LDS afterwards.
   const int first = blk0 + wave;
-  const int ctx_raw = p.cl[b];
-  const int pos = FUSED ? p.append_pos[b] : -1;
-  const int phys0 = p.bt[(int64_t)b * p.bts + min(first, p.max_blocks - 1)];
+  // Vector loads (VGPR results): kept in VGPRs until the barrier below, so the
+  // wait for them and their move to scalar registers come after every load of
+  // the prologue has been issued.
+  int ctx_v = p.cl[b];
+  int pos_v = FUSED ? p.append_pos[b] : -1;
+  int phys_v = p.bt[(int64_t)b * p.bts + min(first, p.max_blocks - 1)];
   constexpr int NROW = GQ + 2;  // fused rows: GQ q heads, then k, then v
   static_assert(NROW * (FD / 4) <= AT - 64, "the last wave fetches no q|k|v row");
   const int row = tid / (FD / 4), d4 = 4 * (tid % (FD / 4));
@@ -200,10 +204,14 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
   }
   int bt_v = 0;
   if (tid < p.bps) bt_v = p.bt[(int64_t)b * p.bts + min(blk0 + tid, p.max_blocks - 1)];
-  // Consumed together here, the three scalar loads (issued above, ahead of
-  // the predicated vector loads) are waited for once (otherwise the compiler
-  // sinks the last two below the early exit and waits for each in turn).
-  asm volatile("" ::"s"(ctx_raw), "s"(pos), "s"(phys0));
+  // The context length, append position and first block id are consumed
+  // here, after every prologue load has been issued (without the barrier the
+  // compiler moves them to scalar registers right after their loads, which
+  // stalls the wave for a round trip before it issues anything else).
+  asm volatile("" : "+v"(ctx_v), "+v"(pos_v), "+v"(phys_v));
+  const int ctx_raw = __builtin_amdgcn_readfirstlane(ctx_v);
+  const int pos = __builtin_amdgcn_readfirstlane(pos_v);
+  const int phys0 = __builtin_amdgcn_readfirstlane(phys_v);
   const int ctx = max(0, min(ctx_raw, p.max_blocks * FBS));
   const int nblk = (ctx + FBS - 1) / FBS;
   const int nsplit = nblk > 0 ? (nblk + p.bps - 1) / p.bps : 1;
@@ -573,10 +581,13 @@ int launch_split(const AttnArgs& a, hipStream_t st) {
   const size_t lds = (size_t)AW * GQ * FD * sizeof(float) + (size_t)a.bps * sizeof(int);
   if (lds > 65536) return einval("context too long for the split attention kernel");
   const dim3 grid(a.S, a.Hkv, a.B);
-  if (FUSED && a.qkv.S > QKV_SLICES_SMALL)
-    paged_attn_split<GQ, FUSED, MAX_SLICES><<<grid, AT, lds, st>>>(a);
-  else
-    paged_attn_split<GQ, FUSED><<<grid, AT, lds, st>>>(a);
+  if constexpr (FUSED) {
+    if (a.qkv.S > QKV_SLICES_SMALL) {
+      paged_attn_split<GQ, FUSED, MAX_SLICES><<<grid, AT, lds, st>>>(a);
+      return launch_check("paged_attn_split");
+    }
+  }
+  paged_attn_split<GQ, FUSED><<<grid, AT, lds, st>>>(a);
   return launch_check("paged_attn_split");
 }
 
