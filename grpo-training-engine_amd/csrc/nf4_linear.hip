@@ -834,6 +834,131 @@ __global__ void __launch_bounds__(128 * S) nf4_gate_up_silu(GuArgs p) {
   }
 }
 
+// gate|up + SiLU in units of 8 output columns over a grid of at most one
+// workgroup per CU.  Unit u covers act columns 8u .. 8u+7: the MFMA tile's 16
+// B-columns are gate rows 8u .. 8u+7 (lanes n < 8) and up rows I+8u .. I+8u+7
+// (lanes n >= 8), so the SiLU pairs a tile's columns n and n + 8.  Workgroup
+// g takes units g, g + G, g + 2G, ...; its W waves take the (unit, k-step)
+// items of those units round-robin, each item one k-step of 256 on one wave.
+// Against one workgroup per 16 columns (nf4_gate_up_silu) this stages x into
+// LDS once per CU instead of once per workgroup -- x was half the bytes each
+// CU moved -- and balances the decode at the grain of one k-step (a CU's share
+// of 8-column units differs by at most one unit, not by one 16-column pair).
+// Item partial tiles meet in LDS and are summed in k-step order.
+constexpr int GUU_XU = 6;  // x chunks per thread loaded before the weights
+#ifndef GRPO_GUU_LA
+#define GRPO_GUU_LA 1
+#endif
+constexpr int GUU_LA = GRPO_GUU_LA;  // items whose weights are in flight ahead of the one decoded
+
+template <int W, int IPW>
+__global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
+  constexpr int NTH = 64 * W;
+  extern __shared__ __align__(16) uint16_t xs[];  // [M][K + 8] (decode8 order), then tiles
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 15, lg = lane >> 4;
+  const int G = gridDim.x, g0 = blockIdx.x;
+  const int KS = p.K / KSTEP;
+  const int U = p.I / 8;
+  const int nu = (U - g0 + G - 1) / G;  // >= 1: the grid has at most U workgroups
+  const int nitems = nu * KS;
+  const int xstride = p.K + 8;
+  float* red = reinterpret_cast<float*>(xs + p.M * xstride);  // [nitems][M][16]
+  const int rsel = ln < 8 ? ln : p.I + ln - 8;  // row of unit u: 8u + rsel
+
+  // x first (exactly GUU_XU chunks per thread, clamped), then the weights of
+  // this wave's first GUU_LA items; every item then issues the loads of the
+  // item GUU_LA ahead before it waits for its own.  All loads are
+  // unconditional (an item past the wave's last re-reads the last one), so
+  // each wait is exact: staging waits only for x, an item only for its own
+  // weights, and the decode of one item overlaps the loads of the next ones.
+  float code[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
+  const int chunks = p.K / 8, total = p.M * chunks;
+  uint4 xv[GUU_XU];
+#pragma unroll
+  for (int u = 0; u < GUU_XU; ++u) {
+    const int i = min(u * NTH + tid, total - 1);
+    const int m = i / chunks, c = i - m * chunks;
+    xv[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + 8 * c);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  uint4 wv[2 * IPW];
+  float av[IPW];
+  auto load_item = [&](int t) __attribute__((always_inline)) {
+    const int q = min(wave + W * t, nitems - 1);
+    const int i = q / KS, k = q - i * KS;
+    const int64_t row = (int64_t)8 * (g0 + i * G) + rsel;
+    const int kc = k * KSTEP + 64 * lg;
+    const uint4* wp = reinterpret_cast<const uint4*>(p.w + row * (p.K / 2) + kc / 2);
+    wv[2 * t] = wp[0];
+    wv[2 * t + 1] = wp[1];
+    av[t] = p.absmax[(row * p.K + kc) >> p.bs_shift];
+  };
+#pragma unroll
+  for (int t = 0; t < GUU_LA && t < IPW; ++t) load_item(t);
+  for (int base = 0; base < total; base += GUU_XU * NTH) {
+#pragma unroll
+    for (int u = 0; u < GUU_XU; ++u) {
+      if (base + u * NTH >= total) break;
+      const int i = min(base + u * NTH + tid, total - 1);
+      const int m = i / chunks, c = i - m * chunks;
+      const uint4 v = base == 0 ? xv[u]
+                                : *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + 8 * c);
+      *reinterpret_cast<uint4*>(xs + m * xstride + 8 * c) = deinterleave8(v);
+    }
+  }
+  __syncthreads();
+
+  const uint16_t* xrow = xs + min(ln, p.M - 1) * xstride + 64 * lg;
+  const int my_items = (nitems - wave + W - 1) / W;  // items of this wave (may be 0)
+#pragma unroll
+  for (int t = 0; t < IPW; ++t) {
+    if (t >= my_items) break;
+    if (t + GUU_LA < IPW) load_item(t + GUU_LA);
+    const int k = (wave + W * t) % KS;
+    const Lut lt = make_lut(code, av[t]);
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      acc = mfma16x16x32(*reinterpret_cast<const uint4*>(xrow + k * KSTEP + 8 * j),
+                         decode8(word(wv[2 * t + (j >> 2)], j & 3), lt), acc);
+    // lane (n = ln, group lg) holds D[m = 4*lg + r][n]
+    const int q = wave + W * t;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * lg + r;
+      if (m < p.M) red[(q * p.M + m) * 16 + ln] = acc[r];
+    }
+  }
+  __syncthreads();
+  for (int i = tid; i < nu * p.M * 8; i += NTH) {
+    const int un = i / (p.M * 8), rem = i - un * p.M * 8;
+    const int m = rem >> 3, n = rem & 7;
+    float g = 0.f, u = 0.f;
+    for (int k = 0; k < KS; ++k) {
+      const float* tile = red + ((un * KS + k) * p.M + m) * 16;
+      g += tile[n];
+      u += tile[n + 8];
+    }
+    const float gv = round_bf(g);
+    const float o = round_bf(gv * (1.f / (1.f + expf(-gv)))) * round_bf(u);
+    p.act[(int64_t)m * p.lda + 8 * (g0 + un * G) + n] = f2bf(o);
+  }
+}
+
+#ifndef GRPO_GU_UNITS_GRID
+#define GRPO_GU_UNITS_GRID 256
+#endif
+#ifndef GRPO_GU_UNITS_W
+#define GRPO_GU_UNITS_W 8
+#endif
+int g_gu_units_grid = GRPO_GU_UNITS_GRID;  // workgroups of nf4_gate_up_units (the CU count)
+constexpr int GU_UNITS_W = GRPO_GU_UNITS_W;  // waves per workgroup
+constexpr int GU_UNITS_IPW = 8;              // most (unit, k-step) items per wave
+
 #ifndef GRPO_GU_KPW
 #define GRPO_GU_KPW 3
 #endif
@@ -1255,8 +1380,19 @@ extern "C" int grpo_nf4_gate_up_silu(const void* x, int64_t ldx, const uint8_t* 
   a.M = M;
   a.I = I;
   a.K = K;
-  const dim3 grid((unsigned)(I / 16)), block(128 * pl.S);
   hipStream_t st = as_stream(stream);
+  {
+    // units kernel: at most one workgroup per CU, every item of a wave in registers
+    const int U = I / 8, KS = K / KSTEP;
+    const int G = std::min(U, g_gu_units_grid);
+    const int nu = (U + G - 1) / G;
+    const size_t lds = (size_t)M * (K + 8) * 2 + (size_t)nu * KS * M * 16 * 4;
+    if (I % 8 == 0 && (nu * KS + GU_UNITS_W - 1) / GU_UNITS_W <= GU_UNITS_IPW && lds <= 65536) {
+      nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW><<<dim3((unsigned)G), 64 * GU_UNITS_W, lds, st>>>(a);
+      return launch_check("nf4_gate_up_units");
+    }
+  }
+  const dim3 grid((unsigned)(I / 16)), block(128 * pl.S);
   switch (pl.kpw * 16 + pl.S) {
 #define GU_CASE(KPW, S) \
   case KPW * 16 + S: nf4_gate_up_silu<KPW, S><<<grid, block, pl.lds, st>>>(a); break;
