@@ -10,9 +10,11 @@
 // block the 4 KB K tile is read with 16-byte loads straight into the A operand
 // of v_mfma_f32_16x16x32_bf16 (rows = tokens) against the B operand Q^T of all
 // query heads of the GQA group (columns = heads), giving S^T[token][head] in 4
-// MFMAs.  The online softmax runs in the exp2 domain; P and the per-head
-// rescale go through a per-wave LDS slot; P.V runs on VALU with every V
-// element loaded once and applied to all heads of the group.  The 8 waves
+// MFMAs.  The online softmax runs in the exp2 domain; P goes through a
+// per-wave LDS slot; P.V runs on float32 MFMA (v_mfma_f32_16x16x4_f32: O^T
+// tiles of 16 head-dimension rows x 16 heads), every V element loaded once and
+// applied to all heads of the group, each lane ending with distinct outputs
+// (no cross-lane sums).  The 8 waves
 // merge through LDS and every split writes (max, sum, unnormalised O): the
 // standalone entry point merges them in a second kernel, the decode step merges
 // them while the o_proj kernel stages its input (linear_parts.hpp, nf4_linear.hip).
@@ -135,8 +137,9 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
   __shared__ __align__(16) uint16_t sQ[GQ][FD];
   __shared__ __align__(16) uint16_t sNew[2][FD];  // appended token: rotated K, V
   __shared__ float sTs[MAXSEG * 16];
-  __shared__ __align__(16) float sP[AW][16][16];
-  __shared__ float sC[AW][16];
+  // P of the wave's block, [head][token]; rows padded to 20 floats so the
+  // P.V operand reads (token 4s + lane group) spread over the banks
+  __shared__ __align__(16) float sP[AW][16][20];
   __shared__ float sM[AW][16];
   __shared__ float sL[AW][16];
   int* sBT = reinterpret_cast<int*>(sO + (size_t)AW * GQ * FD);  // the split's table slice
@@ -153,7 +156,7 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       kf[i] = *reinterpret_cast<const uint4*>(kb + ln * FD + 8 * lg + 32 * i);
-      vf[i] = *reinterpret_cast<const uint4*>(vb + (4 * lg + i) * FD + 8 * ln);
+      vf[i] = *reinterpret_cast<const uint4*>(vb + (4 * i + lg) * FD + 8 * ln);
     }
     return ok;
   };
@@ -296,7 +299,7 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       if (ln == t) kn[i] = *reinterpret_cast<const uint4*>(&sNew[0][8 * lg + 32 * i]);
-      if (4 * lg + i == t) vn[i] = *reinterpret_cast<const uint4*>(&sNew[1][8 * ln]);
+      if (4 * i + lg == t) vn[i] = *reinterpret_cast<const uint4*>(&sNew[1][8 * ln]);
     }
   }
 
@@ -309,13 +312,14 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
                     : make_uint4(0, 0, 0, 0);
   const float sl2 = p.scale * LOG2E;
   float m_run = -INFINITY, l_run = 0.f;  // softmax state of head ln
-  float o[GQ][8];
+  // O^T in eight 16x16 tiles: tile i holds rows d = 8*r + i (r = 0..15) and
+  // columns = heads; lane (head ln, group lg) holds O[ln][8*(4*lg + q) + i]
+  // in oacc[i][q].
+  f32x4_t oacc[8];
 #pragma unroll
-  for (int h = 0; h < GQ; ++h)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) o[h][j] = 0.f;
+  for (int i = 0; i < 8; ++i) oacc[i] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // One 16-token block: S^T on MFMA, online softmax, P.V on VALU.  (Inlined
+  // One 16-token block: S^T on MFMA, online softmax, P.V on float32 MFMA.  (Inlined
   // at both call sites: a call would pass every captured variable, the kernel
   // arguments included, through scratch memory.)
   auto block = [&](int blk, const uint4 (&kf)[4], const uint4 (&vf)[4])
@@ -346,25 +350,24 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
     l_run = l_run * corr + ps;
     m_run = m_new;
     *reinterpret_cast<float4*>(&sP[wave][ln][4 * lg]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
-    if (lg == 0) sC[wave][ln] = corr;
     wave_sync();
-    // P.V: lane (token group lg, d chunk ln) owns O[h][8*ln + j] over tokens 4*lg..4*lg+3.
+    // P.V on v_mfma_f32_16x16x4_f32 (float32 products and sums, as the
+    // reference's float32 p * v): O^T tile i += V^T (16 d x 4 tokens) . P
+    // (4 tokens x 16 heads) over tokens 4s + lg, s = 0..3.  Lane (ln, lg)
+    // gives A = V[4s + lg][8*ln + i] (element i of vf[s]) and B = P[4s + lg][ln];
+    // the rescale by this lane's head's corr comes first.
+    float pb[4];
 #pragma unroll
-    for (int h = 0; h < GQ; ++h) {
-      const float c = sC[wave][h];
-      const float4 ph = *reinterpret_cast<const float4*>(&sP[wave][h][4 * lg]);
-      const float pr[4] = {ph.x, ph.y, ph.z, ph.w};
+    for (int q = 0; q < 4; ++q) pb[q] = sP[wave][ln][4 * q + lg];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) o[h][j] *= c;
+    for (int i = 0; i < 8; ++i) oacc[i] *= corr;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t vw[4] = {vf[r].x, vf[r].y, vf[r].z, vf[r].w};
+    for (int q = 0; q < 4; ++q) {
+      const uint32_t vw[4] = {vf[q].x, vf[q].y, vf[q].z, vf[q].w};
 #pragma unroll
-        for (int c2 = 0; c2 < 4; ++c2) {
-          o[h][2 * c2] += pr[r] * bf_lo(vw[c2]);
-          o[h][2 * c2 + 1] += pr[r] * bf_hi(vw[c2]);
-        }
-      }
+      for (int i = 0; i < 8; ++i)
+        oacc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+            (i & 1) ? bf_hi(vw[i >> 1]) : bf_lo(vw[i >> 1]), pb[q], oacc[i], 0, 0, 0);
     }
     wave_sync();
   };
@@ -390,21 +393,21 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
     }
   }
 
-  // Sum the four token groups of the wave, then merge the AW waves.
-#pragma unroll
-  for (int h = 0; h < GQ; ++h)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      o[h][j] = pair32_sum(pair16_sum(o[h][j]));
-    }
+  // Merge the AW waves: each lane of a head column writes its 32 elements of
+  // O[head][:] (rows 8*(4*lg + q) + i of the tiles) to the wave's slot.
   if (lg == 0) {
     sM[wave][ln] = m_run;
     sL[wave][ln] = l_run;
+  }
+  if (ln < GQ) {
+    float* dst = sO + ((size_t)wave * GQ + ln) * FD;
 #pragma unroll
-    for (int h = 0; h < GQ; ++h) {
-      float* dst = sO + ((size_t)wave * GQ + h) * FD + 8 * ln;
-      *reinterpret_cast<float4*>(dst) = make_float4(o[h][0], o[h][1], o[h][2], o[h][3]);
-      *reinterpret_cast<float4*>(dst + 4) = make_float4(o[h][4], o[h][5], o[h][6], o[h][7]);
+    for (int q = 0; q < 4; ++q) {
+      const int d0 = 8 * (4 * lg + q);
+      *reinterpret_cast<float4*>(dst + d0) =
+          make_float4(oacc[0][q], oacc[1][q], oacc[2][q], oacc[3][q]);
+      *reinterpret_cast<float4*>(dst + d0 + 4) =
+          make_float4(oacc[4][q], oacc[5][q], oacc[6][q], oacc[7][q]);
     }
   }
   __syncthreads();
