@@ -476,7 +476,7 @@ def main():
         achieved = tot_b / (tot_us * 1e-6) / 1e9
         roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
                         frac=round(achieved / PEAK_HBM_GBS, 4), traffic=measured_traffic(),
-                        kernel="NF4 linears: nf4_part_mfma (q|k|v, o, down) + nf4_gate_up_silu (gate|up)",
+                        kernel="NF4 linears: nf4_part_mfma (q|k|v, o, down) + nf4_gate_up_units (gate|up)",
                         avg_launch_us=round(tot_us / n, 3), bytes_per_launch=tot_b // n)
         log(f"kernel timing: {kernels}")
 
