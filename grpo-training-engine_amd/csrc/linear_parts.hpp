@@ -35,10 +35,13 @@ struct LinParts {
 // Host: validates a descriptor and converts it.  Returns GRPO_OK or einval.
 int make_parts(const grpo_linear_parts_t* h, LinParts* d);
 
+// Segment of column n, branch-free: the segment ends are increasing (checked by
+// make_parts) and n < N = the last end.  (A loop over seg_end made the compiler
+// load one argument per iteration and wait for each in turn.)
 __device__ __forceinline__ int lin_seg(const LinParts& o, int n) {
-  int s = 0;
-  while (s + 1 < o.nseg && n >= o.seg_end[s]) ++s;
-  return s;
+  const int e0 = o.seg_end[0], e1 = o.seg_end[1], e2 = o.seg_end[2];
+  return (o.nseg > 1 && n >= e0 ? 1 : 0) + (o.nseg > 2 && n >= e1 ? 1 : 0) +
+         (o.nseg > 3 && n >= e2 ? 1 : 0);
 }
 
 // a[i] of a kernel-argument array for a per-lane i < MAXSEG, by selects over
