@@ -19,7 +19,10 @@ using namespace grpo;
 namespace {
 
 constexpr int LM_KSTEP = 256;
-constexpr int LM_WAVES = 4;  // vocabulary tiles per workgroup (x staged once per workgroup)
+#ifndef GRPO_LM_WAVES
+#define GRPO_LM_WAVES 8
+#endif
+constexpr int LM_WAVES = GRPO_LM_WAVES;  // vocabulary tiles per workgroup (x staged once per workgroup)
 constexpr int ADV_T = 1024;
 constexpr size_t LM_LDS_MAX = 163840;  // gfx950: 160 KiB of LDS per workgroup
 

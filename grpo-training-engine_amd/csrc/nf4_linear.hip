@@ -167,8 +167,11 @@ enum XSource { X_BF16 = 0, X_ATTN = 1, X_SILU = 2 };
 // slice it stages; the SiLU source reads 16 bytes of partial sums per element,
 // so its workgroups are larger (fewer rebuilds).  Measured at decode shapes:
 // the attention-merge source is fastest with the default 4.
+#ifndef GRPO_ATTN_WAVES
+#define GRPO_ATTN_WAVES PART_WAVES
+#endif
 __host__ __device__ constexpr int waves_per_group(int xsrc) {
-  return xsrc == X_SILU ? 8 : PART_WAVES;
+  return xsrc == X_SILU ? 8 : (xsrc == X_ATTN ? GRPO_ATTN_WAVES : PART_WAVES);
 }
 constexpr int GU_MAX_SLICES = 2;  // K slices of the gate|up partial sums read while staging
 

@@ -102,10 +102,14 @@ def test_add_rmsnorm_parts_matches_oracle(dev, n, lora, offset):
 
 
 @pytest.mark.parametrize("m,i,k", [(8, 8960, 1536), (3, 256, 512), (16, 512, 1536),
-                                   (8, 512, 3584)])
+                                   (8, 512, 3584), (8, 17920, 3584), (5, 4112, 512)])
 def test_gate_up_silu_matches_oracle(dev, m, i, k):
     """grpo_nf4_gate_up_silu = oracle NF4 linear of the gate and up halves of a
-    stacked weight, then oracle SiLU*mul (fused_ops.py:79-112)."""
+    stacked weight, then oracle SiLU*mul (fused_ops.py:79-112).  The first four
+    and the last shape run the 8-column-unit kernel (the last has 514 units over
+    256 workgroups: two workgroups take a third unit); [8, 17920, 3584] has more
+    items per wave than the unit kernel keeps in registers and runs one
+    workgroup per 16 columns."""
     from grpo_mi355x import _lib
 
     from oracle.decode import silu_mul
