@@ -61,6 +61,9 @@ def parse():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="first stream a 256 MiB buffer through a copy-like kernel 3 times "
                          "(scale reference for the HBM FETCH_SIZE/WRITE_SIZE counters)")
+    ap.add_argument("--sample", action="store_true",
+                    help="config 3 with the reference trainer's default sampling (temperature "
+                         "0.7, top-p 0.9) instead of greedy decoding (an extra measurement)")
     ap.add_argument("--config", type=int, default=3, choices=(3, 4, 5),
                     help="BASELINE config: 3 (default, the headline metric), 4 (G=32 ragged "
                          "group, blocks freed as rows stop) or 5 (Qwen2-7B shape, G=64, "
@@ -131,6 +134,8 @@ def kernel_timing(eng, dev, reps: int = 20) -> dict:
             kinds.append(k)
     for kind in kinds:
         g = torch.cuda.CUDAGraph()
+        if kind == "sample" and eng.generator is not None:
+            g.register_generator_state(eng.generator)
         with torch.cuda.graph(g, stream=side):
             fns = [fn for k, fn in eng.launches() if k == kind]
             fns = fns * -(-28 // len(fns))
@@ -375,6 +380,11 @@ def main():
               "multi-GPU path (rollout groups would shard data-parallel, one group per GPU).",
               file=sys.stderr)
         sys.exit(2)
+    if args.sample:
+        print("bench.py --sample is disabled: the sampled rollout at the full vocabulary has "
+              "not passed on the GPU yet (an earlier version faulted inside torch's radix sort "
+              "in the captured step graph)", file=sys.stderr)
+        sys.exit(2)
     if args.config != 3:
         from grpo_mi355x import _lib
 
@@ -423,7 +433,13 @@ def main():
     pool.free(parent)
     pool.check_invariants()
     del eng1
-    eng = DecodeEngine(model, pool, G, width)
+    if args.sample:
+        sgen = torch.Generator(device=dev)
+        sgen.manual_seed(args.seed)
+        eng = DecodeEngine(model, pool, G, width, do_sample=True, temperature=0.7, top_p=0.9,
+                           generator=sgen)
+    else:
+        eng = DecodeEngine(model, pool, G, width)
     tables = pool.block_table(kids, width, device=dev)
     start = dict(tokens=torch.full((G,), prompt[-1], dtype=torch.int64, device=dev),
                  positions=torch.full((G,), P - 1, device=dev), block_tables=tables,
@@ -450,7 +466,7 @@ def main():
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     elapsed = t1 - t0
-    if args.warmup > 0:
+    if args.warmup > 0 and not args.sample:
         assert torch.equal(eng.generated, gen), "rollouts are not deterministic"
     tokens = sum(stops) * args.steps
     value = tokens / elapsed
@@ -503,7 +519,8 @@ def main():
         "data": "synthetic (random-init weights N(0,0.02) -> NF4, LoRA N(0,0.01); random prompt)",
         "config": {
             "workload": "BASELINE config 3: Qwen2-1.5B-shaped NF4+LoRA decode, G=8, 512-token "
-                        "prompt, greedy, per-sequence stops U[64,512]; step = one ragged rollout",
+                        "prompt, " + ("sampled (T 0.7, top-p 0.9)" if args.sample else "greedy")
+                        + ", per-sequence stops U[64,512]; step = one ragged rollout",
             "group": G, "prompt_len": P, "max_new_tokens": NEW, "stops": stops,
             "layers": cfg.num_hidden_layers, "block_size": BS, "parallelism": "single GPU",
         },

@@ -90,8 +90,16 @@ def paged_kv_decode(model: object, input_ids: object, attention_mask: object | N
     model_kernel = _get_hip_kernel("paged_kv_decode_model")
     if model_kernel is None:
         raise _unavailable("paged_kv_decode_model")
+    # the reference's model-path defaults (src/triton_kernels/__init__.py:283-296)
     return model_kernel(model, input_ids_t, attention_mask=attention_mask,
-                        max_new_tokens=max_new_tokens, **kwargs)
+                        max_new_tokens=max_new_tokens,
+                        do_sample=kwargs.pop("do_sample", True),
+                        temperature=kwargs.pop("temperature", 1.0),
+                        top_p=kwargs.pop("top_p", 1.0),
+                        pad_token_id=kwargs.pop("pad_token_id", 0),
+                        eos_token_id=kwargs.pop("eos_token_id", None),
+                        seed=kwargs.pop("seed", None),
+                        block_size=kwargs.pop("block_size", 16), **kwargs)
 
 
 def lora_fused_forward(x: object, base_layer: object | None = None, lora_A: object | None = None,

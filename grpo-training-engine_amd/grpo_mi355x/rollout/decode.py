@@ -50,11 +50,17 @@ class DecodeEngine:
     """Static-shape decode step for ``batch`` rows over a KV pool."""
 
     def __init__(self, model: Qwen2ForCausalLM, pool: PagedKVPool, batch: int, max_blocks: int,
-                 max_pos: Optional[int] = None, keep_logits: bool = False):
+                 max_pos: Optional[int] = None, keep_logits: bool = False,
+                 do_sample: bool = False, temperature: float = 1.0, top_p: float = 1.0,
+                 generator: Optional[torch.Generator] = None):
         self.lib = _lib.device_library()
         # Greedy decoding needs only each step's argmax; keep_logits also fills
         # self.logits [B, V] (bf16) every step, for callers that inspect them.
-        self.keep_logits = keep_logits
+        # Sampling (do_sample with temperature > 0) needs the logits too.
+        self.sampling = bool(do_sample) and temperature > 0.0
+        self.temperature, self.top_p = float(temperature), float(top_p)
+        self.generator = generator
+        self.keep_logits = keep_logits or self.sampling
         cfg = model.config
         self.model, self.pool, self.cfg = model, pool, cfg
         self.B, self.max_blocks = batch, max_blocks
@@ -78,7 +84,6 @@ class DecodeEngine:
         self.active = torch.zeros(B, dtype=torch.bool, device=dev)
         self.count = torch.zeros(B, **i32)
         self.limit = torch.zeros(B, **i32)
-        self.step_idx = torch.zeros(1, dtype=torch.int64, device=dev)
         self.eos = torch.full((1,), -1, dtype=torch.int64, device=dev)
         self.pad = torch.zeros(1, dtype=torch.int64, device=dev)
         self.block_tables = torch.full((B, max_blocks), -1, **i32)
@@ -268,7 +273,15 @@ class DecodeEngine:
         out.append(("rmsnorm", lambda P=prev: chk(lib.grpo_add_rmsnorm_parts(
             P["down_parts"], h, h, self.final_norm.data_ptr(), x, self.final_eps, st),
             "final_norm")))
-        if self.lm_fused:
+        if self.sampling:
+            if self.lm_fused:
+                out.append(("lm_head", lambda: chk(lib.grpo_lm_head_argmax(
+                    x, H, self.lm_head.data_ptr(), self.V, H, B, self.logits.data_ptr(), self.V,
+                    self.ws_lm.data_ptr(), self.ws_lm.numel(), st), "lm_head")))
+            else:
+                out.append(("lm_head",
+                            lambda: torch.matmul(self.x, self.lm_head.t(), out=self.logits)))
+        elif self.lm_fused:
             gen = self.generated
             logits = self.logits.data_ptr() if self.keep_logits else None
             out.append(("lm_head", lambda: chk(lib.grpo_lm_head_argmax(
@@ -299,10 +312,16 @@ class DecodeEngine:
 
     def _advance(self, greedy_tokens: torch.Tensor):
         """Record the step's tokens and move the per-row state (device only)."""
-        out = torch.where(self.active, greedy_tokens, self.pad)
         if self.generated is not None:
-            self.generated.scatter_(1, self.step_idx.view(1, 1).expand(self.B, 1), out.view(-1, 1))
-        self.step_idx.add_(1)
+            # an active row's token goes to column count[b]; rows that stopped,
+            # and columns past the buffer, keep what they hold (the gather and
+            # scatter then touch column 0 with its own value)
+            col = self.count.to(torch.int64)
+            ok = self.active & (col >= 0) & (col < self.generated.shape[1])
+            col = torch.where(ok, col, torch.zeros_like(col)).view(-1, 1)
+            keep = self.generated.gather(1, col)
+            self.generated.scatter_(1, col, torch.where(ok.view(-1, 1),
+                                                        greedy_tokens.view(-1, 1), keep))
         act = self.active.to(torch.int32)
         self.pos.add_(act)
         self.count.add_(act)
@@ -317,7 +336,7 @@ class DecodeEngine:
 
     def _step(self):
         self._forward()
-        if not self.lm_fused:  # the fused path advanced the rows on the device
+        if not self.lm_fused and not self.sampling:  # fused: advanced; sampling: in step()
             self._advance(self.next)
 
     # ------------------------------------------------------------ control --
@@ -331,7 +350,6 @@ class DecodeEngine:
         self.count.zero_()
         self.limit.copy_(limits.view(B).to(torch.int32))
         self.active.copy_(self.limit > 0)
-        self.step_idx.zero_()
         self.eos.fill_(-1 if eos_token_id is None else int(eos_token_id))
         self.pad.fill_(int(pad_token_id))
         w = block_tables.shape[1]
@@ -350,8 +368,7 @@ class DecodeEngine:
         # A warm-up step writes K/V only at each active row's slot pos[b], which
         # is not yet valid cache content: the first real step rewrites it before
         # attention reads it.  Row state is saved and restored around them.
-        saved = [t.clone() for t in (self.tokens, self.pos, self.count, self.active,
-                                     self.step_idx)]
+        saved = [t.clone() for t in (self.tokens, self.pos, self.count, self.active)]
         s = torch.cuda.Stream(device=self.device)
         s.wait_stream(torch.cuda.current_stream(self.device))
         with torch.cuda.stream(s):
@@ -366,7 +383,7 @@ class DecodeEngine:
         self.graph = g
 
     def _restore(self, saved):
-        for t, v in zip((self.tokens, self.pos, self.count, self.active, self.step_idx), saved):
+        for t, v in zip((self.tokens, self.pos, self.count, self.active), saved):
             t.copy_(v)
         if self.generated is not None:
             self.generated.fill_(int(self.pad.item()))
@@ -377,6 +394,11 @@ class DecodeEngine:
             self.graph.replay()
         else:
             self._step()
+        if self.sampling:
+            # Eager, after the graph: torch's sort records memset nodes (radix
+            # sort state) when captured, and those are not reliable on replays.
+            self._advance(sample_rows(self.logits, self.temperature, self.top_p,
+                                      self.generator))
 
     def run(self, steps: int):
         for _ in range(steps):
@@ -438,6 +460,29 @@ class DecodeEngine:
         return dict(steps=steps, peak_blocks=peak)
 
 
+def sample_rows(logits: torch.Tensor, temperature: float, top_p: float,
+                generator: Optional[torch.Generator]) -> torch.Tensor:
+    """Sampled next token per row: the reference's ``fused_logits_sampling``
+    (``src/triton_kernels/fused_ops.py:236-248``) on the bf16 logits, op for op
+    (bf16 division by the temperature, descending sort, softmax, running sum,
+    cut after the running sum passes ``top_p`` but always keep the first,
+    softmax, one multinomial draw), all on the device with no host
+    synchronisation.  It runs eagerly after the captured step: the sort is not
+    captured (its radix-sort state is cleared by memset nodes, which are not
+    reliable on graph replays)."""
+    scaled = logits / max(temperature, 1e-6)
+    if top_p < 1.0:
+        sorted_logits, sorted_indices = torch.sort(scaled, descending=True, dim=-1)
+        cumulative = torch.softmax(sorted_logits, dim=-1).cumsum(dim=-1)
+        cutoff = cumulative > top_p
+        cutoff[..., 0] = False
+        sorted_logits = sorted_logits.masked_fill(cutoff, -float("inf"))
+        scaled = torch.full_like(scaled, -float("inf")).scatter(dim=-1, index=sorted_indices,
+                                                                src=sorted_logits)
+    probs = torch.softmax(scaled, dim=-1)
+    return torch.multinomial(probs, num_samples=1, generator=generator).squeeze(-1)
+
+
 # ------------------------------------------------------------- drop-in ---
 
 def _prompt_rows(input_ids: torch.Tensor, attention_mask: Optional[torch.Tensor]):
@@ -486,7 +531,9 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
     Rows with identical (unpadded) prompts share one prefill; their full prompt
     blocks are shared through the pool and the partial last block is copied
     per row.  ``stop_lengths`` (an extension) caps each row's generated length.
-    Greedy decoding runs in the captured graph; every block-size steps the host
+    Decoding (greedy, or sampled with the reference's temperature / top-p rule
+    and a generator seeded from ``seed``) runs in the captured graph; every
+    block-size steps the host
     gives growing rows their next block and frees the blocks of rows that
     stopped (``DecodeEngine.run_paged``), and decoding ends once every row has
     stopped (the reference's ``finished.all()`` exit, ``paged_kv.py:903``).
@@ -495,9 +542,6 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
         raise ValueError(f"max_new_tokens must be > 0, got {max_new_tokens}.")
     if input_ids.ndim != 2 or input_ids.shape[1] == 0:
         raise ValueError("input_ids must be [batch, seq_len] with at least 1 token.")
-    if do_sample and temperature > 0.0:
-        raise ValueError("sampling (do_sample=True) is not implemented on the HIP decode "
-                         "graph yet; use greedy decoding")
     model = decode_model_from(model)
     cfg = model.config
     dev = input_ids.device
@@ -520,7 +564,12 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
     for p in parents.values():
         pool.free(p)
     pool.check_invariants()
-    eng = DecodeEngine(model, pool, B, width)
+    generator = None
+    if do_sample and temperature > 0.0 and seed is not None:  # paged_kv.py:668-671
+        generator = torch.Generator(device=dev)
+        generator.manual_seed(int(seed))
+    eng = DecodeEngine(model, pool, B, width, do_sample=do_sample, temperature=temperature,
+                       top_p=top_p, generator=generator)
     limits = torch.tensor(stop_lengths if stop_lengths is not None else [max_new_tokens] * B,
                           dtype=torch.int32, device=dev).clamp(max=max_new_tokens)
     eng.start(torch.tensor([r[-1] for r in rows], device=dev),

@@ -185,3 +185,78 @@ def test_run_paged_reserves_ahead_and_frees_stopped_rows():
     assert stats["peak_blocks"] <= 1 + 3 + 2 + 2 + 5
     assert pool.num_free == pool.num_blocks and not pool.blocks
     assert torch.all(s.block_tables == -1)
+
+
+def _bf16_logits_for(probs):
+    """bf16 logits whose softmax is ``probs`` up to bf16 rounding of the logits."""
+    import numpy as np
+
+    return torch.tensor(np.log(np.asarray(probs, dtype=np.float64)), dtype=torch.float32).to(
+        torch.bfloat16)
+
+
+def test_sample_rows_top_p_cuts_the_token_that_crosses():
+    """The reference's rule (fused_ops.py:236-245): sorted descending, a token is
+    cut when the running sum up to and including it exceeds top_p; the first is
+    always kept.  probs 0.5, 0.3, 0.15, 0.05 with top_p = 0.9: running sums 0.5,
+    0.8, 0.95, 1.0, so only the first two remain, drawn 0.625 / 0.375 (a
+    'keep the crossing token' rule would keep three)."""
+    from grpo_mi355x.rollout.decode import sample_rows
+
+    logits = _bf16_logits_for([0.15, 0.5, 0.05, 0.3]).repeat(4000, 1)
+    g = torch.Generator().manual_seed(0)
+    tok = sample_rows(logits, 1.0, 0.9, g)
+    counts = torch.bincount(tok, minlength=4).double() / tok.numel()
+    assert counts[0] == 0 and counts[2] == 0
+    assert abs(counts[1] - 0.625) < 0.03 and abs(counts[3] - 0.375) < 0.03
+
+
+def test_sample_rows_full_distribution_and_tiny_top_p():
+    """top_p = 1: the draws follow softmax(bf16(logits / T)) (chi-square against
+    scipy's softmax of the same bf16 values); top_p -> 0 keeps only the argmax."""
+    import numpy as np
+    from scipy import stats
+    from scipy.special import softmax
+
+    from grpo_mi355x.rollout.decode import sample_rows
+
+    rng = np.random.default_rng(3)
+    base = torch.tensor(rng.normal(0, 1.5, 12), dtype=torch.float32).to(torch.bfloat16)
+    n = 20000
+    g = torch.Generator().manual_seed(1)
+    tok = sample_rows(base.repeat(n, 1), 0.7, 1.0, g)
+    scaled = (base / 0.7).float().numpy().astype(np.float64)
+    expect = softmax(scaled) * n
+    obs = np.bincount(tok.numpy(), minlength=12)
+    keep = expect > 5
+    chi2 = (((obs - expect) ** 2) / expect)[keep].sum()
+    assert chi2 < stats.chi2.ppf(0.999, keep.sum() - 1)
+    tok = sample_rows(base.repeat(64, 1), 0.7, 1e-6, g)
+    assert torch.all(tok == int(torch.argmax(base.float())))
+
+
+def test_torch_advance_stays_inside_the_generated_buffer():
+    """The torch-side step bookkeeping (used with sampling and the unfused
+    lm_head) records an active row's token at column count[b] and nothing once
+    count reaches the buffer width, as the HIP advance does: replaying the step
+    past the width (as a timing loop does) writes no column out of range."""
+    import types
+
+    from grpo_mi355x.rollout.decode import DecodeEngine
+
+    B, W = 3, 4
+    e = types.SimpleNamespace(
+        B=B, generated=torch.full((B, W), 7, dtype=torch.int64),
+        count=torch.tensor([0, 2, 0], dtype=torch.int32),
+        pos=torch.tensor([10, 20, 30], dtype=torch.int32),
+        limit=torch.tensor([100, 100, 1], dtype=torch.int32),
+        active=torch.tensor([True, True, False]), eos=torch.tensor([-1]),
+        tokens=torch.zeros(B, dtype=torch.int64), pad=torch.tensor([7]),
+        append_pos=torch.zeros(B, dtype=torch.int32), attn_len=torch.zeros(B, dtype=torch.int32))
+    e._masks = lambda: DecodeEngine._masks(e)
+    for step in range(10):
+        DecodeEngine._advance(e, torch.tensor([100 + step, 200 + step, 300 + step]))
+    assert e.generated.tolist() == [[100, 101, 102, 103], [7, 7, 200, 201], [7, 7, 7, 7]]
+    assert e.count.tolist() == [10, 12, 0] and e.pos.tolist() == [20, 30, 30]
+    assert e.active.tolist() == [True, True, False]
+    assert e.append_pos.tolist() == [20, 30, -1] and e.attn_len.tolist() == [21, 31, 0]
