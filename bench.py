@@ -134,8 +134,6 @@ def kernel_timing(eng, dev, reps: int = 20) -> dict:
             kinds.append(k)
     for kind in kinds:
         g = torch.cuda.CUDAGraph()
-        if kind == "sample" and eng.generator is not None:
-            g.register_generator_state(eng.generator)
         with torch.cuda.graph(g, stream=side):
             fns = [fn for k, fn in eng.launches() if k == kind]
             fns = fns * -(-28 // len(fns))
@@ -434,10 +432,8 @@ def main():
     pool.check_invariants()
     del eng1
     if args.sample:
-        sgen = torch.Generator(device=dev)
-        sgen.manual_seed(args.seed)
         eng = DecodeEngine(model, pool, G, width, do_sample=True, temperature=0.7, top_p=0.9,
-                           generator=sgen)
+                           seed=args.seed)
     else:
         eng = DecodeEngine(model, pool, G, width)
     tables = pool.block_table(kids, width, device=dev)

@@ -21,7 +21,8 @@ NATIVE_DIR = PKG_DIR / "_native"
 LIB_PATH = NATIVE_DIR / "libgrpo_hip.so"
 ARCH = "gfx950"
 
-SOURCES = ("capi.hip", "nf4_linear.hip", "paged_attention.hip", "decode_ops.hip", "lm_head.hip")
+SOURCES = ("capi.hip", "nf4_linear.hip", "paged_attention.hip", "decode_ops.hip", "lm_head.hip",
+           "sampling.hip")
 
 
 def hipcc() -> str:

@@ -52,14 +52,15 @@ class DecodeEngine:
     def __init__(self, model: Qwen2ForCausalLM, pool: PagedKVPool, batch: int, max_blocks: int,
                  max_pos: Optional[int] = None, keep_logits: bool = False,
                  do_sample: bool = False, temperature: float = 1.0, top_p: float = 1.0,
-                 generator: Optional[torch.Generator] = None):
+                 seed: int = 0):
         self.lib = _lib.device_library()
         # Greedy decoding needs only each step's argmax; keep_logits also fills
         # self.logits [B, V] (bf16) every step, for callers that inspect them.
         # Sampling (do_sample with temperature > 0) needs the logits too.
         self.sampling = bool(do_sample) and temperature > 0.0
         self.temperature, self.top_p = float(temperature), float(top_p)
-        self.generator = generator
+        # row b's draw at its n-th token is SplitMix64 of (seed, b, n): fixed by the seed
+        self.seed = int(seed) & 0xFFFFFFFFFFFFFFFF
         self.keep_logits = keep_logits or self.sampling
         cfg = model.config
         self.model, self.pool, self.cfg = model, pool, cfg
@@ -281,6 +282,14 @@ class DecodeEngine:
             else:
                 out.append(("lm_head",
                             lambda: torch.matmul(self.x, self.lm_head.t(), out=self.logits)))
+            gen = self.generated
+            out.append(("sample", lambda: chk(lib.grpo_sample_advance(
+                self.logits.data_ptr(), self.V, B, self.V, self.temperature, self.top_p,
+                self.seed, self.next.data_ptr(), self.tokens.data_ptr(), self.pos.data_ptr(),
+                self.count.data_ptr(), self.limit.data_ptr(), self.active.data_ptr(),
+                self.eos.data_ptr(), None if gen is None else gen.data_ptr(),
+                0 if gen is None else gen.shape[1], self.append_pos.data_ptr(),
+                self.attn_len.data_ptr(), st), "sample")))
         elif self.lm_fused:
             gen = self.generated
             logits = self.logits.data_ptr() if self.keep_logits else None
@@ -336,7 +345,7 @@ class DecodeEngine:
 
     def _step(self):
         self._forward()
-        if not self.lm_fused and not self.sampling:  # fused: advanced; sampling: in step()
+        if not self.lm_fused and not self.sampling:  # the fused and sampling paths advanced
             self._advance(self.next)
 
     # ------------------------------------------------------------ control --
@@ -394,11 +403,6 @@ class DecodeEngine:
             self.graph.replay()
         else:
             self._step()
-        if self.sampling:
-            # Eager, after the graph: torch's sort records memset nodes (radix
-            # sort state) when captured, and those are not reliable on replays.
-            self._advance(sample_rows(self.logits, self.temperature, self.top_p,
-                                      self.generator))
 
     def run(self, steps: int):
         for _ in range(steps):
@@ -460,29 +464,6 @@ class DecodeEngine:
         return dict(steps=steps, peak_blocks=peak)
 
 
-def sample_rows(logits: torch.Tensor, temperature: float, top_p: float,
-                generator: Optional[torch.Generator]) -> torch.Tensor:
-    """Sampled next token per row: the reference's ``fused_logits_sampling``
-    (``src/triton_kernels/fused_ops.py:236-248``) on the bf16 logits, op for op
-    (bf16 division by the temperature, descending sort, softmax, running sum,
-    cut after the running sum passes ``top_p`` but always keep the first,
-    softmax, one multinomial draw), all on the device with no host
-    synchronisation.  It runs eagerly after the captured step: the sort is not
-    captured (its radix-sort state is cleared by memset nodes, which are not
-    reliable on graph replays)."""
-    scaled = logits / max(temperature, 1e-6)
-    if top_p < 1.0:
-        sorted_logits, sorted_indices = torch.sort(scaled, descending=True, dim=-1)
-        cumulative = torch.softmax(sorted_logits, dim=-1).cumsum(dim=-1)
-        cutoff = cumulative > top_p
-        cutoff[..., 0] = False
-        sorted_logits = sorted_logits.masked_fill(cutoff, -float("inf"))
-        scaled = torch.full_like(scaled, -float("inf")).scatter(dim=-1, index=sorted_indices,
-                                                                src=sorted_logits)
-    probs = torch.softmax(scaled, dim=-1)
-    return torch.multinomial(probs, num_samples=1, generator=generator).squeeze(-1)
-
-
 # ------------------------------------------------------------- drop-in ---
 
 def _prompt_rows(input_ids: torch.Tensor, attention_mask: Optional[torch.Tensor]):
@@ -531,8 +512,8 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
     Rows with identical (unpadded) prompts share one prefill; their full prompt
     blocks are shared through the pool and the partial last block is copied
     per row.  ``stop_lengths`` (an extension) caps each row's generated length.
-    Decoding (greedy, or sampled with the reference's temperature / top-p rule
-    and a generator seeded from ``seed``) runs in the captured graph; every
+    Decoding (greedy, or sampled with the reference's temperature / top-p rule,
+    draws fixed by ``seed``) runs in the captured graph; every
     block-size steps the host
     gives growing rows their next block and frees the blocks of rows that
     stopped (``DecodeEngine.run_paged``), and decoding ends once every row has
@@ -564,12 +545,10 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
     for p in parents.values():
         pool.free(p)
     pool.check_invariants()
-    generator = None
-    if do_sample and temperature > 0.0 and seed is not None:  # paged_kv.py:668-671
-        generator = torch.Generator(device=dev)
-        generator.manual_seed(int(seed))
+    if seed is None:  # paged_kv.py:668-671: unseeded calls draw from torch's global RNG
+        seed = int(torch.randint(0, 2 ** 62, (1,)).item())
     eng = DecodeEngine(model, pool, B, width, do_sample=do_sample, temperature=temperature,
-                       top_p=top_p, generator=generator)
+                       top_p=top_p, seed=seed)
     limits = torch.tensor(stop_lengths if stop_lengths is not None else [max_new_tokens] * B,
                           dtype=torch.int32, device=dev).clamp(max=max_new_tokens)
     eng.start(torch.tensor([r[-1] for r in rows], device=dev),

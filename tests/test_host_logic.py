@@ -187,54 +187,6 @@ def test_run_paged_reserves_ahead_and_frees_stopped_rows():
     assert torch.all(s.block_tables == -1)
 
 
-def _bf16_logits_for(probs):
-    """bf16 logits whose softmax is ``probs`` up to bf16 rounding of the logits."""
-    import numpy as np
-
-    return torch.tensor(np.log(np.asarray(probs, dtype=np.float64)), dtype=torch.float32).to(
-        torch.bfloat16)
-
-
-def test_sample_rows_top_p_cuts_the_token_that_crosses():
-    """The reference's rule (fused_ops.py:236-245): sorted descending, a token is
-    cut when the running sum up to and including it exceeds top_p; the first is
-    always kept.  probs 0.5, 0.3, 0.15, 0.05 with top_p = 0.9: running sums 0.5,
-    0.8, 0.95, 1.0, so only the first two remain, drawn 0.625 / 0.375 (a
-    'keep the crossing token' rule would keep three)."""
-    from grpo_mi355x.rollout.decode import sample_rows
-
-    logits = _bf16_logits_for([0.15, 0.5, 0.05, 0.3]).repeat(4000, 1)
-    g = torch.Generator().manual_seed(0)
-    tok = sample_rows(logits, 1.0, 0.9, g)
-    counts = torch.bincount(tok, minlength=4).double() / tok.numel()
-    assert counts[0] == 0 and counts[2] == 0
-    assert abs(counts[1] - 0.625) < 0.03 and abs(counts[3] - 0.375) < 0.03
-
-
-def test_sample_rows_full_distribution_and_tiny_top_p():
-    """top_p = 1: the draws follow softmax(bf16(logits / T)) (chi-square against
-    scipy's softmax of the same bf16 values); top_p -> 0 keeps only the argmax."""
-    import numpy as np
-    from scipy import stats
-    from scipy.special import softmax
-
-    from grpo_mi355x.rollout.decode import sample_rows
-
-    rng = np.random.default_rng(3)
-    base = torch.tensor(rng.normal(0, 1.5, 12), dtype=torch.float32).to(torch.bfloat16)
-    n = 20000
-    g = torch.Generator().manual_seed(1)
-    tok = sample_rows(base.repeat(n, 1), 0.7, 1.0, g)
-    scaled = (base / 0.7).float().numpy().astype(np.float64)
-    expect = softmax(scaled) * n
-    obs = np.bincount(tok.numpy(), minlength=12)
-    keep = expect > 5
-    chi2 = (((obs - expect) ** 2) / expect)[keep].sum()
-    assert chi2 < stats.chi2.ppf(0.999, keep.sum() - 1)
-    tok = sample_rows(base.repeat(64, 1), 0.7, 1e-6, g)
-    assert torch.all(tok == int(torch.argmax(base.float())))
-
-
 def test_torch_advance_stays_inside_the_generated_buffer():
     """The torch-side step bookkeeping (used with sampling and the unfused
     lm_head) records an active row's token at column count[b] and nothing once
