@@ -109,17 +109,6 @@ __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
   return z ^ (z >> 31);
 }
 
-// 8 scaled keys of one 16-byte group of logits.
-__device__ __forceinline__ void group_keys(const uint16_t* p, float inv_t, uint32_t (&k)[8]) {
-  const uint4 v = *reinterpret_cast<const uint4*>(p);
-  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    k[2 * i] = okey(f2bf(bf_lo(w[i]) * inv_t));
-    k[2 * i + 1] = okey(f2bf(bf_hi(w[i]) * inv_t));
-  }
-}
-
 template <typename T>
 __device__ __forceinline__ T wave_sum(T v) {
 #pragma unroll
@@ -194,14 +183,46 @@ __device__ __forceinline__ void block_excl_scan(uint64_t& a, uint32_t& b, uint64
   b = pb + ib - b;
 }
 
+constexpr int SMP_U = 8;     // 16-byte group loads in flight per thread in the row passes
+constexpr int SMP_RMAX = 64; // rounds (64 groups each) per wave slice: V <= 16 * 64 * 64 * 8
+
+// Calls f(group index, its 16 bytes) for the groups first, first + stride, ...
+// below G, with SMP_U loads issued before any is used (clamped addresses, so
+// every load is unconditional and in bounds).
+template <typename F>
+__device__ __forceinline__ void for_groups(const uint16_t* row, int G, int first, int stride,
+                                           F&& f) {
+  for (int g = first; g < G; g += SMP_U * stride) {
+    uint4 v[SMP_U];
+#pragma unroll
+    for (int u = 0; u < SMP_U; ++u)
+      v[u] = *reinterpret_cast<const uint4*>(row + 8 * (int64_t)min(g + u * stride, G - 1));
+#pragma unroll
+    for (int u = 0; u < SMP_U; ++u)
+      if (g + u * stride < G) f(g + u * stride, v[u]);
+  }
+}
+
+// 8 scaled keys of one 16-byte group of logits.
+__device__ __forceinline__ void keys_of(const uint4& v, float inv_t, uint32_t (&k)[8]) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    k[2 * i] = okey(f2bf(bf_lo(w[i]) * inv_t));
+    k[2 * i + 1] = okey(f2bf(bf_hi(w[i]) * inv_t));
+  }
+}
+
 __global__ void __launch_bounds__(SMP_T) sample_top_p_kernel(SampleArgs a) {
   touch_kernargs<sizeof(SampleArgs)>();
-  extern __shared__ uint32_t hist[];  // [SMP_KEYS] counts, later kept bf16 q bits
+  extern __shared__ uint32_t hist[];  // [SMP_KEYS]: counts, then e (float), then kept q (bf16)
   __shared__ uint64_t s64[SMP_W];
   __shared__ uint32_t s32[SMP_W];
   __shared__ uint64_t wmass[SMP_W];
   __shared__ uint32_t wties[SMP_W];
-  __shared__ int64_t s_cut[4];  // bin, tied tokens kept, tokens above the bin, q62 of the bin
+  __shared__ uint64_t rmass[SMP_W][SMP_RMAX];  // per wave and round: kept mass w/o cut ties
+  __shared__ uint32_t rties[SMP_W][SMP_RMAX];  // per wave and round: tokens in the cut bin
+  __shared__ int64_t s_cut[4];  // cut bin, its tied tokens kept, tokens above it, its q (2^-62)
   __shared__ int64_t s_token;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int m = blockIdx.x;
@@ -217,123 +238,147 @@ __global__ void __launch_bounds__(SMP_T) sample_top_p_kernel(SampleArgs a) {
   }
   const uint16_t* row = a.logits + (int64_t)m * a.ld;
   const int G = a.V >> 3;
+  const float inv_t = a.inv_t;
   for (int i = tid; i < SMP_KEYS; i += SMP_T) hist[i] = 0;
+  if (tid == 0) {
+    s_cut[0] = SMP_KEYS;
+    s_cut[1] = 0;
+    s_cut[2] = 0;
+    s_cut[3] = 0;
+    s_token = -1;
+  }
 
   // 1. row maximum of the scaled values
   uint32_t kmax = 0;
-  for (int g = tid; g < G; g += SMP_T) {
+  for_groups(row, G, tid, SMP_T, [&](int, const uint4& v) {
     uint32_t k[8];
-    group_keys(row + 8 * (int64_t)g, a.inv_t, k);
+    keys_of(v, inv_t, k);
 #pragma unroll
     for (int i = 0; i < 8; ++i) kmax = max(kmax, k[i]);
-  }
-  kmax = block_max(kmax, s32);  // (its barriers also order the histogram clear)
+  });
+  kmax = block_max(kmax, s32);  // (its barriers also order the clear above)
   const float mf = bf2f((uint16_t)key_bits(kmax));
   int64_t token = 0;
   int64_t nkept = 1;
   if (!isfinite(mf)) {
     // +inf or NaN maximum: the first index holding it (no distribution exists)
     uint32_t first = 0xFFFFFFFFu;
-    for (int g = tid; g < G; g += SMP_T) {
+    for_groups(row, G, tid, SMP_T, [&](int g, const uint4& v) {
       uint32_t k[8];
-      group_keys(row + 8 * (int64_t)g, a.inv_t, k);
+      keys_of(v, inv_t, k);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         if (k[i] == kmax) first = min(first, (uint32_t)(8 * g + i));
-    }
+    });
     first = block_min(first, s32);
     token = first < (uint32_t)a.V ? first : 0;
   } else {
     // 2. counts per distinct value within the window
-    for (int g = tid; g < G; g += SMP_T) {
+    for_groups(row, G, tid, SMP_T, [&](int, const uint4& v) {
       uint32_t k[8];
-      group_keys(row + 8 * (int64_t)g, a.inv_t, k);
+      keys_of(v, inv_t, k);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const float x = bf2f((uint16_t)key_bits(k[i])) - mf;
         if (x > EXP_MIN_X) atomicAdd(&hist[kmax - k[i]], 1u);
       }
-    }
+    });
     __syncthreads();
 
-    // 3. bin scan; thread t holds bins [t*KPT, (t+1)*KPT) (descending values)
-    // (counts stay in LDS and are re-read per phase; e is recomputed for
-    // non-empty bins only, which keeps the phase cost at one wave's bins)
+    // 3. bin scan; thread t holds bins [t*KPT, (t+1)*KPT) (descending values).
+    // Counts move to registers; each non-empty bin's e is computed once and
+    // parked in its LDS slot.
     const int b0 = tid * SMP_KPT;
-    auto e_of = [&](int bin) {
-      return exp_nonpos(bf2f((uint16_t)key_bits(kmax - (uint32_t)bin)) - mf);
-    };
+    uint32_t cnt[SMP_KPT];
+#pragma unroll
+    for (int j = 0; j < SMP_KPT; ++j) cnt[j] = hist[b0 + j];
     uint64_t z = 0;
+#pragma unroll
     for (int j = 0; j < SMP_KPT; ++j) {
-      const uint32_t c = hist[b0 + j];
-      if (c) z += (uint64_t)c * to_fixed(e_of(b0 + j), 17592186044416.0f);  // 2^44
+      float e = 0.0f;
+      if (cnt[j]) {
+        e = exp_nonpos(bf2f((uint16_t)key_bits(kmax - (uint32_t)(b0 + j))) - mf);
+        z += (uint64_t)cnt[j] * to_fixed(e, 17592186044416.0f);  // 2^44
+      }
+      hist[b0 + j] = __float_as_uint(e);
+      if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
     }
     const float zf = (float)block_sum(z, s64) * 5.684341886080802e-14f;  // 2^-44
-    // p = bf16(e / Z) in 2^-62 units (recomputed below rather than held)
-    auto p62 = [&](int bin) {
-      return to_fixed(bf2f(f2bf(e_of(bin) / zf)), 4611686018427387904.0f);
+    // p = bf16(e / Z) in 2^-62 units
+    auto p62 = [&](int j) {
+      return to_fixed(bf2f(f2bf(__uint_as_float(hist[b0 + j]) / zf)), 4611686018427387904.0f);
     };
     uint64_t mass = 0;
     uint32_t ntok = 0;
+#pragma unroll
     for (int j = 0; j < SMP_KPT; ++j) {
-      const uint32_t c = hist[b0 + j];
-      if (c) mass += (uint64_t)c * p62(b0 + j);
-      ntok += c;
+      if (cnt[j]) mass += (uint64_t)cnt[j] * p62(j);
+      ntok += cnt[j];
+      if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bound the hoisted LDS reads
     }
     uint64_t cum = mass;
     uint32_t above = ntok;
     block_excl_scan(cum, above, s64, s32);
-    // first bin whose last token passes the bound, and how many of its ties stay
-    uint32_t cut = SMP_KEYS;
-    int64_t keep_ties = 0, above_cut = 0;
+    // The cut: the first bin whose last token's running sum passes the bound,
+    // and how many of its tied tokens stay (the first token always stays).
     if (!a.nofilter) {
-      for (int j = 0; j < SMP_KPT && cut == SMP_KEYS; ++j) {
-        const uint32_t c = hist[b0 + j];
-        if (!c) continue;
-        const uint64_t pj = p62(b0 + j);
-        const uint64_t end = cum + (uint64_t)c * pj;
-        if ((int64_t)end > a.keep) {
-          cut = b0 + j;
-          above_cut = above;
-          keep_ties = a.keep < (int64_t)cum
-                          ? 0
-                          : (int64_t)min((uint64_t)c, ((uint64_t)a.keep - cum) / pj);
+      if (a.keep < 0) {
+        if (tid == 0) {
+          s_cut[0] = 0;
+          s_cut[1] = 1;
+          s_cut[2] = 0;
         }
-        cum = end;
-        above += c;
+      } else if ((int64_t)cum <= a.keep && (int64_t)(cum + mass) > a.keep) {
+        // this thread's range holds the crossing
+        for (int j = 0; j < SMP_KPT; ++j) {
+          if (!cnt[j]) continue;
+          const uint64_t pj = p62(j);
+          const uint64_t end = cum + (uint64_t)cnt[j] * pj;
+          if ((int64_t)end > a.keep) {
+            const int64_t kt =
+                (int64_t)min((uint64_t)cnt[j], ((uint64_t)a.keep - cum) / pj);
+            s_cut[0] = b0 + j;
+            s_cut[1] = (b0 + j == 0 && kt == 0) ? 1 : kt;
+            s_cut[2] = above;
+            break;
+          }
+          cum = end;
+          above += cnt[j];
+        }
       }
     }
-    const uint32_t gcut = block_min(cut, s32);
-    if (cut == gcut && gcut < SMP_KEYS) {
-      // the first token in sorted order is always kept
-      s_cut[1] = (gcut == 0 && keep_ties == 0) ? 1 : keep_ties;
-      s_cut[2] = above_cut;
-    }
     __syncthreads();
-    const int64_t kties = gcut < SMP_KEYS ? s_cut[1] : 0;
-    nkept = gcut < SMP_KEYS ? s_cut[2] + kties : a.V;
+    const uint32_t gcut = (uint32_t)s_cut[0];
+    const int64_t kties = s_cut[1];
+    nkept = gcut < (uint32_t)SMP_KEYS ? s_cut[2] + kties : a.V;
 
-    // Z' over the kept tokens, their bf16 probabilities and fixed-point total
-    uint64_t zk = 0;
-    for (int j = 0; j < SMP_KPT; ++j) {
+    // Z' over the kept tokens, their bf16 probabilities q and total W
+    auto kept_n = [&](int j) -> uint64_t {
       const uint32_t bin = b0 + j;
-      const uint64_t n = bin < gcut ? hist[bin] : (bin == gcut ? (uint64_t)kties : 0);
-      if (n) zk += n * to_fixed(e_of(bin), 17592186044416.0f);
+      return bin < gcut ? cnt[j] : (bin == gcut ? (uint64_t)kties : 0);
+    };
+    uint64_t zk = 0;
+#pragma unroll
+    for (int j = 0; j < SMP_KPT; ++j) {
+      const uint64_t n = kept_n(j);
+      if (n) zk += n * to_fixed(__uint_as_float(hist[b0 + j]), 17592186044416.0f);
+      if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
     }
     const float zkf = (float)block_sum(zk, s64) * 5.684341886080802e-14f;
     uint64_t w = 0;
+#pragma unroll
     for (int j = 0; j < SMP_KPT; ++j) {
       const uint32_t bin = b0 + j;
-      const uint32_t c = hist[bin];
-      const uint16_t qb = (bin <= gcut && c) ? f2bf(e_of(bin) / zkf) : (uint16_t)0;
+      const uint16_t qb =
+          (bin <= gcut && cnt[j]) ? f2bf(__uint_as_float(hist[bin]) / zkf) : (uint16_t)0;
       const uint64_t q62 = to_fixed(bf2f(qb), 4611686018427387904.0f);
-      const uint64_t n = bin < gcut ? c : (bin == gcut ? (uint64_t)kties : 0);
-      w += n * q62;
+      w += kept_n(j) * q62;
       hist[bin] = qb;
       if (bin == gcut) s_cut[3] = (int64_t)q62;
+      if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
     }
     const uint64_t W = block_sum(w, s64);  // (its barriers publish hist and s_cut[3])
-    const uint64_t qcut = gcut < SMP_KEYS ? (uint64_t)s_cut[3] : 0;
+    const uint64_t qcut = gcut < (uint32_t)SMP_KEYS ? (uint64_t)s_cut[3] : 0;
 
     // 4. draw
     uint64_t r;
@@ -345,13 +390,12 @@ __global__ void __launch_bounds__(SMP_T) sample_top_p_kernel(SampleArgs a) {
     }
     const uint64_t t = __umul64hi(r, W);
     const int GW = (G + SMP_W - 1) / SMP_W;  // groups per wave slice
-    const int g0 = wave * GW, g1 = min(G, g0 + GW);
-    // kept mass (excluding the cut bin's ties) and cut-bin ties of this wave's slice
-    uint64_t km = 0;
-    uint32_t tc = 0;
-    for (int g = g0 + lane; g < g1; g += 64) {
+    const int g0 = min(G, wave * GW), g1 = min(G, g0 + GW);
+    const int R = (g1 - g0 + 63) / 64;      // rounds of 64 groups in this slice
+    // per round: kept mass outside the cut bin, and tokens in the cut bin
+    auto group_q = [&](const uint4& v, uint64_t& km, uint32_t& tc) {
       uint32_t k[8];
-      group_keys(row + 8 * (int64_t)g, a.inv_t, k);
+      keys_of(v, inv_t, k);
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const uint32_t bin = kmax - k[i];
@@ -361,16 +405,37 @@ __global__ void __launch_bounds__(SMP_T) sample_top_p_kernel(SampleArgs a) {
           km += to_fixed(bf2f((uint16_t)hist[bin]), 4611686018427387904.0f);
         }
       }
+    };
+    uint64_t wkm = 0;
+    uint32_t wtc = 0;
+    for (int rb = 0; rb < R; rb += SMP_U) {
+      uint4 v[SMP_U];
+#pragma unroll
+      for (int u = 0; u < SMP_U; ++u)
+        v[u] = *reinterpret_cast<const uint4*>(
+            row + 8 * (int64_t)min(g0 + (rb + u) * 64 + lane, G - 1));
+#pragma unroll
+      for (int u = 0; u < SMP_U; ++u) {
+        if (rb + u >= R) break;  // wave-uniform
+        uint64_t km = 0;
+        uint32_t tc = 0;
+        if (g0 + (rb + u) * 64 + lane < g1) group_q(v[u], km, tc);
+        km = wave_sum(km);
+        tc = wave_sum(tc);
+        if (lane == 0) {
+          rmass[wave][rb + u] = km;
+          rties[wave][rb + u] = tc;
+        }
+        wkm += km;
+        wtc += tc;
+      }
     }
-    km = wave_sum(km);
-    tc = wave_sum(tc);
     if (lane == 0) {
-      wmass[wave] = km;
-      wties[wave] = tc;
+      wmass[wave] = wkm;
+      wties[wave] = wtc;
     }
-    if (tid == 0) s_token = -1;
     __syncthreads();
-    // the wave whose slice holds t; each thread finds it from the 16 totals
+    // the wave whose slice holds t (each thread finds it from the 16 totals)
     uint64_t base = 0;
     int64_t ties_before = 0;
     int hold = SMP_W - 1;
@@ -385,63 +450,80 @@ __global__ void __launch_bounds__(SMP_T) sample_top_p_kernel(SampleArgs a) {
       ties_before += wties[v];
     }
     if (wave == hold) {
-      for (int gr = g0; gr < g1; gr += 64) {
-        const int g = gr + lane;
-        uint32_t k[8] = {0, 0, 0, 0, 0, 0, 0, 0};
-        bool valid = g < g1;
-        if (valid) group_keys(row + 8 * (int64_t)g, a.inv_t, k);
-        uint32_t lt = 0;
+      // the round holding t: lane l looks at round l of the slice
+      const uint64_t rm = lane < R ? rmass[wave][lane] : 0;
+      const uint32_t rt = lane < R ? rties[wave][lane] : 0;
+      uint32_t it = rt;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) lt += (valid && kmax - k[i] == gcut) ? 1u : 0u;
-        uint32_t it = lt;
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t x = __shfl_up(it, o);
+        if (lane >= o) it += x;
+      }
+      const int64_t tb_round = ties_before + (it - rt);  // cut ties before this round
+      const int64_t kt = min((int64_t)rt, max((int64_t)0, kties - tb_round));
+      const uint64_t rk = rm + (uint64_t)kt * qcut;
+      uint64_t im = rk;
 #pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const uint32_t x = __shfl_up(it, o);
-          if (lane >= o) it += x;
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t x = __shfl_up(im, o);
+        if (lane >= o) im += x;
+      }
+      const uint64_t hitr = __ballot(lane < R && base + im > t);
+      const int rsel = hitr ? __ffsll((unsigned long long)hitr) - 1 : R - 1;
+      const uint64_t rbase = base + __shfl(im - rk, rsel);
+      const int64_t rties0 = __shfl(tb_round, rsel);
+      // that round: one group per lane
+      const int g = g0 + rsel * 64 + lane;
+      const bool valid = g < g1;
+      const uint4 v = *reinterpret_cast<const uint4*>(row + 8 * (int64_t)min(g, G - 1));
+      uint32_t k[8];
+      keys_of(v, inv_t, k);
+      uint32_t lt = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) lt += (valid && kmax - k[i] == gcut) ? 1u : 0u;
+      uint32_t il = lt;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint32_t x = __shfl_up(il, o);
+        if (lane >= o) il += x;
+      }
+      int64_t rank = rties0 + (il - lt);  // tie rank of this lane's first cut-bin token
+      uint64_t wq[8];
+      uint64_t lm = 0;
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const uint32_t bin = kmax - k[i];
+        uint64_t q = 0;
+        if (valid) {
+          if (bin == gcut) {
+            q = rank < kties ? qcut : 0;
+            ++rank;
+          } else if (bin < (uint32_t)SMP_KEYS) {
+            q = to_fixed(bf2f((uint16_t)hist[bin]), 4611686018427387904.0f);
+          }
         }
-        int64_t rank = ties_before + (it - lt);  // tie rank of this lane's first tie
-        uint64_t wq[8];
-        uint64_t lm = 0;
+        wq[i] = q;
+        lm += q;
+      }
+      uint64_t ig = lm;
+#pragma unroll
+      for (int o = 1; o < 64; o <<= 1) {
+        const uint64_t x = __shfl_up(ig, o);
+        if (lane >= o) ig += x;
+      }
+      const uint64_t hit = __ballot(valid && rbase + ig > t);
+      if (hit && lane == __ffsll((unsigned long long)hit) - 1) {
+        uint64_t acc = rbase + ig - lm;
+        int64_t tok = 8 * (int64_t)g + 7;
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-          const uint32_t bin = kmax - k[i];
-          uint64_t q = 0;
-          if (valid) {
-            if (bin == gcut) {
-              q = rank < kties ? qcut : 0;
-              ++rank;
-            } else if (bin < (uint32_t)SMP_KEYS) {
-              q = to_fixed(bf2f((uint16_t)hist[bin]), 4611686018427387904.0f);
-            }
+          if (acc + wq[i] > t) {
+            tok = 8 * (int64_t)g + i;
+            break;
           }
-          wq[i] = q;
-          lm += q;
+          acc += wq[i];
         }
-        uint64_t im = lm;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-          const uint64_t x = __shfl_up(im, o);
-          if (lane >= o) im += x;
-        }
-        const uint64_t hit = __ballot(base + im > t);
-        if (hit) {
-          if (lane == __ffsll((unsigned long long)hit) - 1) {
-            uint64_t acc = base + im - lm;
-            int64_t tok = 8 * (int64_t)g + 7;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-              if (acc + wq[i] > t) {
-                tok = 8 * (int64_t)g + i;
-                break;
-              }
-              acc += wq[i];
-            }
-            s_token = tok;
-          }
-          break;
-        }
-        base += __shfl(im, 63);
-        ties_before += __shfl(it, 63);
+        s_token = tok;
       }
     }
     __syncthreads();
@@ -484,6 +566,7 @@ int launch(const SampleArgs& a, grpo_stream_t stream) {
 int check_common(const void* logits, int64_t ld, int M, int V, float temperature) {
   if (M <= 0 || V <= 0) return einval("bad sampling dimensions");
   if (V % 8 || ld % 8 || ld < V) return einval("sampling needs V % 8 == 0 and ld % 8 == 0, ld >= V");
+  if (V > SMP_W * SMP_RMAX * 64 * 8) return einval("sampling supports V <= 524288");
   if (!logits || !aligned16(logits)) return einval("logits must be 16-byte aligned");
   if (!(temperature > 0.0f)) return einval("temperature must be > 0 (greedy decoding otherwise)");
   return GRPO_OK;
