@@ -4,29 +4,38 @@
 // (src/triton_kernels/paged_kv.py:437-450) followed by the row update of
 // paged_kv.py:800-820, :938, :978.
 //
-// The reference sorts the whole vocabulary per row.  This kernel needs no sort:
-// one workgroup per row, 1024 threads.
-//   1. max: scaled = bf16(logit * (1/T)); the row maximum m of the scaled values
-//      (as order-preserving 16-bit keys of their bf16 bit patterns).
-//   2. histogram: every token whose scaled value lies within 86 of m gets
-//      counted in an LDS bin per distinct bf16 value (bin = key(m) - key); the
-//      86-wide window holds at most 33906 distinct bf16 values.  Tokens further
-//      down have exp(s - m) < 2^-124, i.e. probability 0 in bf16.
-//   3. bin scan: the bins in descending value order are the sorted vocabulary
-//      in runs of equal values.  Per bin: e = exp(v - m); Z = sum of count * e
-//      (exact fixed-point sum); p = bf16(e / Z); the running sum of p in sorted
-//      order (exact, 2^-62 units) locates the cut: the bin where the running sum
-//      passes the keep bound and how many of its tied tokens (lowest indices
-//      first) stay.  Then Z' over the kept tokens, q = bf16(e / Z') per bin,
-//      and W = the fixed-point total of the kept q.
-//   4. draw: t = floor(r * W / 2^64) for the row's 64-bit uniform r; the token
-//      is the first index whose running sum of kept q (index order) exceeds t.
-//      Each wave sums the kept mass of its slice of the row, the wave holding t
-//      walks its slice.
+// The reference sorts the whole vocabulary per row.  Here no sort is needed:
+// the distinct bf16 values of a row are counted, and the counts in descending
+// value order ARE the sorted vocabulary in runs of equal values.  Each row is
+// cut into S slices (S * rows ~ 256 workgroups, so the passes over the row use
+// the whole chip); five launches:
+//   K0 smp_max     (slice, row): the slice's maximum scaled value
+//                  (scaled = bf16(logit * (1/T)), as order-preserving 16-bit
+//                  keys of the bf16 bit patterns).
+//   K1 smp_hist    (slice, row): counts per distinct value within 86 of the row
+//                  maximum m in LDS (bin = key(m) - key; at most 33906 values;
+//                  tokens further down have exp(s - m) < 2^-124, probability 0
+//                  in bf16), added into the row's bins in the workspace.
+//   K2 smp_scan    (row): reads and clears the row's bins.  Per bin: e =
+//                  exp(v - m); Z = sum count * e (exact fixed point); p =
+//                  bf16(e / Z); the exact running sum of p (2^-62 units) in
+//                  descending order locates the cut: the bin where the sum
+//                  passes the keep bound and how many of its tied tokens
+//                  (lowest indices first) stay.  Then Z' over the kept tokens,
+//                  q = bf16(e / Z'), and the draw: t = floor(r * W / 2^64), W
+//                  the fixed-point total of the kept q, located in the kept
+//                  tokens taken in sorted order (value descending, index
+//                  ascending): a value and the rank of the token among that
+//                  value's tokens.
+//   K3 smp_count   (slice, row): tokens of that value per slice.
+//   K4 smp_pick    (row): the slice and position of the rank-th such token;
+//                  the token; the row bookkeeping.
 // Every rounding point is fixed (a bespoke exp with no fused multiply-adds,
-// exact integer sums, correctly rounded float32 division), so the result is a
+// exact integer sums, correctly rounded float32 division), so the token is a
 // deterministic function of (logits, T, top_p, r) that a float32 host
-// restatement reproduces bit for bit.
+// restatement reproduces bit for bit.  The workspace's bins are zero between
+// calls (K2 clears what K1 added), so no memset is ever issued: the five
+// launches can be captured into a HIP graph and replayed.
 
 #include <math.h>
 
@@ -36,23 +45,40 @@
 namespace grpo {
 namespace {
 
-constexpr int SMP_T = 1024;                // threads per workgroup
-constexpr int SMP_W = SMP_T / 64;          // waves per workgroup
 constexpr int SMP_KEYS = 34816;            // LDS bins (>= 33906 values in the window)
-constexpr int SMP_KPT = SMP_KEYS / SMP_T;  // bins per thread
+constexpr int SMP_SMAX = 32;               // slices per row at most
+constexpr int SMP_T1 = 256;                // threads of the slice kernels K0, K3
+constexpr int SMP_TH = 512;                // threads of the histogram kernel K1
+constexpr int SMP_T = 1024;                // threads of the row kernels K2, K4
+constexpr int SMP_KPT = SMP_KEYS / SMP_T;  // bins per K2 thread
 constexpr size_t SMP_LDS = (size_t)SMP_KEYS * 4;
 constexpr float EXP_MIN_X = -86.0f;
-static_assert(SMP_KEYS % SMP_T == 0, "bins must split evenly over the threads");
+constexpr int SMP_U = 8;  // 16-byte group loads in flight per thread in the row passes
+static_assert(SMP_KEYS % SMP_T == 0 && SMP_KEYS % 4 == 0, "bins must split evenly");
+
+// Per-row workspace.
+struct RowWs {
+  uint32_t slice_max[SMP_SMAX];  // K0
+  uint32_t slice_cnt[SMP_SMAX];  // K3
+  int64_t sel_key;               // K2: the drawn token's value (as a key)
+  int64_t sel_rank;              // K2: its rank among that value's tokens, index order
+  int64_t nkept;                 // K2: tokens in the top-p set
+  int64_t pad;
+  uint32_t bins[SMP_KEYS];       // K1 adds, K2 reads and clears: zero between calls
+};
+static_assert(sizeof(RowWs) % 16 == 0, "row workspaces must stay 16-byte aligned");
 
 struct SampleArgs {
   const uint16_t* logits;
   int64_t ld;
   int M, V;
+  int S, SG;         // slices per row, 8-token groups per slice
   float inv_t;       // float32(1 / max(T, 1e-6))
   int nofilter;      // top_p >= 1: no cut
   int64_t keep;      // keep a token while the running sum (2^-62 units) <= keep
   const uint64_t* draws;  // [M] uniforms, or null: SplitMix64 of (seed, row, count[row])
   uint64_t seed;
+  RowWs* ws;
   int64_t* out_tokens;    // [M] or null
   int32_t* out_kept;      // [M] or null
   // decode bookkeeping (tokens == null: sampling only)
@@ -100,6 +126,9 @@ __device__ __forceinline__ float exp_nonpos(float x) {
 __device__ __forceinline__ uint64_t to_fixed(float v, float scale) {
   return (uint64_t)(v * scale);  // v >= 0; exact power-of-two scaling, truncation
 }
+constexpr float TWO44 = 17592186044416.0f;
+constexpr float TWO62 = 4611686018427387904.0f;
+constexpr float TWO_M44 = 5.684341886080802e-14f;
 
 // SplitMix64 output function (Steele, Lea and Flood, OOPSLA 2014).
 __device__ __forceinline__ uint64_t splitmix64(uint64_t z) {
@@ -116,19 +145,20 @@ __device__ __forceinline__ T wave_sum(T v) {
   return v;
 }
 
-// Block-wide sum / max / min through one LDS slot per wave.  Every thread gets
-// the result; the trailing barrier lets the slots be reused at once.
-template <typename T>
+// Block-wide sum / max over NW waves through one LDS slot per wave.  Every
+// thread gets the result; the trailing barrier lets the slots be reused.
+template <int NW, typename T>
 __device__ __forceinline__ T block_sum(T v, T* slots) {
   v = wave_sum(v);
   if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
   __syncthreads();
   T s = 0;
 #pragma unroll
-  for (int w = 0; w < SMP_W; ++w) s += slots[w];
+  for (int w = 0; w < NW; ++w) s += slots[w];
   __syncthreads();
   return s;
 }
+template <int NW>
 __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* slots) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = max(v, (uint32_t)__shfl_xor(v, o));
@@ -136,18 +166,7 @@ __device__ __forceinline__ uint32_t block_max(uint32_t v, uint32_t* slots) {
   __syncthreads();
   uint32_t s = 0;
 #pragma unroll
-  for (int w = 0; w < SMP_W; ++w) s = max(s, slots[w]);
-  __syncthreads();
-  return s;
-}
-__device__ __forceinline__ uint32_t block_min(uint32_t v, uint32_t* slots) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = min(v, (uint32_t)__shfl_xor(v, o));
-  if ((threadIdx.x & 63) == 0) slots[threadIdx.x >> 6] = v;
-  __syncthreads();
-  uint32_t s = 0xFFFFFFFFu;
-#pragma unroll
-  for (int w = 0; w < SMP_W; ++w) s = min(s, slots[w]);
+  for (int w = 0; w < NW; ++w) s = max(s, slots[w]);
   __syncthreads();
   return s;
 }
@@ -183,23 +202,20 @@ __device__ __forceinline__ void block_excl_scan(uint64_t& a, uint32_t& b, uint64
   b = pb + ib - b;
 }
 
-constexpr int SMP_U = 8;     // 16-byte group loads in flight per thread in the row passes
-constexpr int SMP_RMAX = 64; // rounds (64 groups each) per wave slice: V <= 16 * 64 * 64 * 8
-
 // Calls f(group index, its 16 bytes) for the groups first, first + stride, ...
-// below G, with SMP_U loads issued before any is used (clamped addresses, so
+// below end, with SMP_U loads issued before any is used (clamped addresses, so
 // every load is unconditional and in bounds).
 template <typename F>
-__device__ __forceinline__ void for_groups(const uint16_t* row, int G, int first, int stride,
+__device__ __forceinline__ void for_groups(const uint16_t* row, int end, int first, int stride,
                                            F&& f) {
-  for (int g = first; g < G; g += SMP_U * stride) {
+  for (int g = first; g < end; g += SMP_U * stride) {
     uint4 v[SMP_U];
 #pragma unroll
     for (int u = 0; u < SMP_U; ++u)
-      v[u] = *reinterpret_cast<const uint4*>(row + 8 * (int64_t)min(g + u * stride, G - 1));
+      v[u] = *reinterpret_cast<const uint4*>(row + 8 * (int64_t)min(g + u * stride, end - 1));
 #pragma unroll
     for (int u = 0; u < SMP_U; ++u)
-      if (g + u * stride < G) f(g + u * stride, v[u]);
+      if (g + u * stride < end) f(g + u * stride, v[u]);
   }
 }
 
@@ -213,21 +229,258 @@ __device__ __forceinline__ void keys_of(const uint4& v, float inv_t, uint32_t (&
   }
 }
 
-__global__ void __launch_bounds__(SMP_T) sample_top_p_kernel(SampleArgs a) {
+__device__ __forceinline__ bool row_stopped(const SampleArgs& a, int m) {
+  return a.tokens != nullptr && !a.active[m];
+}
+__device__ __forceinline__ uint32_t row_max_key(const SampleArgs& a, const RowWs& w) {
+  uint32_t k = 0;
+  for (int i = 0; i < a.S; ++i) k = max(k, w.slice_max[i]);
+  return k;
+}
+
+// K0: the slice's maximum key.
+__global__ void __launch_bounds__(SMP_T1) smp_max_kernel(SampleArgs a) {
+  touch_kernargs<sizeof(SampleArgs)>();
+  __shared__ uint32_t s32[SMP_T1 / 64];
+  const int s = blockIdx.x, m = blockIdx.y;
+  if (row_stopped(a, m)) return;
+  const uint16_t* row = a.logits + (int64_t)m * a.ld;
+  const int G = a.V >> 3, g0 = min(G, s * a.SG), g1 = min(G, g0 + a.SG);
+  const float inv_t = a.inv_t;
+  uint32_t kmax = 0;
+  for_groups(row, g1, g0 + (int)threadIdx.x, SMP_T1, [&](int, const uint4& v) {
+    uint32_t k[8];
+    keys_of(v, inv_t, k);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kmax = max(kmax, k[i]);
+  });
+  kmax = block_max<SMP_T1 / 64>(kmax, s32);
+  if (threadIdx.x == 0) a.ws[m].slice_max[s] = kmax;
+}
+
+// K1: the slice's counts per value within the window, added into the row's bins.
+__global__ void __launch_bounds__(SMP_TH) smp_hist_kernel(SampleArgs a) {
+  touch_kernargs<sizeof(SampleArgs)>();
+  extern __shared__ uint32_t hist[];  // [SMP_KEYS]
+  const int s = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
+  if (row_stopped(a, m)) return;
+  RowWs& w = a.ws[m];
+  const uint32_t kmax = row_max_key(a, w);
+  const float mf = bf2f((uint16_t)key_bits(kmax));
+  if (!isfinite(mf)) return;  // no distribution: K2 picks the first maximum
+  for (int i = tid; i < SMP_KEYS; i += SMP_TH) hist[i] = 0;
+  __syncthreads();
+  const uint16_t* row = a.logits + (int64_t)m * a.ld;
+  const int G = a.V >> 3, g0 = min(G, s * a.SG), g1 = min(G, g0 + a.SG);
+  const float inv_t = a.inv_t;
+  for_groups(row, g1, g0 + tid, SMP_TH, [&](int, const uint4& v) {
+    uint32_t k[8];
+    keys_of(v, inv_t, k);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float x = bf2f((uint16_t)key_bits(k[i])) - mf;
+      if (x > EXP_MIN_X) atomicAdd(&hist[kmax - k[i]], 1u);
+    }
+  });
+  __syncthreads();
+  for (int i = tid; i < SMP_KEYS; i += SMP_TH) {
+    const uint32_t c = hist[i];
+    if (c) atomicAdd(&w.bins[i], c);
+  }
+}
+
+// K2: the row's bin scan: cut, kept probabilities, draw (value and rank).
+__global__ void __launch_bounds__(SMP_T) smp_scan_kernel(SampleArgs a) {
   touch_kernargs<sizeof(SampleArgs)>();
   extern __shared__ uint32_t hist[];  // [SMP_KEYS]: counts, then e (float), then kept q (bf16)
-  __shared__ uint64_t s64[SMP_W];
-  __shared__ uint32_t s32[SMP_W];
-  __shared__ uint64_t wmass[SMP_W];
-  __shared__ uint32_t wties[SMP_W];
-  __shared__ uint64_t rmass[SMP_W][SMP_RMAX];  // per wave and round: kept mass w/o cut ties
-  __shared__ uint32_t rties[SMP_W][SMP_RMAX];  // per wave and round: tokens in the cut bin
-  __shared__ int64_t s_cut[4];  // cut bin, its tied tokens kept, tokens above it, its q (2^-62)
-  __shared__ int64_t s_token;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  __shared__ uint64_t s64[SMP_T / 64];
+  __shared__ uint32_t s32[SMP_T / 64];
+  __shared__ int64_t s_cut[4];  // cut bin, its tied tokens kept, tokens above it
+  __shared__ int64_t s_sel[2];  // drawn bin, rank within it
+  __shared__ uint64_t s_w;
+  const int tid = threadIdx.x;
   const int m = blockIdx.x;
-  const bool bookkeeping = a.tokens != nullptr;
-  if (bookkeeping && !a.active[m]) {  // stopped row: no draw, the row state stays put
+  if (row_stopped(a, m)) return;
+  RowWs& ws = a.ws[m];
+  const uint32_t kmax = row_max_key(a, ws);
+  const float mf = bf2f((uint16_t)key_bits(kmax));
+  if (!isfinite(mf)) {  // +inf or NaN maximum: the first index holding it
+    if (tid == 0) {
+      ws.sel_key = kmax;
+      ws.sel_rank = 0;
+      ws.nkept = 1;
+    }
+    return;
+  }
+  {
+    uint4* src = reinterpret_cast<uint4*>(ws.bins);
+    uint4* dst = reinterpret_cast<uint4*>(hist);
+    for (int i = tid; i < SMP_KEYS / 4; i += SMP_T) {
+      dst[i] = src[i];
+      src[i] = make_uint4(0, 0, 0, 0);  // zero for the next call
+    }
+  }
+  if (tid == 0) {
+    s_cut[0] = SMP_KEYS;
+    s_cut[1] = 0;
+    s_cut[2] = 0;
+    s_sel[0] = 0;
+    s_sel[1] = 0;
+  }
+  __syncthreads();
+
+  // Thread t holds bins [t*KPT, (t+1)*KPT) (descending values).  Counts move
+  // to registers; each non-empty bin's e is computed once and parked in its
+  // LDS slot.
+  const int b0 = tid * SMP_KPT;
+  uint32_t cnt[SMP_KPT];
+#pragma unroll
+  for (int j = 0; j < SMP_KPT; ++j) cnt[j] = hist[b0 + j];
+  uint64_t z = 0;
+#pragma unroll
+  for (int j = 0; j < SMP_KPT; ++j) {
+    float e = 0.0f;
+    if (cnt[j]) {
+      e = exp_nonpos(bf2f((uint16_t)key_bits(kmax - (uint32_t)(b0 + j))) - mf);
+      z += (uint64_t)cnt[j] * to_fixed(e, TWO44);
+    }
+    hist[b0 + j] = __float_as_uint(e);
+  }
+  const float zf = (float)block_sum<SMP_T / 64>(z, s64) * TWO_M44;
+  // p = bf16(e / Z) in 2^-62 units
+  auto p62 = [&](int j) {
+    return to_fixed(bf2f(f2bf(__uint_as_float(hist[b0 + j]) / zf)), TWO62);
+  };
+  uint64_t mass = 0;
+  uint32_t ntok = 0;
+#pragma unroll
+  for (int j = 0; j < SMP_KPT; ++j) {
+    if (cnt[j]) mass += (uint64_t)cnt[j] * p62(j);
+    ntok += cnt[j];
+  }
+  uint64_t cum = mass;
+  uint32_t above = ntok;
+  block_excl_scan(cum, above, s64, s32);
+  // The cut: the first bin whose last token's running sum passes the bound,
+  // and how many of its tied tokens stay (the first token always stays).
+  if (!a.nofilter) {
+    if (a.keep < 0) {
+      if (tid == 0) {
+        s_cut[0] = 0;
+        s_cut[1] = 1;
+        s_cut[2] = 0;
+      }
+    } else if ((int64_t)cum <= a.keep && (int64_t)(cum + mass) > a.keep) {
+      // this thread's bins hold the crossing
+      for (int j = 0; j < SMP_KPT; ++j) {
+        if (!cnt[j]) continue;
+        const uint64_t pj = p62(j);
+        const uint64_t end = cum + (uint64_t)cnt[j] * pj;
+        if ((int64_t)end > a.keep) {
+          const int64_t kt = (int64_t)min((uint64_t)cnt[j], ((uint64_t)a.keep - cum) / pj);
+          s_cut[0] = b0 + j;
+          s_cut[1] = (b0 + j == 0 && kt == 0) ? 1 : kt;
+          s_cut[2] = above;
+          break;
+        }
+        cum = end;
+        above += cnt[j];
+      }
+    }
+  }
+  __syncthreads();
+  const uint32_t gcut = (uint32_t)s_cut[0];
+  const int64_t kties = s_cut[1];
+  const int64_t nkept = gcut < (uint32_t)SMP_KEYS ? s_cut[2] + kties : a.V;
+
+  // Z' over the kept tokens, their bf16 probabilities q and total W
+  auto kept_n = [&](int j) -> uint64_t {
+    const uint32_t bin = b0 + j;
+    return bin < gcut ? cnt[j] : (bin == gcut ? (uint64_t)kties : 0);
+  };
+  uint64_t zk = 0;
+#pragma unroll
+  for (int j = 0; j < SMP_KPT; ++j) {
+    const uint64_t n = kept_n(j);
+    if (n) zk += n * to_fixed(__uint_as_float(hist[b0 + j]), TWO44);
+  }
+  const float zkf = (float)block_sum<SMP_T / 64>(zk, s64) * TWO_M44;
+  uint64_t w = 0;
+#pragma unroll
+  for (int j = 0; j < SMP_KPT; ++j) {
+    const uint64_t n = kept_n(j);
+    const uint16_t qb = n ? f2bf(__uint_as_float(hist[b0 + j]) / zkf) : (uint16_t)0;
+    w += n * to_fixed(bf2f(qb), TWO62);
+    hist[b0 + j] = qb;  // this thread's bins only
+  }
+  uint64_t wpre = w;
+  uint32_t unused = 0;
+  block_excl_scan(wpre, unused, s64, s32);
+  if (tid == SMP_T - 1) s_w = wpre + w;  // W: the last thread's inclusive prefix
+  __syncthreads();
+  const uint64_t W = s_w;
+
+  // draw: t in [0, W), located among the kept tokens in sorted order
+  uint64_t r;
+  if (a.draws) {
+    r = a.draws[m];
+  } else {
+    const uint32_t step = a.tokens ? (uint32_t)a.count[m] : 0u;
+    r = splitmix64(a.seed + splitmix64(((uint64_t)(uint32_t)m << 32) | step));
+  }
+  const uint64_t t = __umul64hi(r, W);
+  if (t >= wpre && t < wpre + w) {
+    uint64_t c = wpre;
+    for (int j = 0; j < SMP_KPT; ++j) {
+      const uint64_t n = kept_n(j);
+      if (!n) continue;
+      const uint64_t q62 = to_fixed(bf2f((uint16_t)hist[b0 + j]), TWO62);
+      if (t < c + n * q62) {  // (then q62 > 0)
+        s_sel[0] = b0 + j;
+        s_sel[1] = (int64_t)((t - c) / q62);
+        break;
+      }
+      c += n * q62;
+    }
+  }
+  __syncthreads();
+  if (tid == 0) {
+    ws.sel_key = kmax - (uint32_t)s_sel[0];
+    ws.sel_rank = s_sel[1];
+    ws.nkept = nkept;
+  }
+}
+
+// K3: tokens of the drawn value per slice.
+__global__ void __launch_bounds__(SMP_T1) smp_count_kernel(SampleArgs a) {
+  touch_kernargs<sizeof(SampleArgs)>();
+  __shared__ uint32_t s32[SMP_T1 / 64];
+  const int s = blockIdx.x, m = blockIdx.y;
+  if (row_stopped(a, m)) return;
+  const uint32_t key = (uint32_t)a.ws[m].sel_key;
+  const uint16_t* row = a.logits + (int64_t)m * a.ld;
+  const int G = a.V >> 3, g0 = min(G, s * a.SG), g1 = min(G, g0 + a.SG);
+  const float inv_t = a.inv_t;
+  uint32_t c = 0;
+  for_groups(row, g1, g0 + (int)threadIdx.x, SMP_T1, [&](int, const uint4& v) {
+    uint32_t k[8];
+    keys_of(v, inv_t, k);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) c += k[i] == key ? 1u : 0u;
+  });
+  c = block_sum<SMP_T1 / 64>(c, s32);
+  if (threadIdx.x == 0) a.ws[m].slice_cnt[s] = c;
+}
+
+// K4: the rank-th token of the drawn value (index order), and the row update.
+__global__ void __launch_bounds__(SMP_T) smp_pick_kernel(SampleArgs a) {
+  touch_kernargs<sizeof(SampleArgs)>();
+  __shared__ uint64_t s64[SMP_T / 64];
+  __shared__ uint32_t s32[SMP_T / 64];
+  __shared__ int64_t s_token;
+  __shared__ uint64_t s_round;
+  const int tid = threadIdx.x, m = blockIdx.x;
+  if (row_stopped(a, m)) {  // stopped row: no draw, the row state stays put
     if (tid == 0) {
       const int64_t g = a.tokens[m];
       if (a.out_tokens) a.out_tokens[m] = g;
@@ -236,304 +489,61 @@ __global__ void __launch_bounds__(SMP_T) sample_top_p_kernel(SampleArgs a) {
     }
     return;
   }
-  const uint16_t* row = a.logits + (int64_t)m * a.ld;
-  const int G = a.V >> 3;
-  const float inv_t = a.inv_t;
-  for (int i = tid; i < SMP_KEYS; i += SMP_T) hist[i] = 0;
-  if (tid == 0) {
-    s_cut[0] = SMP_KEYS;
-    s_cut[1] = 0;
-    s_cut[2] = 0;
-    s_cut[3] = 0;
-    s_token = -1;
+  const RowWs& ws = a.ws[m];
+  const uint32_t key = (uint32_t)ws.sel_key;
+  int64_t rank = ws.sel_rank;
+  int hold = a.S - 1;
+  for (int s = 0; s < a.S; ++s) {
+    const int64_t c = ws.slice_cnt[s];
+    if (rank < c) {
+      hold = s;
+      break;
+    }
+    rank -= c;
   }
-
-  // 1. row maximum of the scaled values
-  uint32_t kmax = 0;
-  for_groups(row, G, tid, SMP_T, [&](int, const uint4& v) {
+  if (tid == 0) s_token = -1;
+  __syncthreads();
+  const uint16_t* row = a.logits + (int64_t)m * a.ld;
+  const int G = a.V >> 3, g0 = min(G, hold * a.SG), g1 = min(G, g0 + a.SG);
+  const float inv_t = a.inv_t;
+  for (int gr = g0; gr < g1; gr += SMP_T) {
+    const int g = gr + tid;
+    const bool valid = g < g1;
+    const uint4 v = *reinterpret_cast<const uint4*>(row + 8 * (int64_t)min(g, G - 1));
     uint32_t k[8];
     keys_of(v, inv_t, k);
+    uint32_t hits = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) kmax = max(kmax, k[i]);
-  });
-  kmax = block_max(kmax, s32);  // (its barriers also order the clear above)
-  const float mf = bf2f((uint16_t)key_bits(kmax));
-  int64_t token = 0;
-  int64_t nkept = 1;
-  if (!isfinite(mf)) {
-    // +inf or NaN maximum: the first index holding it (no distribution exists)
-    uint32_t first = 0xFFFFFFFFu;
-    for_groups(row, G, tid, SMP_T, [&](int g, const uint4& v) {
-      uint32_t k[8];
-      keys_of(v, inv_t, k);
+    for (int i = 0; i < 8; ++i) hits |= (valid && k[i] == key) ? (1u << i) : 0u;
+    const uint64_t mine = (uint64_t)__popc(hits);
+    uint64_t ex = mine;
+    uint32_t unused = 0;
+    block_excl_scan(ex, unused, s64, s32);
+    if ((int64_t)ex <= rank && rank < (int64_t)(ex + mine)) {
+      int left = (int)(rank - (int64_t)ex);
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        if (k[i] == kmax) first = min(first, (uint32_t)(8 * g + i));
-    });
-    first = block_min(first, s32);
-    token = first < (uint32_t)a.V ? first : 0;
-  } else {
-    // 2. counts per distinct value within the window
-    for_groups(row, G, tid, SMP_T, [&](int, const uint4& v) {
-      uint32_t k[8];
-      keys_of(v, inv_t, k);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const float x = bf2f((uint16_t)key_bits(k[i])) - mf;
-        if (x > EXP_MIN_X) atomicAdd(&hist[kmax - k[i]], 1u);
-      }
-    });
-    __syncthreads();
-
-    // 3. bin scan; thread t holds bins [t*KPT, (t+1)*KPT) (descending values).
-    // Counts move to registers; each non-empty bin's e is computed once and
-    // parked in its LDS slot.
-    const int b0 = tid * SMP_KPT;
-    uint32_t cnt[SMP_KPT];
-#pragma unroll
-    for (int j = 0; j < SMP_KPT; ++j) cnt[j] = hist[b0 + j];
-    uint64_t z = 0;
-#pragma unroll
-    for (int j = 0; j < SMP_KPT; ++j) {
-      float e = 0.0f;
-      if (cnt[j]) {
-        e = exp_nonpos(bf2f((uint16_t)key_bits(kmax - (uint32_t)(b0 + j))) - mf);
-        z += (uint64_t)cnt[j] * to_fixed(e, 17592186044416.0f);  // 2^44
-      }
-      hist[b0 + j] = __float_as_uint(e);
-      if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-    }
-    const float zf = (float)block_sum(z, s64) * 5.684341886080802e-14f;  // 2^-44
-    // p = bf16(e / Z) in 2^-62 units
-    auto p62 = [&](int j) {
-      return to_fixed(bf2f(f2bf(__uint_as_float(hist[b0 + j]) / zf)), 4611686018427387904.0f);
-    };
-    uint64_t mass = 0;
-    uint32_t ntok = 0;
-#pragma unroll
-    for (int j = 0; j < SMP_KPT; ++j) {
-      if (cnt[j]) mass += (uint64_t)cnt[j] * p62(j);
-      ntok += cnt[j];
-      if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);  // bound the hoisted LDS reads
-    }
-    uint64_t cum = mass;
-    uint32_t above = ntok;
-    block_excl_scan(cum, above, s64, s32);
-    // The cut: the first bin whose last token's running sum passes the bound,
-    // and how many of its tied tokens stay (the first token always stays).
-    if (!a.nofilter) {
-      if (a.keep < 0) {
-        if (tid == 0) {
-          s_cut[0] = 0;
-          s_cut[1] = 1;
-          s_cut[2] = 0;
-        }
-      } else if ((int64_t)cum <= a.keep && (int64_t)(cum + mass) > a.keep) {
-        // this thread's range holds the crossing
-        for (int j = 0; j < SMP_KPT; ++j) {
-          if (!cnt[j]) continue;
-          const uint64_t pj = p62(j);
-          const uint64_t end = cum + (uint64_t)cnt[j] * pj;
-          if ((int64_t)end > a.keep) {
-            const int64_t kt =
-                (int64_t)min((uint64_t)cnt[j], ((uint64_t)a.keep - cum) / pj);
-            s_cut[0] = b0 + j;
-            s_cut[1] = (b0 + j == 0 && kt == 0) ? 1 : kt;
-            s_cut[2] = above;
+        if (hits & (1u << i)) {
+          if (left == 0) {
+            s_token = 8 * (int64_t)g + i;
             break;
           }
-          cum = end;
-          above += cnt[j];
+          --left;
         }
-      }
     }
+    if (tid == SMP_T - 1) s_round = ex + mine;  // tokens of the value in this round
     __syncthreads();
-    const uint32_t gcut = (uint32_t)s_cut[0];
-    const int64_t kties = s_cut[1];
-    nkept = gcut < (uint32_t)SMP_KEYS ? s_cut[2] + kties : a.V;
-
-    // Z' over the kept tokens, their bf16 probabilities q and total W
-    auto kept_n = [&](int j) -> uint64_t {
-      const uint32_t bin = b0 + j;
-      return bin < gcut ? cnt[j] : (bin == gcut ? (uint64_t)kties : 0);
-    };
-    uint64_t zk = 0;
-#pragma unroll
-    for (int j = 0; j < SMP_KPT; ++j) {
-      const uint64_t n = kept_n(j);
-      if (n) zk += n * to_fixed(__uint_as_float(hist[b0 + j]), 17592186044416.0f);
-      if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-    }
-    const float zkf = (float)block_sum(zk, s64) * 5.684341886080802e-14f;
-    uint64_t w = 0;
-#pragma unroll
-    for (int j = 0; j < SMP_KPT; ++j) {
-      const uint32_t bin = b0 + j;
-      const uint16_t qb =
-          (bin <= gcut && cnt[j]) ? f2bf(__uint_as_float(hist[bin]) / zkf) : (uint16_t)0;
-      const uint64_t q62 = to_fixed(bf2f(qb), 4611686018427387904.0f);
-      w += kept_n(j) * q62;
-      hist[bin] = qb;
-      if (bin == gcut) s_cut[3] = (int64_t)q62;
-      if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
-    }
-    const uint64_t W = block_sum(w, s64);  // (its barriers publish hist and s_cut[3])
-    const uint64_t qcut = gcut < (uint32_t)SMP_KEYS ? (uint64_t)s_cut[3] : 0;
-
-    // 4. draw
-    uint64_t r;
-    if (a.draws) {
-      r = a.draws[m];
-    } else {
-      const uint32_t step = bookkeeping ? (uint32_t)a.count[m] : 0u;
-      r = splitmix64(a.seed + splitmix64(((uint64_t)(uint32_t)m << 32) | step));
-    }
-    const uint64_t t = __umul64hi(r, W);
-    const int GW = (G + SMP_W - 1) / SMP_W;  // groups per wave slice
-    const int g0 = min(G, wave * GW), g1 = min(G, g0 + GW);
-    const int R = (g1 - g0 + 63) / 64;      // rounds of 64 groups in this slice
-    // per round: kept mass outside the cut bin, and tokens in the cut bin
-    auto group_q = [&](const uint4& v, uint64_t& km, uint32_t& tc) {
-      uint32_t k[8];
-      keys_of(v, inv_t, k);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t bin = kmax - k[i];
-        if (bin == gcut) {
-          ++tc;
-        } else if (bin < (uint32_t)SMP_KEYS) {
-          km += to_fixed(bf2f((uint16_t)hist[bin]), 4611686018427387904.0f);
-        }
-      }
-    };
-    uint64_t wkm = 0;
-    uint32_t wtc = 0;
-    for (int rb = 0; rb < R; rb += SMP_U) {
-      uint4 v[SMP_U];
-#pragma unroll
-      for (int u = 0; u < SMP_U; ++u)
-        v[u] = *reinterpret_cast<const uint4*>(
-            row + 8 * (int64_t)min(g0 + (rb + u) * 64 + lane, G - 1));
-#pragma unroll
-      for (int u = 0; u < SMP_U; ++u) {
-        if (rb + u >= R) break;  // wave-uniform
-        uint64_t km = 0;
-        uint32_t tc = 0;
-        if (g0 + (rb + u) * 64 + lane < g1) group_q(v[u], km, tc);
-        km = wave_sum(km);
-        tc = wave_sum(tc);
-        if (lane == 0) {
-          rmass[wave][rb + u] = km;
-          rties[wave][rb + u] = tc;
-        }
-        wkm += km;
-        wtc += tc;
-      }
-    }
-    if (lane == 0) {
-      wmass[wave] = wkm;
-      wties[wave] = wtc;
-    }
+    const int64_t found = s_token;
+    rank -= (int64_t)s_round;
     __syncthreads();
-    // the wave whose slice holds t (each thread finds it from the 16 totals)
-    uint64_t base = 0;
-    int64_t ties_before = 0;
-    int hold = SMP_W - 1;
-    for (int v = 0; v < SMP_W; ++v) {
-      const int64_t kt = min((int64_t)wties[v], max((int64_t)0, kties - ties_before));
-      const uint64_t kmv = wmass[v] + (uint64_t)kt * qcut;
-      if (t < base + kmv) {
-        hold = v;
-        break;
-      }
-      base += kmv;
-      ties_before += wties[v];
-    }
-    if (wave == hold) {
-      // the round holding t: lane l looks at round l of the slice
-      const uint64_t rm = lane < R ? rmass[wave][lane] : 0;
-      const uint32_t rt = lane < R ? rties[wave][lane] : 0;
-      uint32_t it = rt;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t x = __shfl_up(it, o);
-        if (lane >= o) it += x;
-      }
-      const int64_t tb_round = ties_before + (it - rt);  // cut ties before this round
-      const int64_t kt = min((int64_t)rt, max((int64_t)0, kties - tb_round));
-      const uint64_t rk = rm + (uint64_t)kt * qcut;
-      uint64_t im = rk;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint64_t x = __shfl_up(im, o);
-        if (lane >= o) im += x;
-      }
-      const uint64_t hitr = __ballot(lane < R && base + im > t);
-      const int rsel = hitr ? __ffsll((unsigned long long)hitr) - 1 : R - 1;
-      const uint64_t rbase = base + __shfl(im - rk, rsel);
-      const int64_t rties0 = __shfl(tb_round, rsel);
-      // that round: one group per lane
-      const int g = g0 + rsel * 64 + lane;
-      const bool valid = g < g1;
-      const uint4 v = *reinterpret_cast<const uint4*>(row + 8 * (int64_t)min(g, G - 1));
-      uint32_t k[8];
-      keys_of(v, inv_t, k);
-      uint32_t lt = 0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) lt += (valid && kmax - k[i] == gcut) ? 1u : 0u;
-      uint32_t il = lt;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint32_t x = __shfl_up(il, o);
-        if (lane >= o) il += x;
-      }
-      int64_t rank = rties0 + (il - lt);  // tie rank of this lane's first cut-bin token
-      uint64_t wq[8];
-      uint64_t lm = 0;
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const uint32_t bin = kmax - k[i];
-        uint64_t q = 0;
-        if (valid) {
-          if (bin == gcut) {
-            q = rank < kties ? qcut : 0;
-            ++rank;
-          } else if (bin < (uint32_t)SMP_KEYS) {
-            q = to_fixed(bf2f((uint16_t)hist[bin]), 4611686018427387904.0f);
-          }
-        }
-        wq[i] = q;
-        lm += q;
-      }
-      uint64_t ig = lm;
-#pragma unroll
-      for (int o = 1; o < 64; o <<= 1) {
-        const uint64_t x = __shfl_up(ig, o);
-        if (lane >= o) ig += x;
-      }
-      const uint64_t hit = __ballot(valid && rbase + ig > t);
-      if (hit && lane == __ffsll((unsigned long long)hit) - 1) {
-        uint64_t acc = rbase + ig - lm;
-        int64_t tok = 8 * (int64_t)g + 7;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          if (acc + wq[i] > t) {
-            tok = 8 * (int64_t)g + i;
-            break;
-          }
-          acc += wq[i];
-        }
-        s_token = tok;
-      }
-    }
-    __syncthreads();
-    token = s_token;
-    if (token < 0 || token >= a.V) token = 0;  // unreachable: t < W always lands
+    if (found >= 0) break;
   }
+  int64_t token = s_token;
+  if (token < 0 || token >= a.V) token = 0;  // unreachable: the rank lies in the row
   if (tid == 0) {
     if (a.out_tokens) a.out_tokens[m] = token;
-    if (a.out_kept) a.out_kept[m] = (int32_t)nkept;
-    if (bookkeeping)
+    if (a.out_kept) a.out_kept[m] = (int32_t)ws.nkept;
+    if (a.tokens)
       advance_row(m, token, a.tokens, a.pos, a.count, a.limit, a.active, a.eos, a.generated,
                   a.gen_ld, a.append_pos, a.attn_len);
   }
@@ -553,27 +563,42 @@ int64_t keep_bound(double top_p) {
   return (b & 1u) ? bound - 1 : bound;
 }
 
-int launch(const SampleArgs& a, grpo_stream_t stream) {
-  static const int rc = hip_check(
-      hipFuncSetAttribute(reinterpret_cast<const void*>(sample_top_p_kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)SMP_LDS),
-      "hipFuncSetAttribute");
+template <typename K>
+int allow_lds(K kernel) {
+  return hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)SMP_LDS),
+                   "hipFuncSetAttribute");
+}
+
+int launch(SampleArgs a, grpo_stream_t stream) {
+  static const int rc = allow_lds(smp_hist_kernel) ? 1 : allow_lds(smp_scan_kernel);
   if (rc) return rc;
-  sample_top_p_kernel<<<dim3(a.M), SMP_T, SMP_LDS, as_stream(stream)>>>(a);
+  const int G = a.V / 8;
+  a.S = max(1, min(SMP_SMAX, 256 / a.M));
+  a.SG = (G + a.S - 1) / a.S;
+  hipStream_t st = as_stream(stream);
+  const dim3 slices((unsigned)a.S, (unsigned)a.M);
+  smp_max_kernel<<<slices, SMP_T1, 0, st>>>(a);
+  smp_hist_kernel<<<slices, SMP_TH, SMP_LDS, st>>>(a);
+  smp_scan_kernel<<<dim3(a.M), SMP_T, SMP_LDS, st>>>(a);
+  smp_count_kernel<<<slices, SMP_T1, 0, st>>>(a);
+  smp_pick_kernel<<<dim3(a.M), SMP_T, 0, st>>>(a);
   return launch_check("sample_top_p");
 }
 
-int check_common(const void* logits, int64_t ld, int M, int V, float temperature) {
+int check_common(const void* logits, int64_t ld, int M, int V, float temperature,
+                 const void* workspace, size_t workspace_bytes) {
   if (M <= 0 || V <= 0) return einval("bad sampling dimensions");
   if (V % 8 || ld % 8 || ld < V) return einval("sampling needs V % 8 == 0 and ld % 8 == 0, ld >= V");
-  if (V > SMP_W * SMP_RMAX * 64 * 8) return einval("sampling supports V <= 524288");
   if (!logits || !aligned16(logits)) return einval("logits must be 16-byte aligned");
   if (!(temperature > 0.0f)) return einval("temperature must be > 0 (greedy decoding otherwise)");
+  if (!workspace || !aligned16(workspace)) return einval("workspace must be 16-byte aligned");
+  if (workspace_bytes < (size_t)M * sizeof(RowWs)) return einval("sampling workspace too small");
   return GRPO_OK;
 }
 
 SampleArgs make_args(const void* logits, int64_t ld, int M, int V, float temperature,
-                     double top_p) {
+                     double top_p, void* workspace) {
   SampleArgs a = {};
   a.logits = static_cast<const uint16_t*>(logits);
   a.ld = ld;
@@ -582,6 +607,7 @@ SampleArgs make_args(const void* logits, int64_t ld, int M, int V, float tempera
   a.inv_t = 1.0f / fmaxf(temperature, 1e-6f);
   a.nofilter = top_p >= 1.0 ? 1 : 0;
   a.keep = a.nofilter ? INT64_MAX : keep_bound(top_p);
+  a.ws = static_cast<RowWs*>(workspace);
   return a;
 }
 
@@ -590,12 +616,19 @@ SampleArgs make_args(const void* logits, int64_t ld, int M, int V, float tempera
 
 using namespace grpo;
 
+extern "C" size_t grpo_sample_workspace_bytes(int M, int V) {
+  if (M <= 0 || V <= 0) return 0;
+  return (size_t)M * sizeof(RowWs);
+}
+
 extern "C" int grpo_sample_top_p(const void* logits, int64_t ld_logits, int M, int V,
                                  float temperature, double top_p, const uint64_t* draws,
-                                 int64_t* tokens_out, int32_t* kept_out, grpo_stream_t stream) {
-  if (int rc = check_common(logits, ld_logits, M, V, temperature)) return rc;
+                                 int64_t* tokens_out, int32_t* kept_out, void* workspace,
+                                 size_t workspace_bytes, grpo_stream_t stream) {
+  if (int rc = check_common(logits, ld_logits, M, V, temperature, workspace, workspace_bytes))
+    return rc;
   if (!draws || !tokens_out) return einval("null draws or tokens");
-  SampleArgs a = make_args(logits, ld_logits, M, V, temperature, top_p);
+  SampleArgs a = make_args(logits, ld_logits, M, V, temperature, top_p, workspace);
   a.draws = draws;
   a.out_tokens = tokens_out;
   a.out_kept = kept_out;
@@ -607,12 +640,14 @@ extern "C" int grpo_sample_advance(const void* logits, int64_t ld_logits, int M,
                                    int64_t* next_tokens, int64_t* tokens, int32_t* pos,
                                    int32_t* count, const int32_t* limit, uint8_t* active,
                                    const int64_t* eos, int64_t* generated, int64_t gen_ld,
-                                   int32_t* append_pos, int32_t* attn_len, grpo_stream_t stream) {
-  if (int rc = check_common(logits, ld_logits, M, V, temperature)) return rc;
+                                   int32_t* append_pos, int32_t* attn_len, void* workspace,
+                                   size_t workspace_bytes, grpo_stream_t stream) {
+  if (int rc = check_common(logits, ld_logits, M, V, temperature, workspace, workspace_bytes))
+    return rc;
   if (!tokens || !pos || !count || !limit || !active || !eos || !append_pos || !attn_len)
     return einval("null row state");
   if (generated && gen_ld <= 0) return einval("gen_ld must be > 0");
-  SampleArgs a = make_args(logits, ld_logits, M, V, temperature, top_p);
+  SampleArgs a = make_args(logits, ld_logits, M, V, temperature, top_p, workspace);
   a.seed = seed;
   a.out_tokens = next_tokens;
   a.tokens = tokens;

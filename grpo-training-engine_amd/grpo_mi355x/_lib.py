@@ -91,12 +91,13 @@ SIGNATURES = {
         _I32,
         [_VP, _I32, _I32, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _VP, _I64, _VP, _VP, _VP],
     ),
+    "grpo_sample_workspace_bytes": (_SZ, [_I32, _I32]),
     "grpo_sample_top_p": (
-        _I32, [_VP, _I64, _I32, _I32, _F32, _c.c_double, _VP, _VP, _VP, _VP]),
+        _I32, [_VP, _I64, _I32, _I32, _F32, _c.c_double, _VP, _VP, _VP, _VP, _SZ, _VP]),
     "grpo_sample_advance": (
         _I32,
         [_VP, _I64, _I32, _I32, _F32, _c.c_double, _c.c_uint64, _VP, _VP, _VP, _VP, _VP, _VP,
-         _VP, _VP, _I64, _VP, _VP, _VP],
+         _VP, _VP, _I64, _VP, _VP, _VP, _SZ, _VP],
     ),
     "grpo_paged_kv_append": (
         _I32,

@@ -183,6 +183,11 @@ class DecodeEngine:
         self.lm_fused = (self.V % 16 == 0 and H % 256 == 0 and B <= 64
                          and B * (H + 8) * 2 <= 160 * 1024)
         self.ws_lm = torch.empty(max(lm_bytes, 16), dtype=torch.uint8, device=dev)
+        # the sampler's workspace starts zero-filled and every call leaves it so
+        self.ws_smp = None
+        if self.sampling:
+            self.ws_smp = torch.zeros(int(self.lib.grpo_sample_workspace_bytes(B, self.V)),
+                                      dtype=torch.uint8, device=dev)
         # MLP: gate|up and SiLU*up in one kernel that writes the bf16 input of
         # down_proj, when the shape allows; else down_proj stages SiLU(gate)*up
         # from the gate|up partial sums (at most 2 K slices), else a SiLU*mul
@@ -289,7 +294,8 @@ class DecodeEngine:
                 self.count.data_ptr(), self.limit.data_ptr(), self.active.data_ptr(),
                 self.eos.data_ptr(), None if gen is None else gen.data_ptr(),
                 0 if gen is None else gen.shape[1], self.append_pos.data_ptr(),
-                self.attn_len.data_ptr(), st), "sample")))
+                self.attn_len.data_ptr(), self.ws_smp.data_ptr(), self.ws_smp.numel(), st),
+                "sample")))
         elif self.lm_fused:
             gen = self.generated
             logits = self.logits.data_ptr() if self.keep_logits else None

@@ -327,21 +327,28 @@ int grpo_decode_advance(const void* lm_workspace, int M, int V, int64_t* next_to
 int grpo_argmax_bf16(const void* logits, int64_t ld, int V, int M, int64_t* out,
                      grpo_stream_t stream);
 
+/* Workspace bytes of grpo_sample_top_p / grpo_sample_advance for M rows: per
+ * row, the counts of the row's distinct values and the draw's intermediate
+ * results.  It must be zero-filled once before its first use; every call
+ * leaves it zero-filled again (no memset between calls, so the calls can be
+ * captured into a HIP graph).  Calls that share a workspace must be ordered
+ * on one stream. */
+size_t grpo_sample_workspace_bytes(int M, int V);
+
 /* One sampled token per row from bf16 logits [M, V] (row stride ld_logits),
  * the reference's temperature / top-p rule (fused_logits_sampling,
  * fused_ops.py:236-248; _sample_tokens, paged_kv.py:437-450): scaled =
  * bf16(logits * (1 / max(T, 1e-6))); probabilities bf16(softmax(scaled)) in
  * descending order (ties by index); a token is kept while bf16(running sum) <=
- * bf16(top_p), the first always; top_p >= 1 keeps all.  The draw is the inverse
- * CDF, in index order, of the kept tokens' bf16(softmax) at t = floor(draws[m]
- * * W / 2^64), W their total in 2^-62 units.  tokens_out[m] = the token,
- * kept_out[m] (may be NULL) = the number of kept tokens.  No sort, no
- * workspace, no memset: safe inside a captured HIP graph.  Needs temperature >
- * 0 (greedy decoding otherwise), V % 8 == 0, ld_logits % 8 == 0 and 16-byte
- * aligned logits. */
+ * bf16(top_p), the first always; top_p >= 1 keeps all.  The draw is the
+ * inverse CDF of the kept tokens' bf16(softmax), taken in that sorted order, at
+ * t = floor(draws[m] * W / 2^64), W their total in 2^-62 units.  tokens_out[m]
+ * = the token, kept_out[m] (may be NULL) = the number of kept tokens.  No sort
+ * and no memset.  Needs temperature > 0 (greedy decoding otherwise), V % 8 ==
+ * 0, ld_logits % 8 == 0, 16-byte aligned logits and workspace. */
 int grpo_sample_top_p(const void* logits, int64_t ld_logits, int M, int V, float temperature,
                       double top_p, const uint64_t* draws, int64_t* tokens_out, int32_t* kept_out,
-                      grpo_stream_t stream);
+                      void* workspace, size_t workspace_bytes, grpo_stream_t stream);
 
 /* grpo_sample_top_p with the decode loop's bookkeeping of grpo_decode_advance
  * (paged_kv.py:800-820, :938, :978): row m's draw is SplitMix64 of (seed, m,
@@ -351,7 +358,8 @@ int grpo_sample_advance(const void* logits, int64_t ld_logits, int M, int V, flo
                         double top_p, uint64_t seed, int64_t* next_tokens, int64_t* tokens,
                         int32_t* pos, int32_t* count, const int32_t* limit, uint8_t* active,
                         const int64_t* eos, int64_t* generated, int64_t gen_ld,
-                        int32_t* append_pos, int32_t* attn_len, grpo_stream_t stream);
+                        int32_t* append_pos, int32_t* attn_len, void* workspace,
+                        size_t workspace_bytes, grpo_stream_t stream);
 
 #ifdef __cplusplus
 }

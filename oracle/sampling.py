@@ -29,10 +29,11 @@ bit for bit:
   the rule;
 * ties in the sort are ordered by index (a stable sort), which decides which of
   several equal logits at the cut are kept;
-* the draw is the inverse CDF, in index order, of the kept bf16 probabilities at
-  a 64-bit uniform ``r``: ``t = floor(r * W / 2^64)`` with ``W`` their 2^-62
-  fixed-point total; torch's ``multinomial`` picks ``argmax(p / E)`` with
-  ``E ~ Exp(1)``, the same distribution.
+* the draw is the inverse CDF of the kept bf16 probabilities, taken in sorted
+  order (value descending, index ascending), at a 64-bit uniform ``r``:
+  ``t = floor(r * W / 2^64)`` with ``W`` their 2^-62 fixed-point total; torch's
+  ``multinomial`` picks ``argmax(p / E)`` with ``E ~ Exp(1)``, the same
+  distribution.
 
 Pins (tests/test_oracle_sampling.py): the kept set against torch's CPU ops
 (sort, softmax, cumsum, compare) on the same bf16 logits, a known-answer case,
@@ -158,11 +159,11 @@ def sample_row(logit_bits, temperature: float, top_p: float, draw: int):
     W = sum(q62)
     t = (int(draw) * W) >> 64
     acc = 0
-    for i in range(V):
+    for i in order:  # the kept tokens in sorted order (others have q = 0)
         acc += q62[i]
         if acc > t:
-            return i, nkept
-    return V - 1, nkept
+            return int(i), nkept
+    return int(order[0]), nkept
 
 
 def sample_rows(logit_bits, temperature: float, top_p: float, draws):

@@ -53,11 +53,19 @@ def _run(dev, bits, T, top_p, draws):
     dr = torch.from_numpy(draws.view(np.int64)).to(dev)
     tok = torch.full((M,), -7, dtype=torch.int64, device=dev)
     kept = torch.full((M,), -7, dtype=torch.int32, device=dev)
+    ws = _workspace(dev, lib, M, V)
     print(f"sample_top_p M={M} V={V} T={T} top_p={top_p}", flush=True)
     _lib.check(lib.grpo_sample_top_p(lg.data_ptr(), V, M, V, T, top_p, dr.data_ptr(),
-                                     tok.data_ptr(), kept.data_ptr(), st), "sample_top_p")
+                                     tok.data_ptr(), kept.data_ptr(), ws.data_ptr(), ws.numel(),
+                                     st), "sample_top_p")
     torch.cuda.synchronize()
+    # every call leaves the workspace zero-filled for the next one (bins cleared)
+    assert not torch.any(ws.view(M, -1)[:, 288:]), "sampling bins not cleared"
     return tok.cpu().numpy(), kept.cpu().numpy()
+
+
+def _workspace(dev, lib, M, V):
+    return torch.zeros(int(lib.grpo_sample_workspace_bytes(M, V)), dtype=torch.uint8, device=dev)
 
 
 @pytest.mark.parametrize("kind,M,V,T,top_p", [
@@ -135,12 +143,13 @@ def test_sample_advance_bookkeeping_and_draw_stream(dev):
     draws = np.array([S.step_draw(seed, m, int(c0[m])) for m in range(M)], dtype=np.uint64)
     want_tok, _ = S.sample_rows(bits, 0.7, 0.9, draws)
     eos = torch.tensor([int(want_tok[4])], dtype=torch.int64, device=dev)
+    ws = _workspace(dev, lib, M, V)
     print("sample_advance M=6 V=151936", flush=True)
     _lib.check(lib.grpo_sample_advance(lg.data_ptr(), V, M, V, 0.7, 0.9, seed, nxt.data_ptr(),
                                        tokens.data_ptr(), pos.data_ptr(), count.data_ptr(),
                                        limit.data_ptr(), active.data_ptr(), eos.data_ptr(),
-                                       gen.data_ptr(), 8, app.data_ptr(), alen.data_ptr(), st),
-               "sample_advance")
+                                       gen.data_ptr(), 8, app.data_ptr(), alen.data_ptr(),
+                                       ws.data_ptr(), ws.numel(), st), "sample_advance")
     torch.cuda.synchronize()
     was = [1, 1, 0, 1, 1, 1]
     for m in range(M):
