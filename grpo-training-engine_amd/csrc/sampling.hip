@@ -12,11 +12,11 @@
 //   K0 smp_max     (slice, row): the slice's maximum scaled value
 //                  (scaled = bf16(logit * (1/T)), as order-preserving 16-bit
 //                  keys of the bf16 bit patterns).
-//   K1 smp_hist    (slice, row): counts per distinct value within 86 of the row
+//   K1 smp_hist    (slice, row; coarser slices): counts per distinct value within 86 of the row
 //                  maximum m in LDS (bin = key(m) - key; at most 33906 values;
 //                  tokens further down have exp(s - m) < 2^-124, probability 0
 //                  in bf16), added into the row's bins in the workspace.
-//   K2 smp_scan    (row): reads and clears the row's bins.  Per bin: e =
+//   K2 smp_scan    (row): takes the row's bins into LDS (clearing them).  Per bin: e =
 //                  exp(v - m); Z = sum count * e (exact fixed point); p =
 //                  bf16(e / Z); the exact running sum of p (2^-62 units) in
 //                  descending order locates the cut: the bin where the sum
@@ -72,7 +72,8 @@ struct SampleArgs {
   const uint16_t* logits;
   int64_t ld;
   int M, V;
-  int S, SG;         // slices per row, 8-token groups per slice
+  int S, SG;         // slices per row, 8-token groups per slice (K0, K3)
+  int SH, SGH;       // the same for the histogram kernel K1
   float inv_t;       // float32(1 / max(T, 1e-6))
   int nofilter;      // top_p >= 1: no cut
   int64_t keep;      // keep a token while the running sum (2^-62 units) <= keep
@@ -268,10 +269,15 @@ __global__ void __launch_bounds__(SMP_TH) smp_hist_kernel(SampleArgs a) {
   const uint32_t kmax = row_max_key(a, w);
   const float mf = bf2f((uint16_t)key_bits(kmax));
   if (!isfinite(mf)) return;  // no distribution: K2 picks the first maximum
-  for (int i = tid; i < SMP_KEYS; i += SMP_TH) hist[i] = 0;
+  {
+    uint4* h4 = reinterpret_cast<uint4*>(hist);
+#pragma unroll
+    for (int k = 0; k < (SMP_KEYS / 4 + SMP_TH - 1) / SMP_TH; ++k)
+      if (tid + k * SMP_TH < SMP_KEYS / 4) h4[tid + k * SMP_TH] = make_uint4(0, 0, 0, 0);
+  }
   __syncthreads();
   const uint16_t* row = a.logits + (int64_t)m * a.ld;
-  const int G = a.V >> 3, g0 = min(G, s * a.SG), g1 = min(G, g0 + a.SG);
+  const int G = a.V >> 3, g0 = min(G, s * a.SGH), g1 = min(G, g0 + a.SGH);
   const float inv_t = a.inv_t;
   for_groups(row, g1, g0 + tid, SMP_TH, [&](int, const uint4& v) {
     uint32_t k[8];
@@ -283,19 +289,59 @@ __global__ void __launch_bounds__(SMP_TH) smp_hist_kernel(SampleArgs a) {
     }
   });
   __syncthreads();
-  for (int i = tid; i < SMP_KEYS; i += SMP_TH) {
-    const uint32_t c = hist[i];
-    if (c) atomicAdd(&w.bins[i], c);
+  {
+    const uint4* h4 = reinterpret_cast<const uint4*>(hist);
+#pragma unroll 4
+    for (int k = 0; k < (SMP_KEYS / 4 + SMP_TH - 1) / SMP_TH; ++k) {
+      const int i4 = tid + k * SMP_TH;
+      if (i4 >= SMP_KEYS / 4) break;
+      const uint4 c = h4[i4];
+      if (c.x) atomicAdd(&w.bins[4 * i4], c.x);
+      if (c.y) atomicAdd(&w.bins[4 * i4 + 1], c.y);
+      if (c.z) atomicAdd(&w.bins[4 * i4 + 2], c.z);
+      if (c.w) atomicAdd(&w.bins[4 * i4 + 3], c.w);
+    }
   }
 }
 
+// The row's counts from the workspace into LDS (16-byte loads, all issued
+// before the stores), the workspace copy cleared for the next call, then a
+// barrier.
+__device__ __forceinline__ void take_counts(uint32_t* bins, uint32_t* lds) {
+  constexpr int N4 = SMP_KEYS / 4, PER = (N4 + SMP_T - 1) / SMP_T;
+  uint4* src = reinterpret_cast<uint4*>(bins);
+  uint4* dst = reinterpret_cast<uint4*>(lds);
+  uint4 v[PER];
+#pragma unroll
+  for (int k = 0; k < PER; ++k) v[k] = src[min((int)threadIdx.x + k * SMP_T, N4 - 1)];
+#pragma unroll
+  for (int k = 0; k < PER; ++k)
+    if ((int)threadIdx.x + k * SMP_T < N4) {
+      dst[threadIdx.x + k * SMP_T] = v[k];
+      src[threadIdx.x + k * SMP_T] = make_uint4(0, 0, 0, 0);
+    }
+  __syncthreads();
+}
+
+// LDS word of a bin: count in bits 0..17 (V < 2^18), and a probability in
+// [0, 1] as bf16 bits (at most 0x3F80, 14 bits) in bits 18..31.
+constexpr uint32_t CNT_MASK = (1u << 18) - 1;
+__device__ __forceinline__ uint32_t cnt_of(uint32_t w) { return w & CNT_MASK; }
+__device__ __forceinline__ uint64_t prob62(uint32_t w) {
+  return to_fixed(bf2f((uint16_t)(w >> 18)), TWO62);
+}
+
 // K2: the row's bin scan: cut, kept probabilities, draw (value and rank).
+// The per-bin arithmetic (exp, divisions) runs in balanced passes, thread t
+// taking bins t, t + 1024, ... (the populated bins cluster near the top of the
+// window); the ordered prefixes run over contiguous ranges, thread t taking
+// bins [34t, 34t + 34).  Everything after the first read lives in LDS.
 __global__ void __launch_bounds__(SMP_T) smp_scan_kernel(SampleArgs a) {
   touch_kernargs<sizeof(SampleArgs)>();
-  extern __shared__ uint32_t hist[];  // [SMP_KEYS]: counts, then e (float), then kept q (bf16)
+  extern __shared__ uint32_t lds[];  // [SMP_KEYS] packed (count, p or q) words
   __shared__ uint64_t s64[SMP_T / 64];
   __shared__ uint32_t s32[SMP_T / 64];
-  __shared__ int64_t s_cut[4];  // cut bin, its tied tokens kept, tokens above it
+  __shared__ int64_t s_cut[3];  // cut bin, its tied tokens kept, tokens above it
   __shared__ int64_t s_sel[2];  // drawn bin, rank within it
   __shared__ uint64_t s_w;
   const int tid = threadIdx.x;
@@ -312,14 +358,6 @@ __global__ void __launch_bounds__(SMP_T) smp_scan_kernel(SampleArgs a) {
     }
     return;
   }
-  {
-    uint4* src = reinterpret_cast<uint4*>(ws.bins);
-    uint4* dst = reinterpret_cast<uint4*>(hist);
-    for (int i = tid; i < SMP_KEYS / 4; i += SMP_T) {
-      dst[i] = src[i];
-      src[i] = make_uint4(0, 0, 0, 0);  // zero for the next call
-    }
-  }
   if (tid == 0) {
     s_cut[0] = SMP_KEYS;
     s_cut[1] = 0;
@@ -327,64 +365,78 @@ __global__ void __launch_bounds__(SMP_T) smp_scan_kernel(SampleArgs a) {
     s_sel[0] = 0;
     s_sel[1] = 0;
   }
-  __syncthreads();
+  take_counts(ws.bins, lds);
+  // e of a bin.  Each pass takes its own opaque copy of (kmax, m): otherwise
+  // the compiler keeps every bin's exponent argument live from pass to pass.
+  uint32_t km = kmax;
+  float mfv = mf;
+  auto fresh = [&]() { asm volatile("" : "+s"(km), "+s"(mfv)); };
+  auto e_of = [&](int bin) {
+    return exp_nonpos(bf2f((uint16_t)key_bits(km - (uint32_t)bin)) - mfv);
+  };
 
-  // Thread t holds bins [t*KPT, (t+1)*KPT) (descending values).  Counts move
-  // to registers; each non-empty bin's e is computed once and parked in its
-  // LDS slot.
-  const int b0 = tid * SMP_KPT;
-  uint32_t cnt[SMP_KPT];
-#pragma unroll
-  for (int j = 0; j < SMP_KPT; ++j) cnt[j] = hist[b0 + j];
+  // A (balanced): Z = sum count * e over the bins (2^-44 units)
   uint64_t z = 0;
+  fresh();
 #pragma unroll
   for (int j = 0; j < SMP_KPT; ++j) {
-    float e = 0.0f;
-    if (cnt[j]) {
-      e = exp_nonpos(bf2f((uint16_t)key_bits(kmax - (uint32_t)(b0 + j))) - mf);
-      z += (uint64_t)cnt[j] * to_fixed(e, TWO44);
-    }
-    hist[b0 + j] = __float_as_uint(e);
+    const int bin = tid + j * SMP_T;
+    const uint32_t c = lds[bin];
+    if (c) z += (uint64_t)c * to_fixed(e_of(bin), TWO44);
+    if (j & 1) __builtin_amdgcn_sched_barrier(0);  // two exp chains at a time
   }
   const float zf = (float)block_sum<SMP_T / 64>(z, s64) * TWO_M44;
-  // p = bf16(e / Z) in 2^-62 units
-  auto p62 = [&](int j) {
-    return to_fixed(bf2f(f2bf(__uint_as_float(hist[b0 + j]) / zf)), TWO62);
-  };
-  uint64_t mass = 0;
-  uint32_t ntok = 0;
+  // B (balanced): p = bf16(e / Z) packed beside the count
+  fresh();
 #pragma unroll
   for (int j = 0; j < SMP_KPT; ++j) {
-    if (cnt[j]) mass += (uint64_t)cnt[j] * p62(j);
-    ntok += cnt[j];
+    const int bin = tid + j * SMP_T;
+    const uint32_t c = lds[bin];
+    if (c) lds[bin] = c | ((uint32_t)f2bf(e_of(bin) / zf) << 18);
+    if (j & 1) __builtin_amdgcn_sched_barrier(0);
   }
-  uint64_t cum = mass;
-  uint32_t above = ntok;
-  block_excl_scan(cum, above, s64, s32);
-  // The cut: the first bin whose last token's running sum passes the bound,
-  // and how many of its tied tokens stay (the first token always stays).
-  if (!a.nofilter) {
-    if (a.keep < 0) {
-      if (tid == 0) {
-        s_cut[0] = 0;
-        s_cut[1] = 1;
-        s_cut[2] = 0;
-      }
-    } else if ((int64_t)cum <= a.keep && (int64_t)(cum + mass) > a.keep) {
-      // this thread's bins hold the crossing
-      for (int j = 0; j < SMP_KPT; ++j) {
-        if (!cnt[j]) continue;
-        const uint64_t pj = p62(j);
-        const uint64_t end = cum + (uint64_t)cnt[j] * pj;
-        if ((int64_t)end > a.keep) {
-          const int64_t kt = (int64_t)min((uint64_t)cnt[j], ((uint64_t)a.keep - cum) / pj);
-          s_cut[0] = b0 + j;
-          s_cut[1] = (b0 + j == 0 && kt == 0) ? 1 : kt;
-          s_cut[2] = above;
-          break;
+  __syncthreads();
+  // C (contiguous): running sum of p in sorted order; the cut
+  const int b0 = tid * SMP_KPT;
+  {
+    uint64_t mass = 0;
+    uint32_t ntok = 0;
+#pragma unroll
+    for (int j = 0; j < SMP_KPT; ++j) {
+      const uint32_t w = lds[b0 + j];
+      mass += (uint64_t)cnt_of(w) * prob62(w);
+      ntok += cnt_of(w);
+      if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+    }
+    uint64_t cum = mass;
+    uint32_t above = ntok;
+    block_excl_scan(cum, above, s64, s32);
+    // the first bin whose last token's running sum passes the bound, and how
+    // many of its tied tokens stay (the first token always stays)
+    if (!a.nofilter) {
+      if (a.keep < 0) {
+        if (tid == 0) {
+          s_cut[0] = 0;
+          s_cut[1] = 1;
+          s_cut[2] = 0;
         }
-        cum = end;
-        above += cnt[j];
+      } else if ((int64_t)cum <= a.keep && (int64_t)(cum + mass) > a.keep) {
+        for (int j = 0; j < SMP_KPT; ++j) {  // this thread's bins hold the crossing
+          const uint32_t w = lds[b0 + j];
+          const uint32_t cj = cnt_of(w);
+          if (!cj) continue;
+          const uint64_t pj = prob62(w);
+          const uint64_t end = cum + (uint64_t)cj * pj;
+          if ((int64_t)end > a.keep) {
+            const int64_t kt = (int64_t)min((uint64_t)cj, ((uint64_t)a.keep - cum) / pj);
+            s_cut[0] = b0 + j;
+            s_cut[1] = (b0 + j == 0 && kt == 0) ? 1 : kt;
+            s_cut[2] = above;
+            break;
+          }
+          cum = end;
+          above += cj;
+        }
       }
     }
   }
@@ -392,55 +444,69 @@ __global__ void __launch_bounds__(SMP_T) smp_scan_kernel(SampleArgs a) {
   const uint32_t gcut = (uint32_t)s_cut[0];
   const int64_t kties = s_cut[1];
   const int64_t nkept = gcut < (uint32_t)SMP_KEYS ? s_cut[2] + kties : a.V;
-
-  // Z' over the kept tokens, their bf16 probabilities q and total W
-  auto kept_n = [&](int j) -> uint64_t {
-    const uint32_t bin = b0 + j;
-    return bin < gcut ? cnt[j] : (bin == gcut ? (uint64_t)kties : 0);
+  auto kept = [&](uint32_t bin, uint32_t c) -> uint64_t {
+    return bin < gcut ? c : (bin == gcut ? (uint64_t)kties : 0);
   };
+
+  // D (balanced): Z' = sum kept * e
   uint64_t zk = 0;
+  fresh();
 #pragma unroll
   for (int j = 0; j < SMP_KPT; ++j) {
-    const uint64_t n = kept_n(j);
-    if (n) zk += n * to_fixed(__uint_as_float(hist[b0 + j]), TWO44);
+    const int bin = tid + j * SMP_T;
+    const uint64_t n = kept((uint32_t)bin, cnt_of(lds[bin]));
+    if (n) zk += n * to_fixed(e_of(bin), TWO44);
+    if (j & 1) __builtin_amdgcn_sched_barrier(0);
   }
   const float zkf = (float)block_sum<SMP_T / 64>(zk, s64) * TWO_M44;
-  uint64_t w = 0;
+  // E (balanced): q = bf16(e / Z') of the kept bins in place of p (0 elsewhere)
+  fresh();
 #pragma unroll
   for (int j = 0; j < SMP_KPT; ++j) {
-    const uint64_t n = kept_n(j);
-    const uint16_t qb = n ? f2bf(__uint_as_float(hist[b0 + j]) / zkf) : (uint16_t)0;
-    w += n * to_fixed(bf2f(qb), TWO62);
-    hist[b0 + j] = qb;  // this thread's bins only
+    const int bin = tid + j * SMP_T;
+    const uint32_t c = cnt_of(lds[bin]);
+    const uint32_t qb = kept((uint32_t)bin, c) ? f2bf(e_of(bin) / zkf) : 0u;
+    lds[bin] = c | (qb << 18);
+    if (j & 1) __builtin_amdgcn_sched_barrier(0);
   }
-  uint64_t wpre = w;
-  uint32_t unused = 0;
-  block_excl_scan(wpre, unused, s64, s32);
-  if (tid == SMP_T - 1) s_w = wpre + w;  // W: the last thread's inclusive prefix
   __syncthreads();
-  const uint64_t W = s_w;
-
-  // draw: t in [0, W), located among the kept tokens in sorted order
-  uint64_t r;
-  if (a.draws) {
-    r = a.draws[m];
-  } else {
-    const uint32_t step = a.tokens ? (uint32_t)a.count[m] : 0u;
-    r = splitmix64(a.seed + splitmix64(((uint64_t)(uint32_t)m << 32) | step));
-  }
-  const uint64_t t = __umul64hi(r, W);
-  if (t >= wpre && t < wpre + w) {
-    uint64_t c = wpre;
+  // F (contiguous): the kept mass in sorted order, W, and the draw
+  {
+    uint64_t w = 0;
+#pragma unroll
     for (int j = 0; j < SMP_KPT; ++j) {
-      const uint64_t n = kept_n(j);
-      if (!n) continue;
-      const uint64_t q62 = to_fixed(bf2f((uint16_t)hist[b0 + j]), TWO62);
-      if (t < c + n * q62) {  // (then q62 > 0)
-        s_sel[0] = b0 + j;
-        s_sel[1] = (int64_t)((t - c) / q62);
-        break;
+      const uint32_t v = lds[b0 + j];
+      w += kept((uint32_t)(b0 + j), cnt_of(v)) * prob62(v);
+      if ((j & 3) == 3) __builtin_amdgcn_sched_barrier(0);
+    }
+    uint64_t wpre = w;
+    uint32_t unused = 0;
+    block_excl_scan(wpre, unused, s64, s32);
+    if (tid == SMP_T - 1) s_w = wpre + w;  // W: the last thread's inclusive prefix
+    __syncthreads();
+    const uint64_t W = s_w;
+    uint64_t r;
+    if (a.draws) {
+      r = a.draws[m];
+    } else {
+      const uint32_t step = a.tokens ? (uint32_t)a.count[m] : 0u;
+      r = splitmix64(a.seed + splitmix64(((uint64_t)(uint32_t)m << 32) | step));
+    }
+    const uint64_t t = __umul64hi(r, W);
+    if (t >= wpre && t < wpre + w) {  // t lies in this thread's bins
+      uint64_t acc = wpre;
+      for (int j = 0; j < SMP_KPT; ++j) {
+        const uint32_t v = lds[b0 + j];
+        const uint64_t n = kept((uint32_t)(b0 + j), cnt_of(v));
+        if (!n) continue;
+        const uint64_t q62 = prob62(v);
+        if (t < acc + n * q62) {  // (then q62 > 0)
+          s_sel[0] = b0 + j;
+          s_sel[1] = (int64_t)((t - acc) / q62);
+          break;
+        }
+        acc += n * q62;
       }
-      c += n * q62;
     }
   }
   __syncthreads();
@@ -576,10 +642,14 @@ int launch(SampleArgs a, grpo_stream_t stream) {
   const int G = a.V / 8;
   a.S = max(1, min(SMP_SMAX, 256 / a.M));
   a.SG = (G + a.S - 1) / a.S;
+  // fewer, larger histogram slices: each adds its distinct values once into
+  // the row's bins, and a slice's fixed cost is clearing and reading 34816 bins
+  a.SH = max(1, min(SMP_SMAX, 64 / a.M));
+  a.SGH = (G + a.SH - 1) / a.SH;
   hipStream_t st = as_stream(stream);
   const dim3 slices((unsigned)a.S, (unsigned)a.M);
   smp_max_kernel<<<slices, SMP_T1, 0, st>>>(a);
-  smp_hist_kernel<<<slices, SMP_TH, SMP_LDS, st>>>(a);
+  smp_hist_kernel<<<dim3((unsigned)a.SH, (unsigned)a.M), SMP_TH, SMP_LDS, st>>>(a);
   smp_scan_kernel<<<dim3(a.M), SMP_T, SMP_LDS, st>>>(a);
   smp_count_kernel<<<slices, SMP_T1, 0, st>>>(a);
   smp_pick_kernel<<<dim3(a.M), SMP_T, 0, st>>>(a);
@@ -590,6 +660,7 @@ int check_common(const void* logits, int64_t ld, int M, int V, float temperature
                  const void* workspace, size_t workspace_bytes) {
   if (M <= 0 || V <= 0) return einval("bad sampling dimensions");
   if (V % 8 || ld % 8 || ld < V) return einval("sampling needs V % 8 == 0 and ld % 8 == 0, ld >= V");
+  if (V >= (1 << 18)) return einval("sampling supports V < 262144");
   if (!logits || !aligned16(logits)) return einval("logits must be 16-byte aligned");
   if (!(temperature > 0.0f)) return einval("temperature must be > 0 (greedy decoding otherwise)");
   if (!workspace || !aligned16(workspace)) return einval("workspace must be 16-byte aligned");
