@@ -54,6 +54,8 @@ constexpr int SMP_KPT = SMP_KEYS / SMP_T;  // bins per K2 thread
 constexpr size_t SMP_LDS = (size_t)SMP_KEYS * 4;
 constexpr float EXP_MIN_X = -86.0f;
 constexpr int SMP_U = 8;  // 16-byte group loads in flight per thread in the row passes
+constexpr int SMP_CMAX = SMP_KEYS / 2;                // entries of the compacted bins
+constexpr int SMP_EPT = (SMP_CMAX + SMP_T - 1) / SMP_T;  // entries per thread at most
 static_assert(SMP_KEYS % SMP_T == 0 && SMP_KEYS % 4 == 0, "bins must split evenly");
 
 // Per-row workspace.
@@ -370,10 +372,171 @@ __global__ void __launch_bounds__(SMP_T) smp_scan_kernel(SampleArgs a) {
   // the compiler keeps every bin's exponent argument live from pass to pass.
   uint32_t km = kmax;
   float mfv = mf;
-  auto fresh = [&]() { asm volatile("" : "+s"(km), "+s"(mfv)); };
+  auto fresh = [&]() { asm volatile("" : "+v"(km), "+v"(mfv)); };
   auto e_of = [&](int bin) {
     return exp_nonpos(bf2f((uint16_t)key_bits(km - (uint32_t)bin)) - mfv);
   };
+
+  // Compaction: the non-empty bins, in sorted order, as entries (count, bin,
+  // probability) so that every pass below takes ~N/1024 consecutive entries
+  // per thread instead of 34 mostly-empty bins.  Rows with more than
+  // SMP_CMAX distinct values in the window keep the bin-wise passes.
+  {
+    const int c0 = tid * SMP_KPT;
+    uint64_t nzmask = 0;
+#pragma unroll
+    for (int j = 0; j < SMP_KPT; ++j) nzmask |= (uint64_t)(lds[c0 + j] != 0u) << j;
+    const uint64_t mine = (uint64_t)__popcll(nzmask);
+    uint64_t off = mine;
+    uint32_t unused = 0;
+    block_excl_scan(off, unused, s64, s32);
+    if (tid == SMP_T - 1) s_w = off + mine;
+    __syncthreads();
+    const uint32_t N = (uint32_t)s_w;
+    if (N <= (uint32_t)SMP_CMAX) {
+      uint32_t* ccnt = lds;                                         // [SMP_CMAX]
+      uint16_t* cbin = reinterpret_cast<uint16_t*>(lds + SMP_CMAX);  // [SMP_CMAX]
+      uint16_t* cprob = cbin + SMP_CMAX;                             // [SMP_CMAX]
+      {
+        uint32_t c[SMP_KPT];
+#pragma unroll
+        for (int j = 0; j < SMP_KPT; ++j) c[j] = lds[c0 + j];
+        __syncthreads();  // every count is in registers before the entries overwrite them
+        uint32_t k = (uint32_t)off;
+#pragma unroll
+        for (int j = 0; j < SMP_KPT; ++j)
+          if (c[j]) {
+            ccnt[k] = c[j];
+            cbin[k] = (uint16_t)(c0 + j);
+            ++k;
+          }
+      }
+      __syncthreads();
+      const uint32_t ept = (N + SMP_T - 1) / SMP_T;  // entries per thread (<= SMP_EPT)
+      const uint32_t k0 = tid * ept;
+      float ev[SMP_EPT];
+      // A: e per entry, Z
+      fresh();
+      uint64_t zc = 0;
+#pragma unroll
+      for (int i = 0; i < SMP_EPT; ++i) {
+        const uint32_t k = k0 + i;
+        ev[i] = 0.0f;
+        if (i < (int)ept && k < N) {
+          ev[i] = e_of(cbin[k]);
+          zc += (uint64_t)ccnt[k] * to_fixed(ev[i], TWO44);
+        }
+      }
+      const float zcf = (float)block_sum<SMP_T / 64>(zc, s64) * TWO_M44;
+      // B, C: p per entry; running sum in sorted order; the cut (as an entry index)
+      uint64_t mass = 0;
+      uint32_t ntok = 0;
+#pragma unroll
+      for (int i = 0; i < SMP_EPT; ++i) {
+        const uint32_t k = k0 + i;
+        if (i < (int)ept && k < N) {
+          const uint16_t pb = f2bf(ev[i] / zcf);
+          cprob[k] = pb;
+          mass += (uint64_t)ccnt[k] * to_fixed(bf2f(pb), TWO62);
+          ntok += ccnt[k];
+        }
+      }
+      uint64_t cum = mass;
+      uint32_t above = ntok;
+      block_excl_scan(cum, above, s64, s32);
+      if (tid == 0) {
+        s_cut[0] = N;  // no cut: every entry kept
+        s_cut[1] = 0;
+        s_cut[2] = 0;
+      }
+      __syncthreads();
+      if (!a.nofilter) {
+        if (a.keep < 0) {
+          if (tid == 0) {  // entry 0 is bin 0 (the maximum): its first token only
+            s_cut[0] = 0;
+            s_cut[1] = 1;
+            s_cut[2] = 0;
+          }
+        } else if ((int64_t)cum <= a.keep && (int64_t)(cum + mass) > a.keep) {
+          for (uint32_t k = k0; k < min(N, k0 + ept); ++k) {  // this thread holds the crossing
+            const uint32_t ck = ccnt[k];
+            const uint64_t pk = to_fixed(bf2f(cprob[k]), TWO62);
+            const uint64_t end = cum + (uint64_t)ck * pk;
+            if ((int64_t)end > a.keep) {
+              const int64_t kt = (int64_t)min((uint64_t)ck, ((uint64_t)a.keep - cum) / pk);
+              s_cut[0] = k;
+              s_cut[1] = (k == 0 && kt == 0) ? 1 : kt;
+              s_cut[2] = above;
+              break;
+            }
+            cum = end;
+            above += ck;
+          }
+        }
+      }
+      __syncthreads();
+      const uint32_t kc = (uint32_t)s_cut[0];
+      const int64_t kt_c = s_cut[1];
+      const int64_t nk = kc < N ? s_cut[2] + kt_c : a.V;
+      auto kept_e = [&](uint32_t k) -> uint64_t {
+        return k < kc ? ccnt[k] : (k == kc ? (uint64_t)kt_c : 0);
+      };
+      // D: Z' over the kept entries
+      uint64_t zkc = 0;
+#pragma unroll
+      for (int i = 0; i < SMP_EPT; ++i) {
+        const uint32_t k = k0 + i;
+        if (i < (int)ept && k < N) zkc += kept_e(k) * to_fixed(ev[i], TWO44);
+      }
+      const float zkcf = (float)block_sum<SMP_T / 64>(zkc, s64) * TWO_M44;
+      // E, F: q per kept entry; kept mass in sorted order; W; the draw
+      uint64_t w = 0;
+#pragma unroll
+      for (int i = 0; i < SMP_EPT; ++i) {
+        const uint32_t k = k0 + i;
+        if (i < (int)ept && k < N) {
+          const uint64_t n = kept_e(k);
+          const uint16_t qb = n ? f2bf(ev[i] / zkcf) : (uint16_t)0;
+          cprob[k] = qb;
+          w += n * to_fixed(bf2f(qb), TWO62);
+        }
+      }
+      uint64_t wpre = w;
+      block_excl_scan(wpre, unused, s64, s32);
+      if (tid == SMP_T - 1) s_w = wpre + w;
+      __syncthreads();
+      const uint64_t W = s_w;
+      uint64_t r;
+      if (a.draws) {
+        r = a.draws[m];
+      } else {
+        const uint32_t step = a.tokens ? (uint32_t)a.count[m] : 0u;
+        r = splitmix64(a.seed + splitmix64(((uint64_t)(uint32_t)m << 32) | step));
+      }
+      const uint64_t t = __umul64hi(r, W);
+      if (t >= wpre && t < wpre + w) {  // t lies in this thread's entries
+        uint64_t acc = wpre;
+        for (uint32_t k = k0; k < min(N, k0 + ept); ++k) {
+          const uint64_t n = kept_e(k);
+          if (!n) continue;
+          const uint64_t q62 = to_fixed(bf2f(cprob[k]), TWO62);
+          if (t < acc + n * q62) {  // (then q62 > 0)
+            s_sel[0] = cbin[k];
+            s_sel[1] = (int64_t)((t - acc) / q62);
+            break;
+          }
+          acc += n * q62;
+        }
+      }
+      __syncthreads();
+      if (tid == 0) {
+        ws.sel_key = kmax - (uint32_t)s_sel[0];
+        ws.sel_rank = s_sel[1];
+        ws.nkept = nk;
+      }
+      return;
+    }
+  }
 
   // A (balanced): Z = sum count * e over the bins (2^-44 units)
   uint64_t z = 0;

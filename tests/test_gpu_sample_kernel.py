@@ -32,6 +32,9 @@ def _logits(kind, M, V, seed):
         x = np.round(rng.normal(0, 1.0, (M, V)) * 2) / 2
     elif kind == "wide":      # values across zero up to ~40: the full LDS window
         x = rng.uniform(-60.0, 40.0, (M, V))
+    elif kind == "spread":    # +-2^u over 105 binades: > 17408 distinct values in the
+        # window, more than the compacted list holds (the bin-wise passes run)
+        x = rng.choice([-1.0, 1.0], (M, V)) * np.exp2(rng.uniform(-100.0, 5.0, (M, V)))
     else:
         raise ValueError(kind)
     return f32_to_bf16_bits(x.astype(np.float32)).reshape(M, V)
@@ -74,6 +77,8 @@ def _workspace(dev, lib, M, V):
     ("peaked", 8, 151936, 1.0, 0.5),
     ("ties", 8, 151936, 1.0, 0.9),
     ("wide", 4, 151936, 1.0, 0.999),
+    ("spread", 4, 151936, 1.0, 0.9),
+    ("spread", 2, 151936, 0.7, 1.0),
     ("normal", 64, 4096, 1.3, 0.95),
     ("normal", 8, 4096, 0.7, 1.0),
     ("normal", 8, 4096, 0.7, 0.0),
