@@ -1146,7 +1146,30 @@ int make_parts(const grpo_linear_parts_t* h, LinParts* d) {
   return GRPO_OK;
 }
 
+// Float32 absmax of a double-quantized state: one FMA per block, as the
+// reference's kernel computes it (lora_forward.py:187-199: the multiply and
+// add of code2[q] * absmax2 + offset contract into one fused multiply-add).
+__global__ void __launch_bounds__(256) nf4_absmax_expand_kernel(
+    const uint8_t* __restrict__ q, const float* __restrict__ code2,
+    const float* __restrict__ absmax2, int bs2, float offset, int64_t n, float* __restrict__ out) {
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+    out[i] = __fmaf_rn(code2[q[i]], absmax2[i / bs2], offset);
+}
+
 }  // namespace grpo
+
+extern "C" int grpo_nf4_absmax_expand(const uint8_t* absmax_q, const float* code2,
+                                      const float* absmax2, int bs2, float offset,
+                                      int64_t n_blocks, float* out, grpo_stream_t stream) {
+  if (n_blocks < 0) return einval("n_blocks < 0");
+  if (bs2 <= 0) return einval("state2 blocksize must be > 0");
+  if (n_blocks == 0) return GRPO_OK;
+  if (!absmax_q || !code2 || !absmax2 || !out) return einval("null pointer");
+  const int64_t blocks = std::min<int64_t>(cdiv(n_blocks, 256), 8192);
+  nf4_absmax_expand_kernel<<<dim3((unsigned)blocks), 256, 0, as_stream(stream)>>>(
+      absmax_q, code2, absmax2, bs2, offset, n_blocks, out);
+  return launch_check("nf4_absmax_expand");
+}
 
 extern "C" int grpo_nf4_dequant(const uint8_t* w, const float* absmax, const float* code16,
                                 void* out, int64_t numel, int blocksize, grpo_stream_t stream) {

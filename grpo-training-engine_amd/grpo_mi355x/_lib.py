@@ -50,6 +50,7 @@ SIGNATURES = {
     "grpo_init": (_I32, []),
     "grpo_last_error": (_c.c_char_p, []),
     "grpo_nf4_dequant": (_I32, [_VP, _VP, _VP, _VP, _I64, _I32, _VP]),
+    "grpo_nf4_absmax_expand": (_I32, [_VP, _VP, _VP, _I32, _F32, _I64, _VP, _VP]),
     "grpo_nf4_linear_plan": (
         _I32,
         [_I32, _I32, _I32, _I32, _I32, _I32, _c.POINTER(_I32), _c.POINTER(_SZ),

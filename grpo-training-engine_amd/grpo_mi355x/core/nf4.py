@@ -6,7 +6,8 @@ state2}`` (``src/triton_kernels/lora_forward.py:25-32, 527-576``), and from
 ``base_layer``: ``bias``, ``in_features``, ``out_features`` (``src/core/lora.py:84-85``).
 ``Linear4bitNF4`` provides exactly those, so ``ManualLoRALayer`` and
 ``lora_fused_forward`` work unchanged on it.  A real bitsandbytes
-``Linear4bit`` (non-nested state) is accepted by the same code.
+``Linear4bit`` is accepted by the same code, with a plain or a double-quantized
+(nested) state (``float_absmax``).
 
 Storage: ``weight`` is ``uint8 [ceil(N*K/2), 1]`` (bitsandbytes' packed
 shape), element ``e = n*K + k`` in byte ``e // 2``, even ``e`` = high nibble;
@@ -58,6 +59,34 @@ class QuantState:
         if isinstance(self.offset, torch.Tensor):
             self.offset = self.offset.to(device)
         return self
+
+
+def float_absmax(qs) -> torch.Tensor:
+    """The float32 per-block absmax the kernels read.
+
+    A non-nested state's ``absmax`` as is.  A double-quantized state
+    (bitsandbytes ``compress_statistics=True``, the reference's
+    ``bnb_4bit_use_double_quant=True``, ``src/core/model_loader.py:19``) holds
+    uint8 ``absmax`` with ``state2.{code, absmax, blocksize}`` and ``offset``:
+    it is expanded once on the device (``grpo_nf4_absmax_expand``, the
+    reference kernel's ``code2[q] * absmax2 + offset``, ``lora_forward.py:
+    187-199``) and kept on the state, since NF4 base weights are frozen.
+    """
+    if not getattr(qs, "nested", False) and getattr(qs, "state2", None) is None:
+        return qs.absmax
+    cached = getattr(qs, "_grpo_absmax_f32", None)
+    key = (qs.absmax.data_ptr(), qs.absmax.device)
+    if cached is not None and cached[0] == key:
+        return cached[1]
+    from ..kernels.ops import nf4_absmax_expand
+
+    s2 = qs.state2
+    off = qs.offset
+    off = float(off.item()) if isinstance(off, torch.Tensor) else float(off or 0.0)
+    out = nf4_absmax_expand(qs.absmax.reshape(-1), s2.code.float(), s2.absmax.float().reshape(-1),
+                            int(s2.blocksize), off)
+    qs._grpo_absmax_f32 = (key, out)
+    return out
 
 
 def quantize_nf4(weight: torch.Tensor, blocksize: int = 64):
@@ -160,10 +189,8 @@ class Linear4bitNF4(nn.Module):
         from ..kernels.ops import nf4_dequant
 
         qs = self.weight.quant_state
-        if qs.nested:
-            raise ValueError("nested (double-quantized) NF4 states are not supported yet.")
         n = self.out_features * self.in_features
-        w = nf4_dequant(self.weight.data.view(-1), qs.absmax, qs.code, n, qs.blocksize)
+        w = nf4_dequant(self.weight.data.view(-1), float_absmax(qs), qs.code, n, qs.blocksize)
         return w.view(self.out_features, self.in_features)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:

@@ -64,14 +64,17 @@ def _validate_inputs(x: torch.Tensor, weight_4bit: torch.Tensor, quant_state,
 
 
 def _extract_quant_state(weight_4bit: torch.Tensor, quant_state):
-    """``lora_forward.py:527-576`` for the states this kernel decodes."""
-    if bool(getattr(quant_state, "nested", False)):
-        # Double-quantized absmax (lora_forward.py:187-199) is decoded by the
-        # reference kernel; the HIP kernel does not implement it yet.
-        raise ValueError("nested (double-quantized) NF4 quant_state is not supported by the "
-                         "HIP kernel yet.")
+    """``lora_forward.py:527-576``: the float32 absmax, codebook and blocksize.
+
+    A double-quantized (nested) state's absmax is expanded to float32 once
+    (``lora_forward.py:187-199``, see ``core.nf4.float_absmax``) and cached on
+    the state: the base weights are frozen."""
+    from ..core.nf4 import float_absmax
+
     device = weight_4bit.device
-    absmax = quant_state.absmax.to(device=device).contiguous()
+    if bool(getattr(quant_state, "nested", False)) and quant_state.absmax.device != device:
+        raise ValueError("nested quant_state must be on the weight's device.")
+    absmax = float_absmax(quant_state).to(device=device).contiguous()
     code = quant_state.code.to(device=device, dtype=torch.float32).contiguous()
     if absmax.dtype != torch.float32:
         raise ValueError(f"absmax must be float32 for a non-nested state, got {absmax.dtype}.")

@@ -55,6 +55,29 @@ def _need_dtype(t: torch.Tensor, dtype: torch.dtype, name: str) -> None:
 
 # --------------------------------------------------------------- NF4 ---
 
+def nf4_absmax_expand(absmax_q: torch.Tensor, code2: torch.Tensor, absmax2: torch.Tensor,
+                      blocksize2: int, offset: float) -> torch.Tensor:
+    """Float32 absmax of a double-quantized NF4 state (``lora_forward.py:187-199``):
+    ``fma(code2[absmax_q[i]], absmax2[i // blocksize2], offset)`` per block."""
+    lib = _lib.device_library()
+    _need_cuda(absmax_q, code2, absmax2)
+    _need_dtype(absmax_q, torch.uint8, "nested absmax")
+    _need_dtype(code2, torch.float32, "state2 code")
+    _need_dtype(absmax2, torch.float32, "state2 absmax")
+    n = absmax_q.numel()
+    if code2.numel() != 256:
+        raise ValueError("state2 code must have 256 entries.")
+    if absmax2.numel() * blocksize2 < n:
+        raise ValueError("state2 absmax too short for the nested absmax.")
+    q, c2, a2 = absmax_q.contiguous(), code2.contiguous(), absmax2.contiguous()
+    out = torch.empty(n, dtype=torch.float32, device=absmax_q.device)
+    rc = lib.grpo_nf4_absmax_expand(q.data_ptr(), c2.data_ptr(), a2.data_ptr(), int(blocksize2),
+                                    float(offset), n, out.data_ptr(),
+                                    _lib.stream_handle(absmax_q.device))
+    _lib.check(rc, "grpo_nf4_absmax_expand")
+    return out
+
+
 def nf4_dequant(packed: torch.Tensor, absmax: torch.Tensor, code: torch.Tensor, numel: int,
                 blocksize: int, out: torch.Tensor | None = None) -> torch.Tensor:
     """Bit-exact NF4 dequantization to a flat bf16 tensor of ``numel`` elements."""

@@ -31,6 +31,7 @@ from types import SimpleNamespace
 import torch
 import torch.nn as nn
 
+from ..core.nf4 import float_absmax
 from .qwen2 import Qwen2Config, Qwen2RotaryEmbedding, StackedNF4, _view_linear
 
 _cache: "weakref.WeakKeyDictionary[nn.Module, object]" = weakref.WeakKeyDictionary()
@@ -48,13 +49,11 @@ def _nf4_parts(lin, what: str):
     qs = getattr(w, "quant_state", None)
     if w is None or qs is None or w.dtype != torch.uint8:
         raise ValueError(f"{what}: expected an NF4 (Params4bit-like) weight with quant_state")
-    if getattr(qs, "nested", False) or getattr(qs, "state2", None) is not None:
-        raise ValueError(f"{what}: nested (double-quantized) absmax is not supported by the "
-                         "HIP decode path; quantize with compress_statistics=False")
     n, k = (int(s) for s in qs.shape)
-    if qs.absmax.dtype != torch.float32 or qs.absmax.numel() * int(qs.blocksize) < n * k:
+    absmax = float_absmax(qs)  # a nested state is expanded once (frozen weights)
+    if absmax.dtype != torch.float32 or absmax.numel() * int(qs.blocksize) < n * k:
         raise ValueError(f"{what}: absmax must be float32 with one entry per block")
-    return w.reshape(-1), qs.absmax.reshape(-1), qs.code, int(qs.blocksize), n, k
+    return w.reshape(-1), absmax.reshape(-1), qs.code, int(qs.blocksize), n, k
 
 
 def _stack(parts, what: str):

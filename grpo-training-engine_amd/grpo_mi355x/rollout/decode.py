@@ -37,6 +37,7 @@ import torch
 
 from .. import _lib
 from ..core.kv_pool import PagedKVPool
+from ..core.nf4 import float_absmax
 from ..kernels import ops
 from .adapt import decode_model_from
 from .qwen2 import Qwen2ForCausalLM
@@ -163,11 +164,11 @@ class DecodeEngine:
                                 [p.base_layer.bias.data_ptr() for p in projs],
                                 [p.lora_B.weight.data_ptr() for p in projs], projs[0].rank,
                                 float(projs[0].scaling)),
-                o_w=o.base_layer.weight, o_absmax=oq.absmax, o_code=oq.code, o_la=o_la,
+                o_w=o.base_layer.weight, o_absmax=float_absmax(oq), o_code=oq.code, o_la=o_la,
                 o_parts=parts("o", [H], None, [o.lora_B.weight.data_ptr()], o.rank,
                               float(o.scaling)),
                 gu=mlp.gate_up, gu_parts=parts("gate_up", [2 * I]),
-                down_w=mlp.down_proj.weight, down_absmax=dq.absmax, down_code=dq.code,
+                down_w=mlp.down_proj.weight, down_absmax=float_absmax(dq), down_code=dq.code,
                 down_parts=parts("down", [H])))
         self.final_norm = self.model.model.norm.weight
         self.final_eps = float(self.model.model.norm.variance_epsilon)

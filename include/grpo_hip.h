@@ -42,6 +42,15 @@ int grpo_init(void);
 /* Thread-local description of the last error returned on this thread. */
 const char* grpo_last_error(void);
 
+/* Float32 absmax of a double-quantized (nested) NF4 state, for the kernels
+ * above: out[i] = fma(code2[absmax_q[i]], absmax2[i / bs2], offset) in one
+ * rounding, as the reference's kernel computes it (lora_forward.py:187-199,
+ * whose multiply-add the compiler contracts).  absmax_q uint8 [n_blocks];
+ * code2 float32 [256]; absmax2 float32 [ceil(n_blocks / bs2)]. */
+int grpo_nf4_absmax_expand(const uint8_t* absmax_q, const float* code2, const float* absmax2,
+                           int bs2, float offset, int64_t n_blocks, float* out,
+                           grpo_stream_t stream);
+
 /* ------------------------------------------------------------------ NF4 --
  * NF4 dequantization, bit-exact.  Replaces the dequant half of
  * _lora_forward_kernel (src/triton_kernels/lora_forward.py:171-206) and

@@ -99,22 +99,65 @@ def nibbles(packed, numel: int) -> np.ndarray:
     return np.where((e & 1) == 0, byte >> 4, byte & 0xF).astype(np.int64)
 
 
+def nested_absmax(absmax_q, code2, absmax2, blocksize2: int, offset) -> np.ndarray:
+    """Float32 absmax of a double-quantized state, per block
+    (``lora_forward.py:187-199``): ``code2[q] * absmax2[blk // bs2] + offset``
+    rounded once, as the fused multiply-add the reference kernel compiles to
+    (Triton contracts the multiply and add by default).  The product of two
+    float32 values is exact in float64; the float64 sum is rounded to float32
+    (a double rounding only for a sum within 2^-53 of a float32 midpoint).
+    bitsandbytes' own dequantize rounds the product first, then adds the
+    offset (``nested_absmax_two_roundings``)."""
+    q = np.asarray(absmax_q).reshape(-1).astype(np.int64)
+    blk = np.arange(q.size, dtype=np.int64)
+    c2 = np.asarray(code2, dtype=np.float32)[q].astype(np.float64)
+    a2 = np.asarray(absmax2, dtype=np.float32).reshape(-1)[blk // int(blocksize2)]
+    return (c2 * a2.astype(np.float64) + np.float64(np.float32(offset))).astype(np.float32)
+
+
+def nested_absmax_two_roundings(absmax_q, code2, absmax2, blocksize2: int, offset) -> np.ndarray:
+    """bitsandbytes' form of the same expansion: float32 product, then + offset."""
+    q = np.asarray(absmax_q).reshape(-1).astype(np.int64)
+    blk = np.arange(q.size, dtype=np.int64)
+    c2 = np.asarray(code2, dtype=np.float32)[q]
+    a2 = np.asarray(absmax2, dtype=np.float32).reshape(-1)[blk // int(blocksize2)]
+    return ((c2 * a2).astype(np.float32) + np.float32(offset)).astype(np.float32)
+
+
 def block_scales(absmax, numel: int, blocksize: int, nested: dict | None = None):
     """Per-element float32 scale (``lora_forward.py:186-202``).
 
     ``nested`` (bitsandbytes double quantization) is a dict with ``code``
-    (float32 [256]), ``absmax`` (float32), ``blocksize`` and ``offset``; then
-    ``a = state2.code[absmax_u8[blk]] * state2.absmax[blk // bs2] + offset``
-    (``lora_forward.py:187-199``).  The nested form is parity-unpinned: the
-    reference's tests never build a nested state and bitsandbytes is absent.
+    (float32 [256]), ``absmax`` (float32), ``blocksize`` and ``offset``; the
+    block scales are then :func:`nested_absmax` of the uint8 ``absmax``.
     """
     blk = np.arange(numel, dtype=np.int64) // blocksize
     if nested is None:
         return np.asarray(absmax, dtype=np.float32).reshape(-1)[blk]
-    qa = np.asarray(absmax).reshape(-1).astype(np.int64)[blk]
-    c2 = np.asarray(nested["code"], dtype=np.float32)[qa]
-    a2 = np.asarray(nested["absmax"], dtype=np.float32).reshape(-1)[blk // int(nested["blocksize"])]
-    return (c2 * a2 + np.float32(nested["offset"])).astype(np.float32)
+    full = nested_absmax(absmax, nested["code"], nested["absmax"], int(nested["blocksize"]),
+                         nested["offset"])
+    return full[blk]
+
+
+def quantize_absmax_nested(absmax, blocksize2: int = 256, code2=None):
+    """Double quantization of float32 block scales (test-data generator in the
+    shape bitsandbytes produces: uint8 codes of ``absmax - mean`` per
+    ``blocksize2`` blocks with a signed 256-entry codebook).  Returns
+    ``(q uint8, code2 float32 [256], absmax2 float32, offset float32)``."""
+    a = np.asarray(absmax, dtype=np.float32).reshape(-1)
+    if code2 is None:
+        code2 = np.linspace(-1.0, 1.0, 256, dtype=np.float32)
+    code2 = np.asarray(code2, dtype=np.float32)
+    offset = np.float32(a.astype(np.float64).mean())
+    c = (a - offset).astype(np.float32)
+    nb2 = -(-a.size // blocksize2)
+    pad = np.zeros(nb2 * blocksize2, dtype=np.float32)
+    pad[: a.size] = c
+    a2 = np.abs(pad.reshape(nb2, blocksize2)).max(axis=1).astype(np.float32)
+    a2 = np.where(a2 == 0, np.float32(1.0), a2).astype(np.float32)
+    ratio = pad.reshape(nb2, blocksize2) / a2[:, None]
+    q = np.abs(ratio[..., None] - code2[None, None, :]).argmin(axis=-1).astype(np.uint8)
+    return q.reshape(-1)[: a.size], code2, a2, offset
 
 
 def dequantize_nf4(packed, absmax, numel: int, blocksize: int,

@@ -135,3 +135,34 @@ def test_blocked_dequant_equals_elementwise():
         ref = f32_to_bf16_bits(NF4_CODE[q] * np.repeat(absmax, bs))
         assert np.array_equal(_dequantize_blocked(packed, absmax, numel, bs, NF4_CODE), ref)
         assert np.array_equal(dequantize_nf4(packed, absmax, numel, bs), ref)
+
+
+def test_nested_absmax_rounds_once_and_bounds_the_error():
+    """nested_absmax = code2[q] * absmax2 + offset rounded once: the nearest
+    float32 of the exact value (rational arithmetic); bitsandbytes' two
+    roundings differ from it by at most the product's rounding; the double
+    quantization keeps
+    each scale within half a step of the 256-entry code of its block."""
+    from fractions import Fraction
+
+    from oracle import nf4
+
+    rng = np.random.default_rng(11)
+    a = rng.uniform(1e-3, 0.3, 4000).astype(np.float32)
+    q, c2, a2, off = nf4.quantize_absmax_nested(a, 256)
+    got = nf4.nested_absmax(q, c2, a2, 256, off)
+    for i in range(0, 4000, 7):
+        exact = Fraction(float(c2[q[i]])) * Fraction(float(a2[i // 256])) + Fraction(float(off))
+        x = got[i]
+        lo = np.nextafter(x, np.float32(-np.inf))
+        hi = np.nextafter(x, np.float32(np.inf))
+        d = abs(Fraction(float(x)) - exact)
+        assert d <= abs(Fraction(float(lo)) - exact) and d <= abs(Fraction(float(hi)) - exact)
+    two = nf4.nested_absmax_two_roundings(q, c2, a2, 256, off)
+    prod = np.abs(c2[q].astype(np.float64) * a2[np.arange(4000) // 256])
+    # the product's rounding (<= 2^-24 of it) plus the two final roundings
+    bound = 2.0 ** -24 * prod + 2.0 ** -23 * np.abs(got.astype(np.float64))
+    assert np.all(np.abs(got.astype(np.float64) - two) <= bound)
+    assert np.mean(got == two) > 0.5
+    step = a2[np.arange(4000) // 256] * np.float32(2.0 / 255)
+    assert np.all(np.abs(got - a) <= step / 2 * 1.001 + 1e-7)
