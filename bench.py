@@ -241,7 +241,7 @@ def run_cfg4(args):
     import torch
 
     from grpo_mi355x.core.kv_pool import PagedKVPool
-    from grpo_mi355x.rollout.decode import DecodeEngine, prefill
+    from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill, prefill_chunk
     from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
 
     dev = torch.device("cuda:0")
@@ -258,10 +258,9 @@ def run_cfg4(args):
     G = P * S
     pool = PagedKVPool(cfg.num_hidden_layers, P * width + G * (width + 1),
                        cfg.num_key_value_heads, cfg.head_dim, BS, device=dev)
-    eng1 = DecodeEngine(model, pool, 1, width)
-    eng1.capture()
-    parents = [prefill(eng1, pool, tuple(p), width) for p in prompts]
-    del eng1
+    pre = PrefillEngine(model, pool, prefill_chunk(max(lens) - 1), width)
+    parents = [prefill(pre, pool, tuple(p), width) for p in prompts]
+    del pre
     eng = DecodeEngine(model, pool, G, width)
     rows = [prompts[i // S] for i in range(G)]
 
@@ -393,7 +392,7 @@ def main():
 
     from grpo_mi355x import _lib
     from grpo_mi355x.core.kv_pool import PagedKVPool
-    from grpo_mi355x.rollout.decode import DecodeEngine, prefill
+    from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill, prefill_chunk
     from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
 
     _lib.device_library()
@@ -420,17 +419,21 @@ def main():
     width = -(-(P + NEW) // BS)
     pool = PagedKVPool(cfg.num_hidden_layers, width * (G + 2), cfg.num_key_value_heads,
                        cfg.head_dim, BS, device=dev)
-    eng1 = DecodeEngine(model, pool, 1, width)
-    if not args.eager:
-        eng1.capture()
-    t = time.time()
-    parent = prefill(eng1, pool, tuple(prompt), width)
+    # chunked prefill of the shared prompt (not part of the timed decode)
+    pre = PrefillEngine(model, pool, prefill_chunk(P - 1), width)
+    pre.capture()
     torch.cuda.synchronize()
-    log(f"prefill of {P - 1} tokens in {time.time() - t:.2f}s")
+    t = time.time()
+    parent = prefill(pre, pool, tuple(prompt), width)
+    torch.cuda.synchronize()
+    prefill_s = time.time() - t
+    log(f"prefill of {P - 1} tokens in {prefill_s * 1e3:.1f} ms ({pre.B}-token chunks)")
+    prefill_info = dict(tokens=P - 1, chunk=pre.B, ms=round(prefill_s * 1e3, 2),
+                        tokens_per_s=round((P - 1) / prefill_s, 1))
     kids = pool.fork(parent, G, reserve_tokens=P - 1 + NEW + 1)
     pool.free(parent)
     pool.check_invariants()
-    del eng1
+    del pre
     if args.sample:
         eng = DecodeEngine(model, pool, G, width, do_sample=True, temperature=0.7, top_p=0.9,
                            seed=args.seed)
@@ -522,6 +525,7 @@ def main():
         },
         "decode_steps_per_rollout": nsteps,
         "us_per_decode_step": round(step_ms * 1e3, 2),
+        "prefill": prefill_info,
         "step_hbm": {
             "alg_bytes_per_rollout": alg,
             "kv_bytes_logical": rb["kv_logical"], "kv_bytes_physical": rb["kv_physical"],

@@ -217,9 +217,8 @@ class DecodeEngine:
         """[(kind, launch())] of one forward pass, in order, bound to torch's
         current stream (call inside the stream/graph context they run in)."""
         lib, st = self.lib, _lib.stream_handle(self.device)
-        B, H, D, Hq, Hkv, I = self.B, self.H, self.D, self.Hq, self.Hkv, self.I
+        B, H, I = self.B, self.H, self.I
         chk = _lib.check
-        wsa, wsa_n = self.ws_attn.data_ptr(), self.ws_attn.numel()
         pool = self.pool
         h, x = self.h.data_ptr(), self.x.data_ptr()
         out = [("embedding", lambda: chk(lib.grpo_embedding(
@@ -238,17 +237,7 @@ class DecodeEngine:
             out.append(("qkv", lambda q=q, L=L: chk(lib.grpo_nf4_linear_partials(
                 x, H, q.packed.data_ptr(), q.absmax.data_ptr(), q.code.data_ptr(), self.bs,
                 L["la"], L["qkv_parts"], st), "qkv")))
-            out.append(("attention", lambda L=L, kc=kc, vc=vc: chk(
-                lib.grpo_paged_attn_decode_qkv(
-                    L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
-                    self.max_pos, self.append_pos.data_ptr(), self.attn_len.data_ptr(), kc, vc,
-                    pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
-                    pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n, st),
-                "attention")))
-            out.append(("o", lambda L=L: chk(lib.grpo_nf4_linear_partials_attn(
-                wsa, self.attn_len.data_ptr(), Hq, Hkv, D, pool.block_size, self.max_blocks,
-                L["o_w"].data_ptr(), L["o_absmax"].data_ptr(), L["o_code"].data_ptr(), self.bs,
-                L["o_la"], L["o_parts"], st), "o_proj")))
+            out += self._attn_launches(L, kc, vc, st)
             out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm_parts(
                 L["o_parts"], h, h, L["post_norm"].data_ptr(), x, L["eps"], st), "post_norm")))
             g = L["gu"]
@@ -277,9 +266,34 @@ class DecodeEngine:
                     L["down_absmax"].data_ptr(), L["down_code"].data_ptr(), self.bs, None,
                     L["down_parts"], st), "down")))
             prev = L
-        out.append(("rmsnorm", lambda P=prev: chk(lib.grpo_add_rmsnorm_parts(
+        return out + self._head_launches(prev, st)
+
+    def _attn_launches(self, L: dict, kc: int, vc: int, st) -> list:
+        """Attention of one layer: RoPE + K/V append of the step's token, paged
+        GQA attention over pos + 1 tokens (split partials), o_proj NF4+LoRA
+        partials merging the splits while staging x."""
+        lib, chk, pool = self.lib, _lib.check, self.pool
+        Hq, Hkv, D = self.Hq, self.Hkv, self.D
+        wsa, wsa_n = self.ws_attn.data_ptr(), self.ws_attn.numel()
+        return [
+            ("attention", lambda: chk(lib.grpo_paged_attn_decode_qkv(
+                L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
+                self.max_pos, self.append_pos.data_ptr(), self.attn_len.data_ptr(), kc, vc,
+                pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
+                pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n, st),
+                "attention")),
+            ("o", lambda: chk(lib.grpo_nf4_linear_partials_attn(
+                wsa, self.attn_len.data_ptr(), Hq, Hkv, D, pool.block_size, self.max_blocks,
+                L["o_w"].data_ptr(), L["o_absmax"].data_ptr(), L["o_code"].data_ptr(), self.bs,
+                L["o_la"], L["o_parts"], st), "o_proj"))]
+
+    def _head_launches(self, prev: dict, st) -> list:
+        """Final norm, lm_head and the token choice with the row advance."""
+        lib, chk, B, H = self.lib, _lib.check, self.B, self.H
+        h, x = self.h.data_ptr(), self.x.data_ptr()
+        out = [("rmsnorm", lambda P=prev: chk(lib.grpo_add_rmsnorm_parts(
             P["down_parts"], h, h, self.final_norm.data_ptr(), x, self.final_eps, st),
-            "final_norm")))
+            "final_norm"))]
         if self.sampling:
             if self.lm_fused:
                 out.append(("lm_head", lambda: chk(lib.grpo_lm_head_argmax(
@@ -471,6 +485,76 @@ class DecodeEngine:
         return dict(steps=steps, peak_blocks=peak)
 
 
+class PrefillEngine(DecodeEngine):
+    """Chunked paged prefill: ``chunk`` prompt tokens of one sequence per pass,
+    as rows at positions p .. p + c - 1 that share the sequence's block table.
+
+    The reference prefills with one transformers forward of ``prompt[:-1]`` and
+    a Python scatter of its K/V into the paged cache, one ``.item()`` per
+    (layer, row, token) (``paged_kv.py:547-586``).  Here a chunk is one pass of
+    the decode layers in which every row's K/V is appended first
+    (``grpo_qkv_rope_append_parts``) and attention runs after
+    (``grpo_paged_attn_decode``, row i over p + i + 1 tokens), so row i sees
+    the chunk's earlier tokens as a causal forward does; o_proj reads the bf16
+    attention output.  No final norm or lm_head runs: prefill only fills the
+    cache.  The pass is captured once into a HIP graph; rows past the end of a
+    short last chunk are masked (slot -1, length 0).
+    """
+
+    def __init__(self, model: Qwen2ForCausalLM, pool: PagedKVPool, chunk: int, max_blocks: int,
+                 max_pos: Optional[int] = None):
+        super().__init__(model, pool, chunk, max_blocks, max_pos=max_pos)
+        bf = dict(dtype=torch.bfloat16, device=self.device)
+        self.q_rot = torch.zeros(chunk, self.Hq, self.D, **bf)
+        self.attn_out = torch.zeros(chunk, self.Hq * self.D, **bf)
+        self._rows = torch.arange(chunk, dtype=torch.int32, device=self.device)
+
+    def _attn_launches(self, L: dict, kc: int, vc: int, st) -> list:
+        lib, chk, pool = self.lib, _lib.check, self.pool
+        Hq, Hkv, D = self.Hq, self.Hkv, self.D
+        wsa, wsa_n = self.ws_attn.data_ptr(), self.ws_attn.numel()
+        q, o = self.q_rot.data_ptr(), self.attn_out.data_ptr()
+        return [
+            ("append", lambda: chk(lib.grpo_qkv_rope_append_parts(
+                L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
+                self.max_pos, self.append_pos.data_ptr(), q, kc, vc, pool.num_blocks,
+                self.block_tables.data_ptr(), self.max_blocks, pool.block_size,
+                self.max_blocks, st), "append")),
+            ("attention", lambda: chk(lib.grpo_paged_attn_decode(
+                q, Hq * D, D, kc, vc, pool.num_blocks, self.block_tables.data_ptr(),
+                self.max_blocks, self.attn_len.data_ptr(), o, 1, self.B, Hq, Hkv, D,
+                pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n, st),
+                "attention")),
+            ("o", lambda: chk(lib.grpo_nf4_linear_partials(
+                o, Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
+                L["o_code"].data_ptr(), self.bs, L["o_la"], L["o_parts"], st), "o_proj"))]
+
+    def _head_launches(self, prev: dict, st) -> list:
+        return []
+
+    def _step(self):
+        self._forward()
+
+    def run_prompt(self, table: torch.Tensor, prompt: torch.Tensor, n: int):
+        """Cache tokens ``prompt[0 .. n-1]`` at positions 0 .. n-1 of the sequence
+        whose block table row is ``table`` ([1, w] int32, its blocks reserved)."""
+        if self.graph is None:
+            self.active.zero_()  # the warm-up passes append nothing
+            self.capture()
+        w = table.shape[1]
+        self.block_tables.fill_(-1)
+        self.block_tables[:, :w].copy_(table.view(1, w).expand(self.B, w))
+        none = torch.full_like(self._rows, -1)
+        for p in range(0, n, self.B):
+            c = min(self.B, n - p)
+            valid = self._rows < c
+            self.tokens.zero_()
+            self.tokens[:c].copy_(prompt[p:p + c])
+            self.append_pos.copy_(torch.where(valid, self._rows + p, none))
+            self.attn_len.copy_(torch.where(valid, self._rows + (p + 1), none + 1))
+            self.step()
+
+
 # ------------------------------------------------------------- drop-in ---
 
 def _prompt_rows(input_ids: torch.Tensor, attention_mask: Optional[torch.Tensor]):
@@ -483,12 +567,23 @@ def _prompt_rows(input_ids: torch.Tensor, attention_mask: Optional[torch.Tensor]
     return rows
 
 
+def prefill_chunk(n: int, cap: int = 64) -> int:
+    """Rows of a ``PrefillEngine`` for prompts of up to ``n`` cached tokens."""
+    return max(1, min(cap, n))
+
+
 @torch.no_grad()
 def prefill(engine1: DecodeEngine, pool: PagedKVPool, prompt: tuple, width: int) -> int:
-    """Teacher-forced prefill of ``prompt[:-1]`` into a new pool sequence (B = 1 engine)."""
+    """Prefill of ``prompt[:-1]`` into a new pool sequence: chunked when
+    ``engine1`` is a ``PrefillEngine``, else teacher-forced one token per step
+    through a B = 1 decode engine."""
     sid = pool.allocate(len(prompt))
     n = len(prompt) - 1
-    if n > 0:
+    if n > 0 and isinstance(engine1, PrefillEngine):
+        dev = engine1.device
+        engine1.run_prompt(pool.block_table([sid], width, device=dev),
+                           torch.tensor(prompt, dtype=torch.int64, device=dev), n)
+    elif n > 0:
         dev = engine1.device
         tbl = pool.block_table([sid], width, device=dev)
         engine1.start(torch.tensor([prompt[0]], device=dev), torch.zeros(1, device=dev), tbl,
@@ -541,9 +636,9 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
     nblocks = len(uniq) * width + B * (width + 1)
     pool = PagedKVPool(cfg.num_hidden_layers, nblocks, cfg.num_key_value_heads, cfg.head_dim,
                        block_size, device=dev)
-    eng1 = DecodeEngine(model, pool, 1, width)
-    eng1.capture()
-    parents = {p: prefill(eng1, pool, p, width) for p in uniq}
+    pre = PrefillEngine(model, pool, prefill_chunk(max(len(r) for r in uniq) - 1), width)
+    parents = {p: prefill(pre, pool, p, width) for p in uniq}
+    del pre
     sids = []
     for r in rows:
         # room for the first decode slot; run_paged grows the row from there
@@ -571,4 +666,5 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
     return eng.generated.clone()
 
 
-__all__ = ["DecodeEngine", "paged_kv_decode_model", "prefill"]
+__all__ = ["DecodeEngine", "PrefillEngine", "paged_kv_decode_model", "prefill",
+           "prefill_chunk"]

@@ -99,7 +99,7 @@ def test_cfg4_ragged_group_matches_oracle(dev):
 
 def test_cfg4_blocks_allocated_ahead_and_freed(dev):
     from grpo_mi355x.core.kv_pool import PagedKVPool
-    from grpo_mi355x.rollout.decode import DecodeEngine, prefill
+    from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill, prefill_chunk
 
     model = _model(dev)
     plist, rows, stops, new = _workload(seed=5)
@@ -107,9 +107,8 @@ def test_cfg4_blocks_allocated_ahead_and_freed(dev):
     B = len(rows)
     nblocks = len(plist) * width + B * (width + 1)
     pool = PagedKVPool(2, nblocks, 2, 128, 16, device=dev)
-    eng1 = DecodeEngine(model, pool, 1, width)
-    eng1.capture()
-    parents = [prefill(eng1, pool, tuple(p), width) for p in plist]
+    pre = PrefillEngine(model, pool, prefill_chunk(max(len(p) for p in plist) - 1), width)
+    parents = [prefill(pre, pool, tuple(p), width) for p in plist]
     sids = [pool.fork(parents[plist.index(r)], 1, reserve_tokens=len(r))[0] for r in rows]
     for p in parents:
         pool.free(p)

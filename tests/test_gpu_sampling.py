@@ -56,16 +56,15 @@ def test_sampled_first_tokens_match_the_oracle(dev):
     import numpy as np
 
     from grpo_mi355x.core.kv_pool import PagedKVPool
-    from grpo_mi355x.rollout.decode import DecodeEngine, prefill
+    from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill, prefill_chunk
     from oracle import sampling as S
 
     model = _model(dev, seed=17)
     prompt = _ids(dev, 1, n=31, seed=4)[0].tolist()
     G, width, T, TOP_P, SEED = 64, 4, 0.8, 0.9, 123
     pool = PagedKVPool(2, width * (G + 2), 2, 128, 16, device=dev)
-    eng1 = DecodeEngine(model, pool, 1, width)
-    eng1.capture()
-    parent = prefill(eng1, pool, tuple(prompt), width)
+    pre = PrefillEngine(model, pool, prefill_chunk(len(prompt) - 1), width)
+    parent = prefill(pre, pool, tuple(prompt), width)
     kids = pool.fork(parent, G, reserve_tokens=len(prompt))
     eng = DecodeEngine(model, pool, G, width, do_sample=True, temperature=T, top_p=TOP_P,
                        seed=SEED)
