@@ -22,7 +22,7 @@ LIB_PATH = NATIVE_DIR / "libgrpo_hip.so"
 ARCH = "gfx950"
 
 SOURCES = ("capi.hip", "nf4_linear.hip", "paged_attention.hip", "decode_ops.hip", "lm_head.hip",
-           "sampling.hip")
+           "sampling.hip", "nf4_backward.hip")
 
 
 def hipcc() -> str:

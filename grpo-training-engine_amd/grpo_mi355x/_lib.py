@@ -51,6 +51,8 @@ SIGNATURES = {
     "grpo_last_error": (_c.c_char_p, []),
     "grpo_nf4_dequant": (_I32, [_VP, _VP, _VP, _VP, _I64, _I32, _VP]),
     "grpo_nf4_absmax_expand": (_I32, [_VP, _VP, _VP, _I32, _F32, _I64, _VP, _VP]),
+    "grpo_nf4_grad_x": (_I32, [_VP, _I64, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _I64, _VP,
+                                _I64, _VP]),
     "grpo_nf4_linear_plan": (
         _I32,
         [_I32, _I32, _I32, _I32, _I32, _I32, _c.POINTER(_I32), _c.POINTER(_SZ),

@@ -22,6 +22,7 @@ from __future__ import annotations
 from typing import Optional
 
 import torch
+import torch.nn.functional as F
 
 from . import ops
 
@@ -83,8 +84,17 @@ def _extract_quant_state(weight_4bit: torch.Tensor, quant_state):
     return absmax, code, int(quant_state.blocksize)
 
 
+# Rows of grad_out from which grad_x's NF4 product runs as dequantize + bf16
+# GEMM instead of the fused nf4_grad_x kernel (MI355X, Qwen2 1.5B shapes: at
+# M = 4096 the GEMM path is ~4x faster; at M = 2048, N = 256 the fused kernel is).
+GRAD_X_GEMM_MIN_ROWS = 1024
+
+
 class FusedLoRAFunction(torch.autograd.Function):
-    """Forward = one fused NF4+LoRA kernel launch (``lora_forward.py:653-759``)."""
+    """Forward = one fused NF4+LoRA kernel launch (``lora_forward.py:653-759``);
+    backward = the reference's gradients (``:761-930``): grad_x from the NF4
+    weight on the HIP kernel with the LoRA part added in its store, the
+    rank-r products as plain bf16 GEMMs (float32 accumulation)."""
 
     @staticmethod
     def forward(ctx, x, weight_4bit, quant_state, lora_A, lora_B, scaling, bias):
@@ -100,16 +110,50 @@ class FusedLoRAFunction(torch.autograd.Function):
             w = w.view(torch.uint8)
         x_flat = x.contiguous().view(m, k)
         out = torch.empty((m, n), device=x.device, dtype=x.dtype)
-        if m > 0 and n > 0:
+        if m > 0 and n > 0 and ops.nf4_linear_plan(m, n, k, r, 1, blocksize) is None:
+            # rows beyond the split-K kernel's (training batches): W dequantized
+            # once (bit-exact), then bf16 GEMMs with the kernel's rounding points
+            # (lora_forward.py:246-257): bf16(x W^T), + bias, t = bf16(x A^T),
+            # u = bf16(bf16(t B^T) * bf16(scaling)), y = bf16(acc + u)
+            wb = ops.nf4_dequant(w, absmax, code, n * k, blocksize).view(n, k)
+            acc = F.linear(x_flat, wb)
+            if bias is not None:
+                acc = acc + bias.to(acc.dtype)
+            u = F.linear(F.linear(x_flat, lora_A), lora_B)
+            out = torch.add(acc, u * u.new_tensor(float(scaling)))
+        elif m > 0 and n > 0:
             ops.nf4_lora_linear(x_flat, w, absmax, code, blocksize, n, bias=bias,
                                 lora_a=lora_A, lora_b=lora_B, scaling=float(scaling), out=out)
+        ctx.save_for_backward(x_flat, lora_A, lora_B, w, absmax, code)
+        ctx.blocksize, ctx.scaling, ctx.has_bias = blocksize, float(scaling), bias is not None
+        ctx.x_shape = x.shape
         return out.view(x.shape[:-1] + (n,))
 
     @staticmethod
-    def backward(ctx, grad_out):  # pragma: no cover - training path, out of scope
-        raise NotImplementedError(
-            "backward of the fused NF4+LoRA linear is not implemented in grpo_mi355x "
-            "(rollout decode runs under torch.no_grad).")
+    def backward(ctx, grad_out):
+        x_flat, lora_A, lora_B, w, absmax, code = ctx.saved_tensors
+        m, k = x_flat.shape
+        n = lora_B.shape[0]
+        g = grad_out.contiguous().view(m, n)
+        if g.dtype != torch.bfloat16:
+            g = g.to(torch.bfloat16)
+        grad_bias = g.sum(dim=0) if ctx.has_bias else None  # lora_forward.py:790
+        # scaled_grad = bf16(g * bf16(scaling)) (:836-837); grad_intermediate,
+        # grad_x_lora, xA, grad_B, grad_A: bf16 GEMMs, float32 accumulation (:839-928)
+        sg = g * g.new_tensor(ctx.scaling)
+        gi = torch.matmul(sg, lora_B)
+        gxl = torch.matmul(gi, lora_A)
+        if m >= GRAD_X_GEMM_MIN_ROWS:
+            # many rows: W dequantized once (bit-exact HIP kernel), then a
+            # plain bf16 GEMM -- the same rounding points as the fused kernel
+            wb = ops.nf4_dequant(w, absmax, code, n * k, ctx.blocksize).view(n, k)
+            grad_x = torch.add(torch.matmul(g, wb), gxl)
+        else:
+            grad_x = ops.nf4_grad_x(g, w, absmax, code, ctx.blocksize, n, k, addend=gxl)
+        xa = torch.matmul(x_flat, lora_A.t().contiguous())
+        grad_B = torch.matmul(sg.t().contiguous(), xa)
+        grad_A = torch.matmul(gi.t().contiguous(), x_flat)
+        return grad_x.view(ctx.x_shape), None, None, grad_A, grad_B, None, grad_bias
 
 
 def lora_fused_forward(x: torch.Tensor, base_layer=None, lora_A=None, lora_B=None,

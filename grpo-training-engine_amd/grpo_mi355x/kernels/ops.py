@@ -101,6 +101,37 @@ def nf4_dequant(packed: torch.Tensor, absmax: torch.Tensor, code: torch.Tensor, 
     return out
 
 
+def nf4_grad_x(grad: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor,
+               code: torch.Tensor, blocksize: int, n: int, k: int,
+               addend: torch.Tensor | None = None) -> torch.Tensor:
+    """``bf16(grad [M, n] @ W_nf4 [n, k])`` (+ ``addend`` [M, k], rounded once more)."""
+    lib = _lib.device_library()
+    _need_cuda(grad, packed, absmax, code, addend)
+    _need_dtype(grad, torch.bfloat16, "grad")
+    _need_dtype(packed, torch.uint8, "packed weight")
+    _need_dtype(absmax, torch.float32, "absmax")
+    if grad.ndim != 2 or grad.shape[1] != n:
+        raise ValueError(f"grad must be [M, {n}], got {tuple(grad.shape)}.")
+    if packed.numel() * 2 < n * k or absmax.numel() * blocksize < n * k:
+        raise ValueError("packed weight or absmax too short for [n, k].")
+    if code.numel() != 16:
+        raise ValueError("code must have 16 entries.")
+    m = grad.shape[0]
+    grad = grad.contiguous()
+    if addend is not None:
+        _need_dtype(addend, torch.bfloat16, "addend")
+        if tuple(addend.shape) != (m, k):
+            raise ValueError(f"addend must be [{m}, {k}], got {tuple(addend.shape)}.")
+        addend = addend.contiguous()
+    out = torch.empty((m, k), dtype=torch.bfloat16, device=grad.device)
+    rc = lib.grpo_nf4_grad_x(grad.data_ptr(), n, packed.data_ptr(), absmax.data_ptr(),
+                             code.contiguous().data_ptr(), blocksize, m, n, k,
+                             None if addend is None else addend.data_ptr(), k, out.data_ptr(), k,
+                             _lib.stream_handle(grad.device))
+    _lib.check(rc, "grpo_nf4_grad_x")
+    return out
+
+
 def nf4_lora_linear(x2d: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor,
                     code: torch.Tensor, blocksize: int, n: int, bias: torch.Tensor | None = None,
                     lora_a: torch.Tensor | None = None, lora_b: torch.Tensor | None = None,

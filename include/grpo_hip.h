@@ -65,6 +65,23 @@ int grpo_nf4_absmax_expand(const uint8_t* absmax_q, const float* code2, const fl
 int grpo_nf4_dequant(const uint8_t* w, const float* absmax, const float* code16, void* out,
                      int64_t numel, int blocksize, grpo_stream_t stream);
 
+/* Input gradient of the NF4 linear (training side of the fused NF4 + LoRA
+ * linear): out[m, k] = bf16(sum_n grad[m, n] * W[n, k]) with W =
+ * bf16_rne(code16[q] * absmax) as in grpo_nf4_dequant and float32
+ * accumulation; with addend != NULL, out = bf16(out + addend[m, k]).
+ * Replaces _lora_grad_x_base_kernel (src/triton_kernels/lora_forward.py:
+ * 262-348) and the `grad_x_base + grad_x_lora` add of
+ * FusedLoRAFunction.backward (:873).
+ *   grad   : bf16 [M, N], row stride ldg (elements, multiple of 8), 16-byte aligned
+ *   w      : packed NF4 [N * K / 2] bytes (W[N, K] row-major, even element =
+ *            high nibble), 4-byte aligned; absmax float32 [N * K / blocksize]
+ *   addend : bf16 [M, K] (row stride ld_add) or NULL
+ *   out    : bf16 [M, K] (row stride ldo)
+ * N % 32 == 0, K % 128 == 0, blocksize % 8 == 0. */
+int grpo_nf4_grad_x(const void* grad, int64_t ldg, const uint8_t* w, const float* absmax,
+                    const float* code16, int blocksize, int M, int N, int K, const void* addend,
+                    int64_t ld_add, void* out, int64_t ldo, grpo_stream_t stream);
+
 /* ------------------------------------------------ split-K NF4 linear --
  * The fast NF4 (+ LoRA) linear runs as a split-K kernel: workgroups own a
  * 16-row tile of W and one slice of K, so every CU gets work even when N/16

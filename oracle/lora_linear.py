@@ -70,3 +70,48 @@ def lora_xa(x_bits, a_bits, k: int) -> np.ndarray:
     x = bf16_bits_to_f32(np.asarray(x_bits)).reshape(-1, k)
     a = bf16_bits_to_f32(a_bits).reshape(-1, k)
     return round_bf16(_mm(x, a.T))
+
+
+def nf4_lora_backward(g_bits, x_bits, packed, absmax, n: int, k: int, blocksize: int,
+                      a_bits, b_bits, scaling: float, has_bias: bool = False,
+                      code: np.ndarray = NF4_CODE, nested: dict | None = None,
+                      exact: bool = False):
+    """Gradients of ``nf4_lora_linear`` as ``FusedLoRAFunction.backward`` computes
+    them (``src/triton_kernels/lora_forward.py:761-930``), each product
+    accumulated in float64, rounded to float32, then to bf16 where the reference
+    stores a bf16 tensor:
+
+    1. ``base = bf16(g @ W)`` with W = bf16(code[q] * absmax), the reduction
+       over the N output features (``_lora_grad_x_base_kernel``, ``:262-348``);
+    2. ``sg = bf16(g * bf16(scaling))`` (``:836-837``);
+    3. ``gi = bf16(sg @ B)`` [M, r]; ``gxl = bf16(gi @ A)`` [M, K];
+       ``grad_x = bf16(base + gxl)`` (``:839-873``);
+    4. ``xA = bf16(x @ A^T)``; ``grad_B = bf16(sg^T @ xA)`` [N, r];
+       ``grad_A = bf16(gi^T @ x)`` [r, K] (``:882-928``);
+    5. ``grad_bias = bf16(sum_m g)`` when the layer has a bias (``:790``).
+
+    ``exact=True`` returns the same four products in float64 with no rounding
+    at all (the linear map's true adjoint, used to pin the formulas).  Returns
+    float arrays ``(grad_x [M, K], grad_A [r, K], grad_B [N, r], grad_bias or
+    None)``.
+    """
+    g = bf16_bits_to_f32(np.asarray(g_bits)).reshape(-1, n).astype(np.float64)
+    x = bf16_bits_to_f32(np.asarray(x_bits)).reshape(-1, k).astype(np.float64)
+    w = nf4_weight_bf16(packed, absmax, n, k, blocksize, code, nested).astype(np.float64)
+    a = bf16_bits_to_f32(a_bits).reshape(-1, k).astype(np.float64)
+    b = bf16_bits_to_f32(b_bits).reshape(n, -1).astype(np.float64)
+    if exact:
+        sg = g * float(scaling)
+        gi = sg @ b
+        return g @ w + gi @ a, gi.T @ x, sg.T @ (x @ a.T), (g.sum(0) if has_bias else None)
+    rb = lambda v: round_bf16(np.asarray(v).astype(np.float32))
+    base = rb(g @ w)
+    sg = rb(g * float(np.ravel(round_bf16(np.float32(scaling)))[0]))
+    gi = rb(sg.astype(np.float64) @ b)
+    gxl = rb(gi.astype(np.float64) @ a)
+    grad_x = rb(base + gxl)
+    xa = rb(x @ a.T)
+    grad_b = rb(sg.astype(np.float64).T @ xa.astype(np.float64))
+    grad_a = rb(gi.astype(np.float64).T @ x)
+    grad_bias = rb(g.sum(0)) if has_bias else None
+    return grad_x, grad_a, grad_b, grad_bias

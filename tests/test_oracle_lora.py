@@ -76,3 +76,62 @@ def test_rounding_points_bias_after_base_round():
                                          bias_bits=bias))
     assert y[0, 0] == np.float32(1.0)
     assert float(round_bf16(np.float32(1 + 2.0 ** -7)).reshape(-1)[0]) == 1 + 2.0 ** -7
+
+
+def _backward_case(g, m, n, k, r, scale_b=0.01):
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    packed, absmax = quantize_nf4(w, 64)
+    x = f32_to_bf16_bits(g.standard_normal((m, k)))
+    a = f32_to_bf16_bits(g.standard_normal((r, k)) * 0.05)
+    b = f32_to_bf16_bits(g.standard_normal((n, r)) * scale_b)
+    gr = f32_to_bf16_bits(g.standard_normal((m, n)))
+    return packed, absmax, x, a, b, gr
+
+
+def test_backward_matches_torch_autograd_float64():
+    """The oracle's gradients against torch.autograd of the same float64 linear
+    (an independent differentiation): exact mode to float64 round-off, the
+    bf16-rounded mode within the op's tolerance; scaling 2 and a bias make a
+    dropped or misplaced term fail."""
+    from oracle.lora_linear import nf4_lora_backward
+
+    g = rng(31)
+    for (m, n, k, r) in [(5, 64, 128, 4), (17, 96, 256, 16)]:
+        packed, absmax, x, a, b, gr = _backward_case(g, m, n, k, r, scale_b=0.2)
+        wd = torch.from_numpy(nf4_weight_bf16(packed, absmax, n, k, 64)).double()
+        xt = torch.from_numpy(bf16_bits_to_f32(x)).double().requires_grad_()
+        at = torch.from_numpy(bf16_bits_to_f32(a)).double().requires_grad_()
+        bt = torch.from_numpy(bf16_bits_to_f32(b)).double().requires_grad_()
+        bias = torch.zeros(n, dtype=torch.float64, requires_grad=True)
+        y = F.linear(xt, wd, bias) + (xt @ at.T) @ bt.T * 2.0
+        y.backward(torch.from_numpy(bf16_bits_to_f32(gr)).double())
+        want = [xt.grad.numpy(), at.grad.numpy(), bt.grad.numpy(), bias.grad.numpy()]
+        ex = nf4_lora_backward(gr, x, packed, absmax, n, k, 64, a, b, 2.0, has_bias=True,
+                               exact=True)
+        rd = nf4_lora_backward(gr, x, packed, absmax, n, k, 64, a, b, 2.0, has_bias=True)
+        for e, q, wt in zip(ex, rd, want):
+            assert np.abs(e - wt).max() <= 1e-10 * max(np.abs(wt).max(), 1.0)
+            assert rel_err(q, wt) <= TOL
+
+
+def test_backward_linearity_identities():
+    """y is linear in x and in each of A, B: <g, y(x)> = <grad_x, x>,
+    <g, y(A) - y(A = 0)> = <grad_A, A>, <g, y(B) - y(B = 0)> = <grad_B, B>, with y
+    from the forward oracle (bf16-rounded) and g chosen along the signal so the
+    rounding noise is small against it."""
+    from oracle.lora_linear import nf4_lora_backward
+
+    m, n, k, r, s = 9, 128, 256, 8, 2.0
+    packed, absmax, x, a, b, _ = _backward_case(rng(32), m, n, k, r, scale_b=0.3)
+    fwd = lambda aa, bb: bf16_bits_to_f32(nf4_lora_linear(
+        x, packed, absmax, n, k, 64, a_bits=aa, b_bits=bb, scaling=s)).astype(np.float64)
+    za, zb = np.zeros_like(a), np.zeros_like(b)
+    y = fwd(a, b)
+    dy_a, dy_b = y - fwd(za, b), y - fwd(a, zb)
+    for sig, pick in ((y, 0), (dy_a, 1), (dy_b, 2)):
+        gr = f32_to_bf16_bits(sig.astype(np.float32))
+        grads = nf4_lora_backward(gr, x, packed, absmax, n, k, 64, a, b, s)
+        lhs = float((bf16_bits_to_f32(gr).astype(np.float64) * sig).sum())
+        var = (x, a, b)[pick]
+        rhs = float((grads[pick].astype(np.float64) * bf16_bits_to_f32(var)).sum())
+        assert abs(lhs - rhs) <= 2e-2 * abs(lhs), (pick, lhs, rhs)
