@@ -64,6 +64,10 @@ def parse():
     ap.add_argument("--sample", action="store_true",
                     help="config 3 with the reference trainer's default sampling (temperature "
                          "0.7, top-p 0.9) instead of greedy decoding (an extra measurement)")
+    ap.add_argument("--grad-x", action="store_true",
+                    help="time the backward's NF4 input-gradient product (grpo_nf4_grad_x and "
+                         "dequantize + bf16 GEMM) at Qwen2-1.5B training shapes, M = 4096 "
+                         "(an extra measurement, not the headline)")
     ap.add_argument("--config", type=int, default=3, choices=(3, 4, 5),
                     help="BASELINE config: 3 (default, the headline metric), 4 (G=32 ragged "
                          "group, blocks freed as rows stop) or 5 (Qwen2-7B shape, G=64, "
@@ -370,6 +374,58 @@ def run_cfg5(args):
                kernels=kernels))
 
 
+def run_grad_x(args):
+    """grad_x = bf16(g [M, N] @ W_nf4 [N, K]) of the fused linear's backward at the
+    Qwen2-1.5B projections' shapes (q/o: 1536 x 1536, gate|up: 8960 x 1536,
+    down: 1536 x 8960) for M = 4096 rows, on random bf16 g and random NF4 bytes.
+    Both paths the backward uses are timed with HIP events on the stream they
+    run on: the fused kernel (below 1024 rows in the backward) and dequantize +
+    hipBLASLt GEMM (from 1024 rows).  One JSON line; roofline = MFMA bf16."""
+    import torch
+
+    from grpo_mi355x import _lib
+    from grpo_mi355x.kernels import ops
+
+    _lib.device_library()
+    dev = torch.device("cuda:0")
+    M, reps, rows = 4096, max(args.steps, 1) * 10, []
+    code = torch.linspace(-1.0, 1.0, 16, device=dev)
+    for (n, k) in ((1536, 1536), (8960, 1536), (1536, 8960)):
+        g = torch.randn(M, n, device=dev).to(torch.bfloat16)
+        packed = torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device=dev)
+        absmax = torch.rand(n * k // 64, device=dev) * 0.1
+        fused = lambda: ops.nf4_grad_x(g, packed, absmax, code, 64, n, k)
+        gemm = lambda: torch.matmul(g, ops.nf4_dequant(packed, absmax, code, n * k, 64).view(n, k))
+        row = dict(N=n, K=k)
+        for name, fn in (("fused_kernel", fused), ("dequant_gemm", gemm)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / reps * 1e3
+            row[name] = dict(us=round(us, 1), tflops=round(2 * M * n * k / us / 1e6, 1))
+        log(f"N={n} K={k}: {row}")
+        rows.append(row)
+    tot_f = sum(r["fused_kernel"]["us"] for r in rows)
+    flops = sum(2 * M * r["N"] * r["K"] for r in rows)
+    ach = flops / tot_f / 1e6
+    print(json.dumps({
+        "metric": "NF4 grad_x TFLOP/s (fused kernel, Qwen2-1.5B projection shapes, M=4096)",
+        "value": round(ach, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps, "warmup": 3,
+        "higher_is_better": True, "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random bf16 gradients, random NF4 bytes)",
+        "config": {"workload": "backward grad_x of the fused NF4+LoRA linear", "M": M,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(ach / 2500.0, 4), "traffic": None},
+        "shapes": rows}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -382,6 +438,8 @@ def main():
               "not passed on the GPU yet (an earlier version faulted inside torch's radix sort "
               "in the captured step graph)", file=sys.stderr)
         sys.exit(2)
+    if args.grad_x:
+        return run_grad_x(args)
     if args.config != 3:
         from grpo_mi355x import _lib
 
