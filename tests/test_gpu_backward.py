@@ -91,3 +91,37 @@ def test_fused_lora_backward_matches_oracle(dev, m, n, k, r):
         e = rel_err(bf16_bits_to_f32(bits(gg)), ww)
         print(f"grad_{name}: rel err {e:.2e}", flush=True)
         assert e <= 1e-2, name
+
+
+@pytest.mark.parametrize("m", [48, 1500])
+def test_manual_lora_layer_trains_through_the_fused_function(dev, m):
+    """ManualLoRALayer (src/core/lora.py:50-163) on the fused path: its
+    gradients for x, lora_A and lora_B equal, within 1e-2 of max|x|, those of
+    the same layer on the PyTorch branch (use_triton=False: dequantized base
+    linear + nn.Linear LoRA, autograd through torch)."""
+    from grpo_mi355x.core.lora import ManualLoRALayer
+    from grpo_mi355x.core.nf4 import Linear4bitNF4
+
+    torch.manual_seed(m)
+    k, n = 512, 1536
+    base = Linear4bitNF4.from_weight(torch.randn(n, k, device=dev) * 0.02,
+                                     bias=torch.randn(n, device=dev) * 0.02, blocksize=64)
+    layers = [ManualLoRALayer(base, rank=16, alpha=32, use_triton=t).to(dev).to(torch.bfloat16)
+              for t in (True, False)]
+    with torch.no_grad():
+        layers[0].lora_A.weight.normal_(0, 0.05)
+        layers[0].lora_B.weight.normal_(0, 0.05)
+        for name in ("lora_A", "lora_B"):
+            getattr(layers[1], name).weight.copy_(getattr(layers[0], name).weight)
+    x0 = torch.randn(1, m, k, device=dev).to(torch.bfloat16)
+    gr = torch.randn(1, m, n, device=dev).to(torch.bfloat16)
+    grads = []
+    print(f"ManualLoRALayer backward, fused vs PyTorch branch, M={m}", flush=True)
+    for layer in layers:
+        x = x0.clone().requires_grad_()
+        layer(x).backward(gr)
+        grads.append([x.grad, layer.lora_A.weight.grad, layer.lora_B.weight.grad])
+    for name, a, b in zip(("x", "A", "B"), grads[0], grads[1]):
+        e = rel_err(a.float().cpu().numpy(), b.float().cpu().numpy())
+        print(f"grad_{name}: rel err {e:.2e}", flush=True)
+        assert e <= 1e-2, name
