@@ -84,6 +84,13 @@ def _extract_quant_state(weight_4bit: torch.Tensor, quant_state):
     return absmax, code, int(quant_state.blocksize)
 
 
+def _bf16_scalar(v: float) -> float:
+    """``v`` rounded to bf16, as a Python float: ``t * _bf16_scalar(v)`` on a bf16
+    tensor is bf16(float(t) * bf16(v)), the reference's product with a bf16
+    0-dim tensor (lora_forward.py:836-837), without a host-to-device copy."""
+    return float(torch.tensor(float(v), dtype=torch.bfloat16))
+
+
 # Rows of grad_out from which grad_x's NF4 product runs as dequantize + bf16
 # GEMM instead of the fused nf4_grad_x kernel (MI355X, Qwen2 1.5B shapes: at
 # M = 4096 the GEMM path is ~4x faster; at M = 2048, N = 256 the fused kernel is).
@@ -120,7 +127,7 @@ class FusedLoRAFunction(torch.autograd.Function):
             if bias is not None:
                 acc = acc + bias.to(acc.dtype)
             u = F.linear(F.linear(x_flat, lora_A), lora_B)
-            out = torch.add(acc, u * u.new_tensor(float(scaling)))
+            out = torch.add(acc, u * _bf16_scalar(scaling))
         elif m > 0 and n > 0:
             ops.nf4_lora_linear(x_flat, w, absmax, code, blocksize, n, bias=bias,
                                 lora_a=lora_A, lora_b=lora_B, scaling=float(scaling), out=out)
@@ -140,7 +147,7 @@ class FusedLoRAFunction(torch.autograd.Function):
         grad_bias = g.sum(dim=0) if ctx.has_bias else None  # lora_forward.py:790
         # scaled_grad = bf16(g * bf16(scaling)) (:836-837); grad_intermediate,
         # grad_x_lora, xA, grad_B, grad_A: bf16 GEMMs, float32 accumulation (:839-928)
-        sg = g * g.new_tensor(ctx.scaling)
+        sg = g * _bf16_scalar(ctx.scaling)
         gi = torch.matmul(sg, lora_B)
         gxl = torch.matmul(gi, lora_A)
         if m >= GRAD_X_GEMM_MIN_ROWS:
