@@ -95,11 +95,21 @@ class PagedKVPool:
         Full blocks are shared; the partial last block (if any) is copied into a
         private block of each child in every layer.  Children get room for
         ``reserve_tokens`` tokens (default: the parent's length).
+
+        All-or-nothing: the free blocks the children need (the private tail
+        plus the reservation's growth, per child) are counted first, and an
+        out-of-memory ``RuntimeError`` leaves the pool unchanged.
         """
         length = self.length[sid]
         full = length // self.block_size
         partial = length % self.block_size != 0
         parent = self.blocks[sid]
+        own = full + int(partial)
+        per_child = int(partial) + max(
+            0, (self.blocks_for(reserve_tokens) if reserve_tokens is not None else 0) - own)
+        if n * per_child > len(self._free):
+            raise RuntimeError(f"out of memory: fork of {n} needs {n * per_child} blocks, "
+                               f"{len(self._free)} free")
         children = []
         for _ in range(n):
             cid = self._next_id

@@ -12,9 +12,13 @@ Same call surface and dispatch as the reference's
 * shape/dtype/device problems -> ``ValueError`` (``_validate_inputs``,
   ``:435-487``); rank <= 0 -> ``ValueError`` (``:670-671``).
 
-The fused forward is one launch of ``grpo_nf4_lora_linear``.  Backward (the
-training-phase kernels of ``:761-930``) is not part of the rollout path and
-raises ``NotImplementedError``.
+The fused forward is ``grpo_nf4_lora_linear`` (split-K kernel) up to 64 rows
+and, for training-sized batches, the weight dequantized once (bit-exact) plus
+bf16 GEMMs with the same rounding points.  The backward (``:761-930``) keeps the
+reference's gradients and rounding points: grad_x's NF4 product on the fused
+``grpo_nf4_grad_x`` kernel (LoRA part added in its store) below
+``GRAD_X_GEMM_MIN_ROWS`` rows for the shapes it tiles, otherwise dequantize +
+bf16 GEMM; the rank-r products and the weight gradients are bf16 GEMMs.
 """
 
 from __future__ import annotations
@@ -150,9 +154,11 @@ class FusedLoRAFunction(torch.autograd.Function):
         sg = g * _bf16_scalar(ctx.scaling)
         gi = torch.matmul(sg, lora_B)
         gxl = torch.matmul(gi, lora_A)
-        if m >= GRAD_X_GEMM_MIN_ROWS:
-            # many rows: W dequantized once (bit-exact HIP kernel), then a
-            # plain bf16 GEMM -- the same rounding points as the fused kernel
+        if m >= GRAD_X_GEMM_MIN_ROWS or not ops.nf4_grad_x_supported(n, k, ctx.blocksize):
+            # many rows, or a shape the fused kernel does not tile (the
+            # reference's masked kernel takes any shape, :262-348): W
+            # dequantized once (bit-exact HIP kernel), then a plain bf16 GEMM
+            # -- the same rounding points as the fused kernel
             wb = ops.nf4_dequant(w, absmax, code, n * k, ctx.blocksize).view(n, k)
             grad_x = torch.add(torch.matmul(g, wb), gxl)
         else:

@@ -101,6 +101,12 @@ def nf4_dequant(packed: torch.Tensor, absmax: torch.Tensor, code: torch.Tensor, 
     return out
 
 
+def nf4_grad_x_supported(n: int, k: int, blocksize: int) -> bool:
+    """Shapes ``grpo_nf4_grad_x`` takes: N a multiple of 32, K of 128, blocksize of 8."""
+    return n > 0 and k > 0 and n % 32 == 0 and k % 128 == 0 and blocksize > 0 \
+        and blocksize % 8 == 0
+
+
 def nf4_grad_x(grad: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor,
                code: torch.Tensor, blocksize: int, n: int, k: int,
                addend: torch.Tensor | None = None) -> torch.Tensor:

@@ -31,13 +31,3 @@ def bf16_bits_to_f32(b) -> np.ndarray:
 def round_bf16(x) -> np.ndarray:
     """float32 -> bfloat16 (RNE) -> float32."""
     return bf16_bits_to_f32(f32_to_bf16_bits(x))
-
-
-def bf16_add(a, b) -> np.ndarray:
-    """bf16 + bf16 -> bf16: exact float32 sum of two bf16 values, then RNE."""
-    return round_bf16(np.asarray(a, np.float32) + np.asarray(b, np.float32))
-
-
-def bf16_mul(a, b) -> np.ndarray:
-    """bf16 * bf16 -> bf16: float32 product (exact for bf16 inputs), then RNE."""
-    return round_bf16(np.asarray(a, np.float32) * np.asarray(b, np.float32))

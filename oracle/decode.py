@@ -44,15 +44,21 @@ def apply_top_p(logits: np.ndarray, top_p: float) -> np.ndarray:
     return out
 
 
+def sampling_probs(logits: np.ndarray, temperature: float, top_p: float) -> np.ndarray:
+    """``paged_kv.py:446-448``: ``softmax(_apply_top_p(logits / max(T, 1e-6), top_p))``
+    in float64, the distribution the multinomial draw of ``:449`` samples."""
+    scaled = apply_top_p(np.asarray(logits, dtype=np.float64) / max(temperature, 1e-6), top_p)
+    p = np.exp(scaled - scaled.max(axis=-1, keepdims=True))
+    return p / p.sum(axis=-1, keepdims=True)
+
+
 def sample_tokens(logits: np.ndarray, do_sample: bool, temperature: float, top_p: float,
                   rng: np.random.Generator | None = None) -> np.ndarray:
     """``paged_kv.py:437-450``: greedy argmax (first max) unless sampling."""
     logits = np.asarray(logits, dtype=np.float64)
     if not do_sample or temperature <= 0.0:
         return np.argmax(logits, axis=-1)
-    scaled = apply_top_p(logits / max(temperature, 1e-6), top_p)
-    p = np.exp(scaled - scaled.max(axis=-1, keepdims=True))
-    p /= p.sum(axis=-1, keepdims=True)
+    p = sampling_probs(logits, temperature, top_p)
     rng = rng or np.random.default_rng()
     return np.array([rng.choice(p.shape[-1], p=row) for row in p])
 

@@ -65,13 +65,6 @@ def nf4_lora_linear(x_bits, packed, absmax, n: int, k: int, blocksize: int,
     return f32_to_bf16_bits(acc)
 
 
-def lora_xa(x_bits, a_bits, k: int) -> np.ndarray:
-    """``t = bf16(x @ A^T)`` as float32 holding bf16 values (step 3 above)."""
-    x = bf16_bits_to_f32(np.asarray(x_bits)).reshape(-1, k)
-    a = bf16_bits_to_f32(a_bits).reshape(-1, k)
-    return round_bf16(_mm(x, a.T))
-
-
 def nf4_lora_backward(g_bits, x_bits, packed, absmax, n: int, k: int, blocksize: int,
                       a_bits, b_bits, scaling: float, has_bias: bool = False,
                       code: np.ndarray = NF4_CODE, nested: dict | None = None,

@@ -54,7 +54,8 @@ def test_nf4_grad_x_matches_oracle(dev, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,r", [(37, 256, 512, 16), (130, 1536, 256, 8),
-                                     (1100, 256, 512, 16)])  # the last: dequant + GEMM
+                                     (1100, 256, 512, 16),   # dequant + GEMM (rows)
+                                     (37, 72, 200, 16)])     # dequant + GEMM (shape)
 def test_fused_lora_backward_matches_oracle(dev, m, n, k, r):
     from grpo_mi355x.core.nf4 import Linear4bitNF4
     from grpo_mi355x.kernels import lora_fused_forward

@@ -212,3 +212,23 @@ def test_torch_advance_stays_inside_the_generated_buffer():
     assert e.count.tolist() == [10, 12, 0] and e.pos.tolist() == [20, 30, 30]
     assert e.active.tolist() == [True, True, False]
     assert e.append_pos.tolist() == [20, 30, -1] and e.attn_len.tolist() == [21, 31, 0]
+
+
+def test_fork_into_a_nearly_full_pool_changes_nothing():
+    pool = PagedKVPool(1, 12, 1, 4, block_size=4)
+    p = pool.allocate(10)
+    pool.set_length(p, 10)          # 2 full blocks + a partial one: 9 blocks free
+    refs = list(pool.refcount)
+    free = pool.num_free
+    # 3 children x (1 private tail + 2 blocks of growth to 20 tokens) = 9: fits
+    kids = pool.fork(p, 3, reserve_tokens=20)
+    pool.check_invariants()
+    for c in kids:
+        pool.free(c)
+    assert pool.refcount == refs and pool.num_free == free
+    # 4 children need 12 > 9 free blocks: refused before any state changes
+    with pytest.raises(RuntimeError, match="out of memory"):
+        pool.fork(p, 4, reserve_tokens=20)
+    assert pool.refcount == refs and pool.num_free == free
+    assert set(pool.blocks) == {p}
+    pool.check_invariants()

@@ -164,3 +164,95 @@ def test_draw_frequencies_follow_kept_probabilities():
     assert np.all(counts[~keep] == 0)
     # bf16 rounding of each probability: 2^-8 relative, plus one draw
     assert np.all(np.abs(counts - n * q) <= n * q * 2.0 ** -7 + 1.5)
+
+
+# ------------------------------------------------ oracle.decode (float64 rule)
+
+from oracle import decode as Dec  # noqa: E402
+
+
+def _torch_apply_top_p(logits, top_p):
+    """``paged_kv.py:418-434`` op for op on float64 CPU tensors."""
+    if top_p >= 1.0:
+        return logits
+    if top_p <= 0.0:
+        return torch.full_like(logits, -float("inf"))
+    srt, idx = torch.sort(logits, descending=True, dim=-1)
+    cum = torch.softmax(srt, dim=-1).cumsum(dim=-1)
+    cut = cum > top_p
+    cut[..., 0] = False
+    srt = srt.masked_fill(cut, -float("inf"))
+    out = torch.full_like(logits, -float("inf"))
+    out.scatter_(dim=-1, index=idx, src=srt)
+    return out
+
+
+@pytest.mark.parametrize("top_p", [1e-9, 0.3, 0.9, 0.999, 1.0, 0.0])
+@pytest.mark.parametrize("T", [0.7, 1.0, 1e-7])
+def test_decode_sampling_probs_match_torch_ops(T, top_p):
+    g = np.random.default_rng(31)
+    logits = g.standard_normal((6, 300)) * 3.0
+    t = torch.from_numpy(logits)
+    filt = _torch_apply_top_p(t / max(T, 1e-6), top_p)
+    got = Dec.apply_top_p(logits / max(T, 1e-6), top_p)
+    assert np.array_equal(np.isinf(got), torch.isinf(filt).numpy())
+    fin = np.isfinite(got)
+    assert np.array_equal(got[fin], filt.numpy()[fin])
+    if top_p > 0.0:
+        ref = torch.softmax(filt, dim=-1).numpy()
+        p = Dec.sampling_probs(logits, T, top_p)
+        assert np.allclose(p, ref, rtol=1e-12, atol=1e-15)
+        kept = np.isfinite(got).sum(-1)
+        if top_p < 1e-6:
+            assert np.all(kept == 1)  # the first token is always kept
+        if top_p >= 1.0:
+            assert np.all(kept == logits.shape[-1])
+
+
+def test_decode_top_p_cuts_the_crossing_token():
+    """probs .5/.3/.15/.05 at top_p .75: cumulative .5, .8 -> the token that
+    crosses the bound is cut (``cumulative > top_p``), so only one is kept."""
+    logits = np.log(np.array([[0.5, 0.3, 0.15, 0.05]]))
+    kept = np.isfinite(Dec.apply_top_p(logits, 0.75))
+    assert kept.tolist() == [[True, False, False, False]]
+    kept = np.isfinite(Dec.apply_top_p(logits, 0.85))
+    assert kept.tolist() == [[True, True, False, False]]
+
+
+def test_decode_sample_tokens_greedy_and_frequencies():
+    g = np.random.default_rng(5)
+    logits = g.standard_normal((3, 50))
+    logits[1, 7] = logits[1, 9] = logits[1].max() + 1.0  # tie: first index wins
+    want = torch.argmax(torch.from_numpy(logits), dim=-1).numpy()
+    assert np.array_equal(Dec.sample_tokens(logits, False, 0.7, 0.9), want)
+    assert np.array_equal(Dec.sample_tokens(logits, True, 0.0, 0.9), want)
+    row = np.log(np.array([[0.4, 0.25, 0.2, 0.1, 0.05]]))
+    p = Dec.sampling_probs(row, 1.0, 0.9)[0]   # cut after .4+.25+.2 = .85 < .9 < .95
+    assert np.isclose(p[:4].sum(), 1.0) and p[4] == 0.0
+    n = 20000
+    r = np.random.default_rng(11)
+    draws = np.array([Dec.sample_tokens(row, True, 1.0, 0.9, r)[0] for _ in range(n)])
+    counts = np.bincount(draws, minlength=5)
+    assert counts[4] == 0
+    sigma = np.sqrt(n * p * (1 - p))
+    assert np.all(np.abs(counts - n * p) <= 4.5 * sigma + 1)
+
+
+def test_splitmix64_published_vectors():
+    """Vigna's splitmix64.c: the generator's i-th output for seed s is the
+    output function at s + (i-1)*0x9E3779B97F4A7C15.  Seed 1234567 gives the
+    five values published with the Rosetta Code task "Pseudo-random
+    numbers/Splitmix64"; seed 1477776061723855037 the first three of the
+    rand_xoshiro crate's reference test."""
+    gamma, m = 0x9E3779B97F4A7C15, (1 << 64) - 1
+    got = [S.splitmix64((1234567 + i * gamma) & m) for i in range(5)]
+    assert got == [6457827717110365317, 3203168211198807973, 9817491932198370423,
+                   4593380528125082431, 16408922859458223821]
+    got = [S.splitmix64((1477776061723855037 + i * gamma) & m) for i in range(3)]
+    assert got == [1985237415132408290, 2979275885539914483, 13511426838097143398]
+    # the same task's distribution check: floor(5 * next / 2^64), seed 987654321
+    counts = [0] * 5
+    s = 987654321
+    for i in range(100000):
+        counts[(S.splitmix64((s + i * gamma) & m) * 5) >> 64] += 1
+    assert counts == [20027, 19892, 20073, 19978, 20030]
