@@ -68,10 +68,11 @@ def parse():
                     help="time the backward's NF4 input-gradient product (grpo_nf4_grad_x and "
                          "dequantize + bf16 GEMM) at Qwen2-1.5B training shapes, M = 4096 "
                          "(an extra measurement, not the headline)")
-    ap.add_argument("--config", type=int, default=3, choices=(3, 4, 5),
-                    help="BASELINE config: 3 (default, the headline metric), 4 (G=32 ragged "
+    ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4, 5),
+                    help="BASELINE config: 3 (default, the headline metric), 1 (one layer of "
+                         "paged decode attention), 2 (NF4+LoRA linear at M=8), 4 (G=32 ragged "
                          "group, blocks freed as rows stop) or 5 (Qwen2-7B shape, G=64, "
-                         "long contexts); 4 and 5 are extra measurements, not the headline")
+                         "long contexts); 1, 2, 4 and 5 are extra measurements")
     return ap.parse_args()
 
 
@@ -213,13 +214,7 @@ def cpu_baseline(model, cfg, group, ctx, seed):
     t0 = time.perf_counter()
     oracle.step(toks, kcs, vcs, tables, pos)
     dt = time.perf_counter() - t0
-    try:
-        from threadpoolctl import threadpool_info
-
-        cores = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
-    except Exception:  # pragma: no cover - threadpoolctl is optional
-        cores = os.cpu_count()
-    return dict(value=round(group / dt, 4), unit="tok/s", cores=cores, kind="port",
+    return dict(value=round(group / dt, 4), unit="tok/s", kind="port", **_host_cores(),
                 sample=(f"1 decode step of the numpy oracle, G={group} rows at context {ctx + 1}, "
                         f"all 28 layers + lm_head, NF4 dequantized per call; {dt:.2f} s "
                         "(numpy: elementwise single-threaded, BLAS matmuls multi-threaded)"))
@@ -374,6 +369,235 @@ def run_cfg5(args):
                kernels=kernels))
 
 
+def _graph_time(fns, dev, reps: int) -> float:
+    """Average µs per call of ``fns`` (one launch sequence each), captured once
+    into a HIP graph and replayed ``reps`` times between HIP events recorded on
+    the stream the graph runs on."""
+    import torch
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        for fn in fns[:2]:
+            fn()  # workspaces sized before capture
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        for fn in fns:
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    with torch.cuda.stream(side):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record(side)
+        for _ in range(reps):
+            g.replay()
+        e1.record(side)
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * len(fns))
+
+
+def _host_cores() -> dict:
+    """Host cores (os.cpu_count()) and the BLAS threads numpy uses."""
+    blas = None
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas = max([i.get("num_threads", 1) for i in threadpool_info()] + [1])
+    except Exception:  # pragma: no cover - threadpoolctl is optional
+        pass
+    return dict(cores=os.cpu_count(), blas_threads=blas)
+
+
+ROTATE_BYTES = 512 << 20  # config 1/2 working sets fit the 256 MB MALL: rotate >= 512 MB
+
+
+def run_cfg1(args):
+    """one layer of paged GQA decode attention, 4 sequences,
+    contexts U[512, 1024], 12 query / 2 KV heads, head_dim 128, block size 16,
+    shuffled block tables, q/K/V ~ N(0, 1) bf16, float32 softmax and output.
+
+    R independent instances (own pool, table permutation, q) of >= 512 MB in
+    total are launched back to back (``grpo_paged_attn_decode``: the split
+    kernel and the merge), so no call finds its K/V in the 256 MB MALL.  One
+    step = one replay of the R calls."""
+    import numpy as np
+    import torch
+
+    from grpo_mi355x.kernels import ops
+
+    dev = torch.device("cuda:0")
+    B, HQ, HKV, D, BS = 4, 12, 2, 128, 16
+    rng = np.random.default_rng(args.seed)
+    ctx = rng.integers(512, 1025, B).astype(np.int32)
+    nblk = [-(-int(c) // BS) for c in ctx]
+    nb = sum(nblk) + 8
+    kv_bytes = int(ctx.sum()) * HKV * D * 2 * 2
+    call_bytes = kv_bytes + B * HQ * D * 2 + B * HQ * D * 4 + sum(nblk) * 4
+    R = -(-ROTATE_BYTES // (nb * HKV * BS * D * 2 * 2))
+    gen = torch.Generator(device=dev).manual_seed(args.seed)
+    inst = []
+    for _ in range(R):
+        kc = torch.randn((nb, HKV, BS, D), generator=gen, device=dev).to(torch.bfloat16)
+        vc = torch.randn((nb, HKV, BS, D), generator=gen, device=dev).to(torch.bfloat16)
+        perm = rng.permutation(nb).astype(np.int32)
+        tab = np.full((B, max(nblk)), -1, np.int32)
+        o = 0
+        for b in range(B):
+            tab[b, :nblk[b]] = perm[o:o + nblk[b]]
+            o += nblk[b]
+        q = torch.randn((B, HQ, D), generator=gen, device=dev).to(torch.bfloat16)
+        inst.append((q, kc, vc, torch.from_numpy(tab).to(dev)))
+    lens = torch.from_numpy(ctx).to(dev)
+    out = torch.empty((B, HQ, D), dtype=torch.float32, device=dev)
+    scale = 1.0 / math.sqrt(D)
+    fns = [lambda i=i: ops.paged_attention_decode(i[0], i[1], i[2], i[3], lens, scale, out=out)
+           for i in inst]
+    for _ in range(args.warmup):
+        _graph_time(fns, dev, 1)
+    us = _graph_time(fns, dev, max(args.steps, 1) * 5)
+    achieved = call_bytes / (us * 1e-6) / 1e9
+    log(f"config 1: {R} rotating instances, {us:.2f} us per call, {achieved:.1f} GB/s")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle.paged import paged_attention_decode as oracle_attn
+
+        def bits(t):
+            return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+        q, kc, vc, tab = (bits(inst[0][0]), bits(inst[0][1]), bits(inst[0][2]),
+                          inst[0][3].cpu().numpy())
+        oracle_attn(q, kc, vc, tab, ctx, scale)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 10.0 or n < 5:
+            oracle_attn(q, kc, vc, tab, ctx, scale)
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        cpu = dict(value=round(call_bytes / dt / 1e9, 4), unit="GB/s", kind="port",
+                   sample=f"{n} calls of the numpy oracle on one instance, {dt * 1e3:.1f} ms "
+                          "per call (algorithmic bytes / time)", **_host_cores())
+    print(json.dumps({
+        "metric": "paged GQA decode attention GB/s (BASELINE config 1); % HBM roofline",
+        "value": round(achieved, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us * R / 1e3, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (q, K, V ~ N(0,1) bf16; shuffled block tables)",
+        "config": {"workload": "BASELINE config 1: one layer of paged decode attention, 4 seqs, "
+                               "ctx U[512,1024], 12Q/2KV, D128, block 16, shuffled tables; step = "
+                               f"{R} rotating instances (>= 512 MB)",
+                   "context_lens": ctx.tolist(), "instances": R, "parallelism": "single GPU"},
+        "us_per_call": round(us, 3), "bytes_per_call": call_bytes,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "grpo_paged_attn_decode: paged_attn_split + paged_attn_merge "
+                               "per call"},
+        "cpu_baseline": cpu}), flush=True)
+
+
+def run_cfg2(args):
+    """the NF4-dequant + fused LoRA linear at a decode batch of
+    8 tokens: q/o 1536x1536 and k/v 256x1536 (NF4, blocksize 64, float32
+    absmax, weights N(0, 0.02) before quantization), LoRA rank 16 / alpha 32
+    with A, B ~ N(0, 0.01), bias on q/k/v, x ~ N(0, 1) bf16.
+
+    R independent sets of the four projections (>= 512 MB of weights) are
+    launched back to back (``grpo_nf4_lora_linear``: split-K partial sums and
+    the finish), so no call finds its weights in the 256 MB MALL.  One step =
+    one replay of the R x 4 calls."""
+    import numpy as np
+    import torch
+
+    from grpo_mi355x.core.nf4 import nf4_code, quantize_nf4
+    from grpo_mi355x.kernels import ops
+
+    dev = torch.device("cuda:0")
+    M, K, R_, BSZ = 8, 1536, 16, 64
+    shapes = dict(q=1536, k=256, v=256, o=1536)
+    rng = torch.Generator(device=dev).manual_seed(args.seed)
+    code = nf4_code(dev)
+
+    def lin_bytes(n, bias):
+        return n * K // 2 + n * K // BSZ * 4 + (R_ * K + n * R_) * 2 + M * K * 2 + M * n * 2 \
+            + (n * 2 if bias else 0)
+
+    per_set = sum(lin_bytes(n, k != "o") for k, n in shapes.items())
+    R = -(-ROTATE_BYTES // per_set)
+    sets = []
+    for _ in range(R):
+        d = {}
+        for name, n in shapes.items():
+            w = torch.randn((n, K), generator=rng, device=dev) * 0.02
+            packed, qs = quantize_nf4(w, BSZ)
+            d[name] = dict(
+                n=n, packed=packed.view(-1), absmax=qs.absmax,
+                bias=(torch.randn(n, generator=rng, device=dev) * 0.02).to(torch.bfloat16)
+                if name != "o" else None,
+                a=(torch.randn((R_, K), generator=rng, device=dev) * 0.01).to(torch.bfloat16),
+                b=(torch.randn((n, R_), generator=rng, device=dev) * 0.01).to(torch.bfloat16),
+                x=torch.randn((M, K), generator=rng, device=dev).to(torch.bfloat16),
+                y=torch.empty((M, n), dtype=torch.bfloat16, device=dev))
+        sets.append(d)
+    per_kind = {}
+    reps = max(args.steps, 1) * 5
+    for name, n in shapes.items():
+        fns = [lambda p=s[name]: ops.nf4_lora_linear(p["x"], p["packed"], p["absmax"], code, BSZ,
+                                                      p["n"], bias=p["bias"], lora_a=p["a"],
+                                                      lora_b=p["b"], scaling=2.0, out=p["y"])
+               for s in sets]
+        for _ in range(args.warmup):
+            _graph_time(fns, dev, 1)
+        us = _graph_time(fns, dev, reps)
+        nb = lin_bytes(n, name != "o")
+        per_kind[name] = dict(us_per_call=round(us, 3), bytes_per_call=nb,
+                              achieved_GBs=round(nb / (us * 1e-6) / 1e9, 1),
+                              splits=ops.nf4_linear_plan(M, n, K, R_, 1, BSZ)[0])
+    tot_us = sum(v["us_per_call"] for v in per_kind.values())
+    achieved = per_set / (tot_us * 1e-6) / 1e9
+    log(f"config 2: {R} rotating sets; {per_kind}")
+    cpu = None
+    if not args.no_cpu_baseline:
+        from oracle.lora_linear import nf4_lora_linear as oracle_linear
+
+        def bits(t):
+            return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+        host = {k: dict(x=bits(p["x"]), packed=p["packed"].cpu().numpy(),
+                        absmax=p["absmax"].cpu().numpy(), n=p["n"],
+                        bias=None if p["bias"] is None else bits(p["bias"]), a=bits(p["a"]),
+                        b=bits(p["b"])) for k, p in sets[0].items()}
+
+        def one_set():
+            for p in host.values():
+                oracle_linear(p["x"], p["packed"], p["absmax"], p["n"], K, BSZ,
+                              bias_bits=p["bias"], a_bits=p["a"], b_bits=p["b"], scaling=2.0)
+
+        one_set()
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < 10.0 or n < 3:
+            one_set()
+            n += 1
+        dt = (time.perf_counter() - t0) / n
+        cpu = dict(value=round(per_set / dt / 1e9, 4), unit="GB/s", kind="port",
+                   sample=f"{n} sets of the four projections on the numpy oracle (NF4 "
+                          f"dequantized per call), {dt * 1e3:.1f} ms per set", **_host_cores())
+    print(json.dumps({
+        "metric": "NF4+LoRA linear GB/s at M=8 (BASELINE config 2); % HBM roofline",
+        "value": round(achieved, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(tot_us * R / 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (W ~ N(0,0.02) -> NF4, A/B ~ N(0,0.01), x ~ N(0,1), bf16)",
+        "config": {"workload": "BASELINE config 2: NF4+LoRA linear, M=8, q/o 1536x1536, k/v "
+                               "256x1536, r16 a32, bias on q/k/v; step = "
+                               f"{R} rotating sets of q,k,v,o (>= 512 MB)",
+                   "sets": R, "parallelism": "single GPU"},
+        "bytes_per_set": per_set, "projections": per_kind,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "kernel": "grpo_nf4_lora_linear: nf4_part_mfma + nf4_finish per call"},
+        "cpu_baseline": cpu}), flush=True)
+
+
 def run_grad_x(args):
     """grad_x = bf16(g [M, N] @ W_nf4 [N, K]) of the fused linear's backward at the
     Qwen2-1.5B projections' shapes (q/o: 1536 x 1536, gate|up: 8960 x 1536,
@@ -433,18 +657,13 @@ def main():
               "multi-GPU path (rollout groups would shard data-parallel, one group per GPU).",
               file=sys.stderr)
         sys.exit(2)
-    if args.sample:
-        print("bench.py --sample is disabled: the sampled rollout at the full vocabulary has "
-              "not passed on the GPU yet (an earlier version faulted inside torch's radix sort "
-              "in the captured step graph)", file=sys.stderr)
-        sys.exit(2)
     if args.grad_x:
         return run_grad_x(args)
     if args.config != 3:
         from grpo_mi355x import _lib
 
         _lib.device_library()
-        return run_cfg4(args) if args.config == 4 else run_cfg5(args)
+        return {1: run_cfg1, 2: run_cfg2, 4: run_cfg4, 5: run_cfg5}[args.config](args)
     import numpy as np
     import torch
 
@@ -533,7 +752,7 @@ def main():
     alg = rb["weights"] + rb["kv_logical"]
     log(f"{value:.1f} tok/s, {ms_rollout:.2f} ms/rollout, {step_ms * 1e3:.1f} us/decode step")
 
-    roofline = None
+    roofline = attention = None
     kernels = {}
     if not args.no_kernel_timing:
         # time the ops at a representative point of the rollout: every row
@@ -541,6 +760,7 @@ def main():
         eng.start(**start)
         eng.run(min(64, nsteps))
         torch.cuda.synchronize()
+        ab = eng.attention_bytes()  # before the timing replays advance the rows
         kernels = kernel_timing(eng, dev)
         nf4 = [kernels[k] for k in eng.NF4_KINDS]
         tot_us = sum(k["avg_us"] * k["launches"] for k in nf4)
@@ -551,6 +771,17 @@ def main():
                         frac=round(achieved / PEAK_HBM_GBS, 4), traffic=measured_traffic(),
                         kernel="NF4 linears: nf4_part_mfma (q|k|v, o, down) + nf4_gate_up_units (gate|up)",
                         avg_launch_us=round(tot_us / n, 3), bytes_per_launch=tot_b // n)
+        shared = ((P - 1) // BS) * BS  # prompt tokens in the rows' shared full blocks
+        ab_phys = ab - (G - 1) * shared * cfg.num_key_value_heads * cfg.head_dim * 2 * 2
+        at_us = kernels["attention"]["avg_us"]
+        attention = dict(
+            kernel="paged_attn_split<6, fused q|k|v finish + RoPE + append> (decode step)",
+            context=P + min(64, nsteps), avg_us=at_us, bytes_per_launch_logical=ab,
+            bytes_per_launch_physical=ab_phys,
+            achieved_GBs_logical=round(ab / (at_us * 1e-6) / 1e9, 1),
+            achieved_GBs_physical=round(ab_phys / (at_us * 1e-6) / 1e9, 1),
+            frac_logical=round(ab / (at_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4),
+            frac_physical=round(ab_phys / (at_us * 1e-6) / 1e9 / PEAK_HBM_GBS, 4))
         log(f"kernel timing: {kernels}")
 
     cpu = None
@@ -559,8 +790,8 @@ def main():
         try:
             cpu = cpu_baseline(model, cfg, G, P, args.seed)
         except MemoryError as exc:  # pragma: no cover
-            cpu = dict(value=None, unit="tok/s", cores=os.cpu_count(), kind="port",
-                       sample=f"not run: {exc}")
+            cpu = dict(value=None, unit="tok/s", kind="port", sample=f"not run: {exc}",
+                       **_host_cores())
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -592,6 +823,7 @@ def main():
             "frac_of_peak": round(alg / (elapsed / args.steps) / 1e9 / PEAK_HBM_GBS, 4),
         },
         "roofline": roofline,
+        "attention": attention,
         "kernels": kernels,
         "cpu_baseline": cpu,
     }

@@ -183,10 +183,14 @@ class Qwen2DecodeOracle:
                                bias_bits=p.get("bias"), a_bits=p.get("A"), b_bits=p.get("B"),
                                scaling=self.cfg["scaling"], weight_f32=wf)
 
-    def step(self, tokens, k_caches, v_caches, block_tables, context_lens):
+    def step(self, tokens, k_caches, v_caches, block_tables, context_lens,
+             with_logits: bool = True):
         """Embed ``tokens`` at positions ``context_lens``; append; attend; return logits.
 
-        Returns ``(logits bf16 bits [B, V], greedy next tokens [B])``.  The
+        Returns ``(logits bf16 bits [B, V], greedy next tokens [B])``, or
+        ``(None, None)`` without ``with_logits`` (a prefill pass).  Every row's
+        K/V of a layer is appended before that layer's attention, so rows at
+        positions 0..n-1 sharing one block table compute a causal prefill.  The
         caches (lists of ``[NB, Hkv, BS, D]`` bf16 bits, one per layer) are
         appended to at ``context_lens[b]``; attention covers
         ``context_lens[b] + 1`` positions (``paged_kv.py:695-697, 731-761``).
@@ -218,9 +222,15 @@ class Qwen2DecodeOracle:
             u = self._linear(li, "up", x)
             d = self._linear(li, "down", silu_mul(g, u))
             h = bf16_residual(res, d)
+        if not with_logits:
+            return None, None
         h = rmsnorm(h, self.w["norm"], c["eps"])
         x = bf16_bits_to_f32(h).astype(np.float64)
-        lm = bf16_bits_to_f32(self.w["lm_head"]).astype(np.float64)
+        lm = self._deq.get("lm_head")
+        if lm is None:
+            lm = bf16_bits_to_f32(self.w["lm_head"]).astype(np.float64)
+            if self.cache_dequant:
+                self._deq["lm_head"] = lm
         logits = f32_to_bf16_bits((x @ lm.T).astype(np.float32))
         nxt = np.argmax(bf16_bits_to_f32(logits), axis=-1)
         return logits, nxt

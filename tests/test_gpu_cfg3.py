@@ -1,0 +1,135 @@
+"""BASELINE config 3 on the GPU at the headline shape: Qwen2-1.5B, G = 8.
+
+Hidden 1536, 12 query / 2 KV heads (GQA ratio 6), head_dim 128, MLP 8960,
+vocab 151936, NF4 weights + rank-16 LoRA on q/k/v/o, with two transformer
+layers instead of 28 so the numpy oracle stays fast; every kernel of the
+benchmarked step runs at its real shape: the fused-prologue split attention at
+GQA 6, o_proj merging the attention splits of 12 heads while staging x, the
+fused gate|up + SiLU units kernel, the split-K RMSNorm consumers, and the
+lm_head GEMV + argmax at V = 151936, all replayed from the captured HIP graph.
+
+1. A 512-token prompt is cached by the chunked ``PrefillEngine`` (511 tokens,
+   64-token chunks); the oracle computes the same prefill as one pass of 511
+   rows sharing the block table.  Cached K/V within 1e-2 of max|x|.
+2. G = 8 rows are forked from it (full prompt blocks shared, the partial last
+   block copied) and decoded with ragged stops; each row starts from its own
+   input token so the rows' trajectories differ.  The oracle steps the active
+   rows from the GPU's own cache and tokens: logits within 1e-2 of max|logit|,
+   the fused argmax equals the oracle's wherever its top-2 margin exceeds that
+   tolerance, the appended K/V rows match, and rows that stopped write nothing.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.bf16 import bf16_bits_to_f32
+from oracle.decode import Qwen2DecodeOracle
+
+from conftest import rel_err
+from model_export import bits, export
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_prefill(oracle, prompt, table_row, nb, cfg):
+    """The oracle's cache after ``prompt[:-1]``: one pass of n rows at positions
+    0..n-1 that share the table (every row appends before attention)."""
+    n = len(prompt) - 1
+    L = cfg.num_hidden_layers
+    shape = (nb, cfg.num_key_value_heads, 16, cfg.head_dim)
+    kcs = [np.zeros(shape, np.uint16) for _ in range(L)]
+    vcs = [np.zeros(shape, np.uint16) for _ in range(L)]
+    tables = np.tile(np.asarray(table_row, np.int32), (n, 1))
+    oracle.step(np.asarray(prompt[:n]), kcs, vcs, tables, np.arange(n), with_logits=False)
+    return kcs, vcs
+
+
+def test_cfg3_headline_shape_prefill_and_ragged_decode_match_oracle(dev):
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill
+    from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
+
+    cfg = Qwen2Config.qwen2_1_5b()
+    cfg.num_hidden_layers = 2
+    model = build_random_model(cfg, dev, seed=31)
+    G, bs, P, steps = 8, 16, 512, 5
+    g = np.random.default_rng(12)
+    prompt = g.integers(0, cfg.vocab_size, P).tolist()
+    width = -(-(P + steps + 1) // bs)
+    nb = width * (G + 1) + 8
+    pool = PagedKVPool(cfg.num_hidden_layers, nb, cfg.num_key_value_heads, cfg.head_dim, bs,
+                       device=dev)
+    print("cfg3 shape: chunked prefill of 511 tokens", flush=True)
+    pre = PrefillEngine(model, pool, 64, width)
+    sid = prefill(pre, pool, tuple(prompt), width)
+    torch.cuda.synchronize()
+    del pre
+    w, c = export(model)
+    oracle = Qwen2DecodeOracle(w, c)
+    prow = pool.blocks[sid]
+    kref, vref = _oracle_prefill(oracle, prompt, prow + [-1] * (width - len(prow)), nb, cfg)
+    kg, vg = [bits(pool.k[i]) for i in range(2)], [bits(pool.v[i]) for i in range(2)]
+    for li in range(cfg.num_hidden_layers):
+        for got, ref in ((kg[li], kref[li]), (vg[li], vref[li])):
+            a = bf16_bits_to_f32(got[prow]).reshape(-1, bs, cfg.head_dim)
+            r = bf16_bits_to_f32(ref[prow]).reshape(-1, bs, cfg.head_dim)
+            e = rel_err(a, r)
+            print(f"prefill layer {li}: K/V rel err {e:.2e}", flush=True)
+            assert e <= 1e-2
+
+    # G rows forked from the cached prompt, ragged stops
+    kids = pool.fork(sid, G, reserve_tokens=P + steps)
+    pool.free(sid)
+    pool.check_invariants()
+    limits = np.array([5, 1, 3, 5, 2, 4, 5, 3])
+    toks = np.concatenate([[prompt[-1]], g.integers(0, cfg.vocab_size, G - 1)])
+    tables = pool.block_table(kids, width)
+    tab_np = tables.cpu().numpy()
+    eng = DecodeEngine(model, pool, G, width, keep_logits=True)
+    start = dict(tokens=torch.from_numpy(toks).to(dev),
+                 positions=torch.full((G,), P - 1, device=dev), block_tables=tables.to(dev),
+                 limits=torch.from_numpy(limits).to(dev), max_new_tokens=steps)
+    eng.start(**start)
+    eng.capture()
+    eng.start(**start)
+    kcs = [bits(pool.k[i]) for i in range(2)]
+    vcs = [bits(pool.v[i]) for i in range(2)]
+    pos = np.full(G, P - 1, np.int64)
+    worst, agree, total = 0.0, 0, 0
+    for t in range(steps):
+        act = np.flatnonzero(t < limits)
+        print(f"cfg3 shape: decode step {t}, active rows {act.tolist()}", flush=True)
+        before = [bits(pool.k[i]) for i in range(2)]
+        eng.step()
+        torch.cuda.synchronize()
+        lg = bf16_bits_to_f32(bits(eng.logits))
+        lr_bits, nxt = oracle.step(toks[act], kcs, vcs, tab_np[act], pos[act])
+        lr = bf16_bits_to_f32(lr_bits)
+        new_toks = eng.tokens.cpu().numpy()
+        for j, b in enumerate(act):
+            worst = max(worst, rel_err(lg[b], lr[j]))
+            assert new_toks[b] == int(np.argmax(lg[b]))  # the fused argmax, first max
+            srt = np.sort(lr[j])
+            if srt[-1] - srt[-2] > 1e-2 * np.abs(lr[j]).max():
+                total += 1
+                agree += int(new_toks[b] == nxt[j])
+        for li in range(2):
+            kga, vga = bits(pool.k[li]), bits(pool.v[li])
+            for b in range(G):
+                blk, off = tab_np[b, pos[b] // bs], pos[b] % bs
+                if b in act:
+                    for got, ref in ((kga, kcs[li]), (vga, vcs[li])):
+                        assert rel_err(bf16_bits_to_f32(got[blk, :, off]),
+                                       bf16_bits_to_f32(ref[blk, :, off])) <= 1e-2
+                else:  # a stopped row appends nothing
+                    assert np.array_equal(kga[blk, :, off], before[li][blk, :, off])
+        toks = new_toks.copy()
+        pos[act] += 1
+    print(f"cfg3 shape: worst logits rel err {worst:.2e}, argmax agree {agree}/{total}",
+          flush=True)
+    assert worst <= 1e-2, worst
+    assert total >= 10 and agree == total
+    gen = eng.generated.cpu().numpy()
+    for b in range(G):
+        assert np.all(gen[b, limits[b]:] == 0)

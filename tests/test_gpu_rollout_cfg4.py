@@ -22,7 +22,7 @@ import torch
 from oracle.bf16 import bf16_bits_to_f32
 from oracle.decode import Qwen2DecodeOracle
 
-from model_export import export
+from model_export import bits, export
 
 pytestmark = pytest.mark.gpu
 
@@ -131,3 +131,110 @@ def test_cfg4_blocks_allocated_ahead_and_freed(dev):
     gen = eng.generated.cpu().numpy()
     for b, s in enumerate(stops):
         assert np.all(gen[b, s:] == 0) and np.all(gen[b, :s] >= 0)
+
+
+def test_cfg4_headline_shape_ragged_group_matches_oracle(dev):
+    """Config 4's recipe on the Qwen2-1.5B shape (two layers): G = 32 rows = 4
+    prompts x 8 samples, prompts U[128, 512], lognormal stops (sigma 0.75,
+    median scaled to 24 and capped at 48 steps for test time), chunked prefill
+    per prompt, rows forked from it, blocks reserved a chunk ahead and freed as
+    rows stop (``run_paged``), greedy tokens from the captured graph.
+
+    The oracle follows each prompt's GPU tokens (teacher forcing, the 4 prompts
+    batched as 4 rows of one step): at every step of every row the GPU's token
+    equals the oracle's argmax wherever the oracle's top-2 margin exceeds 1e-2
+    of max|logit|; the 8 samples of a prompt are equal up to their stops and
+    pad after; every block returns to the free list."""
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill
+    from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
+
+    cfg = Qwen2Config.qwen2_1_5b()
+    cfg.num_hidden_layers = 2
+    model = build_random_model(cfg, dev, seed=41)
+    g = np.random.default_rng(8)
+    prompts, samples, new = 4, 8, 48
+    lens = g.integers(128, 513, prompts)
+    plist = [g.integers(0, cfg.vocab_size, n).tolist() for n in lens]
+    stops = np.minimum(new, np.maximum(1, np.round(
+        g.lognormal(np.log(24.0), 0.75, prompts * samples)))).astype(int)
+    rows = [plist[i // samples] for i in range(prompts * samples)]
+    B, bs = len(rows), 16
+    width = -(-(int(lens.max()) + new) // bs)
+    pool = PagedKVPool(2, prompts * width + B * (width + 1), cfg.num_key_value_heads,
+                       cfg.head_dim, bs, device=dev)
+    print(f"cfg4 shape: prompts {lens.tolist()}, stops {stops.tolist()}", flush=True)
+    pre = PrefillEngine(model, pool, 64, width)
+    parents = [prefill(pre, pool, tuple(p), width) for p in plist]
+    del pre
+    sids = [pool.fork(parents[i // samples], 1, reserve_tokens=len(r))[0]
+            for i, r in enumerate(rows)]
+    # the oracle's caches: the GPU's prefilled prompt blocks
+    ptab = np.full((prompts, width + 4), -1, np.int32)
+    for i, p in enumerate(parents):
+        bl = pool.blocks[p]
+        ptab[i, :len(bl)] = bl
+    kcs = [bits(pool.k[li]) for li in range(2)]
+    vcs = [bits(pool.v[li]) for li in range(2)]
+    for p in parents:
+        pool.free(p)
+    eng = DecodeEngine(model, pool, B, width)
+    start = dict(tokens=torch.tensor([r[-1] for r in rows], device=dev),
+                 positions=torch.tensor([len(r) - 1 for r in rows], device=dev),
+                 block_tables=pool.block_table(sids, width, device=dev),
+                 limits=torch.from_numpy(stops).to(dev), max_new_tokens=new)
+    eng.start(**start)
+    eng.capture()
+    eng.start(**start)
+    stats = eng.run_paged(sids, new, check_invariants=True)
+    torch.cuda.synchronize()
+    assert pool.num_free == pool.num_blocks and not pool.blocks
+    gen = eng.generated.cpu().numpy()
+    for b in range(B):
+        lead = (b // samples) * samples
+        s = min(stops[b], stops[lead])
+        assert np.array_equal(gen[b, :s], gen[lead, :s])
+        assert np.all(gen[b, stops[b]:] == PAD)
+    # teacher-forced oracle along each prompt's longest row
+    w, c = export(model)
+    oracle = Qwen2DecodeOracle(w, c)
+    longest = [max(range(i * samples, (i + 1) * samples), key=lambda b: stops[b])
+               for i in range(prompts)]
+    # oracle tables: the shared full prompt blocks, then fresh blocks past the pool's
+    nb_o = pool.num_blocks
+    tab = np.full((prompts, width + 4), -1, np.int32)
+    extra = nb_o
+    for i in range(prompts):
+        n = len(plist[i]) - 1
+        full = n // bs
+        tab[i, :full] = ptab[i, :full]
+        for j in range(full, width + 4):
+            tab[i, j] = extra
+            extra += 1
+    for li in range(2):
+        pad_blocks = np.zeros((extra - nb_o,) + kcs[li].shape[1:], np.uint16)
+        kcs[li] = np.concatenate([kcs[li], pad_blocks])
+        vcs[li] = np.concatenate([vcs[li], pad_blocks.copy()])
+    for i in range(prompts):  # the partial last prompt block, copied
+        n = len(plist[i]) - 1
+        if n % bs:
+            for li in range(2):
+                kcs[li][tab[i, n // bs]] = kcs[li][ptab[i, n // bs]]
+                vcs[li][tab[i, n // bs]] = vcs[li][ptab[i, n // bs]]
+    pos = np.array([len(p) - 1 for p in plist], np.int64)
+    toks = np.array([p[-1] for p in plist])
+    compared = agree = 0
+    for t in range(int(max(stops[b] for b in longest))):
+        act = np.array([i for i in range(prompts) if t < stops[longest[i]]])
+        lr_bits, nxt = oracle.step(toks[act], kcs, vcs, tab[act], pos[act])
+        lr = bf16_bits_to_f32(lr_bits)
+        for j, i in enumerate(act):
+            srt = np.sort(lr[j])
+            if srt[-1] - srt[-2] > 1e-2 * np.abs(lr[j]).max():
+                compared += 1
+                agree += int(gen[longest[i], t] == nxt[j])
+        toks[act] = gen[[longest[i] for i in act], t]  # teacher forcing on the GPU's tokens
+        pos[act] += 1
+    print(f"cfg4 shape: {stats}, tokens compared {compared}, agree {agree}", flush=True)
+    assert compared >= 0.5 * sum(stops[b] for b in longest)
+    assert agree == compared

@@ -86,3 +86,58 @@ def test_sampled_first_tokens_match_the_oracle(dev):
     want, kept = S.sample_rows(bits, T, TOP_P, draws)
     assert np.array_equal(first, want)
     assert len(set(first.tolist())) > 1 and kept[0] > 1
+
+
+def test_sampled_rollout_at_full_vocabulary_matches_the_oracle_twice(dev):
+    """The sampled decode at the Qwen2-1.5B shape (two layers, V = 151936,
+    T = 0.7, top_p = 0.9, the reference trainer's defaults), G = 8 rows, run as
+    two rollouts of graph replays: at every step every active row's token is
+    the sampling oracle's on that step's bf16 logits with the row's draw
+    SplitMix64(seed, row, step), and the second rollout repeats the first."""
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill, prefill_chunk
+    from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
+    from oracle import sampling as S
+
+    cfg = Qwen2Config.qwen2_1_5b()
+    cfg.num_hidden_layers = 2
+    model = build_random_model(cfg, dev, seed=23)
+    g = np.random.default_rng(3)
+    prompt = g.integers(0, cfg.vocab_size, 40).tolist()
+    G, steps, T, TOP_P, SEED = 8, 6, 0.7, 0.9, 77
+    width = -(-(len(prompt) + steps) // 16)
+    pool = PagedKVPool(2, width * (G + 2), cfg.num_key_value_heads, cfg.head_dim, 16,
+                       device=dev)
+    pre = PrefillEngine(model, pool, prefill_chunk(len(prompt) - 1), width)
+    parent = prefill(pre, pool, tuple(prompt), width)
+    del pre
+    kids = pool.fork(parent, G, reserve_tokens=len(prompt) + steps)
+    eng = DecodeEngine(model, pool, G, width, do_sample=True, temperature=T, top_p=TOP_P,
+                       seed=SEED)
+    limits = torch.tensor([6, 2, 6, 4, 6, 5, 1, 6], device=dev)
+
+    def start():
+        eng.start(torch.full((G,), prompt[-1], device=dev),
+                  torch.full((G,), len(prompt) - 1, device=dev),
+                  pool.block_table(kids, width, device=dev), limits, steps)
+
+    start()
+    eng.capture()
+    runs = []
+    lim = limits.cpu().numpy()
+    for rollout in range(2):
+        start()
+        for t in range(steps):
+            print(f"sampled rollout {rollout}, step {t}", flush=True)
+            eng.step()
+            torch.cuda.synchronize()
+            act = np.flatnonzero(t < lim)
+            bits = eng.logits.cpu().view(torch.int16).numpy().view(np.uint16)
+            got = eng.generated[:, t].cpu().numpy()
+            draws = np.array([S.step_draw(SEED, int(b), t) for b in act], dtype=np.uint64)
+            want, kept = S.sample_rows(bits[act], T, TOP_P, draws)
+            assert np.array_equal(got[act], want), (rollout, t)
+            assert np.all(got[np.flatnonzero(t >= lim)] == 0)
+        runs.append(eng.generated.cpu().numpy().copy())
+    assert np.array_equal(runs[0], runs[1])
+    assert len({tuple(r[:2]) for r in runs[0][lim >= 2]}) > 1
