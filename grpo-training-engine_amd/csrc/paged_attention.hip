@@ -26,6 +26,8 @@
 // neither q nor the RoPE + append needs a launch of its own.
 #include <math.h>
 
+#include <mutex>
+
 #include "linear_parts.hpp"
 
 using namespace grpo;
@@ -746,6 +748,71 @@ extern "C" int grpo_paged_attn_decode_qkv(const grpo_linear_parts_t* qkv, int Hq
   a.append_pos = append_pos;
   if (int rc = use_workspace(a, plan, workspace, workspace_bytes)) return rc;
   return launch_split_gq<true>(a, as_stream(stream));
+}
+
+// ------------------------------------------------- allocation-free entry --
+//
+// grpo_paged_attn_decode_noalloc runs grpo_paged_attn_decode with its split
+// partials in `scratch`, a file-scope device array, instead of a caller
+// workspace.  In host code `scratch` names a host-side stand-in, never the
+// device copy: the device address comes from hipGetSymbolAddress, taken once per
+// device (with that device current) on the entry's first call there and kept in
+// g_scratch_dev[device].  Every call on one GPU shares that GPU's array.
+namespace {
+
+constexpr size_t NOALLOC_SCRATCH_BYTES = size_t(8) << 20;
+constexpr int NOALLOC_MAX_DEVICES = 64;
+__device__ __align__(256) unsigned char scratch[NOALLOC_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch_dev[NOALLOC_MAX_DEVICES] = {};
+
+int scratch_address(void** out) {
+  int dev = 0;
+  if (int rc = hip_check(hipGetDevice(&dev), "hipGetDevice")) return rc;
+  if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return einval("device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_dev[dev]) {
+    void* p = nullptr;
+    if (int rc = hip_check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress"))
+      return rc;
+    if (!p) return hip_check(hipErrorInvalidSymbol, "hipGetSymbolAddress");
+    g_scratch_dev[dev] = p;
+  }
+  *out = g_scratch_dev[dev];
+  return GRPO_OK;
+}
+
+}  // namespace
+
+extern "C" size_t grpo_paged_attn_noalloc_max_bytes(void) { return NOALLOC_SCRATCH_BYTES; }
+
+extern "C" int grpo_paged_attn_decode_noalloc(const void* q, int64_t q_stride_b,
+                                              int64_t q_stride_h, const void* k_cache,
+                                              const void* v_cache, int64_t num_blocks,
+                                              const int32_t* block_tables, int64_t bt_stride,
+                                              const int32_t* context_lens, void* out,
+                                              int out_bf16, int B, int Hq, int Hkv, int D,
+                                              int block_size, int max_blocks, float scale,
+                                              grpo_stream_t stream) {
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || D <= 0 || block_size <= 0 || max_blocks < 0)
+    return einval("bad attention dimensions");
+  const size_t need =
+      B > 0 && max_blocks > 0 ? plan_attn(B, Hq, Hkv, D, block_size, max_blocks).bytes : 0;
+  if (need > NOALLOC_SCRATCH_BYTES) {
+    set_error("invalid argument: this shape needs %zu bytes of split partials; the "
+              "allocation-free entry holds at most %zu (use grpo_paged_attn_decode with a "
+              "workspace)",
+              need, NOALLOC_SCRATCH_BYTES);
+    return GRPO_EWORKSPACE;
+  }
+  void* ws = nullptr;
+  if (need > 0)
+    if (int rc = scratch_address(&ws)) return rc;
+  return grpo_paged_attn_decode(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
+                                block_tables, bt_stride, context_lens, out, out_bf16, B, Hq, Hkv,
+                                D, block_size, max_blocks, scale, ws,
+                                need > 0 ? NOALLOC_SCRATCH_BYTES : 0, stream);
 }
 
 namespace grpo {

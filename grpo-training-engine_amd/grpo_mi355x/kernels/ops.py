@@ -254,8 +254,13 @@ def paged_attention_workspace_bytes(b: int, hq: int, hkv: int, d: int, bs: int,
 def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                            block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
                            out_dtype: torch.dtype = torch.float32,
-                           out: torch.Tensor | None = None) -> torch.Tensor:
-    """GQA paged decode attention; ``q [B, Hq, D]`` bf16 -> ``[B, Hq, D]`` out_dtype."""
+                           out: torch.Tensor | None = None,
+                           no_alloc: bool = False) -> torch.Tensor:
+    """GQA paged decode attention; ``q [B, Hq, D]`` bf16 -> ``[B, Hq, D]`` out_dtype.
+
+    ``no_alloc`` calls ``grpo_paged_attn_decode_noalloc`` (split partials in the
+    library's per-GPU scratch array, no workspace); ``out`` must then be given
+    for the call to allocate nothing at all."""
     lib = _lib.device_library()
     _need_cuda(q, k_cache, v_cache, block_tables, context_lens)
     _check_cache(k_cache, v_cache)
@@ -276,6 +281,14 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     elif out.shape != (b, hq, d) or not out.is_contiguous() or out.dtype != out_dtype:
         raise ValueError("out must be a contiguous [B, Hq, D] tensor of out_dtype.")
     max_blocks = block_tables.shape[1]
+    if no_alloc:
+        rc = lib.grpo_paged_attn_decode_noalloc(
+            q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), nb,
+            block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(),
+            out.data_ptr(), 1 if out_dtype == torch.bfloat16 else 0, b, hq, hkv, d, bs,
+            max_blocks, float(scale), _lib.stream_handle(q.device))
+        _lib.check(rc, "grpo_paged_attn_decode_noalloc")
+        return out
     nbytes = int(lib.grpo_paged_attn_workspace_bytes(b, hq, hkv, d, bs, max_blocks))
     ws = workspace("paged_attn", nbytes, q.device)
     rc = lib.grpo_paged_attn_decode(

@@ -208,6 +208,25 @@ int grpo_paged_attn_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h
                            int Hkv, int D, int block_size, int max_blocks, float scale,
                            void* workspace, size_t workspace_bytes, grpo_stream_t stream);
 
+/* Allocation-free variant of grpo_paged_attn_decode: no counterpart in the
+ * reference.  For callers that cannot allocate device memory or pass a
+ * workspace (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments, kernels and results as
+ * grpo_paged_attn_decode without workspace/workspace_bytes: the split partials
+ * live in a library-owned device array of grpo_paged_attn_noalloc_max_bytes()
+ * bytes per GPU (8 MiB), held until the process ends.  Shapes whose
+ * grpo_paged_attn_workspace_bytes(...) exceeds it return GRPO_EWORKSPACE.  It
+ * calls no allocator.  All calls on one GPU share that array: calls that
+ * overlap on one GPU (two streams, two host threads) race and must be
+ * serialised by the caller. */
+size_t grpo_paged_attn_noalloc_max_bytes(void);
+int grpo_paged_attn_decode_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                   const void* k_cache, const void* v_cache, int64_t num_blocks,
+                                   const int32_t* block_tables, int64_t bt_stride,
+                                   const int32_t* context_lens, void* out, int out_bf16, int B,
+                                   int Hq, int Hkv, int D, int block_size, int max_blocks,
+                                   float scale, grpo_stream_t stream);
+
 /* Decode-step attention: grpo_paged_attn_decode with q, k and v taken from the
  * split-K partial sums of the q|k|v projection (finished here with its bias and
  * LoRA epilogue), RoPE applied to q and k at position append_pos[b] (cos/sin
