@@ -340,7 +340,8 @@ def run_cfg5(args):
                  block_tables=torch.from_numpy(tables).to(dev),
                  limits=torch.full((G,), 1 << 20, device=dev), max_new_tokens=steps + 64)
     eng.start(**start)
-    eng.capture()
+    if not args.eager:
+        eng.capture()
     eng.start(**start)
     eng.run(16 * args.warmup)
     torch.cuda.synchronize()

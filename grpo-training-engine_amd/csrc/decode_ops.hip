@@ -154,7 +154,36 @@ __global__ void __launch_bounds__(AMAX_T) argmax_kernel(const uint16_t* __restri
   const uint16_t* row = logits + (int64_t)blockIdx.x * ld;
   float best = -INFINITY;
   int bi = 0x7fffffff;
-  for (int i = threadIdx.x; i < V; i += AMAX_T) {
+  // 16-byte loads of 8 logits, four in flight per thread before any compare
+  // (one dependent 2-byte load per iteration left the row latency-bound); a
+  // thread's indexes rise through its chunks, so strictly-greater keeps the
+  // first index of a maximum.  Misaligned rows and the tail take 2-byte loads.
+  const bool vec = (reinterpret_cast<uintptr_t>(row) & 15u) == 0;
+  const int nv = vec ? V / 8 : 0;
+  constexpr int AMAX_U = 4;
+  for (int c0 = 0; c0 < nv; c0 += AMAX_U * AMAX_T) {
+    uint4 w[AMAX_U];
+#pragma unroll
+    for (int u = 0; u < AMAX_U; ++u) {
+      const int c = c0 + u * AMAX_T + threadIdx.x;
+      w[u] = c < nv ? reinterpret_cast<const uint4*>(row)[c] : make_uint4(0xFF80FF80u, 0xFF80FF80u,
+                                                                          0xFF80FF80u, 0xFF80FF80u);
+    }
+#pragma unroll
+    for (int u = 0; u < AMAX_U; ++u) {
+      const int c = c0 + u * AMAX_T + threadIdx.x;
+      const uint32_t ww[4] = {w[u].x, w[u].y, w[u].z, w[u].w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float v = (j & 1) ? bf_hi(ww[j >> 1]) : bf_lo(ww[j >> 1]);
+        if (v > best) {
+          best = v;
+          bi = 8 * c + j;
+        }
+      }
+    }
+  }
+  for (int i = 8 * nv + threadIdx.x; i < V; i += AMAX_T) {
     const float v = bf2f(row[i]);
     if (v > best) {  // strictly greater keeps the first index per thread
       best = v;

@@ -54,7 +54,7 @@ __device__ __forceinline__ T sel4(T a0, T a1, T a2, T a3, int i) {
 static_assert(MAXSEG == 4, "sel_seg selects among four entries");
 #define sel_seg(a, i) sel4((a)[0], (a)[1], (a)[2], (a)[3], (i))
 
-constexpr int MAX_SLICES = 16;  // K slices of a split-K linear (the plan keeps S <= 16)
+constexpr int MAX_SLICES = 20;  // K slices of a split-K linear (the plan keeps S <= 20)
 
 // LoRA t of row m rounded to bf16, ts[seg*16 + j], computed by the whole
 // workgroup (the caller synchronises before reading ts).  The S slices of a

@@ -40,7 +40,11 @@ namespace {
 
 constexpr int KSTEP = 256;          // k elements per step: 4 lane groups x 64
 constexpr int PART_WAVES = 4;       // n-tiles (waves) per workgroup, x given in bf16
-constexpr int PART_LDS_MAX = 65536; // bytes of the staged x slice per workgroup
+constexpr int PART_LDS_MAX = 65536; // bytes of the staged x slice per workgroup (M <= 16)
+// Wide batches (M > 16) may stage up to all of gfx950's 160 KiB per workgroup:
+// x of 64 rows then covers 4 k-steps, so K slices stay few (fewer partial sums)
+// and long-K linears need no row chunks (each of which re-read the weights).
+constexpr int PART_LDS_BIG = 163840;
 constexpr int KPW_MAX = 8;          // k-steps per wave (all loads in flight at once)
 #ifndef GRPO_TARGET_WAVES
 #define GRPO_TARGET_WAVES 2048
@@ -161,18 +165,22 @@ struct PartArgs {
   int gu_S;
 };
 
-enum XSource { X_BF16 = 0, X_ATTN = 1, X_SILU = 2 };
+enum XSource { X_BF16 = 0, X_ATTN = 1, X_SILU = 2, X_WIDE = 3 };  // X_WIDE: bf16, 16 waves
 
 // n-tiles (waves) per workgroup.  Every workgroup of a K slice rebuilds the x
 // slice it stages; the SiLU source reads 16 bytes of partial sums per element,
 // so its workgroups are larger (fewer rebuilds).  Measured at decode shapes:
-// the attention-merge source is fastest with the default 4.
+// the attention-merge source is fastest with the default 4.  Wide batches whose
+// x slice takes more than 64 KiB of LDS (X_WIDE) run one workgroup per CU, so
+// it has 16 waves: four per SIMD keep enough weight loads in flight, and 16
+// tiles share each staged copy of x (a quarter of the L2 -> LDS traffic of 4).
 #ifndef GRPO_ATTN_WAVES
 #define GRPO_ATTN_WAVES PART_WAVES
 #endif
 __host__ __device__ constexpr int waves_per_group(int xsrc) {
-  return xsrc == X_SILU ? 8 : (xsrc == X_ATTN ? GRPO_ATTN_WAVES : PART_WAVES);
+  return xsrc == X_SILU ? 8 : (xsrc == X_ATTN ? GRPO_ATTN_WAVES : (xsrc == X_WIDE ? 16 : PART_WAVES));
 }
+__host__ __device__ constexpr bool bf16_source(int xsrc) { return xsrc == X_BF16 || xsrc == X_WIDE; }
 constexpr int GU_MAX_SLICES = 2;  // K slices of the gate|up partial sums read while staging
 
 // Columns k..k+7 of row m of bf16(bf16(silu(g)) * u), with g = bf16(sum of the
@@ -336,7 +344,7 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   constexpr int SF = 2;  // SiLU chunks per thread fetched ahead
   SiluFetch sf[SF];
   AttnFetch af;  // one attention chunk per thread fetched ahead
-  if (XSRC == X_BF16) {
+  if (bf16_source(XSRC)) {
     // bf16 x: whole batch entries past the end are skipped (uniform), a partial
     // one re-reads the last chunk (clamped), so no load is predicated.  (The
     // predicated form makes the compiler wait for every weight after staging.)
@@ -387,7 +395,7 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   // chunk is then written twice with the same value); the other sources
   // predicate.  At decode shapes every chunk comes from the loads issued
   // above; larger M stages the rest here, behind the weights.
-  constexpr bool CLAMP = XSRC == X_BF16;
+  constexpr bool CLAMP = bf16_source(XSRC);
   for (int base = 0; base < total; base += 4 * NT) {
     uint4 v[4];
 #pragma unroll
@@ -511,7 +519,7 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg);
 
 bool part_shape_ok(int M, int N, int K, int r, int nseg, int blocksize, const int* seg_end) {
   if (!(M >= 1 && M <= 64 && N > 0 && N % 16 == 0 && K > 0 && K % KSTEP == 0)) return false;
-  if (K > MAX_SLICES * KPW_MAX * KSTEP) return false;  // K <= 32768
+  if (K > MAX_SLICES * KPW_MAX * KSTEP) return false;  // K <= 40960
   if (!(r >= 0 && r <= 16 && nseg >= 1 && nseg <= MAXSEG)) return false;
   if (!pow2(blocksize) || blocksize < 64) return false;
   for (int s = 0; seg_end && s < nseg; ++s)
@@ -538,7 +546,8 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg) {
       pick = c;
       break;
     }
-  while (pick > 1 && (size_t)M * (pick * KSTEP + 8) * 2 > PART_LDS_MAX) {
+  const size_t lds_cap = M > 16 ? PART_LDS_BIG : PART_LDS_MAX;
+  while (pick > 1 && (size_t)M * (pick * KSTEP + 8) * 2 > lds_cap) {
     int lower = 1;
     for (int c : choices)
       if (c < pick) lower = c;
@@ -561,8 +570,8 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg) {
   // partial-sum layout.
   p.mchunk = M;
   const size_t row_bytes = (size_t)p.xstride * 2;
-  if ((size_t)M * row_bytes > PART_LDS_MAX)
-    p.mchunk = 16 * (int)(PART_LDS_MAX / (16 * row_bytes));
+  if ((size_t)M * row_bytes > lds_cap)
+    p.mchunk = 16 * (int)(lds_cap / (16 * row_bytes));
   p.ok = p.mchunk >= 1 && p.S <= MAX_SLICES;
   if (p.mchunk < M) {
     p.MT = p.mchunk / 16;
@@ -580,20 +589,38 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg) {
 // share are fetched from HBM into one L2 only.
 constexpr int NUM_XCD = 8;
 
+// Lets an instantiation use more than 64 KiB of dynamic LDS (once per kernel).
+template <typename Kern>
+int allow_big_lds(Kern kernel) {
+  static const int rc = hip_check(
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, PART_LDS_BIG),
+      "hipFuncSetAttribute");
+  return rc;
+}
+
+template <int MT, int KPW, int XSRC>
+int launch_part_k(const PartArgs& a, const PartPlan& pl, const dim3& grid, const dim3& block,
+                  hipStream_t st) {
+  if (pl.lds > (size_t)PART_LDS_MAX)
+    if (int rc = allow_big_lds(nf4_part_mfma<MT, KPW, XSRC>)) return rc;
+  nf4_part_mfma<MT, KPW, XSRC><<<grid, block, pl.lds, st>>>(a);
+  return launch_check("nf4_part_mfma");
+}
+
 template <int MT, int XSRC>
 int launch_part(const PartArgs& a, const PartPlan& pl, hipStream_t st) {
   constexpr int WPG = waves_per_group(XSRC);
   const int groups = (int)cdiv(pl.ntiles, WPG);
   const dim3 grid((unsigned)(cdiv(groups, NUM_XCD) * NUM_XCD), (unsigned)pl.S), block(64 * WPG);
   switch (pl.kpw) {
-    case 1: nf4_part_mfma<MT, 1, XSRC><<<grid, block, pl.lds, st>>>(a); break;
-    case 2: nf4_part_mfma<MT, 2, XSRC><<<grid, block, pl.lds, st>>>(a); break;
-    case 3: nf4_part_mfma<MT, 3, XSRC><<<grid, block, pl.lds, st>>>(a); break;
-    case 4: nf4_part_mfma<MT, 4, XSRC><<<grid, block, pl.lds, st>>>(a); break;
-    case 6: nf4_part_mfma<MT, 6, XSRC><<<grid, block, pl.lds, st>>>(a); break;
-    default: nf4_part_mfma<MT, 8, XSRC><<<grid, block, pl.lds, st>>>(a); break;
+    case 1: return launch_part_k<MT, 1, XSRC>(a, pl, grid, block, st);
+    case 2: return launch_part_k<MT, 2, XSRC>(a, pl, grid, block, st);
+    case 3: return launch_part_k<MT, 3, XSRC>(a, pl, grid, block, st);
+    case 4: return launch_part_k<MT, 4, XSRC>(a, pl, grid, block, st);
+    case 6: return launch_part_k<MT, 6, XSRC>(a, pl, grid, block, st);
+    default: return launch_part_k<MT, 8, XSRC>(a, pl, grid, block, st);
   }
-  return launch_check("nf4_part_mfma");
 }
 
 // Attention-output source of x (o_proj of the decode step), or all-null.
@@ -686,10 +713,18 @@ int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* 
     c.part = h.part + (int64_t)m0 * h.N;
     c.tpart = h.tpart ? h.tpart + (int64_t)m0 * 16 : nullptr;
     int rc;
-    switch (pl.MT) {
-      case 1: rc = launch_part<1, X_BF16>(c, pl, st); break;
-      case 2: rc = launch_part<2, X_BF16>(c, pl, st); break;
-      default: rc = launch_part<4, X_BF16>(c, pl, st); break;
+    if (pl.lds > (size_t)PART_LDS_MAX) {
+      switch (pl.MT) {
+        case 1: rc = launch_part<1, X_WIDE>(c, pl, st); break;
+        case 2: rc = launch_part<2, X_WIDE>(c, pl, st); break;
+        default: rc = launch_part<4, X_WIDE>(c, pl, st); break;
+      }
+    } else {
+      switch (pl.MT) {
+        case 1: rc = launch_part<1, X_BF16>(c, pl, st); break;
+        case 2: rc = launch_part<2, X_BF16>(c, pl, st); break;
+        default: rc = launch_part<4, X_BF16>(c, pl, st); break;
+      }
     }
     if (rc) return rc;
   }
@@ -1107,7 +1142,7 @@ namespace grpo {
 int make_parts(const grpo_linear_parts_t* h, LinParts* d) {
   if (!h) return einval("null parts descriptor");
   if (h->splits < 1 || h->M < 1 || h->N < 1 || h->K < 1) return einval("bad parts dimensions");
-  if (h->splits > MAX_SLICES) return einval("parts: at most 16 K slices");
+  if (h->splits > MAX_SLICES) return einval("parts: at most 20 K slices");
   if (h->nseg < 1 || h->nseg > MAXSEG) return einval("nseg must be in [1, 4]");
   if (h->r < 0 || h->r > 16) return einval("parts: r must be in [0, 16]");
   if (!h->part || (h->r > 0 && !h->tpart)) return einval("parts: null partial-sum buffer");

@@ -122,9 +122,10 @@ __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
 }
 
 // K slices of the q|k|v projection the fused prologue reads: MS = 8 covers
-// the decode shapes up to M = 16 rows; wide batches of long-K models (M = 64 at
-// hidden 3584: 14 slices) take the MS = 16 instantiation.
+// the decode shapes (M = 64 at hidden 3584 plans 7 slices); up to 16 slices
+// take the MS = 16 instantiation.
 constexpr int QKV_SLICES_SMALL = 8;
+constexpr int QKV_SLICES_LARGE = 16;
 
 template <int GQ, bool FUSED, int MS = QKV_SLICES_SMALL>
 __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
@@ -451,25 +452,41 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
 }
 
 // Combine split partials: out = sum_s 2^(m_s - M) O_s / max(sum_s 2^(m_s - M) l_s, 1e-6).
+// Every split's (max, sum) and O values of a thread are loaded before any is
+// used (the fast path has at most MAX_SPLITS splits), so the merge is one
+// memory round trip.
 __global__ void __launch_bounds__(128) paged_attn_merge(AttnArgs p) {
   const int hq = blockIdx.x, b = blockIdx.y;
   const int ctx = seq_ctx(p, b);
   const int nblk = (ctx + p.BS - 1) / p.BS;
-  const int nsplit = nblk > 0 ? (nblk + p.bps - 1) / p.bps : 1;
+  const int nsplit = min(nblk > 0 ? (nblk + p.bps - 1) / p.bps : 1, MAX_SPLITS);
   const int64_t base = ((int64_t)b * p.Hq + hq) * p.S;
+  float2 ml[MAX_SPLITS];
+  float ov[MAX_SPLITS];
+  const int d0 = threadIdx.x;
+#pragma unroll
+  for (int s = 0; s < MAX_SPLITS; ++s)
+    if (s < nsplit) {
+      ml[s] = *reinterpret_cast<const float2*>(p.ws_ml + (base + s) * 2);
+      if (d0 < p.D) ov[s] = p.ws_o[(base + s) * p.D + d0];
+    }
   float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p.ws_ml[(base + s) * 2]);
+#pragma unroll
+  for (int s = 0; s < MAX_SPLITS; ++s)
+    if (s < nsplit) M = fmaxf(M, ml[s].x);
   const bool any = M != -INFINITY;  // false only if every block id was invalid
-  float L = 0.f;
-  if (any)
-    for (int s = 0; s < nsplit; ++s)
-      L += exp2f(p.ws_ml[(base + s) * 2] - M) * p.ws_ml[(base + s) * 2 + 1];
+  float L = 0.f, w[MAX_SPLITS];
+#pragma unroll
+  for (int s = 0; s < MAX_SPLITS; ++s) {
+    w[s] = any && s < nsplit ? exp2f(ml[s].x - M) : 0.f;
+    if (s < nsplit) L += w[s] * ml[s].y;
+  }
   const float den = fmaxf(L, 1e-6f);
-  for (int d = threadIdx.x; d < p.D; d += blockDim.x) {
+  for (int d = d0; d < p.D; d += blockDim.x) {
     float O = 0.f;
-    if (any)
-      for (int s = 0; s < nsplit; ++s)
-        O += exp2f(p.ws_ml[(base + s) * 2] - M) * p.ws_o[(base + s) * p.D + d];
+#pragma unroll
+    for (int s = 0; s < MAX_SPLITS; ++s)
+      if (s < nsplit) O += w[s] * (d == d0 ? ov[s] : p.ws_o[(base + s) * p.D + d]);
     store_out(p, ((int64_t)b * p.Hq + hq) * p.D + d, O / den);
   }
 }
@@ -588,7 +605,7 @@ int launch_split(const AttnArgs& a, hipStream_t st) {
   const dim3 grid(a.S, a.Hkv, a.B);
   if constexpr (FUSED) {
     if (a.qkv.S > QKV_SLICES_SMALL) {
-      paged_attn_split<GQ, FUSED, MAX_SLICES><<<grid, AT, lds, st>>>(a);
+      paged_attn_split<GQ, FUSED, QKV_SLICES_LARGE><<<grid, AT, lds, st>>>(a);
       return launch_check("paged_attn_split");
     }
   }
@@ -720,8 +737,9 @@ extern "C" int grpo_paged_attn_decode_qkv(const grpo_linear_parts_t* qkv, int Hq
     return GRPO_EUNSUPPORTED;
   }
   if (a.qkv.N != (Hq + 2 * Hkv) * D) return einval("qkv width must be (Hq + 2 Hkv) * D");
-  if (a.qkv.S > MAX_SLICES) {
-    set_error("fused q|k|v attention reads at most %d K slices of the projection", MAX_SLICES);
+  if (a.qkv.S > QKV_SLICES_LARGE) {
+    set_error("fused q|k|v attention reads at most %d K slices of the projection",
+              QKV_SLICES_LARGE);
     return GRPO_EUNSUPPORTED;
   }
   if (!cos_table || !sin_table || !append_pos || !context_lens || !k_cache || !v_cache ||
@@ -813,6 +831,40 @@ extern "C" int grpo_paged_attn_decode_noalloc(const void* q, int64_t q_stride_b,
                                 block_tables, bt_stride, context_lens, out, out_bf16, B, Hq, Hkv,
                                 D, block_size, max_blocks, scale, ws,
                                 need > 0 ? NOALLOC_SCRATCH_BYTES : 0, stream);
+}
+
+extern "C" int grpo_paged_attn_merge(const void* attn_workspace, const int32_t* context_lens,
+                                     int B, int Hq, int Hkv, int D, int block_size,
+                                     int max_blocks, void* out, int out_bf16,
+                                     grpo_stream_t stream) {
+  if (B < 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || max_blocks <= 0)
+    return einval("bad attention dimensions");
+  if (B == 0) return GRPO_OK;
+  const AttnPlan plan = plan_attn(B, Hq, Hkv, D, block_size, max_blocks);
+  if (!plan.fast) {
+    set_error("the split partials exist only on the fast path (head_dim 128, block size 16, "
+              "Hq/Hkv <= 8)");
+    return GRPO_EUNSUPPORTED;
+  }
+  if (!attn_workspace || !context_lens || !out) return einval("null pointer");
+  if ((reinterpret_cast<uintptr_t>(attn_workspace) & 15u) != 0)
+    return einval("attention workspace must be 16-byte aligned");
+  AttnArgs a{};
+  a.cl = context_lens;
+  a.out = out;
+  a.out_bf16 = out_bf16;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.D = D;
+  a.BS = block_size;
+  a.max_blocks = max_blocks;
+  a.bps = plan.bps;
+  a.S = plan.S;
+  a.ws_o = static_cast<float*>(const_cast<void*>(attn_workspace));
+  a.ws_ml = a.ws_o + (size_t)B * Hq * plan.S * D;
+  paged_attn_merge<<<dim3(Hq, B), 128, 0, as_stream(stream)>>>(a);
+  return launch_check("paged_attn_merge");
 }
 
 namespace grpo {

@@ -125,6 +125,8 @@ SIGNATURES = {
         [_VP, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32,
          _I32, _F32, _VP, _SZ, _VP],
     ),
+    "grpo_paged_attn_merge": (_I32, [_VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32, _VP, _I32,
+                                     _VP]),
     "grpo_paged_attn_noalloc_max_bytes": (_SZ, []),
     "grpo_paged_attn_decode_noalloc": (
         _I32,

@@ -95,6 +95,8 @@ class DecodeEngine:
         self.x = torch.zeros(B, H, **bf)
         self.act = torch.zeros(B, self.I, **bf)
         self.logits = torch.zeros(B, self.V, **bf)
+        self.attn_out = torch.zeros(B, self.Hq * D, **bf) if B > self.ATTN_STAGE_MAX_ROWS \
+            else None
         self.next = torch.zeros(B, dtype=torch.int64, device=dev)
         self._prepare_layers()
         self.graph: Optional[torch.cuda.CUDAGraph] = None
@@ -212,6 +214,8 @@ class DecodeEngine:
         return (n * self.Hkv * self.D * 2 * 2 + self.B * self.Hq * self.D * 2 * 2 + nblk * 4)
 
     NF4_KINDS = ("qkv", "o", "gate_up", "down")
+    # Rows up to which o_proj merges the attention splits while staging x.
+    ATTN_STAGE_MAX_ROWS = 16
 
     def launches(self) -> list:
         """[(kind, launch())] of one forward pass, in order, bound to torch's
@@ -275,6 +279,25 @@ class DecodeEngine:
         lib, chk, pool = self.lib, _lib.check, self.pool
         Hq, Hkv, D = self.Hq, self.Hkv, self.D
         wsa, wsa_n = self.ws_attn.data_ptr(), self.ws_attn.numel()
+        attention = ("attention", lambda: chk(lib.grpo_paged_attn_decode_qkv(
+            L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
+            self.max_pos, self.append_pos.data_ptr(), self.attn_len.data_ptr(), kc, vc,
+            pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
+            pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n, st),
+            "attention"))
+        if self.B > self.ATTN_STAGE_MAX_ROWS:
+            # wide batches: merge the splits once into bf16 rows; o_proj stages
+            # them as plain x (merging while staging repeats the merge in every
+            # workgroup of a K slice: ~0.4 GB of partial-sum reads at 64 rows)
+            ao = self.attn_out.data_ptr()
+            return [
+                attention,
+                ("attn_merge", lambda: chk(lib.grpo_paged_attn_merge(
+                    wsa, self.attn_len.data_ptr(), self.B, Hq, Hkv, D, pool.block_size,
+                    self.max_blocks, ao, 1, st), "attn_merge")),
+                ("o", lambda: chk(lib.grpo_nf4_linear_partials(
+                    ao, Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
+                    L["o_code"].data_ptr(), self.bs, L["o_la"], L["o_parts"], st), "o_proj"))]
         return [
             ("attention", lambda: chk(lib.grpo_paged_attn_decode_qkv(
                 L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),

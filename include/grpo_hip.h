@@ -208,6 +208,17 @@ int grpo_paged_attn_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h
                            int Hkv, int D, int block_size, int max_blocks, float scale,
                            void* workspace, size_t workspace_bytes, grpo_stream_t stream);
 
+/* Merge of the split partials grpo_paged_attn_decode_qkv left in
+ * attn_workspace (same B, Hq, Hkv, D, block_size, max_blocks and
+ * context_lens) into out [B, Hq, D] (float32, or bf16 when out_bf16 != 0):
+ * out = sum_s 2^(m_s - M) O_s / max(sum_s 2^(m_s - M) l_s, 1e-6), the
+ * normalisation of _paged_attention_decode_kernel
+ * (src/triton_kernels/paged_kv.py:243-251).  For wide batches, whose o_proj
+ * then reads the merged bf16 rows instead of merging the splits while staging. */
+int grpo_paged_attn_merge(const void* attn_workspace, const int32_t* context_lens, int B, int Hq,
+                          int Hkv, int D, int block_size, int max_blocks, void* out, int out_bf16,
+                          grpo_stream_t stream);
+
 /* Allocation-free variant of grpo_paged_attn_decode: no counterpart in the
  * reference.  For callers that cannot allocate device memory or pass a
  * workspace (code under HIP graph capture, tight serving loops, harnesses that
