@@ -40,6 +40,7 @@ constexpr int AW = 8;          // waves per workgroup
 constexpr int AT = 64 * AW;    // threads per workgroup
 constexpr int MAX_SPLITS = ATTN_MAX_SPLITS;  // context splits per (sequence, KV head)
 constexpr float LOG2E = 1.4426950408889634f;
+constexpr int ATTN_DEVICE_CUS = 256;  // MI355X
 
 struct AttnArgs {
   const uint16_t* q;
@@ -64,6 +65,9 @@ struct AttnArgs {
   const uint16_t* sin_t;
   int max_pos;
   const int32_t* append_pos;
+  // one split per (sequence, KV head): the split writes the normalised bf16
+  // output [B][Hq][D] here instead of partials (null otherwise)
+  uint16_t* direct_out;
 };
 
 struct AttnPlan {
@@ -81,7 +85,15 @@ AttnPlan plan_attn(int B, int Hq, int Hkv, int D, int BS, int max_blocks) {
     return p;
   }
   const int mb = max_blocks > 0 ? max_blocks : 1;
-  const int bpw = (int)cdiv(mb, (int64_t)AW * MAX_SPLITS);
+  // Context splits per (sequence, KV head): up to MAX_SPLITS while the
+  // (sequence, KV head) pairs alone leave CUs idle; one split once they fill
+  // the device.  The workgroup needs ~150 VGPRs per lane, so one workgroup of
+  // 8 waves runs per CU: every extra round of workgroups repeats the
+  // prologue and the wave merge, and at B * Hkv >= 256 (config 5: 64 rows x 4
+  // KV heads) a single split per pair measured fastest (73 us against 77 at 2
+  // splits and 82 at 8, 4096-token contexts).
+  const int target = (int64_t)B * Hkv >= ATTN_DEVICE_CUS ? 1 : MAX_SPLITS;
+  const int bpw = (int)cdiv(mb, (int64_t)AW * target);
   // one thread per block-table entry of a split: bps <= AT (contexts <= 64K)
   if (AW * bpw > AT) {
     p.fast = false;
@@ -115,6 +127,12 @@ __device__ __forceinline__ void store_out(const AttnArgs& p, int64_t idx, float 
 __device__ __forceinline__ void wave_sync() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_wave_barrier();
+}
+
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ s16x4_t as_s16x4(uint2 v) { return __builtin_bit_cast(s16x4_t, v); }
+__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
+  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
 }
 
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
@@ -354,23 +372,37 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
     m_run = m_new;
     *reinterpret_cast<float4*>(&sP[wave][ln][4 * lg]) = make_float4(pv[0], pv[1], pv[2], pv[3]);
     wave_sync();
-    // P.V on v_mfma_f32_16x16x4_f32 (float32 products and sums, as the
-    // reference's float32 p * v): O^T tile i += V^T (16 d x 4 tokens) . P
-    // (4 tokens x 16 heads) over tokens 4s + lg, s = 0..3.  Lane (ln, lg)
-    // gives A = V[4s + lg][8*ln + i] (element i of vf[s]) and B = P[4s + lg][ln];
-    // the rescale by this lane's head's corr comes first.
+    // P.V on bf16 MFMA with P split in two bf16 terms, P = P_hi + P_lo + e,
+    // |e| <= 2^-17 |P|: V is bf16, so V.P_hi and V.P_lo are exact float32
+    // products summed in float32 (the reference's float32 p * v up to e), at
+    // 16 v_mfma_f32_16x16x16_bf16 per block instead of 32 float32 16x16x4
+    // (an eighth of the matrix-core cycles).  O^T tile i += V^T (16 d x 16
+    // tokens) . P (16 tokens x 16 heads); MFMA k = 4*lg + s is token 4s + lg:
+    // lane (ln, lg) gives A = V[4s + lg][8*ln + i] (element i of vf[s]) and
+    // B = P[4s + lg][head ln], s = 0..3.  The rescale by this lane's head's
+    // corr comes first.
     float pb[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) pb[q] = sP[wave][ln][4 * q + lg];
+    uint2 bh, bl;
+    {
+      const uint32_t h01 = pack_bf2(pb[0], pb[1]), h23 = pack_bf2(pb[2], pb[3]);
+      bh = make_uint2(h01, h23);
+      bl = make_uint2(pack_bf2(pb[0] - bf_lo(h01), pb[1] - bf_hi(h01)),
+                      pack_bf2(pb[2] - bf_lo(h23), pb[3] - bf_hi(h23)));
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) oacc[i] *= corr;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const uint32_t vw[4] = {vf[q].x, vf[q].y, vf[q].z, vf[q].w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        oacc[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(
-            (i & 1) ? bf_hi(vw[i >> 1]) : bf_lo(vw[i >> 1]), pb[q], oacc[i], 0, 0, 0);
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
+      const uint32_t w0 = word(vf[0], i >> 1), w1 = word(vf[1], i >> 1);
+      const uint32_t w2 = word(vf[2], i >> 1), w3 = word(vf[3], i >> 1);
+      const uint2 a = make_uint2(perm(w1, w0, sel), perm(w3, w2, sel));
+      oacc[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s16x4(a), as_s16x4(bh), oacc[i], 0,
+                                                          0, 0);
+      oacc[i] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(as_s16x4(a), as_s16x4(bl), oacc[i], 0,
+                                                          0, 0);
     }
     wave_sync();
   };
@@ -417,6 +449,7 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
   // Per head (one thread each): the split's max M, the waves' weights
   // 2^(m_w - M) and the split's sum L; then O four columns per thread.
   __shared__ float sF[AW][GQ];
+  __shared__ float sDen[GQ];
   if (tid < GQ) {
     const int h = tid;
     float M = -INFINITY;
@@ -430,8 +463,12 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
       L += f * sL[w][h];
     }
     const int64_t slot = ((int64_t)b * p.Hq + kvh * GQ + h) * p.S + s;
-    p.ws_ml[slot * 2] = M;
-    p.ws_ml[slot * 2 + 1] = L;
+    if (p.direct_out) {
+      sDen[h] = fmaxf(L, 1e-6f);
+    } else {
+      p.ws_ml[slot * 2] = M;
+      p.ws_ml[slot * 2 + 1] = L;
+    }
   }
   __syncthreads();
   for (int i = tid; i < GQ * FD / 4; i += AT) {
@@ -446,8 +483,15 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
       O.z += f * v.z;
       O.w += f * v.w;
     }
-    const int64_t slot = ((int64_t)b * p.Hq + kvh * GQ + h) * p.S + s;
-    *reinterpret_cast<float4*>(p.ws_o + slot * FD + d4) = O;
+    if (p.direct_out) {
+      // the whole context in this split: out = O / max(L, 1e-6), bf16
+      const float den = sDen[h];
+      *reinterpret_cast<uint2*>(p.direct_out + ((int64_t)b * p.Hq + kvh * GQ + h) * FD + d4) =
+          make_uint2(pack_bf2(O.x / den, O.y / den), pack_bf2(O.z / den, O.w / den));
+    } else {
+      const int64_t slot = ((int64_t)b * p.Hq + kvh * GQ + h) * p.S + s;
+      *reinterpret_cast<float4*>(p.ws_o + slot * FD + d4) = O;
+    }
   }
 }
 
@@ -725,7 +769,7 @@ extern "C" int grpo_paged_attn_decode_qkv(const grpo_linear_parts_t* qkv, int Hq
                                           void* v_cache, int64_t num_blocks,
                                           const int32_t* block_tables, int64_t bt_stride,
                                           int block_size, int max_blocks, float scale,
-                                          void* workspace, size_t workspace_bytes,
+                                          void* workspace, size_t workspace_bytes, void* out,
                                           grpo_stream_t stream) {
   AttnArgs a{};
   if (int rc = make_parts(qkv, &a.qkv)) return rc;
@@ -764,8 +808,23 @@ extern "C" int grpo_paged_attn_decode_qkv(const grpo_linear_parts_t* qkv, int Hq
   a.sin_t = static_cast<const uint16_t*>(sin_table);
   a.max_pos = max_pos;
   a.append_pos = append_pos;
-  if (int rc = use_workspace(a, plan, workspace, workspace_bytes)) return rc;
+  if (out) {
+    if (plan.S != 1) return einval("direct output needs one context split (grpo_paged_attn_splits)");
+    if ((reinterpret_cast<uintptr_t>(out) & 7u) != 0) return einval("out must be 8-byte aligned");
+    a.direct_out = static_cast<uint16_t*>(out);
+    a.bps = plan.bps;
+    a.S = plan.S;
+  } else if (int rc = use_workspace(a, plan, workspace, workspace_bytes)) {
+    return rc;
+  }
   return launch_split_gq<true>(a, as_stream(stream));
+}
+
+extern "C" int grpo_paged_attn_splits(int B, int Hq, int Hkv, int D, int block_size,
+                                      int max_blocks) {
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || max_blocks <= 0) return 0;
+  const AttnPlan plan = plan_attn(B, Hq, Hkv, D, block_size, max_blocks);
+  return plan.fast ? plan.S : 0;
 }
 
 // ------------------------------------------------- allocation-free entry --

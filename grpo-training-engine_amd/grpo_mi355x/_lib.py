@@ -110,8 +110,9 @@ SIGNATURES = {
     "grpo_paged_attn_decode_qkv": (
         _I32,
         [_PARTS, _I32, _I32, _I32, _VP, _VP, _I32, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I32,
-         _I32, _F32, _VP, _SZ, _VP],
+         _I32, _F32, _VP, _SZ, _VP, _VP],
     ),
+    "grpo_paged_attn_splits": (_I32, [_I32, _I32, _I32, _I32, _I32, _I32]),
     "grpo_nf4_linear_partials_silu": (_I32, [_PARTS, _VP, _VP, _VP, _I32, _PARTS, _VP]),
     "grpo_nf4_gate_up_silu": (
         _I32, [_VP, _I64, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _I64, _VP]),

@@ -179,6 +179,8 @@ class DecodeEngine:
         # workspaces sized before any graph capture
         self.ws_attn = ops.workspace("paged_attn", max(ops.paged_attention_workspace_bytes(
             B, Hq, self.Hkv, D, self.pool.block_size, self.max_blocks), 1), dev)
+        self.attn_splits = int(self.lib.grpo_paged_attn_splits(
+            B, Hq, self.Hkv, D, self.pool.block_size, self.max_blocks))
         self.plans = plans
         # bf16 lm_head GEMV with fused argmax + device-side row advance, when
         # x [B, H] fits the kernel's LDS; otherwise hipBLASLt + argmax + torch ops.
@@ -279,32 +281,29 @@ class DecodeEngine:
         lib, chk, pool = self.lib, _lib.check, self.pool
         Hq, Hkv, D = self.Hq, self.Hkv, self.D
         wsa, wsa_n = self.ws_attn.data_ptr(), self.ws_attn.numel()
+        wide = self.B > self.ATTN_STAGE_MAX_ROWS
+        # one context split: the attention writes its bf16 output itself
+        direct = wide and self.attn_splits == 1
+        ao = self.attn_out.data_ptr() if wide else None
         attention = ("attention", lambda: chk(lib.grpo_paged_attn_decode_qkv(
             L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
             self.max_pos, self.append_pos.data_ptr(), self.attn_len.data_ptr(), kc, vc,
             pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
-            pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n, st),
-            "attention"))
-        if self.B > self.ATTN_STAGE_MAX_ROWS:
-            # wide batches: merge the splits once into bf16 rows; o_proj stages
-            # them as plain x (merging while staging repeats the merge in every
+            pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n,
+            ao if direct else None, st), "attention"))
+        if wide:
+            # wide batches: o_proj stages the merged bf16 rows as plain x
+            # (merging the splits while staging repeats the merge in every
             # workgroup of a K slice: ~0.4 GB of partial-sum reads at 64 rows)
-            ao = self.attn_out.data_ptr()
-            return [
-                attention,
-                ("attn_merge", lambda: chk(lib.grpo_paged_attn_merge(
-                    wsa, self.attn_len.data_ptr(), self.B, Hq, Hkv, D, pool.block_size,
-                    self.max_blocks, ao, 1, st), "attn_merge")),
+            merge = [] if direct else [("attn_merge", lambda: chk(lib.grpo_paged_attn_merge(
+                wsa, self.attn_len.data_ptr(), self.B, Hq, Hkv, D, pool.block_size,
+                self.max_blocks, ao, 1, st), "attn_merge"))]
+            return [attention] + merge + [
                 ("o", lambda: chk(lib.grpo_nf4_linear_partials(
                     ao, Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
                     L["o_code"].data_ptr(), self.bs, L["o_la"], L["o_parts"], st), "o_proj"))]
         return [
-            ("attention", lambda: chk(lib.grpo_paged_attn_decode_qkv(
-                L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
-                self.max_pos, self.append_pos.data_ptr(), self.attn_len.data_ptr(), kc, vc,
-                pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
-                pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n, st),
-                "attention")),
+            attention,
             ("o", lambda: chk(lib.grpo_nf4_linear_partials_attn(
                 wsa, self.attn_len.data_ptr(), Hq, Hkv, D, pool.block_size, self.max_blocks,
                 L["o_w"].data_ptr(), L["o_absmax"].data_ptr(), L["o_code"].data_ptr(), self.bs,

@@ -255,7 +255,14 @@ int grpo_paged_attn_decode_qkv(const grpo_linear_parts_t* qkv, int Hq, int Hkv, 
                                void* k_cache, void* v_cache, int64_t num_blocks,
                                const int32_t* block_tables, int64_t bt_stride, int block_size,
                                int max_blocks, float scale, void* workspace,
-                               size_t workspace_bytes, grpo_stream_t stream);
+                               size_t workspace_bytes, void* out, grpo_stream_t stream);
+
+/* Context splits per (sequence, KV head) that grpo_paged_attn_decode[_qkv]
+ * plans for this shape (0 off the fast path).  When it is 1, the out argument
+ * of grpo_paged_attn_decode_qkv (bf16 [B, Hq * D], 8-byte aligned; NULL
+ * otherwise) receives the normalised attention output directly and no split
+ * partials are written. */
+int grpo_paged_attn_splits(int B, int Hq, int Hkv, int D, int block_size, int max_blocks);
 
 /* grpo_nf4_linear_partials with x = the attention output left by
  * grpo_paged_attn_decode_qkv in attn_workspace (x[b, h*D + d], merged over

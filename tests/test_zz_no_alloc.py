@@ -79,7 +79,8 @@ def test_noalloc_refuses_shapes_beyond_its_array(dev):
     from grpo_mi355x import _lib
 
     lib = _lib.device_library()
-    B, hq, hkv, d, width = 64, 64, 8, 128, 512
+    # the largest partials the fast path plans: 8 splits while B * Hkv < 256
+    B, hq, hkv, d, width = 255, 8, 1, 128, 512
     need = lib.grpo_paged_attn_workspace_bytes(B, hq, hkv, d, 16, width)
     assert need > lib.grpo_paged_attn_noalloc_max_bytes()
     q = torch.zeros((B, hq, d), dtype=torch.bfloat16, device=dev)
