@@ -399,6 +399,25 @@ def _graph_time(fns, dev, reps: int) -> float:
     return e0.elapsed_time(e1) * 1e3 / (reps * len(fns))
 
 
+def _eager_time(fns, dev, reps: int) -> float:
+    """Average µs per call of ``fns`` launched directly (no graph; for
+    profilers whose counter passes cannot follow graph launches)."""
+    import torch
+
+    for fn in fns[:2]:
+        fn()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        for fn in fns:
+            fn()
+    e1.record()
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * len(fns))
+
+
 def _host_cores() -> dict:
     """Host cores (os.cpu_count()) and the BLAS threads numpy uses."""
     blas = None
@@ -457,7 +476,8 @@ def run_cfg1(args):
            for i in inst]
     for _ in range(args.warmup):
         _graph_time(fns, dev, 1)
-    us = _graph_time(fns, dev, max(args.steps, 1) * 5)
+    us = _eager_time(fns, dev, max(args.steps, 1)) if args.eager else \
+        _graph_time(fns, dev, max(args.steps, 1) * 5)
     achieved = call_bytes / (us * 1e-6) / 1e9
     log(f"config 1: {R} rotating instances, {us:.2f} us per call, {achieved:.1f} GB/s")
     cpu = None
@@ -548,7 +568,8 @@ def run_cfg2(args):
                for s in sets]
         for _ in range(args.warmup):
             _graph_time(fns, dev, 1)
-        us = _graph_time(fns, dev, reps)
+        us = _eager_time(fns, dev, max(args.steps, 1)) if args.eager else \
+            _graph_time(fns, dev, reps)
         nb = lin_bytes(n, name != "o")
         per_kind[name] = dict(us_per_call=round(us, 3), bytes_per_call=nb,
                               achieved_GBs=round(nb / (us * 1e-6) / 1e9, 1),

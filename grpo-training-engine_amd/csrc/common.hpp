@@ -119,6 +119,15 @@ __device__ __forceinline__ T load_uniform(const T* ptr) {
   return *(cptr)ptr;
 }
 
+// 16-byte load of data read once per step (NF4 weights, K/V blocks) with the
+// non-temporal hint, so the stream does not evict what other workgroups
+// re-read from L2 (staged x, partial sums, absmax lines).
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream(const void* p) {
+  const u32x4_t v = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 __device__ __forceinline__ f32x4_t mfma16x16x32(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }

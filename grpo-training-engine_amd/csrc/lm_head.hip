@@ -20,6 +20,8 @@ using namespace grpo;
 namespace {
 
 constexpr int LM_KSTEP = 256;
+// lm_head weights are read once per step: loaded with the non-temporal hint
+// (see load_w in nf4_linear.hip).
 #ifndef GRPO_LM_WAVES
 #define GRPO_LM_WAVES 8
 #endif
@@ -96,7 +98,7 @@ __global__ void __launch_bounds__(64 * LM_WAVES) lm_head_argmax_kernel(LmArgs p)
     uint4 w[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      w[j] = *reinterpret_cast<const uint4*>(wrow + ks * LM_KSTEP + 32 * j);
+      w[j] = load_stream(wrow + ks * LM_KSTEP + 32 * j);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
 #pragma unroll

@@ -41,6 +41,9 @@ constexpr int AT = 64 * AW;    // threads per workgroup
 constexpr int MAX_SPLITS = ATTN_MAX_SPLITS;  // context splits per (sequence, KV head)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int ATTN_DEVICE_CUS = 256;  // MI355X
+// K/V blocks: read once per launch, loaded with the non-temporal hint (see
+// load_w in nf4_linear.hip).
+__device__ __forceinline__ uint4 load_kv16(const uint16_t* p) { return load_stream(p); }
 
 struct AttnArgs {
   const uint16_t* q;
@@ -176,8 +179,8 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
     const uint16_t* vb = p.vc + (ph * p.Hkv + kvh) * head_stride;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      kf[i] = *reinterpret_cast<const uint4*>(kb + ln * FD + 8 * lg + 32 * i);
-      vf[i] = *reinterpret_cast<const uint4*>(vb + (4 * i + lg) * FD + 8 * ln);
+      kf[i] = load_kv16(kb + ln * FD + 8 * lg + 32 * i);
+      vf[i] = load_kv16(vb + (4 * i + lg) * FD + 8 * ln);
     }
     return ok;
   };
