@@ -244,6 +244,7 @@ def run_cfg4(args):
     from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
 
     dev = torch.device("cuda:0")
+    copy_calibration(args, dev)
     cfg = Qwen2Config.qwen2_1_5b()
     cfg.num_hidden_layers = args.layers
     rng = np.random.default_rng(args.seed)
@@ -312,6 +313,7 @@ def run_cfg5(args):
     from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
 
     dev = torch.device("cuda:0")
+    copy_calibration(args, dev)
     cfg = Qwen2Config.qwen2_7b()
     cfg.num_hidden_layers = args.layers
     rng = np.random.default_rng(args.seed)
@@ -418,6 +420,23 @@ def _eager_time(fns, dev, reps: int) -> float:
     return e0.elapsed_time(e1) * 1e3 / (reps * len(fns))
 
 
+def copy_calibration(args, dev) -> None:
+    """With --copy-calibration: three float32 multiply kernels that each read and
+    write exactly 256 MiB, the scale reference for the FETCH_SIZE / WRITE_SIZE
+    counters of the same profiler pass."""
+    if not args.copy_calibration:
+        return
+    import torch
+
+    src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+    log("copy calibration: 3 x (read 268435456 B, write 268435456 B) elementwise kernels")
+    del src, dst
+
+
 def _host_cores() -> dict:
     """Host cores (os.cpu_count()) and the BLAS threads numpy uses."""
     blas = None
@@ -448,6 +467,7 @@ def run_cfg1(args):
     from grpo_mi355x.kernels import ops
 
     dev = torch.device("cuda:0")
+    copy_calibration(args, dev)
     B, HQ, HKV, D, BS = 4, 12, 2, 128, 16
     rng = np.random.default_rng(args.seed)
     ctx = rng.integers(512, 1025, B).astype(np.int32)
@@ -533,6 +553,7 @@ def run_cfg2(args):
     from grpo_mi355x.kernels import ops
 
     dev = torch.device("cuda:0")
+    copy_calibration(args, dev)
     M, K, R_, BSZ = 8, 1536, 16, 64
     shapes = dict(q=1536, k=256, v=256, o=1536)
     rng = torch.Generator(device=dev).manual_seed(args.seed)
@@ -696,14 +717,7 @@ def main():
 
     _lib.device_library()
     dev = torch.device("cuda:0")
-    if args.copy_calibration:
-        src = torch.ones(64 << 20, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):  # a float32 multiply kernel: reads 256 MiB, writes 256 MiB
-            torch.mul(src, 1.0, out=dst)
-        torch.cuda.synchronize()
-        log("copy calibration: 3 x (read 268435456 B, write 268435456 B) elementwise kernels")
-        del src, dst
+    copy_calibration(args, dev)
     cfg = Qwen2Config.qwen2_1_5b()
     cfg.num_hidden_layers = args.layers
     G, P, NEW, BS = args.group, args.prompt_len, args.max_new, 16
