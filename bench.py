@@ -158,7 +158,7 @@ def kernel_timing(eng, dev, reps: int = 20) -> dict:
         if kind in eng.NF4_KINDS:
             nb = eng.bytes[kind]
             rec.update(bytes_per_launch=nb, achieved_GBs=round(nb / (us * 1e-6) / 1e9, 1),
-                       splits=eng.plans[kind][0])
+                       splits=eng.splits(kind))
         out[kind] = rec
         del g
     return out

@@ -173,9 +173,19 @@ struct PartArgs {
   // x = SiLU(gate) * up from the gate|up projection's partial sums (down_proj)
   const float* gu_part;  // [gu_S][M][2 * K]
   int gu_S;
+  // x = RMSNorm(h) with the statistic given as per-group sums of squares
+  // (q|k|v of the decode step after nf4_fold_residual)
+  const uint16_t* nh;  // h [M][ldnh] bf16
+  int64_t ldnh;
+  const float* nss;    // [M][nG]: sums of h^2 over column groups
+  int nG;
+  const uint16_t* nw;  // RMSNorm weight [K] bf16
+  float neps;
 };
 
-enum XSource { X_BF16 = 0, X_ATTN = 1, X_SILU = 2, X_WIDE = 3 };  // X_WIDE: bf16, 16 waves
+// X_WIDE: bf16, 16 waves; X_NORM: RMSNorm of h from per-group sums of squares
+enum XSource { X_BF16 = 0, X_ATTN = 1, X_SILU = 2, X_WIDE = 3, X_NORM = 4 };
+constexpr int NORM_MAX_GROUPS = 256;  // sums of squares per row the X_NORM source reads
 
 // n-tiles (waves) per workgroup.  Every workgroup of a K slice rebuilds the x
 // slice it stages; the SiLU source reads 16 bytes of partial sums per element,
@@ -315,6 +325,18 @@ __device__ __forceinline__ uint4 attn_chunk(const PartArgs& p, int m, int k) {
   return attn_finish(p, f);
 }
 
+// Eight columns of the RMSNorm output bf16(bf16(h * inv) * w) (the reference's
+// rounding points, as add_rmsnorm_kernel), h and w in natural order.
+__device__ __forceinline__ uint4 norm8(uint4 hv, uint4 wv, float inv) {
+  const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    o[q] = pack_bf2(round_bf(bf_lo(hw[q]) * inv) * bf_lo(ww[q]),
+                    round_bf(bf_hi(hw[q]) * inv) * bf_hi(ww[q]));
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 template <int MT, int KPW, int XSRC>
 __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(PartArgs p) {
   touch_kernargs<sizeof(PartArgs)>();
@@ -354,7 +376,28 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   constexpr int SF = 2;  // SiLU chunks per thread fetched ahead
   SiluFetch sf[SF];
   AttnFetch af;  // one attention chunk per thread fetched ahead
-  if (bf16_source(XSRC)) {
+  // X_NORM: sums of squares of row tid / 16 (16 threads per row, M <= 16),
+  // then h and the norm weight of this thread's first chunks
+  constexpr int NSS = NORM_MAX_GROUPS / 16;
+  float ssv[NSS];
+  uint4 nwv[4];
+  if (XSRC == X_NORM) {
+    // unconditional loads of clamped indexes (values outside the row's groups
+    // are dropped in the sum): predicated loads here made the compiler copy
+    // the whole array per load and wait for each in turn
+    const float* ssr = p.nss + (int64_t)min(tid >> 4, p.M - 1) * p.nG;
+    const int j = tid & 15;
+#pragma unroll
+    for (int i = 0; i < NSS; ++i) ssv[i] = ssr[min(j + 16 * i, p.nG - 1)];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (u * NT >= total) break;
+      const int i = min(u * NT + tid, total - 1);
+      const int m = i / chunks, c = i - m * chunks;
+      xv[u] = *reinterpret_cast<const uint4*>(p.nh + (int64_t)m * p.ldnh + kbase + 8 * c);
+      nwv[u] = *reinterpret_cast<const uint4*>(p.nw + kbase + 8 * c);
+    }
+  } else if (bf16_source(XSRC)) {
     // bf16 x: whole batch entries past the end are skipped (uniform), a partial
     // one re-reads the last chunk (clamped), so no load is predicated.  (The
     // predicated form makes the compiler wait for every weight after staging.)
@@ -405,7 +448,20 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   // chunk is then written twice with the same value); the other sources
   // predicate.  At decode shapes every chunk comes from the loads issued
   // above; larger M stages the rest here, behind the weights.
-  constexpr bool CLAMP = bf16_source(XSRC);
+  constexpr bool CLAMP = bf16_source(XSRC) || XSRC == X_NORM;
+  __shared__ float sInv[16];
+  if (XSRC == X_NORM) {
+    // 1 / rms of each row: the row's group sums in order per thread, then
+    // across its 16 threads
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NSS; ++i) ss += (tid & 15) + 16 * i < p.nG ? ssv[i] : 0.f;
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);
+    if ((tid & 15) == 0 && (tid >> 4) < p.M)
+      sInv[tid >> 4] = 1.f / sqrtf(ss / (float)p.K + p.neps);
+    __syncthreads();
+  }
   for (int base = 0; base < total; base += 4 * NT) {
     uint4 v[4];
 #pragma unroll
@@ -418,6 +474,12 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
           v[u] = base == 0 && u == 0 ? attn_finish(p, af) : attn_chunk(p, m, kbase + 8 * c);
         else if (XSRC == X_SILU)
           v[u] = base == 0 && u < SF ? silu_finish(p, sf[u]) : silu_chunk(p, m, kbase + 8 * c);
+        else if (XSRC == X_NORM)
+          v[u] = base == 0
+                     ? norm8(xv[u], nwv[u], sInv[m])
+                     : norm8(*reinterpret_cast<const uint4*>(p.nh + (int64_t)m * p.ldnh + kbase +
+                                                             8 * c),
+                             *reinterpret_cast<const uint4*>(p.nw + kbase + 8 * c), sInv[m]);
         else
           v[u] = base == 0 ? xv[u]
                            : *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase +
@@ -651,11 +713,21 @@ struct SiluSource {
   int S = 0;
 };
 
+// RMSNorm source of x (q|k|v of the decode step after nf4_fold_residual), or null.
+struct NormSource {
+  const uint16_t* h = nullptr;
+  int64_t ldh = 0;
+  const float* sumsq = nullptr;
+  int groups = 0;
+  const uint16_t* weight = nullptr;
+  float eps = 0.f;
+};
+
 int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* absmax,
                  const float* code16, int blocksize, const uint16_t* const* la,
                  const grpo_linear_parts_t& h, hipStream_t st, const AttnSource* att = nullptr,
-                 const SiluSource* silu = nullptr) {
-  const bool xsrc = att || silu;
+                 const SiluSource* silu = nullptr, const NormSource* nrm = nullptr) {
+  const bool xsrc = att || silu || nrm;
   if (!part_shape_ok(h.M, h.N, h.K, h.r, h.nseg, blocksize, h.seg_end)) {
     set_error("shape not supported by the split-K NF4 linear");
     return GRPO_EUNSUPPORTED;
@@ -710,6 +782,19 @@ int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* 
       case 2: return launch_part<2, X_ATTN>(a, pl, st);
       default: return launch_part<4, X_ATTN>(a, pl, st);
     }
+  }
+  if (nrm) {
+    if (pl.MT != 1) {
+      set_error("the RMSNorm x source takes at most 16 rows");
+      return GRPO_EUNSUPPORTED;
+    }
+    a.nh = nrm->h;
+    a.ldnh = nrm->ldh;
+    a.nss = nrm->sumsq;
+    a.nG = nrm->groups;
+    a.nw = nrm->weight;
+    a.neps = nrm->eps;
+    return launch_part<1, X_NORM>(a, pl, st);
   }
   if (silu) {
     a.gu_part = silu->part;
@@ -775,7 +860,29 @@ struct GuArgs {
   uint16_t* act;
   int64_t lda;
   int M, I, K;
+  int act_tiles;  // write act in the fold tile layout (fold_tile_index; M <= 8)
 };
+
+// Position of element e (0..7) of an 8-element chunk in the decode8 order
+// [0, 2, 4, 6, 1, 3, 5, 7].
+__host__ __device__ constexpr int il_pos(int e) { return (e >> 1) + 4 * (e & 1); }
+
+// Fold tile layout of an activation [M <= 8][K] read by nf4_fold_residual:
+// for item i = k / 512 and MFMA j = (k / 8) % 8, the 64 lanes' 16-byte A
+// operands are one contiguous 1 KiB block, lane = m + 8 * ((k / 256) % 2) +
+// 16 * ((k / 64) % 4), its 8 elements in the decode8 order.  Rows >= M and
+// columns >= K are never written (the buffer starts zero-filled).
+__host__ __device__ constexpr int64_t fold_tile_index(int m, int k) {
+  return ((int64_t)((k >> 9) * 8 + ((k >> 3) & 7)) * 64 + m + 8 * ((k >> 8) & 1) +
+          16 * ((k >> 6) & 3)) * 8 + il_pos(k & 7);
+}
+
+__device__ __forceinline__ void store_act(const GuArgs& p, int m, int col, float v) {
+  if (p.act_tiles)
+    p.act[fold_tile_index(m, col)] = f2bf(v);
+  else
+    p.act[(int64_t)m * p.lda + col] = f2bf(v);
+}
 
 constexpr int GU_XU = 8;  // x chunks per thread loaded ahead of the weights
 
@@ -882,7 +989,7 @@ __global__ void __launch_bounds__(128 * S) nf4_gate_up_silu(GuArgs p) {
     }
     const float gv = round_bf(g);
     const float o = round_bf(gv * (1.f / (1.f + expf(-gv)))) * round_bf(u);
-    p.act[(int64_t)m * p.lda + t * 16 + n] = f2bf(o);
+    store_act(p, m, t * 16 + n, o);
   }
 }
 
@@ -997,8 +1104,149 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
     }
     const float gv = round_bf(g);
     const float o = round_bf(gv * (1.f / (1.f + expf(-gv)))) * round_bf(u);
-    p.act[(int64_t)m * p.lda + 8 * (g0 + un * G) + n] = f2bf(o);
+    store_act(p, m, 8 * (g0 + un * G) + n, o);
   }
+}
+
+// ------------------------------ down_proj + residual add for M <= 8 rows --
+//
+// h_out[m, n] = bf16(residual[m, n] + bf16(x[m, :] . W[n, :])) (NF4 W, no LoRA,
+// no bias: the MLP's down_proj and the decoder layer's residual add,
+// modeling_qwen2 Qwen2DecoderLayer.forward), and for the next layer's input
+// RMSNorm sumsq[m, g] = sum of h_out[m, n]^2 over the 8 columns n of group g
+// (float32).  The whole K of a column group runs in one workgroup, so the
+// finished rows leave this kernel and the norm needs no launch of its own: the
+// next q|k|v kernel stages RMSNorm(h) from h and these sums (X_NORM).
+//
+// K is folded into the MFMA's rows.  With M <= 8, rows 8..15 of the A operand
+// carry the same x rows over a second K range and B columns 8..15 the same 8
+// weight columns over that range, so one v_mfma_f32_16x16x32_bf16 covers 8
+// columns x 64 K values (the cross quadrants D[0..7][8..15] and D[8..15][0..7]
+// are discarded): every lane decodes weights that are used, and a workgroup
+// needs 8 columns, not 16, which doubles the workgroups that share the decode.
+// Lane (ln, lg) holds column 8t + (ln & 7), x row (ln & 7) and K half
+// ln >> 3: in item i (512 K values) its A and B both cover the 64-value block
+// i*512 + 256*(ln >> 3) + 64*lg over 8 MFMAs (one LUT per item).  x arrives in
+// the fold tile layout (fold_tile_index, written so by the gate|up kernel),
+// where the 64 lanes' A operands of one MFMA are one contiguous 1 KiB block,
+// or natural [M][ldx] (16 bytes per lane from 64 different lines, permuted
+// here: the slow form, for callers without the tile layout).  Waves take
+// items w, w + W, ...; the D quadrants of all waves are summed through LDS in
+// a fixed order.
+struct FoldArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint8_t* w;
+  const float* absmax;
+  const float* code16;
+  int bs_shift;
+  const uint16_t* residual;  // may be null (h_out = y)
+  int64_t ldr;
+  uint16_t* h_out;
+  int64_t ldh;
+  float* sumsq;  // [M][G], G = N / 8
+  int M, N, K, G;
+};
+
+constexpr int FOLD_W = 8;          // waves per workgroup
+constexpr int FOLD_ITEM = 512;     // K values of one item (two 256-value halves)
+constexpr int FOLD_IPW_MAX = 4;    // items per wave (all loads in flight at once): K <= 16384
+
+template <int IPW, bool TILES>
+__global__ void __launch_bounds__(64 * FOLD_W) nf4_fold_residual(FoldArgs p) {
+  __shared__ float red[FOLD_W][2][8][8];  // [wave][K half][row][column]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 15, lg = lane >> 4;
+  const int c = ln & 7, half = ln >> 3;
+  const int t = blockIdx.x;
+  const int n = 8 * t + c;
+  const int items = (p.K + FOLD_ITEM - 1) / FOLD_ITEM;
+  const bool tail = p.K % FOLD_ITEM != 0;  // the last item has its first half only
+
+  // Loads: the epilogue's residual value (wave 0, predicated: issued first,
+  // so it makes no later wait conservative), the codebook (scalar), then per
+  // item the weights, the absmax and x, unconditional (items past the wave's
+  // last re-read the last one; the tail item's missing half re-reads its
+  // first half, and its x is zeroed before use).
+  const int em = tid >> 3, ec = tid & 7;  // epilogue output (row, column) of threads < 64
+  uint16_t rres = 0;
+  if (tid < 64 && p.residual && em < p.M) rres = p.residual[(int64_t)em * p.ldr + 8 * t + ec];
+  float code[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
+  const uint8_t* wrow = p.w + (int64_t)n * (p.K / 2);
+  const uint16_t* xrow = p.x + (int64_t)min(c, p.M - 1) * p.ldx;
+  uint4 wv[2 * IPW], xv[8 * IPW];
+  float av[IPW];
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    const int it = min(wave + FOLD_W * i, items - 1);
+    int kb = it * FOLD_ITEM + 256 * half + 64 * lg;
+    if (kb >= p.K) kb -= 256;
+    const uint4* wp = reinterpret_cast<const uint4*>(wrow + kb / 2);
+    wv[2 * i] = load_w<true>(wp);
+    wv[2 * i + 1] = load_w<true>(wp + 1);
+    av[i] = p.absmax[((int64_t)n * p.K + kb) >> p.bs_shift];
+    if (TILES) {
+      const uint4* xp = reinterpret_cast<const uint4*>(p.x) + (int64_t)it * 8 * 64 + lane;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[8 * i + j] = xp[j * 64];
+    } else {
+      const uint4* xp = reinterpret_cast<const uint4*>(xrow + kb);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[8 * i + j] = xp[j];
+    }
+  }
+
+  f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+  const int my_items = (items - wave + FOLD_W - 1) / FOLD_W;  // may be 0
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    if (i >= my_items) break;
+    if (tail && wave + FOLD_W * i == items - 1 && half) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) xv[8 * i + j] = make_uint4(0, 0, 0, 0);
+    }
+    const Lut lt = make_lut(code, av[i]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint4 a = TILES ? xv[8 * i + j] : deinterleave8(xv[8 * i + j]);
+      acc = mfma16x16x32(a, decode8(word(wv[2 * i + (j >> 2)], j & 3), lt), acc);
+    }
+  }
+  // lane (ln, lg) holds D[4*lg + q][ln]: rows 0..7 of columns 0..7 (lg < 2,
+  // ln < 8) are the first K half, rows 8..15 of columns 8..15 (lg >= 2,
+  // ln >= 8) the second
+  if ((lg >> 1) == half) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) red[wave][half][4 * (lg & 1) + q][c] = acc[q];
+  }
+  __syncthreads();
+  if (tid < 64) {
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < FOLD_W; ++w) sum += red[w][0][em][ec] + red[w][1][em][ec];
+    const float y = round_bf(sum);
+    float hv = 0.f;
+    if (em < p.M) {
+      hv = p.residual ? round_bf(y + bf2f(rres)) : y;
+      p.h_out[(int64_t)em * p.ldh + 8 * t + ec] = f2bf(hv);
+    }
+    float sq = hv * hv;
+    sq += __shfl_xor(sq, 1);
+    sq += __shfl_xor(sq, 2);
+    sq += __shfl_xor(sq, 4);
+    if (ec == 0 && em < p.M) p.sumsq[(int64_t)em * p.G + t] = sq;
+  }
+}
+
+// Shape support of nf4_fold_residual.
+bool fold_ok(int M, int N, int K, int blocksize) {
+  if (M < 1 || M > 8 || N <= 0 || N % 8 || K < KSTEP || K % KSTEP) return false;
+  if (!pow2(blocksize) || blocksize < 64) return false;
+  const int items = (K + FOLD_ITEM - 1) / FOLD_ITEM;
+  return (items + FOLD_W - 1) / FOLD_W <= FOLD_IPW_MAX;
 }
 
 #ifndef GRPO_GU_UNITS_GRID
@@ -1430,10 +1678,117 @@ extern "C" int grpo_nf4_gate_up_silu_supported(int M, int I, int K, int blocksiz
   return plan_gu(M, I, K, blocksize, &pl) ? 1 : 0;
 }
 
+namespace {
+int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                const float* code16, int blocksize, int I, int K, int M, void* act, int64_t lda,
+                int act_tiles, hipStream_t st);
+}  // namespace
+
 extern "C" int grpo_nf4_gate_up_silu(const void* x, int64_t ldx, const uint8_t* w,
                                      const float* absmax, const float* code16, int blocksize,
                                      int I, int K, int M, void* act, int64_t lda,
                                      grpo_stream_t stream) {
+  return run_gate_up(x, ldx, w, absmax, code16, blocksize, I, K, M, act, lda, 0,
+                     as_stream(stream));
+}
+
+extern "C" int grpo_nf4_gate_up_silu_tiles(const void* x, int64_t ldx, const uint8_t* w,
+                                           const float* absmax, const float* code16,
+                                           int blocksize, int I, int K, int M, void* act_tiles,
+                                           grpo_stream_t stream) {
+  if (M > 8) return einval("the fold tile layout holds at most 8 rows");
+  return run_gate_up(x, ldx, w, absmax, code16, blocksize, I, K, M, act_tiles, I, 1,
+                     as_stream(stream));
+}
+
+extern "C" size_t grpo_fold_tiles_elements(int K) {
+  return K > 0 ? (size_t)((K + FOLD_ITEM - 1) / FOLD_ITEM) * FOLD_ITEM * 8 : 0;
+}
+
+extern "C" int grpo_nf4_linear_residual_supported(int M, int N, int K, int blocksize) {
+  return fold_ok(M, N, K, blocksize) ? 1 : 0;
+}
+
+extern "C" int grpo_nf4_linear_residual(const void* x, int64_t ldx, int x_tiles,
+                                        const uint8_t* w, const float* absmax,
+                                        const float* code16, int blocksize, int N, int K, int M,
+                                        const void* residual, int64_t ldr, void* h_out,
+                                        int64_t ldh, float* sumsq, grpo_stream_t stream) {
+  if (!fold_ok(M, N, K, blocksize)) {
+    set_error("shape not supported by the folded NF4 linear (M <= 8, N %% 8 == 0, "
+              "K %% 256 == 0, K <= 16384)");
+    return GRPO_EUNSUPPORTED;
+  }
+  if (!x || !w || !absmax || !code16 || !h_out || !sumsq) return einval("null pointer");
+  if ((!x_tiles && (ldx < K || ldx % 8)) || !aligned16(x) || !aligned16(w))
+    return einval("x and w must be 16-byte aligned with ldx >= K, ldx % 8 == 0");
+  if (ldh < N || (residual && ldr < N)) return einval("ldh / ldr smaller than N");
+  FoldArgs a{};
+  a.x = static_cast<const uint16_t*>(x);
+  a.ldx = ldx;
+  a.w = w;
+  a.absmax = absmax;
+  a.code16 = code16;
+  a.bs_shift = __builtin_ctz((unsigned)blocksize);
+  a.residual = static_cast<const uint16_t*>(residual);
+  a.ldr = ldr;
+  a.h_out = static_cast<uint16_t*>(h_out);
+  a.ldh = ldh;
+  a.sumsq = sumsq;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.G = N / 8;
+  const int ipw = ((K + FOLD_ITEM - 1) / FOLD_ITEM + FOLD_W - 1) / FOLD_W;
+  const dim3 grid((unsigned)(N / 8)), block(64 * FOLD_W);
+  hipStream_t st = as_stream(stream);
+  switch (ipw * 2 + (x_tiles ? 1 : 0)) {
+#define FOLD_CASE(IPW)                                                          \
+  case IPW * 2: nf4_fold_residual<IPW, false><<<grid, block, 0, st>>>(a); break; \
+  case IPW * 2 + 1: nf4_fold_residual<IPW, true><<<grid, block, 0, st>>>(a); break;
+    FOLD_CASE(1) FOLD_CASE(2) FOLD_CASE(3) FOLD_CASE(4)
+#undef FOLD_CASE
+    default:
+      return einval("folded NF4 linear: no instantiation");
+  }
+  return launch_check("nf4_fold_residual");
+}
+
+extern "C" int grpo_nf4_linear_partials_norm(const void* h, int64_t ldh, const float* sumsq,
+                                             int groups, const void* norm_weight, float eps,
+                                             const uint8_t* w, const float* absmax,
+                                             const float* code16, int blocksize,
+                                             const void* const* lora_a,
+                                             const grpo_linear_parts_t* parts,
+                                             grpo_stream_t stream) {
+  if (!parts) return einval("null parts descriptor");
+  if (blocksize <= 0) return einval("blocksize must be > 0");
+  LinParts check;
+  if (int rc = make_parts(parts, &check)) return rc;
+  if (!h || !sumsq || !norm_weight) return einval("null pointer");
+  if (groups < 1 || groups > NORM_MAX_GROUPS) return einval("groups must be in [1, 256]");
+  if (ldh < parts->K || ldh % 8 || !aligned16(h) || !aligned16(norm_weight))
+    return einval("h and norm_weight must be 16-byte aligned with ldh >= K, ldh % 8 == 0");
+  const uint16_t* la[MAXSEG] = {nullptr, nullptr, nullptr, nullptr};
+  if (parts->r > 0) {
+    if (!lora_a) return einval("r > 0 needs lora_a");
+    for (int s = 0; s < parts->nseg; ++s) la[s] = static_cast<const uint16_t*>(lora_a[s]);
+  }
+  NormSource src;
+  src.h = static_cast<const uint16_t*>(h);
+  src.ldh = ldh;
+  src.sumsq = sumsq;
+  src.groups = groups;
+  src.weight = static_cast<const uint16_t*>(norm_weight);
+  src.eps = eps;
+  return run_partials(nullptr, 0, w, absmax, code16, blocksize, la, *parts, as_stream(stream),
+                      nullptr, nullptr, &src);
+}
+
+namespace {
+int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                const float* code16, int blocksize, int I, int K, int M, void* act, int64_t lda,
+                int act_tiles, hipStream_t st) {
   GuPlan pl;
   if (!plan_gu(M, I, K, blocksize, &pl)) {
     set_error("shape not supported by the fused gate|up SiLU kernel");
@@ -1455,7 +1810,7 @@ extern "C" int grpo_nf4_gate_up_silu(const void* x, int64_t ldx, const uint8_t* 
   a.M = M;
   a.I = I;
   a.K = K;
-  hipStream_t st = as_stream(stream);
+  a.act_tiles = act_tiles;
   {
     // units kernel: at most one workgroup per CU, every item of a wave in registers
     const int U = I / 8, KS = K / KSTEP;
@@ -1484,3 +1839,4 @@ extern "C" int grpo_nf4_gate_up_silu(const void* x, int64_t ldx, const uint8_t* 
   }
   return launch_check("nf4_gate_up_silu");
 }
+}  // namespace

@@ -11,10 +11,10 @@
 // of v_mfma_f32_16x16x32_bf16 (rows = tokens) against the B operand Q^T of all
 // query heads of the GQA group (columns = heads), giving S^T[token][head] in 4
 // MFMAs.  The online softmax runs in the exp2 domain; P goes through a
-// per-wave LDS slot; P.V runs on float32 MFMA (v_mfma_f32_16x16x4_f32: O^T
-// tiles of 16 head-dimension rows x 16 heads), every V element loaded once and
-// applied to all heads of the group, each lane ending with distinct outputs
-// (no cross-lane sums).  The 8 waves
+// per-wave LDS slot; P.V runs on bf16 MFMA with P split into two bf16 terms
+// (v_mfma_f32_16x16x16_bf16: O^T tiles of 16 head-dimension rows x 16 heads),
+// every V element loaded once and applied to all heads of the group, each lane
+// ending with distinct outputs (no cross-lane sums).  The 8 waves
 // merge through LDS and every split writes (max, sum, unnormalised O): the
 // standalone entry point merges them in a second kernel, the decode step merges
 // them while the o_proj kernel stages its input (linear_parts.hpp, nf4_linear.hip).

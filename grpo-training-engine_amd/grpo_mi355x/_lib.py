@@ -117,6 +117,15 @@ SIGNATURES = {
     "grpo_nf4_gate_up_silu": (
         _I32, [_VP, _I64, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _I64, _VP]),
     "grpo_nf4_gate_up_silu_supported": (_I32, [_I32, _I32, _I32, _I32]),
+    "grpo_nf4_gate_up_silu_tiles": (
+        _I32, [_VP, _I64, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _VP]),
+    "grpo_fold_tiles_elements": (_SZ, [_I32]),
+    "grpo_nf4_linear_residual": (
+        _I32, [_VP, _I64, _I32, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _I64, _VP, _I64,
+               _VP, _VP]),
+    "grpo_nf4_linear_residual_supported": (_I32, [_I32, _I32, _I32, _I32]),
+    "grpo_nf4_linear_partials_norm": (
+        _I32, [_VP, _I64, _VP, _I32, _VP, _F32, _VP, _VP, _VP, _I32, _VP, _PARTS, _VP]),
     "grpo_nf4_linear_partials_attn": (
         _I32,
         [_VP, _VP, _I32, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _I32, _VP, _PARTS, _VP],

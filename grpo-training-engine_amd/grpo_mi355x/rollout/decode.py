@@ -199,6 +199,18 @@ class DecodeEngine:
         # launch of its own.
         self.gu_fused = bool(self.lib.grpo_nf4_gate_up_silu_supported(B, I, H, bs))
         self.fuse_silu = not self.gu_fused and plans["gate_up"][0] <= 2
+        # Decode batches of <= 8 rows: down_proj finishes its own columns (the
+        # residual add and per-8-column sums of squares in the same launch), and
+        # the next q|k|v kernel stages the input RMSNorm from h and those sums,
+        # so the step has no input-norm launch after layer 0.
+        self.fold = (self.FOLD_DOWN and self.gu_fused and H % 8 == 0
+                     and H // 8 <= self.NORM_MAX_GROUPS
+                     and bool(self.lib.grpo_nf4_linear_residual_supported(B, H, I, bs)))
+        self.ss = torch.zeros(B, max(H // 8, 1), dtype=torch.float32, device=dev)
+        # down_proj's input in the fold tile layout (zero-filled: rows >= B and
+        # columns >= I stay zero)
+        self.act_tiles = torch.zeros(int(self.lib.grpo_fold_tiles_elements(I)) if self.fold
+                                     else 1, dtype=torch.bfloat16, device=dev)
         nf4 = lambda n, k: n * k // 2 + n * k // bs * 4
         # Algorithmic HBM bytes of each NF4 launch: packed weight + absmax +
         # LoRA A + x + the float32 partial sums written (the fused gate|up
@@ -207,6 +219,13 @@ class DecodeEngine:
                       + plans[kind][2] for kind, (n, k, rr, nseg) in shapes.items()}
         if self.gu_fused:
             self.bytes["gate_up"] = nf4(2 * I, H) + B * H * 2 + B * I * 2
+        if self.fold:
+            # weight + absmax + x + residual read + h written + sums of squares
+            self.bytes["down"] = nf4(H, I) + B * I * 2 + 2 * B * H * 2 + B * (H // 8) * 4
+
+    def splits(self, kind: str) -> int:
+        """K slices of an NF4 launch kind (1 for the folded down_proj)."""
+        return 1 if kind == "down" and self.fold else self.plans[kind][0]
 
     # -------------------------------------------------------------- launch --
     def attention_bytes(self) -> int:
@@ -218,6 +237,9 @@ class DecodeEngine:
     NF4_KINDS = ("qkv", "o", "gate_up", "down")
     # Rows up to which o_proj merges the attention splits while staging x.
     ATTN_STAGE_MAX_ROWS = 16
+    # grpo_nf4_linear_residual + grpo_nf4_linear_partials_norm for <= 8 rows
+    FOLD_DOWN = True
+    NORM_MAX_GROUPS = 256  # sums of squares per row the q|k|v norm staging reads
 
     def launches(self) -> list:
         """[(kind, launch())] of one forward pass, in order, bound to torch's
@@ -232,22 +254,34 @@ class DecodeEngine:
         prev = None
         for li, L in enumerate(self.layers):
             kc, vc = (t.data_ptr() for t in pool.layer(li))
+            q = L["qkv"]
             if prev is None:
                 out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm(
                     h, None, None, L["in_norm"].data_ptr(), x, B, H, L["eps"], st), "rmsnorm")))
-            else:
+            elif not self.fold:
                 out.append(("rmsnorm", lambda L=L, P=prev: chk(lib.grpo_add_rmsnorm_parts(
                     P["down_parts"], h, h, L["in_norm"].data_ptr(), x, L["eps"], st),
                     "add_rmsnorm")))
-            q = L["qkv"]
-            out.append(("qkv", lambda q=q, L=L: chk(lib.grpo_nf4_linear_partials(
-                x, H, q.packed.data_ptr(), q.absmax.data_ptr(), q.code.data_ptr(), self.bs,
-                L["la"], L["qkv_parts"], st), "qkv")))
+            if prev is not None and self.fold:
+                ss = self.ss.data_ptr()
+                out.append(("qkv", lambda q=q, L=L, ss=ss: chk(lib.grpo_nf4_linear_partials_norm(
+                    h, H, ss, H // 8, L["in_norm"].data_ptr(), L["eps"], q.packed.data_ptr(),
+                    q.absmax.data_ptr(), q.code.data_ptr(), self.bs, L["la"], L["qkv_parts"],
+                    st), "qkv")))
+            else:
+                out.append(("qkv", lambda q=q, L=L: chk(lib.grpo_nf4_linear_partials(
+                    x, H, q.packed.data_ptr(), q.absmax.data_ptr(), q.code.data_ptr(), self.bs,
+                    L["la"], L["qkv_parts"], st), "qkv")))
             out += self._attn_launches(L, kc, vc, st)
             out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm_parts(
                 L["o_parts"], h, h, L["post_norm"].data_ptr(), x, L["eps"], st), "post_norm")))
             g = L["gu"]
-            if self.gu_fused:
+            if self.fold:
+                # act in the tile layout the folded down_proj loads
+                out.append(("gate_up", lambda g=g: chk(lib.grpo_nf4_gate_up_silu_tiles(
+                    x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
+                    I, H, B, self.act_tiles.data_ptr(), st), "gate_up")))
+            elif self.gu_fused:
                 out.append(("gate_up", lambda g=g: chk(lib.grpo_nf4_gate_up_silu(
                     x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
                     I, H, B, self.act.data_ptr(), I, st), "gate_up")))
@@ -255,7 +289,12 @@ class DecodeEngine:
                 out.append(("gate_up", lambda g=g, L=L: chk(lib.grpo_nf4_linear_partials(
                     x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
                     None, L["gu_parts"], st), "gate_up")))
-            if self.gu_fused:
+            if self.fold:
+                out.append(("down", lambda L=L: chk(lib.grpo_nf4_linear_residual(
+                    self.act_tiles.data_ptr(), I, 1, L["down_w"].data_ptr(),
+                    L["down_absmax"].data_ptr(), L["down_code"].data_ptr(), self.bs, H, I, B,
+                    h, H, h, H, self.ss.data_ptr(), st), "down")))
+            elif self.gu_fused:
                 out.append(("down", lambda L=L: chk(lib.grpo_nf4_linear_partials(
                     self.act.data_ptr(), I, L["down_w"].data_ptr(),
                     L["down_absmax"].data_ptr(), L["down_code"].data_ptr(), self.bs, None,
@@ -313,9 +352,14 @@ class DecodeEngine:
         """Final norm, lm_head and the token choice with the row advance."""
         lib, chk, B, H = self.lib, _lib.check, self.B, self.H
         h, x = self.h.data_ptr(), self.x.data_ptr()
-        out = [("rmsnorm", lambda P=prev: chk(lib.grpo_add_rmsnorm_parts(
-            P["down_parts"], h, h, self.final_norm.data_ptr(), x, self.final_eps, st),
-            "final_norm"))]
+        if self.fold:  # h is finished: the final norm reads it alone
+            out = [("rmsnorm", lambda: chk(lib.grpo_add_rmsnorm(
+                h, None, None, self.final_norm.data_ptr(), x, B, H, self.final_eps, st),
+                "final_norm"))]
+        else:
+            out = [("rmsnorm", lambda P=prev: chk(lib.grpo_add_rmsnorm_parts(
+                P["down_parts"], h, h, self.final_norm.data_ptr(), x, self.final_eps, st),
+                "final_norm"))]
         if self.sampling:
             if self.lm_fused:
                 out.append(("lm_head", lambda: chk(lib.grpo_lm_head_argmax(

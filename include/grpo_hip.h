@@ -301,6 +301,52 @@ int grpo_nf4_gate_up_silu(const void* x, int64_t ldx, const uint8_t* w, const fl
 /* 1 if grpo_nf4_gate_up_silu takes this shape, else 0. */
 int grpo_nf4_gate_up_silu_supported(int M, int I, int K, int blocksize);
 
+/* grpo_nf4_gate_up_silu writing act (M <= 8 rows) in the fold tile layout that
+ * grpo_nf4_linear_residual reads with x_tiles = 1: bf16 [ceil(I / 512) * 8][64][8]
+ * (grpo_fold_tiles_elements(I) elements), element (m, k) at
+ *   ((k/512 * 8 + (k/8) % 8) * 64 + m + 8 ((k/256) % 2) + 16 ((k/64) % 4)) * 8 + p(k % 8),
+ *   p(e) = e/2 + 4 (e % 2),
+ * so the 16-byte MFMA operands of the 64 lanes of one wave are one contiguous
+ * KiB.  Slots of rows >= M and columns >= I are not written: allocate the
+ * buffer zero-filled. */
+int grpo_nf4_gate_up_silu_tiles(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                                const float* code16, int blocksize, int I, int K, int M,
+                                void* act_tiles, grpo_stream_t stream);
+
+/* Elements (bf16) of a fold tile layout buffer of K columns. */
+size_t grpo_fold_tiles_elements(int K);
+
+/* h_out[m, n] = bf16(residual[m, n] + bf16(x[m] . W[n])) and, for the next
+ * RMSNorm, sumsq[m, g] = sum over n in [8g, 8g + 8) of h_out[m, n]^2 (float32,
+ * G = N / 8 groups per row): the MLP's down_proj (NF4 weight [N, K], no bias,
+ * no LoRA: fused_mlp, fused_ops.py:184-193, with the dequant of
+ * lora_forward.py:171-206) followed by the decoder layer's residual add
+ * (paged_kv.py:791-798) in one launch, for decode batches of M <= 8 rows.
+ * x bf16 [M, ldx] (16-byte aligned, ldx % 8 == 0), or in the fold tile
+ * layout when x_tiles (grpo_nf4_gate_up_silu_tiles; ldx ignored).
+ * residual may be NULL (h_out = y) and may alias h_out.  Shapes: M <= 8,
+ * N % 8 == 0, K % 256 == 0, K <= 16384, power-of-two blocksize >= 64
+ * (grpo_nf4_linear_residual_supported); GRPO_EUNSUPPORTED otherwise. */
+int grpo_nf4_linear_residual(const void* x, int64_t ldx, int x_tiles, const uint8_t* w,
+                             const float* absmax, const float* code16, int blocksize, int N, int K,
+                             int M, const void* residual, int64_t ldr, void* h_out, int64_t ldh,
+                             float* sumsq, grpo_stream_t stream);
+
+/* 1 if grpo_nf4_linear_residual takes this shape, else 0. */
+int grpo_nf4_linear_residual_supported(int M, int N, int K, int blocksize);
+
+/* grpo_nf4_linear_partials with x = RMSNorm(h): x[m, k] = bf16(bf16(h[m, k] *
+ * inv[m]) * norm_weight[k]), inv[m] = 1 / sqrt(sum_g sumsq[m, g] / K + eps), the
+ * sums of squares as grpo_nf4_linear_residual writes them (groups <= 256 per
+ * row).  The decoder layer's input RMSNorm (fused_rmsnorm, fused_ops.py:34-77;
+ * paged_kv.py:706-711) staged by the q|k|v projection's kernel.  h bf16 [M, ldh];
+ * parts->M <= 16. */
+int grpo_nf4_linear_partials_norm(const void* h, int64_t ldh, const float* sumsq, int groups,
+                                  const void* norm_weight, float eps, const uint8_t* w,
+                                  const float* absmax, const float* code16, int blocksize,
+                                  const void* const* lora_a, const grpo_linear_parts_t* parts,
+                                  grpo_stream_t stream);
+
 /* ------------------------------------------------------- decode step --
  * Ops of the model-level decode step around the two hot-path kernels
  * (src/triton_kernels/paged_kv.py:690-820).  bf16 tensors are row-major. */

@@ -1,0 +1,268 @@
+"""The decode step's folded down_proj and its norm-staging consumer, through the C ABI.
+
+``grpo_nf4_linear_residual`` (down_proj + the residual add for <= 8 rows, with
+per-8-column sums of squares) is compared with the oracle linear
+(``oracle.lora_linear.nf4_lora_linear``, pinned by the golden fixtures) followed
+by the bf16 residual add: bf16 tolerance 1e-2 and >= 97 % bit-identical outputs
+(the products are the reference's exactly; only the float32 summation order
+differs).  The sums of squares are checked against float64 sums of the kernel's
+own h (tolerance 1e-6: eight float32 terms).  ``grpo_nf4_linear_partials_norm``
+(q|k|v with x = RMSNorm(h) staged from those sums) is compared with the oracle
+RMSNorm + linear and with the GPU's two-launch path (``grpo_add_rmsnorm`` +
+``grpo_nf4_linear_partials``).  ``grpo_nf4_gate_up_silu_tiles`` must equal
+``grpo_nf4_gate_up_silu`` rearranged into the fold tile layout, bit for bit.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+from oracle.decode import rmsnorm
+from oracle.lora_linear import nf4_lora_linear
+from oracle.nf4 import NF4_CODE, quantize_nf4
+
+from conftest import rel_err
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+IL = np.array([0, 4, 1, 5, 2, 6, 3, 7])  # position of element e of a chunk: (e >> 1) + 4 (e & 1)
+
+
+def _bits(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def _dev(arr, dev):
+    return torch.from_numpy(np.ascontiguousarray(arr)).to(dev)
+
+
+def _dev_bf16(bits, dev):
+    return torch.from_numpy(np.ascontiguousarray(bits).view(np.int16)).view(torch.bfloat16).to(dev)
+
+
+def tile_index(m, k):
+    """Index of element (m, k) in the fold tile layout (the header's formula)."""
+    return (((k // 512) * 8 + (k // 8) % 8) * 64 + m + 8 * ((k // 256) % 2)
+            + 16 * ((k // 64) % 4)) * 8 + IL[k % 8]
+
+
+def tiles(x_bits):
+    """x [M <= 8, K] in the fold tile layout, unwritten slots zero."""
+    m, k = x_bits.shape
+    out = np.zeros(-(-k // 512) * 512 * 8, np.uint16)
+    mm, kk = np.meshgrid(np.arange(m), np.arange(k), indexing="ij")
+    out[tile_index(mm, kk)] = x_bits
+    return out
+
+
+def test_tile_layout_is_a_bijection_onto_1kib_lane_blocks():
+    k = 1024
+    idx = tile_index(*np.meshgrid(np.arange(8), np.arange(k), indexing="ij"))
+    assert np.array_equal(np.sort(idx.reshape(-1)), np.arange(8 * k))
+    # lane (ln, lg) of MFMA j in item i reads x[ln % 8][i*512 + 256 (ln // 8) + 64 lg + 8 j ...]
+    i, j, ln, lg = 1, 5, 11, 2
+    k0 = i * 512 + 256 * (ln // 8) + 64 * lg + 8 * j
+    assert tile_index(ln % 8, k0) // 8 == (i * 8 + j) * 64 + ln + 16 * lg
+    assert [tile_index(3, k0 + e) % 8 for e in range(8)] == [0, 4, 1, 5, 2, 6, 3, 7]
+
+
+RESIDUAL = [
+    # m, n, k, x in the tile layout, residual
+    (8, 1536, 8960, 1, True),    # config 3 down_proj (18 items: a half item at the end)
+    (8, 1536, 8960, 0, True),
+    (1, 64, 256, 0, False),      # one item, first half only; 7 waves without items
+    (5, 96, 768, 1, True),       # 1.5 items
+    (3, 512, 1024, 0, True),     # whole items
+    (8, 256, 16384, 1, True),    # the largest K (4 items per wave)
+    (7, 3584, 2048, 1, False),
+]
+
+
+@pytest.mark.parametrize("m,n,k,il,with_res", RESIDUAL)
+def test_linear_residual_matches_oracle(dev, m, n, k, il, with_res):
+    from grpo_mi355x import _lib
+
+    lib = _lib.device_library()
+    bs = 64
+    assert lib.grpo_nf4_linear_residual_supported(m, n, k, bs) == 1
+    g = np.random.default_rng(m * 131 + n + k + il)
+    x = f32_to_bf16_bits(g.standard_normal((m, k)).astype(np.float32))
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    packed, absmax = quantize_nf4(w, bs)
+    res = f32_to_bf16_bits(g.standard_normal((m, n)).astype(np.float32))
+    x_d = _dev_bf16(tiles(x) if il else x, dev)
+    pk_d, am_d, code_d = _dev(packed, dev), _dev(absmax, dev), _dev(NF4_CODE.astype(np.float32), dev)
+    # h has one row more than M: the kernel must not write it; the residual is
+    # read from and h written to the same buffer, as in the decode step
+    h_d = torch.zeros(m + 1, n, dtype=torch.bfloat16, device=dev)
+    if with_res:
+        h_d[:m] = _dev_bf16(res, dev)
+    ss_d = torch.full((m + 1, n // 8), -1.0, dtype=torch.float32, device=dev)
+    print(f"linear_residual m={m} n={n} k={k} il={il} residual={with_res}", flush=True)
+    _lib.check(lib.grpo_nf4_linear_residual(
+        x_d.data_ptr(), k, il, pk_d.data_ptr(), am_d.data_ptr(), code_d.data_ptr(), bs, n, k, m,
+        h_d.data_ptr() if with_res else None, n, h_d.data_ptr(), n, ss_d.data_ptr(),
+        _lib.stream_handle(dev)), "linear_residual")
+    torch.cuda.synchronize()
+    lin = nf4_lora_linear(x, packed, absmax, n, k, bs)
+    ref = f32_to_bf16_bits(bf16_bits_to_f32(lin) + bf16_bits_to_f32(res)) if with_res else lin
+    hb = _bits(h_d)
+    got = hb[:m]
+    assert np.all(hb[m] == 0)
+    gf, rf = bf16_bits_to_f32(got), bf16_bits_to_f32(ref)
+    assert np.all(np.isfinite(gf))
+    assert rel_err(gf, rf) <= TOL
+    assert np.mean(got == ref) >= 0.97
+    ss = ss_d.cpu().numpy()
+    assert np.all(ss[m] == -1.0)
+    want = (gf.astype(np.float64) ** 2).reshape(m, n // 8, 8).sum(-1)
+    assert np.allclose(ss[:m], want, rtol=1e-6, atol=0)
+
+
+def _qkv_case(g, m, k, segs, r, bs):
+    n = sum(segs)
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    packed, absmax = quantize_nf4(w, bs)
+    bias = f32_to_bf16_bits((g.standard_normal(n) * 0.02).astype(np.float32))
+    a = [f32_to_bf16_bits((g.standard_normal((r, k)) * 0.01).astype(np.float32)) for _ in segs]
+    b = [f32_to_bf16_bits((g.standard_normal((s, r)) * 0.01).astype(np.float32)) for s in segs]
+    return dict(packed=packed, absmax=absmax, bias=bias, a=a, b=b, n=n)
+
+
+def _parts(lib, dev, m, k, c, segs, r, bs, keep):
+    from grpo_mi355x import _lib
+    from grpo_mi355x.kernels import ops
+
+    plan = ops.nf4_linear_plan(m, c["n"], k, r, len(segs), bs)
+    assert plan is not None
+    splits, pbytes, tbytes = plan
+    part = torch.empty(max(pbytes, 16) // 4, dtype=torch.float32, device=dev)
+    tpart = torch.empty(max(tbytes, 16) // 4, dtype=torch.float32, device=dev)
+    bias_d = _dev_bf16(c["bias"], dev)
+    a_d = [_dev_bf16(v, dev) for v in c["a"]]
+    b_d = [_dev_bf16(v, dev) for v in c["b"]]
+    d = _lib.LinearParts()
+    d.part, d.tpart = part.data_ptr(), tpart.data_ptr()
+    d.splits, d.M, d.N, d.K, d.nseg, d.r = splits, m, c["n"], k, len(segs), r
+    end = 0
+    for i, s in enumerate(segs):
+        d.bias[i] = bias_d.data_ptr() + 2 * end
+        end += s
+        d.seg_end[i] = end
+        d.lora_b[i] = b_d[i].data_ptr()
+    d.scaling = 2.0
+    la = (ctypes.c_void_p * len(segs))(*[t.data_ptr() for t in a_d])
+    keep += [part, tpart, bias_d, a_d, b_d, la, d]
+    return d, la
+
+
+@pytest.mark.parametrize("m,k,segs,groups", [(8, 1536, (1536, 256, 256), 192),
+                                              (8, 1536, (1536, 256, 256), 37),
+                                              (1, 512, (512, 128, 128), 64),
+                                              (16, 1024, (256,), 256)])
+def test_partials_norm_matches_oracle_and_the_two_launch_path(dev, m, k, segs, groups):
+    from grpo_mi355x import _lib
+
+    lib = _lib.device_library()
+    st = _lib.stream_handle(dev)
+    bs, r, eps = 64, 16, 1e-6
+    g = np.random.default_rng(m + k + groups)
+    c = _qkv_case(g, m, k, segs, r, bs)
+    h = f32_to_bf16_bits((g.standard_normal((m, k)) * 3).astype(np.float32))
+    nw = f32_to_bf16_bits((1 + 0.1 * g.standard_normal(k)).astype(np.float32))
+    hf = bf16_bits_to_f32(h).astype(np.float64)
+    # sums of squares over an arbitrary partition of each row into `groups` parts
+    cuts = np.linspace(0, k, groups + 1).astype(int)
+    ss = np.stack([np.add.reduceat(hf[i] ** 2, cuts[:-1]) for i in range(m)]).astype(np.float32)
+    keep = []
+    h_d, nw_d, ss_d = _dev_bf16(h, dev), _dev_bf16(nw, dev), _dev(ss, dev)
+    pk_d, am_d = _dev(c["packed"], dev), _dev(c["absmax"], dev)
+    code_d = _dev(NF4_CODE.astype(np.float32), dev)
+    n = c["n"]
+
+    d1, la1 = _parts(lib, dev, m, k, c, segs, r, bs, keep)
+    y1 = torch.zeros(m, n, dtype=torch.bfloat16, device=dev)
+    print(f"partials_norm m={m} k={k} segs={segs} groups={groups}", flush=True)
+    _lib.check(lib.grpo_nf4_linear_partials_norm(
+        h_d.data_ptr(), k, ss_d.data_ptr(), groups, nw_d.data_ptr(), eps, pk_d.data_ptr(),
+        am_d.data_ptr(), code_d.data_ptr(), bs, la1, ctypes.byref(d1), st), "partials_norm")
+    _lib.check(lib.grpo_nf4_linear_finish(ctypes.byref(d1), y1.data_ptr(), n, st), "finish")
+
+    # the two-launch path: RMSNorm kernel, then the bf16-x partials
+    x_d = torch.zeros(m, k, dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.grpo_add_rmsnorm(h_d.data_ptr(), None, None, nw_d.data_ptr(), x_d.data_ptr(),
+                                    m, k, eps, st), "rmsnorm")
+    d2, la2 = _parts(lib, dev, m, k, c, segs, r, bs, keep)
+    y2 = torch.zeros(m, n, dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.grpo_nf4_linear_partials(
+        x_d.data_ptr(), k, pk_d.data_ptr(), am_d.data_ptr(), code_d.data_ptr(), bs, la2,
+        ctypes.byref(d2), st), "partials")
+    _lib.check(lib.grpo_nf4_linear_finish(ctypes.byref(d2), y2.data_ptr(), n, st), "finish")
+    torch.cuda.synchronize()
+
+    x_ref = rmsnorm(h, nw, eps)
+    # the oracle linear segment by segment (each with its bias and LoRA)
+    outs, off = [], 0
+    for i, s in enumerate(segs):
+        pk = c["packed"][off * k // 2:(off + s) * k // 2]
+        am = c["absmax"][off * k // bs:(off + s) * k // bs]
+        outs.append(nf4_lora_linear(x_ref, pk, am, s, k, bs, bias_bits=c["bias"][off:off + s],
+                                    a_bits=c["a"][i], b_bits=c["b"][i], scaling=2.0))
+        off += s
+    ref = np.concatenate(outs, axis=1)
+    got, two = _bits(y1), _bits(y2)
+    assert rel_err(bf16_bits_to_f32(got), bf16_bits_to_f32(ref)) <= TOL
+    assert np.mean(got == ref) >= 0.95
+    # against the two-launch GPU path only the norm's sum order differs
+    assert np.mean(got == two) >= 0.97
+    assert rel_err(bf16_bits_to_f32(got), bf16_bits_to_f32(two)) <= TOL
+
+
+@pytest.mark.parametrize("m,i,k", [(8, 8960, 1536), (8, 17920, 3584), (5, 4112, 512)])
+def test_gate_up_silu_tiles_is_the_tiled_gate_up_silu(dev, m, i, k):
+    from grpo_mi355x import _lib
+
+    lib = _lib.device_library()
+    st = _lib.stream_handle(dev)
+    bs = 64
+    g = np.random.default_rng(m + i + k)
+    x = f32_to_bf16_bits(g.standard_normal((m, k)).astype(np.float32))
+    w = (g.standard_normal((2 * i, k)) * 0.05).astype(np.float32)
+    packed, absmax = quantize_nf4(w, bs)
+    x_d, pk_d, am_d = _dev_bf16(x, dev), _dev(packed, dev), _dev(absmax, dev)
+    code_d = _dev(NF4_CODE.astype(np.float32), dev)
+    plain = torch.zeros(m, i, dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.grpo_nf4_gate_up_silu(x_d.data_ptr(), k, pk_d.data_ptr(), am_d.data_ptr(),
+                                         code_d.data_ptr(), bs, i, k, m, plain.data_ptr(), i, st),
+               "gate_up")
+    n_t = int(lib.grpo_fold_tiles_elements(i))
+    assert n_t == -(-i // 512) * 512 * 8
+    til = torch.zeros(n_t, dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.grpo_nf4_gate_up_silu_tiles(x_d.data_ptr(), k, pk_d.data_ptr(),
+                                               am_d.data_ptr(), code_d.data_ptr(), bs, i, k, m,
+                                               til.data_ptr(), st), "gate_up_tiles")
+    torch.cuda.synchronize()
+    assert np.array_equal(_bits(til), tiles(_bits(plain)))
+
+
+def test_decode_engine_folds_small_batches(dev):
+    """Decode batches of <= 8 rows run the folded down_proj and no input-norm
+    launches after layer 0; wider ones keep the split-K path."""
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine
+    from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
+
+    cfg = Qwen2Config.tiny(layers=3, heads=4, kv_heads=2, head_dim=128, inter=1024, vocab=1024)
+    model = build_random_model(cfg, dev, seed=5)
+    pool = PagedKVPool(3, 64, 2, 128, 16, device=dev)
+    small = DecodeEngine(model, pool, 8, 4)
+    wide = DecodeEngine(model, pool, 12, 4)
+    assert small.fold and not wide.fold
+    kinds = [k for k, _ in small.launches()]
+    assert kinds.count("rmsnorm") == 1 + 3 + 1  # layer 0's input, post-attention, final
+    assert kinds.count("down") == 3
+    kinds_w = [k for k, _ in wide.launches()]
+    assert kinds_w.count("rmsnorm") == 2 * 3 + 1
