@@ -102,13 +102,15 @@ def rollout_bytes(cfg, model, stops, prompt_len, group, block_size=16):
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "nf4_linears_traffic_cfg3.md")
+ATTN_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_attention_cfg1.md")
 
 
-def measured_traffic():
-    """HBM bytes per NF4 launch from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE
-    summary (two counter passes, scaled by a copy kernel of known size), or None."""
+def measured_traffic(path: str = TRAFFIC_FILE):
+    """HBM bytes per launch (per call for config 1) from a committed rocprofv3
+    FETCH_SIZE/WRITE_SIZE summary (two counter passes, scaled by a copy kernel of
+    known size), or None."""
     try:
-        with open(TRAFFIC_FILE) as fh:
+        with open(path) as fh:
             for line in fh:
                 if line.startswith("traffic_bytes_per_launch:"):
                     return int(line.split(":", 1)[1])
@@ -530,7 +532,8 @@ def run_cfg1(args):
                    "context_lens": ctx.tolist(), "instances": R, "parallelism": "single GPU"},
         "us_per_call": round(us, 3), "bytes_per_call": call_bytes,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
-                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                     "traffic": measured_traffic(ATTN_TRAFFIC_FILE),
                      "kernel": "grpo_paged_attn_decode: paged_attn_split + paged_attn_merge "
                                "per call"},
         "cpu_baseline": cpu}), flush=True)
