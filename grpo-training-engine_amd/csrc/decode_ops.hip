@@ -297,6 +297,47 @@ __global__ void __launch_bounds__(PARTS_T) add_rmsnorm_parts_kernel(
   }
 }
 
+// h = bf16(residual + y) for the finished linear output y (the epilogue of
+// linear_parts.hpp) and, for the RMSNorm its consumer stages, sumsq[m, g] = sum
+// of h^2 over the FRS_COLS columns of group g.  One wave per (group, row), so a
+// row's partial sums, LoRA B rows and residual are fetched by N / 256 CUs, not
+// one: the per-row RMSNorm kernel above moved ~90 KB through a single CU per
+// row for o_proj at hidden 1536.
+constexpr int FRS_T = 64;
+constexpr int FRS_COLS = 4 * FRS_T;
+__global__ void __launch_bounds__(FRS_T) finish_residual_sumsq_kernel(
+    LinParts o, const uint16_t* residual, uint16_t* h_out, int64_t ld, float* __restrict__ sumsq,
+    int G) {
+  touch_kernargs<sizeof(LinParts) + 5 * sizeof(void*)>();
+  __shared__ float ts[MAXSEG * 16];
+  const int g = blockIdx.x, m = blockIdx.y;
+  const int n = g * FRS_COLS + 4 * threadIdx.x;
+  const bool ok = n < o.N;
+  Fetch4<> f;
+  uint2 rr = make_uint2(0, 0);
+  if (ok) {
+    lin_fetch4(o, m, n, f);
+    if (residual) rr = *reinterpret_cast<const uint2*>(residual + (int64_t)m * ld + n);
+  }
+  lin_load_t(o, m, ts);
+  __syncthreads();
+  float ss = 0.f;
+  if (ok) {
+    float v[4];
+    lin_finish4(o, ts, f, v);
+    const float r[4] = {bf_lo(rr.x), bf_hi(rr.x), bf_lo(rr.y), bf_hi(rr.y)};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (residual) v[c] = round_bf(v[c] + r[c]);
+      ss += v[c] * v[c];
+    }
+    *reinterpret_cast<uint2*>(h_out + (int64_t)m * ld + n) =
+        make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+  }
+  ss = wave_sum(ss);
+  if (threadIdx.x == 0) sumsq[(int64_t)m * G + g] = ss;
+}
+
 // rope_append_kernel with qkv = the finished q|k|v output of row b; one
 // workgroup per (row, head): q and k heads rotate column pairs (d, d + D/2),
 // v heads are copied to the cache.
@@ -460,6 +501,23 @@ extern "C" int grpo_add_rmsnorm_parts(const grpo_linear_parts_t* x, const void* 
       o, static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(h_out),
       static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(y), eps, vec);
   return launch_check("add_rmsnorm_parts");
+}
+
+extern "C" int grpo_linear_finish_residual(const grpo_linear_parts_t* x, const void* residual,
+                                           void* h_out, int64_t ld, float* sumsq,
+                                           grpo_stream_t stream) {
+  LinParts o;
+  if (int rc = make_parts(x, &o)) return rc;
+  if (!h_out || !sumsq) return einval("null pointer");
+  if (ld < o.N || ld % 4) return einval("ld must be >= N and a multiple of 4");
+  auto a8 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 7u) == 0; };
+  if (!a8(h_out) || (residual && !a8(residual)))
+    return einval("residual and h_out must be 8-byte aligned");
+  const int G = (int)cdiv(o.N, FRS_COLS);
+  finish_residual_sumsq_kernel<<<dim3((unsigned)G, (unsigned)o.M), FRS_T, 0,
+                                 as_stream(stream)>>>(
+      o, static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(h_out), ld, sumsq, G);
+  return launch_check("finish_residual_sumsq");
 }
 
 extern "C" int grpo_qkv_rope_append_parts(const grpo_linear_parts_t* qkv, int Hq, int Hkv, int D,

@@ -325,6 +325,25 @@ __device__ __forceinline__ uint4 attn_chunk(const PartArgs& p, int m, int k) {
   return attn_finish(p, f);
 }
 
+// Sum over each aligned group of 8 lanes (every lane of the group gets it):
+// DPP quad_perm xor 1, xor 2, then the half-row mirror (lane i + lane 7 - i).
+template <int CTRL>
+__device__ __forceinline__ float dpp_f(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_f<0x141>(v);  // row_half_mirror
+  return v;
+}
+// The same over each DPP row of 16 lanes (then the row mirror, lane i + 15 - i).
+__device__ __forceinline__ float sum16(float v) {
+  v = sum8(v);
+  v += dpp_f<0x140>(v);  // row_mirror
+  return v;
+}
+
 // Eight columns of the RMSNorm output bf16(bf16(h * inv) * w) (the reference's
 // rounding points, as add_rmsnorm_kernel), h and w in natural order.
 __device__ __forceinline__ uint4 norm8(uint4 hv, uint4 wv, float inv) {
@@ -456,8 +475,7 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
     float ss = 0.f;
 #pragma unroll
     for (int i = 0; i < NSS; ++i) ss += (tid & 15) + 16 * i < p.nG ? ssv[i] : 0.f;
-#pragma unroll
-    for (int o = 1; o < 16; o <<= 1) ss += __shfl_xor(ss, o);
+    ss = sum16(ss);
     if ((tid & 15) == 0 && (tid >> 4) < p.M)
       sInv[tid >> 4] = 1.f / sqrtf(ss / (float)p.K + p.neps);
     __syncthreads();
@@ -861,7 +879,15 @@ struct GuArgs {
   int64_t lda;
   int M, I, K;
   int act_tiles;  // write act in the fold tile layout (fold_tile_index; M <= 8)
+  // x = RMSNorm(h) from per-group sums of squares, when nh is set (units kernel, M <= 8)
+  const uint16_t* nh;
+  int64_t ldnh;
+  const float* nss;  // [M][nG], nG <= 64
+  int nG;
+  const uint16_t* nw;
+  float neps;
 };
+constexpr int GU_NORM_MAX_GROUPS = 16;  // sums of squares per row (8 lanes x 2)
 
 // Position of element e (0..7) of an 8-element chunk in the decode8 order
 // [0, 2, 4, 6, 1, 3, 5, 7].
@@ -1010,7 +1036,7 @@ constexpr int GUU_XU = 6;  // x chunks per thread loaded before the weights
 #endif
 constexpr int GUU_LA = GRPO_GUU_LA;  // items whose weights are in flight ahead of the one decoded
 
-template <int W, int IPW>
+template <int W, int IPW, bool NORM>
 __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
   constexpr int NTH = 64 * W;
   extern __shared__ __align__(16) uint16_t xs[];  // [M][K + 8] (decode8 order), then tiles
@@ -1036,12 +1062,24 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
 #pragma unroll
   for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
   const int chunks = p.K / 8, total = p.M * chunks;
-  uint4 xv[GUU_XU];
+  // RMSNorm source (NORM): every wave holds the group sums of squares of all
+  // rows, lane l those of row l / 8 (groups l % 8, l % 8 + 8); loaded first,
+  // unconditionally (clamped indexes, dropped in the sum)
+  float ssv[GU_NORM_MAX_GROUPS / 8];
+  if (NORM) {
+    const float* ssr = p.nss + (int64_t)min(lane >> 3, p.M - 1) * p.nG;
+#pragma unroll
+    for (int q = 0; q < GU_NORM_MAX_GROUPS / 8; ++q) ssv[q] = ssr[min((lane & 7) + 8 * q, p.nG - 1)];
+  }
+  const uint16_t* xsrc = NORM ? p.nh : p.x;
+  const int64_t xld = NORM ? p.ldnh : p.ldx;
+  uint4 xv[GUU_XU], nwv[GUU_XU];
 #pragma unroll
   for (int u = 0; u < GUU_XU; ++u) {
     const int i = min(u * NTH + tid, total - 1);
     const int m = i / chunks, c = i - m * chunks;
-    xv[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + 8 * c);
+    xv[u] = *reinterpret_cast<const uint4*>(xsrc + (int64_t)m * xld + 8 * c);
+    if (NORM) nwv[u] = *reinterpret_cast<const uint4*>(p.nw + 8 * c);
   }
   __builtin_amdgcn_sched_barrier(0);
   uint4 wv[2 * IPW];
@@ -1058,14 +1096,26 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
   };
 #pragma unroll
   for (int t = 0; t < GUU_LA && t < IPW; ++t) load_item(t);
+  // lane l: 1 / rms of row l / 8 (the row's sum over its 8 lanes by DPP)
+  float inv_l = 0.f;
+  if (NORM) {
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < GU_NORM_MAX_GROUPS / 8; ++q) ss += (lane & 7) + 8 * q < p.nG ? ssv[q] : 0.f;
+    ss = sum8(ss);
+    inv_l = 1.f / sqrtf(ss / (float)p.K + p.neps);
+  }
   for (int base = 0; base < total; base += GUU_XU * NTH) {
 #pragma unroll
     for (int u = 0; u < GUU_XU; ++u) {
       if (base + u * NTH >= total) break;
       const int i = min(base + u * NTH + tid, total - 1);
       const int m = i / chunks, c = i - m * chunks;
-      const uint4 v = base == 0 ? xv[u]
-                                : *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + 8 * c);
+      uint4 v = base == 0 ? xv[u]
+                          : *reinterpret_cast<const uint4*>(xsrc + (int64_t)m * xld + 8 * c);
+      if (NORM)
+        v = norm8(v, base == 0 ? nwv[u] : *reinterpret_cast<const uint4*>(p.nw + 8 * c),
+                  __shfl(inv_l, 8 * m));
       *reinterpret_cast<uint4*>(xs + m * xstride + 8 * c) = deinterleave8(v);
     }
   }
@@ -1268,6 +1318,23 @@ struct GuPlan {
   int kpw, S, MT;
   size_t lds;
 };
+
+// LDS of nf4_gate_up_units (x, then the item tiles) and whether it takes the
+// shape (units of 8 columns over at most one workgroup per CU, every item of
+// a wave in registers, 64 KiB of LDS).
+size_t units_lds(int M, int I, int K) {
+  const int U = I / 8, KS = K / KSTEP;
+  const int G = std::min(U, g_gu_units_grid);
+  const int nu = (U + G - 1) / G;
+  return (size_t)M * (K + 8) * 2 + (size_t)nu * KS * M * 16 * 4;
+}
+bool units_ok(int M, int I, int K) {
+  if (I <= 0 || I % 8 || K <= 0 || K % KSTEP) return false;
+  const int U = I / 8, KS = K / KSTEP;
+  const int G = std::min(U, g_gu_units_grid);
+  const int nu = (U + G - 1) / G;
+  return (nu * KS + GU_UNITS_W - 1) / GU_UNITS_W <= GU_UNITS_IPW && units_lds(M, I, K) <= 65536;
+}
 
 // Shape support of nf4_gate_up_silu; returns false for shapes it does not take.
 bool plan_gu(int M, int I, int K, int blocksize, GuPlan* pl) {
@@ -1681,7 +1748,7 @@ extern "C" int grpo_nf4_gate_up_silu_supported(int M, int I, int K, int blocksiz
 namespace {
 int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
                 const float* code16, int blocksize, int I, int K, int M, void* act, int64_t lda,
-                int act_tiles, hipStream_t st);
+                int act_tiles, hipStream_t st, const NormSource* nrm = nullptr);
 }  // namespace
 
 extern "C" int grpo_nf4_gate_up_silu(const void* x, int64_t ldx, const uint8_t* w,
@@ -1699,6 +1766,31 @@ extern "C" int grpo_nf4_gate_up_silu_tiles(const void* x, int64_t ldx, const uin
   if (M > 8) return einval("the fold tile layout holds at most 8 rows");
   return run_gate_up(x, ldx, w, absmax, code16, blocksize, I, K, M, act_tiles, I, 1,
                      as_stream(stream));
+}
+
+extern "C" int grpo_nf4_gate_up_silu_tiles_norm(const void* h, int64_t ldh, const float* sumsq,
+                                                int groups, const void* norm_weight, float eps,
+                                                const uint8_t* w, const float* absmax,
+                                                const float* code16, int blocksize, int I, int K,
+                                                int M, void* act_tiles, grpo_stream_t stream) {
+  if (M > 8) return einval("the fold tile layout holds at most 8 rows");
+  if (!h || !sumsq || !norm_weight) return einval("null pointer");
+  if (groups < 1 || groups > GU_NORM_MAX_GROUPS) return einval("groups must be in [1, 16]");
+  if (!aligned16(norm_weight)) return einval("norm_weight must be 16-byte aligned");
+  NormSource src;
+  src.h = static_cast<const uint16_t*>(h);
+  src.ldh = ldh;
+  src.sumsq = sumsq;
+  src.groups = groups;
+  src.weight = static_cast<const uint16_t*>(norm_weight);
+  src.eps = eps;
+  return run_gate_up(h, ldh, w, absmax, code16, blocksize, I, K, M, act_tiles, I, 1,
+                     as_stream(stream), &src);
+}
+
+extern "C" int grpo_nf4_gate_up_silu_tiles_norm_supported(int M, int I, int K, int blocksize) {
+  GuPlan pl;
+  return M <= 8 && plan_gu(M, I, K, blocksize, &pl) && units_ok(M, I, K) ? 1 : 0;
 }
 
 extern "C" size_t grpo_fold_tiles_elements(int K) {
@@ -1788,7 +1880,7 @@ extern "C" int grpo_nf4_linear_partials_norm(const void* h, int64_t ldh, const f
 namespace {
 int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
                 const float* code16, int blocksize, int I, int K, int M, void* act, int64_t lda,
-                int act_tiles, hipStream_t st) {
+                int act_tiles, hipStream_t st, const NormSource* nrm) {
   GuPlan pl;
   if (!plan_gu(M, I, K, blocksize, &pl)) {
     set_error("shape not supported by the fused gate|up SiLU kernel");
@@ -1811,16 +1903,32 @@ int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absma
   a.I = I;
   a.K = K;
   a.act_tiles = act_tiles;
+  if (nrm) {
+    a.nh = nrm->h;
+    a.ldnh = nrm->ldh;
+    a.nss = nrm->sumsq;
+    a.nG = nrm->groups;
+    a.nw = nrm->weight;
+    a.neps = nrm->eps;
+  }
   {
     // units kernel: at most one workgroup per CU, every item of a wave in registers
     const int U = I / 8, KS = K / KSTEP;
     const int G = std::min(U, g_gu_units_grid);
-    const int nu = (U + G - 1) / G;
-    const size_t lds = (size_t)M * (K + 8) * 2 + (size_t)nu * KS * M * 16 * 4;
-    if (I % 8 == 0 && (nu * KS + GU_UNITS_W - 1) / GU_UNITS_W <= GU_UNITS_IPW && lds <= 65536) {
-      nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW><<<dim3((unsigned)G), 64 * GU_UNITS_W, lds, st>>>(a);
+    const size_t lds = units_lds(M, I, K);
+    if (units_ok(M, I, K)) {
+      if (nrm)
+        nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, true>
+            <<<dim3((unsigned)G), 64 * GU_UNITS_W, lds, st>>>(a);
+      else
+        nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, false>
+            <<<dim3((unsigned)G), 64 * GU_UNITS_W, lds, st>>>(a);
       return launch_check("nf4_gate_up_units");
     }
+  }
+  if (nrm) {
+    set_error("the RMSNorm x source needs the 8-column-unit gate|up kernel for this shape");
+    return GRPO_EUNSUPPORTED;
   }
   const dim3 grid((unsigned)(I / 16)), block(128 * pl.S);
   switch (pl.kpw * 16 + pl.S) {

@@ -120,6 +120,10 @@ SIGNATURES = {
     "grpo_nf4_gate_up_silu_tiles": (
         _I32, [_VP, _I64, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _VP]),
     "grpo_fold_tiles_elements": (_SZ, [_I32]),
+    "grpo_nf4_gate_up_silu_tiles_norm": (
+        _I32, [_VP, _I64, _VP, _I32, _VP, _F32, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _VP]),
+    "grpo_nf4_gate_up_silu_tiles_norm_supported": (_I32, [_I32, _I32, _I32, _I32]),
+    "grpo_linear_finish_residual": (_I32, [_PARTS, _VP, _VP, _I64, _VP, _VP]),
     "grpo_nf4_linear_residual": (
         _I32, [_VP, _I64, _I32, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _I64, _VP, _I64,
                _VP, _VP]),

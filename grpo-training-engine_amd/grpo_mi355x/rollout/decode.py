@@ -203,10 +203,15 @@ class DecodeEngine:
         # residual add and per-8-column sums of squares in the same launch), and
         # the next q|k|v kernel stages the input RMSNorm from h and those sums,
         # so the step has no input-norm launch after layer 0.
+        # The post-attention norm likewise: o_proj's epilogue + residual add +
+        # per-256-column sums of squares over N / 256 workgroups per row, and
+        # gate|up stages the norm.
         self.fold = (self.FOLD_DOWN and self.gu_fused and H % 8 == 0
-                     and H // 8 <= self.NORM_MAX_GROUPS
-                     and bool(self.lib.grpo_nf4_linear_residual_supported(B, H, I, bs)))
+                     and H // 8 <= self.NORM_MAX_GROUPS and -(-H // 256) <= 16
+                     and bool(self.lib.grpo_nf4_linear_residual_supported(B, H, I, bs))
+                     and bool(self.lib.grpo_nf4_gate_up_silu_tiles_norm_supported(B, I, H, bs)))
         self.ss = torch.zeros(B, max(H // 8, 1), dtype=torch.float32, device=dev)
+        self.ss_post = torch.zeros(B, -(-H // 256), dtype=torch.float32, device=dev)
         # down_proj's input in the fold tile layout (zero-filled: rows >= B and
         # columns >= I stay zero)
         self.act_tiles = torch.zeros(int(self.lib.grpo_fold_tiles_elements(I)) if self.fold
@@ -273,22 +278,31 @@ class DecodeEngine:
                     x, H, q.packed.data_ptr(), q.absmax.data_ptr(), q.code.data_ptr(), self.bs,
                     L["la"], L["qkv_parts"], st), "qkv")))
             out += self._attn_launches(L, kc, vc, st)
-            out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm_parts(
-                L["o_parts"], h, h, L["post_norm"].data_ptr(), x, L["eps"], st), "post_norm")))
             g = L["gu"]
             if self.fold:
-                # act in the tile layout the folded down_proj loads
-                out.append(("gate_up", lambda g=g: chk(lib.grpo_nf4_gate_up_silu_tiles(
-                    x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
-                    I, H, B, self.act_tiles.data_ptr(), st), "gate_up")))
-            elif self.gu_fused:
-                out.append(("gate_up", lambda g=g: chk(lib.grpo_nf4_gate_up_silu(
-                    x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
-                    I, H, B, self.act.data_ptr(), I, st), "gate_up")))
+                # o_proj finish + residual (h in place) + sums of squares, then
+                # gate|up staging RMSNorm(h) and writing act in the tile layout
+                # the folded down_proj loads
+                sp = self.ss_post.data_ptr()
+                out.append(("rmsnorm", lambda L=L, sp=sp: chk(lib.grpo_linear_finish_residual(
+                    L["o_parts"], h, h, H, sp, st), "post_finish")))
+                out.append(("gate_up", lambda g=g, L=L, sp=sp: chk(
+                    lib.grpo_nf4_gate_up_silu_tiles_norm(
+                        h, H, sp, self.ss_post.shape[1], L["post_norm"].data_ptr(), L["eps"],
+                        g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
+                        I, H, B, self.act_tiles.data_ptr(), st), "gate_up")))
             else:
-                out.append(("gate_up", lambda g=g, L=L: chk(lib.grpo_nf4_linear_partials(
-                    x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), self.bs,
-                    None, L["gu_parts"], st), "gate_up")))
+                out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm_parts(
+                    L["o_parts"], h, h, L["post_norm"].data_ptr(), x, L["eps"], st),
+                    "post_norm")))
+                if self.gu_fused:
+                    out.append(("gate_up", lambda g=g: chk(lib.grpo_nf4_gate_up_silu(
+                        x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(),
+                        self.bs, I, H, B, self.act.data_ptr(), I, st), "gate_up")))
+                else:
+                    out.append(("gate_up", lambda g=g, L=L: chk(lib.grpo_nf4_linear_partials(
+                        x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(),
+                        self.bs, None, L["gu_parts"], st), "gate_up")))
             if self.fold:
                 out.append(("down", lambda L=L: chk(lib.grpo_nf4_linear_residual(
                     self.act_tiles.data_ptr(), I, 1, L["down_w"].data_ptr(),

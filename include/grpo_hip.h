@@ -316,6 +316,20 @@ int grpo_nf4_gate_up_silu_tiles(const void* x, int64_t ldx, const uint8_t* w, co
 /* Elements (bf16) of a fold tile layout buffer of K columns. */
 size_t grpo_fold_tiles_elements(int K);
 
+/* grpo_nf4_gate_up_silu_tiles with x = RMSNorm(h): x[m, k] = bf16(bf16(h[m, k] *
+ * inv[m]) * norm_weight[k]), inv[m] = 1 / sqrt(sum_g sumsq[m, g] / K + eps), the
+ * sums as grpo_linear_finish_residual writes them (groups <= 16 per row): the
+ * decoder layer's post-attention RMSNorm (fused_rmsnorm, fused_ops.py:34-77;
+ * paged_kv.py:791-798) staged by the gate|up kernel.  M <= 8; shapes as
+ * grpo_nf4_gate_up_silu_tiles_norm_supported. */
+int grpo_nf4_gate_up_silu_tiles_norm(const void* h, int64_t ldh, const float* sumsq, int groups,
+                                     const void* norm_weight, float eps, const uint8_t* w,
+                                     const float* absmax, const float* code16, int blocksize,
+                                     int I, int K, int M, void* act_tiles, grpo_stream_t stream);
+
+/* 1 if grpo_nf4_gate_up_silu_tiles_norm takes this shape, else 0. */
+int grpo_nf4_gate_up_silu_tiles_norm_supported(int M, int I, int K, int blocksize);
+
 /* h_out[m, n] = bf16(residual[m, n] + bf16(x[m] . W[n])) and, for the next
  * RMSNorm, sumsq[m, g] = sum over n in [8g, 8g + 8) of h_out[m, n]^2 (float32,
  * G = N / 8 groups per row): the MLP's down_proj (NF4 weight [N, K], no bias,
@@ -363,6 +377,16 @@ int grpo_embedding(const int64_t* ids, const void* table, int64_t V, int H, void
  * fused_ops.py:34-77). */
 int grpo_add_rmsnorm(const void* x, const void* residual, void* h_out, const void* weight,
                      void* y, int M, int H, float eps, grpo_stream_t stream);
+
+/* h_out = bf16(residual + y) for the finished linear output y (the epilogue of
+ * grpo_nf4_linear_finish: bias, LoRA), and sumsq[m, g] = sum of h_out[m, n]^2
+ * over the 256 columns of group g (G = ceil(N / 256) per row, float32): the
+ * decoder layer's residual add after o_proj (paged_kv.py:791-798) with the
+ * statistic of the post-attention RMSNorm, which the gate|up kernel then
+ * stages (grpo_nf4_gate_up_silu_tiles_norm).  residual may be NULL and may
+ * alias h_out; row stride ld for both (8-byte aligned). */
+int grpo_linear_finish_residual(const grpo_linear_parts_t* parts, const void* residual,
+                                void* h_out, int64_t ld, float* sumsq, grpo_stream_t stream);
 
 /* RoPE on q and k of one token per sequence (position context_lens[b], cos/sin
  * tables bf16 [max_pos, D]), q -> q_out [B, Hq, D], rotated k and v appended to

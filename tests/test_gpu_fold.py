@@ -248,6 +248,110 @@ def test_gate_up_silu_tiles_is_the_tiled_gate_up_silu(dev, m, i, k):
     assert np.array_equal(_bits(til), tiles(_bits(plain)))
 
 
+@pytest.mark.parametrize("n,lora", [(1536, True), (3584, False), (1040, True)])
+def test_linear_finish_residual_matches_oracle(dev, n, lora):
+    """o_proj's epilogue + residual add + per-256-column sums of squares from
+    GPU split-K partials, against the oracle linear + bf16 residual add."""
+    from grpo_mi355x import _lib
+    from grpo_mi355x.kernels import ops
+
+    lib = _lib.device_library()
+    st = _lib.stream_handle(dev)
+    m, k, r, bs = 8, 512, 16, 64
+    n_pad = n + 16  # h has 16 columns more than N: they must stay untouched
+    g = np.random.default_rng(n + lora)
+    x = f32_to_bf16_bits(g.standard_normal((m, k)).astype(np.float32))
+    w = (g.standard_normal((n, k)) * 0.05).astype(np.float32)
+    packed, absmax = quantize_nf4(w, bs)
+    a = f32_to_bf16_bits((g.standard_normal((r, k)) * 0.05).astype(np.float32))
+    b = f32_to_bf16_bits((g.standard_normal((n, r)) * 0.05).astype(np.float32))
+    res = f32_to_bf16_bits(g.standard_normal((m, n_pad)).astype(np.float32))
+    rr = r if lora else 0
+    splits, pbytes, tbytes = ops.nf4_linear_plan(m, n, k, rr, 1, bs)
+    x_d, a_d, b_d = _dev_bf16(x, dev), _dev_bf16(a, dev), _dev_bf16(b, dev)
+    pk_d, am_d, code_d = _dev(packed, dev), _dev(absmax, dev), _dev(NF4_CODE.astype(np.float32), dev)
+    part = torch.empty(max(pbytes, 16) // 4, dtype=torch.float32, device=dev)
+    tpart = torch.empty(max(tbytes, 16) // 4, dtype=torch.float32, device=dev)
+    d = _lib.LinearParts()
+    d.part, d.tpart = part.data_ptr(), tpart.data_ptr()
+    d.splits, d.M, d.N, d.K, d.nseg, d.r = splits, m, n, k, 1, rr
+    d.seg_end[0] = n
+    d.lora_b[0] = b_d.data_ptr() if lora else None
+    d.scaling = 2.0
+    la = (ctypes.c_void_p * 1)(a_d.data_ptr() if lora else None)
+    _lib.check(lib.grpo_nf4_linear_partials(x_d.data_ptr(), k, pk_d.data_ptr(), am_d.data_ptr(),
+                                            code_d.data_ptr(), bs, la, ctypes.byref(d), st), "p")
+    # h rows of n + 16 columns (ld = n + 16); N = 1040 leaves a partial last group
+    h_d = _dev_bf16(res, dev)
+    groups = -(-n // 256)
+    ss_d = torch.full((m, groups + 1), -1.0, dtype=torch.float32, device=dev)
+    print(f"finish_residual n={n} lora={lora}", flush=True)
+    _lib.check(lib.grpo_linear_finish_residual(ctypes.byref(d), h_d.data_ptr(), h_d.data_ptr(),
+                                               n_pad, ss_d.data_ptr(), st), "finish_residual")
+    torch.cuda.synchronize()
+    lin = nf4_lora_linear(x, packed, absmax, n, k, bs, a_bits=a if lora else None,
+                          b_bits=b if lora else None, scaling=2.0)
+    ref = f32_to_bf16_bits(bf16_bits_to_f32(lin) + bf16_bits_to_f32(res[:, :n]))
+    hb = _bits(h_d)
+    got = hb[:, :n]
+    assert np.array_equal(hb[:, n:], res[:, n:])  # columns past N untouched
+    gf = bf16_bits_to_f32(got)
+    assert rel_err(gf, bf16_bits_to_f32(ref)) <= TOL
+    assert np.mean(got == ref) >= 0.97
+    ss = ss_d.cpu().numpy()
+    # the kernel writes one sum per (row, group) at row stride ceil(N / 256)
+    flat = ss.reshape(-1)[:m * groups].reshape(m, groups)
+    pad = np.zeros((m, groups * 256))
+    pad[:, :n] = gf.astype(np.float64) ** 2
+    assert np.allclose(flat, pad.reshape(m, groups, 256).sum(-1), rtol=1e-6, atol=0)
+
+
+@pytest.mark.parametrize("m,i,k", [(8, 8960, 1536), (3, 512, 1024)])
+def test_gate_up_tiles_norm_matches_the_two_launch_path_and_oracle(dev, m, i, k):
+    from grpo_mi355x import _lib
+
+    from oracle.decode import silu_mul
+
+    lib = _lib.device_library()
+    st = _lib.stream_handle(dev)
+    bs, eps = 64, 1e-6
+    assert lib.grpo_nf4_gate_up_silu_tiles_norm_supported(m, i, k, bs) == 1
+    g = np.random.default_rng(m + i + k + 1)
+    h = f32_to_bf16_bits((g.standard_normal((m, k)) * 2).astype(np.float32))
+    nw = f32_to_bf16_bits((1 + 0.1 * g.standard_normal(k)).astype(np.float32))
+    w = (g.standard_normal((2 * i, k)) * 0.05).astype(np.float32)
+    packed, absmax = quantize_nf4(w, bs)
+    groups = -(-k // 256)
+    hf = bf16_bits_to_f32(h).astype(np.float64)
+    ss = np.stack([np.add.reduceat(hf[r] ** 2, np.arange(0, k, 256)) for r in range(m)])
+    h_d, nw_d, ss_d = _dev_bf16(h, dev), _dev_bf16(nw, dev), _dev(ss.astype(np.float32), dev)
+    pk_d, am_d, code_d = _dev(packed, dev), _dev(absmax, dev), _dev(NF4_CODE.astype(np.float32), dev)
+    n_t = int(lib.grpo_fold_tiles_elements(i))
+    t1 = torch.zeros(n_t, dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.grpo_nf4_gate_up_silu_tiles_norm(
+        h_d.data_ptr(), k, ss_d.data_ptr(), groups, nw_d.data_ptr(), eps, pk_d.data_ptr(),
+        am_d.data_ptr(), code_d.data_ptr(), bs, i, k, m, t1.data_ptr(), st), "gu_norm")
+    x_d = torch.zeros(m, k, dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.grpo_add_rmsnorm(h_d.data_ptr(), None, None, nw_d.data_ptr(), x_d.data_ptr(),
+                                    m, k, eps, st), "rmsnorm")
+    t2 = torch.zeros(n_t, dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.grpo_nf4_gate_up_silu_tiles(x_d.data_ptr(), k, pk_d.data_ptr(),
+                                               am_d.data_ptr(), code_d.data_ptr(), bs, i, k, m,
+                                               t2.data_ptr(), st), "gu")
+    torch.cuda.synchronize()
+    a1, a2 = _bits(t1), _bits(t2)
+    assert np.mean(a1 == a2) >= 0.97
+    x_ref = rmsnorm(h, nw, eps)
+    half = packed.size // 2, absmax.size // 2
+    gate = nf4_lora_linear(x_ref, packed[:half[0]], absmax[:half[1]], i, k, bs)
+    up = nf4_lora_linear(x_ref, packed[half[0]:], absmax[half[1]:], i, k, bs)
+    ref = tiles(silu_mul(gate, up))
+    live = tiles(np.ones((m, i), np.uint16)) == 1
+    assert np.all(a1[~live] == 0)
+    assert rel_err(bf16_bits_to_f32(a1[live]), bf16_bits_to_f32(ref[live])) <= TOL
+    assert np.mean(a1[live] == ref[live]) >= 0.95
+
+
 def test_decode_engine_folds_small_batches(dev):
     """Decode batches of <= 8 rows run the folded down_proj and no input-norm
     launches after layer 0; wider ones keep the split-K path."""
@@ -262,7 +366,8 @@ def test_decode_engine_folds_small_batches(dev):
     wide = DecodeEngine(model, pool, 12, 4)
     assert small.fold and not wide.fold
     kinds = [k for k, _ in small.launches()]
-    assert kinds.count("rmsnorm") == 1 + 3 + 1  # layer 0's input, post-attention, final
+    # layer 0's input norm, the post-attention finish of each layer, the final norm
+    assert kinds.count("rmsnorm") == 1 + 3 + 1
     assert kinds.count("down") == 3
     kinds_w = [k for k, _ in wide.launches()]
     assert kinds_w.count("rmsnorm") == 2 * 3 + 1
