@@ -394,8 +394,13 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
       bl = make_uint2(pack_bf2(pb[0] - bf_lo(h01), pb[1] - bf_hi(h01)),
                       pack_bf2(pb[2] - bf_lo(h23), pb[3] - bf_hi(h23)));
     }
+    // Rescale only when some head's running max moved in this block (corr is
+    // exactly 1 otherwise, so skipping the 32 multiplies changes no bit): a
+    // wave-uniform test, true on the first blocks and rarely after.
+    if (__builtin_amdgcn_ballot_w64(corr != 1.f)) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) oacc[i] *= corr;
+      for (int i = 0; i < 8; ++i) oacc[i] *= corr;
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const uint32_t sel = (i & 1) ? 0x07060302u : 0x05040100u;
