@@ -128,6 +128,33 @@ __device__ __forceinline__ uint4 load_stream(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Sum over the 64 lanes of a wave, every lane gets the total: DPP within each
+// row of 16 lanes (quad_perm xor 1, xor 2, half-row mirror, row mirror), then
+// the permlane swaps across rows.
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float wave_sum_dpp(float v) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  v += dpp_move<0x140>(v);  // row_mirror
+  return pair32_sum(pair16_sum(v));
+}
+
+// Eight columns of the RMSNorm output bf16(bf16(h * inv) * w) (the reference's
+// rounding points, as add_rmsnorm_kernel), h and w in natural order.
+__device__ __forceinline__ uint4 norm8(uint4 hv, uint4 wv, float inv) {
+  const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
+  uint32_t o[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    o[q] = pack_bf2(round_bf(bf_lo(hw[q]) * inv) * bf_lo(ww[q]),
+                    round_bf(bf_hi(hw[q]) * inv) * bf_hi(ww[q]));
+  return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
 __device__ __forceinline__ f32x4_t mfma16x16x32(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
 }

@@ -62,6 +62,27 @@ __global__ void __launch_bounds__(ROW_T) embedding_kernel(const int64_t* __restr
   for (int i = threadIdx.x; i < H; i += ROW_T) out[(int64_t)b * H + i] = ok ? src[i] : 0;
 }
 
+// embedding_kernel that also writes the RMSNorm statistic of each row:
+// sumsq[b, t] = sum of out[b, i]^2 over i = t, t + ROW_T, ... (ROW_T groups per
+// row), which the first q|k|v kernel stages the input norm from.
+__global__ void __launch_bounds__(ROW_T) embedding_sumsq_kernel(const int64_t* __restrict__ ids,
+                                                                const uint16_t* __restrict__ table,
+                                                                int64_t V, int H,
+                                                                uint16_t* __restrict__ out,
+                                                                float* __restrict__ sumsq) {
+  const int b = blockIdx.x;
+  const int64_t id = ids[b];
+  const bool ok = id >= 0 && id < V;
+  const uint16_t* src = table + (ok ? id : 0) * (int64_t)H;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < H; i += ROW_T) {
+    const uint16_t v = ok ? src[i] : 0;
+    out[(int64_t)b * H + i] = v;
+    ss += bf2f(v) * bf2f(v);
+  }
+  sumsq[(int64_t)b * ROW_T + threadIdx.x] = ss;
+}
+
 // h = residual ? bf16(x + residual) : x; y = bf16(bf16(h * rsqrt(mean(h^2) + eps)) * w)
 // (fused_ops.py:34-77; transformers' Qwen2RMSNorm).  h is written to h_out when given.
 __global__ void __launch_bounds__(ROW_T) add_rmsnorm_kernel(
@@ -430,6 +451,18 @@ extern "C" int grpo_embedding(const int64_t* ids, const void* table, int64_t V, 
       ids, static_cast<const uint16_t*>(table), V, H, static_cast<uint16_t*>(out));
   return launch_check("embedding");
 }
+
+extern "C" int grpo_embedding_sumsq(const int64_t* ids, const void* table, int64_t V, int H,
+                                    void* out, int B, float* sumsq, grpo_stream_t stream) {
+  if (B < 0 || H <= 0 || V <= 0) return einval("bad embedding dimensions");
+  if (B == 0) return GRPO_OK;
+  if (!ids || !table || !out || !sumsq) return einval("null pointer");
+  embedding_sumsq_kernel<<<dim3(B), ROW_T, 0, as_stream(stream)>>>(
+      ids, static_cast<const uint16_t*>(table), V, H, static_cast<uint16_t*>(out), sumsq);
+  return launch_check("embedding_sumsq");
+}
+
+extern "C" int grpo_embedding_sumsq_groups(void) { return ROW_T; }
 
 extern "C" int grpo_add_rmsnorm(const void* x, const void* residual, void* h_out,
                                 const void* weight, void* y, int M, int H, float eps,

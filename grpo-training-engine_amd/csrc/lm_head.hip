@@ -48,7 +48,14 @@ struct LmArgs {
   int64_t ldl;
   float* pval;       // [M][NT]
   int* pidx;         // [M][NT]
+  // x = RMSNorm(h) staged from h (x above) and per-group sums of squares
+  // (NORM instantiation, M <= LM_WAVES rows, nG <= 256 groups per row)
+  const float* nss;
+  int nG;
+  const uint16_t* nw;
+  float neps;
 };
+constexpr int LM_NORM_MAX_GROUPS = 256;
 
 // Strictly better in the argmax order: larger value, or equal value at a
 // smaller index (the first maximum).  NaN never wins.
@@ -56,7 +63,7 @@ __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
 }
 
-template <int MT>
+template <int MT, bool NORM>
 __global__ void __launch_bounds__(64 * LM_WAVES) lm_head_argmax_kernel(LmArgs p) {
   touch_kernargs<sizeof(LmArgs)>();
   extern __shared__ __align__(16) uint16_t xs[];  // [M][K + 8]
@@ -75,10 +82,28 @@ __global__ void __launch_bounds__(64 * LM_WAVES) lm_head_argmax_kernel(LmArgs p)
   const uint16_t* wrow = p.w + (int64_t)(live ? tile * 16 + ln : 0) * p.K + 8 * lg;
   {
     const int chunks = p.K / 8, total = p.M * chunks;
+    // after x in the dynamic LDS (a static array would lower the dynamic limit
+    // that allow_lds sets for every instantiation)
+    float* sInv = reinterpret_cast<float*>(xs + p.M * xstride);
+    if (NORM) {
+      // wave w: 1 / rms of row w from its group sums (4 per lane, clamped
+      // indexes, dropped in the sum)
+      const float* ssr = p.nss + (int64_t)min(wave, p.M - 1) * p.nG;
+      float v[LM_NORM_MAX_GROUPS / 64];
+#pragma unroll
+      for (int q = 0; q < LM_NORM_MAX_GROUPS / 64; ++q) v[q] = ssr[min(lane + 64 * q, p.nG - 1)];
+      float ss = 0.f;
+#pragma unroll
+      for (int q = 0; q < LM_NORM_MAX_GROUPS / 64; ++q) ss += lane + 64 * q < p.nG ? v[q] : 0.f;
+      ss = wave_sum_dpp(ss);
+      if (lane == 0) sInv[wave] = 1.f / sqrtf(ss / (float)p.K + p.neps);
+      __syncthreads();
+    }
     for (int i = tid; i < total; i += 64 * LM_WAVES) {
       const int m = i / chunks, c = i - m * chunks;
-      *reinterpret_cast<uint4*>(xs + m * xstride + 8 * c) =
-          *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + 8 * c);
+      uint4 v = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + 8 * c);
+      if (NORM) v = norm8(v, *reinterpret_cast<const uint4*>(p.nw + 8 * c), sInv[m]);
+      *reinterpret_cast<uint4*>(xs + m * xstride + 8 * c) = v;
     }
   }
   __syncthreads();
@@ -197,9 +222,47 @@ extern "C" size_t grpo_lm_head_workspace_bytes(int M, int V) {
   return (size_t)M * cdiv(V, 16) * 8;
 }
 
+namespace {
+
+struct LmNorm {
+  const float* sumsq;
+  int groups;
+  const uint16_t* weight;
+  float eps;
+};
+
+int run_lm_head(const void* x, int64_t ldx, const void* w, int V, int K, int M, void* logits,
+                int64_t ld_logits, void* workspace, size_t workspace_bytes, hipStream_t st,
+                const LmNorm* nrm);
+
+}  // namespace
+
 extern "C" int grpo_lm_head_argmax(const void* x, int64_t ldx, const void* w, int V, int K, int M,
                                    void* logits, int64_t ld_logits, void* workspace,
                                    size_t workspace_bytes, grpo_stream_t stream) {
+  return run_lm_head(x, ldx, w, V, K, M, logits, ld_logits, workspace, workspace_bytes,
+                     as_stream(stream), nullptr);
+}
+
+extern "C" int grpo_lm_head_argmax_norm(const void* h, int64_t ldh, const float* sumsq,
+                                        int groups, const void* norm_weight, float eps,
+                                        const void* w, int V, int K, int M, void* logits,
+                                        int64_t ld_logits, void* workspace,
+                                        size_t workspace_bytes, grpo_stream_t stream) {
+  if (M > LM_WAVES) return einval("the RMSNorm x source takes at most 8 rows");
+  if (!sumsq || !norm_weight) return einval("null pointer");
+  if (groups < 1 || groups > LM_NORM_MAX_GROUPS) return einval("groups must be in [1, 256]");
+  if (!aligned16(norm_weight)) return einval("norm_weight must be 16-byte aligned");
+  const LmNorm n{sumsq, groups, static_cast<const uint16_t*>(norm_weight), eps};
+  return run_lm_head(h, ldh, w, V, K, M, logits, ld_logits, workspace, workspace_bytes,
+                     as_stream(stream), &n);
+}
+
+namespace {
+
+int run_lm_head(const void* x, int64_t ldx, const void* w, int V, int K, int M, void* logits,
+                int64_t ld_logits, void* workspace, size_t workspace_bytes, hipStream_t st,
+                const LmNorm* nrm) {
   if (M <= 0 || V <= 0 || K <= 0) return einval("bad lm_head dimensions");
   if (M > 64) return einval("lm_head argmax supports M <= 64 rows");
   if (V % 16 || K % LM_KSTEP) return einval("lm_head needs V % 16 == 0 and K % 256 == 0");
@@ -213,7 +276,7 @@ extern "C" int grpo_lm_head_argmax(const void* x, int64_t ldx, const void* w, in
               workspace_bytes);
     return GRPO_EWORKSPACE;
   }
-  const size_t lds = (size_t)M * (K + 8) * 2;
+  const size_t lds = (size_t)M * (K + 8) * 2 + (nrm ? LM_WAVES * sizeof(float) : 0);
   if (lds > LM_LDS_MAX) {
     set_error("lm_head: x [M, K] does not fit in LDS (M * (K + 8) * 2 > 160 KiB)");
     return GRPO_EUNSUPPORTED;
@@ -231,19 +294,27 @@ extern "C" int grpo_lm_head_argmax(const void* x, int64_t ldx, const void* w, in
   a.pval = static_cast<float*>(workspace);
   a.pidx = reinterpret_cast<int*>(a.pval + (size_t)M * a.NT);
   const dim3 grid((unsigned)cdiv(a.NT, LM_WAVES)), block(64 * LM_WAVES);
-  hipStream_t st = as_stream(stream);
-  if (M <= 16) {
-    if (int rc = allow_lds(lm_head_argmax_kernel<1>)) return rc;
-    lm_head_argmax_kernel<1><<<grid, block, lds, st>>>(a);
+  if (nrm) {
+    a.nss = nrm->sumsq;
+    a.nG = nrm->groups;
+    a.nw = nrm->weight;
+    a.neps = nrm->eps;
+    if (int rc = allow_lds(lm_head_argmax_kernel<1, true>)) return rc;
+    lm_head_argmax_kernel<1, true><<<grid, block, lds, st>>>(a);
+  } else if (M <= 16) {
+    if (int rc = allow_lds(lm_head_argmax_kernel<1, false>)) return rc;
+    lm_head_argmax_kernel<1, false><<<grid, block, lds, st>>>(a);
   } else if (M <= 32) {
-    if (int rc = allow_lds(lm_head_argmax_kernel<2>)) return rc;
-    lm_head_argmax_kernel<2><<<grid, block, lds, st>>>(a);
+    if (int rc = allow_lds(lm_head_argmax_kernel<2, false>)) return rc;
+    lm_head_argmax_kernel<2, false><<<grid, block, lds, st>>>(a);
   } else {
-    if (int rc = allow_lds(lm_head_argmax_kernel<4>)) return rc;
-    lm_head_argmax_kernel<4><<<grid, block, lds, st>>>(a);
+    if (int rc = allow_lds(lm_head_argmax_kernel<4, false>)) return rc;
+    lm_head_argmax_kernel<4, false><<<grid, block, lds, st>>>(a);
   }
   return launch_check("lm_head_argmax");
 }
+
+}  // namespace
 
 extern "C" int grpo_decode_advance(const void* lm_workspace, int M, int V, int64_t* next_tokens,
                                    int64_t* tokens, int32_t* pos, int32_t* count,

@@ -327,34 +327,19 @@ __device__ __forceinline__ uint4 attn_chunk(const PartArgs& p, int m, int k) {
 
 // Sum over each aligned group of 8 lanes (every lane of the group gets it):
 // DPP quad_perm xor 1, xor 2, then the half-row mirror (lane i + lane 7 - i).
-template <int CTRL>
-__device__ __forceinline__ float dpp_f(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
-}
 __device__ __forceinline__ float sum8(float v) {
-  v += dpp_f<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_f<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_f<0x141>(v);  // row_half_mirror
+  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
   return v;
 }
 // The same over each DPP row of 16 lanes (then the row mirror, lane i + 15 - i).
 __device__ __forceinline__ float sum16(float v) {
   v = sum8(v);
-  v += dpp_f<0x140>(v);  // row_mirror
+  v += dpp_move<0x140>(v);  // row_mirror
   return v;
 }
 
-// Eight columns of the RMSNorm output bf16(bf16(h * inv) * w) (the reference's
-// rounding points, as add_rmsnorm_kernel), h and w in natural order.
-__device__ __forceinline__ uint4 norm8(uint4 hv, uint4 wv, float inv) {
-  const uint32_t hw[4] = {hv.x, hv.y, hv.z, hv.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
-  uint32_t o[4];
-#pragma unroll
-  for (int q = 0; q < 4; ++q)
-    o[q] = pack_bf2(round_bf(bf_lo(hw[q]) * inv) * bf_lo(ww[q]),
-                    round_bf(bf_hi(hw[q]) * inv) * bf_hi(ww[q]));
-  return make_uint4(o[0], o[1], o[2], o[3]);
-}
 
 template <int MT, int KPW, int XSRC>
 __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(PartArgs p) {

@@ -124,6 +124,10 @@ SIGNATURES = {
         _I32, [_VP, _I64, _VP, _I32, _VP, _F32, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _VP]),
     "grpo_nf4_gate_up_silu_tiles_norm_supported": (_I32, [_I32, _I32, _I32, _I32]),
     "grpo_linear_finish_residual": (_I32, [_PARTS, _VP, _VP, _I64, _VP, _VP]),
+    "grpo_embedding_sumsq": (_I32, [_VP, _VP, _I64, _I32, _VP, _I32, _VP, _VP]),
+    "grpo_embedding_sumsq_groups": (_I32, []),
+    "grpo_lm_head_argmax_norm": (
+        _I32, [_VP, _I64, _VP, _I32, _VP, _F32, _VP, _I32, _I32, _I32, _VP, _I64, _VP, _SZ, _VP]),
     "grpo_nf4_linear_residual": (
         _I32, [_VP, _I64, _I32, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _I64, _VP, _I64,
                _VP, _VP]),

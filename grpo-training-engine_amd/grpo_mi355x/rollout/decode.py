@@ -212,6 +212,9 @@ class DecodeEngine:
                      and bool(self.lib.grpo_nf4_gate_up_silu_tiles_norm_supported(B, I, H, bs)))
         self.ss = torch.zeros(B, max(H // 8, 1), dtype=torch.float32, device=dev)
         self.ss_post = torch.zeros(B, -(-H // 256), dtype=torch.float32, device=dev)
+        # the embedding's row statistic for layer 0's input norm
+        self.ss_embed = torch.zeros(B, int(self.lib.grpo_embedding_sumsq_groups()),
+                                    dtype=torch.float32, device=dev)
         # down_proj's input in the fold tile layout (zero-filled: rows >= B and
         # columns >= I stay zero)
         self.act_tiles = torch.zeros(int(self.lib.grpo_fold_tiles_elements(I)) if self.fold
@@ -254,25 +257,36 @@ class DecodeEngine:
         chk = _lib.check
         pool = self.pool
         h, x = self.h.data_ptr(), self.x.data_ptr()
-        out = [("embedding", lambda: chk(lib.grpo_embedding(
-            self.tokens.data_ptr(), self.embed.data_ptr(), self.V, H, h, B, st), "embedding"))]
+        if self.fold:  # the embedding also writes the statistic of layer 0's input norm
+            out = [("embedding", lambda: chk(lib.grpo_embedding_sumsq(
+                self.tokens.data_ptr(), self.embed.data_ptr(), self.V, H, h, B,
+                self.ss_embed.data_ptr(), st), "embedding"))]
+        else:
+            out = [("embedding", lambda: chk(lib.grpo_embedding(
+                self.tokens.data_ptr(), self.embed.data_ptr(), self.V, H, h, B, st),
+                "embedding"))]
         prev = None
         for li, L in enumerate(self.layers):
             kc, vc = (t.data_ptr() for t in pool.layer(li))
             q = L["qkv"]
-            if prev is None:
-                out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm(
-                    h, None, None, L["in_norm"].data_ptr(), x, B, H, L["eps"], st), "rmsnorm")))
-            elif not self.fold:
-                out.append(("rmsnorm", lambda L=L, P=prev: chk(lib.grpo_add_rmsnorm_parts(
-                    P["down_parts"], h, h, L["in_norm"].data_ptr(), x, L["eps"], st),
-                    "add_rmsnorm")))
-            if prev is not None and self.fold:
-                ss = self.ss.data_ptr()
-                out.append(("qkv", lambda q=q, L=L, ss=ss: chk(lib.grpo_nf4_linear_partials_norm(
-                    h, H, ss, H // 8, L["in_norm"].data_ptr(), L["eps"], q.packed.data_ptr(),
-                    q.absmax.data_ptr(), q.code.data_ptr(), self.bs, L["la"], L["qkv_parts"],
-                    st), "qkv")))
+            if not self.fold:
+                if prev is None:
+                    out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm(
+                        h, None, None, L["in_norm"].data_ptr(), x, B, H, L["eps"], st),
+                        "rmsnorm")))
+                else:
+                    out.append(("rmsnorm", lambda L=L, P=prev: chk(lib.grpo_add_rmsnorm_parts(
+                        P["down_parts"], h, h, L["in_norm"].data_ptr(), x, L["eps"], st),
+                        "add_rmsnorm")))
+            if self.fold:
+                # layer 0 from the embedding's statistic, the others from down_proj's
+                ss, ng = ((self.ss_embed.data_ptr(), self.ss_embed.shape[1]) if prev is None
+                          else (self.ss.data_ptr(), H // 8))
+                out.append(("qkv", lambda q=q, L=L, ss=ss, ng=ng: chk(
+                    lib.grpo_nf4_linear_partials_norm(
+                        h, H, ss, ng, L["in_norm"].data_ptr(), L["eps"], q.packed.data_ptr(),
+                        q.absmax.data_ptr(), q.code.data_ptr(), self.bs, L["la"],
+                        L["qkv_parts"], st), "qkv")))
             else:
                 out.append(("qkv", lambda q=q, L=L: chk(lib.grpo_nf4_linear_partials(
                     x, H, q.packed.data_ptr(), q.absmax.data_ptr(), q.code.data_ptr(), self.bs,
@@ -366,6 +380,9 @@ class DecodeEngine:
         """Final norm, lm_head and the token choice with the row advance."""
         lib, chk, B, H = self.lib, _lib.check, self.B, self.H
         h, x = self.h.data_ptr(), self.x.data_ptr()
+        if self.fold and self.lm_fused:
+            # the lm_head kernel stages the final norm from h and down_proj's sums
+            return self._head_launches_norm(st)
         if self.fold:  # h is finished: the final norm reads it alone
             out = [("rmsnorm", lambda: chk(lib.grpo_add_rmsnorm(
                 h, None, None, self.final_norm.data_ptr(), x, B, H, self.final_eps, st),
@@ -409,6 +426,35 @@ class DecodeEngine:
             out.append(("argmax", lambda: chk(lib.grpo_argmax_bf16(
                 self.logits.data_ptr(), self.V, self.V, B, self.next.data_ptr(), st),
                 "argmax")))
+        return out
+
+    def _head_launches_norm(self, st) -> list:
+        """lm_head staging the final RMSNorm from h and the sums of squares of
+        the last down_proj, then the sampler or the greedy advance."""
+        lib, chk, B, H = self.lib, _lib.check, self.B, self.H
+        h, ss = self.h.data_ptr(), self.ss.data_ptr()
+        gen = self.generated
+        logits = self.logits.data_ptr() if (self.keep_logits or self.sampling) else None
+        out = [("lm_head", lambda: chk(lib.grpo_lm_head_argmax_norm(
+            h, H, ss, H // 8, self.final_norm.data_ptr(), self.final_eps, self.lm_head.data_ptr(),
+            self.V, H, B, logits, self.V, self.ws_lm.data_ptr(), self.ws_lm.numel(), st),
+            "lm_head"))]
+        if self.sampling:
+            out.append(("sample", lambda: chk(lib.grpo_sample_advance(
+                self.logits.data_ptr(), self.V, B, self.V, self.temperature, self.top_p,
+                self.seed, self.next.data_ptr(), self.tokens.data_ptr(), self.pos.data_ptr(),
+                self.count.data_ptr(), self.limit.data_ptr(), self.active.data_ptr(),
+                self.eos.data_ptr(), None if gen is None else gen.data_ptr(),
+                0 if gen is None else gen.shape[1], self.append_pos.data_ptr(),
+                self.attn_len.data_ptr(), self.ws_smp.data_ptr(), self.ws_smp.numel(), st),
+                "sample")))
+        else:
+            out.append(("advance", lambda: chk(lib.grpo_decode_advance(
+                self.ws_lm.data_ptr(), B, self.V, self.next.data_ptr(), self.tokens.data_ptr(),
+                self.pos.data_ptr(), self.count.data_ptr(), self.limit.data_ptr(),
+                self.active.data_ptr(), self.eos.data_ptr(),
+                None if gen is None else gen.data_ptr(), 0 if gen is None else gen.shape[1],
+                self.append_pos.data_ptr(), self.attn_len.data_ptr(), st), "advance")))
         return out
 
     def nf4_launches(self) -> list:

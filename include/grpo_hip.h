@@ -370,6 +370,16 @@ int grpo_nf4_linear_partials_norm(const void* h, int64_t ldh, const float* sumsq
 int grpo_embedding(const int64_t* ids, const void* table, int64_t V, int H, void* out, int B,
                    grpo_stream_t stream);
 
+/* grpo_embedding that also writes sumsq[b, t] = sum of out[b, i]^2 over
+ * i = t, t + G, t + 2G, ... for t < G = grpo_embedding_sumsq_groups() (256):
+ * the statistic of the first decoder layer's input RMSNorm, which the q|k|v
+ * kernel stages (grpo_nf4_linear_partials_norm with groups = G). */
+int grpo_embedding_sumsq(const int64_t* ids, const void* table, int64_t V, int H, void* out, int B,
+                         float* sumsq, grpo_stream_t stream);
+
+/* Groups per row written by grpo_embedding_sumsq. */
+int grpo_embedding_sumsq_groups(void);
+
 /* h = residual ? bf16(x + residual) : x  (written to h_out when residual and
  * h_out are given; h_out may alias residual); y = bf16(bf16(h * rsqrt(mean(h^2)
  * + eps)) * weight).  x, residual, h_out, y: [M, H]; weight [H].  Replaces the
@@ -441,6 +451,15 @@ size_t grpo_lm_head_workspace_bytes(int M, int V);
 int grpo_lm_head_argmax(const void* x, int64_t ldx, const void* w, int V, int K, int M,
                         void* logits, int64_t ld_logits, void* workspace, size_t workspace_bytes,
                         grpo_stream_t stream);
+
+/* grpo_lm_head_argmax with x = RMSNorm(h): x[m, k] = bf16(bf16(h[m, k] * inv[m]) *
+ * norm_weight[k]), inv[m] = 1 / sqrt(sum_g sumsq[m, g] / K + eps) (groups <= 256
+ * per row, as grpo_nf4_linear_residual writes them): the model's final norm
+ * (paged_kv.py:806) staged by the lm_head kernel.  M <= 8. */
+int grpo_lm_head_argmax_norm(const void* h, int64_t ldh, const float* sumsq, int groups,
+                             const void* norm_weight, float eps, const void* w, int V, int K,
+                             int M, void* logits, int64_t ld_logits, void* workspace,
+                             size_t workspace_bytes, grpo_stream_t stream);
 
 /* Greedy token of every row from grpo_lm_head_argmax's workspace (first index
  * of the maximum), written to next_tokens (may be NULL), and the decode loop's

@@ -352,6 +352,66 @@ def test_gate_up_tiles_norm_matches_the_two_launch_path_and_oracle(dev, m, i, k)
     assert np.mean(a1[live] == ref[live]) >= 0.95
 
 
+def test_embedding_sumsq(dev):
+    from grpo_mi355x import _lib
+
+    lib = _lib.device_library()
+    V, H, B = 1000, 1536, 5
+    G = int(lib.grpo_embedding_sumsq_groups())
+    g = np.random.default_rng(3)
+    table = f32_to_bf16_bits(g.standard_normal((V, H)).astype(np.float32))
+    ids = np.array([0, 999, 17, -1, 1000], np.int64)  # the last two are out of range: zero rows
+    t_d, i_d = _dev_bf16(table, dev), _dev(ids, dev)
+    out = torch.empty(B, H, dtype=torch.bfloat16, device=dev)
+    ss = torch.full((B, G), -1.0, dtype=torch.float32, device=dev)
+    _lib.check(lib.grpo_embedding_sumsq(i_d.data_ptr(), t_d.data_ptr(), V, H, out.data_ptr(), B,
+                                        ss.data_ptr(), _lib.stream_handle(dev)), "emb")
+    torch.cuda.synchronize()
+    want = np.zeros((B, H), np.uint16)
+    want[:3] = table[ids[:3]]
+    assert np.array_equal(_bits(out), want)
+    wf = bf16_bits_to_f32(want).astype(np.float64) ** 2
+    ref = np.stack([[wf[b, t::G].sum() for t in range(G)] for b in range(B)])
+    assert np.allclose(ss.cpu().numpy(), ref, rtol=1e-6, atol=0)
+
+
+def test_lm_head_norm_matches_the_two_launch_path(dev):
+    """lm_head staging the final RMSNorm from h and per-group sums of squares ==
+    grpo_add_rmsnorm + grpo_lm_head_argmax up to the norm's summation order."""
+    from grpo_mi355x import _lib
+
+    lib = _lib.device_library()
+    st = _lib.stream_handle(dev)
+    M, K, V, eps = 8, 1536, 4096, 1e-6
+    g = np.random.default_rng(4)
+    h = f32_to_bf16_bits((g.standard_normal((M, K)) * 3).astype(np.float32))
+    nw = f32_to_bf16_bits((1 + 0.1 * g.standard_normal(K)).astype(np.float32))
+    w = f32_to_bf16_bits((g.standard_normal((V, K)) * 0.05).astype(np.float32))
+    hf = bf16_bits_to_f32(h).astype(np.float64)
+    ss = (hf ** 2).reshape(M, K // 8, 8).sum(-1).astype(np.float32)  # 192 groups
+    h_d, nw_d, w_d, ss_d = _dev_bf16(h, dev), _dev_bf16(nw, dev), _dev_bf16(w, dev), _dev(ss, dev)
+    nbytes = int(lib.grpo_lm_head_workspace_bytes(M, V))
+    ws1 = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    ws2 = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    l1 = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+    l2 = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.grpo_lm_head_argmax_norm(h_d.data_ptr(), K, ss_d.data_ptr(), K // 8,
+                                            nw_d.data_ptr(), eps, w_d.data_ptr(), V, K, M,
+                                            l1.data_ptr(), V, ws1.data_ptr(), nbytes, st), "lm1")
+    x_d = torch.empty(M, K, dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.grpo_add_rmsnorm(h_d.data_ptr(), None, None, nw_d.data_ptr(), x_d.data_ptr(),
+                                    M, K, eps, st), "rmsnorm")
+    _lib.check(lib.grpo_lm_head_argmax(x_d.data_ptr(), K, w_d.data_ptr(), V, K, M, l2.data_ptr(),
+                                       V, ws2.data_ptr(), nbytes, st), "lm2")
+    torch.cuda.synchronize()
+    a, b = _bits(l1), _bits(l2)
+    assert np.mean(a == b) >= 0.97
+    assert rel_err(bf16_bits_to_f32(a), bf16_bits_to_f32(b)) <= TOL
+    x_ref = rmsnorm(h, nw, eps)
+    ref = bf16_bits_to_f32(x_ref).astype(np.float64) @ bf16_bits_to_f32(w).astype(np.float64).T
+    assert rel_err(bf16_bits_to_f32(a), ref.astype(np.float32)) <= TOL
+
+
 def test_decode_engine_folds_small_batches(dev):
     """Decode batches of <= 8 rows run the folded down_proj and no input-norm
     launches after layer 0; wider ones keep the split-K path."""
@@ -366,8 +426,10 @@ def test_decode_engine_folds_small_batches(dev):
     wide = DecodeEngine(model, pool, 12, 4)
     assert small.fold and not wide.fold
     kinds = [k for k, _ in small.launches()]
-    # layer 0's input norm, the post-attention finish of each layer, the final norm
-    assert kinds.count("rmsnorm") == 1 + 3 + 1
+    # only the post-attention finish of each layer: the embedding carries layer
+    # 0's norm statistic, the lm_head kernel stages the final norm
+    assert kinds.count("rmsnorm") == 3
+    assert len(kinds) == 1 + 3 * 6 + 2  # embedding, 6 per layer, lm_head + advance
     assert kinds.count("down") == 3
     kinds_w = [k for k, _ in wide.launches()]
     assert kinds_w.count("rmsnorm") == 2 * 3 + 1
