@@ -12,6 +12,8 @@
 // pass instead of re-reading the logits.
 #include <math.h>
 
+#include <algorithm>
+
 #include "common.hpp"
 #include "decode_state.hpp"
 
@@ -61,6 +63,44 @@ constexpr int LM_NORM_MAX_GROUPS = 256;
 // smaller index (the first maximum).  NaN never wins.
 __device__ __forceinline__ bool better(float v, int i, float bv, int bi) {
   return v > bv || (v == bv && i < bi);
+}
+
+// The tile's logits (bf16) and, per row, its (max, first index) pair: lane
+// (n = ln, group lg) holds logits[m = mt*16 + 4*lg + q][tile*16 + ln].
+template <int MT>
+__device__ __forceinline__ void lm_epilogue(const LmArgs& p, int tile, int ln, int lg,
+                                            const f32x4_t (&acc)[MT]) {
+  const int v = tile * 16 + ln;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int m = mt * 16 + 4 * lg + q;
+      const uint16_t b = f2bf(acc[mt][q]);
+      float bv = bf2f(b);
+      int bi = v;
+      if (bv != bv) {  // NaN never wins
+        bv = -INFINITY;
+        bi = 0x7fffffff;
+      }
+      // (max, first index) over the 16 lanes of this lane group
+#pragma unroll
+      for (int o = 1; o < 16; o <<= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (better(ov, oi, bv, bi)) {
+          bv = ov;
+          bi = oi;
+        }
+      }
+      if (m < p.M) {
+        if (p.logits) p.logits[(int64_t)m * p.ldl + v] = b;
+        if (ln == 0) {
+          p.pval[(int64_t)m * p.NT + tile] = bv;
+          p.pidx[(int64_t)m * p.NT + tile] = bi;
+        }
+      }
+    }
 }
 
 template <int MT, bool NORM>
@@ -132,38 +172,95 @@ __global__ void __launch_bounds__(64 * LM_WAVES) lm_head_argmax_kernel(LmArgs p)
             *reinterpret_cast<const uint4*>(xrow[mt] + ks * LM_KSTEP + 32 * j), w[j], acc[mt]);
   }
 
-  // lane (n = ln, group lg) holds logits[m = mt*16 + 4*lg + q][tile*16 + ln].
-  const int v = tile * 16 + ln;
+  lm_epilogue<MT>(p, tile, ln, lg, acc);
+}
+
+// Wide batches (x [M, K] beyond 160 KiB of LDS, e.g. Qwen2-7B at G = 64): one
+// workgroup per CU, each wave owning up to TPW vocabulary tiles (wave w of the
+// grid takes tiles w, w + waves, ...), their accumulators in registers.  x is
+// staged in K chunks of KC columns, once per chunk per workgroup, and every
+// wave streams the W rows of all its tiles over the chunk, the next 256-column
+// step's W loads issued before the current step's MFMAs.  (Staging x once per
+// tile instead -- one workgroup per 8 tiles, 1 per CU for LDS -- read x from
+// L2 ~40 times per CU and left 8 waves per CU without loads in flight during
+// each staging: 320 us at M = 64.)  At M = 64, V = 152064, K = 3584 it streams
+// W at 4.2 TB/s (257 us, the argmax included); hipBLASLt's GEMM alone takes
+// 202 us, its logits then need an argmax launch (9.6 us).
+constexpr int LM_WIDE_WAVES = 8;
+constexpr int LM_WIDE_TPW = 5;     // tiles per wave: V <= 5 * 2048 * 16 = 163840
+
+template <int MT>
+__global__ void __launch_bounds__(64 * LM_WIDE_WAVES) lm_head_argmax_wide(LmArgs p, int KC) {
+  touch_kernargs<sizeof(LmArgs)>();
+  extern __shared__ __align__(16) uint16_t xs[];  // [M][KC + 8]
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 15, lg = lane >> 4;
+  const int gw = blockIdx.x * LM_WIDE_WAVES + wave, nw = gridDim.x * LM_WIDE_WAVES;
+  const int ntiles = gw < p.NT ? (p.NT - gw + nw - 1) / nw : 0;  // this wave's tiles (<= TPW)
+  const int xstride = KC + 8;
+  const int KS = p.K / LM_KSTEP, kpc = KC / LM_KSTEP;
+  f32x4_t acc[LM_WIDE_TPW][MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+  for (int t = 0; t < LM_WIDE_TPW; ++t)
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      const int m = mt * 16 + 4 * lg + q;
-      const uint16_t b = f2bf(acc[mt][q]);
-      float bv = bf2f(b);
-      int bi = v;
-      if (bv != bv) {  // NaN never wins
-        bv = -INFINITY;
-        bi = 0x7fffffff;
-      }
-      // (max, first index) over the 16 lanes of this lane group
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  const uint16_t* xrow[MT];
 #pragma unroll
-      for (int o = 1; o < 16; o <<= 1) {
-        const float ov = __shfl_xor(bv, o);
-        const int oi = __shfl_xor(bi, o);
-        if (better(ov, oi, bv, bi)) {
-          bv = ov;
-          bi = oi;
-        }
-      }
-      if (m < p.M) {
-        if (p.logits) p.logits[(int64_t)m * p.ldl + v] = b;
-        if (ln == 0) {
-          p.pval[(int64_t)m * p.NT + tile] = bv;
-          p.pidx[(int64_t)m * p.NT + tile] = bi;
-        }
+  for (int mt = 0; mt < MT; ++mt) xrow[mt] = xs + min(mt * 16 + ln, p.M - 1) * xstride + 8 * lg;
+  // W of (tile slot t, k-step ks): rows of tile gw + t*nw, clamped into range
+  // for a wave without that tile (its loads are then re-reads, never used)
+  auto wptr = [&](int t, int ks) __attribute__((always_inline)) {
+    const int tile = min(gw + min(t, max(ntiles - 1, 0)) * nw, p.NT - 1);
+    return p.w + (int64_t)(tile * 16 + ln) * p.K + 8 * lg + ks * LM_KSTEP;
+  };
+  for (int c0 = 0; c0 < KS; c0 += kpc) {
+    const int nks = min(kpc, KS - c0);
+    const int chunks = nks * LM_KSTEP / 8, total = p.M * chunks;
+    __syncthreads();  // every wave is done with the previous chunk
+    for (int i = tid; i < total; i += 64 * LM_WIDE_WAVES) {
+      const int m = i / chunks, c = i - m * chunks;
+      *reinterpret_cast<uint4*>(xs + m * xstride + 8 * c) =
+          *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + c0 * LM_KSTEP + 8 * c);
+    }
+    __syncthreads();
+    if (ntiles == 0) continue;
+    // (tile slot, k-step) items of this chunk in order, the next step's W in
+    // flight while one is multiplied; the loads are unconditional (the item
+    // past the last re-reads it), so every wait is exact.  (Two steps ahead,
+    // with three register sets, measured slower: 268 against 257 us.)
+    const int nitems = ntiles * nks;
+    uint4 wr[2][8];
+    auto load_item = [&](uint4 (&w)[8], int item) __attribute__((always_inline)) {
+      const int q = min(item, nitems - 1);
+      const uint16_t* wp = wptr(q / nks, c0 + q % nks);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) w[j] = load_stream(wp + 32 * j);
+    };
+    load_item(wr[0], 0);
+    for (int it = 0; it < nitems; it += 2) {
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int cur = it + h;
+        if (cur >= nitems) break;
+        load_item(wr[h ^ 1], cur + 1);
+        const int t = cur / nks, ks = cur - t * nks;
+#pragma unroll
+        for (int ts = 0; ts < LM_WIDE_TPW; ++ts)
+          if (ts == t)
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt)
+                acc[ts][mt] = mfma16x16x32(
+                    *reinterpret_cast<const uint4*>(xrow[mt] + ks * LM_KSTEP + 32 * j),
+                    wr[h][j], acc[ts][mt]);
       }
     }
+  }
+#pragma unroll
+  for (int t = 0; t < LM_WIDE_TPW; ++t)
+    if (t < ntiles) lm_epilogue<MT>(p, gw + t * nw, ln, lg, acc[t]);
 }
 
 // Greedy token of row m from the per-tile (max, index) pairs, then the row's
@@ -277,8 +374,8 @@ int run_lm_head(const void* x, int64_t ldx, const void* w, int V, int K, int M, 
     return GRPO_EWORKSPACE;
   }
   const size_t lds = (size_t)M * (K + 8) * 2 + (nrm ? LM_WAVES * sizeof(float) : 0);
-  if (lds > LM_LDS_MAX) {
-    set_error("lm_head: x [M, K] does not fit in LDS (M * (K + 8) * 2 > 160 KiB)");
+  if (lds > LM_LDS_MAX && nrm) {
+    set_error("lm_head: x [M, K] of the RMSNorm source does not fit in LDS");
     return GRPO_EUNSUPPORTED;
   }
   LmArgs a{};
@@ -294,6 +391,28 @@ int run_lm_head(const void* x, int64_t ldx, const void* w, int V, int K, int M, 
   a.pval = static_cast<float*>(workspace);
   a.pidx = reinterpret_cast<int*>(a.pval + (size_t)M * a.NT);
   const dim3 grid((unsigned)cdiv(a.NT, LM_WAVES)), block(64 * LM_WAVES);
+  if (lds > LM_LDS_MAX) {
+    // x staged in K chunks (the widest multiple of 256 columns that fits), one
+    // workgroup per CU, every tile of a wave accumulated in registers
+    const int KC = (int)(((LM_LDS_MAX / (2 * (size_t)M)) - 8) / LM_KSTEP) * LM_KSTEP;
+    if (KC < LM_KSTEP) return einval("lm_head: too many rows for one x chunk in LDS");
+    const size_t clds = (size_t)M * (KC + 8) * 2;
+    const int G = std::min((int)cdiv(a.NT, LM_WIDE_WAVES), 256);
+    if (cdiv(a.NT, (int64_t)G * LM_WIDE_WAVES) > LM_WIDE_TPW)
+      return einval("lm_head: vocabulary too large for the wide kernel");
+    const dim3 wgrid((unsigned)G), wblock(64 * LM_WIDE_WAVES);
+    if (M <= 16) {
+      if (int rc = allow_lds(lm_head_argmax_wide<1>)) return rc;
+      lm_head_argmax_wide<1><<<wgrid, wblock, clds, st>>>(a, KC);
+    } else if (M <= 32) {
+      if (int rc = allow_lds(lm_head_argmax_wide<2>)) return rc;
+      lm_head_argmax_wide<2><<<wgrid, wblock, clds, st>>>(a, KC);
+    } else {
+      if (int rc = allow_lds(lm_head_argmax_wide<4>)) return rc;
+      lm_head_argmax_wide<4><<<wgrid, wblock, clds, st>>>(a, KC);
+    }
+    return launch_check("lm_head_argmax_wide");
+  }
   if (nrm) {
     a.nss = nrm->sumsq;
     a.nG = nrm->groups;

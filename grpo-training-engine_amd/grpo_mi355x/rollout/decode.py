@@ -182,11 +182,11 @@ class DecodeEngine:
         self.attn_splits = int(self.lib.grpo_paged_attn_splits(
             B, Hq, self.Hkv, D, self.pool.block_size, self.max_blocks))
         self.plans = plans
-        # bf16 lm_head GEMV with fused argmax + device-side row advance, when
-        # x [B, H] fits the kernel's LDS; otherwise hipBLASLt + argmax + torch ops.
+        # bf16 lm_head GEMV with fused argmax + device-side row advance (x staged
+        # whole in LDS, or in K chunks past 160 KiB); otherwise hipBLASLt +
+        # argmax + torch ops.
         lm_bytes = int(self.lib.grpo_lm_head_workspace_bytes(B, self.V))
-        self.lm_fused = (self.V % 16 == 0 and H % 256 == 0 and B <= 64
-                         and B * (H + 8) * 2 <= 160 * 1024)
+        self.lm_fused = self.V % 16 == 0 and H % 256 == 0 and B <= 64
         self.ws_lm = torch.empty(max(lm_bytes, 16), dtype=torch.uint8, device=dev)
         # the sampler's workspace starts zero-filled and every call leaves it so
         self.ws_smp = None

@@ -235,3 +235,32 @@ def test_lm_head_argmax_and_advance(dev):
         assert int(app[m]) == (int(pos[m]) if still else -1)
         assert int(alen[m]) == (int(pos[m]) + 1 if still else 0)
     assert not bool(active[1]) and not bool(active[4])  # limit reached / EOS
+
+
+@pytest.mark.parametrize("M,K", [(64, 3584), (24, 8192), (64, 1024)])
+def test_lm_head_argmax_wide_x_in_k_chunks(dev, M, K):
+    """x [M, K] beyond 160 KiB of LDS (Qwen2-7B at G = 64, and a 24-row case
+    with a short last chunk): staged in K chunks; logits within the bf16
+    tolerance of a float32 product, the per-tile pairs reduce to torch's
+    first-index argmax of the returned logits.  [64, 1024] fits LDS whole."""
+    from grpo_mi355x import _lib
+
+    lib = _lib.device_library()
+    st = _lib.stream_handle(dev)
+    g = torch.Generator().manual_seed(M + K)
+    V = 2048
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(V, K, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    w[700:703] = w[9]  # exact ties: the first index must win
+    logits = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(int(lib.grpo_lm_head_workspace_bytes(M, V)), dtype=torch.uint8, device=dev)
+    print(f"lm_head wide M={M} K={K}", flush=True)
+    _lib.check(lib.grpo_lm_head_argmax(x.data_ptr(), K, w.data_ptr(), V, K, M, logits.data_ptr(),
+                                       V, ws.data_ptr(), ws.numel(), st), "lm_head")
+    nxt = torch.full((M,), -5, dtype=torch.int64, device=dev)
+    _lib.check(lib.grpo_decode_advance(ws.data_ptr(), M, V, nxt.data_ptr(), None, None, None,
+                                       None, None, None, None, 0, None, None, st), "argmax")
+    torch.cuda.synchronize()
+    ref = x.float() @ w.float().t()
+    assert rel_err(logits.float().cpu().numpy(), ref.cpu().numpy()) <= 1e-2
+    assert torch.equal(nxt, logits.float().argmax(dim=1))
