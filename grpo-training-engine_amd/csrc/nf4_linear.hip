@@ -1143,6 +1143,178 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
   }
 }
 
+// ------------------------------------ gate|up + SiLU for 17..64 rows --
+//
+// act[m, 8u + n] = bf16(bf16(silu(bf16(g))) * bf16(u)) for wide decode batches,
+// g and u the gate and up products of x row m with W rows 8u + n and I + 8u + n
+// (the units of nf4_gate_up_units: one 16-column MFMA tile pairs 8 gate and 8
+// up rows).  x of 64 rows does not fit LDS whole, and split-K partial sums of
+// [2I] columns (64 x 37,888 x 4 B per slice for the 7B MLP) plus a SiLU*mul
+// launch cost more than the products, so every unit's accumulators stay in
+// registers across K while x passes through LDS in chunks of 512 K values
+// (two k-steps), double-buffered: the next chunk is loaded into registers
+// while the current one is multiplied, and the next chunk's weights are in
+// flight as well.  One workgroup per CU takes units g, g + G, ...; wave w
+// takes k-step lane w & 1 (k-steps 2c + (w & 1) of chunk c) and the
+// workgroup's units j = (w >> 1) + 4i, so one staged A operand (x rows, 32 K)
+// feeds the MFMAs of up to GUW_UPW units.  At the end the two k-step lanes of
+// a unit are summed through LDS (even k-steps + odd k-steps), the gate and up
+// columns meet by a row rotation of 8 lanes, and lanes n < 8 write act.
+constexpr int GUW_W = 8;                   // waves per workgroup
+constexpr int GUW_S = 2;                   // k-step lanes
+constexpr int GUW_GROUPS = GUW_W / GUW_S;  // unit groups
+constexpr int GUW_UPW = 3;                 // most units per wave
+constexpr int GUW_KC = GUW_S * KSTEP;      // K values of one staged chunk
+constexpr int GUW_XSTRIDE = GUW_KC + 8;    // LDS row stride of a chunk (elements)
+
+template <int MT>
+__global__ void __launch_bounds__(64 * GUW_W) nf4_gate_up_wide(GuArgs p) {
+  constexpr int NTH = 64 * GUW_W;
+  constexpr int XU = 2 * MT;  // x chunks (16 B) per thread per staged chunk: 16*MT rows x 64
+  extern __shared__ __align__(16) uint16_t xs[];  // 2 x [M][GUW_XSTRIDE], decode8 order
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int ln = lane & 15, lg = lane >> 4;
+  const int ksl = wave & (GUW_S - 1), grp = wave / GUW_S;
+  const int G = gridDim.x, g0 = blockIdx.x;
+  const int KS = p.K / KSTEP;
+  const int NC = (KS + GUW_S - 1) / GUW_S;
+  const int U = p.I / 8;
+  const int nu = (U - g0 + G - 1) / G;                          // >= 1 (grid <= U)
+  const int myu = (nu - grp + GUW_GROUPS - 1) / GUW_GROUPS;     // units of this wave, 0..UPW
+  const int rsel = ln < 8 ? ln : p.I + ln - 8;                  // row of unit u: 8u + rsel
+  const int bufsz = p.M * GUW_XSTRIDE;
+  const int total = p.M * (GUW_KC / 8);                          // 16-byte x chunks per chunk
+
+  float code[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
+
+  // Loads: all unconditional with clamped indexes, so every wait is exact
+  // (a chunk past the end re-reads the last one, a missing unit the wave's
+  // last or the workgroup's first).
+  uint4 xv[XU];
+  auto load_x = [&](int c) __attribute__((always_inline)) {
+    c = min(c, NC - 1);
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+      const int i = min(u * NTH + tid, total - 1);
+      const int m = i >> 6, cc = i & 63;
+      const int col = min(c * GUW_KC + 8 * cc, p.K - 8);
+      xv[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + col);
+    }
+  };
+  auto store_x = [&](int c) __attribute__((always_inline)) {
+    uint16_t* buf = xs + (c & 1) * bufsz;
+#pragma unroll
+    for (int u = 0; u < XU; ++u) {
+      const int i = min(u * NTH + tid, total - 1);
+      const int m = i >> 6, cc = i & 63;
+      *reinterpret_cast<uint4*>(buf + m * GUW_XSTRIDE + 8 * cc) = deinterleave8(xv[u]);
+    }
+  };
+  auto load_w_chunk = [&](int c, uint4 (&wv)[2 * GUW_UPW], float (&av)[GUW_UPW])
+      __attribute__((always_inline)) {
+    const int ks = min(c * GUW_S + ksl, KS - 1);
+    const int kc = ks * KSTEP + 64 * lg;
+#pragma unroll
+    for (int t = 0; t < GUW_UPW; ++t) {
+      const int j = min(grp + GUW_GROUPS * min(t, max(myu - 1, 0)), nu - 1);
+      const int64_t row = (int64_t)8 * (g0 + j * G) + rsel;
+      const uint4* wp = reinterpret_cast<const uint4*>(p.w + row * (p.K / 2) + kc / 2);
+      wv[2 * t] = load_w<false>(wp);
+      wv[2 * t + 1] = load_w<false>(wp + 1);
+      av[t] = p.absmax[(row * p.K + kc) >> p.bs_shift];
+    }
+  };
+
+  f32x4_t acc[GUW_UPW][MT];
+#pragma unroll
+  for (int t = 0; t < GUW_UPW; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int c, const uint4 (&wv)[2 * GUW_UPW], const float (&av)[GUW_UPW])
+      __attribute__((always_inline)) {
+    if (c * GUW_S + ksl >= KS || myu == 0) return;  // wave-uniform
+    const uint16_t* buf = xs + (c & 1) * bufsz + ksl * KSTEP + 64 * lg;
+    const uint16_t* xrow[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) xrow[mt] = buf + min(mt * 16 + ln, p.M - 1) * GUW_XSTRIDE;
+    Lut lt[GUW_UPW];
+#pragma unroll
+    for (int t = 0; t < GUW_UPW; ++t) lt[t] = make_lut(code, av[t]);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      uint4 a[MT];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) a[mt] = *reinterpret_cast<const uint4*>(xrow[mt] + 8 * j);
+#pragma unroll
+      for (int t = 0; t < GUW_UPW; ++t) {
+        if (t >= myu) break;
+        const uint4 bw = decode8(word(wv[2 * t + (j >> 2)], j & 3), lt[t]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[t][mt] = mfma16x16x32(a[mt], bw, acc[t][mt]);
+      }
+    }
+  };
+
+  uint4 wa[2 * GUW_UPW], wb[2 * GUW_UPW];
+  float aa[GUW_UPW], ab[GUW_UPW];
+  load_x(0);
+  load_w_chunk(0, wa, aa);
+  store_x(0);
+  load_x(1);
+  __syncthreads();
+  // chunk c: the next chunk's weights are issued, chunk c is multiplied from
+  // LDS buffer c & 1, chunk c + 1 (loaded during chunk c - 1) goes into the
+  // other buffer, chunk c + 2 is loaded.
+  auto step = [&](int c, const uint4 (&wc)[2 * GUW_UPW], const float (&ac)[GUW_UPW],
+                  uint4 (&wn)[2 * GUW_UPW], float (&an)[GUW_UPW]) __attribute__((always_inline)) {
+    load_w_chunk(c + 1, wn, an);
+    compute(c, wc, ac);
+    store_x(c + 1);
+    load_x(c + 2);
+    __syncthreads();
+  };
+  for (int c = 0; c < NC; c += 2) {
+    step(c, wa, aa, wb, ab);
+    if (c + 1 < NC) step(c + 1, wb, ab, wa, aa);
+  }
+
+  // k-step lane 1 hands its sums to lane 0 through LDS (both x buffers are free)
+  f32x4_t* red = reinterpret_cast<f32x4_t*>(xs);  // [GROUPS][UPW][MT][64]
+  if (ksl == 1) {
+#pragma unroll
+    for (int t = 0; t < GUW_UPW; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) red[((grp * GUW_UPW + t) * MT + mt) * 64 + lane] = acc[t][mt];
+  }
+  __syncthreads();
+  if (ksl != 0) return;
+#pragma unroll
+  for (int t = 0; t < GUW_UPW; ++t) {
+    if (t >= myu) break;
+    const int col = 8 * (g0 + (grp + GUW_GROUPS * t) * G) + (ln & 7);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const f32x4_t o1 = red[((grp * GUW_UPW + t) * MT + mt) * 64 + lane];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        // lane (n = ln, group lg) holds D[m = 4*lg + r][n]; n < 8 gate, n >= 8 up
+        const float v = acc[t][mt][r] + o1[r];
+        const float other = dpp_move<0x128>(v);  // row_ror:8: the lane 8 columns away
+        const int m = mt * 16 + 4 * lg + r;
+        if (ln < 8 && m < p.M) {
+          const float gv = round_bf(v);
+          const float o = round_bf(gv * (1.f / (1.f + expf(-gv)))) * round_bf(other);
+          p.act[(int64_t)m * p.lda + col] = f2bf(o);
+        }
+      }
+    }
+  }
+}
+
 // ------------------------------ down_proj + residual add for M <= 8 rows --
 //
 // h_out[m, n] = bf16(residual[m, n] + bf16(x[m, :] . W[n, :])) (NF4 W, no LoRA,
@@ -1334,6 +1506,20 @@ bool plan_gu(int M, int I, int K, int blocksize, GuPlan* pl) {
   pl->MT = 1;
   pl->lds = (size_t)M * (K + 8) * 2 + (size_t)2 * pl->S * M * 16 * 4;
   return pl->lds <= 65536;
+}
+
+// Shape support of nf4_gate_up_wide (17..64 rows) and its LDS bytes.
+bool gu_wide_ok(int M, int I, int K, int blocksize, size_t* lds) {
+  if (M < 17 || M > 64 || I <= 0 || I % 8 || K < KSTEP || K % KSTEP) return false;
+  if (!pow2(blocksize) || blocksize < 64) return false;
+  const int U = I / 8;
+  const int G = std::min(U, g_gu_units_grid);
+  if ((U + G - 1) / G > GUW_GROUPS * GUW_UPW) return false;
+  const int MT = (M + 15) / 16;
+  const size_t xbytes = (size_t)2 * M * GUW_XSTRIDE * 2;
+  const size_t rbytes = (size_t)GUW_GROUPS * GUW_UPW * MT * 64 * 16;
+  *lds = std::max(xbytes, rbytes);
+  return *lds <= (size_t)PART_LDS_BIG;
 }
 
 // ---------------------------------------------------- generic linear --
@@ -1727,7 +1913,8 @@ extern "C" int grpo_nf4_linear_partials_silu(const grpo_linear_parts_t* gate_up,
 
 extern "C" int grpo_nf4_gate_up_silu_supported(int M, int I, int K, int blocksize) {
   GuPlan pl;
-  return plan_gu(M, I, K, blocksize, &pl) ? 1 : 0;
+  size_t lds;
+  return plan_gu(M, I, K, blocksize, &pl) || gu_wide_ok(M, I, K, blocksize, &lds) ? 1 : 0;
 }
 
 namespace {
@@ -1867,7 +2054,9 @@ int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absma
                 const float* code16, int blocksize, int I, int K, int M, void* act, int64_t lda,
                 int act_tiles, hipStream_t st, const NormSource* nrm) {
   GuPlan pl;
-  if (!plan_gu(M, I, K, blocksize, &pl)) {
+  size_t wlds = 0;
+  const bool wide = !nrm && !act_tiles && gu_wide_ok(M, I, K, blocksize, &wlds);
+  if (!wide && !plan_gu(M, I, K, blocksize, &pl)) {
     set_error("shape not supported by the fused gate|up SiLU kernel");
     return GRPO_EUNSUPPORTED;
   }
@@ -1895,6 +2084,21 @@ int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absma
     a.nG = nrm->groups;
     a.nw = nrm->weight;
     a.neps = nrm->eps;
+  }
+  if (wide) {
+    const int G = std::min(I / 8, g_gu_units_grid);
+    const dim3 grid((unsigned)G), block(64 * GUW_W);
+    switch ((M + 15) / 16) {
+#define GUW_CASE(MT)                                                        \
+  case MT:                                                                  \
+    if (int rc = allow_big_lds(nf4_gate_up_wide<MT>)) return rc;            \
+    nf4_gate_up_wide<MT><<<grid, block, wlds, st>>>(a);                     \
+    break;
+      GUW_CASE(2) GUW_CASE(3) GUW_CASE(4)
+#undef GUW_CASE
+      default: return einval("gate|up wide kernel: 17..64 rows");
+    }
+    return launch_check("nf4_gate_up_wide");
   }
   {
     // units kernel: at most one workgroup per CU, every item of a wave in registers

@@ -102,14 +102,22 @@ def test_add_rmsnorm_parts_matches_oracle(dev, n, lora, offset):
 
 
 @pytest.mark.parametrize("m,i,k", [(8, 8960, 1536), (3, 256, 512), (16, 512, 1536),
-                                   (8, 512, 3584), (8, 17920, 3584), (5, 4112, 512)])
+                                   (8, 512, 3584), (8, 17920, 3584), (5, 4112, 512),
+                                   (17, 256, 512), (32, 8960, 1536), (40, 8960, 1536),
+                                   (64, 2048, 768), (48, 20480, 256), (64, 18944, 3584)])
 def test_gate_up_silu_matches_oracle(dev, m, i, k):
     """grpo_nf4_gate_up_silu = oracle NF4 linear of the gate and up halves of a
     stacked weight, then oracle SiLU*mul (fused_ops.py:79-112).  The first four
-    and the last shape run the 8-column-unit kernel (the last has 514 units over
-    256 workgroups: two workgroups take a third unit); [8, 17920, 3584] has more
-    items per wave than the unit kernel keeps in registers and runs one
-    workgroup per 16 columns."""
+    and the sixth shape run the 8-column-unit kernel (the sixth has 514 units
+    over 256 workgroups: two workgroups take a third unit); [8, 17920, 3584]
+    has more items per wave than the unit kernel keeps in registers and runs
+    one workgroup per 16 columns.  17..64 rows run the wide kernel (x staged in
+    512-column chunks, unit accumulators in registers across K): one unit per
+    workgroup, so three of the four unit groups are empty (17 x 256); config
+    4's and a 3-row-tile shape; an odd number of k-steps, whose last chunk has
+    one (64 x 2048 x 768); a single k-step and 10 units per workgroup
+    (48 x 20480 x 256); config 5's Qwen2-7B MLP (2368 units: 9 or 10 per
+    workgroup)."""
     from grpo_mi355x import _lib
 
     from oracle.decode import silu_mul
@@ -145,9 +153,13 @@ def test_gate_up_silu_rejects_unsupported(dev):
     from grpo_mi355x import _lib
 
     lib = _lib.device_library()
-    assert lib.grpo_nf4_gate_up_silu_supported(17, 256, 512, 64) == 0  # M > 16
+    assert lib.grpo_nf4_gate_up_silu_supported(65, 256, 512, 64) == 0  # M > 64
     assert lib.grpo_nf4_gate_up_silu_supported(8, 250, 512, 64) == 0   # I % 16
+    assert lib.grpo_nf4_gate_up_silu_supported(32, 250, 512, 64) == 0  # I % 8
     assert lib.grpo_nf4_gate_up_silu_supported(8, 256, 500, 64) == 0   # K % 256
+    assert lib.grpo_nf4_gate_up_silu_supported(32, 256, 500, 64) == 0  # K % 256
     assert lib.grpo_nf4_gate_up_silu_supported(8, 256, 6400, 64) == 0  # K > 6144
-    assert lib.grpo_nf4_gate_up_silu(None, 512, None, None, None, 64, 256, 512, 17, None, 256,
+    assert lib.grpo_nf4_gate_up_silu_supported(32, 256, 512, 32) == 0  # blocksize < 64
+    assert lib.grpo_nf4_gate_up_silu_supported(32, 24584, 512, 64) == 0  # > 12 units per CU
+    assert lib.grpo_nf4_gate_up_silu(None, 512, None, None, None, 64, 256, 512, 65, None, 256,
                                      None) == -2  # GRPO_EUNSUPPORTED
