@@ -37,6 +37,9 @@ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 __host__ __device__ inline bool aligned16(const void* ptr) {
   return (reinterpret_cast<uintptr_t>(ptr) & 15u) == 0;
 }
+__host__ __device__ inline bool aligned8(const void* ptr) {
+  return (reinterpret_cast<uintptr_t>(ptr) & 7u) == 0;
+}
 
 // ---------------------------------------------------------------- bf16 ---
 // float -> bf16 round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).

@@ -181,10 +181,26 @@ struct PartArgs {
   int nG;
   const uint16_t* nw;  // RMSNorm weight [K] bf16
   float neps;
+  // Finish in the kernel (FIN): the K slice of a tile group that arrives last
+  // sums the group's partials and writes h = residual + y for its columns.
+  float* fin_tpart;         // [groups][S][M][16]: LoRA t partials of each group's slices
+  int* fin_cnt;             // [groups * FIN_CNT_STRIDE] arrival counters: zero, left zero
+  const uint16_t* fin_res;  // residual [M][fin_ld] bf16 (may alias fin_h)
+  uint16_t* fin_h;          // h [M][fin_ld] bf16
+  int64_t fin_ld;
+  float* fin_ss;            // [M][groups]: sums of h^2 over each group's columns
+  const uint16_t* fin_bias; // [N] bf16 or null
+  const uint16_t* fin_lb;   // LoRA B [N][r] bf16 (r > 0)
+  float fin_scaling;
+  int fin_lb_vec;           // r == 16 and lora_b 16-byte aligned
 };
 
 // X_WIDE: bf16, 16 waves; X_NORM: RMSNorm of h from per-group sums of squares
 enum XSource { X_BF16 = 0, X_ATTN = 1, X_SILU = 2, X_WIDE = 3, X_NORM = 4 };
+// One arrival counter per 128-byte line: a tile group's counter line is only
+// ever touched by the workgroups of that group, which share one XCD's L2.
+constexpr int FIN_CNT_STRIDE = 32;
+constexpr int FIN_MAX_SLICES = 8;
 constexpr int NORM_MAX_GROUPS = 256;  // sums of squares per row the X_NORM source reads
 
 // n-tiles (waves) per workgroup.  Every workgroup of a K slice rebuilds the x
@@ -341,7 +357,124 @@ __device__ __forceinline__ float sum16(float v) {
 }
 
 
-template <int MT, int KPW, int XSRC>
+// Last-arriver finish of tile group g (FIN): columns n0 .. n0 + 16 * WPG - 1 of
+// every row, n0 = g * 16 * WPG, from the partial sums and LoRA t partials that
+// the group's S workgroups (one per K slice) stored.  The reference epilogue
+// and residual add in the order and roundings of lin_finish4 and
+// finish_residual_sumsq_kernel (linear_parts.hpp, decode_ops.hip), and
+// fin_ss[m][g] = sum over the group's columns of h^2.  Thread t < M * 16 * WPG / 4
+// owns row t / (4 * WPG), columns n0 + 4 (t % (4 * WPG)) .. + 3; the inputs
+// that no K slice produces (residual, bias, LoRA B) were loaded at kernel
+// start into res/bias/lb.
+template <int WPG>
+struct FinPre {
+  uint2 res, bias;
+  uint4 lb[8];
+};
+
+template <int WPG>
+__device__ __forceinline__ void fin_prefetch(const PartArgs& p, int g, FinPre<WPG>& f) {
+  constexpr int TPR = 4 * WPG;  // threads per row
+  const int t = threadIdx.x;
+  const int m = min(t / TPR, p.M - 1);
+  const int n = g * 16 * WPG + 4 * (t % TPR);
+  f.res = *reinterpret_cast<const uint2*>(p.fin_res + (int64_t)m * p.fin_ld + n);
+  if (p.fin_bias) f.bias = *reinterpret_cast<const uint2*>(p.fin_bias + n);
+  if (p.r > 0 && p.fin_lb_vec) {
+    const uint4* br = reinterpret_cast<const uint4*>(p.fin_lb + (int64_t)n * 16);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f.lb[j] = br[j];
+  }
+}
+
+template <int WPG>
+__device__ __forceinline__ void fin_group(const PartArgs& p, int g, const FinPre<WPG>& f) {
+  constexpr int TPR = 4 * WPG;
+  constexpr int COLS = 16 * WPG;
+  __shared__ float ts[16 * 16];  // LoRA t of each row (M <= 16)
+  const int t = threadIdx.x;
+  const int S = gridDim.y;
+  const int G = p.NT / WPG;
+  const int m = t / TPR;
+  const bool act = m < p.M;
+  const int n = g * COLS + 4 * (t % TPR);
+  // every load of the finish goes out before the barrier
+  float4 pv[FIN_MAX_SLICES];
+  {
+    const float4* pp =
+        reinterpret_cast<const float4*>(p.part + (int64_t)min(m, p.M - 1) * p.N + n);
+    const int64_t stride = (int64_t)p.Mp * p.N / 4;
+#pragma unroll
+    for (int s = 0; s < FIN_MAX_SLICES; ++s) pv[s] = pp[min(s, S - 1) * stride];
+  }
+  float tv[FIN_MAX_SLICES];
+  const bool tlane = t < p.M * 16 && p.r > 0;
+  if (p.r > 0) {
+    const float* tp = p.fin_tpart + ((int64_t)g * S * p.M) * 16 + min(t, p.M * 16 - 1);
+#pragma unroll
+    for (int s = 0; s < FIN_MAX_SLICES; ++s) tv[s] = tp[(int64_t)min(s, S - 1) * p.M * 16];
+  }
+  if (tlane) {
+    float acc = 0.f;
+#pragma unroll
+    for (int s = 0; s < FIN_MAX_SLICES; ++s)
+      if (s < S) acc += tv[s];
+    ts[t] = round_bf(acc);
+  }
+  __syncthreads();
+  if (!act) return;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int s = 0; s < FIN_MAX_SLICES; ++s)
+    if (s < S) {
+      acc.x += pv[s].x;
+      acc.y += pv[s].y;
+      acc.z += pv[s].z;
+      acc.w += pv[s].w;
+    }
+  float v[4] = {round_bf(acc.x), round_bf(acc.y), round_bf(acc.z), round_bf(acc.w)};
+  if (p.fin_bias) {
+    const float b[4] = {bf_lo(f.bias.x), bf_hi(f.bias.x), bf_lo(f.bias.y), bf_hi(f.bias.y)};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) v[c] = round_bf(v[c] + b[c]);
+  }
+  if (p.r > 0) {
+    const float* tr = ts + m * 16;
+    const float sc = round_bf(p.fin_scaling);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float u = 0.f;
+      if (p.fin_lb_vec) {
+        const uint4 b0 = f.lb[2 * c], b1 = f.lb[2 * c + 1];
+        const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          u += tr[2 * j] * bf_lo(bw[j]);
+          u += tr[2 * j + 1] * bf_hi(bw[j]);
+        }
+      } else {
+        const uint16_t* br = p.fin_lb + (int64_t)(n + c) * p.r;
+        for (int j = 0; j < p.r; ++j) u += tr[j] * bf2f(br[j]);
+      }
+      u = round_bf(round_bf(u) * sc);
+      v[c] = round_bf(v[c] + u);
+    }
+  }
+  const float r[4] = {bf_lo(f.res.x), bf_hi(f.res.x), bf_lo(f.res.y), bf_hi(f.res.y)};
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < 4; ++c) {
+    v[c] = round_bf(v[c] + r[c]);
+    ss += v[c] * v[c];
+  }
+  *reinterpret_cast<uint2*>(p.fin_h + (int64_t)m * p.fin_ld + n) =
+      make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+  // the TPR = 16 threads of a row are one DPP row of 16 lanes
+  ss = sum16(ss);
+  if (t % TPR == 0) p.fin_ss[(int64_t)m * G + g] = ss;
+}
+
+template <int MT, int KPW, int XSRC, bool FIN = false>
 __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(PartArgs p) {
   touch_kernargs<sizeof(PartArgs)>();
   constexpr int WPG = waves_per_group(XSRC), NT = 64 * WPG;
@@ -351,6 +484,10 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
+  // FIN: wave 0 also takes the LoRA-A tile of this K slice for its group
+  // after its weight tile (every group computes its own copy, so the group's
+  // finish reads nothing written on another XCD).
+  const bool lwave = FIN && wave == 0;
   const int tile = blockIdx.x * WPG + wave;
   const int slice = blockIdx.y;
   const int ks0 = slice * KPW;
@@ -445,6 +582,19 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
       av[i] = p.absmax[((int64_t)wr * p.K + kc) >> p.bs_shift];
     }
   }
+  // FIN: the finish's inputs that no K slice produces, behind the weights (the
+  // MFMAs wait only for the loads before them), and the LoRA wave's A rows
+  FinPre<WPG> fpre;
+  if (FIN) fin_prefetch<WPG>(p, blockIdx.x, fpre);
+  uint4 a8f[FIN ? 8 * KPW : 1];
+  if (FIN && lwave && p.r > 0) {
+    const uint16_t* arow = p.la[0] + (int64_t)(ln < p.r ? ln : 0) * p.K + kbase + 64 * lg;
+#pragma unroll
+    for (int i = 0; i < KPW; ++i)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        a8f[8 * i + j] = *reinterpret_cast<const uint4*>(arow + min(i, nk - 1) * KSTEP + 8 * j);
+  }
 
   // Stage x[:, kbase : kbase + nk*256] in LDS (decode8 order), four chunks per
   // thread per batch.  A batch entry that starts past the end is skipped by
@@ -500,7 +650,7 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
     }
   }
   __syncthreads();
-  if (tile >= p.ntiles) return;
+  if (!FIN && tile >= p.ntiles) return;
 
   f32x4_t acc[MT];
 #pragma unroll
@@ -531,9 +681,12 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
         const int m = mt * 16 + 4 * lg + q;
         if (m < p.M) out[(int64_t)m * p.N] = acc[mt][q];
       }
-  } else {
+  }
+  if (FIN ? lwave && p.r > 0 : !wtile) {
     // LoRA-A tile of segment seg: lane n = rank index, A is read as bf16.
-    const int seg = tile - p.NT;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int seg = FIN ? 0 : tile - p.NT;
     const bool r_ok = ln < p.r;
     const uint16_t* arow = sel_seg(p.la, seg) + (int64_t)(r_ok ? ln : 0) * p.K + kbase + 64 * lg;
 #pragma unroll
@@ -541,9 +694,13 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
       if (i >= nk) break;
       uint4 a8[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        a8[j] = r_ok ? *reinterpret_cast<const uint4*>(arow + i * KSTEP + 8 * j)
-                     : make_uint4(0, 0, 0, 0);
+      for (int j = 0; j < 8; ++j) {
+        if (FIN)
+          a8[j] = r_ok ? a8f[8 * i + j] : make_uint4(0, 0, 0, 0);
+        else
+          a8[j] = r_ok ? *reinterpret_cast<const uint4*>(arow + i * KSTEP + 8 * j)
+                       : make_uint4(0, 0, 0, 0);
+      }
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const uint4 bv = deinterleave8(a8[j]);
@@ -553,7 +710,8 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
               *reinterpret_cast<const uint4*>(xrow[mt] + i * KSTEP + 8 * j), bv, acc[mt]);
       }
     }
-    float* out = p.tpart + ((int64_t)slice * p.nseg + seg) * p.Mp * 16 + ln;
+    float* out = FIN ? p.fin_tpart + ((int64_t)blockIdx.x * gridDim.y + slice) * p.M * 16 + ln
+                     : p.tpart + ((int64_t)slice * p.nseg + seg) * p.Mp * 16 + ln;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -561,6 +719,29 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
         const int m = mt * 16 + 4 * lg + q;
         if (m < p.M) out[m * 16] = acc[mt][q];
       }
+  }
+  if (FIN) {
+    // Arrival: this workgroup's partials are in the XCD's L2 once its stores
+    // are acknowledged (the vector L1 writes through); the group's counter is
+    // an L2 atomic.  The last of the S slices resets the counter, drops its
+    // L1 lines (a CU keeps no line of another workgroup's partials from this
+    // kernel, but the invalidate costs nothing) and finishes the group.  Every
+    // workgroup of a group has the same linear id modulo 8 (gridDim.x is a
+    // multiple of 8), so the group runs on one XCD and shares one L2.
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ int s_last;
+    if (tid == 0) {
+      int* c = p.fin_cnt + (int64_t)blockIdx.x * FIN_CNT_STRIDE;
+      const int old = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      const int last = old == (int)gridDim.y - 1;
+      if (last) *c = 0;
+      s_last = last;
+    }
+    __syncthreads();
+    if (!s_last) return;
+    asm volatile("buffer_inv sc0" ::: "memory");
+    fin_group<WPG>(p, blockIdx.x, fpre);
   }
 }
 
@@ -678,12 +859,12 @@ int allow_big_lds(Kern kernel) {
   return rc;
 }
 
-template <int MT, int KPW, int XSRC>
+template <int MT, int KPW, int XSRC, bool FIN = false>
 int launch_part_k(const PartArgs& a, const PartPlan& pl, const dim3& grid, const dim3& block,
                   hipStream_t st) {
   if (pl.lds > (size_t)PART_LDS_MAX)
-    if (int rc = allow_big_lds(nf4_part_mfma<MT, KPW, XSRC>)) return rc;
-  nf4_part_mfma<MT, KPW, XSRC><<<grid, block, pl.lds, st>>>(a);
+    if (int rc = allow_big_lds(nf4_part_mfma<MT, KPW, XSRC, FIN>)) return rc;
+  nf4_part_mfma<MT, KPW, XSRC, FIN><<<grid, block, pl.lds, st>>>(a);
   return launch_check("nf4_part_mfma");
 }
 
@@ -701,6 +882,31 @@ int launch_part(const PartArgs& a, const PartPlan& pl, hipStream_t st) {
     default: return launch_part_k<MT, 8, XSRC>(a, pl, grid, block, st);
   }
 }
+
+// FIN launch: one workgroup per (tile group, K slice), the LoRA-A tile of
+// every workgroup on its wave 0; a.ntiles = NT (no LoRA tiles).  gridDim.x is a multiple of 8, so
+// the K slices of a tile group share an XCD (the finish relies on it).
+template <int XSRC>
+int launch_part_fin(const PartArgs& a, const PartPlan& pl, hipStream_t st) {
+  constexpr int WPG = waves_per_group(XSRC);
+  const int groups = pl.NT / WPG;
+  const dim3 grid((unsigned)(cdiv(groups, NUM_XCD) * NUM_XCD), (unsigned)pl.S), block(64 * WPG);
+  switch (pl.kpw) {
+    case 1: return launch_part_k<1, 1, XSRC, true>(a, pl, grid, block, st);
+    case 2: return launch_part_k<1, 2, XSRC, true>(a, pl, grid, block, st);
+    default: return einval("in-kernel finish: at most 2 k-steps per K slice");
+  }
+}
+
+// Where a FIN launch writes (the residual add after the linear).
+struct FinTarget {
+  float* tpart = nullptr;  // [groups][S][M][16]
+  int* cnt = nullptr;      // [groups * FIN_CNT_STRIDE]
+  const uint16_t* res = nullptr;
+  uint16_t* h = nullptr;
+  int64_t ld = 0;
+  float* ss = nullptr;     // [M][groups]
+};
 
 // Attention-output source of x (o_proj of the decode step), or all-null.
 struct AttnSource {
@@ -729,7 +935,8 @@ struct NormSource {
 int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* absmax,
                  const float* code16, int blocksize, const uint16_t* const* la,
                  const grpo_linear_parts_t& h, hipStream_t st, const AttnSource* att = nullptr,
-                 const SiluSource* silu = nullptr, const NormSource* nrm = nullptr) {
+                 const SiluSource* silu = nullptr, const NormSource* nrm = nullptr,
+                 const FinTarget* fin = nullptr) {
   const bool xsrc = att || silu || nrm;
   if (!part_shape_ok(h.M, h.N, h.K, h.r, h.nseg, blocksize, h.seg_end)) {
     set_error("shape not supported by the split-K NF4 linear");
@@ -772,6 +979,34 @@ int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* 
   a.nseg = h.nseg;
   a.r = h.r;
   a.xstride = pl.xstride;
+  if (fin) {
+    // in-kernel finish: <= 16 rows, one LoRA segment, whole tile groups
+    constexpr int WPG = waves_per_group(X_ATTN);
+    if (!att || pl.MT != 1 || h.nseg != 1 || pl.NT % WPG != 0 || pl.S > FIN_MAX_SLICES ||
+        pl.kpw > 2) {
+      set_error("shape not supported by the in-kernel linear finish");
+      return GRPO_EUNSUPPORTED;
+    }
+    const int groups = pl.NT / WPG;
+    if (!fin->cnt || !fin->res || !fin->h || !fin->ss || (h.r > 0 && !fin->tpart))
+      return einval("null pointer");
+    if (fin->ld < h.N || fin->ld % 4 || !aligned8(fin->res) || !aligned8(fin->h))
+      return einval("residual/h: ld must be >= N and a multiple of 4, rows 8-byte aligned");
+    if (h.bias[0] && !aligned8(h.bias[0])) return einval("bias must be 8-byte aligned");
+    if (h.r > 0 && !h.lora_b[0]) return einval("r > 0 needs lora_b");
+    a.ntiles = pl.NT;
+    a.fin_tpart = fin->tpart;
+    a.fin_cnt = fin->cnt;
+    a.fin_res = fin->res;
+    a.fin_h = fin->h;
+    a.fin_ld = fin->ld;
+    a.fin_ss = fin->ss;
+    a.fin_bias = static_cast<const uint16_t*>(h.bias[0]);
+    a.fin_lb = static_cast<const uint16_t*>(h.lora_b[0]);
+    a.fin_scaling = h.scaling;
+    a.fin_lb_vec = h.r == 16 && aligned16(h.lora_b[0]);
+    (void)groups;
+  }
   if (att) {
     a.att_o = att->o;
     a.att_ml = att->ml;
@@ -780,6 +1015,7 @@ int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* 
     a.att_bps = att->bps;
     a.att_Hq = att->Hq;
     a.att_cap = att->cap;
+    if (fin) return launch_part_fin<X_ATTN>(a, pl, st);
     switch (pl.MT) {
       case 1: return launch_part<1, X_ATTN>(a, pl, st);
       case 2: return launch_part<2, X_ATTN>(a, pl, st);
@@ -872,7 +1108,7 @@ struct GuArgs {
   const uint16_t* nw;
   float neps;
 };
-constexpr int GU_NORM_MAX_GROUPS = 16;  // sums of squares per row (8 lanes x 2)
+constexpr int GU_NORM_MAX_GROUPS = 32;  // sums of squares per row (8 lanes x 4)
 
 // Position of element e (0..7) of an 8-element chunk in the decode8 order
 // [0, 2, 4, 6, 1, 3, 5, 7].
@@ -1848,14 +2084,12 @@ extern "C" int grpo_nf4_lora_linear_grouped(const void* x, int64_t ldx, const ui
   return run_linear(g, workspace, workspace_bytes, as_stream(stream));
 }
 
-extern "C" int grpo_nf4_linear_partials_attn(const void* attn_workspace,
-                                             const int32_t* context_lens, int Hq, int Hkv,
-                                             int D, int block_size, int max_blocks,
-                                             const uint8_t* w, const float* absmax,
-                                             const float* code16, int blocksize,
-                                             const void* const* lora_a,
-                                             const grpo_linear_parts_t* parts,
-                                             grpo_stream_t stream) {
+namespace {
+int run_partials_attn(const void* attn_workspace, const int32_t* context_lens, int Hq, int Hkv,
+                      int D, int block_size, int max_blocks, const uint8_t* w,
+                      const float* absmax, const float* code16, int blocksize,
+                      const void* const* lora_a, const grpo_linear_parts_t* parts,
+                      grpo_stream_t stream, const FinTarget* fin) {
   if (!parts) return einval("null parts descriptor");
   if (blocksize <= 0) return einval("blocksize must be > 0");
   LinParts check;
@@ -1881,7 +2115,49 @@ extern "C" int grpo_nf4_linear_partials_attn(const void* attn_workspace,
     for (int s = 0; s < parts->nseg; ++s) la[s] = static_cast<const uint16_t*>(lora_a[s]);
   }
   return run_partials(nullptr, 0, w, absmax, code16, blocksize, la, *parts, as_stream(stream),
-                      &att);
+                      &att, nullptr, nullptr, fin);
+}
+}  // namespace
+
+extern "C" int grpo_nf4_linear_partials_attn(const void* attn_workspace,
+                                             const int32_t* context_lens, int Hq, int Hkv,
+                                             int D, int block_size, int max_blocks,
+                                             const uint8_t* w, const float* absmax,
+                                             const float* code16, int blocksize,
+                                             const void* const* lora_a,
+                                             const grpo_linear_parts_t* parts,
+                                             grpo_stream_t stream) {
+  return run_partials_attn(attn_workspace, context_lens, Hq, Hkv, D, block_size, max_blocks, w,
+                           absmax, code16, blocksize, lora_a, parts, stream, nullptr);
+}
+
+extern "C" int grpo_nf4_linear_attn_residual_groups(int M, int N, int K, int r, int blocksize,
+                                                    size_t* tpart_bytes, size_t* counter_bytes) {
+  constexpr int WPG = waves_per_group(X_ATTN);
+  if (!part_shape_ok(M, N, K, r, 1, blocksize, nullptr)) return 0;
+  const PartPlan pl = plan_part(M, N, K, r, 1);
+  if (!pl.ok || pl.MT != 1 || pl.NT % WPG != 0 || pl.S > FIN_MAX_SLICES || pl.kpw > 2) return 0;
+  const int groups = pl.NT / WPG;
+  if (tpart_bytes) *tpart_bytes = (size_t)groups * pl.S * M * 16 * sizeof(float);
+  if (counter_bytes) *counter_bytes = (size_t)groups * FIN_CNT_STRIDE * sizeof(int);
+  return groups;
+}
+
+extern "C" int grpo_nf4_linear_attn_residual(
+    const void* attn_workspace, const int32_t* context_lens, int Hq, int Hkv, int D,
+    int block_size, int max_blocks, const uint8_t* w, const float* absmax, const float* code16,
+    int blocksize, const void* const* lora_a, const grpo_linear_parts_t* parts,
+    float* group_tpart, int* counters, const void* residual, void* h_out, int64_t ld,
+    float* sumsq, grpo_stream_t stream) {
+  FinTarget fin;
+  fin.tpart = group_tpart;
+  fin.cnt = counters;
+  fin.res = static_cast<const uint16_t*>(residual);
+  fin.h = static_cast<uint16_t*>(h_out);
+  fin.ld = ld;
+  fin.ss = sumsq;
+  return run_partials_attn(attn_workspace, context_lens, Hq, Hkv, D, block_size, max_blocks, w,
+                           absmax, code16, blocksize, lora_a, parts, stream, &fin);
 }
 
 extern "C" int grpo_nf4_linear_partials_silu(const grpo_linear_parts_t* gate_up, const uint8_t* w,
@@ -1947,7 +2223,7 @@ extern "C" int grpo_nf4_gate_up_silu_tiles_norm(const void* h, int64_t ldh, cons
                                                 int M, void* act_tiles, grpo_stream_t stream) {
   if (M > 8) return einval("the fold tile layout holds at most 8 rows");
   if (!h || !sumsq || !norm_weight) return einval("null pointer");
-  if (groups < 1 || groups > GU_NORM_MAX_GROUPS) return einval("groups must be in [1, 16]");
+  if (groups < 1 || groups > GU_NORM_MAX_GROUPS) return einval("groups must be in [1, 32]");
   if (!aligned16(norm_weight)) return einval("norm_weight must be 16-byte aligned");
   NormSource src;
   src.h = static_cast<const uint16_t*>(h);

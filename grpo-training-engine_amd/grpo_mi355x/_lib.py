@@ -138,6 +138,13 @@ SIGNATURES = {
         _I32,
         [_VP, _VP, _I32, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _I32, _VP, _PARTS, _VP],
     ),
+    "grpo_nf4_linear_attn_residual": (
+        _I32,
+        [_VP, _VP, _I32, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _I32, _VP, _PARTS, _VP, _VP,
+         _VP, _VP, _I64, _VP, _VP],
+    ),
+    "grpo_nf4_linear_attn_residual_groups": (
+        _I32, [_I32, _I32, _I32, _I32, _I32, _VP, _VP]),
     "grpo_paged_attn_decode": (
         _I32,
         [_VP, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32,

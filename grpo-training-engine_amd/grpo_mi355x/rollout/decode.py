@@ -212,6 +212,20 @@ class DecodeEngine:
                      and bool(self.lib.grpo_nf4_gate_up_silu_tiles_norm_supported(B, I, H, bs)))
         self.ss = torch.zeros(B, max(H // 8, 1), dtype=torch.float32, device=dev)
         self.ss_post = torch.zeros(B, -(-H // 256), dtype=torch.float32, device=dev)
+        # o_proj finishing its own columns (the K slice of each 64-column group
+        # that ends last adds the epilogue and the residual, and writes the
+        # group's sums of squares): no separate finish launch
+        self.o_fin = False
+        if self.fold and self.O_FIN and B <= self.ATTN_STAGE_MAX_ROWS:
+            tb, cb = ctypes.c_size_t(0), ctypes.c_size_t(0)
+            G = int(self.lib.grpo_nf4_linear_attn_residual_groups(
+                B, H, Hq * D, r, bs, ctypes.byref(tb), ctypes.byref(cb)))
+            if 0 < G <= self.GU_NORM_MAX_GROUPS:
+                self.o_fin = True
+                self.o_tpart = torch.zeros(max(tb.value // 4, 1), dtype=torch.float32, device=dev)
+                # arrival counters: zero before the first launch, left zero by every launch
+                self.o_cnt = torch.zeros(cb.value // 4, dtype=torch.int32, device=dev)
+                self.ss_post = torch.zeros(B, G, dtype=torch.float32, device=dev)
         # the embedding's row statistic for layer 0's input norm
         self.ss_embed = torch.zeros(B, int(self.lib.grpo_embedding_sumsq_groups()),
                                     dtype=torch.float32, device=dev)
@@ -230,6 +244,9 @@ class DecodeEngine:
         if self.fold:
             # weight + absmax + x + residual read + h written + sums of squares
             self.bytes["down"] = nf4(H, I) + B * I * 2 + 2 * B * H * 2 + B * (H // 8) * 4
+        if self.o_fin:
+            # ... and o_proj's residual read, h written and sums of squares
+            self.bytes["o"] += 2 * B * H * 2 + B * self.ss_post.shape[1] * 4
 
     def splits(self, kind: str) -> int:
         """K slices of an NF4 launch kind (1 for the folded down_proj)."""
@@ -248,6 +265,9 @@ class DecodeEngine:
     # grpo_nf4_linear_residual + grpo_nf4_linear_partials_norm for <= 8 rows
     FOLD_DOWN = True
     NORM_MAX_GROUPS = 256  # sums of squares per row the q|k|v norm staging reads
+    GU_NORM_MAX_GROUPS = 32  # ... and the gate|up norm staging
+    # o_proj + its epilogue + residual add in one launch (<= 16 rows)
+    O_FIN = True
 
     def launches(self) -> list:
         """[(kind, launch())] of one forward pass, in order, bound to torch's
@@ -298,8 +318,10 @@ class DecodeEngine:
                 # gate|up staging RMSNorm(h) and writing act in the tile layout
                 # the folded down_proj loads
                 sp = self.ss_post.data_ptr()
-                out.append(("rmsnorm", lambda L=L, sp=sp: chk(lib.grpo_linear_finish_residual(
-                    L["o_parts"], h, h, H, sp, st), "post_finish")))
+                if not self.o_fin:
+                    out.append(("rmsnorm", lambda L=L, sp=sp: chk(
+                        lib.grpo_linear_finish_residual(L["o_parts"], h, h, H, sp, st),
+                        "post_finish")))
                 out.append(("gate_up", lambda g=g, L=L, sp=sp: chk(
                     lib.grpo_nf4_gate_up_silu_tiles_norm(
                         h, H, sp, self.ss_post.shape[1], L["post_norm"].data_ptr(), L["eps"],
@@ -369,6 +391,16 @@ class DecodeEngine:
                 ("o", lambda: chk(lib.grpo_nf4_linear_partials(
                     ao, Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
                     L["o_code"].data_ptr(), self.bs, L["o_la"], L["o_parts"], st), "o_proj"))]
+        if self.o_fin:
+            h = self.h.data_ptr()
+            return [
+                attention,
+                ("o", lambda: chk(lib.grpo_nf4_linear_attn_residual(
+                    wsa, self.attn_len.data_ptr(), Hq, Hkv, D, pool.block_size, self.max_blocks,
+                    L["o_w"].data_ptr(), L["o_absmax"].data_ptr(), L["o_code"].data_ptr(),
+                    self.bs, L["o_la"], L["o_parts"], self.o_tpart.data_ptr(),
+                    self.o_cnt.data_ptr(), h, h, self.H, self.ss_post.data_ptr(), st),
+                    "o_proj"))]
         return [
             attention,
             ("o", lambda: chk(lib.grpo_nf4_linear_partials_attn(
@@ -626,6 +658,8 @@ class PrefillEngine(DecodeEngine):
     cache.  The pass is captured once into a HIP graph; rows past the end of a
     short last chunk are masked (slot -1, length 0).
     """
+    # o_proj stages the bf16 attention output here (no in-kernel finish)
+    O_FIN = False
 
     def __init__(self, model: Qwen2ForCausalLM, pool: PagedKVPool, chunk: int, max_blocks: int,
                  max_pos: Optional[int] = None):

@@ -275,6 +275,33 @@ int grpo_nf4_linear_partials_attn(const void* attn_workspace, const int32_t* con
                                   int blocksize, const void* const* lora_a,
                                   const grpo_linear_parts_t* parts, grpo_stream_t stream);
 
+/* grpo_nf4_linear_partials_attn followed by grpo_linear_finish_residual in one
+ * launch: the o_proj of _step and the decoder layer's residual add after it
+ * (paged_kv.py:762-775, 791-798), h_out = bf16(residual + y) with y the
+ * finished o_proj output (bias, LoRA: the epilogue of grpo_nf4_linear_finish,
+ * same roundings), and sumsq[m, g] = sum of h_out[m, n]^2 over the 64 columns
+ * of group g (G = grpo_nf4_linear_attn_residual_groups(...) per row) for the
+ * post-attention RMSNorm that grpo_nf4_gate_up_silu_tiles_norm stages.  The
+ * K slice of each 64-column group that finishes last sums the group's partial
+ * sums (parts->part, written as by grpo_nf4_linear_partials_attn) and applies
+ * the epilogue.  group_tpart: float32 workspace of the LoRA partials per group
+ * (tpart_bytes); counters: int32 workspace of counter_bytes, ZERO before the
+ * first call (every call leaves it zero; calls sharing it must not overlap).
+ * residual may alias h_out; row stride ld (a multiple of 4, rows 8-byte
+ * aligned).  M <= 16, one LoRA segment; other shapes return GRPO_EUNSUPPORTED. */
+int grpo_nf4_linear_attn_residual(const void* attn_workspace, const int32_t* context_lens,
+                                  int Hq, int Hkv, int D, int block_size, int max_blocks,
+                                  const uint8_t* w, const float* absmax, const float* code16,
+                                  int blocksize, const void* const* lora_a,
+                                  const grpo_linear_parts_t* parts, float* group_tpart,
+                                  int* counters, const void* residual, void* h_out, int64_t ld,
+                                  float* sumsq, grpo_stream_t stream);
+
+/* Column groups G per row of grpo_nf4_linear_attn_residual for this shape (0 if
+ * unsupported) and the bytes of its two workspaces. */
+int grpo_nf4_linear_attn_residual_groups(int M, int N, int K, int r, int blocksize,
+                                         size_t* tpart_bytes, size_t* counter_bytes);
+
 /* grpo_nf4_linear_partials with x = bf16(bf16(silu(g)) * u), g and u the
  * finished gate and up halves of the gate|up projection given by its partial
  * sums (no bias or LoRA, at most 2 K slices; gate_up->N = 2 * parts->K),
@@ -318,7 +345,8 @@ size_t grpo_fold_tiles_elements(int K);
 
 /* grpo_nf4_gate_up_silu_tiles with x = RMSNorm(h): x[m, k] = bf16(bf16(h[m, k] *
  * inv[m]) * norm_weight[k]), inv[m] = 1 / sqrt(sum_g sumsq[m, g] / K + eps), the
- * sums as grpo_linear_finish_residual writes them (groups <= 16 per row): the
+ * sums as grpo_linear_finish_residual or grpo_nf4_linear_attn_residual write
+ * them (groups <= 32 per row): the
  * decoder layer's post-attention RMSNorm (fused_rmsnorm, fused_ops.py:34-77;
  * paged_kv.py:791-798) staged by the gate|up kernel.  M <= 8; shapes as
  * grpo_nf4_gate_up_silu_tiles_norm_supported. */

@@ -413,8 +413,9 @@ def test_lm_head_norm_matches_the_two_launch_path(dev):
 
 
 def test_decode_engine_folds_small_batches(dev):
-    """Decode batches of <= 8 rows run the folded down_proj and no input-norm
-    launches after layer 0; wider ones keep the split-K path."""
+    """Decode batches of <= 8 rows run the folded down_proj, no input-norm
+    launches after layer 0 and o_proj with its finish and the residual add in
+    one launch (no norm launch at all); wider ones keep the split-K path."""
     from grpo_mi355x.core.kv_pool import PagedKVPool
     from grpo_mi355x.rollout.decode import DecodeEngine
     from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
@@ -424,12 +425,13 @@ def test_decode_engine_folds_small_batches(dev):
     pool = PagedKVPool(3, 64, 2, 128, 16, device=dev)
     small = DecodeEngine(model, pool, 8, 4)
     wide = DecodeEngine(model, pool, 12, 4)
-    assert small.fold and not wide.fold
+    assert small.fold and small.o_fin and not wide.fold
     kinds = [k for k, _ in small.launches()]
-    # only the post-attention finish of each layer: the embedding carries layer
-    # 0's norm statistic, the lm_head kernel stages the final norm
-    assert kinds.count("rmsnorm") == 3
-    assert len(kinds) == 1 + 3 * 6 + 2  # embedding, 6 per layer, lm_head + advance
+    # no norm launch: the embedding carries layer 0's norm statistic, o_proj
+    # the post-attention one, down_proj the next input norm's, and the lm_head
+    # kernel stages the final norm
+    assert kinds.count("rmsnorm") == 0
+    assert len(kinds) == 1 + 3 * 5 + 2  # embedding, 5 per layer, lm_head + advance
     assert kinds.count("down") == 3
     kinds_w = [k for k, _ in wide.launches()]
     assert kinds_w.count("rmsnorm") == 2 * 3 + 1
