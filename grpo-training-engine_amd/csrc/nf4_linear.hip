@@ -359,119 +359,147 @@ __device__ __forceinline__ float sum16(float v) {
 
 // Last-arriver finish of tile group g (FIN): columns n0 .. n0 + 16 * WPG - 1 of
 // every row, n0 = g * 16 * WPG, from the partial sums and LoRA t partials that
-// the group's S workgroups (one per K slice) stored.  The reference epilogue
-// and residual add in the order and roundings of lin_finish4 and
-// finish_residual_sumsq_kernel (linear_parts.hpp, decode_ops.hip), and
-// fin_ss[m][g] = sum over the group's columns of h^2.  Thread t < M * 16 * WPG / 4
-// owns row t / (4 * WPG), columns n0 + 4 (t % (4 * WPG)) .. + 3; the inputs
-// that no K slice produces (residual, bias, LoRA B) were loaded at kernel
-// start into res/bias/lb.
-template <int WPG>
+// the group's S workgroups (one per K slice) stored.  Wave w finishes the
+// group's n-tile w in the MFMA layout of the linear itself: lane (n = lane %
+// 16, lg = lane / 16) owns rows m = 4 lg + r (r < 4) of column n0 + 16 w + n.
+// The reference epilogue (lora_forward.py:243-257) in the order and roundings
+// of lin_finish4 (linear_parts.hpp), except that the LoRA product
+// u = t . B[n, :] is one 16x16x16 bf16 MFMA (bf16 t and B, float32
+// accumulation, as the reference's tl.dot), then h = bf16(residual + y) and
+// fin_ss[m][g] = sum over the group's columns of h^2.  The finish code is short
+// on purpose: the last arriver runs it once per launch with a cold instruction
+// cache, and one wave's serial VALU chain is its critical path.
 struct FinPre {
-  uint2 res, bias;
-  uint4 lb[8];
+  uint32_t res[2];  // residual of rows 4 lg .. 4 lg + 3 at this lane's column (bf16 pairs)
+  uint32_t lb[2];   // LoRA B[column][4 lg .. 4 lg + 3] (bf16, zero past r)
+  float bias;
 };
 
-template <int WPG>
-__device__ __forceinline__ void fin_prefetch(const PartArgs& p, int g, FinPre<WPG>& f) {
-  constexpr int TPR = 4 * WPG;  // threads per row
-  const int t = threadIdx.x;
-  const int m = min(t / TPR, p.M - 1);
-  const int n = g * 16 * WPG + 4 * (t % TPR);
-  f.res = *reinterpret_cast<const uint2*>(p.fin_res + (int64_t)m * p.fin_ld + n);
-  if (p.fin_bias) f.bias = *reinterpret_cast<const uint2*>(p.fin_bias + n);
-  if (p.r > 0 && p.fin_lb_vec) {
-    const uint4* br = reinterpret_cast<const uint4*>(p.fin_lb + (int64_t)n * 16);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) f.lb[j] = br[j];
-  }
+__device__ __forceinline__ int fin_col(int g, int wpg) {
+  return g * 16 * wpg + 16 * (threadIdx.x >> 6) + (threadIdx.x & 15);
 }
 
 template <int WPG>
-__device__ __forceinline__ void fin_group(const PartArgs& p, int g, const FinPre<WPG>& f) {
-  constexpr int TPR = 4 * WPG;
-  constexpr int COLS = 16 * WPG;
-  __shared__ float ts[16 * 16];  // LoRA t of each row (M <= 16)
-  const int t = threadIdx.x;
-  const int S = gridDim.y;
-  const int G = p.NT / WPG;
-  const int m = t / TPR;
-  const bool act = m < p.M;
-  const int n = g * COLS + 4 * (t % TPR);
-  // every load of the finish goes out before the barrier
-  float4 pv[FIN_MAX_SLICES];
-  {
-    const float4* pp =
-        reinterpret_cast<const float4*>(p.part + (int64_t)min(m, p.M - 1) * p.N + n);
-    const int64_t stride = (int64_t)p.Mp * p.N / 4;
+__device__ __forceinline__ void fin_prefetch(const PartArgs& p, int g, FinPre& f) {
+  const int lg = (threadIdx.x & 63) >> 4;
+  const int col = fin_col(g, WPG);
+  uint32_t rv[4];
 #pragma unroll
-    for (int s = 0; s < FIN_MAX_SLICES; ++s) pv[s] = pp[min(s, S - 1) * stride];
-  }
-  float tv[FIN_MAX_SLICES];
-  const bool tlane = t < p.M * 16 && p.r > 0;
+  for (int r = 0; r < 4; ++r) rv[r] = p.fin_res[(int64_t)min(4 * lg + r, p.M - 1) * p.fin_ld + col];
+  f.res[0] = rv[0] | (rv[1] << 16);
+  f.res[1] = rv[2] | (rv[3] << 16);
+  f.bias = p.fin_bias ? bf2f(p.fin_bias[col]) : 0.f;
+  f.lb[0] = f.lb[1] = 0;
   if (p.r > 0) {
-    const float* tp = p.fin_tpart + ((int64_t)g * S * p.M) * 16 + min(t, p.M * 16 - 1);
+    if (p.fin_lb_vec) {
+      const uint2 v = *reinterpret_cast<const uint2*>(p.fin_lb + (int64_t)col * 16 + 4 * lg);
+      f.lb[0] = v.x;
+      f.lb[1] = v.y;
+    } else {
+      uint32_t b[4];
 #pragma unroll
-    for (int s = 0; s < FIN_MAX_SLICES; ++s) tv[s] = tp[(int64_t)min(s, S - 1) * p.M * 16];
+      for (int j = 0; j < 4; ++j)
+        b[j] = 4 * lg + j < p.r ? p.fin_lb[(int64_t)col * p.r + 4 * lg + j] : 0u;
+      f.lb[0] = b[0] | (b[1] << 16);
+      f.lb[1] = b[2] | (b[3] << 16);
+    }
   }
-  if (tlane) {
-    float acc = 0.f;
+}
+
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+template <int WPG, int S>
+__device__ __forceinline__ void fin_group_s(const PartArgs& p, int g, const FinPre& f) {
+  __shared__ float red[WPG][16];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  const int G = p.NT / WPG;
+  const int col = fin_col(g, WPG);
+  // every load goes out at once: buffer loads with the slice offset in a
+  // scalar register (no per-load address arithmetic)
+  constexpr int BUF_FLAGS = 0x00020000;
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(p.part), 0, 0x7fffffff, BUF_FLAGS);
+  float pv[S][4];
 #pragma unroll
-    for (int s = 0; s < FIN_MAX_SLICES; ++s)
-      if (s < S) acc += tv[s];
-    ts[t] = round_bf(acc);
+  for (int r = 0; r < 4; ++r) {
+    const int vo = (min(4 * lg + r, p.M - 1) * p.N + col) * 4;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      pv[s][r] = __uint_as_float(
+          __builtin_amdgcn_raw_buffer_load_b32(rp, vo, s * p.Mp * p.N * 4, 0));
+  }
+  u32x4_t tv[S];
+  if (p.r > 0) {
+    const __amdgpu_buffer_rsrc_t rt =
+        __builtin_amdgcn_make_buffer_rsrc(p.fin_tpart, 0, 0x7fffffff, BUF_FLAGS);
+    const int vo = (min(ln, p.M - 1) * 16 + 4 * lg) * 4;
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+      tv[s] = __builtin_amdgcn_raw_buffer_load_b128(rt, vo, (g * S + s) * p.M * 64, 0);
+  }
+  // u[m][n] = t[m, :] . B[n, :]: t = bf16(sum over slices), rows m = lane % 16
+  f32x4_t u = {0.f, 0.f, 0.f, 0.f};
+  if (p.r > 0) {
+    float t[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < S; ++s)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t[i] += __uint_as_float(tv[s][i]);
+    const uint32_t a0 = pack_bf2(t[0], t[1]), a1 = pack_bf2(t[2], t[3]);
+    const i16x4_t av = __builtin_bit_cast(i16x4_t, make_uint2(a0, a1));
+    const i16x4_t bv = __builtin_bit_cast(i16x4_t, make_uint2(f.lb[0], f.lb[1]));
+    u = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(av, bv, u, 0, 0, 0);
+  }
+  const float sc = round_bf(p.fin_scaling);
+  const float res[4] = {bf_lo(f.res[0]), bf_hi(f.res[0]), bf_lo(f.res[1]), bf_hi(f.res[1])};
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) acc[r] += pv[s][r];
+  float sq[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    float v = round_bf(acc[r]);
+    if (p.fin_bias) v = round_bf(v + f.bias);
+    if (p.r > 0) v = round_bf(v + round_bf(round_bf(u[r]) * sc));
+    const float h = round_bf(v + res[r]);
+    const int m = 4 * lg + r;
+    if (m < p.M) p.fin_h[(int64_t)m * p.fin_ld + col] = f2bf(h);
+    sq[r] = m < p.M ? h * h : 0.f;
+  }
+  // sums of h^2 of each row: over this wave's 16 columns (one DPP row of
+  // lanes), then over the group's WPG waves in wave order
+#pragma unroll
+  for (int r = 0; r < 4; ++r) sq[r] = sum16(sq[r]);
+  if (ln == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) red[w][4 * lg + r] = sq[r];
   }
   __syncthreads();
-  if (!act) return;
-  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (threadIdx.x < p.M) {
+    float tot = 0.f;
 #pragma unroll
-  for (int s = 0; s < FIN_MAX_SLICES; ++s)
-    if (s < S) {
-      acc.x += pv[s].x;
-      acc.y += pv[s].y;
-      acc.z += pv[s].z;
-      acc.w += pv[s].w;
-    }
-  float v[4] = {round_bf(acc.x), round_bf(acc.y), round_bf(acc.z), round_bf(acc.w)};
-  if (p.fin_bias) {
-    const float b[4] = {bf_lo(f.bias.x), bf_hi(f.bias.x), bf_lo(f.bias.y), bf_hi(f.bias.y)};
-#pragma unroll
-    for (int c = 0; c < 4; ++c) v[c] = round_bf(v[c] + b[c]);
+    for (int i = 0; i < WPG; ++i) tot += red[i][threadIdx.x];
+    p.fin_ss[(int64_t)threadIdx.x * G + g] = tot;
   }
-  if (p.r > 0) {
-    const float* tr = ts + m * 16;
-    const float sc = round_bf(p.fin_scaling);
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      float u = 0.f;
-      if (p.fin_lb_vec) {
-        const uint4 b0 = f.lb[2 * c], b1 = f.lb[2 * c + 1];
-        const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          u += tr[2 * j] * bf_lo(bw[j]);
-          u += tr[2 * j + 1] * bf_hi(bw[j]);
-        }
-      } else {
-        const uint16_t* br = p.fin_lb + (int64_t)(n + c) * p.r;
-        for (int j = 0; j < p.r; ++j) u += tr[j] * bf2f(br[j]);
-      }
-      u = round_bf(round_bf(u) * sc);
-      v[c] = round_bf(v[c] + u);
-    }
+}
+
+// The slice count is a template argument, so the finish has no per-slice
+// selects (gridDim.y = S <= FIN_MAX_SLICES, checked by the host).
+template <int WPG>
+__device__ __forceinline__ void fin_group(const PartArgs& p, int g, const FinPre& f) {
+  switch (gridDim.y) {
+    case 1: fin_group_s<WPG, 1>(p, g, f); break;
+    case 2: fin_group_s<WPG, 2>(p, g, f); break;
+    case 3: fin_group_s<WPG, 3>(p, g, f); break;
+    case 4: fin_group_s<WPG, 4>(p, g, f); break;
+    case 5: fin_group_s<WPG, 5>(p, g, f); break;
+    case 6: fin_group_s<WPG, 6>(p, g, f); break;
+    case 7: fin_group_s<WPG, 7>(p, g, f); break;
+    default: fin_group_s<WPG, 8>(p, g, f); break;
   }
-  const float r[4] = {bf_lo(f.res.x), bf_hi(f.res.x), bf_lo(f.res.y), bf_hi(f.res.y)};
-  float ss = 0.f;
-#pragma unroll
-  for (int c = 0; c < 4; ++c) {
-    v[c] = round_bf(v[c] + r[c]);
-    ss += v[c] * v[c];
-  }
-  *reinterpret_cast<uint2*>(p.fin_h + (int64_t)m * p.fin_ld + n) =
-      make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
-  // the TPR = 16 threads of a row are one DPP row of 16 lanes
-  ss = sum16(ss);
-  if (t % TPR == 0) p.fin_ss[(int64_t)m * G + g] = ss;
 }
 
 template <int MT, int KPW, int XSRC, bool FIN = false>
@@ -584,7 +612,7 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   }
   // FIN: the finish's inputs that no K slice produces, behind the weights (the
   // MFMAs wait only for the loads before them), and the LoRA wave's A rows
-  FinPre<WPG> fpre;
+  FinPre fpre;
   if (FIN) fin_prefetch<WPG>(p, blockIdx.x, fpre);
   uint4 a8f[FIN ? 8 * KPW : 1];
   if (FIN && lwave && p.r > 0) {

@@ -1,14 +1,17 @@
 """o_proj with its epilogue and the residual add in one launch, through the C ABI.
 
 ``grpo_nf4_linear_attn_residual`` (the K slice of each 64-column group that
-arrives last finishes the group) must give h bit for bit as the two-launch path
-``grpo_nf4_linear_partials_attn`` + ``grpo_linear_finish_residual`` on the same
-attention split partials (same partial sums, same epilogue roundings), whose
-outputs other tests compare with the oracle.  Its per-64-column sums of squares
-are checked against float64 sums of its own h (sixty-four float32 terms:
-tolerance 1e-5).  Each case runs the fused launch three times in a row (the
-arrival counters must come back to zero, checked after the calls) and once more
-after the inputs changed.
+arrives last finishes the group) is compared on the same attention split
+partials with the oracle (``oracle.lora_linear.nf4_lora_linear`` of the merged
+attention rows, which ``grpo_paged_attn_merge`` writes, plus the bf16 residual
+add): bf16 tolerance 1e-2 and >= 97 % bit-identical outputs, as the other NF4
+linear tests.  Against the two-launch path ``grpo_nf4_linear_partials_attn`` +
+``grpo_linear_finish_residual`` (same partial sums and roundings; only the LoRA
+product t . B runs on an MFMA instead of sequential FMAs) >= 99 % of the
+outputs are bit-identical.  The per-64-column sums of squares are checked
+against float64 sums of the kernel's own h (tolerance 1e-5).  Each case runs
+the fused launch three times in a row (the arrival counters must come back to
+zero, checked after the calls) and once more after the inputs changed.
 """
 
 import ctypes
@@ -18,7 +21,10 @@ import pytest
 import torch
 
 from oracle.bf16 import bf16_bits_to_f32, f32_to_bf16_bits
+from oracle.lora_linear import nf4_lora_linear
 from oracle.nf4 import NF4_CODE, quantize_nf4
+
+from conftest import rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -53,7 +59,7 @@ def _attn_workspace(lib, g, dev, m, hq, hkv, bs, max_blocks, lens):
 
 @pytest.mark.parametrize("m,hq,hkv,r,bias", [(8, 12, 2, 16, False), (5, 28, 4, 16, True),
                                               (16, 12, 2, 0, False), (1, 12, 2, 8, True)])
-def test_attn_residual_is_the_two_launch_path(dev, m, hq, hkv, r, bias):
+def test_attn_residual_matches_oracle_and_the_two_launch_path(dev, m, hq, hkv, r, bias):
     from grpo_mi355x import _lib
     from grpo_mi355x.kernels import ops
 
@@ -97,8 +103,16 @@ def test_attn_residual_is_the_two_launch_path(dev, m, hq, hkv, r, bias):
     _lib.check(lib.grpo_nf4_linear_partials_attn(*args, st), "partials_attn")
     _lib.check(lib.grpo_linear_finish_residual(ctypes.byref(d), h2.data_ptr(), h2.data_ptr(), ld,
                                                ss2.data_ptr(), st), "finish_residual")
+    # the oracle on the merged bf16 attention rows
+    xm = torch.zeros(m, k, dtype=torch.bfloat16, device=dev)
+    _lib.check(lib.grpo_paged_attn_merge(ws.data_ptr(), len_d.data_ptr(), m, hq, hkv, 128, block,
+                                         max_blocks, xm.data_ptr(), 1, st), "merge")
     torch.cuda.synchronize()
     want = _bits(h2)
+    lin = nf4_lora_linear(_bits(xm), packed, absmax, n, k, bs,
+                          bias_bits=bias_bits if bias else None, a_bits=a if r else None,
+                          b_bits=b if r else None, scaling=2.0)
+    ref = f32_to_bf16_bits(bf16_bits_to_f32(lin) + bf16_bits_to_f32(res[:, :n]))
 
     tb, cb = ctypes.c_size_t(0), ctypes.c_size_t(0)
     groups = lib.grpo_nf4_linear_attn_residual_groups(m, n, k, r, bs, ctypes.byref(tb),
@@ -115,7 +129,15 @@ def test_attn_residual_is_the_two_launch_path(dev, m, hq, hkv, r, bias):
                                                      ss.data_ptr(), st), "attn_residual")
         torch.cuda.synchronize()
         got = _bits(h)
-        assert np.array_equal(got, want), f"call {call}: {np.mean(got != want):.4f} differ"
+        assert np.array_equal(got[:, n:], res[:, n:])  # columns past N untouched
+        gf = bf16_bits_to_f32(got[:, :n])
+        assert rel_err(gf, bf16_bits_to_f32(ref)) <= 1e-2
+        assert np.mean(got[:, :n] == ref) >= 0.97
+        assert rel_err(gf, bf16_bits_to_f32(want[:, :n])) <= 1e-2
+        assert np.mean(got == want) >= 0.99, f"call {call}: {np.mean(got != want):.4f} differ"
+        if call > 0:
+            assert np.array_equal(got, first)  # deterministic
+        first = got
         assert np.count_nonzero(cnt.cpu().numpy()) == 0
         hf = bf16_bits_to_f32(got[:, :n]).astype(np.float64)
         ref_ss = (hf ** 2).reshape(m, groups, 64).sum(-1)
@@ -134,7 +156,9 @@ def test_attn_residual_is_the_two_launch_path(dev, m, hq, hkv, r, bias):
                                                  h.data_ptr(), h.data_ptr(), ld, ss.data_ptr(),
                                                  st), "attn_residual")
     torch.cuda.synchronize()
-    assert np.array_equal(_bits(h), _bits(h2))
+    got, want = _bits(h), _bits(h2)
+    assert rel_err(bf16_bits_to_f32(got), bf16_bits_to_f32(want)) <= 1e-2
+    assert np.mean(got == want) >= 0.99
     assert np.count_nonzero(cnt.cpu().numpy()) == 0
 
 
