@@ -513,8 +513,8 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   const int lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
   // FIN: wave 0 also takes the LoRA-A tile of this K slice for its group
-  // after its weight tile (every group computes its own copy, so the group's
-  // finish reads nothing written on another XCD).
+  // (every group computes its own copy, so the group's finish reads nothing
+  // written on another XCD).
   const bool lwave = FIN && wave == 0;
   const int tile = blockIdx.x * WPG + wave;
   const int slice = blockIdx.y;
@@ -701,6 +701,21 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
               *reinterpret_cast<const uint4*>(xrow[mt] + i * KSTEP + 8 * j), bw, acc[mt]);
       }
     }
+    // FIN: wave 0's LoRA-A tile before any store (the wait for the A rows
+    // would otherwise also wait for the stores to be acknowledged)
+    f32x4_t lacc = {0.f, 0.f, 0.f, 0.f};
+    if (FIN && lwave && p.r > 0) {
+      const bool r_ok = ln < p.r;
+#pragma unroll
+      for (int i = 0; i < KPW; ++i) {
+        if (i >= nk) break;
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          lacc = mfma16x16x32(*reinterpret_cast<const uint4*>(xrow[0] + i * KSTEP + 8 * j),
+                              deinterleave8(r_ok ? a8f[8 * i + j] : make_uint4(0, 0, 0, 0)),
+                              lacc);
+      }
+    }
     float* out = p.part + (int64_t)slice * p.Mp * p.N + n_row;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
@@ -709,12 +724,18 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
         const int m = mt * 16 + 4 * lg + q;
         if (m < p.M) out[(int64_t)m * p.N] = acc[mt][q];
       }
-  }
-  if (FIN ? lwave && p.r > 0 : !wtile) {
-    // LoRA-A tile of segment seg: lane n = rank index, A is read as bf16.
+    if (FIN && lwave && p.r > 0) {
+      float* tout = p.fin_tpart + ((int64_t)blockIdx.x * gridDim.y + slice) * p.M * 16 + ln;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    const int seg = FIN ? 0 : tile - p.NT;
+      for (int q = 0; q < 4; ++q) {
+        const int m = 4 * lg + q;
+        if (m < p.M) tout[m * 16] = lacc[q];
+      }
+    }
+  }
+  if (!FIN && !wtile) {
+    // LoRA-A tile of segment seg: lane n = rank index, A is read as bf16.
+    const int seg = tile - p.NT;
     const bool r_ok = ln < p.r;
     const uint16_t* arow = sel_seg(p.la, seg) + (int64_t)(r_ok ? ln : 0) * p.K + kbase + 64 * lg;
 #pragma unroll
@@ -722,13 +743,9 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
       if (i >= nk) break;
       uint4 a8[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        if (FIN)
-          a8[j] = r_ok ? a8f[8 * i + j] : make_uint4(0, 0, 0, 0);
-        else
-          a8[j] = r_ok ? *reinterpret_cast<const uint4*>(arow + i * KSTEP + 8 * j)
-                       : make_uint4(0, 0, 0, 0);
-      }
+      for (int j = 0; j < 8; ++j)
+        a8[j] = r_ok ? *reinterpret_cast<const uint4*>(arow + i * KSTEP + 8 * j)
+                     : make_uint4(0, 0, 0, 0);
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const uint4 bv = deinterleave8(a8[j]);
@@ -738,8 +755,7 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
               *reinterpret_cast<const uint4*>(xrow[mt] + i * KSTEP + 8 * j), bv, acc[mt]);
       }
     }
-    float* out = FIN ? p.fin_tpart + ((int64_t)blockIdx.x * gridDim.y + slice) * p.M * 16 + ln
-                     : p.tpart + ((int64_t)slice * p.nseg + seg) * p.Mp * 16 + ln;
+    float* out = p.tpart + ((int64_t)slice * p.nseg + seg) * p.Mp * 16 + ln;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
