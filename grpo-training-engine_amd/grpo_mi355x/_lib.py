@@ -128,6 +128,11 @@ SIGNATURES = {
     "grpo_embedding_sumsq_groups": (_I32, []),
     "grpo_lm_head_argmax_norm": (
         _I32, [_VP, _I64, _VP, _I32, _VP, _F32, _VP, _I32, _I32, _I32, _VP, _I64, _VP, _SZ, _VP]),
+    "grpo_lm_head_argmax_norm_tiles": (
+        _I32, [_VP, _I64, _VP, _I32, _VP, _F32, _VP, _I32, _I32, _I32, _VP, _I64, _VP, _SZ, _VP]),
+    "grpo_lm_head_argmax_tiles": (
+        _I32, [_VP, _I64, _VP, _I32, _I32, _I32, _VP, _I64, _VP, _SZ, _VP]),
+    "grpo_lm_head_weight_tiles": (_I32, [_VP, _I32, _I32, _VP, _VP]),
     "grpo_nf4_linear_residual": (
         _I32, [_VP, _I64, _I32, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _I64, _VP, _I64,
                _VP, _VP]),

@@ -187,6 +187,12 @@ class DecodeEngine:
         # argmax + torch ops.
         lm_bytes = int(self.lib.grpo_lm_head_workspace_bytes(B, self.V))
         self.lm_fused = self.V % 16 == 0 and H % 256 == 0 and B <= 64
+        # lm_head weight in the kernel's tile order (contiguous 1 KiB per load
+        # instruction) when x fits LDS; the weight is frozen during rollouts
+        self.lm_w = self.lm_head
+        self.lm_tiled = self.LM_TILES and self.lm_fused and B * (H + 8) * 2 <= 160 * 1024
+        if self.lm_tiled:
+            self.lm_w = self._lm_tiles(self.model, self.lm_head, dev)
         self.ws_lm = torch.empty(max(lm_bytes, 16), dtype=torch.uint8, device=dev)
         # the sampler's workspace starts zero-filled and every call leaves it so
         self.ws_smp = None
@@ -268,6 +274,25 @@ class DecodeEngine:
     GU_NORM_MAX_GROUPS = 32  # ... and the gate|up norm staging
     # o_proj + its epilogue + residual add in one launch (<= 16 rows)
     O_FIN = True
+    # lm_head weight read in the kernel's tile order
+    LM_TILES = True
+
+    @staticmethod
+    def _lm_tiles(model, w: torch.Tensor, dev) -> torch.Tensor:
+        """The tile-order copy of the lm_head weight, built once per model and
+        weight version (kept on the model object; the weight is frozen while
+        rollouts run)."""
+        key = (w.data_ptr(), w._version, tuple(w.shape))
+        cache = getattr(model, "_grpo_lm_tiles", None)
+        if cache is not None and cache[0] == key:
+            return cache[1]
+        lib = _lib.device_library()
+        V, K = w.shape
+        wt = torch.empty_like(w)
+        _lib.check(lib.grpo_lm_head_weight_tiles(w.data_ptr(), V, K, wt.data_ptr(),
+                                                  _lib.stream_handle(dev)), "lm_weight_tiles")
+        model._grpo_lm_tiles = (key, wt)
+        return wt
 
     def launches(self) -> list:
         """[(kind, launch())] of one forward pass, in order, bound to torch's
@@ -425,8 +450,9 @@ class DecodeEngine:
                 "final_norm"))]
         if self.sampling:
             if self.lm_fused:
-                out.append(("lm_head", lambda: chk(lib.grpo_lm_head_argmax(
-                    x, H, self.lm_head.data_ptr(), self.V, H, B, self.logits.data_ptr(), self.V,
+                fn = lib.grpo_lm_head_argmax_tiles if self.lm_tiled else lib.grpo_lm_head_argmax
+                out.append(("lm_head", lambda: chk(fn(
+                    x, H, self.lm_w.data_ptr(), self.V, H, B, self.logits.data_ptr(), self.V,
                     self.ws_lm.data_ptr(), self.ws_lm.numel(), st), "lm_head")))
             else:
                 out.append(("lm_head",
@@ -443,8 +469,9 @@ class DecodeEngine:
         elif self.lm_fused:
             gen = self.generated
             logits = self.logits.data_ptr() if self.keep_logits else None
-            out.append(("lm_head", lambda: chk(lib.grpo_lm_head_argmax(
-                x, H, self.lm_head.data_ptr(), self.V, H, B, logits, self.V,
+            fn = lib.grpo_lm_head_argmax_tiles if self.lm_tiled else lib.grpo_lm_head_argmax
+            out.append(("lm_head", lambda: chk(fn(
+                x, H, self.lm_w.data_ptr(), self.V, H, B, logits, self.V,
                 self.ws_lm.data_ptr(), self.ws_lm.numel(), st), "lm_head")))
             out.append(("advance", lambda: chk(lib.grpo_decode_advance(
                 self.ws_lm.data_ptr(), B, self.V, self.next.data_ptr(), self.tokens.data_ptr(),
@@ -467,8 +494,9 @@ class DecodeEngine:
         h, ss = self.h.data_ptr(), self.ss.data_ptr()
         gen = self.generated
         logits = self.logits.data_ptr() if (self.keep_logits or self.sampling) else None
-        out = [("lm_head", lambda: chk(lib.grpo_lm_head_argmax_norm(
-            h, H, ss, H // 8, self.final_norm.data_ptr(), self.final_eps, self.lm_head.data_ptr(),
+        fn = lib.grpo_lm_head_argmax_norm_tiles if self.lm_tiled else lib.grpo_lm_head_argmax_norm
+        out = [("lm_head", lambda: chk(fn(
+            h, H, ss, H // 8, self.final_norm.data_ptr(), self.final_eps, self.lm_w.data_ptr(),
             self.V, H, B, logits, self.V, self.ws_lm.data_ptr(), self.ws_lm.numel(), st),
             "lm_head"))]
         if self.sampling:

@@ -489,6 +489,27 @@ int grpo_lm_head_argmax_norm(const void* h, int64_t ldh, const float* sumsq, int
                              int M, void* logits, int64_t ld_logits, void* workspace,
                              size_t workspace_bytes, grpo_stream_t stream);
 
+/* The lm_head weight W bf16 [V, K] rearranged for the _tiles variants below
+ * (w_tiles: V * K bf16, 16-byte aligned; V % 16 == 0, K % 256 == 0): chunk
+ * ((t * K / 256 + s) * 8 + j) * 64 + l of 8 bf16 holds W[16 t + l % 16][256 s +
+ * 32 j + 8 (l / 16) .. + 7], the order in which one wave's loads consume a
+ * vocabulary tile, so every load instruction reads 1 KiB of contiguous
+ * memory.  Built once per weight (frozen during rollouts); no reference
+ * counterpart (the reference reads the weight through torch/Triton). */
+int grpo_lm_head_weight_tiles(const void* w, int V, int K, void* w_tiles, grpo_stream_t stream);
+
+/* grpo_lm_head_argmax / grpo_lm_head_argmax_norm with W given in the layout of
+ * grpo_lm_head_weight_tiles (same results, bit for bit).  x [M, K] must fit
+ * LDS (M * (K + 8) * 2 <= 160 KiB); GRPO_EUNSUPPORTED otherwise. */
+int grpo_lm_head_argmax_tiles(const void* x, int64_t ldx, const void* w_tiles, int V, int K,
+                              int M, void* logits, int64_t ld_logits, void* workspace,
+                              size_t workspace_bytes, grpo_stream_t stream);
+int grpo_lm_head_argmax_norm_tiles(const void* h, int64_t ldh, const float* sumsq, int groups,
+                                   const void* norm_weight, float eps, const void* w_tiles,
+                                   int V, int K, int M, void* logits, int64_t ld_logits,
+                                   void* workspace, size_t workspace_bytes,
+                                   grpo_stream_t stream);
+
 /* Greedy token of every row from grpo_lm_head_argmax's workspace (first index
  * of the maximum), written to next_tokens (may be NULL), and the decode loop's
  * per-row bookkeeping (paged_kv.py:903-980, with per-row stop lengths): for an

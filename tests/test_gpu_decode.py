@@ -237,6 +237,55 @@ def test_lm_head_argmax_and_advance(dev):
     assert not bool(active[1]) and not bool(active[4])  # limit reached / EOS
 
 
+@pytest.mark.parametrize("M,V,K", [(8, 4096, 1536), (32, 2048, 512), (1, 160, 256)])
+def test_lm_head_weight_tiles_give_the_same_bits(dev, M, V, K):
+    """grpo_lm_head_weight_tiles rearranges W so that each wave load reads 1 KiB
+    of contiguous memory; the _tiles entry points on it must reproduce the
+    row-major entry points bit for bit (logits and per-tile argmax pairs),
+    with and without the staged RMSNorm, and the rearrangement must be the
+    documented permutation of W's 16-byte chunks."""
+    from grpo_mi355x import _lib
+
+    lib = _lib.device_library()
+    st = _lib.stream_handle(dev)
+    g = torch.Generator().manual_seed(M + V + K)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(dev)
+    w = (torch.randn(V, K, generator=g) * 0.05).to(torch.bfloat16).to(dev)
+    wt = torch.empty_like(w)
+    _lib.check(lib.grpo_lm_head_weight_tiles(w.data_ptr(), V, K, wt.data_ptr(), st), "tiles")
+    torch.cuda.synchronize()
+    # the layout: chunk ((t * K/256 + s) * 8 + j) * 64 + l = W[16t + l%16][256s + 32j + 8(l//16) ..]
+    q = torch.arange(V * K // 8)
+    l, j, tk = q % 64, (q // 64) % 8, q // 512
+    t, s_ = tk // (K // 256), tk % (K // 256)
+    rows = 16 * t + l % 16
+    cols = 256 * s_ + 32 * j + 8 * (l // 16)
+    want = w.cpu().view(V, K // 8, 8)[rows, cols // 8]
+    assert torch.equal(wt.cpu().view(-1, 8), want)
+    nws = int(lib.grpo_lm_head_workspace_bytes(M, V))
+    outs = []
+    for fn, wp in ((lib.grpo_lm_head_argmax, w), (lib.grpo_lm_head_argmax_tiles, wt)):
+        logits = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+        ws = torch.empty(nws, dtype=torch.uint8, device=dev)
+        _lib.check(fn(x.data_ptr(), K, wp.data_ptr(), V, K, M, logits.data_ptr(), V,
+                      ws.data_ptr(), nws, st), "lm_head")
+        outs.append((logits, ws))
+    if M <= 8:
+        ss = (x.float() ** 2).reshape(M, K // 8, 8).sum(-1).contiguous()
+        nw = (torch.randn(K, generator=g) * 0.1 + 1).to(torch.bfloat16).to(dev)
+        for fn, wp in ((lib.grpo_lm_head_argmax_norm, w), (lib.grpo_lm_head_argmax_norm_tiles, wt)):
+            logits = torch.empty(M, V, dtype=torch.bfloat16, device=dev)
+            ws = torch.empty(nws, dtype=torch.uint8, device=dev)
+            _lib.check(fn(x.data_ptr(), K, ss.data_ptr(), K // 8, nw.data_ptr(), 1e-6,
+                          wp.data_ptr(), V, K, M, logits.data_ptr(), V, ws.data_ptr(), nws, st),
+                       "lm_head_norm")
+            outs.append((logits, ws))
+    torch.cuda.synchronize()
+    for a_, b_ in ((0, 1), (2, 3)) if M <= 8 else ((0, 1),):
+        assert torch.equal(outs[a_][0].view(torch.int16), outs[b_][0].view(torch.int16))
+        assert torch.equal(outs[a_][1], outs[b_][1])
+
+
 @pytest.mark.parametrize("M,K", [(64, 3584), (24, 8192), (64, 1024)])
 def test_lm_head_argmax_wide_x_in_k_chunks(dev, M, K):
     """x [M, K] beyond 160 KiB of LDS (Qwen2-7B at G = 64, and a 24-row case
