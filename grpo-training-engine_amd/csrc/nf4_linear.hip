@@ -1314,8 +1314,18 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
   const int nu = (U - g0 + G - 1) / G;  // >= 1: the grid has at most U workgroups
   const int nitems = nu * KS;
   const int xstride = p.K + 8;
-  float* red = reinterpret_cast<float*>(xs + p.M * xstride);  // [nitems][M][16]
+  // item tiles [nitems][Mp / 4][16][4] (Mp = M rounded up to 4): lane (n, lg)
+  // stores its rows 4 lg .. 4 lg + 3 of column n as one 16-byte write
+  const int mq = (p.M + 3) >> 2;
+  float* red = reinterpret_cast<float*>(xs + p.M * xstride);
   const int rsel = ln < 8 ? ln : p.I + ln - 8;  // row of unit u: 8u + rsel
+  // Element e = row * K + k of item (unit i, k-step k) splits into a uniform
+  // part (8 (g0 + i G) K + 256 k) and this lane's constant part
+  // (rsel K + 64 lg): the weight bytes are the uniform base plus a 32-bit lane
+  // offset (no per-item vector address arithmetic), and so is the absmax index
+  // when the blocksize divides 256 (then it divides both parts).
+  const uint32_t lane_e = (uint32_t)rsel * (uint32_t)p.K + 64u * lg;
+  const bool sep = p.bs_shift <= 8;
 
   // x first (exactly GUU_XU chunks per thread, clamped), then the weights of
   // this wave's first GUU_LA items; every item then issues the loads of the
@@ -1349,15 +1359,25 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
   __builtin_amdgcn_sched_barrier(0);
   uint4 wv[2 * IPW];
   float av[IPW];
+  // (unit slot, k-step) of this wave's item t = wave + W t, advanced without
+  // divisions (uniform); items past the last re-read the last one
+  const int qlast = nitems - 1;
+  const int il = qlast / KS, kl = qlast - il * KS;
+  int ci = wave / KS, ck = wave - ci * KS, cq = wave;  // item of the next load_item
   auto load_item = [&](int t) __attribute__((always_inline)) {
-    const int q = min(wave + W * t, nitems - 1);
-    const int i = q / KS, k = q - i * KS;
-    const int64_t row = (int64_t)8 * (g0 + i * G) + rsel;
-    const int kc = k * KSTEP + 64 * lg;
-    const uint4* wp = reinterpret_cast<const uint4*>(p.w + row * (p.K / 2) + kc / 2);
+    const int i = cq <= qlast ? ci : il, k = cq <= qlast ? ck : kl;
+    const uint32_t ue = (uint32_t)(8 * (g0 + i * G)) * (uint32_t)p.K + (uint32_t)(k * KSTEP);
+    const uint4* wp = reinterpret_cast<const uint4*>(p.w + (ue >> 1) + (lane_e >> 1));
     wv[2 * t] = load_w<true>(wp);
     wv[2 * t + 1] = load_w<true>(wp + 1);
-    av[t] = p.absmax[(row * p.K + kc) >> p.bs_shift];
+    av[t] = sep ? (p.absmax + (ue >> p.bs_shift))[lane_e >> p.bs_shift]
+                : p.absmax[(ue + lane_e) >> p.bs_shift];
+    cq += W;
+    ck += W;
+    while (ck >= KS) {
+      ck -= KS;
+      ++ci;
+    }
   };
 #pragma unroll
   for (int t = 0; t < GUU_LA && t < IPW; ++t) load_item(t);
@@ -1401,11 +1421,8 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
                          decode8(word(wv[2 * t + (j >> 2)], j & 3), lt), acc);
     // lane (n = ln, group lg) holds D[m = 4*lg + r][n]
     const int q = wave + W * t;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 4 * lg + r;
-      if (m < p.M) red[(q * p.M + m) * 16 + ln] = acc[r];
-    }
+    if (lg < mq)
+      *reinterpret_cast<f32x4_t*>(red + ((q * mq + lg) * 16 + ln) * 4) = acc;
   }
   __syncthreads();
   for (int i = tid; i < nu * p.M * 8; i += NTH) {
@@ -1413,9 +1430,9 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
     const int m = rem >> 3, n = rem & 7;
     float g = 0.f, u = 0.f;
     for (int k = 0; k < KS; ++k) {
-      const float* tile = red + ((un * KS + k) * p.M + m) * 16;
-      g += tile[n];
-      u += tile[n + 8];
+      const float* tile = red + ((un * KS + k) * mq + (m >> 2)) * 64 + (m & 3);
+      g += tile[4 * n];
+      u += tile[4 * (n + 8)];
     }
     const float gv = round_bf(g);
     const float o = round_bf(gv * (1.f / (1.f + expf(-gv)))) * round_bf(u);
@@ -1763,10 +1780,11 @@ size_t units_lds(int M, int I, int K) {
   const int U = I / 8, KS = K / KSTEP;
   const int G = std::min(U, g_gu_units_grid);
   const int nu = (U + G - 1) / G;
-  return (size_t)M * (K + 8) * 2 + (size_t)nu * KS * M * 16 * 4;
+  return (size_t)M * (K + 8) * 2 + (size_t)nu * KS * ((M + 3) / 4 * 4) * 16 * 4;
 }
 bool units_ok(int M, int I, int K) {
   if (I <= 0 || I % 8 || K <= 0 || K % KSTEP) return false;
+  if ((int64_t)2 * I * K >= ((int64_t)1 << 32)) return false;  // 32-bit element offsets
   const int U = I / 8, KS = K / KSTEP;
   const int G = std::min(U, g_gu_units_grid);
   const int nu = (U + G - 1) / G;
