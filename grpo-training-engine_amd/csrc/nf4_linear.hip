@@ -1701,6 +1701,8 @@ __global__ void __launch_bounds__(64 * FOLD_W) nf4_fold_residual(FoldArgs p) {
 #pragma unroll
       for (int j = 0; j < 8; ++j) xv[8 * i + j] = xp[j];
     }
+    // item i's loads stay ahead of item i + 1's, so its decode waits for them only
+    __builtin_amdgcn_sched_barrier(0);
   }
 
   f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -1708,14 +1710,16 @@ __global__ void __launch_bounds__(64 * FOLD_W) nf4_fold_residual(FoldArgs p) {
 #pragma unroll
   for (int i = 0; i < IPW; ++i) {
     if (i >= my_items) break;
-    if (tail && wave + FOLD_W * i == items - 1 && half) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) xv[8 * i + j] = make_uint4(0, 0, 0, 0);
-    }
+    // The tail item's missing half: in the tile layout its x slots (columns
+    // >= K) are zero, in the natural layout it re-read the first half, whose
+    // x is dropped here by a select (overwriting the loaded registers would
+    // make the compiler wait for every load in flight).
+    const bool drop = !TILES && tail && wave + FOLD_W * i == items - 1 && half;
     const Lut lt = make_lut(code, av[i]);
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const uint4 a = TILES ? xv[8 * i + j] : deinterleave8(xv[8 * i + j]);
+      uint4 a = TILES ? xv[8 * i + j] : deinterleave8(xv[8 * i + j]);
+      if (!TILES) a = drop ? make_uint4(0, 0, 0, 0) : a;
       acc = mfma16x16x32(a, decode8(word(wv[2 * i + (j >> 2)], j & 3), lt), acc);
     }
   }
