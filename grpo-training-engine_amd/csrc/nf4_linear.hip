@@ -31,6 +31,7 @@
 //    order) and the reference epilogue run in the consuming kernel
 //    (linear_parts.hpp): nf4_finish here, or a fused decode-step op.
 #include <algorithm>
+#include <type_traits>
 
 #include "linear_parts.hpp"
 
@@ -56,6 +57,9 @@ constexpr int PART_LDS_MAX = 65536; // bytes of the staged x slice per workgroup
 // and long-K linears need no row chunks (each of which re-read the weights).
 constexpr int PART_LDS_BIG = 163840;
 constexpr int KPW_MAX = 8;          // k-steps per wave (all loads in flight at once)
+// x slices of 5 k-steps (only planned for more than 16 rows) are staged
+// chunk-major in LDS (nf4_part_mfma's xs_offset).
+__host__ __device__ constexpr bool xs_chunk_major(int MT, int kpw) { return MT > 1 && kpw == 5; }
 #ifndef GRPO_TARGET_WAVES
 #define GRPO_TARGET_WAVES 2048
 #endif
@@ -506,7 +510,7 @@ template <int MT, int KPW, int XSRC, bool FIN = false>
 __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(PartArgs p) {
   touch_kernargs<sizeof(PartArgs)>();
   constexpr int WPG = waves_per_group(XSRC), NT = 64 * WPG;
-  extern __shared__ __align__(16) uint16_t xs[];  // [M][xstride], decode8 order
+  extern __shared__ __align__(16) uint16_t xs[];  // x slice in decode8 order (xs_offset)
   // Padding workgroups of the XCD-aligned grid have no tile at all.
   if ((int)blockIdx.x * WPG >= p.ntiles) return;
   const int tid = threadIdx.x;
@@ -539,8 +543,34 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
 #pragma unroll
   for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
 
+  // x chunk i (16 bytes: 8 K values of one row) -> (row m, chunk c of the
+  // slice): row-major, or (CM) in groups of 64 chunks of 8 rows x 8
+  // consecutive chunks, 8 consecutive threads on one row, so every 8 threads
+  // load one 128-byte line (a row-fastest order, which writes LDS without
+  // bank conflicts, measured 1.4 us slower on Qwen2-7B's down_proj: its loads
+  // touch 4x the lines per quad); rows past M repeat row M - 1.
+  constexpr bool CM = xs_chunk_major(MT, KPW);
+  constexpr int XROWS = MT * 16;  // CM: LDS rows of each chunk
   const int chunks = nk * (KSTEP / 8);
-  const int total = p.M * chunks;
+  const int total = CM ? ((p.M + 7) & ~7) * chunks : p.M * chunks;
+  auto chunk_mc = [&](int i, int& m, int& c) __attribute__((always_inline)) {
+    if (CM) {
+      const int blk = i >> 6, l = i & 63, nbc = chunks >> 3;
+      const int mb = blk / nbc;
+      m = min(8 * mb + (l >> 3), p.M - 1);
+      c = 8 * (blk - mb * nbc) + (l & 7);
+    } else {
+      m = i / chunks;
+      c = i - m * chunks;
+    }
+  };
+  // LDS element offset of chunk c of row m: row-major [M][xstride] (8 padding
+  // columns stagger the rows over the banks), or (CM) chunk-major
+  // [chunk][XROWS][8], where the 16 rows of one MFMA A operand are 256
+  // contiguous bytes (no bank conflict without padding)
+  auto xs_offset = [&](int m, int c) __attribute__((always_inline)) {
+    return CM ? (c * XROWS + m) * 8 : m * p.xstride + 8 * c;
+  };
   uint4 xv[4];
   constexpr int SF = 2;  // SiLU chunks per thread fetched ahead
   SiluFetch sf[SF];
@@ -562,7 +592,8 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
     for (int u = 0; u < 4; ++u) {
       if (u * NT >= total) break;
       const int i = min(u * NT + tid, total - 1);
-      const int m = i / chunks, c = i - m * chunks;
+      int m, c;
+      chunk_mc(i, m, c);
       xv[u] = *reinterpret_cast<const uint4*>(p.nh + (int64_t)m * p.ldnh + kbase + 8 * c);
       nwv[u] = *reinterpret_cast<const uint4*>(p.nw + kbase + 8 * c);
     }
@@ -574,7 +605,8 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
     for (int u = 0; u < 4; ++u) {
       if (u * NT >= total) break;
       const int i = min(u * NT + tid, total - 1);
-      const int m = i / chunks, c = i - m * chunks;
+      int m, c;
+      chunk_mc(i, m, c);
       xv[u] = *reinterpret_cast<const uint4*>(p.x + (int64_t)m * p.ldx + kbase + 8 * c);
     }
   } else if (XSRC == X_SILU) {
@@ -582,12 +614,14 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
     for (int u = 0; u < SF; ++u) {
       const int i = u * NT + tid;
       if (i < total) {
-        const int m = i / chunks, c = i - m * chunks;
+        int m, c;
+        chunk_mc(i, m, c);
         silu_fetch(p, m, kbase + 8 * c, sf[u]);
       }
     }
   } else if (tid < total) {
-    const int m = tid / chunks, c = tid - m * chunks;
+    int m, c;
+    chunk_mc(tid, m, c);
     attn_fetch(p, m, kbase + 8 * c, af);
   }
   // Keep the scheduler from hoisting the (cheaper to address) weight loads
@@ -650,7 +684,8 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
       if (base + u * NT >= total) break;
       const int i = CLAMP ? min(base + u * NT + tid, total - 1) : base + u * NT + tid;
       if (CLAMP || i < total) {
-        const int m = i / chunks, c = i - m * chunks;
+        int m, c;
+        chunk_mc(i, m, c);
         if (XSRC == X_ATTN)
           v[u] = base == 0 && u == 0 ? attn_finish(p, af) : attn_chunk(p, m, kbase + 8 * c);
         else if (XSRC == X_SILU)
@@ -672,8 +707,9 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
       if (base + u * NT >= total) break;
       const int i = CLAMP ? min(base + u * NT + tid, total - 1) : base + u * NT + tid;
       if (CLAMP || i < total) {
-        const int m = i / chunks, c = i - m * chunks;
-        *reinterpret_cast<uint4*>(xs + m * p.xstride + 8 * c) = deinterleave8(v[u]);
+        int m, c;
+        chunk_mc(i, m, c);
+        *reinterpret_cast<uint4*>(xs + xs_offset(m, c)) = deinterleave8(v[u]);
       }
     }
   }
@@ -683,9 +719,14 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
   f32x4_t acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  // lane (ln, lg) multiplies row 16 mt + ln over K values 64 lg + 8 j of each
+  // k-step: chunk 8 lg + j, then + 32 per k-step (xstep)
   const uint16_t* xrow[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) xrow[mt] = xs + min(mt * 16 + ln, p.M - 1) * p.xstride + 64 * lg;
+  for (int mt = 0; mt < MT; ++mt) xrow[mt] = xs + xs_offset(min(mt * 16 + ln, p.M - 1), 8 * lg);
+  auto xstep = [&](int i, int j) __attribute__((always_inline)) {
+    return CM ? (32 * i + j) * XROWS * 8 : i * KSTEP + 8 * j;
+  };
 
   if (wtile) {
 #pragma unroll
@@ -698,7 +739,7 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           acc[mt] = mfma16x16x32(
-              *reinterpret_cast<const uint4*>(xrow[mt] + i * KSTEP + 8 * j), bw, acc[mt]);
+              *reinterpret_cast<const uint4*>(xrow[mt] + xstep(i, j)), bw, acc[mt]);
       }
     }
     // FIN: wave 0's LoRA-A tile before any store (the wait for the A rows
@@ -711,7 +752,7 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
         if (i >= nk) break;
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          lacc = mfma16x16x32(*reinterpret_cast<const uint4*>(xrow[0] + i * KSTEP + 8 * j),
+          lacc = mfma16x16x32(*reinterpret_cast<const uint4*>(xrow[0] + xstep(i, j)),
                               deinterleave8(r_ok ? a8f[8 * i + j] : make_uint4(0, 0, 0, 0)),
                               lacc);
       }
@@ -752,7 +793,7 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt)
           acc[mt] = mfma16x16x32(
-              *reinterpret_cast<const uint4*>(xrow[mt] + i * KSTEP + 8 * j), bv, acc[mt]);
+              *reinterpret_cast<const uint4*>(xrow[mt] + xstep(i, j)), bv, acc[mt]);
       }
     }
     float* out = p.tpart + ((int64_t)slice * p.nseg + seg) * p.Mp * 16 + ln;
@@ -831,6 +872,17 @@ bool part_shape_ok(int M, int N, int K, int r, int nseg, int blocksize, const in
   return plan_part(M, N, K, r, nseg).ok;
 }
 
+// LDS bytes of an x slice of kpw k-steps for a launch of `rows` rows:
+// row-major with 8 padding columns, or chunk-major over the row tile count
+// (xs_chunk_major: 5 k-steps of more than 16 rows, which fit 160 KiB only
+// without padding; the row-major staging loads are better coalesced).
+size_t xs_bytes(int rows, int kpw) {
+  int mt = (rows + 15) / 16;
+  if (mt == 3) mt = 4;
+  return xs_chunk_major(mt, kpw) ? (size_t)mt * 16 * kpw * KSTEP * 2
+                                 : (size_t)rows * (kpw * KSTEP + 8) * 2;
+}
+
 PartPlan plan_part(int M, int N, int K, int r, int nseg) {
   PartPlan p{};
   p.MT = (M + 15) / 16;
@@ -843,45 +895,48 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg) {
   const int target = K >= 4096 ? g_target_waves / 2 : g_target_waves;
   const int s_target = (target + p.ntiles - 1) / p.ntiles;
   int kpw = (KS + s_target - 1) / s_target;
-  static const int choices[] = {1, 2, 3, 4, 6, 8};
+  // More than 16 rows may take 5 k-steps per slice, staged chunk-major
+  // (xs_chunk_major), which needs no padding columns, so 64 rows fit LDS
+  // exactly (Qwen2-7B's down_proj at 64 rows: 15 K slices x 16 tile groups =
+  // 240 workgroups, one per CU, where 4 k-steps gave 19 x 16 = 304 and a
+  // second round on 48 CUs).
+  static const int choices_n[] = {1, 2, 3, 4, 6, 8};
+  static const int choices_w[] = {1, 2, 3, 4, 5, 6, 8};
+  const bool wide = p.MT > 1;
+  const int* choices = wide ? choices_w : choices_n;
+  const int nch = wide ? 7 : 6;
   int pick = KPW_MAX;
-  for (int c : choices)
-    if (c >= kpw) {
-      pick = c;
+  for (int i = 0; i < nch; ++i)
+    if (choices[i] >= kpw) {
+      pick = choices[i];
       break;
     }
   const size_t lds_cap = M > 16 ? PART_LDS_BIG : PART_LDS_MAX;
-  while (pick > 1 && (size_t)M * (pick * KSTEP + 8) * 2 > lds_cap) {
+  while (pick > 1 && xs_bytes(M, pick) > lds_cap) {
     int lower = 1;
-    for (int c : choices)
-      if (c < pick) lower = c;
+    for (int i = 0; i < nch; ++i)
+      if (choices[i] < pick) lower = choices[i];
     pick = lower;
   }
   // consumers read at most MAX_SLICES partial sums per output
   while ((KS + pick - 1) / pick > MAX_SLICES && pick < KPW_MAX) {
-    for (int c : choices)
-      if (c > pick) {
-        pick = c;
+    for (int i = 0; i < nch; ++i)
+      if (choices[i] > pick) {
+        pick = choices[i];
         break;
       }
   }
   p.kpw = pick;
   p.S = (KS + pick - 1) / pick;
   p.xstride = pick * KSTEP + 8;
-  // Wide batches of long-K linears (M = 64 at K = 18944 needs 6 k-steps per
-  // slice for <= MAX_SLICES slices) stage more x than LDS holds: their rows are
-  // launched in chunks of 16-row multiples, each writing its rows of the same
-  // partial-sum layout.
+  // Wide batches of very long K (> 20 slices of 5 k-steps) stage more x than
+  // LDS holds: their rows are launched in chunks of 32 or 16 rows, each writing
+  // its rows of the same partial-sum layout.
   p.mchunk = M;
-  const size_t row_bytes = (size_t)p.xstride * 2;
-  if ((size_t)M * row_bytes > lds_cap)
-    p.mchunk = 16 * (int)(lds_cap / (16 * row_bytes));
-  p.ok = p.mchunk >= 1 && p.S <= MAX_SLICES;
-  if (p.mchunk < M) {
-    p.MT = p.mchunk / 16;
-    if (p.MT == 3) p.MT = 2, p.mchunk = 32;  // chunks run on the MT = 1, 2 or 4 kernel
-  }
-  p.lds = (size_t)std::min(M, std::max(p.mchunk, 1)) * row_bytes;
+  if (xs_bytes(M, pick) > lds_cap) p.mchunk = xs_bytes(32, pick) <= lds_cap ? 32 : 16;
+  p.ok = xs_bytes(std::min(M, p.mchunk), pick) <= lds_cap && p.S <= MAX_SLICES;
+  if (p.mchunk < M) p.MT = p.mchunk / 16;
+  p.lds = xs_bytes(std::min(M, p.mchunk), pick);
   p.part_bytes = (size_t)p.S * M * N * 4;
   p.tpart_bytes = r > 0 ? (size_t)p.S * nseg * M * 16 * 4 : 0;
   return p;
@@ -922,6 +977,9 @@ int launch_part(const PartArgs& a, const PartPlan& pl, hipStream_t st) {
     case 2: return launch_part_k<MT, 2, XSRC>(a, pl, grid, block, st);
     case 3: return launch_part_k<MT, 3, XSRC>(a, pl, grid, block, st);
     case 4: return launch_part_k<MT, 4, XSRC>(a, pl, grid, block, st);
+    case 5:
+      if constexpr (MT > 1) return launch_part_k<MT, 5, XSRC>(a, pl, grid, block, st);
+      return einval("5 k-steps per K slice take more than 16 rows");
     case 6: return launch_part_k<MT, 6, XSRC>(a, pl, grid, block, st);
     default: return launch_part_k<MT, 8, XSRC>(a, pl, grid, block, st);
   }
@@ -1144,6 +1202,7 @@ struct GuArgs {
   int64_t lda;
   int M, I, K;
   int act_tiles;  // write act in the fold tile layout (fold_tile_index; M <= 8)
+  int act_vec;    // act 16-byte aligned and lda % 8 == 0: 8 columns per 16-byte store
   // x = RMSNorm(h) from per-group sums of squares, when nh is set (units kernel, M <= 8)
   const uint16_t* nh;
   int64_t ldnh;
@@ -1463,6 +1522,7 @@ constexpr int GUW_GROUPS = GUW_W / GUW_S;  // unit groups
 constexpr int GUW_UPW = 3;                 // most units per wave
 constexpr int GUW_KC = GUW_S * KSTEP;      // K values of one staged chunk
 constexpr int GUW_XSTRIDE = GUW_KC + 8;    // LDS row stride of a chunk (elements)
+constexpr int GUW_EPS = 20;                // LDS row stride of the epilogue's sums (floats)
 
 template <int MT>
 __global__ void __launch_bounds__(64 * GUW_W) nf4_gate_up_wide(GuArgs p) {
@@ -1579,35 +1639,52 @@ __global__ void __launch_bounds__(64 * GUW_W) nf4_gate_up_wide(GuArgs p) {
     if (c + 1 < NC) step(c + 1, wb, ab, wa, aa);
   }
 
-  // k-step lane 1 hands its sums to lane 0 through LDS (both x buffers are free)
-  f32x4_t* red = reinterpret_cast<f32x4_t*>(xs);  // [GROUPS][UPW][MT][64]
-  if (ksl == 1) {
-#pragma unroll
-    for (int t = 0; t < GUW_UPW; ++t)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) red[((grp * GUW_UPW + t) * MT + mt) * 64 + lane] = acc[t][mt];
-  }
-  __syncthreads();
-  if (ksl != 0) return;
+  // Both k-step lanes leave their sums in LDS (the x buffers are free) as
+  // [slot][lane][m][GUW_EPS] floats, slot = grp + GROUPS t: columns 0..7 gate,
+  // 8..15 up, padded to 20 so that the 64 lanes' stores of one r hit 64
+  // distinct banks.  Then every thread finishes (slot, row) pairs: both lanes'
+  // gate and up sums, SiLU, 8 bf16 in one 16-byte store.
+  float* red = reinterpret_cast<float*>(xs);
 #pragma unroll
   for (int t = 0; t < GUW_UPW; ++t) {
     if (t >= myu) break;
-    const int col = 8 * (g0 + (grp + GUW_GROUPS * t) * G) + (ln & 7);
+    const int slot = grp + GUW_GROUPS * t;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const f32x4_t o1 = red[((grp * GUW_UPW + t) * MT + mt) * 64 + lane];
+    for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        // lane (n = ln, group lg) holds D[m = 4*lg + r][n]; n < 8 gate, n >= 8 up
-        const float v = acc[t][mt][r] + o1[r];
-        const float other = dpp_move<0x128>(v);  // row_ror:8: the lane 8 columns away
+        // lane (n = ln, group lg) holds D[m = 16 mt + 4 lg + r][n]
         const int m = mt * 16 + 4 * lg + r;
-        if (ln < 8 && m < p.M) {
-          const float gv = round_bf(v);
-          const float o = round_bf(gv * (1.f / (1.f + expf(-gv)))) * round_bf(other);
-          p.act[(int64_t)m * p.lda + col] = f2bf(o);
-        }
+        if (m < p.M) red[((slot * GUW_S + ksl) * p.M + m) * GUW_EPS + ln] = acc[t][mt][r];
       }
+  }
+  __syncthreads();
+  for (int i = tid; i < nu * p.M; i += NTH) {
+    const int slot = i / p.M, m = i - slot * p.M;
+    const float* r0 = red + ((slot * GUW_S) * p.M + m) * GUW_EPS;
+    const float* r1 = r0 + p.M * GUW_EPS;
+    float o[8];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const float4 g0 = *reinterpret_cast<const float4*>(r0 + 4 * q);
+      const float4 g1 = *reinterpret_cast<const float4*>(r1 + 4 * q);
+      const float4 u0 = *reinterpret_cast<const float4*>(r0 + 8 + 4 * q);
+      const float4 u1 = *reinterpret_cast<const float4*>(r1 + 8 + 4 * q);
+      const float gs[4] = {g0.x + g1.x, g0.y + g1.y, g0.z + g1.z, g0.w + g1.w};
+      const float us[4] = {u0.x + u1.x, u0.y + u1.y, u0.z + u1.z, u0.w + u1.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float gv = round_bf(gs[e]);
+        o[4 * q + e] = round_bf(gv * (1.f / (1.f + expf(-gv)))) * round_bf(us[e]);
+      }
+    }
+    uint16_t* dst = p.act + (int64_t)m * p.lda + 8 * (g0 + slot * G);
+    if (p.act_vec) {
+      *reinterpret_cast<uint4*>(dst) = make_uint4(pack_bf2(o[0], o[1]), pack_bf2(o[2], o[3]),
+                                                  pack_bf2(o[4], o[5]), pack_bf2(o[6], o[7]));
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dst[e] = f2bf(o[e]);
     }
   }
 }
@@ -1817,9 +1894,8 @@ bool gu_wide_ok(int M, int I, int K, int blocksize, size_t* lds) {
   const int U = I / 8;
   const int G = std::min(U, g_gu_units_grid);
   if ((U + G - 1) / G > GUW_GROUPS * GUW_UPW) return false;
-  const int MT = (M + 15) / 16;
   const size_t xbytes = (size_t)2 * M * GUW_XSTRIDE * 2;
-  const size_t rbytes = (size_t)GUW_GROUPS * GUW_UPW * MT * 64 * 16;
+  const size_t rbytes = (size_t)GUW_GROUPS * GUW_UPW * GUW_S * M * GUW_EPS * 4;
   *lds = std::max(xbytes, rbytes);
   return *lds <= (size_t)PART_LDS_BIG;
 }
@@ -2419,6 +2495,7 @@ int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absma
   a.I = I;
   a.K = K;
   a.act_tiles = act_tiles;
+  a.act_vec = aligned16(act) && lda % 8 == 0;
   if (nrm) {
     a.nh = nrm->h;
     a.ldnh = nrm->ldh;

@@ -96,8 +96,10 @@ FAST = [
     (32, 3584, 3584, 16, True),   # 7B q_proj at G = 32
     (64, 512, 3584, 16, True),    # 7B k/v_proj at G = 64
     (8, 3584, 18944, 0, False),   # 7B down_proj (deepest k-split)
-    (64, 3584, 18944, 0, False),  # 7B down_proj at G = 64: x over LDS, rows in 16-row launches
-    (48, 1536, 18944, 16, True),  # row chunks with LoRA partials (tpart row offsets)
+    (64, 3584, 18944, 0, False),  # 7B down_proj at G = 64: 5 k-steps per slice, x chunk-major
+    (57, 3584, 18944, 16, True),  # the same with ragged rows (57) and LoRA partials
+    (48, 1536, 18944, 16, True),  # 6 k-steps per slice with LoRA partials
+    (64, 256, 40960, 16, True),   # x over LDS: 32-row launches (tpart row offsets)
     (64, 256, 4096, 16, True),    # LoRA with two k-steps per wave
 ]
 

@@ -106,6 +106,17 @@ def test_add_rmsnorm_parts_matches_oracle(dev, n, lora, offset):
                                    (17, 256, 512), (32, 8960, 1536), (40, 8960, 1536),
                                    (64, 2048, 768), (48, 20480, 256), (64, 18944, 3584)])
 def test_gate_up_silu_matches_oracle(dev, m, i, k):
+    _check_gate_up_silu(dev, m, i, k, 8)
+
+
+@pytest.mark.parametrize("m,i,k", [(40, 8960, 1536), (5, 4112, 512)])
+def test_gate_up_silu_unaligned_act_rows(dev, m, i, k):
+    """act rows of I + 3 columns: the wide kernel's epilogue then stores
+    column by column instead of 8 columns per 16-byte store."""
+    _check_gate_up_silu(dev, m, i, k, 3)
+
+
+def _check_gate_up_silu(dev, m, i, k, pad):
     """grpo_nf4_gate_up_silu = oracle NF4 linear of the gate and up halves of a
     stacked weight, then oracle SiLU*mul (fused_ops.py:79-112).  The first four
     and the sixth shape run the 8-column-unit kernel (the sixth has 514 units
@@ -134,9 +145,9 @@ def test_gate_up_silu_matches_oracle(dev, m, i, k):
     # freed before the asynchronous launch may be reused by the next copy)
     x_d, pk_d, am_d = _dev_bf16(x, dev), t(packed), t(absmax)
     code_d = t(NF4_CODE.astype(np.float32))
-    act = torch.zeros(m, i + 8, dtype=torch.bfloat16, device=dev)  # lda > I
+    act = torch.zeros(m, i + pad, dtype=torch.bfloat16, device=dev)  # lda > I
     _lib.check(lib.grpo_nf4_gate_up_silu(x_d.data_ptr(), k, pk_d.data_ptr(), am_d.data_ptr(),
-                                         code_d.data_ptr(), bs, i, k, m, act.data_ptr(), i + 8,
+                                         code_d.data_ptr(), bs, i, k, m, act.data_ptr(), i + pad,
                                          _lib.stream_handle(dev)), "gu")
     torch.cuda.synchronize()
     half = packed.size // 2, absmax.size // 2
