@@ -238,9 +238,16 @@ __global__ void __launch_bounds__(AMAX_T) argmax_kernel(const uint16_t* __restri
 // add_rmsnorm_kernel with x = the finished linear output of row m (a thread
 // finishes four columns at a time; the first four columns of every thread are
 // fetched before the LoRA-t barrier, so most rows need one memory round trip).
-__global__ void __launch_bounds__(PARTS_T) add_rmsnorm_parts_kernel(
-    LinParts o, const uint16_t* residual, uint16_t* h_out, const uint16_t* __restrict__ w,
+// T threads per row, MS the most K slices it fetches (S <= MS): rows of up to
+// 4 * T columns are finished from the loads issued before the LoRA-t barrier.
+// LORA false: the host guarantees r == 0 (no registers for LoRA B rows).
+template <int T, int MS, bool LORA>
+__global__ void __launch_bounds__(T) add_rmsnorm_parts_kernel(
+    LinParts op, const uint16_t* residual, uint16_t* h_out, const uint16_t* __restrict__ w,
     uint16_t* __restrict__ y, float eps, bool vec) {
+  constexpr int PARTS_T = T;
+  LinParts o = op;
+  if (!LORA) o.r = 0;
   touch_kernargs<sizeof(LinParts) + 4 * sizeof(void*) + 8>();
   __shared__ float red[PARTS_T / 64];
   __shared__ float ts[MAXSEG * 16];
@@ -254,7 +261,7 @@ __global__ void __launch_bounds__(PARTS_T) add_rmsnorm_parts_kernel(
   // round trip at the end of the kernel).  Wider rows (> 4 * PARTS_T) put the
   // rest through LDS.
   const bool first = tid < H / 4;
-  Fetch4<> f;
+  Fetch4<MS> f;
   uint2 res0 = make_uint2(0, 0), w0 = make_uint2(0, 0);
   if (first) {
     lin_fetch4(o, m, 4 * tid, f);
@@ -266,7 +273,7 @@ __global__ void __launch_bounds__(PARTS_T) add_rmsnorm_parts_kernel(
       w0.y = pack2(w[4 * tid + 2], w[4 * tid + 3]);
     }
   }
-  lin_load_t(o, m, ts);
+  lin_load_t<MS>(o, m, ts);
   __syncthreads();
   float ss = 0.f;
   float h0[4] = {0.f, 0.f, 0.f, 0.f};
@@ -283,7 +290,8 @@ __global__ void __launch_bounds__(PARTS_T) add_rmsnorm_parts_kernel(
     lin_finish4(o, ts, f, v);
     add_res(v, res0, h0);
   }
-  for (int i4 = tid + PARTS_T; i4 < H / 4; i4 += PARTS_T) {  // rows wider than 4 * PARTS_T
+  // rows wider than 4 * PARTS_T (the 1024-thread forms take at most 4096 columns)
+  for (int i4 = tid + PARTS_T; T < 1024 && i4 < H / 4; i4 += PARTS_T) {
     float v[4], h[4];
     lin_values4(o, ts, m, 4 * i4, v);
     add_res(v, residual ? *reinterpret_cast<const uint2*>(residual + row + 4 * i4)
@@ -311,7 +319,7 @@ __global__ void __launch_bounds__(PARTS_T) add_rmsnorm_parts_kernel(
       }
     }
   }
-  for (int i = 4 * PARTS_T + tid; i < H; i += PARTS_T) {
+  for (int i = 4 * PARTS_T + tid; T < 1024 && i < H; i += PARTS_T) {
     const float h = hs[i];
     if (residual && h_out) h_out[row + i] = f2bf(h);
     y[row + i] = f2bf(round_bf(h * inv) * bf2f(w[i]));
@@ -530,9 +538,29 @@ extern "C" int grpo_add_rmsnorm_parts(const grpo_linear_parts_t* x, const void* 
     return einval("residual must be 8-byte aligned");
   auto a8 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 7u) == 0; };
   const bool vec = a8(weight) && a8(y) && (!h_out || a8(h_out));  // rows: N % 16 == 0
-  add_rmsnorm_parts_kernel<<<dim3(o.M), PARTS_T, o.N * sizeof(float), as_stream(stream)>>>(
-      o, static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(h_out),
-      static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(y), eps, vec);
+  const uint16_t* res = static_cast<const uint16_t*>(residual);
+  uint16_t* ho = static_cast<uint16_t*>(h_out);
+  const uint16_t* wt = static_cast<const uint16_t*>(weight);
+  uint16_t* yo = static_cast<uint16_t*>(y);
+  // Rows wider than 4 * PARTS_T (Qwen2-7B's 3584) take 1024 threads when the
+  // slices fit their registers (8 with LoRA, 16 without), so no column waits
+  // for a second round trip after the LoRA-t barrier (64 x 3584 from 7 slices
+  // with LoRA: 11.8 us with 512 threads).
+  const bool one_pass = o.N > 4 * PARTS_T && o.N <= 4 * 1024;
+  if (one_pass && o.S <= 8)
+    add_rmsnorm_parts_kernel<1024, 8, true><<<dim3(o.M), 1024, 0, as_stream(stream)>>>(
+        o, res, ho, wt, yo, eps, vec);
+  else if (one_pass && o.S <= 16 && o.r == 0)
+    add_rmsnorm_parts_kernel<1024, 16, false><<<dim3(o.M), 1024, 0, as_stream(stream)>>>(
+        o, res, ho, wt, yo, eps, vec);
+  else if (o.S <= 8)
+    add_rmsnorm_parts_kernel<PARTS_T, 8, true>
+        <<<dim3(o.M), PARTS_T, o.N * sizeof(float), as_stream(stream)>>>(o, res, ho, wt, yo, eps,
+                                                                         vec);
+  else
+    add_rmsnorm_parts_kernel<PARTS_T, MAX_SLICES, true>
+        <<<dim3(o.M), PARTS_T, o.N * sizeof(float), as_stream(stream)>>>(o, res, ho, wt, yo, eps,
+                                                                         vec);
   return launch_check("add_rmsnorm_parts");
 }
 

@@ -59,19 +59,21 @@ constexpr int MAX_SLICES = 20;  // K slices of a split-K linear (the plan keeps 
 // LoRA t of row m rounded to bf16, ts[seg*16 + j], computed by the whole
 // workgroup (the caller synchronises before reading ts).  The S slices of a
 // float4 are loaded together (predicated, no loop), so this is one round trip.
+// MS: the most slices (S <= MS).
+template <int MS = MAX_SLICES>
 __device__ __forceinline__ void lin_load_t(const LinParts& o, int m, float* ts) {
   if (o.r <= 0) return;
   for (int i = threadIdx.x; i < o.nseg * 4; i += blockDim.x) {
     const int seg = i >> 2, q = i & 3;
     const float4* p = reinterpret_cast<const float4*>(o.tpart + ((int64_t)seg * o.M + m) * 16) + q;
     const int64_t stride = (int64_t)o.nseg * o.M * 4;
-    float4 v[MAX_SLICES];
+    float4 v[MS];
 #pragma unroll
-    for (int k = 0; k < MAX_SLICES; ++k)
+    for (int k = 0; k < MS; ++k)
       if (k < o.S) v[k] = p[k * stride];
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-    for (int k = 0; k < MAX_SLICES; ++k)
+    for (int k = 0; k < MS; ++k)
       if (k < o.S) {
         acc.x += v[k].x;
         acc.y += v[k].y;

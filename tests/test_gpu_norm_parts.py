@@ -39,16 +39,21 @@ def _dev_bf16(bits, dev, offset=0):
     return t[offset:].view(bits.shape)
 
 
-@pytest.mark.parametrize("n,lora,offset", [(1536, False, 0), (1536, True, 1), (3584, True, 0),
-                                           (3584, False, 1)])
-def test_add_rmsnorm_parts_matches_oracle(dev, n, lora, offset):
+@pytest.mark.parametrize("m,n,k,lora,offset", [(8, 1536, 512, False, 0), (8, 1536, 512, True, 1),
+                                               (8, 3584, 512, True, 0), (8, 3584, 512, False, 1),
+                                               (64, 3584, 3584, True, 0),
+                                               (64, 3584, 18944, False, 0)])
+def test_add_rmsnorm_parts_matches_oracle(dev, m, n, k, lora, offset):
+    """The last two are config 5's post-attention norm (7 slices of o_proj
+    partials with LoRA) and input norm (15 slices of down_proj partials, no
+    LoRA): rows of 3584 columns finished by 1024 threads in one pass."""
     from grpo_mi355x import _lib
     from grpo_mi355x.kernels import ops
 
     lib = _lib.device_library()
     st = _lib.stream_handle(dev)
-    m, k, r, bs, eps = 8, 512, 16, 64, 1e-6
-    g = np.random.default_rng(n + 10 * lora + offset)
+    r, bs, eps = 16, 64, 1e-6
+    g = np.random.default_rng(n + 10 * lora + offset + m + k)
     x = f32_to_bf16_bits(g.standard_normal((m, k)).astype(np.float32))
     w = (g.standard_normal((n, k)) * 0.05).astype(np.float32)
     packed, absmax = quantize_nf4(w, bs)
