@@ -215,8 +215,9 @@ __global__ void __launch_bounds__(64 * LM_WAVES) lm_head_argmax_kernel(LmArgs p)
 // tile instead -- one workgroup per 8 tiles, 1 per CU for LDS -- read x from
 // L2 ~40 times per CU and left 8 waves per CU without loads in flight during
 // each staging: 320 us at M = 64.)  At M = 64, V = 152064, K = 3584 it streams
-// W at 4.2 TB/s (257 us, the argmax included); hipBLASLt's GEMM alone takes
-// 202 us, its logits then need an argmax launch (9.6 us).
+// W at 5.5 TB/s from the tile order (198 us, the argmax included; 257 us from
+// the row-major layout); hipBLASLt's GEMM alone takes 202 us, its logits then
+// need an argmax launch (9.6 us).
 constexpr int LM_WIDE_WAVES = 8;
 constexpr int LM_WIDE_TPW = 5;     // tiles per wave: V <= 5 * 2048 * 16 = 163840
 
@@ -240,10 +241,14 @@ __global__ void __launch_bounds__(64 * LM_WIDE_WAVES) lm_head_argmax_wide(LmArgs
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) xrow[mt] = xs + min(mt * 16 + ln, p.M - 1) * xstride + 8 * lg;
   // W of (tile slot t, k-step ks): rows of tile gw + t*nw, clamped into range
-  // for a wave without that tile (its loads are then re-reads, never used)
+  // for a wave without that tile (its loads are then re-reads, never used);
+  // MFMA j's operands are 32 j further (row-major) or 512 j (tile order:
+  // lm_weight_tiles_kernel, 1 KiB of contiguous memory per load instruction)
+  const int64_t wj = p.tiled ? 512 : 32;
   auto wptr = [&](int t, int ks) __attribute__((always_inline)) {
     const int tile = min(gw + min(t, max(ntiles - 1, 0)) * nw, p.NT - 1);
-    return p.w + (int64_t)(tile * 16 + ln) * p.K + 8 * lg + ks * LM_KSTEP;
+    return p.tiled ? p.w + (((int64_t)tile * KS + ks) * 512 + lane) * 8
+                   : p.w + (int64_t)(tile * 16 + ln) * p.K + 8 * lg + ks * LM_KSTEP;
   };
   for (int c0 = 0; c0 < KS; c0 += kpc) {
     const int nks = min(kpc, KS - c0);
@@ -266,7 +271,7 @@ __global__ void __launch_bounds__(64 * LM_WIDE_WAVES) lm_head_argmax_wide(LmArgs
       const int q = min(item, nitems - 1);
       const uint16_t* wp = wptr(q / nks, c0 + q % nks);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) w[j] = load_stream(wp + 32 * j);
+      for (int j = 0; j < 8; ++j) w[j] = load_stream(wp + wj * j);
     };
     load_item(wr[0], 0);
     for (int it = 0; it < nitems; it += 2) {
@@ -459,10 +464,6 @@ int run_lm_head(const void* x, int64_t ldx, const void* w, int V, int K, int M, 
   a.tiled = tiled ? 1 : 0;
   const dim3 grid((unsigned)cdiv(a.NT, LM_WAVES)), block(64 * LM_WAVES);
   if (lds > LM_LDS_MAX) {
-    if (tiled) {
-      set_error("lm_head: the tile layout is read by the staged-x kernel only (x fits LDS)");
-      return GRPO_EUNSUPPORTED;
-    }
     // x staged in K chunks (the widest multiple of 256 columns that fits), one
     // workgroup per CU, every tile of a wave accumulated in registers
     const int KC = (int)(((LM_LDS_MAX / (2 * (size_t)M)) - 8) / LM_KSTEP) * LM_KSTEP;

@@ -187,10 +187,10 @@ class DecodeEngine:
         # argmax + torch ops.
         lm_bytes = int(self.lib.grpo_lm_head_workspace_bytes(B, self.V))
         self.lm_fused = self.V % 16 == 0 and H % 256 == 0 and B <= 64
-        # lm_head weight in the kernel's tile order (contiguous 1 KiB per load
-        # instruction) when x fits LDS; the weight is frozen during rollouts
+        # lm_head weight in the kernels' tile order (contiguous 1 KiB per load
+        # instruction); the weight is frozen during rollouts
         self.lm_w = self.lm_head
-        self.lm_tiled = self.LM_TILES and self.lm_fused and B * (H + 8) * 2 <= 160 * 1024
+        self.lm_tiled = self.LM_TILES and self.lm_fused
         if self.lm_tiled:
             self.lm_w = self._lm_tiles(self.model, self.lm_head, dev)
         self.ws_lm = torch.empty(max(lm_bytes, 16), dtype=torch.uint8, device=dev)

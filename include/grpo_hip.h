@@ -499,8 +499,10 @@ int grpo_lm_head_argmax_norm(const void* h, int64_t ldh, const float* sumsq, int
 int grpo_lm_head_weight_tiles(const void* w, int V, int K, void* w_tiles, grpo_stream_t stream);
 
 /* grpo_lm_head_argmax / grpo_lm_head_argmax_norm with W given in the layout of
- * grpo_lm_head_weight_tiles (same results, bit for bit).  x [M, K] must fit
- * LDS (M * (K + 8) * 2 <= 160 KiB); GRPO_EUNSUPPORTED otherwise. */
+ * grpo_lm_head_weight_tiles (same results, bit for bit).  As for the row-major
+ * entries, the _norm form needs x [M, K] to fit LDS (M * (K + 8) * 2 <= 160
+ * KiB; GRPO_EUNSUPPORTED otherwise); the plain form stages wider x in K
+ * chunks. */
 int grpo_lm_head_argmax_tiles(const void* x, int64_t ldx, const void* w_tiles, int V, int K,
                               int M, void* logits, int64_t ld_logits, void* workspace,
                               size_t workspace_bytes, grpo_stream_t stream);

@@ -237,13 +237,15 @@ def test_lm_head_argmax_and_advance(dev):
     assert not bool(active[1]) and not bool(active[4])  # limit reached / EOS
 
 
-@pytest.mark.parametrize("M,V,K", [(8, 4096, 1536), (32, 2048, 512), (1, 160, 256)])
+@pytest.mark.parametrize("M,V,K", [(8, 4096, 1536), (32, 2048, 512), (1, 160, 256),
+                                   (64, 4096, 3584), (40, 2064, 3584)])
 def test_lm_head_weight_tiles_give_the_same_bits(dev, M, V, K):
     """grpo_lm_head_weight_tiles rearranges W so that each wave load reads 1 KiB
     of contiguous memory; the _tiles entry points on it must reproduce the
     row-major entry points bit for bit (logits and per-tile argmax pairs),
     with and without the staged RMSNorm, and the rearrangement must be the
-    documented permutation of W's 16-byte chunks."""
+    documented permutation of W's 16-byte chunks.  The last two shapes stage x
+    in K chunks (lm_head_argmax_wide: x beyond 160 KiB of LDS)."""
     from grpo_mi355x import _lib
 
     lib = _lib.device_library()
