@@ -890,9 +890,13 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg) {
   const int KS = K / KSTEP;
   p.NT = N / 16;
   p.ntiles = p.NT + (r > 0 ? nseg : 0);
-  // Long K (down_proj, K = 8960): fewer, longer K slices measured faster
-  // (fewer partial sums to write and for the consumer to read back).
-  const int target = K >= 4096 ? g_target_waves / 2 : g_target_waves;
+  // Long K (down_proj, K = 8960) at decode batches: fewer, longer K slices
+  // measured faster (fewer partial sums to write and for the consumer to read
+  // back).  Wider batches keep the full target: their x slices take 16-wave
+  // workgroups, so the halved target left most CUs idle (config 4's down_proj
+  // at 32 rows: 9 slices x 8 groups = 72 workgroups; 18 slices of 2 k-steps on
+  // 8-wave workgroups give 288: 5861 -> 6517 tok/s).
+  const int target = K >= 4096 && M <= 16 ? g_target_waves / 2 : g_target_waves;
   const int s_target = (target + p.ntiles - 1) / p.ntiles;
   int kpw = (KS + s_target - 1) / s_target;
   // More than 16 rows may take 5 k-steps per slice, staged chunk-major
