@@ -1364,8 +1364,11 @@ constexpr int GUU_XU = 6;  // x chunks per thread loaded before the weights
 #endif
 constexpr int GUU_LA = GRPO_GUU_LA;  // items whose weights are in flight ahead of the one decoded
 
-template <int W, int IPW, bool NORM>
+// MT row tiles of 16 (MT = 2: 17..32 rows, whose x of K <= 1536 still fits
+// LDS whole with the item tiles: config 4's G = 32).
+template <int W, int IPW, bool NORM, int MT = 1>
 __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
+  static_assert(!NORM || MT == 1, "the RMSNorm source takes at most 8 rows");
   constexpr int NTH = 64 * W;
   extern __shared__ __align__(16) uint16_t xs[];  // [M][K + 8] (decode8 order), then tiles
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1469,7 +1472,9 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
   }
   __syncthreads();
 
-  const uint16_t* xrow = xs + min(ln, p.M - 1) * xstride + 64 * lg;
+  const uint16_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) xrow[mt] = xs + min(16 * mt + ln, p.M - 1) * xstride + 64 * lg;
   const int my_items = (nitems - wave + W - 1) / W;  // items of this wave (may be 0)
 #pragma unroll
   for (int t = 0; t < IPW; ++t) {
@@ -1477,15 +1482,23 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
     if (t + GUU_LA < IPW) load_item(t + GUU_LA);
     const int k = (wave + W * t) % KS;
     const Lut lt = make_lut(code, av[t]);
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    f32x4_t acc[MT];
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      acc = mfma16x16x32(*reinterpret_cast<const uint4*>(xrow + k * KSTEP + 8 * j),
-                         decode8(word(wv[2 * t + (j >> 2)], j & 3), lt), acc);
-    // lane (n = ln, group lg) holds D[m = 4*lg + r][n]
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const uint4 bw = decode8(word(wv[2 * t + (j >> 2)], j & 3), lt);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        acc[mt] = mfma16x16x32(*reinterpret_cast<const uint4*>(xrow[mt] + k * KSTEP + 8 * j), bw,
+                               acc[mt]);
+    }
+    // lane (n = ln, group lg) holds D[m = 16 mt + 4 lg + r][n]
     const int q = wave + W * t;
-    if (lg < mq)
-      *reinterpret_cast<f32x4_t*>(red + ((q * mq + lg) * 16 + ln) * 4) = acc;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+      if (4 * mt + lg < mq)
+        *reinterpret_cast<f32x4_t*>(red + ((q * mq + 4 * mt + lg) * 16 + ln) * 4) = acc[mt];
   }
   __syncthreads();
   for (int i = tid; i < nu * p.M * 8; i += NTH) {
@@ -1868,12 +1881,14 @@ size_t units_lds(int M, int I, int K) {
   return (size_t)M * (K + 8) * 2 + (size_t)nu * KS * ((M + 3) / 4 * 4) * 16 * 4;
 }
 bool units_ok(int M, int I, int K) {
-  if (I <= 0 || I % 8 || K <= 0 || K % KSTEP) return false;
+  if (M < 1 || M > 32 || I <= 0 || I % 8 || K <= 0 || K % KSTEP) return false;
   if ((int64_t)2 * I * K >= ((int64_t)1 << 32)) return false;  // 32-bit element offsets
   const int U = I / 8, KS = K / KSTEP;
   const int G = std::min(U, g_gu_units_grid);
   const int nu = (U + G - 1) / G;
-  return (nu * KS + GU_UNITS_W - 1) / GU_UNITS_W <= GU_UNITS_IPW && units_lds(M, I, K) <= 65536;
+  // up to 16 rows in 64 KiB of LDS; 17..32 rows (two row tiles) in up to 160 KiB
+  const size_t cap = M <= 16 ? 65536 : (size_t)PART_LDS_BIG;
+  return (nu * KS + GU_UNITS_W - 1) / GU_UNITS_W <= GU_UNITS_IPW && units_lds(M, I, K) <= cap;
 }
 
 // Shape support of nf4_gate_up_silu; returns false for shapes it does not take.
@@ -2477,8 +2492,14 @@ int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absma
                 int act_tiles, hipStream_t st, const NormSource* nrm) {
   GuPlan pl;
   size_t wlds = 0;
-  const bool wide = !nrm && !act_tiles && gu_wide_ok(M, I, K, blocksize, &wlds);
-  if (!wide && !plan_gu(M, I, K, blocksize, &pl)) {
+  // 17..32 rows whose x and item tiles fit LDS run the units kernel on two row
+  // tiles (x staged once, no chunk barriers; config 4's 32 x 8960 x 1536: 14.3
+  // -> 13.2 us per traced launch, 6522 -> 6842 tok/s), the other wide shapes
+  // the chunked wide kernel
+  const bool units2 = !nrm && !act_tiles && M > 16 && pow2(blocksize) && blocksize >= 64 &&
+                      units_ok(M, I, K);
+  const bool wide = !units2 && !nrm && !act_tiles && gu_wide_ok(M, I, K, blocksize, &wlds);
+  if (!wide && !units2 && !plan_gu(M, I, K, blocksize, &pl)) {
     set_error("shape not supported by the fused gate|up SiLU kernel");
     return GRPO_EUNSUPPORTED;
   }
@@ -2528,6 +2549,12 @@ int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absma
     const int U = I / 8, KS = K / KSTEP;
     const int G = std::min(U, g_gu_units_grid);
     const size_t lds = units_lds(M, I, K);
+    if (units2) {
+      if (int rc = allow_big_lds(nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, false, 2>)) return rc;
+      nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, false, 2>
+          <<<dim3((unsigned)G), 64 * GU_UNITS_W, lds, st>>>(a);
+      return launch_check("nf4_gate_up_units");
+    }
     if (units_ok(M, I, K)) {
       if (nrm)
         nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, true>

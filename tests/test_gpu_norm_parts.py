@@ -109,12 +109,13 @@ def test_add_rmsnorm_parts_matches_oracle(dev, m, n, k, lora, offset):
 @pytest.mark.parametrize("m,i,k", [(8, 8960, 1536), (3, 256, 512), (16, 512, 1536),
                                    (8, 512, 3584), (8, 17920, 3584), (5, 4112, 512),
                                    (17, 256, 512), (32, 8960, 1536), (40, 8960, 1536),
-                                   (64, 2048, 768), (48, 20480, 256), (64, 18944, 3584)])
+                                   (64, 2048, 768), (48, 20480, 256), (32, 18944, 3584),
+                                   (64, 18944, 3584)])
 def test_gate_up_silu_matches_oracle(dev, m, i, k):
     _check_gate_up_silu(dev, m, i, k, 8)
 
 
-@pytest.mark.parametrize("m,i,k", [(40, 8960, 1536), (5, 4112, 512)])
+@pytest.mark.parametrize("m,i,k", [(40, 8960, 1536), (5, 4112, 512), (24, 8960, 1536)])
 def test_gate_up_silu_unaligned_act_rows(dev, m, i, k):
     """act rows of I + 3 columns: the wide kernel's epilogue then stores
     column by column instead of 8 columns per 16-byte store."""
@@ -127,12 +128,14 @@ def _check_gate_up_silu(dev, m, i, k, pad):
     and the sixth shape run the 8-column-unit kernel (the sixth has 514 units
     over 256 workgroups: two workgroups take a third unit); [8, 17920, 3584]
     has more items per wave than the unit kernel keeps in registers and runs
-    one workgroup per 16 columns.  17..64 rows run the wide kernel (x staged in
-    512-column chunks, unit accumulators in registers across K): one unit per
-    workgroup, so three of the four unit groups are empty (17 x 256); config
-    4's and a 3-row-tile shape; an odd number of k-steps, whose last chunk has
-    one (64 x 2048 x 768); a single k-step and 10 units per workgroup
-    (48 x 20480 x 256); config 5's Qwen2-7B MLP (2368 units: 9 or 10 per
+    one workgroup per 16 columns.  17..32 rows whose x and item tiles fit LDS
+    (17 x 256 x 512: one unit per workgroup; config 4's 32 x 8960 x 1536) run
+    the unit kernel on two 16-row tiles.  The other 17..64-row shapes run the
+    wide kernel (x staged in 512-column chunks, unit accumulators in registers
+    across K): a 3-row-tile shape (40 rows); an odd number of k-steps, whose
+    last chunk has one (64 x 2048 x 768); a single k-step and 10 units per
+    workgroup (48 x 20480 x 256); two row tiles whose x exceeds LDS
+    (32 x 18944 x 3584); config 5's Qwen2-7B MLP (2368 units: 9 or 10 per
     workgroup)."""
     from grpo_mi355x import _lib
 
