@@ -57,7 +57,8 @@ def test_version_and_workspace_sizes(lib):
 
 def test_split_k_plan_covers_k_exactly():
     """Every plan's slices cover K: splits * kpw >= K/256 > (splits - 1) * kpw for a
-    k-steps-per-slice value kpw in {1, 2, 3, 4, 6, 8}; partial bytes match the layout."""
+    k-steps-per-slice value kpw in {1, 2, 3, 4, 5, 6, 8} (5 only for more than 16
+    rows); partial bytes match the layout."""
     from grpo_mi355x.kernels import ops
 
     for m, n, k, r, nseg in [(8, 2048, 1536, 16, 3), (8, 1536, 1536, 16, 1), (8, 17920, 1536, 0, 1),
@@ -66,9 +67,12 @@ def test_split_k_plan_covers_k_exactly():
                              (64, 3584, 18944, 0, 1), (64, 4608, 3584, 16, 3)]:
         splits, pb, tb = ops.nf4_linear_plan(m, n, k, r, nseg, 64)
         ks = k // 256
-        assert any(splits * kpw >= ks > (splits - 1) * kpw for kpw in (1, 2, 3, 4, 6, 8))
+        kpws = (1, 2, 3, 4, 5, 6, 8) if m > 16 else (1, 2, 3, 4, 6, 8)
+        assert any(splits * kpw >= ks > (splits - 1) * kpw for kpw in kpws)
         assert pb == splits * m * n * 4
         assert tb == (splits * nseg * m * 16 * 4 if r else 0)
+    # Qwen2-7B's down_proj at 64 rows: 15 slices of 5 k-steps (one workgroup round)
+    assert ops.nf4_linear_plan(64, 3584, 18944, 0, 1, 64)[0] == 15
     assert ops.nf4_linear_plan(8, 40, 512, 0, 1, 64) is None  # N % 16
     assert ops.nf4_linear_plan(65, 256, 512, 0, 1, 64) is None  # M > 64
     # 16 slices of 8 k-steps: even 16 staged rows of x exceed LDS
