@@ -454,46 +454,39 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
     }
   }
   __syncthreads();
-  // Per head (one thread each): the split's max M, the waves' weights
-  // 2^(m_w - M) and the split's sum L; then O four columns per thread.
-  __shared__ float sF[AW][GQ];
-  __shared__ float sDen[GQ];
-  if (tid < GQ) {
-    const int h = tid;
+  // Four columns of one head per thread: the split's max M and the waves'
+  // weights 2^(m_w - M) computed by every thread of the head (no second
+  // barrier behind a per-head pass), O summed in wave order; the head's first
+  // thread writes (M, L).
+  for (int i = tid; i < GQ * FD / 4; i += AT) {
+    const int h = i / (FD / 4), d4 = 4 * (i - h * (FD / 4));
     float M = -INFINITY;
 #pragma unroll
     for (int w = 0; w < AW; ++w) M = fmaxf(M, sM[w][h]);
+    float f[AW];
     float L = 0.f;
 #pragma unroll
     for (int w = 0; w < AW; ++w) {
-      const float f = M == -INFINITY ? 0.f : exp2f(sM[w][h] - M);
-      sF[w][h] = f;
-      L += f * sL[w][h];
+      f[w] = M == -INFINITY ? 0.f : exp2f(sM[w][h] - M);
+      L += f[w] * sL[w][h];
     }
-    const int64_t slot = ((int64_t)b * p.Hq + kvh * GQ + h) * p.S + s;
-    if (p.direct_out) {
-      sDen[h] = fmaxf(L, 1e-6f);
-    } else {
-      p.ws_ml[slot * 2] = M;
-      p.ws_ml[slot * 2 + 1] = L;
-    }
-  }
-  __syncthreads();
-  for (int i = tid; i < GQ * FD / 4; i += AT) {
-    const int h = i / (FD / 4), d4 = 4 * (i - h * (FD / 4));
     float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int w = 0; w < AW; ++w) {
-      const float f = sF[w][h];
       const float4 v = *reinterpret_cast<const float4*>(sO + ((size_t)w * GQ + h) * FD + d4);
-      O.x += f * v.x;
-      O.y += f * v.y;
-      O.z += f * v.z;
-      O.w += f * v.w;
+      O.x += f[w] * v.x;
+      O.y += f[w] * v.y;
+      O.z += f[w] * v.z;
+      O.w += f[w] * v.w;
+    }
+    if (!p.direct_out && d4 == 0) {
+      const int64_t slot = ((int64_t)b * p.Hq + kvh * GQ + h) * p.S + s;
+      p.ws_ml[slot * 2] = M;
+      p.ws_ml[slot * 2 + 1] = L;
     }
     if (p.direct_out) {
       // the whole context in this split: out = O / max(L, 1e-6), bf16
-      const float den = sDen[h];
+      const float den = fmaxf(L, 1e-6f);
       *reinterpret_cast<uint2*>(p.direct_out + ((int64_t)b * p.Hq + kvh * GQ + h) * FD + d4) =
           make_uint2(pack_bf2(O.x / den, O.y / den), pack_bf2(O.z / den, O.w / den));
     } else {
