@@ -199,8 +199,10 @@ struct PartArgs {
   int fin_lb_vec;           // r == 16 and lora_b 16-byte aligned
 };
 
-// X_WIDE: bf16, 16 waves; X_NORM: RMSNorm of h from per-group sums of squares
-enum XSource { X_BF16 = 0, X_ATTN = 1, X_SILU = 2, X_WIDE = 3, X_NORM = 4 };
+// X_WIDE: bf16, 16 waves; X_NORM: RMSNorm of h from per-group sums of squares;
+// X_WIDE8: X_WIDE on 8 waves (launches whose 16-wave grid fills at most half
+// the CUs)
+enum XSource { X_BF16 = 0, X_ATTN = 1, X_SILU = 2, X_WIDE = 3, X_NORM = 4, X_WIDE8 = 5 };
 // One arrival counter per 128-byte line: a tile group's counter line is only
 // ever touched by the workgroups of that group, which share one XCD's L2.
 constexpr int FIN_CNT_STRIDE = 32;
@@ -214,13 +216,21 @@ constexpr int NORM_MAX_GROUPS = 256;  // sums of squares per row the X_NORM sour
 // x slice takes more than 64 KiB of LDS (X_WIDE) run one workgroup per CU, so
 // it has 16 waves: four per SIMD keep enough weight loads in flight, and 16
 // tiles share each staged copy of x (a quarter of the L2 -> LDS traffic of 4).
+// When 16-wave workgroups would leave more than half of the CUs idle and two
+// workgroups fit a CU, X_WIDE8 takes twice as many 8-wave workgroups
+// (Qwen2-7B's o_proj at 64 rows: 112 -> 224 workgroups, 11.9 -> 9.0 us).
 #ifndef GRPO_ATTN_WAVES
 #define GRPO_ATTN_WAVES PART_WAVES
 #endif
 __host__ __device__ constexpr int waves_per_group(int xsrc) {
-  return xsrc == X_SILU ? 8 : (xsrc == X_ATTN ? GRPO_ATTN_WAVES : (xsrc == X_WIDE ? 16 : PART_WAVES));
+  return xsrc == X_SILU || xsrc == X_WIDE8
+             ? 8
+             : (xsrc == X_ATTN ? GRPO_ATTN_WAVES : (xsrc == X_WIDE ? 16 : PART_WAVES));
 }
-__host__ __device__ constexpr bool bf16_source(int xsrc) { return xsrc == X_BF16 || xsrc == X_WIDE; }
+__host__ __device__ constexpr bool wide_source(int xsrc) { return xsrc == X_WIDE || xsrc == X_WIDE8; }
+__host__ __device__ constexpr bool bf16_source(int xsrc) {
+  return xsrc == X_BF16 || wide_source(xsrc);
+}
 constexpr int GU_MAX_SLICES = 2;  // K slices of the gate|up partial sums read while staging
 
 // Columns k..k+7 of row m of bf16(bf16(silu(g)) * u), with g = bf16(sum of the
@@ -639,8 +649,8 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
     for (int i = 0; i < KPW; ++i) {
       const int kc = kbase + min(i, nk - 1) * KSTEP + 64 * lg;
       const uint4* wp = reinterpret_cast<const uint4*>(wrow + kc / 2);
-      wv[2 * i] = load_w<XSRC != X_WIDE>(wp);
-      wv[2 * i + 1] = load_w<XSRC != X_WIDE>(wp + 1);
+      wv[2 * i] = load_w<!wide_source(XSRC)>(wp);
+      wv[2 * i + 1] = load_w<!wide_source(XSRC)>(wp + 1);
       av[i] = p.absmax[((int64_t)wr * p.K + kc) >> p.bs_shift];
     }
   }
@@ -1157,7 +1167,14 @@ int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* 
     c.part = h.part + (int64_t)m0 * h.N;
     c.tpart = h.tpart ? h.tpart + (int64_t)m0 * 16 : nullptr;
     int rc;
-    if (pl.lds > (size_t)PART_LDS_MAX) {
+    const int64_t wgs16 = cdiv(cdiv(pl.ntiles, 16), NUM_XCD) * NUM_XCD * pl.S;
+    if (pl.lds > (size_t)PART_LDS_MAX && wgs16 <= 128 && 2 * pl.lds <= (size_t)PART_LDS_BIG) {
+      switch (pl.MT) {
+        case 1: rc = launch_part<1, X_WIDE8>(c, pl, st); break;
+        case 2: rc = launch_part<2, X_WIDE8>(c, pl, st); break;
+        default: rc = launch_part<4, X_WIDE8>(c, pl, st); break;
+      }
+    } else if (pl.lds > (size_t)PART_LDS_MAX) {
       switch (pl.MT) {
         case 1: rc = launch_part<1, X_WIDE>(c, pl, st); break;
         case 2: rc = launch_part<2, X_WIDE>(c, pl, st); break;

@@ -99,7 +99,8 @@ FAST = [
     (64, 3584, 18944, 0, False),  # 7B down_proj at G = 64: 5 k-steps per slice, x chunk-major
     (57, 3584, 18944, 16, True),  # the same with ragged rows (57) and LoRA partials
     (20, 2048, 18944, 16, True),  # 5 k-steps chunk-major on two row tiles (rows 20..31 unused)
-    (48, 1536, 18944, 16, True),  # 6 k-steps per slice with LoRA partials
+    (48, 1536, 18944, 16, True),  # 19 slices of 4 k-steps with LoRA partials
+    (64, 3584, 3584, 16, False),  # 7B o_proj at G = 64: 8-wave wide workgroups (224 of them)
     (64, 256, 40960, 16, True),   # x over LDS: 32-row launches (tpart row offsets)
     (64, 256, 4096, 16, True),    # LoRA with two k-steps per wave
 ]
