@@ -1908,6 +1908,11 @@ bool units_ok(int M, int I, int K) {
   return (nu * KS + GU_UNITS_W - 1) / GU_UNITS_W <= GU_UNITS_IPW && units_lds(M, I, K) <= cap;
 }
 
+// 17..32 rows on the unit kernel with two row tiles (x and the item tiles in LDS).
+bool units2_ok(int M, int I, int K, int blocksize) {
+  return M > 16 && pow2(blocksize) && blocksize >= 64 && units_ok(M, I, K);
+}
+
 // Shape support of nf4_gate_up_silu; returns false for shapes it does not take.
 bool plan_gu(int M, int I, int K, int blocksize, GuPlan* pl) {
   if (M < 1 || M > 16 || I <= 0 || I % 16 || K <= 0 || K % KSTEP) return false;
@@ -2368,7 +2373,10 @@ extern "C" int grpo_nf4_linear_partials_silu(const grpo_linear_parts_t* gate_up,
 extern "C" int grpo_nf4_gate_up_silu_supported(int M, int I, int K, int blocksize) {
   GuPlan pl;
   size_t lds;
-  return plan_gu(M, I, K, blocksize, &pl) || gu_wide_ok(M, I, K, blocksize, &lds) ? 1 : 0;
+  return plan_gu(M, I, K, blocksize, &pl) || units2_ok(M, I, K, blocksize) ||
+                 gu_wide_ok(M, I, K, blocksize, &lds)
+             ? 1
+             : 0;
 }
 
 namespace {
@@ -2513,8 +2521,7 @@ int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absma
   // tiles (x staged once, no chunk barriers; config 4's 32 x 8960 x 1536: 14.3
   // -> 13.2 us per traced launch, 6522 -> 6842 tok/s), the other wide shapes
   // the chunked wide kernel
-  const bool units2 = !nrm && !act_tiles && M > 16 && pow2(blocksize) && blocksize >= 64 &&
-                      units_ok(M, I, K);
+  const bool units2 = !nrm && !act_tiles && units2_ok(M, I, K, blocksize);
   const bool wide = !units2 && !nrm && !act_tiles && gu_wide_ok(M, I, K, blocksize, &wlds);
   if (!wide && !units2 && !plan_gu(M, I, K, blocksize, &pl)) {
     set_error("shape not supported by the fused gate|up SiLU kernel");

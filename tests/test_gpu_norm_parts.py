@@ -110,7 +110,7 @@ def test_add_rmsnorm_parts_matches_oracle(dev, m, n, k, lora, offset):
                                    (8, 512, 3584), (8, 17920, 3584), (5, 4112, 512),
                                    (17, 256, 512), (32, 8960, 1536), (40, 8960, 1536),
                                    (64, 2048, 768), (48, 20480, 256), (32, 18944, 3584),
-                                   (64, 18944, 3584)])
+                                   (64, 18944, 3584), (24, 40000, 256)])
 def test_gate_up_silu_matches_oracle(dev, m, i, k):
     _check_gate_up_silu(dev, m, i, k, 8)
 
@@ -129,8 +129,9 @@ def _check_gate_up_silu(dev, m, i, k, pad):
     over 256 workgroups: two workgroups take a third unit); [8, 17920, 3584]
     has more items per wave than the unit kernel keeps in registers and runs
     one workgroup per 16 columns.  17..32 rows whose x and item tiles fit LDS
-    (17 x 256 x 512: one unit per workgroup; config 4's 32 x 8960 x 1536) run
-    the unit kernel on two 16-row tiles.  The other 17..64-row shapes run the
+    (17 x 256 x 512: one unit per workgroup; config 4's 32 x 8960 x 1536;
+    24 x 40000 x 256: 19 or 20 units per workgroup, more than the wide kernel
+    takes) run the unit kernel on two 16-row tiles.  The other 17..64-row shapes run the
     wide kernel (x staged in 512-column chunks, unit accumulators in registers
     across K): a 3-row-tile shape (40 rows); an odd number of k-steps, whose
     last chunk has one (64 x 2048 x 768); a single k-step and 10 units per
@@ -179,6 +180,9 @@ def test_gate_up_silu_rejects_unsupported(dev):
     assert lib.grpo_nf4_gate_up_silu_supported(32, 256, 500, 64) == 0  # K % 256
     assert lib.grpo_nf4_gate_up_silu_supported(8, 256, 6400, 64) == 0  # K > 6144
     assert lib.grpo_nf4_gate_up_silu_supported(32, 256, 512, 32) == 0  # blocksize < 64
-    assert lib.grpo_nf4_gate_up_silu_supported(32, 24584, 512, 64) == 0  # > 12 units per CU
+    # more than 12 units per CU for the wide kernel, more than 32 rows for the
+    # unit kernel (32 rows take it on two row tiles)
+    assert lib.grpo_nf4_gate_up_silu_supported(40, 24584, 512, 64) == 0
+    assert lib.grpo_nf4_gate_up_silu_supported(32, 24584, 512, 64) == 1
     assert lib.grpo_nf4_gate_up_silu(None, 512, None, None, None, 64, 256, 512, 65, None, 256,
                                      None) == -2  # GRPO_EUNSUPPORTED
