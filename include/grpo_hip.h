@@ -316,11 +316,15 @@ int grpo_nf4_linear_partials_silu(const grpo_linear_parts_t* gate_up, const uint
  * weight (bnb Params4bit, non-nested absmax; dequant of lora_forward.py:171-206,
  * no bias, no LoRA) with fused_silu_mul (fused_ops.py:79-112) applied, as
  * fused_mlp feeds down_proj (fused_ops.py:184-193).  act is bf16 [M, lda].
- * Fast path only: M <= 16, I % 16 == 0, K % 256 == 0, K <= 6144, power-of-two
- * blocksize >= 64, M * (K + 8) * 2 bytes of x plus the slice sums in 64 KiB of
- * LDS; GRPO_EUNSUPPORTED otherwise (see grpo_nf4_gate_up_silu_supported).
- * Shapes with I % 8 == 0 whose 8-column units fit one workgroup per CU run
- * those units; the others run one workgroup per 16 columns. */
+ * Fast paths only (GRPO_EUNSUPPORTED otherwise; see
+ * grpo_nf4_gate_up_silu_supported); K % 256 == 0, power-of-two blocksize >= 64:
+ *   M <= 16: I % 16 == 0, K <= 6144, x and the slice sums in 64 KiB of LDS;
+ *     shapes with I % 8 == 0 whose 8-column units fit one workgroup per CU
+ *     run those units, the others one workgroup per 16 columns;
+ *   17..32 rows whose x [M, K] and unit tiles fit 160 KiB of LDS: the unit
+ *     kernel on two 16-row tiles;
+ *   other 17..64-row shapes with I % 8 == 0 and at most 12 units per CU: x
+ *     staged in 512-column chunks, unit accumulators in registers across K. */
 int grpo_nf4_gate_up_silu(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
                           const float* code16, int blocksize, int I, int K, int M, void* act,
                           int64_t lda, grpo_stream_t stream);
