@@ -478,8 +478,9 @@ size_t grpo_lm_head_workspace_bytes(int M, int V);
  * in the workspace, the (max, first index) of every 16-column tile of every
  * row for grpo_decode_advance.  The bf16 lm_head of _step
  * (paged_kv.py:800-806) followed by the first pass of the greedy argmax
- * (paged_kv.py:444-445).  Needs V % 16 == 0, K % 256 == 0, M <= 64 and
- * M * (K + 8) * 2 <= 160 KiB (GRPO_EUNSUPPORTED otherwise). */
+ * (paged_kv.py:444-445).  Needs V % 16 == 0, K % 256 == 0 and M <= 64; x of
+ * more than 160 KiB (M * (K + 8) * 2) is staged in K chunks by a one-workgroup-
+ * per-CU kernel, which takes V <= 163840 (einval otherwise). */
 int grpo_lm_head_argmax(const void* x, int64_t ldx, const void* w, int V, int K, int M,
                         void* logits, int64_t ld_logits, void* workspace, size_t workspace_bytes,
                         grpo_stream_t stream);
