@@ -67,10 +67,11 @@ __device__ __forceinline__ void lin_load_t(const LinParts& o, int m, float* ts) 
     const int seg = i >> 2, q = i & 3;
     const float4* p = reinterpret_cast<const float4*>(o.tpart + ((int64_t)seg * o.M + m) * 16) + q;
     const int64_t stride = (int64_t)o.nseg * o.M * 4;
+    // Every load unconditional (slices >= S re-read the last one): predicated
+    // loads in this divergent loop were issued one round trip apart.
     float4 v[MS];
 #pragma unroll
-    for (int k = 0; k < MS; ++k)
-      if (k < o.S) v[k] = p[k * stride];
+    for (int k = 0; k < MS; ++k) v[k] = p[min(k, o.S - 1) * stride];
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
     for (int k = 0; k < MS; ++k)
