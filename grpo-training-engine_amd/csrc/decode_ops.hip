@@ -251,10 +251,23 @@ __global__ void __launch_bounds__(T) add_rmsnorm_parts_kernel(
   touch_kernargs<sizeof(LinParts) + 4 * sizeof(void*) + 8>();
   __shared__ float red[PARTS_T / 64];
   __shared__ float ts[MAXSEG * 16];
-  extern __shared__ float hs[];  // H floats (columns past 4 * PARTS_T only)
+  // Dynamic LDS: max(H, 4 * PARTS_T) floats with LoRA, else H (512 threads)
+  // or none.  hs holds the columns past 4 * PARTS_T; lu, the LoRA sums of
+  // each wave's 256 columns, the first 4 * PARTS_T floats (disjoint from
+  // every hs entry used).
+  extern __shared__ float hs[];
+  float* lu = hs;
   const int m = blockIdx.x, H = o.N;
   const int64_t row = (int64_t)m * H;
   const int tid = threadIdx.x;
+  // Rank-16 LoRA of one aligned segment: each wave reads the B rows of its
+  // 256 columns in 1 KiB loads (lin_fetch_lb_wave) instead of 128 bytes per
+  // lane.  o1 serves the first pass (other LoRA shapes read B per element
+  // there), o the wide rows.
+  const int c0 = 4 * (tid & ~63);
+  const bool wave_lb = LORA && o.r == 16 && o.lb_vec && o.nseg == 1 && c0 < H;
+  LinParts o1 = o;
+  o1.lb_vec = false;
   // Thread tid owns columns 4*tid .. 4*tid+3 from the loads to the final
   // stores, so its h stays in registers; the norm weight is fetched with the
   // partial sums (a load after the row reduction would be one more memory
@@ -263,8 +276,10 @@ __global__ void __launch_bounds__(T) add_rmsnorm_parts_kernel(
   const bool first = tid < H / 4;
   Fetch4<MS> f;
   uint2 res0 = make_uint2(0, 0), w0 = make_uint2(0, 0);
+  uint4 lbw[8];
+  if (wave_lb) lin_fetch_lb_wave(o, c0, lbw);
   if (first) {
-    lin_fetch4(o, m, 4 * tid, f);
+    lin_fetch4(o1, m, 4 * tid, f);
     if (residual) res0 = *reinterpret_cast<const uint2*>(residual + row + 4 * tid);
     if (vec) {
       w0 = *reinterpret_cast<const uint2*>(w + 4 * tid);
@@ -275,6 +290,8 @@ __global__ void __launch_bounds__(T) add_rmsnorm_parts_kernel(
   }
   lin_load_t<MS>(o, m, ts);
   __syncthreads();
+  float4 lora_u = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (wave_lb) lora_u = lin_lora_wave(ts, lbw, lu + c0);
   float ss = 0.f;
   float h0[4] = {0.f, 0.f, 0.f, 0.f};
   auto add_res = [&](const float (&v)[4], uint2 rr, float (&h)[4]) {
@@ -287,7 +304,7 @@ __global__ void __launch_bounds__(T) add_rmsnorm_parts_kernel(
   };
   if (first) {
     float v[4];
-    lin_finish4(o, ts, f, v);
+    lin_finish4(o1, ts, f, v, wave_lb, lora_u);
     add_res(v, res0, h0);
   }
   // rows wider than 4 * PARTS_T (the 1024-thread forms take at most 4096 columns)
@@ -547,20 +564,20 @@ extern "C" int grpo_add_rmsnorm_parts(const grpo_linear_parts_t* x, const void* 
   // for a second round trip after the LoRA-t barrier (64 x 3584 from 7 slices
   // with LoRA: 11.8 us with 512 threads).
   const bool one_pass = o.N > 4 * PARTS_T && o.N <= 4 * 1024;
+  const size_t lds512 = std::max(o.N, 4 * PARTS_T) * sizeof(float);
   if (one_pass && o.S <= 8)
-    add_rmsnorm_parts_kernel<1024, 8, true><<<dim3(o.M), 1024, 0, as_stream(stream)>>>(
-        o, res, ho, wt, yo, eps, vec);
+    add_rmsnorm_parts_kernel<1024, 8, true>
+        <<<dim3(o.M), 1024, 4 * 1024 * sizeof(float), as_stream(stream)>>>(o, res, ho, wt, yo,
+                                                                           eps, vec);
   else if (one_pass && o.S <= 16 && o.r == 0)
     add_rmsnorm_parts_kernel<1024, 16, false><<<dim3(o.M), 1024, 0, as_stream(stream)>>>(
         o, res, ho, wt, yo, eps, vec);
   else if (o.S <= 8)
     add_rmsnorm_parts_kernel<PARTS_T, 8, true>
-        <<<dim3(o.M), PARTS_T, o.N * sizeof(float), as_stream(stream)>>>(o, res, ho, wt, yo, eps,
-                                                                         vec);
+        <<<dim3(o.M), PARTS_T, lds512, as_stream(stream)>>>(o, res, ho, wt, yo, eps, vec);
   else
     add_rmsnorm_parts_kernel<PARTS_T, MAX_SLICES, true>
-        <<<dim3(o.M), PARTS_T, o.N * sizeof(float), as_stream(stream)>>>(o, res, ho, wt, yo, eps,
-                                                                         vec);
+        <<<dim3(o.M), PARTS_T, lds512, as_stream(stream)>>>(o, res, ho, wt, yo, eps, vec);
   return launch_check("add_rmsnorm_parts");
 }
 

@@ -153,11 +153,58 @@ __device__ __forceinline__ void lin_store_t(const LinParts& o, const float4 (&v)
   t[3] = round_bf(acc.w);
 }
 
+// LoRA B rows of one wave's 256 consecutive output columns c0 .. c0 + 255
+// (r == 16, one segment, 16-byte aligned B): load k of lane l is the 16 bytes
+// of ranks 8 (l & 1) .. + 7 of column c0 + 32 k + l / 2, so every load
+// instruction reads 1 KiB contiguous.  (Lane l's own four columns are 128
+// contiguous bytes; read that way each instruction touches 64 cache lines,
+// and the address unit takes a cycle per line.)  Columns past N re-read
+// column N - 1.  Every lane of the wave calls it.
+__device__ __forceinline__ void lin_fetch_lb_wave(const LinParts& o, int c0, uint4 (&lb)[8]) {
+  const int l = threadIdx.x & 63;
+  const uint16_t* b = o.lb[0] + 8 * (l & 1);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const int col = min(c0 + 32 * k + (l >> 1), o.N - 1);
+    lb[k] = *reinterpret_cast<const uint4*>(b + (int64_t)col * 16);
+  }
+}
+
+// t . B[n, :] for lane l's four columns c0 + 4 l .. + 3 from the rows of
+// lin_fetch_lb_wave: the two lanes of a column each sum eight ranks (in rank
+// order) and add the other's sum; the column sums pass through lu (this
+// wave's 256 floats of LDS) to the lane that owns the column.  Every lane of
+// the wave calls it.
+__device__ __forceinline__ float4 lin_lora_wave(const float* ts, const uint4 (&lb)[8],
+                                                float* lu) {
+  const int l = threadIdx.x & 63;
+  const float* t = ts + 8 * (l & 1);
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t w[4] = {lb[k].x, lb[k].y, lb[k].z, lb[k].w};
+    float s = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      s += t[2 * j] * bf_lo(w[j]);
+      s += t[2 * j + 1] * bf_hi(w[j]);
+    }
+    s += __shfl_xor(s, 1);
+    if (!(l & 1)) lu[32 * k + (l >> 1)] = s;
+  }
+  // LDS serves one wave's instructions in order: no barrier between the
+  // writes and the reads of other lanes' sums
+  __builtin_amdgcn_wave_barrier();
+  return *reinterpret_cast<const float4*>(lu + 4 * l);
+}
+
 // The reference's bf16 values (as floats) of the four outputs; ts holds the
 // row's LoRA t (lin_load_t) when r > 0.
+// has_u: lora_u holds the four t . B[n, :] sums (lin_lora_wave); else they
+// are computed here from f.lb or B.
 template <int MS>
 __device__ __forceinline__ void lin_finish4(const LinParts& o, const float* ts,
-                                            const Fetch4<MS>& f, float v[4]) {
+                                            const Fetch4<MS>& f, float v[4], bool has_u = false,
+                                            float4 lora_u = float4{0.f, 0.f, 0.f, 0.f}) {
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
   for (int k = 0; k < MS; ++k)
@@ -192,7 +239,9 @@ __device__ __forceinline__ void lin_finish4(const LinParts& o, const float* ts,
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
       float u = 0.f;
-      if (o.lb_vec) {
+      if (has_u) {
+        u = c == 0 ? lora_u.x : (c == 1 ? lora_u.y : (c == 2 ? lora_u.z : lora_u.w));
+      } else if (o.lb_vec) {
         const uint4 b0 = f.lb[2 * c], b1 = f.lb[2 * c + 1];
         const uint32_t bw[8] = {b0.x, b0.y, b0.z, b0.w, b1.x, b1.y, b1.z, b1.w};
 #pragma unroll
