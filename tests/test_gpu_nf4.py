@@ -103,6 +103,8 @@ FAST = [
     (64, 3584, 3584, 16, False),  # 7B o_proj at G = 64: 8-wave wide workgroups (224 of them)
     (64, 256, 40960, 16, True),   # x over LDS: 32-row launches (tpart row offsets)
     (64, 256, 4096, 16, True),    # LoRA with two k-steps per wave
+    (8, 400, 512, 16, True),      # N not a multiple of 256: the finish's last wave ragged
+    (3, 1040, 512, 16, False),    # ... a second finish workgroup with 16 columns
 ]
 
 

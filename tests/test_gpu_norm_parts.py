@@ -43,12 +43,14 @@ def _dev_bf16(bits, dev, offset=0):
                                                (8, 3584, 512, True, 0), (8, 3584, 512, False, 1),
                                                (64, 3584, 3584, True, 0),
                                                (64, 3584, 18944, False, 0),
-                                               (16, 3584, 18944, False, 1)])
+                                               (16, 3584, 18944, False, 1),
+                                               (4, 1040, 512, True, 0)])
 def test_add_rmsnorm_parts_matches_oracle(dev, m, n, k, lora, offset):
     """The 64-row cases are config 5's post-attention norm (7 slices of o_proj
     partials with LoRA) and input norm (15 slices of down_proj partials, no
     LoRA): rows of 3584 columns finished by 1024 threads in one pass; the last
-    takes the 16-slice form with a 2-byte aligned weight and output."""
+    takes the 16-slice form with a 2-byte aligned weight and output.  1040
+    columns leave the LoRA B wave loads one wave of 16 columns."""
     from grpo_mi355x import _lib
     from grpo_mi355x.kernels import ops
 
