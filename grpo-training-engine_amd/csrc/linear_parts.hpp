@@ -188,7 +188,7 @@ __device__ __forceinline__ float4 lin_lora_wave(const float* ts, const uint4 (&l
       s += t[2 * j] * bf_lo(w[j]);
       s += t[2 * j + 1] * bf_hi(w[j]);
     }
-    s += __shfl_xor(s, 1);
+    s += dpp_move<0xB1>(s);  // quad_perm [1,0,3,2]: the other half of the column
     if (!(l & 1)) lu[32 * k + (l >> 1)] = s;
   }
   // LDS serves one wave's instructions in order: no barrier between the
