@@ -138,6 +138,21 @@ template <int CTRL>
 __device__ __forceinline__ float dpp_move(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
 }
+// Sum over each aligned group of 8 lanes (every lane of the group gets it):
+// DPP quad_perm xor 1, xor 2, then the half-row mirror (lane i + lane 7 - i).
+__device__ __forceinline__ float sum8(float v) {
+  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
+  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
+  v += dpp_move<0x141>(v);  // row_half_mirror
+  return v;
+}
+// The same over each DPP row of 16 lanes (then the row mirror, lane i + 15 - i).
+__device__ __forceinline__ float sum16(float v) {
+  v = sum8(v);
+  v += dpp_move<0x140>(v);  // row_mirror
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum_dpp(float v) {
   v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
   v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
@@ -156,6 +171,53 @@ __device__ __forceinline__ uint4 norm8(uint4 hv, uint4 wv, float inv) {
     o[q] = pack_bf2(round_bf(bf_lo(hw[q]) * inv) * bf_lo(ww[q]),
                     round_bf(bf_hi(hw[q]) * inv) * bf_hi(ww[q]));
   return make_uint4(o[0], o[1], o[2], o[3]);
+}
+
+// ------------------------------------------------ same-XCD hand-over ------
+// Several kernels hand a group's partial results to the last-arriving
+// workgroup of the group through an L2 atomic counter and plain stores.  That
+// is correct only if every workgroup of the group runs on one XCD (one L2):
+// the launches give a group's workgroups equal linear ids modulo 8, and the
+// dispatcher places workgroup i on XCD (i + c) mod 8 (c fixed per launch).
+// The assumption is checked, not trusted: every arrival adds 1 to a 4-bit
+// field of the counter selected by the XCD it runs on (HW_REG_XCC_ID), so
+//  * a group on one XCD ends with n arrivals in one field (the last arriver
+//    resets the counter to zero);
+//  * a group whose arrivals reach one counter from two XCDs ends with two
+//    non-zero fields: the arriver that completes the count sets *err;
+//  * a group split over two L2s never completes a count in either: its
+//    counter is left non-zero.
+// The host reads the counters and *err after a run; non-zero means the
+// hand-over was not on one XCD and the results of that run are not valid.
+
+// XCD of the calling wave (hardware register 20 = XCC_ID, bits 3:0).
+__device__ __forceinline__ uint32_t xcc_id() {
+  return (uint32_t)__builtin_amdgcn_s_getreg((3 << 11) | 20) & 15u;
+}
+
+// Sum of the eight 4-bit fields of v.
+__device__ __forceinline__ uint32_t nibble_sum(uint32_t v) {
+  v = (v & 0x0F0F0F0Fu) + ((v >> 4) & 0x0F0F0F0Fu);
+  v += v >> 8;
+  v += v >> 16;
+  return v & 0xFFu;
+}
+
+// One arrival of a group of n <= 15 workgroups at *cnt (called by one thread,
+// after the workgroup's stores are acknowledged).  Returns true for the
+// arrival that completes the group; that one resets *cnt.
+__device__ __forceinline__ bool xcd_arrive(int* cnt, int n, int* err) {
+  const uint32_t x = xcc_id();
+  const uint32_t inc = 1u << (4 * (x & 7u));
+  const uint32_t old = (uint32_t)__hip_atomic_fetch_add(cnt, (int)inc, __ATOMIC_RELAXED,
+                                                        __HIP_MEMORY_SCOPE_WORKGROUP);
+  const uint32_t now = old + inc;
+  if (nibble_sum(now) != (uint32_t)n) return false;
+  if (x > 7u || now != (uint32_t)n << (4 * (x & 7u))) {
+    if (err) *err = 1;
+  }
+  *cnt = 0;
+  return true;
 }
 
 __device__ __forceinline__ f32x4_t mfma16x16x32(uint4 a, uint4 b, f32x4_t c) {

@@ -345,7 +345,7 @@ __global__ void __launch_bounds__(T) add_rmsnorm_parts_kernel(
 
 // h = bf16(residual + y) for the finished linear output y (the epilogue of
 // linear_parts.hpp) and, for the RMSNorm its consumer stages, sumsq[m, g] = sum
-// of h^2 over the FRS_COLS columns of group g.  One wave per (group, row), so a
+// of h^2 over the 64 columns of group g.  One wave per (256 columns, row), so a
 // row's partial sums, LoRA B rows and residual are fetched by N / 256 CUs, not
 // one: the per-row RMSNorm kernel above moved ~90 KB through a single CU per
 // row for o_proj at hidden 1536.
@@ -380,8 +380,10 @@ __global__ void __launch_bounds__(FRS_T) finish_residual_sumsq_kernel(
     *reinterpret_cast<uint2*>(h_out + (int64_t)m * ld + n) =
         make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
   }
-  ss = wave_sum(ss);
-  if (threadIdx.x == 0) sumsq[(int64_t)m * G + g] = ss;
+  // per 64 columns (16 lanes of 4): one sum per DPP row of the wave
+  ss = sum16(ss);
+  const int c64 = (g * FRS_COLS + 64 * (threadIdx.x >> 4)) / 64;
+  if ((threadIdx.x & 15) == 0 && c64 < G) sumsq[(int64_t)m * G + c64] = ss;
 }
 
 // rope_append_kernel with qkv = the finished q|k|v output of row b; one
@@ -591,8 +593,9 @@ extern "C" int grpo_linear_finish_residual(const grpo_linear_parts_t* x, const v
   auto a8 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 7u) == 0; };
   if (!a8(h_out) || (residual && !a8(residual)))
     return einval("residual and h_out must be 8-byte aligned");
-  const int G = (int)cdiv(o.N, FRS_COLS);
-  finish_residual_sumsq_kernel<<<dim3((unsigned)G, (unsigned)o.M), FRS_T, 0,
+  if (o.N % 64) return einval("N must be a multiple of 64");
+  const int G = o.N / 64;  // sums of squares per row, one per 64 columns
+  finish_residual_sumsq_kernel<<<dim3((unsigned)cdiv(o.N, FRS_COLS), (unsigned)o.M), FRS_T, 0,
                                  as_stream(stream)>>>(
       o, static_cast<const uint16_t*>(residual), static_cast<uint16_t*>(h_out), ld, sumsq, G);
   return launch_check("finish_residual_sumsq");

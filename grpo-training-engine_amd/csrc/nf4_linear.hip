@@ -34,22 +34,12 @@
 #include <type_traits>
 
 #include "linear_parts.hpp"
+#include "nf4_decode.hpp"
 
 using namespace grpo;
 
 namespace {
 
-constexpr int KSTEP = 256;          // k elements per step: 4 lane groups x 64
-// NF4 weight bytes are read once per step.  Decode batches (M <= 16) load
-// them with the non-temporal hint: with the weight, K/V and lm_head streams
-// all marked so, a config-3 decode step keeps its small per-step data (split-K
-// partials, activations, norms, LoRA, absmax) in L2 across kernels and runs in
-// 1291 us against 1342 (each hint alone changes nothing).  Wide batches load
-// them plainly (the hint cost 3 % at config 5).
-template <bool NT>
-__device__ __forceinline__ uint4 load_w(const uint4* p) {
-  return NT ? load_stream(p) : *p;
-}
 constexpr int PART_WAVES = 4;       // n-tiles (waves) per workgroup, x given in bf16
 constexpr int PART_LDS_MAX = 65536; // bytes of the staged x slice per workgroup (M <= 16)
 // Wide batches (M > 16) may stage up to all of gfx950's 160 KiB per workgroup:
@@ -105,55 +95,6 @@ __global__ void __launch_bounds__(256) nf4_dequant_scalar(const uint8_t* __restr
   }
 }
 
-// ------------------------------------------------------- nibble decode --
-
-__device__ __forceinline__ uint32_t bfi(uint32_t m, uint32_t a, uint32_t b) {
-  return (m & a) | (~m & b);
-}
-
-// 16-entry bf16 codebook of one absmax block, split into high bytes (hb) and
-// low bytes (lb): hb[i] byte j = high byte of bf16(code[4i+j] * a).
-struct Lut {
-  uint32_t hb[4], lb[4];
-};
-
-__device__ __forceinline__ Lut make_lut(const float (&code)[16], float a) {
-  Lut t;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint32_t p01 = pack_bf2(code[4 * i] * a, code[4 * i + 1] * a);
-    const uint32_t p23 = pack_bf2(code[4 * i + 2] * a, code[4 * i + 3] * a);
-    t.hb[i] = perm(p23, p01, 0x07050301u);
-    t.lb[i] = perm(p23, p01, 0x06040200u);
-  }
-  return t;
-}
-
-// Eight nibbles of one little-endian dword (bytes b0..b3; element 2i = high
-// nibble of b_i) -> eight bf16 as 4 dwords in element order [0,2,4,6,1,3,5,7].
-__device__ __forceinline__ uint4 decode8(uint32_t wd, const Lut& t) {
-  const uint32_t sh = (wd >> 4) & 0x07070707u;               // low 3 bits, even elements
-  const uint32_t sl = wd & 0x07070707u;                      // low 3 bits, odd elements
-  const uint32_t mh = perm(wd << 8, wd, 0x090B080Au);        // 0xFF where nibble bit 3 set
-  const uint32_t ml = perm(wd << 12, wd << 4, 0x090B080Au);
-  const uint32_t Hh = bfi(mh, perm(t.hb[3], t.hb[2], sh), perm(t.hb[1], t.hb[0], sh));
-  const uint32_t Lh = bfi(mh, perm(t.lb[3], t.lb[2], sh), perm(t.lb[1], t.lb[0], sh));
-  const uint32_t Hl = bfi(ml, perm(t.hb[3], t.hb[2], sl), perm(t.hb[1], t.hb[0], sl));
-  const uint32_t Ll = bfi(ml, perm(t.lb[3], t.lb[2], sl), perm(t.lb[1], t.lb[0], sl));
-  return make_uint4(perm(Hh, Lh, 0x05010400u), perm(Hh, Lh, 0x07030602u),
-                    perm(Hl, Ll, 0x05010400u), perm(Hl, Ll, 0x07030602u));
-}
-
-// Eight bf16 in natural order (4 dwords) -> the decode8 order [0,2,4,6,1,3,5,7].
-__device__ __forceinline__ uint4 deinterleave8(uint4 v) {
-  return make_uint4(perm(v.y, v.x, 0x05040100u), perm(v.w, v.z, 0x05040100u),
-                    perm(v.y, v.x, 0x07060302u), perm(v.w, v.z, 0x07060302u));
-}
-
-__device__ __forceinline__ uint32_t word(const uint4& v, int i) {
-  return i == 0 ? v.x : (i == 1 ? v.y : (i == 2 ? v.z : v.w));
-}
-
 // ---------------------------------------------------- split-K linear --
 
 struct PartArgs {
@@ -189,6 +130,7 @@ struct PartArgs {
   // sums the group's partials and writes h = residual + y for its columns.
   float* fin_tpart;         // [groups][S][M][16]: LoRA t partials of each group's slices
   int* fin_cnt;             // [groups * FIN_CNT_STRIDE] arrival counters: zero, left zero
+  int* fin_err;             // set to 1 when a group's slices ran on two XCDs (xcd_arrive)
   const uint16_t* fin_res;  // residual [M][fin_ld] bf16 (may alias fin_h)
   uint16_t* fin_h;          // h [M][fin_ld] bf16
   int64_t fin_ld;
@@ -354,22 +296,6 @@ __device__ __forceinline__ uint4 attn_chunk(const PartArgs& p, int m, int k) {
   attn_fetch(p, m, k, f);
   return attn_finish(p, f);
 }
-
-// Sum over each aligned group of 8 lanes (every lane of the group gets it):
-// DPP quad_perm xor 1, xor 2, then the half-row mirror (lane i + lane 7 - i).
-__device__ __forceinline__ float sum8(float v) {
-  v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]
-  v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]
-  v += dpp_move<0x141>(v);  // row_half_mirror
-  return v;
-}
-// The same over each DPP row of 16 lanes (then the row mirror, lane i + 15 - i).
-__device__ __forceinline__ float sum16(float v) {
-  v = sum8(v);
-  v += dpp_move<0x140>(v);  // row_mirror
-  return v;
-}
-
 
 // Last-arriver finish of tile group g (FIN): columns n0 .. n0 + 16 * WPG - 1 of
 // every row, n0 = g * 16 * WPG, from the partial sums and LoRA t partials that
@@ -822,17 +748,14 @@ __global__ void __launch_bounds__(64 * waves_per_group(XSRC)) nf4_part_mfma(Part
     // L1 lines (a CU keeps no line of another workgroup's partials from this
     // kernel, but the invalidate costs nothing) and finishes the group.  Every
     // workgroup of a group has the same linear id modulo 8 (gridDim.x is a
-    // multiple of 8), so the group runs on one XCD and shares one L2.
+    // multiple of 8), so the group runs on one XCD and shares one L2;
+    // xcd_arrive checks that and flags a group that did not (fin_err).
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     __shared__ int s_last;
-    if (tid == 0) {
-      int* c = p.fin_cnt + (int64_t)blockIdx.x * FIN_CNT_STRIDE;
-      const int old = __hip_atomic_fetch_add(c, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      const int last = old == (int)gridDim.y - 1;
-      if (last) *c = 0;
-      s_last = last;
-    }
+    if (tid == 0)
+      s_last = xcd_arrive(p.fin_cnt + (int64_t)blockIdx.x * FIN_CNT_STRIDE, (int)gridDim.y,
+                          p.fin_err);
     __syncthreads();
     if (!s_last) return;
     asm volatile("buffer_inv sc0" ::: "memory");
@@ -1018,6 +941,7 @@ int launch_part_fin(const PartArgs& a, const PartPlan& pl, hipStream_t st) {
 struct FinTarget {
   float* tpart = nullptr;  // [groups][S][M][16]
   int* cnt = nullptr;      // [groups * FIN_CNT_STRIDE]
+  int* err = nullptr;      // XCD check flag
   const uint16_t* res = nullptr;
   uint16_t* h = nullptr;
   int64_t ld = 0;
@@ -1104,7 +1028,7 @@ int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* 
       return GRPO_EUNSUPPORTED;
     }
     const int groups = pl.NT / WPG;
-    if (!fin->cnt || !fin->res || !fin->h || !fin->ss || (h.r > 0 && !fin->tpart))
+    if (!fin->cnt || !fin->err || !fin->res || !fin->h || !fin->ss || (h.r > 0 && !fin->tpart))
       return einval("null pointer");
     if (fin->ld < h.N || fin->ld % 4 || !aligned8(fin->res) || !aligned8(fin->h))
       return einval("residual/h: ld must be >= N and a multiple of 4, rows 8-byte aligned");
@@ -1113,6 +1037,7 @@ int run_partials(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* 
     a.ntiles = pl.NT;
     a.fin_tpart = fin->tpart;
     a.fin_cnt = fin->cnt;
+    a.fin_err = fin->err;
     a.fin_res = fin->res;
     a.fin_h = fin->h;
     a.fin_ld = fin->ld;
@@ -1227,12 +1152,12 @@ struct GuArgs {
   // x = RMSNorm(h) from per-group sums of squares, when nh is set (units kernel, M <= 8)
   const uint16_t* nh;
   int64_t ldnh;
-  const float* nss;  // [M][nG], nG <= 64
+  const float* nss;  // [M][nG], nG % 4 == 0, nG <= GU_NORM_MAX_GROUPS, rows 16-byte aligned
   int nG;
   const uint16_t* nw;
   float neps;
 };
-constexpr int GU_NORM_MAX_GROUPS = 32;  // sums of squares per row (8 lanes x 4)
+constexpr int GU_NORM_MAX_GROUPS = 256;  // sums of squares per row (8 lanes x 8 float4)
 
 // Position of element e (0..7) of an 8-element chunk in the decode8 order
 // [0, 2, 4, 6, 1, 3, 5, 7].
@@ -1423,11 +1348,13 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
   // RMSNorm source (NORM): every wave holds the group sums of squares of all
   // rows, lane l those of row l / 8 (groups l % 8, l % 8 + 8); loaded first,
   // unconditionally (clamped indexes, dropped in the sum)
-  float ssv[GU_NORM_MAX_GROUPS / 8];
+  // (four groups per float4 load: lane l takes float4s l % 8, l % 8 + 8, ...)
+  float4 ssv[GU_NORM_MAX_GROUPS / 32];
   if (NORM) {
-    const float* ssr = p.nss + (int64_t)min(lane >> 3, p.M - 1) * p.nG;
+    const float4* ssr = reinterpret_cast<const float4*>(p.nss + (int64_t)min(lane >> 3, p.M - 1) * p.nG);
 #pragma unroll
-    for (int q = 0; q < GU_NORM_MAX_GROUPS / 8; ++q) ssv[q] = ssr[min((lane & 7) + 8 * q, p.nG - 1)];
+    for (int q = 0; q < GU_NORM_MAX_GROUPS / 32; ++q)
+      ssv[q] = ssr[min((lane & 7) + 8 * q, (p.nG >> 2) - 1)];
   }
   const uint16_t* xsrc = NORM ? p.nh : p.x;
   const int64_t xld = NORM ? p.ldnh : p.ldx;
@@ -1469,7 +1396,8 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
   if (NORM) {
     float ss = 0.f;
 #pragma unroll
-    for (int q = 0; q < GU_NORM_MAX_GROUPS / 8; ++q) ss += (lane & 7) + 8 * q < p.nG ? ssv[q] : 0.f;
+    for (int q = 0; q < GU_NORM_MAX_GROUPS / 32; ++q)
+      if ((lane & 7) + 8 * q < (p.nG >> 2)) ss += (ssv[q].x + ssv[q].y) + (ssv[q].z + ssv[q].w);
     ss = sum8(ss);
     inv_l = 1.f / sqrtf(ss / (float)p.K + p.neps);
   }
@@ -2330,11 +2258,12 @@ extern "C" int grpo_nf4_linear_attn_residual(
     const void* attn_workspace, const int32_t* context_lens, int Hq, int Hkv, int D,
     int block_size, int max_blocks, const uint8_t* w, const float* absmax, const float* code16,
     int blocksize, const void* const* lora_a, const grpo_linear_parts_t* parts,
-    float* group_tpart, int* counters, const void* residual, void* h_out, int64_t ld,
-    float* sumsq, grpo_stream_t stream) {
+    float* group_tpart, int* counters, int* xcd_err, const void* residual, void* h_out,
+    int64_t ld, float* sumsq, grpo_stream_t stream) {
   FinTarget fin;
   fin.tpart = group_tpart;
   fin.cnt = counters;
+  fin.err = xcd_err;
   fin.res = static_cast<const uint16_t*>(residual);
   fin.h = static_cast<uint16_t*>(h_out);
   fin.ld = ld;
@@ -2409,8 +2338,10 @@ extern "C" int grpo_nf4_gate_up_silu_tiles_norm(const void* h, int64_t ldh, cons
                                                 int M, void* act_tiles, grpo_stream_t stream) {
   if (M > 8) return einval("the fold tile layout holds at most 8 rows");
   if (!h || !sumsq || !norm_weight) return einval("null pointer");
-  if (groups < 1 || groups > GU_NORM_MAX_GROUPS) return einval("groups must be in [1, 32]");
-  if (!aligned16(norm_weight)) return einval("norm_weight must be 16-byte aligned");
+  if (groups < 4 || groups > GU_NORM_MAX_GROUPS || groups % 4)
+    return einval("groups must be a multiple of 4 in [4, 256]");
+  if (!aligned16(norm_weight) || !aligned16(sumsq))
+    return einval("norm_weight and sumsq must be 16-byte aligned");
   NormSource src;
   src.h = static_cast<const uint16_t*>(h);
   src.ldh = ldh;

@@ -41,6 +41,10 @@ constexpr int AT = 64 * AW;    // threads per workgroup
 constexpr int MAX_SPLITS = ATTN_MAX_SPLITS;  // context splits per (sequence, KV head)
 constexpr float LOG2E = 1.4426950408889634f;
 constexpr int ATTN_DEVICE_CUS = 256;  // MI355X
+// One merge counter per 128-byte line (a line is touched only by the splits
+// of one pair, which run on one XCD).
+constexpr int MERGE_CNT_STRIDE = 32;
+constexpr int NUM_XCD = 8;
 // K/V blocks: read once per launch, loaded with the non-temporal hint (see
 // load_w in nf4_linear.hip).
 __device__ __forceinline__ uint4 load_kv16(const uint16_t* p) { return load_stream(p); }
@@ -71,6 +75,19 @@ struct AttnArgs {
   // one split per (sequence, KV head): the split writes the normalised bf16
   // output [B][Hq][D] here instead of partials (null otherwise)
   uint16_t* direct_out;
+  // In-kernel merge (decode step, null otherwise): the split of each
+  // (sequence, KV head) that arrives last merges the pair's splits into the
+  // bf16 output mout [B][Hq * D]; counters [B * Hkv * MERGE_CNT_STRIDE]
+  // (zero, left zero), xcd_err set when a pair's splits did not share an XCD.
+  int* mcnt;
+  int* xcd_err;
+  uint16_t* mout;
+  // ... and, with lora_r > 0, the pair's share of the next linear's LoRA-A
+  // product: lora_t[b][kvh][r] = sum over the pair's Hq / Hkv heads of
+  // mout[b, k] * lora_a[r][k] (float32; the consumer sums the Hkv shares)
+  const uint16_t* lora_a;  // [lora_r][Hq * D] bf16
+  int lora_r;
+  float* lora_t;           // [B][Hkv][16]
 };
 
 struct AttnPlan {
@@ -151,7 +168,11 @@ constexpr int QKV_SLICES_LARGE = 16;
 template <int GQ, bool FUSED, int MS = QKV_SLICES_SMALL>
 __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
   touch_kernargs<sizeof(AttnArgs)>();
-  const int s = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+  // grid (pairs padded to a multiple of 8, splits): the splits of a (sequence,
+  // KV head) pair have linear ids equal modulo 8, so they run on one XCD
+  const int pair = blockIdx.x;
+  if (pair >= p.B * p.Hkv) return;
+  const int s = blockIdx.y, b = pair / p.Hkv, kvh = pair - b * p.Hkv;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int ln = lane & 15, lg = lane >> 4;
@@ -454,6 +475,25 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
     }
   }
   __syncthreads();
+  // In-kernel merge (decode step): a pair whose whole context is this split
+  // writes its output directly; otherwise the split arriving last merges.
+  const bool merge = p.mcnt != nullptr;
+  const bool single = merge && nsplit == 1;
+  // LoRA-A rows of this thread's four columns k (the output's columns of
+  // head kvh * GQ + h, d4 .. d4 + 3), for the next linear's t: issued before
+  // they are needed (ranks past lora_r read rank 0, dropped in the sum)
+  const int mh = tid / (FD / 4), md4 = 4 * (tid - mh * (FD / 4));
+  const int64_t kcol = (int64_t)(kvh * GQ + mh) * FD + md4;
+  const bool lora = merge && p.lora_r > 0 && tid < GQ * (FD / 4);
+  uint2 arow[16];
+  auto load_lora_a = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r)
+      arow[r] = *reinterpret_cast<const uint2*>(p.lora_a + (int64_t)(r < p.lora_r ? r : 0) *
+                                                               p.Hq * FD + kcol);
+  };
+  if (single && lora) load_lora_a();
+  float xr[4] = {0.f, 0.f, 0.f, 0.f};  // this thread's bf16 output values (merge)
   // Four columns of one head per thread: the split's max M and the waves'
   // weights 2^(m_w - M) computed by every thread of the head (no second
   // barrier behind a per-head pass), O summed in wave order; the head's first
@@ -479,20 +519,104 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
       O.z += f[w] * v.z;
       O.w += f[w] * v.w;
     }
-    if (!p.direct_out && d4 == 0) {
-      const int64_t slot = ((int64_t)b * p.Hq + kvh * GQ + h) * p.S + s;
-      p.ws_ml[slot * 2] = M;
-      p.ws_ml[slot * 2 + 1] = L;
-    }
-    if (p.direct_out) {
+    if (p.direct_out || single) {
       // the whole context in this split: out = O / max(L, 1e-6), bf16
       const float den = fmaxf(L, 1e-6f);
-      *reinterpret_cast<uint2*>(p.direct_out + ((int64_t)b * p.Hq + kvh * GQ + h) * FD + d4) =
-          make_uint2(pack_bf2(O.x / den, O.y / den), pack_bf2(O.z / den, O.w / den));
+      const uint2 ov = make_uint2(pack_bf2(O.x / den, O.y / den), pack_bf2(O.z / den, O.w / den));
+      uint16_t* dst = single ? p.mout : p.direct_out;
+      *reinterpret_cast<uint2*>(dst + ((int64_t)b * p.Hq + kvh * GQ + h) * FD + d4) = ov;
+      xr[0] = bf_lo(ov.x);
+      xr[1] = bf_hi(ov.x);
+      xr[2] = bf_lo(ov.y);
+      xr[3] = bf_hi(ov.y);
     } else {
       const int64_t slot = ((int64_t)b * p.Hq + kvh * GQ + h) * p.S + s;
+      if (d4 == 0) {
+        p.ws_ml[slot * 2] = M;
+        p.ws_ml[slot * 2 + 1] = L;
+      }
       *reinterpret_cast<float4*>(p.ws_o + slot * FD + d4) = O;
     }
+  }
+  if (!merge) return;
+  if (!single) {
+    // Arrival: this split's partials are in the XCD's L2 once its stores are
+    // acknowledged (the vector L1 writes through); the pair's counter is an
+    // L2 atomic (xcd_arrive: checks that the pair's splits share an XCD).
+    // The last of the nsplit splits drops its L1 lines and merges:
+    // out = sum_s 2^(m_s - M) O_s / max(sum_s 2^(m_s - M) l_s, 1e-6).
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ int s_last;
+    if (tid == 0)
+      s_last = xcd_arrive(p.mcnt + (int64_t)(b * p.Hkv + kvh) * MERGE_CNT_STRIDE, nsplit,
+                          p.xcd_err);
+    __syncthreads();
+    if (!s_last) return;
+    asm volatile("buffer_inv sc0" ::: "memory");
+    if (tid < GQ * (FD / 4)) {
+      const int64_t base = ((int64_t)b * p.Hq + kvh * GQ + mh) * p.S;
+      float2 ml[MAX_SPLITS];
+      float4 ov[MAX_SPLITS];
+#pragma unroll
+      for (int q = 0; q < MAX_SPLITS; ++q)
+        if (q < nsplit) {
+          ml[q] = *reinterpret_cast<const float2*>(p.ws_ml + (base + q) * 2);
+          ov[q] = *reinterpret_cast<const float4*>(p.ws_o + (base + q) * FD + md4);
+        }
+      if (lora) load_lora_a();
+      float M = -INFINITY;
+#pragma unroll
+      for (int q = 0; q < MAX_SPLITS; ++q)
+        if (q < nsplit) M = fmaxf(M, ml[q].x);
+      float L = 0.f;
+      float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (M != -INFINITY) {
+#pragma unroll
+        for (int q = 0; q < MAX_SPLITS; ++q)
+          if (q < nsplit) {
+            const float w = exp2f(ml[q].x - M);
+            L += w * ml[q].y;
+            O.x += w * ov[q].x;
+            O.y += w * ov[q].y;
+            O.z += w * ov[q].z;
+            O.w += w * ov[q].w;
+          }
+      }
+      const float den = fmaxf(L, 1e-6f);
+      const uint2 o2 = make_uint2(pack_bf2(O.x / den, O.y / den), pack_bf2(O.z / den, O.w / den));
+      *reinterpret_cast<uint2*>(p.mout + ((int64_t)b * p.Hq + kvh * GQ + mh) * FD + md4) = o2;
+      xr[0] = bf_lo(o2.x);
+      xr[1] = bf_hi(o2.x);
+      xr[2] = bf_lo(o2.y);
+      xr[3] = bf_hi(o2.y);
+    }
+  }
+  if (p.lora_r <= 0) return;
+  // The pair's share of t = out . A^T: per rank, the thread's four products,
+  // summed over each wave (DPP) and then over the waves in order.
+  __shared__ float sT[AW][16];
+  float tp[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float v = 0.f;
+    if (lora && r < p.lora_r) {
+      v = xr[0] * bf_lo(arow[r].x) + xr[1] * bf_hi(arow[r].x) + xr[2] * bf_lo(arow[r].y) +
+          xr[3] * bf_hi(arow[r].y);
+    }
+    tp[r] = wave_sum_dpp(v);
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sT[wave][r] = tp[r];
+  }
+  __syncthreads();
+  if (tid < 16) {
+    constexpr int TW = (GQ * (FD / 4) + 63) / 64;  // waves holding columns
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < TW; ++w) t += sT[w][tid];
+    p.lora_t[((int64_t)b * p.Hkv + kvh) * 16 + tid] = t;
   }
 }
 
@@ -647,7 +771,7 @@ int launch_split(const AttnArgs& a, hipStream_t st) {
   // then the split's block-table slice
   const size_t lds = (size_t)AW * GQ * FD * sizeof(float) + (size_t)a.bps * sizeof(int);
   if (lds > 65536) return einval("context too long for the split attention kernel");
-  const dim3 grid(a.S, a.Hkv, a.B);
+  const dim3 grid((unsigned)(cdiv((int64_t)a.B * a.Hkv, NUM_XCD) * NUM_XCD), (unsigned)a.S);
   if constexpr (FUSED) {
     if (a.qkv.S > QKV_SLICES_SMALL) {
       paged_attn_split<GQ, FUSED, QKV_SLICES_LARGE><<<grid, AT, lds, st>>>(a);
@@ -763,15 +887,24 @@ extern "C" int grpo_paged_attn_decode(const void* q, int64_t q_stride_b, int64_t
   return launch_check("paged_attn_generic");
 }
 
-extern "C" int grpo_paged_attn_decode_qkv(const grpo_linear_parts_t* qkv, int Hq, int Hkv, int D,
-                                          const void* cos_table, const void* sin_table,
-                                          int max_pos, const int32_t* append_pos,
-                                          const int32_t* context_lens, void* k_cache,
-                                          void* v_cache, int64_t num_blocks,
-                                          const int32_t* block_tables, int64_t bt_stride,
-                                          int block_size, int max_blocks, float scale,
-                                          void* workspace, size_t workspace_bytes, void* out,
-                                          grpo_stream_t stream) {
+namespace {
+
+// In-kernel merge target of the decode-step attention (all-null: none).
+struct MergeTarget {
+  int* cnt = nullptr;
+  int* err = nullptr;
+  uint16_t* out = nullptr;
+  const uint16_t* lora_a = nullptr;
+  int lora_r = 0;
+  float* lora_t = nullptr;
+};
+
+int run_attn_qkv(const grpo_linear_parts_t* qkv, int Hq, int Hkv, int D, const void* cos_table,
+                 const void* sin_table, int max_pos, const int32_t* append_pos,
+                 const int32_t* context_lens, void* k_cache, void* v_cache, int64_t num_blocks,
+                 const int32_t* block_tables, int64_t bt_stride, int block_size, int max_blocks,
+                 float scale, void* workspace, size_t workspace_bytes, void* out,
+                 const MergeTarget& mg, grpo_stream_t stream) {
   AttnArgs a{};
   if (int rc = make_parts(qkv, &a.qkv)) return rc;
   if (Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || max_blocks <= 0 || num_blocks < 0 || max_pos <= 0)
@@ -818,8 +951,63 @@ extern "C" int grpo_paged_attn_decode_qkv(const grpo_linear_parts_t* qkv, int Hq
   } else if (int rc = use_workspace(a, plan, workspace, workspace_bytes)) {
     return rc;
   }
+  if (mg.cnt) {
+    if (!mg.out || !mg.err) return einval("null pointer");
+    if ((reinterpret_cast<uintptr_t>(mg.out) & 7u) != 0) return einval("out must be 8-byte aligned");
+    if (mg.lora_r < 0 || mg.lora_r > 16) return einval("LoRA rank must be in [0, 16]");
+    if (mg.lora_r > 0 && (!mg.lora_a || !mg.lora_t || !aligned8(mg.lora_a)))
+      return einval("LoRA rank > 0 needs lora_a (8-byte aligned) and lora_t");
+    a.mcnt = mg.cnt;
+    a.xcd_err = mg.err;
+    a.mout = mg.out;
+    a.lora_a = mg.lora_a;
+    a.lora_r = mg.lora_r;
+    a.lora_t = mg.lora_t;
+  }
   return launch_split_gq<true>(a, as_stream(stream));
 }
+
+}  // namespace
+
+extern "C" int grpo_paged_attn_decode_qkv(const grpo_linear_parts_t* qkv, int Hq, int Hkv, int D,
+                                          const void* cos_table, const void* sin_table,
+                                          int max_pos, const int32_t* append_pos,
+                                          const int32_t* context_lens, void* k_cache,
+                                          void* v_cache, int64_t num_blocks,
+                                          const int32_t* block_tables, int64_t bt_stride,
+                                          int block_size, int max_blocks, float scale,
+                                          void* workspace, size_t workspace_bytes, void* out,
+                                          grpo_stream_t stream) {
+  return run_attn_qkv(qkv, Hq, Hkv, D, cos_table, sin_table, max_pos, append_pos, context_lens,
+                      k_cache, v_cache, num_blocks, block_tables, bt_stride, block_size,
+                      max_blocks, scale, workspace, workspace_bytes, out, MergeTarget{}, stream);
+}
+
+extern "C" size_t grpo_paged_attn_merge_counter_bytes(int B, int Hkv) {
+  return B > 0 && Hkv > 0 ? (size_t)B * Hkv * MERGE_CNT_STRIDE * sizeof(int) : 0;
+}
+
+extern "C" int grpo_paged_attn_decode_qkv_merged(
+    const grpo_linear_parts_t* qkv, int Hq, int Hkv, int D, const void* cos_table,
+    const void* sin_table, int max_pos, const int32_t* append_pos, const int32_t* context_lens,
+    void* k_cache, void* v_cache, int64_t num_blocks, const int32_t* block_tables,
+    int64_t bt_stride, int block_size, int max_blocks, float scale, void* workspace,
+    size_t workspace_bytes, int* counters, int* xcd_err, void* out, const void* o_lora_a,
+    int o_lora_r, float* o_lora_t, grpo_stream_t stream) {
+  if (!counters) return einval("null counters");
+  MergeTarget mg;
+  mg.cnt = counters;
+  mg.err = xcd_err;
+  mg.out = static_cast<uint16_t*>(out);
+  mg.lora_a = static_cast<const uint16_t*>(o_lora_a);
+  mg.lora_r = o_lora_r;
+  mg.lora_t = o_lora_t;
+  return run_attn_qkv(qkv, Hq, Hkv, D, cos_table, sin_table, max_pos, append_pos, context_lens,
+                      k_cache, v_cache, num_blocks, block_tables, bt_stride, block_size,
+                      max_blocks, scale, workspace, workspace_bytes, nullptr, mg, stream);
+}
+
+extern "C" int grpo_paged_attn_qkv_max_slices(void) { return QKV_SLICES_LARGE; }
 
 extern "C" int grpo_paged_attn_splits(int B, int Hq, int Hkv, int D, int block_size,
                                       int max_blocks) {

@@ -44,6 +44,29 @@ class LinearParts(ctypes.Structure):
 
 _PARTS = ctypes.POINTER(LinearParts)
 
+
+class TileLinear(ctypes.Structure):
+    """``grpo_tile_linear_t``: one NF4 (+ LoRA, + bias) linear finished in one
+    launch (device pointers for lora_a, lora_b and bias)."""
+
+    _fields_ = [
+        ("M", _I32),
+        ("N", _I32),
+        ("K", _I32),
+        ("nseg", _I32),
+        ("r", _I32),
+        ("seg_end", _I32 * MAX_SEGMENTS),
+        ("lora_a", _VP * MAX_SEGMENTS),
+        ("lora_b", _VP * MAX_SEGMENTS),
+        ("bias", _VP * MAX_SEGMENTS),
+        ("scaling", _F32),
+        ("lora_t", _VP),
+        ("lora_t_parts", _I32),
+    ]
+
+
+_TILE = ctypes.POINTER(TileLinear)
+
 # name -> (restype, argtypes); mirrors include/grpo_hip.h one to one.
 SIGNATURES = {
     "grpo_version": (_I32, []),
@@ -113,6 +136,13 @@ SIGNATURES = {
          _I32, _F32, _VP, _SZ, _VP, _VP],
     ),
     "grpo_paged_attn_splits": (_I32, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "grpo_paged_attn_qkv_max_slices": (_I32, []),
+    "grpo_paged_attn_merge_counter_bytes": (_SZ, [_I32, _I32]),
+    "grpo_paged_attn_decode_qkv_merged": (
+        _I32,
+        [_PARTS, _I32, _I32, _I32, _VP, _VP, _I32, _VP, _VP, _VP, _VP, _I64, _VP, _I64, _I32,
+         _I32, _F32, _VP, _SZ, _VP, _VP, _VP, _VP, _I32, _VP, _VP],
+    ),
     "grpo_nf4_linear_partials_silu": (_I32, [_PARTS, _VP, _VP, _VP, _I32, _PARTS, _VP]),
     "grpo_nf4_gate_up_silu": (
         _I32, [_VP, _I64, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _I64, _VP]),
@@ -146,7 +176,7 @@ SIGNATURES = {
     "grpo_nf4_linear_attn_residual": (
         _I32,
         [_VP, _VP, _I32, _I32, _I32, _I32, _I32, _VP, _VP, _VP, _I32, _VP, _PARTS, _VP, _VP,
-         _VP, _VP, _I64, _VP, _VP],
+         _VP, _VP, _VP, _I64, _VP, _VP],
     ),
     "grpo_nf4_linear_attn_residual_groups": (
         _I32, [_I32, _I32, _I32, _I32, _I32, _VP, _VP]),
@@ -157,6 +187,16 @@ SIGNATURES = {
     ),
     "grpo_paged_attn_merge": (_I32, [_VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32, _VP, _I32,
                                      _VP]),
+    "grpo_nf4_tile_supported": (_I32, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "grpo_nf4_tile_norm_supported": (_I32, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "grpo_nf4_tile_sumsq_groups": (_I32, [_I32, _I32, _I32, _I32, _I32]),
+    "grpo_nf4_tile_packed_lora_a_bytes": (_SZ, [_I32]),
+    "grpo_nf4_tile_pack_lora_a": (_I32, [_VP, _I32, _I32, _I64, _VP, _VP]),
+    "grpo_nf4_tile_linear": (_I32, [_VP, _I64, _VP, _VP, _VP, _I32, _TILE, _VP, _I64, _VP]),
+    "grpo_nf4_tile_linear_norm": (
+        _I32, [_VP, _I64, _VP, _I32, _VP, _F32, _VP, _VP, _VP, _I32, _TILE, _VP, _I64, _VP]),
+    "grpo_nf4_tile_linear_residual": (
+        _I32, [_VP, _I64, _VP, _VP, _VP, _I32, _TILE, _VP, _VP, _I64, _VP, _VP]),
     "grpo_paged_attn_noalloc_max_bytes": (_SZ, []),
     "grpo_paged_attn_decode_noalloc": (
         _I32,

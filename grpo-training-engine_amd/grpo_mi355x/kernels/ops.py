@@ -184,6 +184,107 @@ def nf4_lora_linear(x2d: torch.Tensor, packed: torch.Tensor, absmax: torch.Tenso
     return out
 
 
+def pack_lora_a(a: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """LoRA A [r, K] bf16 in the MFMA order the one-launch linear reads
+    (``grpo_nf4_tile_pack_lora_a``); valid until A changes."""
+    lib = _lib.device_library()
+    _need_cuda(a)
+    _need_dtype(a, torch.bfloat16, "lora_A")
+    r, k = a.shape
+    a = a.contiguous()
+    nbytes = int(lib.grpo_nf4_tile_packed_lora_a_bytes(k))
+    if out is None:
+        out = torch.empty(nbytes // 2, dtype=torch.bfloat16, device=a.device)
+    elif out.numel() * out.element_size() < nbytes:
+        raise ValueError(f"packed LoRA A needs {nbytes} bytes.")
+    _lib.check(lib.grpo_nf4_tile_pack_lora_a(a.data_ptr(), r, k, k, out.data_ptr(),
+                                             _lib.stream_handle(a.device)), "pack_lora_a")
+    return out
+
+
+def tile_linear_desc(m: int, k: int, seg_rows, biases=None, lora_a=None, lora_b=None,
+                     scaling: float = 1.0):
+    """``grpo_tile_linear_t`` of an [M, K] x [N = sum(seg_rows), K] NF4 linear:
+    per segment an optional bf16 bias and LoRA A [r, K] / B [rows, r] (device
+    tensors, kept referenced by the returned descriptor)."""
+    d = _lib.TileLinear()
+    d.M, d.K, d.nseg = m, k, len(seg_rows)
+    if not 1 <= d.nseg <= _lib.MAX_SEGMENTS:
+        raise ValueError(f"1..{_lib.MAX_SEGMENTS} segments, got {d.nseg}.")
+    keep = []
+    end, r = 0, 0
+    for i, rows in enumerate(seg_rows):
+        end += int(rows)
+        d.seg_end[i] = end
+        if biases is not None and biases[i] is not None:
+            b = biases[i].to(torch.bfloat16).contiguous()
+            if b.numel() != rows:
+                raise ValueError(f"bias {i} must have {rows} elements.")
+            keep.append(b)
+            d.bias[i] = b.data_ptr()
+        if lora_a is not None:
+            a, bb = lora_a[i].contiguous(), lora_b[i].contiguous()
+            r = a.shape[0]
+            if a.shape != (r, k) or bb.shape != (rows, r):
+                raise ValueError("lora_A must be [r, K] and lora_B [rows, r] per segment.")
+            _need_dtype(a, torch.bfloat16, "lora_A")
+            _need_dtype(bb, torch.bfloat16, "lora_B")
+            ap = pack_lora_a(a)
+            keep += [ap, bb]
+            d.lora_a[i], d.lora_b[i] = ap.data_ptr(), bb.data_ptr()
+    d.N, d.r, d.scaling = end, r, float(scaling)
+    d._keep = keep
+    return d
+
+
+def nf4_tile_linear(x: torch.Tensor, packed: torch.Tensor, absmax: torch.Tensor,
+                    code: torch.Tensor, blocksize: int, desc, out: torch.Tensor | None = None,
+                    norm: tuple | None = None, residual: torch.Tensor | None = None,
+                    sumsq: torch.Tensor | None = None) -> torch.Tensor:
+    """The one-launch NF4 (+ LoRA) linear (``grpo_nf4_tile_linear*``) for a
+    ``tile_linear_desc`` descriptor.
+
+    ``norm = (sumsq [M, G] float32, weight [K] bf16, eps)``: ``x`` is h and the
+    kernel stages RMSNorm(h).  ``residual`` ([M, N] bf16, may be ``out``):
+    ``out = bf16(residual + y)`` and ``sumsq`` ([M, G] float32, G =
+    ``grpo_nf4_tile_sumsq_groups``) receives the per-group sums of ``out**2``."""
+    lib = _lib.device_library()
+    _need_cuda(x, packed, absmax, code, out, residual, sumsq)
+    _need_dtype(x, torch.bfloat16, "x")
+    m, n, k = desc.M, desc.N, desc.K
+    if x.ndim != 2 or x.shape != (m, k) or x.stride(1) != 1:
+        raise ValueError(f"x must be [{m}, {k}] with unit column stride.")
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.bfloat16, device=x.device)
+    if out.shape != (m, n) or out.stride(1) != 1 or out.dtype != torch.bfloat16:
+        raise ValueError("out must be a bf16 [M, N] tensor with unit column stride.")
+    st = _lib.stream_handle(x.device)
+    args = (packed.data_ptr(), absmax.data_ptr(), code.data_ptr(), int(blocksize),
+            ctypes_byref(desc))
+    if norm is not None:
+        ss, w, eps = norm
+        rc = lib.grpo_nf4_tile_linear_norm(x.data_ptr(), x.stride(0), ss.data_ptr(), ss.shape[1],
+                                           w.data_ptr(), float(eps), *args, out.data_ptr(),
+                                           out.stride(0), st)
+    elif residual is not None:
+        if sumsq is None or residual.stride() != out.stride():
+            raise ValueError("residual needs sumsq and the row stride of out.")
+        rc = lib.grpo_nf4_tile_linear_residual(x.data_ptr(), x.stride(0), *args,
+                                               residual.data_ptr(), out.data_ptr(), out.stride(0),
+                                               sumsq.data_ptr(), st)
+    else:
+        rc = lib.grpo_nf4_tile_linear(x.data_ptr(), x.stride(0), *args, out.data_ptr(),
+                                      out.stride(0), st)
+    _lib.check(rc, "grpo_nf4_tile_linear")
+    return out
+
+
+def ctypes_byref(obj):
+    import ctypes
+
+    return ctypes.byref(obj)
+
+
 def nf4_linear_plan(m: int, n: int, k: int, r: int, nseg: int,
                     blocksize: int) -> tuple[int, int, int] | None:
     """(splits, part_bytes, tpart_bytes) of the split-K path, or None if the

@@ -181,6 +181,14 @@ class DecodeEngine:
             B, Hq, self.Hkv, D, self.pool.block_size, self.max_blocks), 1), dev)
         self.attn_splits = int(self.lib.grpo_paged_attn_splits(
             B, Hq, self.Hkv, D, self.pool.block_size, self.max_blocks))
+        # the fused attention prologue finishes q|k|v from at most this many K
+        # slices; a plan with more takes the unfused launches (append, then
+        # attention over the finished q, then o_proj from its bf16 rows)
+        self.attn_fused = (self.attn_splits > 0 and plans["qkv"][0]
+                           <= int(self.lib.grpo_paged_attn_qkv_max_slices()))
+        if not self.attn_fused:
+            self.q_rot = torch.zeros(B, Hq, D, dtype=torch.bfloat16, device=dev)
+            self.attn_out = torch.zeros(B, Hq * D, dtype=torch.bfloat16, device=dev)
         self.plans = plans
         # bf16 lm_head GEMV with fused argmax + device-side row advance (x staged
         # whole in LDS, or in K chunks past 160 KiB); otherwise hipBLASLt +
@@ -212,17 +220,63 @@ class DecodeEngine:
         # The post-attention norm likewise: o_proj's epilogue + residual add +
         # per-256-column sums of squares over N / 256 workgroups per row, and
         # gate|up stages the norm.
-        self.fold = (self.FOLD_DOWN and self.gu_fused and H % 8 == 0
-                     and H // 8 <= self.NORM_MAX_GROUPS and -(-H // 256) <= 16
+        self.fold = (self.FOLD_DOWN and self.gu_fused and H % 64 == 0
+                     and H // 8 <= self.NORM_MAX_GROUPS and H // 64 <= self.GU_NORM_MAX_GROUPS
                      and bool(self.lib.grpo_nf4_linear_residual_supported(B, H, I, bs))
                      and bool(self.lib.grpo_nf4_gate_up_silu_tiles_norm_supported(B, I, H, bs)))
         self.ss = torch.zeros(B, max(H // 8, 1), dtype=torch.float32, device=dev)
-        self.ss_post = torch.zeros(B, -(-H // 256), dtype=torch.float32, device=dev)
+        # the post-attention norm's statistic: per-64-column sums of squares of
+        # h from grpo_linear_finish_residual (or from the o_proj kernels below)
+        self.ss_post = torch.zeros(B, max(H // 64, 1), dtype=torch.float32, device=dev)
+        # XCD check word of the in-kernel hand-overs (attention merge, o_proj
+        # finish): zero, and zero after every run (verify_handover)
+        self.xcd_err = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.m_cnt = None
+        # o_proj as the one-launch tile linear (grpo_nf4_tile_linear_residual):
+        # the epilogue, the residual add and per-column-group sums of squares
+        # of h in the same launch, x = the attention's bf16 rows.  With
+        # attn_merge the attention merges its context splits in the kernel and
+        # also leaves o_proj's LoRA-A product (no launch between them);
+        # otherwise a merge launch writes the rows and the tile kernel
+        # multiplies by LoRA A itself (packed once per engine).
+        self.o_tile = False
+        self.attn_merge = False
+        if (self.fold and self.O_TILE and self.attn_fused
+                and bool(self.lib.grpo_nf4_tile_supported(B, H, Hq * D, r, 1, bs))):
+            G = int(self.lib.grpo_nf4_tile_sumsq_groups(B, H, Hq * D, r, bs))
+            if 0 < G <= self.GU_NORM_MAX_GROUPS and G % 4 == 0:
+                self.o_tile = True
+                self.ss_post = torch.zeros(B, G, dtype=torch.float32, device=dev)
+                self.attn_out = torch.zeros(B, Hq * D, dtype=torch.bfloat16, device=dev)
+                self.attn_merge = self.ATTN_MERGE and self.Hkv <= 4
+                if self.attn_merge:
+                    self.m_cnt = torch.zeros(
+                        int(self.lib.grpo_paged_attn_merge_counter_bytes(B, self.Hkv)) // 4,
+                        dtype=torch.int32, device=dev)
+                    self.o_lora_t = torch.zeros(B, self.Hkv, 16, dtype=torch.float32,
+                                                device=dev)
+                for L, layer in zip(self.layers, self.model.model.layers):
+                    o = layer.self_attn.o_proj
+                    d = _lib.TileLinear()
+                    d.M, d.N, d.K, d.nseg, d.r = B, H, Hq * D, 1, o.rank
+                    d.seg_end[0] = H
+                    d.scaling = float(o.scaling)
+                    if o.rank > 0:
+                        d.lora_b[0] = o.lora_B.weight.data_ptr()
+                        if self.attn_merge:
+                            d.lora_t, d.lora_t_parts = self.o_lora_t.data_ptr(), self.Hkv
+                        else:
+                            L["o_la_packed"] = ops.pack_lora_a(o.lora_A.weight)
+                            d.lora_a[0] = L["o_la_packed"].data_ptr()
+                    L["o_tile"] = d
+                    L["o_la_rows"] = o.lora_A.weight
+                    self._keep.append(d)
         # o_proj finishing its own columns (the K slice of each 64-column group
         # that ends last adds the epilogue and the residual, and writes the
         # group's sums of squares): no separate finish launch
         self.o_fin = False
-        if self.fold and self.O_FIN and B <= self.ATTN_STAGE_MAX_ROWS:
+        if (self.fold and self.O_FIN and self.attn_fused and not self.o_tile
+                and B <= self.ATTN_STAGE_MAX_ROWS):
             tb, cb = ctypes.c_size_t(0), ctypes.c_size_t(0)
             G = int(self.lib.grpo_nf4_linear_attn_residual_groups(
                 B, H, Hq * D, r, bs, ctypes.byref(tb), ctypes.byref(cb)))
@@ -250,9 +304,16 @@ class DecodeEngine:
         if self.fold:
             # weight + absmax + x + residual read + h written + sums of squares
             self.bytes["down"] = nf4(H, I) + B * I * 2 + 2 * B * H * 2 + B * (H // 8) * 4
-        if self.o_fin:
+        if self.o_fin or self.o_tile:
             # ... and o_proj's residual read, h written and sums of squares
             self.bytes["o"] += 2 * B * H * 2 + B * self.ss_post.shape[1] * 4
+        if self.o_tile:
+            # no partial sums: weight + absmax + x + LoRA (A, or its product
+            # from the attention) + B + residual, h and sums
+            n_, k_, rr, _ = shapes["o"]
+            self.bytes["o"] = (nf4(n_, k_) + B * k_ * 2 + rr * n_ * 2
+                               + (B * self.Hkv * 16 * 4 if self.attn_merge else rr * k_ * 2)
+                               + 2 * B * H * 2 + B * self.ss_post.shape[1] * 4)
 
     def splits(self, kind: str) -> int:
         """K slices of an NF4 launch kind (1 for the folded down_proj)."""
@@ -271,8 +332,19 @@ class DecodeEngine:
     # grpo_nf4_linear_residual + grpo_nf4_linear_partials_norm for <= 8 rows
     FOLD_DOWN = True
     NORM_MAX_GROUPS = 256  # sums of squares per row the q|k|v norm staging reads
-    GU_NORM_MAX_GROUPS = 32  # ... and the gate|up norm staging
-    # o_proj + its epilogue + residual add in one launch (<= 16 rows)
+    GU_NORM_MAX_GROUPS = 256  # ... and the gate|up norm staging
+    # o_proj as the one-launch tile linear (<= 8 rows, the fold path), after
+    # an attention that merges its splits in the kernel (ATTN_MERGE).  Off by
+    # default: at config 3 the attention's in-kernel merge and LoRA-A product
+    # cost 3.4 us per launch against 1.2 us saved in o_proj (3345 against
+    # 3503 tok/s); o_proj merging the splits while it stages x (O_FIN) is
+    # faster.  The in-kernel hand-overs are checked after every run
+    # (verify_handover), which switches ATTN_MERGE and O_FIN off for later
+    # engines if one fails.
+    O_TILE = False
+    ATTN_MERGE = True
+    # o_proj + its epilogue + residual add in one launch through the last
+    # K slice of each column group (<= 16 rows; used when O_TILE is off)
     O_FIN = True
     # lm_head weight read in the kernel's tile order
     LM_TILES = True
@@ -343,7 +415,7 @@ class DecodeEngine:
                 # gate|up staging RMSNorm(h) and writing act in the tile layout
                 # the folded down_proj loads
                 sp = self.ss_post.data_ptr()
-                if not self.o_fin:
+                if not (self.o_fin or self.o_tile):
                     out.append(("rmsnorm", lambda L=L, sp=sp: chk(
                         lib.grpo_linear_finish_residual(L["o_parts"], h, h, H, sp, st),
                         "post_finish")))
@@ -392,6 +464,8 @@ class DecodeEngine:
         """Attention of one layer: RoPE + K/V append of the step's token, paged
         GQA attention over pos + 1 tokens (split partials), o_proj NF4+LoRA
         partials merging the splits while staging x."""
+        if not self.attn_fused:
+            return self._attn_launches_unfused(L, kc, vc, st)
         lib, chk, pool = self.lib, _lib.check, self.pool
         Hq, Hkv, D = self.Hq, self.Hkv, self.D
         wsa, wsa_n = self.ws_attn.data_ptr(), self.ws_attn.numel()
@@ -416,6 +490,27 @@ class DecodeEngine:
                 ("o", lambda: chk(lib.grpo_nf4_linear_partials(
                     ao, Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
                     L["o_code"].data_ptr(), self.bs, L["o_la"], L["o_parts"], st), "o_proj"))]
+        if self.o_tile:
+            h, ao = self.h.data_ptr(), self.attn_out.data_ptr()
+            o_tile = ("o", lambda: chk(lib.grpo_nf4_tile_linear_residual(
+                ao, Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
+                L["o_code"].data_ptr(), self.bs, ctypes.byref(L["o_tile"]), h, h, self.H,
+                self.ss_post.data_ptr(), st), "o_proj"))
+            if self.attn_merge:
+                la = L["o_la_rows"]
+                merged = ("attention", lambda: chk(lib.grpo_paged_attn_decode_qkv_merged(
+                    L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
+                    self.max_pos, self.append_pos.data_ptr(), self.attn_len.data_ptr(), kc, vc,
+                    pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
+                    pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n,
+                    self.m_cnt.data_ptr(), self.xcd_err.data_ptr(), ao,
+                    la.data_ptr() if L["o_tile"].r > 0 else None, L["o_tile"].r,
+                    self.o_lora_t.data_ptr(), st), "attention"))
+                return [merged, o_tile]
+            merge = ("attn_merge", lambda: chk(lib.grpo_paged_attn_merge(
+                wsa, self.attn_len.data_ptr(), self.B, Hq, Hkv, D, pool.block_size,
+                self.max_blocks, ao, 1, st), "attn_merge"))
+            return [attention, merge, o_tile]
         if self.o_fin:
             h = self.h.data_ptr()
             return [
@@ -424,14 +519,37 @@ class DecodeEngine:
                     wsa, self.attn_len.data_ptr(), Hq, Hkv, D, pool.block_size, self.max_blocks,
                     L["o_w"].data_ptr(), L["o_absmax"].data_ptr(), L["o_code"].data_ptr(),
                     self.bs, L["o_la"], L["o_parts"], self.o_tpart.data_ptr(),
-                    self.o_cnt.data_ptr(), h, h, self.H, self.ss_post.data_ptr(), st),
-                    "o_proj"))]
+                    self.o_cnt.data_ptr(), self.xcd_err.data_ptr(), h, h, self.H,
+                    self.ss_post.data_ptr(), st), "o_proj"))]
         return [
             attention,
             ("o", lambda: chk(lib.grpo_nf4_linear_partials_attn(
                 wsa, self.attn_len.data_ptr(), Hq, Hkv, D, pool.block_size, self.max_blocks,
                 L["o_w"].data_ptr(), L["o_absmax"].data_ptr(), L["o_code"].data_ptr(), self.bs,
                 L["o_la"], L["o_parts"], st), "o_proj"))]
+
+    def _attn_launches_unfused(self, L: dict, kc: int, vc: int, st) -> list:
+        """Append (q|k|v finished from the partial sums, RoPE, K/V to the cache)
+        as a launch of its own, attention over the rotated q (bf16 rows), o_proj
+        partial sums from those rows."""
+        lib, chk, pool = self.lib, _lib.check, self.pool
+        Hq, Hkv, D = self.Hq, self.Hkv, self.D
+        wsa, wsa_n = self.ws_attn.data_ptr(), self.ws_attn.numel()
+        q, o = self.q_rot.data_ptr(), self.attn_out.data_ptr()
+        return [
+            ("append", lambda: chk(lib.grpo_qkv_rope_append_parts(
+                L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
+                self.max_pos, self.append_pos.data_ptr(), q, kc, vc, pool.num_blocks,
+                self.block_tables.data_ptr(), self.max_blocks, pool.block_size,
+                self.max_blocks, st), "append")),
+            ("attention", lambda: chk(lib.grpo_paged_attn_decode(
+                q, Hq * D, D, kc, vc, pool.num_blocks, self.block_tables.data_ptr(),
+                self.max_blocks, self.attn_len.data_ptr(), o, 1, self.B, Hq, Hkv, D,
+                pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n, st),
+                "attention")),
+            ("o", lambda: chk(lib.grpo_nf4_linear_partials(
+                o, Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
+                L["o_code"].data_ptr(), self.bs, L["o_la"], L["o_parts"], st), "o_proj"))]
 
     def _head_launches(self, prev: dict, st) -> list:
         """Final norm, lm_head and the token choice with the row advance."""
@@ -605,6 +723,28 @@ class DecodeEngine:
             self.generated.fill_(int(self.pad.item()))
         self._masks()
 
+    def verify_handover(self):
+        """Check the in-kernel hand-overs of the steps run so far (host sync).
+
+        The attention's split merge and o_proj's in-kernel finish hand partial
+        results to the last-arriving workgroup of a group through an L2 counter,
+        which is correct only when the group's workgroups ran on one XCD.  The
+        kernels flag a group that did not (``xcd_err``), and such a group leaves
+        its counter non-zero.  Either means the outputs of the run are not
+        valid: this raises ``RuntimeError`` and switches the in-kernel
+        hand-overs off (``ATTN_MERGE``, ``O_FIN``) for engines built later, which
+        then take the launches that need no hand-over."""
+        bad = int(self.xcd_err.item()) != 0
+        for cnt in (self.m_cnt, getattr(self, "o_cnt", None) if self.o_fin else None):
+            if cnt is not None and bool((cnt != 0).any()):
+                bad = True
+        if bad:
+            DecodeEngine.ATTN_MERGE = False
+            DecodeEngine.O_FIN = False
+            raise RuntimeError("decode step: a group of workgroups that hands data over "
+                               "through L2 did not run on one XCD; the results of this run "
+                               "are not valid (in-kernel hand-overs now off; run again)")
+
     def step(self):
         if self.graph is not None:
             self.graph.replay()
@@ -668,6 +808,7 @@ class DecodeEngine:
         for b in list(live):  # rows cut off by max_steps
             pool.free(live.pop(b))
             self.block_tables[b].fill_(-1)
+        self.verify_handover()
         return dict(steps=steps, peak_blocks=peak)
 
 
@@ -686,8 +827,9 @@ class PrefillEngine(DecodeEngine):
     cache.  The pass is captured once into a HIP graph; rows past the end of a
     short last chunk are masked (slot -1, length 0).
     """
-    # o_proj stages the bf16 attention output here (no in-kernel finish)
+    # o_proj partial sums from the bf16 attention output (no in-kernel finish)
     O_FIN = False
+    O_TILE = False
 
     def __init__(self, model: Qwen2ForCausalLM, pool: PagedKVPool, chunk: int, max_blocks: int,
                  max_pos: Optional[int] = None):
@@ -698,24 +840,7 @@ class PrefillEngine(DecodeEngine):
         self._rows = torch.arange(chunk, dtype=torch.int32, device=self.device)
 
     def _attn_launches(self, L: dict, kc: int, vc: int, st) -> list:
-        lib, chk, pool = self.lib, _lib.check, self.pool
-        Hq, Hkv, D = self.Hq, self.Hkv, self.D
-        wsa, wsa_n = self.ws_attn.data_ptr(), self.ws_attn.numel()
-        q, o = self.q_rot.data_ptr(), self.attn_out.data_ptr()
-        return [
-            ("append", lambda: chk(lib.grpo_qkv_rope_append_parts(
-                L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
-                self.max_pos, self.append_pos.data_ptr(), q, kc, vc, pool.num_blocks,
-                self.block_tables.data_ptr(), self.max_blocks, pool.block_size,
-                self.max_blocks, st), "append")),
-            ("attention", lambda: chk(lib.grpo_paged_attn_decode(
-                q, Hq * D, D, kc, vc, pool.num_blocks, self.block_tables.data_ptr(),
-                self.max_blocks, self.attn_len.data_ptr(), o, 1, self.B, Hq, Hkv, D,
-                pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n, st),
-                "attention")),
-            ("o", lambda: chk(lib.grpo_nf4_linear_partials(
-                o, Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
-                L["o_code"].data_ptr(), self.bs, L["o_la"], L["o_parts"], st), "o_proj"))]
+        return self._attn_launches_unfused(L, kc, vc, st)
 
     def _head_launches(self, prev: dict, st) -> list:
         return []
@@ -789,7 +914,8 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
                           attention_mask: Optional[torch.Tensor] = None,
                           max_new_tokens: int = 128, do_sample: bool = False,
                           temperature: float = 1.0, top_p: float = 1.0,
-                          pad_token_id: int = 0, eos_token_id: Optional[int] = None,
+                          pad_token_id: Optional[int] = 0,
+                          eos_token_id: Optional[int] = None,
                           seed: Optional[int] = None, block_size: int = 16,
                           use_cache: Optional[bool] = None,
                           stop_lengths: Optional[list[int]] = None) -> torch.Tensor:
@@ -811,6 +937,8 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
     """
     if max_new_tokens <= 0:
         raise ValueError(f"max_new_tokens must be > 0, got {max_new_tokens}.")
+    if pad_token_id is None:  # as the low-level entry (paged_kv.py:876-877)
+        pad_token_id = 0
     if input_ids.ndim != 2 or input_ids.shape[1] == 0:
         raise ValueError("input_ids must be [batch, seq_len] with at least 1 token.")
     model = decode_model_from(model)

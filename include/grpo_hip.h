@@ -131,6 +131,87 @@ int grpo_nf4_linear_partials(const void* x, int64_t ldx, const uint8_t* w, const
 int grpo_nf4_linear_finish(const grpo_linear_parts_t* parts, void* y, int64_t ldy,
                            grpo_stream_t stream);
 
+/* ---- one-launch NF4 (+ LoRA) linear for decode batches (M <= 32) --------
+ *
+ * The fused forward of _lora_forward_kernel (lora_forward.py:107-260) with
+ * its epilogue, finished in ONE launch without partial sums: one workgroup
+ * per 16 output columns takes the whole of K (its waves split the k-steps and
+ * meet in LDS), stages all of x in LDS and multiplies it by the segment's
+ * LoRA A itself.  Same roundings as grpo_nf4_linear_finish:
+ * y = bf16(bf16(bf16(acc) + bias) + bf16(bf16(bf16(t) B^T) * bf16(scaling))).
+ * Shapes: M <= 32, N % 16 == 0, K % 256 == 0 with x [M, K] (+ 32 KiB per 16
+ * waves) within 160 KiB of LDS, segment ends multiples of 16, r <= 16,
+ * power-of-two blocksize >= 64 (grpo_nf4_tile_supported).  Up to 8 rows with
+ * K % 512 == 0 take 8 columns per workgroup (K folded into the MFMA's idle
+ * rows), otherwise 16.  lora_a / lora_b / bias are DEVICE pointers here;
+ * lora_a in the packed order of grpo_nf4_tile_pack_lora_a. */
+typedef struct grpo_tile_linear {
+  int M, N, K, nseg, r;
+  int seg_end[GRPO_MAX_SEGMENTS];         /* exclusive end row of each segment */
+  const void* lora_a[GRPO_MAX_SEGMENTS];  /* packed LoRA A when r > 0          */
+  const void* lora_b[GRPO_MAX_SEGMENTS];  /* bf16 [rows_s, r] when r > 0       */
+  const void* bias[GRPO_MAX_SEGMENTS];    /* bf16 [rows_s] or NULL             */
+  float scaling;                          /* LoRA alpha / r                    */
+  /* Optional (one segment, r > 0): x A^T given as float32 partial sums
+   * lora_t[m][q][16], q < lora_t_parts <= 4, which the kernel adds in order
+   * and rounds to bf16 instead of computing x A^T (lora_a unused): the
+   * attention of the decode step leaves them for o_proj
+   * (grpo_paged_attn_decode_qkv_merged). */
+  const float* lora_t;
+  int lora_t_parts;
+} grpo_tile_linear_t;
+
+/* 1 if the one-launch linear takes this shape, else 0 (_norm: with the
+ * RMSNorm source of grpo_nf4_tile_linear_norm, which also stages the norm
+ * weight in LDS). */
+int grpo_nf4_tile_supported(int M, int N, int K, int r, int nseg, int blocksize);
+int grpo_nf4_tile_norm_supported(int M, int N, int K, int r, int nseg, int blocksize);
+
+/* Column groups per row of the sumsq that grpo_nf4_tile_linear_residual
+ * writes for this shape (N / 8 or N / 16), 0 if the shape is not taken. */
+int grpo_nf4_tile_sumsq_groups(int M, int N, int K, int r, int blocksize);
+
+/* LoRA A [r <= 16, K] (bf16, row stride lda % 8 == 0, 16-byte aligned) in the
+ * order the one-launch linear reads it: for k-step s = k / 256 and j =
+ * (k % 64) / 8, the 16-byte B operands of one MFMA, lane = rank + 16 ((k %
+ * 256) / 64), are one contiguous KiB, 8 elements per lane in the decode8
+ * order [0,2,4,6,1,3,5,7], ranks >= r zero.  out: 16-byte aligned,
+ * grpo_nf4_tile_packed_lora_a_bytes(K) bytes.  A is frozen while it is used
+ * packed: repack after every update (the decode engine packs once per
+ * rollout). */
+size_t grpo_nf4_tile_packed_lora_a_bytes(int K);
+int grpo_nf4_tile_pack_lora_a(const void* lora_a, int r, int K, int64_t lda, void* out,
+                              grpo_stream_t stream);
+
+/* y[M, N] (bf16, row stride ldy) = the finished linear of x (bf16 [M, K], row
+ * stride ldx % 8 == 0, 16-byte aligned). */
+int grpo_nf4_tile_linear(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                         const float* code16, int blocksize, const grpo_tile_linear_t* lin,
+                         void* y, int64_t ldy, grpo_stream_t stream);
+
+/* grpo_nf4_tile_linear with x = RMSNorm(h) = bf16(bf16(h * inv) * norm_weight),
+ * inv = 1 / sqrt(sum_g sumsq[m, g] / K + eps) (groups: a multiple of 4, <= 256
+ * partial sums of h^2 per row, as grpo_nf4_linear_residual /
+ * grpo_embedding_sumsq / grpo_nf4_tile_linear_residual write them; sumsq rows
+ * and norm_weight 16-byte aligned): the q|k|v projection of _step with the
+ * layer's input norm (paged_kv.py:712-724). */
+int grpo_nf4_tile_linear_norm(const void* h, int64_t ldh, const float* sumsq, int groups,
+                              const void* norm_weight, float eps, const uint8_t* w,
+                              const float* absmax, const float* code16, int blocksize,
+                              const grpo_tile_linear_t* lin, void* y, int64_t ldy,
+                              grpo_stream_t stream);
+
+/* grpo_nf4_tile_linear followed by the decoder layer's residual add:
+ * h_out[m, n] = bf16(residual[m, n] + y[m, n]) (residual may alias h_out; row
+ * stride ld), and sumsq[m, g] = sum of h_out[m, n]^2 over the columns of
+ * group g (G = grpo_nf4_tile_sumsq_groups per row, N / G consecutive columns
+ * each) for the next RMSNorm: o_proj and the residual of _step
+ * (paged_kv.py:762-798). */
+int grpo_nf4_tile_linear_residual(const void* x, int64_t ldx, const uint8_t* w,
+                                  const float* absmax, const float* code16, int blocksize,
+                                  const grpo_tile_linear_t* lin, const void* residual,
+                                  void* h_out, int64_t ld, float* sumsq, grpo_stream_t stream);
+
 /* Workspace bytes of grpo_nf4_lora_linear[_grouped] for this shape (0 when
  * the shape takes the workspace-free generic kernel). */
 size_t grpo_nf4_lora_linear_workspace_bytes(int M, int N, int K, int r, int nseg, int blocksize);
@@ -257,6 +338,39 @@ int grpo_paged_attn_decode_qkv(const grpo_linear_parts_t* qkv, int Hq, int Hkv, 
                                int max_blocks, float scale, void* workspace,
                                size_t workspace_bytes, void* out, grpo_stream_t stream);
 
+/* grpo_paged_attn_decode_qkv that also merges its context splits: the split
+ * of each (sequence, KV head) pair that finishes last combines the pair's
+ * split partials (the normalisation of paged_kv.py:243-251) and writes the
+ * bf16 attention output out [B, Hq * D] (8-byte aligned), which o_proj reads
+ * as plain rows; a pair whose context fits one split writes it directly.
+ * With o_lora_r > 0 the same step leaves the LoRA-A product of o_proj's input
+ * in o_lora_t: float32 [B][Hkv][16], part kvh = sum over the pair's heads of
+ * out[b, k] * o_lora_a[r][k] (o_lora_a: bf16 [o_lora_r, Hq * D], 8-byte
+ * aligned), for grpo_tile_linear_t.lora_t.
+ * The hand-over runs through an L2 atomic counter per pair (counters: int32
+ * of grpo_paged_attn_merge_counter_bytes(B, Hkv), ZERO before the first call,
+ * left zero by every call) and relies on the pair's splits running on one
+ * XCD (they are launched with linear ids equal modulo 8); every arrival checks
+ * its XCD, and *xcd_err becomes 1 (else left as it is) when a pair's splits
+ * ran on two XCDs.  The caller checks that *xcd_err is 0 and the counters are
+ * zero after a run, or the outputs of that run are not valid.  Calls sharing
+ * the counters must not overlap. */
+size_t grpo_paged_attn_merge_counter_bytes(int B, int Hkv);
+int grpo_paged_attn_decode_qkv_merged(const grpo_linear_parts_t* qkv, int Hq, int Hkv, int D,
+                                      const void* cos_table, const void* sin_table, int max_pos,
+                                      const int32_t* append_pos, const int32_t* context_lens,
+                                      void* k_cache, void* v_cache, int64_t num_blocks,
+                                      const int32_t* block_tables, int64_t bt_stride,
+                                      int block_size, int max_blocks, float scale,
+                                      void* workspace, size_t workspace_bytes, int* counters,
+                                      int* xcd_err, void* out, const void* o_lora_a,
+                                      int o_lora_r, float* o_lora_t, grpo_stream_t stream);
+
+/* Most K slices of the q|k|v partial sums that grpo_paged_attn_decode_qkv[_merged]
+ * reads (parts->splits above it returns GRPO_EUNSUPPORTED: finish q|k|v with
+ * grpo_qkv_rope_append_parts and run grpo_paged_attn_decode instead). */
+int grpo_paged_attn_qkv_max_slices(void);
+
 /* Context splits per (sequence, KV head) that grpo_paged_attn_decode[_qkv]
  * plans for this shape (0 off the fast path).  When it is 1, the out argument
  * of grpo_paged_attn_decode_qkv (bf16 [B, Hq * D], 8-byte aligned; NULL
@@ -287,6 +401,11 @@ int grpo_nf4_linear_partials_attn(const void* attn_workspace, const int32_t* con
  * the epilogue.  group_tpart: float32 workspace of the LoRA partials per group
  * (tpart_bytes); counters: int32 workspace of counter_bytes, ZERO before the
  * first call (every call leaves it zero; calls sharing it must not overlap).
+ * The hand-over to the last slice relies on a group's K slices running on one
+ * XCD (linear ids equal modulo 8); each arrival checks its XCD and *xcd_err
+ * becomes 1 when a group's slices ran on two XCDs (a group split over two L2s
+ * leaves its counter non-zero instead): the caller checks that *xcd_err is 0
+ * and the counters are zero after a run, or its outputs are not valid.
  * residual may alias h_out; row stride ld (a multiple of 4, rows 8-byte
  * aligned).  M <= 16, one LoRA segment; other shapes return GRPO_EUNSUPPORTED. */
 int grpo_nf4_linear_attn_residual(const void* attn_workspace, const int32_t* context_lens,
@@ -294,8 +413,8 @@ int grpo_nf4_linear_attn_residual(const void* attn_workspace, const int32_t* con
                                   const uint8_t* w, const float* absmax, const float* code16,
                                   int blocksize, const void* const* lora_a,
                                   const grpo_linear_parts_t* parts, float* group_tpart,
-                                  int* counters, const void* residual, void* h_out, int64_t ld,
-                                  float* sumsq, grpo_stream_t stream);
+                                  int* counters, int* xcd_err, const void* residual, void* h_out,
+                                  int64_t ld, float* sumsq, grpo_stream_t stream);
 
 /* Column groups G per row of grpo_nf4_linear_attn_residual for this shape (0 if
  * unsupported) and the bytes of its two workspaces. */
@@ -349,8 +468,9 @@ size_t grpo_fold_tiles_elements(int K);
 
 /* grpo_nf4_gate_up_silu_tiles with x = RMSNorm(h): x[m, k] = bf16(bf16(h[m, k] *
  * inv[m]) * norm_weight[k]), inv[m] = 1 / sqrt(sum_g sumsq[m, g] / K + eps), the
- * sums as grpo_linear_finish_residual or grpo_nf4_linear_attn_residual write
- * them (groups <= 32 per row): the
+ * sums as grpo_linear_finish_residual, grpo_nf4_linear_attn_residual or
+ * grpo_nf4_tile_linear_residual write them (groups per row: a multiple of 4,
+ * <= 256; sumsq rows and norm_weight 16-byte aligned): the
  * decoder layer's post-attention RMSNorm (fused_rmsnorm, fused_ops.py:34-77;
  * paged_kv.py:791-798) staged by the gate|up kernel.  M <= 8; shapes as
  * grpo_nf4_gate_up_silu_tiles_norm_supported. */
@@ -422,7 +542,7 @@ int grpo_add_rmsnorm(const void* x, const void* residual, void* h_out, const voi
 
 /* h_out = bf16(residual + y) for the finished linear output y (the epilogue of
  * grpo_nf4_linear_finish: bias, LoRA), and sumsq[m, g] = sum of h_out[m, n]^2
- * over the 256 columns of group g (G = ceil(N / 256) per row, float32): the
+ * over the 64 columns of group g (G = N / 64 per row, float32; N % 64 == 0): the
  * decoder layer's residual add after o_proj (paged_kv.py:791-798) with the
  * statistic of the post-attention RMSNorm, which the gate|up kernel then
  * stages (grpo_nf4_gate_up_silu_tiles_norm).  residual may be NULL and may

@@ -114,3 +114,28 @@ def test_group_size_must_be_positive():
     ids, mask = _batch()
     with pytest.raises(ValueError):
         generate_group_token_ids(None, ids, mask, 0, 4, decode_fn=_StubDecode())
+
+
+def test_pad_token_id_none_pads_with_zero_and_generate_keeps_none():
+    """A tokenizer without a pad id: the paged decode pads stopped rows with 0
+    (the left padding's id), and the model.generate fallback still receives
+    None so it applies its own default."""
+    ids, mask = _batch()
+    dec = _StubDecode()
+    rows = generate_group_token_ids(None, ids, mask, group_size=2, max_new_tokens=8,
+                                    pad_token_id=None, decode_fn=dec)
+    assert dec.calls[0][3]["pad_token_id"] == 0
+    assert all(int(r[-1]) == 0 for r in rows)
+    seen = {}
+
+    def no_backend(*a, **k):
+        raise ImportError("no HIP")
+
+    class _Gen:
+        def generate(self, input_ids, attention_mask, max_new_tokens, **kw):
+            seen.update(kw)
+            return torch.cat([input_ids, input_ids[:, :1].expand(-1, max_new_tokens)], dim=1)
+
+    generate_group_token_ids(_Gen(), ids, mask, group_size=2, max_new_tokens=4,
+                             pad_token_id=None, decode_fn=no_backend)
+    assert "pad_token_id" in seen and seen["pad_token_id"] is None

@@ -65,11 +65,23 @@ def _oracle_caches(cfg, B, width, bs=16):
     return ([np.zeros(shape, np.uint16) for _ in range(2)], tables)
 
 
-@pytest.mark.parametrize("layers", [2])
-def test_decode_step_matches_oracle(dev, layers):
+# The decode step's attention -> o_proj variants at <= 8 rows: the attention
+# merging its splits in the kernel + one-launch o_proj (default); a merge launch
+# + one-launch o_proj computing its own LoRA-A product (the path after a failed
+# XCD check); o_proj finished by its last K slice (O_TILE off).
+PATHS = {"tile_merged": dict(O_TILE=True, ATTN_MERGE=True),
+         "tile_merge_launch": dict(O_TILE=True, ATTN_MERGE=False),
+         "o_fin": dict(O_TILE=False, ATTN_MERGE=False)}
+
+
+@pytest.mark.parametrize("layers,path", [(2, "tile_merged"), (2, "tile_merge_launch"),
+                                         (2, "o_fin")])
+def test_decode_step_matches_oracle(dev, layers, path, monkeypatch):
     from grpo_mi355x.core.kv_pool import PagedKVPool
     from grpo_mi355x.rollout.decode import DecodeEngine
 
+    for k, v in PATHS[path].items():
+        monkeypatch.setattr(DecodeEngine, k, v)
     model = _model(dev, layers=layers)
     w, c = export(model)
     oracle = Qwen2DecodeOracle(w, c)
@@ -81,6 +93,8 @@ def test_decode_step_matches_oracle(dev, layers):
     pool = PagedKVPool(layers, B * width, 2, 128, bs, device=dev)
     sids = [pool.allocate(width * bs) for _ in range(B)]
     eng = DecodeEngine(model, pool, B, width, keep_logits=True)
+    assert eng.o_tile == PATHS[path]["O_TILE"] and eng.attn_merge == PATHS[path]["ATTN_MERGE"]
+    assert eng.o_fin == (path == "o_fin")
     tbl = pool.block_table(sids, width, device=dev)
     eng.start(torch.zeros(B, dtype=torch.int64, device=dev), torch.zeros(B, device=dev), tbl,
               torch.full((B,), 100, device=dev), 100)
@@ -118,6 +132,7 @@ def test_decode_step_matches_oracle(dev, layers):
         pos += 1
     assert worst <= 1e-2, worst
     assert total > 0 and agree == total
+    eng.verify_handover()  # counters back to zero, XCD check word clear
 
 
 def test_paged_kv_decode_model_greedy_matches_oracle(dev):

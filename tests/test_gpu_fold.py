@@ -248,9 +248,9 @@ def test_gate_up_silu_tiles_is_the_tiled_gate_up_silu(dev, m, i, k):
     assert np.array_equal(_bits(til), tiles(_bits(plain)))
 
 
-@pytest.mark.parametrize("n,lora", [(1536, True), (3584, False), (1040, True)])
+@pytest.mark.parametrize("n,lora", [(1536, True), (3584, False), (1088, True)])
 def test_linear_finish_residual_matches_oracle(dev, n, lora):
-    """o_proj's epilogue + residual add + per-256-column sums of squares from
+    """o_proj's epilogue + residual add + per-64-column sums of squares from
     GPU split-K partials, against the oracle linear + bf16 residual add."""
     from grpo_mi355x import _lib
     from grpo_mi355x.kernels import ops
@@ -281,9 +281,9 @@ def test_linear_finish_residual_matches_oracle(dev, n, lora):
     la = (ctypes.c_void_p * 1)(a_d.data_ptr() if lora else None)
     _lib.check(lib.grpo_nf4_linear_partials(x_d.data_ptr(), k, pk_d.data_ptr(), am_d.data_ptr(),
                                             code_d.data_ptr(), bs, la, ctypes.byref(d), st), "p")
-    # h rows of n + 16 columns (ld = n + 16); N = 1040 leaves a partial last group
+    # h rows of n + 16 columns (ld = n + 16); N = 1088 leaves a partial last wave
     h_d = _dev_bf16(res, dev)
-    groups = -(-n // 256)
+    groups = n // 64
     ss_d = torch.full((m, groups + 1), -1.0, dtype=torch.float32, device=dev)
     print(f"finish_residual n={n} lora={lora}", flush=True)
     _lib.check(lib.grpo_linear_finish_residual(ctypes.byref(d), h_d.data_ptr(), h_d.data_ptr(),
@@ -299,11 +299,11 @@ def test_linear_finish_residual_matches_oracle(dev, n, lora):
     assert rel_err(gf, bf16_bits_to_f32(ref)) <= TOL
     assert np.mean(got == ref) >= 0.97
     ss = ss_d.cpu().numpy()
-    # the kernel writes one sum per (row, group) at row stride ceil(N / 256)
+    # the kernel writes one sum per (row, 64 columns) at row stride N / 64
     flat = ss.reshape(-1)[:m * groups].reshape(m, groups)
-    pad = np.zeros((m, groups * 256))
-    pad[:, :n] = gf.astype(np.float64) ** 2
-    assert np.allclose(flat, pad.reshape(m, groups, 256).sum(-1), rtol=1e-6, atol=0)
+    want = (gf.astype(np.float64) ** 2).reshape(m, groups, 64).sum(-1)
+    assert np.allclose(flat, want, rtol=1e-6, atol=0)
+    assert np.all(ss.reshape(-1)[m * groups:] == -1.0)  # nothing past the last group
 
 
 @pytest.mark.parametrize("m,i,k", [(8, 8960, 1536), (3, 512, 1024)])
@@ -321,9 +321,9 @@ def test_gate_up_tiles_norm_matches_the_two_launch_path_and_oracle(dev, m, i, k)
     nw = f32_to_bf16_bits((1 + 0.1 * g.standard_normal(k)).astype(np.float32))
     w = (g.standard_normal((2 * i, k)) * 0.05).astype(np.float32)
     packed, absmax = quantize_nf4(w, bs)
-    groups = -(-k // 256)
+    groups = k // 64
     hf = bf16_bits_to_f32(h).astype(np.float64)
-    ss = np.stack([np.add.reduceat(hf[r] ** 2, np.arange(0, k, 256)) for r in range(m)])
+    ss = np.stack([np.add.reduceat(hf[r] ** 2, np.arange(0, k, 64)) for r in range(m)])
     h_d, nw_d, ss_d = _dev_bf16(h, dev), _dev_bf16(nw, dev), _dev(ss.astype(np.float32), dev)
     pk_d, am_d, code_d = _dev(packed, dev), _dev(absmax, dev), _dev(NF4_CODE.astype(np.float32), dev)
     n_t = int(lib.grpo_fold_tiles_elements(i))
@@ -412,10 +412,13 @@ def test_lm_head_norm_matches_the_two_launch_path(dev):
     assert rel_err(bf16_bits_to_f32(a), ref.astype(np.float32)) <= TOL
 
 
-def test_decode_engine_folds_small_batches(dev):
+def test_decode_engine_folds_small_batches(dev, monkeypatch):
     """Decode batches of <= 8 rows run the folded down_proj, no input-norm
-    launches after layer 0 and o_proj with its finish and the residual add in
-    one launch (no norm launch at all); wider ones keep the split-K path."""
+    launches after layer 0, the attention merging its own splits and o_proj
+    with its epilogue and the residual add in one launch (no norm launch at
+    all); without the in-kernel merge a merge launch is added per layer, and
+    with O_TILE off o_proj is finished by its last K slice; wider batches keep
+    the split-K path."""
     from grpo_mi355x.core.kv_pool import PagedKVPool
     from grpo_mi355x.rollout.decode import DecodeEngine
     from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
@@ -423,9 +426,21 @@ def test_decode_engine_folds_small_batches(dev):
     cfg = Qwen2Config.tiny(layers=3, heads=4, kv_heads=2, head_dim=128, inter=1024, vocab=1024)
     model = build_random_model(cfg, dev, seed=5)
     pool = PagedKVPool(3, 64, 2, 128, 16, device=dev)
+    monkeypatch.setattr(DecodeEngine, "O_TILE", True)
+    monkeypatch.setattr(DecodeEngine, "ATTN_MERGE", True)
     small = DecodeEngine(model, pool, 8, 4)
     wide = DecodeEngine(model, pool, 12, 4)
-    assert small.fold and small.o_fin and not wide.fold
+    assert small.fold and small.o_tile and small.attn_merge and not small.o_fin
+    assert not wide.fold and not wide.o_tile
+    monkeypatch.setattr(DecodeEngine, "ATTN_MERGE", False)
+    nomerge = DecodeEngine(model, pool, 8, 4)
+    assert nomerge.o_tile and not nomerge.attn_merge
+    kinds_nm = [k for k, _ in nomerge.launches()]
+    assert kinds_nm.count("attn_merge") == 3 and len(kinds_nm) == 1 + 3 * 6 + 2
+    monkeypatch.setattr(DecodeEngine, "O_TILE", False)
+    fin = DecodeEngine(model, pool, 8, 4)
+    assert fin.o_fin and not fin.o_tile
+    assert len(fin.launches()) == 1 + 3 * 5 + 2
     kinds = [k for k, _ in small.launches()]
     # no norm launch: the embedding carries layer 0's norm statistic, o_proj
     # the post-attention one, down_proj the next input norm's, and the lm_head

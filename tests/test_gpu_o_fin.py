@@ -98,7 +98,7 @@ def test_attn_residual_matches_oracle_and_the_two_launch_path(dev, m, hq, hkv, r
 
     # two-launch path
     h2 = _dev_bf16(res, dev)
-    ss2 = torch.zeros(m, -(-n // 256), dtype=torch.float32, device=dev)
+    ss2 = torch.zeros(m, n // 64, dtype=torch.float32, device=dev)
     print(f"attn_residual m={m} hq={hq} r={r} bias={bias}: two-launch path", flush=True)
     _lib.check(lib.grpo_nf4_linear_partials_attn(*args, st), "partials_attn")
     _lib.check(lib.grpo_linear_finish_residual(ctypes.byref(d), h2.data_ptr(), h2.data_ptr(), ld,
@@ -120,13 +120,14 @@ def test_attn_residual_matches_oracle_and_the_two_launch_path(dev, m, hq, hkv, r
     assert groups == n // 64
     gt = torch.zeros(max(tb.value, 16) // 4, dtype=torch.float32, device=dev)
     cnt = torch.zeros(cb.value // 4, dtype=torch.int32, device=dev)
+    err = torch.zeros(1, dtype=torch.int32, device=dev)
     for call in range(3):
         h = _dev_bf16(res, dev)
         ss = torch.full((m, groups), -1.0, dtype=torch.float32, device=dev)
         print(f"  fused call {call}", flush=True)
         _lib.check(lib.grpo_nf4_linear_attn_residual(*args, gt.data_ptr(), cnt.data_ptr(),
-                                                     h.data_ptr(), h.data_ptr(), ld,
-                                                     ss.data_ptr(), st), "attn_residual")
+                                                     err.data_ptr(), h.data_ptr(), h.data_ptr(),
+                                                     ld, ss.data_ptr(), st), "attn_residual")
         torch.cuda.synchronize()
         got = _bits(h)
         assert np.array_equal(got[:, n:], res[:, n:])  # columns past N untouched
@@ -139,6 +140,7 @@ def test_attn_residual_matches_oracle_and_the_two_launch_path(dev, m, hq, hkv, r
             assert np.array_equal(got, first)  # deterministic
         first = got
         assert np.count_nonzero(cnt.cpu().numpy()) == 0
+        assert int(err.item()) == 0  # every group's K slices ran on one XCD
         hf = bf16_bits_to_f32(got[:, :n]).astype(np.float64)
         ref_ss = (hf ** 2).reshape(m, groups, 64).sum(-1)
         assert np.allclose(ss.cpu().numpy(), ref_ss, rtol=1e-5, atol=1e-30)
@@ -153,13 +155,14 @@ def test_attn_residual_matches_oracle_and_the_two_launch_path(dev, m, hq, hkv, r
     h = _dev_bf16(res2, dev)
     ss = torch.zeros(m, groups, dtype=torch.float32, device=dev)
     _lib.check(lib.grpo_nf4_linear_attn_residual(*args, gt.data_ptr(), cnt.data_ptr(),
-                                                 h.data_ptr(), h.data_ptr(), ld, ss.data_ptr(),
-                                                 st), "attn_residual")
+                                                 err.data_ptr(), h.data_ptr(), h.data_ptr(), ld,
+                                                 ss.data_ptr(), st), "attn_residual")
     torch.cuda.synchronize()
     got, want = _bits(h), _bits(h2)
     assert rel_err(bf16_bits_to_f32(got), bf16_bits_to_f32(want)) <= 1e-2
     assert np.mean(got == want) >= 0.99
     assert np.count_nonzero(cnt.cpu().numpy()) == 0
+    assert int(err.item()) == 0
 
 
 def test_attn_residual_rejects_unsupported(dev):

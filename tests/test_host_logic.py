@@ -164,6 +164,10 @@ def test_run_paged_reserves_ahead_and_frees_stopped_rows():
             self.active = torch.ones(3, dtype=torch.bool)
             self.block_tables = pool.block_table(sids, 8)
             self.in_use = []
+            self.verified = 0
+
+        def verify_handover(self):
+            self.verified += 1
 
         def step(self):
             self.in_use.append(pool.num_blocks - pool.num_free)
@@ -179,6 +183,7 @@ def test_run_paged_reserves_ahead_and_frees_stopped_rows():
 
     s = Stand()
     stats = DecodeEngine.run_paged(s, sids, 50, check_invariants=True)
+    assert s.verified == 1  # the in-kernel hand-overs are checked after the run
     assert stats["steps"] == 16  # the longest row stops in the 4th chunk of 4
     assert s.count.tolist() == limits
     # 7 private slots for 6 + 13 tokens: at most one chunk ahead of each live row
@@ -232,3 +237,36 @@ def test_fork_into_a_nearly_full_pool_changes_nothing():
     assert pool.refcount == refs and pool.num_free == free
     assert set(pool.blocks) == {p}
     pool.check_invariants()
+
+
+def test_verify_handover_raises_and_switches_the_hand_overs_off():
+    """DecodeEngine.verify_handover: a set XCD check word, or a hand-over
+    counter left non-zero, raises RuntimeError and turns the in-kernel
+    hand-overs (attention merge, o_proj finish) off for engines built later;
+    clear words and counters pass."""
+    from types import SimpleNamespace
+
+    from grpo_mi355x.rollout.decode import DecodeEngine
+
+    saved = (DecodeEngine.ATTN_MERGE, DecodeEngine.O_FIN)
+
+    def stand(err=0, mcnt=None, ocnt=None, o_fin=False):
+        return SimpleNamespace(
+            xcd_err=torch.tensor([err], dtype=torch.int32),
+            m_cnt=None if mcnt is None else torch.tensor(mcnt, dtype=torch.int32),
+            o_cnt=None if ocnt is None else torch.tensor(ocnt, dtype=torch.int32), o_fin=o_fin)
+
+    try:
+        DecodeEngine.ATTN_MERGE, DecodeEngine.O_FIN = True, True
+        DecodeEngine.verify_handover(stand(mcnt=[0] * 64, ocnt=[0] * 32, o_fin=True))
+        assert DecodeEngine.ATTN_MERGE and DecodeEngine.O_FIN
+        # o_proj finish counters are ignored when that path is not in use
+        DecodeEngine.verify_handover(stand(ocnt=[5], o_fin=False))
+        assert DecodeEngine.ATTN_MERGE and DecodeEngine.O_FIN
+        for bad in (stand(err=1), stand(mcnt=[0, 0, 0x100, 0]), stand(ocnt=[0, 3], o_fin=True)):
+            DecodeEngine.ATTN_MERGE, DecodeEngine.O_FIN = True, True
+            with pytest.raises(RuntimeError, match="XCD"):
+                DecodeEngine.verify_handover(bad)
+            assert not DecodeEngine.ATTN_MERGE and not DecodeEngine.O_FIN
+    finally:
+        DecodeEngine.ATTN_MERGE, DecodeEngine.O_FIN = saved
