@@ -102,17 +102,18 @@ def rollout_bytes(cfg, model, stops, prompt_len, group, block_size=16):
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "nf4_linears_traffic_cfg3.md")
+PREFILL_REPS = 5  # timed prefills (mean reported)
 ATTN_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "paged_attention_cfg1.md")
 
 
-def measured_traffic(path: str = TRAFFIC_FILE):
+def measured_traffic(path: str = TRAFFIC_FILE, key: str = "traffic_bytes_per_launch"):
     """HBM bytes per launch (per call for config 1) from a committed rocprofv3
     FETCH_SIZE/WRITE_SIZE summary (two counter passes, scaled by a copy kernel of
     known size), or None."""
     try:
         with open(path) as fh:
             for line in fh:
-                if line.startswith("traffic_bytes_per_launch:"):
+                if line.startswith(key + ":"):
                     return int(line.split(":", 1)[1])
     except OSError:
         pass
@@ -166,8 +167,9 @@ def kernel_timing(eng, dev, reps: int = 20) -> dict:
     return out
 
 
-def cpu_baseline(model, cfg, group, ctx, seed):
-    """One decode step of the numpy oracle on the host (bounded sample)."""
+def cpu_baseline(model, cfg, group, ctx, seed, timed: int = 2):
+    """Decode steps of the numpy oracle on the host (bounded sample: one
+    warm-up step, then ``timed`` timed steps; about 10 s each at config 3)."""
     import numpy as np
 
     from oracle.decode import Qwen2DecodeOracle
@@ -205,7 +207,7 @@ def cpu_baseline(model, cfg, group, ctx, seed):
              scaling=cfg.lora_alpha / cfg.lora_rank)
     oracle = Qwen2DecodeOracle(w, c, cache_dequant=False)
     g = np.random.default_rng(seed)
-    width = -(-(ctx + 1) // 16)
+    width = -(-(ctx + timed + 2) // 16)
     nb = group * width
     kcs = [g.integers(0, 1 << 16, (nb, cfg.num_key_value_heads, 16, cfg.head_dim),
                       dtype=np.uint16) & 0xBFFF for _ in range(cfg.num_hidden_layers)]
@@ -213,13 +215,20 @@ def cpu_baseline(model, cfg, group, ctx, seed):
     tables = np.arange(nb, dtype=np.int32).reshape(group, width)
     toks = g.integers(0, cfg.vocab_size, group)
     pos = np.full(group, ctx, dtype=np.int64)
+    # one untimed warm-up step (first-touch page faults, BLAS start-up), then
+    # `timed` steps, each at the next position
+    toks = oracle.step(toks, kcs, vcs, tables, pos)[1]
+    pos = pos + 1
     t0 = time.perf_counter()
-    oracle.step(toks, kcs, vcs, tables, pos)
-    dt = time.perf_counter() - t0
+    for _ in range(timed):
+        toks = oracle.step(toks, kcs, vcs, tables, pos)[1]
+        pos = pos + 1
+    dt = (time.perf_counter() - t0) / timed
     return dict(value=round(group / dt, 4), unit="tok/s", kind="port", **_host_cores(),
-                sample=(f"1 decode step of the numpy oracle, G={group} rows at context {ctx + 1}, "
-                        f"all 28 layers + lm_head, NF4 dequantized per call; {dt:.2f} s "
-                        "(numpy: elementwise single-threaded, BLAS matmuls multi-threaded)"))
+                sample=(f"{timed} decode steps of the numpy oracle after 1 warm-up step, G={group} "
+                        f"rows at context {ctx + 2}..{ctx + 1 + timed}, all 28 layers + lm_head, "
+                        f"NF4 dequantized per call; {dt:.2f} s per step (numpy: elementwise "
+                        "single-threaded, BLAS matmuls multi-threaded)"))
 
 
 def _emit(args, value, unit, ms_step, workload, extra):
@@ -383,8 +392,8 @@ def _graph_time(fns, dev, reps: int) -> float:
     side = torch.cuda.Stream(device=dev)
     side.wait_stream(torch.cuda.current_stream(dev))
     with torch.cuda.stream(side):
-        for fn in fns[:2]:
-            fn()  # workspaces sized before capture
+        for fn in fns:
+            fn()  # workspaces sized and per-weight layouts (packed LoRA A) built before capture
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=side):
@@ -546,9 +555,10 @@ def run_cfg2(args):
     with A, B ~ N(0, 0.01), bias on q/k/v, x ~ N(0, 1) bf16.
 
     R independent sets of the four projections (>= 512 MB of weights) are
-    launched back to back (``grpo_nf4_lora_linear``: split-K partial sums and
-    the finish), so no call finds its weights in the 256 MB MALL.  One step =
-    one replay of the R x 4 calls."""
+    launched back to back (``ops.nf4_lora_linear``: at 8 rows the one-launch
+    tile kernel, ``grpo_nf4_tile_linear``, with each LoRA A packed once before
+    the timed region), so no call finds its weights in the 256 MB MALL.  One
+    step = one replay of the R x 4 calls."""
     import numpy as np
     import torch
 
@@ -597,7 +607,7 @@ def run_cfg2(args):
         nb = lin_bytes(n, name != "o")
         per_kind[name] = dict(us_per_call=round(us, 3), bytes_per_call=nb,
                               achieved_GBs=round(nb / (us * 1e-6) / 1e9, 1),
-                              splits=ops.nf4_linear_plan(M, n, K, R_, 1, BSZ)[0])
+                              launches_per_call=1)
     tot_us = sum(v["us_per_call"] for v in per_kind.values())
     achieved = per_set / (tot_us * 1e-6) / 1e9
     log(f"config 2: {R} rotating sets; {per_kind}")
@@ -640,7 +650,7 @@ def run_cfg2(args):
         "bytes_per_set": per_set, "projections": per_kind,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4), "traffic": None,
-                     "kernel": "grpo_nf4_lora_linear: nf4_part_mfma + nf4_finish per call"},
+                     "kernel": "grpo_nf4_tile_linear: nf4_tile_mfma (one launch per call)"},
         "cpu_baseline": cpu}), flush=True)
 
 
@@ -739,13 +749,24 @@ def main():
     pre = PrefillEngine(model, pool, prefill_chunk(P - 1), width)
     pre.capture()
     torch.cuda.synchronize()
-    t = time.time()
-    parent = prefill(pre, pool, tuple(prompt), width)
-    torch.cuda.synchronize()
-    prefill_s = time.time() - t
-    log(f"prefill of {P - 1} tokens in {prefill_s * 1e3:.1f} ms ({pre.B}-token chunks)")
+    # one untimed prefill (first use of the pool blocks and of the graph), then
+    # the mean of PREFILL_REPS timed ones (each into a fresh pool sequence)
+    pool.free(prefill(pre, pool, tuple(prompt), width))
+    times = []
+    for i in range(PREFILL_REPS):
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        parent = prefill(pre, pool, tuple(prompt), width)
+        torch.cuda.synchronize()
+        times.append(time.perf_counter() - t)
+        if i + 1 < PREFILL_REPS:
+            pool.free(parent)
+    prefill_s = sum(times) / len(times)
+    log(f"prefill of {P - 1} tokens in {prefill_s * 1e3:.1f} ms ({pre.B}-token chunks; mean of "
+        f"{PREFILL_REPS}, min {min(times) * 1e3:.1f}, max {max(times) * 1e3:.1f})")
     prefill_info = dict(tokens=P - 1, chunk=pre.B, ms=round(prefill_s * 1e3, 2),
-                        tokens_per_s=round((P - 1) / prefill_s, 1))
+                        ms_min=round(min(times) * 1e3, 2), ms_max=round(max(times) * 1e3, 2),
+                        reps=PREFILL_REPS, tokens_per_s=round((P - 1) / prefill_s, 1))
     kids = pool.fork(parent, G, reserve_tokens=P - 1 + NEW + 1)
     pool.free(parent)
     pool.check_invariants()
@@ -783,6 +804,7 @@ def main():
     elapsed = t1 - t0
     if args.warmup > 0 and not args.sample:
         assert torch.equal(eng.generated, gen), "rollouts are not deterministic"
+    eng.verify_handover()  # the in-kernel hand-overs ran on one XCD (outside the timed region)
     tokens = sum(stops) * args.steps
     value = tokens / elapsed
     ms_rollout = elapsed / args.steps * 1e3
@@ -805,11 +827,22 @@ def main():
         tot_us = sum(k["avg_us"] * k["launches"] for k in nf4)
         tot_b = sum(k["bytes_per_launch"] * k["launches"] for k in nf4)
         n = sum(k["launches"] for k in nf4)
-        achieved = tot_b / (tot_us * 1e-6) / 1e9
+        agg = tot_b / (tot_us * 1e-6) / 1e9
+        # the dominant kernel of the step (most GPU time per step): gate|up
+        dom = max(eng.NF4_KINDS, key=lambda k: kernels[k]["avg_us"] * kernels[k]["launches"])
+        dk = kernels[dom]
+        achieved = dk["bytes_per_launch"] / (dk["avg_us"] * 1e-6) / 1e9
         roofline = dict(bound="hbm", achieved=round(achieved, 1), peak=PEAK_HBM_GBS, unit="GB/s",
-                        frac=round(achieved / PEAK_HBM_GBS, 4), traffic=measured_traffic(),
-                        kernel="NF4 linears: nf4_part_mfma (q|k|v, o, down) + nf4_gate_up_units (gate|up)",
-                        avg_launch_us=round(tot_us / n, 3), bytes_per_launch=tot_b // n)
+                        frac=round(achieved / PEAK_HBM_GBS, 4),
+                        traffic=measured_traffic(key=f"traffic_{dom}"),
+                        kernel=f"{dom}: {eng.kernel_name(dom)}", avg_launch_us=dk["avg_us"],
+                        bytes_per_launch=dk["bytes_per_launch"],
+                        step_share=round(dk["avg_us"] * dk["launches"] / (step_ms * 1e3), 4),
+                        nf4_aggregate=dict(
+                            kernels={k: eng.kernel_name(k) for k in eng.NF4_KINDS},
+                            achieved=round(agg, 1), frac=round(agg / PEAK_HBM_GBS, 4),
+                            avg_launch_us=round(tot_us / n, 3), bytes_per_launch=tot_b // n,
+                            traffic=measured_traffic()))
         shared = ((P - 1) // BS) * BS  # prompt tokens in the rows' shared full blocks
         ab_phys = ab - (G - 1) * shared * cfg.num_key_value_heads * cfg.head_dim * 2 * 2
         at_us = kernels["attention"]["avg_us"]
@@ -825,7 +858,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        log("CPU baseline (numpy oracle, one decode step) ...")
+        log("CPU baseline (numpy oracle: one warm-up + two timed decode steps) ...")
         try:
             cpu = cpu_baseline(model, cfg, G, P, args.seed)
         except MemoryError as exc:  # pragma: no cover

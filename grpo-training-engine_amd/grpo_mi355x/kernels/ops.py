@@ -144,8 +144,9 @@ def nf4_lora_linear(x2d: torch.Tensor, packed: torch.Tensor, absmax: torch.Tenso
                     scaling: float = 1.0, out: torch.Tensor | None = None) -> torch.Tensor:
     """``y[M, N] = W_nf4(x) + bias + B(A(x)) * scaling`` (bf16).
 
-    Split-K partial sums + finish (two launches) on the fast path, one generic
-    launch otherwise.
+    Up to 32 rows: the one-launch tile kernel (``grpo_nf4_tile_linear``, LoRA A
+    packed once per tensor version); otherwise split-K partial sums + finish
+    (two launches) on the fast path, one generic launch for other shapes.
     """
     lib = _lib.device_library()
     _need_cuda(x2d, packed, absmax, code, bias, lora_a, lora_b)
@@ -173,6 +174,25 @@ def nf4_lora_linear(x2d: torch.Tensor, packed: torch.Tensor, absmax: torch.Tenso
         out = torch.empty((m, n), dtype=torch.bfloat16, device=x2d.device)
     elif out.shape != (m, n) or out.stride(1) != 1 or out.dtype != torch.bfloat16:
         raise ValueError("out must be a bf16 [M, N] tensor with unit column stride.")
+    if (m <= TILE_MAX_ROWS and x2d.stride(0) % 8 == 0 and x2d.data_ptr() % 16 == 0
+            and packed.data_ptr() % 16 == 0 and out.data_ptr() % 2 == 0
+            and lib.grpo_nf4_tile_supported(m, n, k, r, 1, int(blocksize))):
+        # decode batches: the one-launch tile linear (LoRA A in its packed
+        # order, built once per A version)
+        d = _lib.TileLinear()
+        d.M, d.N, d.K, d.nseg, d.r = m, n, k, 1, r
+        d.seg_end[0] = n
+        d.bias[0] = _lib.ptr(bias)
+        if r > 0:
+            d.lora_a[0] = packed_lora_a(lora_a).data_ptr()
+            d.lora_b[0] = lora_b.data_ptr()
+        d.scaling = float(scaling)
+        rc = lib.grpo_nf4_tile_linear(x2d.data_ptr(), x2d.stride(0), packed.data_ptr(),
+                                      absmax.data_ptr(), code.data_ptr(), int(blocksize),
+                                      ctypes_byref(d), out.data_ptr(), out.stride(0),
+                                      _lib.stream_handle(x2d.device))
+        _lib.check(rc, "grpo_nf4_tile_linear")
+        return out
     nbytes = int(lib.grpo_nf4_lora_linear_workspace_bytes(m, n, k, r, 1, int(blocksize)))
     ws = workspace("nf4_linear", nbytes, x2d.device)
     rc = lib.grpo_nf4_lora_linear(
@@ -182,6 +202,28 @@ def nf4_lora_linear(x2d: torch.Tensor, packed: torch.Tensor, absmax: torch.Tenso
         _lib.stream_handle(x2d.device))
     _lib.check(rc, "grpo_nf4_lora_linear")
     return out
+
+
+TILE_MAX_ROWS = 32  # rows up to which nf4_lora_linear runs the one-launch tile kernel
+
+# Packed LoRA A per live A tensor: id(A) -> (weakref to A, A._version, packed).
+# An entry is valid while A is the same object at the same version (an
+# optimizer step updates A in place and bumps the version) and is dropped
+# when A is freed.
+_packed_a: dict[int, tuple] = {}
+
+
+def packed_lora_a(a: torch.Tensor) -> torch.Tensor:
+    """``pack_lora_a(a)``, cached per A tensor and version."""
+    import weakref
+
+    key = id(a)
+    e = _packed_a.get(key)
+    if e is not None and e[0]() is a and e[1] == a._version:
+        return e[2]
+    p = pack_lora_a(a)
+    _packed_a[key] = (weakref.ref(a, lambda _r, k=key: _packed_a.pop(k, None)), a._version, p)
+    return p
 
 
 def pack_lora_a(a: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:

@@ -18,9 +18,10 @@ returns an object with the layout ``DecodeEngine`` needs:
 
 A weight is accepted when it has the bnb ``Params4bit`` surface: a uint8
 tensor with ``quant_state.{absmax, code, blocksize, shape}``.  Nested
-(double-quantized) absmax is rejected with ``ValueError``: the split-K kernel
-reads float32 absmax.  A model that already has the stacked layout (for
-example ``rollout.qwen2.Qwen2ForCausalLM``) is returned unchanged.
+(double-quantized) absmax is expanded once to the float32 absmax the kernels
+read (``_nf4_parts``, ``grpo_nf4_absmax_expand``: lora_forward.py:187-199).  A
+model that already has the stacked layout (for example
+``rollout.qwen2.Qwen2ForCausalLM``) is returned unchanged.
 """
 
 from __future__ import annotations

@@ -315,6 +315,25 @@ class DecodeEngine:
                                + (B * self.Hkv * 16 * 4 if self.attn_merge else rr * k_ * 2)
                                + 2 * B * H * 2 + B * self.ss_post.shape[1] * 4)
 
+    def kernel_name(self, kind: str) -> str:
+        """The kernel an NF4 launch kind of this engine runs (for reports)."""
+        if kind == "qkv":
+            return ("nf4_part_mfma (split-K, input RMSNorm staged)" if self.fold
+                    else "nf4_part_mfma (split-K)")
+        if kind == "o":
+            if self.o_tile:
+                return "nf4_tile_mfma (one launch: epilogue + residual)"
+            if self.o_fin:
+                return ("nf4_part_mfma (split-K, attention splits merged while staging, "
+                        "last K slice finishes + residual)")
+            return "nf4_part_mfma (split-K)"
+        if kind == "gate_up":
+            return "nf4_gate_up (SiLU*up fused)" if self.gu_fused else "nf4_part_mfma (split-K)"
+        if kind == "down":
+            return ("nf4_fold_residual (whole K per 8 columns, residual)" if self.fold
+                    else "nf4_part_mfma (split-K)")
+        return kind
+
     def splits(self, kind: str) -> int:
         """K slices of an NF4 launch kind (1 for the folded down_proj)."""
         return 1 if kind == "down" and self.fold else self.plans[kind][0]
@@ -352,8 +371,9 @@ class DecodeEngine:
     @staticmethod
     def _lm_tiles(model, w: torch.Tensor, dev) -> torch.Tensor:
         """The tile-order copy of the lm_head weight, built once per model and
-        weight version (kept on the model object; the weight is frozen while
-        rollouts run)."""
+        weight version (kept on the model object, V * H * 2 bytes: 0.47 GB at
+        Qwen2-1.5B, 1.09 GB at 7B, until ``release_decode_caches(model)``; the
+        weight is frozen while rollouts run)."""
         key = (w.data_ptr(), w._version, tuple(w.shape))
         cache = getattr(model, "_grpo_lm_tiles", None)
         if cache is not None and cache[0] == key:
@@ -868,6 +888,20 @@ class PrefillEngine(DecodeEngine):
             self.step()
 
 
+def release_decode_caches(model=None) -> None:
+    """Free what the decode path keeps between rollouts, e.g. before the
+    training phase: the tile-order lm_head copy on ``model`` (and on its
+    adapted decode view; V * H * 2 bytes) and the packed LoRA A copies of the
+    one-launch linear.  The next rollout rebuilds them (one copy kernel each)."""
+    from . import adapt
+
+    models = [] if model is None else [model, adapt._cache.get(model)]
+    for m in models:
+        if m is not None and hasattr(m, "_grpo_lm_tiles"):
+            del m._grpo_lm_tiles
+    ops._packed_a.clear()
+
+
 # ------------------------------------------------------------- drop-in ---
 
 def _prompt_rows(input_ids: torch.Tensor, attention_mask: Optional[torch.Tensor]):
@@ -983,4 +1017,4 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
 
 
 __all__ = ["DecodeEngine", "PrefillEngine", "paged_kv_decode_model", "prefill",
-           "prefill_chunk"]
+           "prefill_chunk", "release_decode_caches"]

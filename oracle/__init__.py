@@ -16,6 +16,9 @@ This package restates, in numpy, the arithmetic of the reference's hot path
                             the low-level decode loop (``paged_kv.py:840-985``)
                             and a Qwen2-shaped decode step
                             (``paged_kv.py:690-820``, ``fused_ops.py:34-251``).
+* ``oracle.sampling``    -- the sampled-token rule of the device sampler for a
+                            given uniform draw (temperature, top-p cut, ties),
+                            and the SplitMix64 draw of (seed, row, step).
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import this package, and only as the checker or as the timed
@@ -46,6 +49,14 @@ Pinning (what each function is checked against, besides the GPU kernels):
 * ``decode.Qwen2DecodeOracle``   -- per-op checks above, plus
                                     ``transformers``' ``Qwen2RMSNorm`` and
                                     ``apply_rotary_pos_emb`` on CPU.
+* ``sampling`` (kept set, draw)  -- torch's CPU sort / softmax / cumsum on the
+                                    same bf16 logits; closed-form edge cases
+                                    (top_p 0 and 1, ties in index order, a
+                                    two-of-four known answer); draw frequencies
+                                    against the kept probabilities;
+                                    ``exp_nonpos`` against float64 ``exp``;
+                                    ``splitmix64`` against published vectors
+                                    (``tests/test_oracle_sampling.py``).
 """
 
-__all__ = ["bf16", "nf4", "lora_linear", "paged", "decode"]
+__all__ = ["bf16", "nf4", "lora_linear", "paged", "decode", "sampling"]

@@ -5,8 +5,9 @@ vocab 152064, NF4 weights + rank-16 LoRA; 64 rows with context lengths uniform
 in [1024, 4096] over a KV pool pre-filled with N(0, 1) bf16 (config 5's
 decode-only measurement: no 4k-token prefill) behind shuffled block tables.
 One transformer layer instead of 28 keeps the numpy oracle to seconds; every
-kernel runs at its 7B shape (M = 64 takes the split-K gate|up path and the
-hipBLASLt lm_head).  Two decode steps, each compared with the oracle on the
+kernel runs at its 7B shape (M = 64 takes the chunked wide gate|up kernel,
+nf4_gate_up_wide, and the wide lm_head with fused argmax, lm_head_argmax_wide).
+Two decode steps, each compared with the oracle on the
 same caches: logits within 1e-2 of max|logit|, greedy tokens equal wherever
 the oracle's top-2 margin exceeds that tolerance, and the appended K/V rows
 equal the oracle's (bf16 bits) up to rounding.

@@ -330,3 +330,25 @@ def test_lm_head_argmax_wide_x_in_k_chunks(dev, M, K):
     ref = x.float() @ w.float().t()
     assert rel_err(logits.float().cpu().numpy(), ref.cpu().numpy()) <= 1e-2
     assert torch.equal(nxt, logits.float().argmax(dim=1))
+
+
+def test_release_decode_caches_frees_the_lm_head_copy(dev):
+    """The tile-order lm_head copy lives on the model between rollouts and
+    release_decode_caches drops it; the next engine rebuilds the same bits."""
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.kernels import ops
+    from grpo_mi355x.rollout.decode import DecodeEngine, release_decode_caches
+
+    model = _model(dev, layers=1)
+    pool = PagedKVPool(1, 16, 2, 128, 16, device=dev)
+    eng = DecodeEngine(model, pool, 4, 4)
+    assert eng.lm_tiled and hasattr(model, "_grpo_lm_tiles")
+    first = eng.lm_w.clone()
+    ops.packed_lora_a(model.model.layers[0].self_attn.o_proj.lora_A.weight)
+    assert len(ops._packed_a) > 0
+    del eng
+    release_decode_caches(model)
+    assert not hasattr(model, "_grpo_lm_tiles") and len(ops._packed_a) == 0
+    eng = DecodeEngine(model, pool, 4, 4)
+    torch.cuda.synchronize()
+    assert torch.equal(eng.lm_w.view(torch.int16), first.view(torch.int16))

@@ -91,3 +91,70 @@ def test_noalloc_refuses_shapes_beyond_its_array(dev):
     rc = _call(lib, q, kc, kc, tab, lens, out)
     assert rc == -3  # GRPO_EWORKSPACE, nothing launched
     assert b"allocation-free" in lib.grpo_last_error()
+
+
+_CHILD = r"""
+import sys
+sys.path[:0] = sys.argv[1:3]
+import torch
+from grpo_mi355x import _lib
+
+lib = _lib.library()  # loaded, grpo_init not called: nothing has resolved the scratch address
+dev = torch.device("cuda:0")
+gen = torch.Generator().manual_seed(7)
+B, hq, hkv, d, bs, width = 6, 12, 2, 128, 16, 40
+nb = B * width
+kc = torch.randn((nb, hkv, bs, d), generator=gen).to(torch.bfloat16).to(dev)
+vc = torch.randn((nb, hkv, bs, d), generator=gen).to(torch.bfloat16).to(dev)
+q = torch.randn((B, hq, d), generator=gen).to(torch.bfloat16).to(dev)
+tab = torch.randperm(nb, generator=gen).to(torch.int32).view(B, width).to(dev)
+lens = torch.tensor([640, 17, 1, 333, 600, 129], dtype=torch.int32, device=dev)
+got = torch.zeros((B, hq, d), dtype=torch.float32, device=dev)
+want = torch.zeros((B, hq, d), dtype=torch.float32, device=dev)
+need = lib.grpo_paged_attn_workspace_bytes(B, hq, hkv, d, bs, width)
+ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+
+def args(out):
+    return (q.data_ptr(), q.stride(0), q.stride(1), kc.data_ptr(), vc.data_ptr(), nb,
+            tab.data_ptr(), tab.stride(0), lens.data_ptr(), out.data_ptr(), 0, B, hq, hkv, d, bs,
+            width, float(d) ** -0.5)
+
+torch.cuda.synchronize()
+side = torch.cuda.Stream(device=dev)
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g, stream=side):
+    rc = lib.grpo_paged_attn_decode_noalloc(*args(got), _lib.stream_handle(dev))
+print("first call inside capture: rc", rc, flush=True)
+assert rc == 0, lib.grpo_last_error()
+assert lib.grpo_paged_attn_decode(*args(want), ws.data_ptr(), need,
+                                  _lib.stream_handle(dev)) == 0
+for i in range(3):
+    got.fill_(float("nan"))
+    g.replay()
+    torch.cuda.synchronize()
+    same = torch.equal(got.view(torch.int32), want.view(torch.int32))
+    print("replay", i, "bit-equal", same, flush=True)
+    assert same
+    lens.add_(1)  # the next replay reads the new lengths, as does the eager reference
+    assert lib.grpo_paged_attn_decode(*args(want), ws.data_ptr(), need,
+                                      _lib.stream_handle(dev)) == 0
+    torch.cuda.synchronize()
+print("ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_graph_capture(dev):
+    """The entry's first call in a process (where it resolves its scratch
+    array's device address) made inside a HIP graph capture: the capture
+    succeeds and every replay equals the workspace entry bit for bit.  Run in
+    a child process so that no earlier call has resolved the address."""
+    import subprocess
+    import sys
+
+    from conftest import PKG, ROOT
+
+    r = subprocess.run([sys.executable, "-c", _CHILD, ROOT, PKG], capture_output=True,
+                       text=True, timeout=180)
+    print(r.stdout[-2000:], r.stderr[-2000:], flush=True)
+    assert r.returncode == 0
+    assert r.stdout.strip().endswith("ok")
