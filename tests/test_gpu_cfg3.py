@@ -133,3 +133,52 @@ def test_cfg3_headline_shape_prefill_and_ragged_decode_match_oracle(dev):
     gen = eng.generated.cpu().numpy()
     for b in range(G):
         assert np.all(gen[b, limits[b]:] == 0)
+
+
+def test_cfg3_full_depth_rollouts_keep_the_xcd_check_clear(dev):
+    """The benchmarked rollout itself -- 28 layers, G = 8, 512-token prompt,
+    512 greedy steps from the captured graph -- twice: both give the same
+    tokens, every row generates up to its stop and pads after, and the
+    in-kernel hand-over of the default path (o_proj's last K slice of a column
+    group finishing it) leaves its counters at zero with the XCD check word
+    clear over all 28 x 512 layer-steps (``DecodeEngine.verify_handover``)."""
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill, prefill_chunk
+    from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
+
+    cfg = Qwen2Config.qwen2_1_5b()
+    model = build_random_model(cfg, dev, seed=0)
+    G, P, NEW, bs = 8, 512, 512, 16
+    g = np.random.default_rng(0)
+    stops = g.integers(64, NEW + 1, G).tolist()
+    stops[3] = NEW
+    prompt = g.integers(0, cfg.vocab_size, P).tolist()
+    width = -(-(P + NEW) // bs)
+    pool = PagedKVPool(cfg.num_hidden_layers, width * (G + 2), cfg.num_key_value_heads,
+                       cfg.head_dim, bs, device=dev)
+    print("cfg3 full depth: prefill", flush=True)
+    pre = PrefillEngine(model, pool, prefill_chunk(P - 1), width)
+    parent = prefill(pre, pool, tuple(prompt), width)
+    del pre
+    kids = pool.fork(parent, G, reserve_tokens=P + NEW)
+    pool.free(parent)
+    eng = DecodeEngine(model, pool, G, width)
+    assert eng.attn_fused and eng.o_fin
+    start = dict(tokens=torch.full((G,), prompt[-1], dtype=torch.int64, device=dev),
+                 positions=torch.full((G,), P - 1, device=dev),
+                 block_tables=pool.block_table(kids, width, device=dev),
+                 limits=torch.tensor(stops, device=dev), max_new_tokens=NEW)
+    eng.start(**start)
+    eng.capture()
+    outs = []
+    for rep in range(2):
+        print(f"cfg3 full depth: rollout {rep}", flush=True)
+        eng.start(**start)
+        eng.run(max(stops))
+        torch.cuda.synchronize()
+        outs.append(eng.generated.cpu().numpy().copy())
+        eng.verify_handover()
+    assert np.array_equal(outs[0], outs[1])
+    for b, s in enumerate(stops):
+        assert np.all(outs[0][b, s:] == 0)
+    assert len({tuple(r[:64]) for r in outs[0]}) == 1  # one prompt, greedy: equal prefixes

@@ -238,3 +238,105 @@ def test_cfg4_headline_shape_ragged_group_matches_oracle(dev):
     print(f"cfg4 shape: {stats}, tokens compared {compared}, agree {agree}", flush=True)
     assert compared >= 0.5 * sum(stops[b] for b in longest)
     assert agree == compared
+
+
+def _oracle_check_steps(oracle, prompt, gen, steps, width, chunk=256):
+    """Teacher-forced oracle at decode steps ``steps`` (increasing) of one row:
+    tokens by position are the prompt, then the GPU's generated tokens; the
+    oracle caches every position before the checked one by a batched causal
+    prefill (rows of one step call sharing the row's block table), then runs
+    the checked position with logits.  Returns [(step, oracle next token,
+    safe top-2 margin)]."""
+    n = len(prompt)
+    toks = list(prompt) + [int(t) for t in gen]
+    kcs = [np.zeros((width, 2, 16, 128), np.uint16) for _ in range(2)]
+    vcs = [np.zeros_like(k) for k in kcs]
+    done, out = 0, []
+    for s in steps:
+        pos = n - 1 + s  # the step's input token and position
+        while done < pos:
+            j = np.arange(done, min(pos, done + chunk))
+            oracle.step(np.array([toks[i] for i in j]), kcs, vcs,
+                        np.zeros((len(j), width), np.int32) + np.arange(width, dtype=np.int32),
+                        j, with_logits=False)
+            done = int(j[-1]) + 1
+        logits, nxt = oracle.step(np.array([toks[pos]]), kcs, vcs,
+                                  np.arange(width, dtype=np.int32)[None], np.array([pos]))
+        done = pos + 1
+        lr = bf16_bits_to_f32(logits[0])
+        srt = np.sort(lr)
+        out.append((s, int(nxt[0]), bool(srt[-1] - srt[-2] > 1e-2 * np.abs(lr).max())))
+        print(f"  oracle step {s} (position {pos}): {out[-1]}", flush=True)
+    return out
+
+
+@pytest.mark.timeout(600)
+def test_cfg4_long_tail_rows_match_oracle_at_sampled_steps(dev):
+    """Config 4's long tail on the Qwen2-1.5B shape (two layers): G = 32 rows =
+    4 prompts x 8 samples, prompts U[128, 512], lognormal stops (median 200,
+    sigma 0.75, capped at 1024) with one row of prompt 0 running 1160 tokens, so
+    its context grows past 1,500 through blocks reserved a chunk ahead while
+    the other rows stop and free theirs (``run_paged``).  Every block is back
+    on the free list at the end and the in-kernel hand-overs check clear.  The
+    oracle, teacher-forced on the GPU's tokens, recomputes the long row at
+    steps 0, 255, 511, 767, 1023 and 1159 and each other prompt's longest row
+    at its last step: the GPU's token equals the oracle's argmax wherever the
+    oracle's top-2 margin exceeds 1e-2 of max|logit|."""
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill
+    from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
+
+    cfg = Qwen2Config.qwen2_1_5b()
+    cfg.num_hidden_layers = 2
+    model = build_random_model(cfg, dev, seed=43)
+    g = np.random.default_rng(12)
+    prompts, samples, new, long_steps = 4, 8, 1160, 1160
+    lens = g.integers(128, 513, prompts)
+    plist = [g.integers(0, cfg.vocab_size, n).tolist() for n in lens]
+    stops = np.minimum(1024, np.maximum(1, np.round(
+        g.lognormal(np.log(200.0), 0.75, prompts * samples)))).astype(int)
+    stops[0] = long_steps
+    rows = [plist[i // samples] for i in range(prompts * samples)]
+    B, bs = len(rows), 16
+    width = -(-(int(lens.max()) + new) // bs)
+    pool = PagedKVPool(2, prompts * width + B * (width + 1), cfg.num_key_value_heads,
+                       cfg.head_dim, bs, device=dev)
+    print(f"cfg4 long tail: prompts {lens.tolist()}, stops {stops.tolist()}", flush=True)
+    pre = PrefillEngine(model, pool, 64, width)
+    parents = [prefill(pre, pool, tuple(p), width) for p in plist]
+    del pre
+    sids = [pool.fork(parents[i // samples], 1, reserve_tokens=len(r))[0]
+            for i, r in enumerate(rows)]
+    for p in parents:
+        pool.free(p)
+    eng = DecodeEngine(model, pool, B, width)
+    start = dict(tokens=torch.tensor([r[-1] for r in rows], device=dev),
+                 positions=torch.tensor([len(r) - 1 for r in rows], device=dev),
+                 block_tables=pool.block_table(sids, width, device=dev),
+                 limits=torch.from_numpy(stops).to(dev), max_new_tokens=new)
+    eng.start(**start)
+    eng.capture()
+    eng.start(**start)
+    stats = eng.run_paged(sids, new, check_invariants=True)  # also checks the hand-overs
+    torch.cuda.synchronize()
+    assert long_steps <= stats["steps"] <= long_steps + 16
+    assert pool.num_free == pool.num_blocks and not pool.blocks
+    gen = eng.generated.cpu().numpy()
+    for b in range(B):
+        lead = (b // samples) * samples
+        s = min(stops[b], stops[lead])
+        assert np.array_equal(gen[b, :s], gen[lead, :s])
+        assert np.all(gen[b, stops[b]:] == PAD)
+    print(f"cfg4 long tail: {stats}", flush=True)
+    w, c = export(model)
+    oracle = Qwen2DecodeOracle(w, c)
+    checks = [(0,) + c for c in _oracle_check_steps(oracle, plist[0], gen[0, :long_steps],
+                                                    [0, 255, 511, 767, 1023, 1159], width)]
+    for i in range(1, prompts):
+        b = max(range(i * samples, (i + 1) * samples), key=lambda r: stops[r])
+        checks += [(b,) + c for c in _oracle_check_steps(oracle, plist[i], gen[b, :stops[b]],
+                                                         [int(stops[b]) - 1], width)]
+    safe = [(b, s, nxt) for b, s, nxt, ok in checks if ok]
+    assert len(safe) >= len(checks) // 2
+    for b, s, nxt in safe:
+        assert gen[b, s] == nxt, (b, s, gen[b, s], nxt)
