@@ -1302,15 +1302,23 @@ __global__ void __launch_bounds__(128 * S) nf4_gate_up_silu(GuArgs p) {
 // Item partial tiles meet in LDS and are summed in k-step order.
 constexpr int GUU_XU = 6;  // x chunks per thread loaded before the weights
 #ifndef GRPO_GUU_LA
-#define GRPO_GUU_LA 1
+#define GRPO_GUU_LA 2
 #endif
 constexpr int GUU_LA = GRPO_GUU_LA;  // items whose weights are in flight ahead of the one decoded
 
 // MT row tiles of 16 (MT = 2: 17..32 rows, whose x of K <= 1536 still fits
-// LDS whole with the item tiles: config 4's G = 32).
-template <int W, int IPW, bool NORM, int MT = 1>
+// LDS whole with the item tiles: config 4's G = 32).  ROWS (M <= 8, the
+// decode step's rows): wave w stages columns [w c, w c + c) of every row
+// (c = ceil(K / 8 / W) chunks of 8), lane l row l / 8 and chunks l % 8,
+// l % 8 + 8, ... of the range -- no row/column division per chunk, and each
+// RMSNorm weight chunk is loaded by one wave (8 lanes, one address) instead
+// of every wave.  Otherwise chunk i of the M x K/8 chunks goes to thread
+// i mod (64 W).
+template <int W, int IPW, bool NORM, int MT = 1, bool ROWS = false>
 __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
   static_assert(!NORM || MT == 1, "the RMSNorm source takes at most 8 rows");
+  static_assert(!ROWS || (MT == 1 && W >= 8), "8 lanes per row, rows <= 8");
+  touch_kernargs<sizeof(GuArgs)>();
   constexpr int NTH = 64 * W;
   extern __shared__ __align__(16) uint16_t xs[];  // [M][K + 8] (decode8 order), then tiles
   const int tid = threadIdx.x, lane = tid & 63;
@@ -1318,53 +1326,88 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
   const int ln = lane & 15, lg = lane >> 4;
   const int G = gridDim.x, g0 = blockIdx.x;
   const int KS = p.K / KSTEP;
-  const int U = p.I / 8;
+  // FOLD (with ROWS; K / 256 even): units of 4 gate + 4 up columns, an item
+  // two k-steps of a unit: B columns n < 8 take the first k-step of the pair,
+  // columns n >= 8 the same 8 weight rows at the second, and A rows m >= 8
+  // hold x row m - 8 at the second (D[m][n] + D[m + 8][n + 8] is the item's
+  // product).  Twice the units per workgroup at the same item size: a
+  // workgroup's share of the 6720 config-3 items is 24 or 27 (at most 7 per
+  // SIMD) instead of 24 or 30 (8 per SIMD).
+  constexpr bool FOLD = ROWS;
+  constexpr int UC = FOLD ? 4 : 8;     // act columns per unit
+  const int KI = FOLD ? KS / 2 : KS;  // items per unit
+  constexpr int KI_STEP = FOLD ? 2 * KSTEP : KSTEP;
+  const int U = p.I / UC;
   const int nu = (U - g0 + G - 1) / G;  // >= 1: the grid has at most U workgroups
-  const int nitems = nu * KS;
+  const int nitems = nu * KI;
   const int xstride = p.K + 8;
   // item tiles [nitems][Mp / 4][16][4] (Mp = M rounded up to 4): lane (n, lg)
   // stores its rows 4 lg .. 4 lg + 3 of column n as one 16-byte write
+  // (FOLD: [nitems][2 halves][8 columns][8 rows], 512 bytes)
   const int mq = (p.M + 3) >> 2;
   float* red = reinterpret_cast<float*>(xs + p.M * xstride);
-  const int rsel = ln < 8 ? ln : p.I + ln - 8;  // row of unit u: 8u + rsel
+  // row of unit u for this lane's column: UC u + rsel
+  const int rsel = FOLD ? ((ln & 7) < 4 ? (ln & 7) : p.I + (ln & 7) - 4)
+                        : (ln < 8 ? ln : p.I + ln - 8);
   // Element e = row * K + k of item (unit i, k-step k) splits into a uniform
-  // part (8 (g0 + i G) K + 256 k) and this lane's constant part
-  // (rsel K + 64 lg): the weight bytes are the uniform base plus a 32-bit lane
-  // offset (no per-item vector address arithmetic), and so is the absmax index
-  // when the blocksize divides 256 (then it divides both parts).
-  const uint32_t lane_e = (uint32_t)rsel * (uint32_t)p.K + 64u * lg;
+  // part (UC (g0 + i G) K + KI_STEP k) and this lane's constant part
+  // (rsel K + 64 lg, + 256 for FOLD's columns n >= 8): the weight bytes are
+  // the uniform base plus a 32-bit lane offset (no per-item vector address
+  // arithmetic), and so is the absmax index when the blocksize divides 256
+  // (then it divides both parts).
+  const uint32_t lane_e = (uint32_t)rsel * (uint32_t)p.K + 64u * lg + (FOLD && ln >= 8 ? KSTEP : 0);
   const bool sep = p.bs_shift <= 8;
 
-  // x first (exactly GUU_XU chunks per thread, clamped), then the weights of
-  // this wave's first GUU_LA items; every item then issues the loads of the
-  // item GUU_LA ahead before it waits for its own.  All loads are
-  // unconditional (an item past the wave's last re-reads the last one), so
-  // each wait is exact: staging waits only for x, an item only for its own
-  // weights, and the decode of one item overlaps the loads of the next ones.
-  float code[16];
-#pragma unroll
-  for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
+  // x first (GUU_XU chunks per thread: clamped, or for ROWS only the lane's
+  // own), then the weights of this wave's first item; its next GUU_LA - 1
+  // items after the staging (a longer burst at entry delays the x loads the
+  // staging waits for); every item then issues the loads of the item GUU_LA
+  // ahead before it waits for its own.  The weight loads are unconditional
+  // (an item past the workgroup's last reads the codebook), so each wait is
+  // exact: staging waits only for x, an item only for its own weights, and
+  // the decode of one item overlaps the loads of the next ones.  The codebook (first needed by the first item) is
+  // loaded after the first item's weights: a scalar load issued earlier makes
+  // the waits for the kernel arguments that address the weights wait for it.
   const int chunks = p.K / 8, total = p.M * chunks;
   // RMSNorm source (NORM): every wave holds the group sums of squares of all
-  // rows, lane l those of row l / 8 (groups l % 8, l % 8 + 8); loaded first,
-  // unconditionally (clamped indexes, dropped in the sum)
-  // (four groups per float4 load: lane l takes float4s l % 8, l % 8 + 8, ...)
-  float4 ssv[GU_NORM_MAX_GROUPS / 32];
-  if (NORM) {
-    const float4* ssr = reinterpret_cast<const float4*>(p.nss + (int64_t)min(lane >> 3, p.M - 1) * p.nG);
-#pragma unroll
-    for (int q = 0; q < GU_NORM_MAX_GROUPS / 32; ++q)
-      ssv[q] = ssr[min((lane & 7) + 8 * q, (p.nG >> 2) - 1)];
-  }
+  // rows, lane l those of row l / 8 (four groups per float4 load: float4s
+  // l % 8, l % 8 + 8, ...), loaded first
+  constexpr int NSS = GU_NORM_MAX_GROUPS / 32;
+  float4 ssv[NSS];
   const uint16_t* xsrc = NORM ? p.nh : p.x;
   const int64_t xld = NORM ? p.ldnh : p.ldx;
+  const int sub = lane & 7, lrow = min(lane >> 3, p.M - 1);
+  if (NORM) {
+    const float4* ssr = reinterpret_cast<const float4*>(p.nss + (int64_t)lrow * p.nG);
+#pragma unroll
+    for (int q = 0; q < NSS; ++q)
+      if (ROWS) {
+        // conditional: no loads issued before these, so no wait depends on them
+        if (sub + 8 * q < (p.nG >> 2)) ssv[q] = ssr[sub + 8 * q];
+      } else {
+        ssv[q] = ssr[min(sub + 8 * q, (p.nG >> 2) - 1)];
+      }
+  }
+  // ROWS: this wave's chunk range [c_lo, c_hi), lane l chunks c_lo + l % 8 + 8 u
+  const int cpw = (chunks + W - 1) / W;
+  const int c_lo = min(wave * cpw, chunks), c_hi = min(c_lo + cpw, chunks);
   uint4 xv[GUU_XU], nwv[GUU_XU];
 #pragma unroll
   for (int u = 0; u < GUU_XU; ++u) {
-    const int i = min(u * NTH + tid, total - 1);
-    const int m = i / chunks, c = i - m * chunks;
-    xv[u] = *reinterpret_cast<const uint4*>(xsrc + (int64_t)m * xld + 8 * c);
-    if (NORM) nwv[u] = *reinterpret_cast<const uint4*>(p.nw + 8 * c);
+    if (ROWS) {
+      // conditional: the loads after these (the weights) are not, so the
+      // staging's wait for them is exact
+      const int c = c_lo + sub + 8 * u;
+      if (c < c_hi) {
+        xv[u] = *reinterpret_cast<const uint4*>(xsrc + (int64_t)lrow * xld + 8 * c);
+        if (NORM) nwv[u] = *reinterpret_cast<const uint4*>(p.nw + 8 * c);
+      }
+    } else {
+      const int i = min(u * NTH + tid, total - 1);
+      const int m = i / chunks, c = i - m * chunks;
+      xv[u] = *reinterpret_cast<const uint4*>(xsrc + (int64_t)m * xld + 8 * c);
+      if (NORM) nwv[u] = *reinterpret_cast<const uint4*>(p.nw + 8 * c);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   uint4 wv[2 * IPW];
@@ -1372,36 +1415,63 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
   // (unit slot, k-step) of this wave's item t = wave + W t, advanced without
   // divisions (uniform); items past the last re-read the last one
   const int qlast = nitems - 1;
-  const int il = qlast / KS, kl = qlast - il * KS;
-  int ci = wave / KS, ck = wave - ci * KS, cq = wave;  // item of the next load_item
+  int ci = wave / KI, ck = wave - ci * KI, cq = wave;  // item of the next load_item
   auto load_item = [&](int t) __attribute__((always_inline)) {
-    const int i = cq <= qlast ? ci : il, k = cq <= qlast ? ck : kl;
-    const uint32_t ue = (uint32_t)(8 * (g0 + i * G)) * (uint32_t)p.K + (uint32_t)(k * KSTEP);
-    const uint4* wp = reinterpret_cast<const uint4*>(p.w + (ue >> 1) + (lane_e >> 1));
+    // An item past the workgroup's last (the look-ahead of a wave's last
+    // item) loads the 64-byte codebook instead, an L2 hit: the epilogue
+    // reuses those registers, so it waits for these loads.
+    const bool past = cq > qlast;
+    const uint32_t ue = (uint32_t)(UC * (g0 + ci * G)) * (uint32_t)p.K + (uint32_t)(ck * KI_STEP);
+    const uint4* wp = past ? reinterpret_cast<const uint4*>(p.code16)
+                           : reinterpret_cast<const uint4*>(p.w + (ue >> 1) + (lane_e >> 1));
     wv[2 * t] = load_w<true>(wp);
     wv[2 * t + 1] = load_w<true>(wp + 1);
-    av[t] = sep ? (p.absmax + (ue >> p.bs_shift))[lane_e >> p.bs_shift]
-                : p.absmax[(ue + lane_e) >> p.bs_shift];
+    const float* ap = past ? p.code16
+                    : sep  ? p.absmax + (ue >> p.bs_shift) + (lane_e >> p.bs_shift)
+                           : p.absmax + ((ue + lane_e) >> p.bs_shift);
+    av[t] = *ap;
     cq += W;
     ck += W;
-    while (ck >= KS) {
-      ck -= KS;
+    while (ck >= KI) {
+      ck -= KI;
       ++ci;
     }
   };
+  load_item(0);  // the look-ahead's other items after the staging
+  __builtin_amdgcn_sched_barrier(0);
+  float code[16];
 #pragma unroll
-  for (int t = 0; t < GUU_LA && t < IPW; ++t) load_item(t);
+  for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
   // lane l: 1 / rms of row l / 8 (the row's sum over its 8 lanes by DPP)
   float inv_l = 0.f;
   if (NORM) {
     float ss = 0.f;
 #pragma unroll
-    for (int q = 0; q < GU_NORM_MAX_GROUPS / 32; ++q)
-      if ((lane & 7) + 8 * q < (p.nG >> 2)) ss += (ssv[q].x + ssv[q].y) + (ssv[q].z + ssv[q].w);
+    for (int q = 0; q < NSS; ++q)
+      if (sub + 8 * q < (p.nG >> 2)) ss += (ssv[q].x + ssv[q].y) + (ssv[q].z + ssv[q].w);
     ss = sum8(ss);
     inv_l = 1.f / sqrtf(ss / (float)p.K + p.neps);
   }
-  for (int base = 0; base < total; base += GUU_XU * NTH) {
+  if (ROWS) {
+    if ((lane >> 3) < p.M) {
+      const int m = lane >> 3;
+      for (int c0 = c_lo; c0 < c_hi; c0 += 8 * GUU_XU) {
+#pragma unroll
+        for (int u = 0; u < GUU_XU; ++u) {
+          const int c = c0 + sub + 8 * u;
+          if (c < c_hi) {
+            uint4 v = c0 == c_lo ? xv[u]
+                                 : *reinterpret_cast<const uint4*>(xsrc + (int64_t)m * xld + 8 * c);
+            if (NORM)
+              v = norm8(v, c0 == c_lo ? nwv[u] : *reinterpret_cast<const uint4*>(p.nw + 8 * c),
+                        inv_l);
+            *reinterpret_cast<uint4*>(xs + m * xstride + 8 * c) = deinterleave8(v);
+          }
+        }
+      }
+    }
+  }
+  for (int base = 0; !ROWS && base < total; base += GUU_XU * NTH) {
 #pragma unroll
     for (int u = 0; u < GUU_XU; ++u) {
       if (base + u * NTH >= total) break;
@@ -1415,17 +1485,21 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
       *reinterpret_cast<uint4*>(xs + m * xstride + 8 * c) = deinterleave8(v);
     }
   }
+#pragma unroll
+  for (int t = 1; t < GUU_LA && t < IPW; ++t) load_item(t);
   __syncthreads();
 
   const uint16_t* xrow[MT];
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) xrow[mt] = xs + min(16 * mt + ln, p.M - 1) * xstride + 64 * lg;
+  for (int mt = 0; mt < MT; ++mt)
+    xrow[mt] = FOLD ? xs + min(ln & 7, p.M - 1) * xstride + 64 * lg + (ln >= 8 ? KSTEP : 0)
+                    : xs + min(16 * mt + ln, p.M - 1) * xstride + 64 * lg;
   const int my_items = (nitems - wave + W - 1) / W;  // items of this wave (may be 0)
 #pragma unroll
   for (int t = 0; t < IPW; ++t) {
     if (t >= my_items) break;
     if (t + GUU_LA < IPW) load_item(t + GUU_LA);
-    const int k = (wave + W * t) % KS;
+    const int k = (wave + W * t) % KI;
     const Lut lt = make_lut(code, av[t]);
     f32x4_t acc[MT];
 #pragma unroll
@@ -1435,29 +1509,60 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
       const uint4 bw = decode8(word(wv[2 * t + (j >> 2)], j & 3), lt);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
-        acc[mt] = mfma16x16x32(*reinterpret_cast<const uint4*>(xrow[mt] + k * KSTEP + 8 * j), bw,
-                               acc[mt]);
+        acc[mt] = mfma16x16x32(*reinterpret_cast<const uint4*>(xrow[mt] + k * KI_STEP + 8 * j),
+                               bw, acc[mt]);
     }
     // lane (n = ln, group lg) holds D[m = 16 mt + 4 lg + r][n]
     const int q = wave + W * t;
+    if (FOLD) {
+      // item tile [2 halves][8 columns][8 rows]: half h = n / 8 from the
+      // lanes with rows 8 h .. 8 h + 7 (lg / 2 == h)
+      if ((ln >> 3) == (lg >> 1))
+        *reinterpret_cast<f32x4_t*>(red + q * 128 + (ln >> 3) * 64 + (ln & 7) * 8 + 4 * (lg & 1)) =
+            acc[0];
+    } else {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-      if (4 * mt + lg < mq)
-        *reinterpret_cast<f32x4_t*>(red + ((q * mq + 4 * mt + lg) * 16 + ln) * 4) = acc[mt];
+      for (int mt = 0; mt < MT; ++mt)
+        if (4 * mt + lg < mq)
+          *reinterpret_cast<f32x4_t*>(red + ((q * mq + 4 * mt + lg) * 16 + ln) * 4) = acc[mt];
+    }
   }
   __syncthreads();
-  for (int i = tid; i < nu * p.M * 8; i += NTH) {
-    const int un = i / (p.M * 8), rem = i - un * p.M * 8;
-    const int m = rem >> 3, n = rem & 7;
+  // (unit, row, column) outputs, output i to thread i mod NTH: FOLD, i =
+  // 32 un + 4 m + n (column n < 4 of the unit: gate n, up n + 4, each the sum
+  // of the two halves of its items); otherwise i = (un M + m) 8 + n (gate n,
+  // up n + 8).  The sums run over the unit's k-steps in order.
+  const int nout = FOLD ? nu * 32 : nu * p.M * 8;
+  for (int i = tid; i < nout; i += NTH) {
+    int un, m, n;
+    if (FOLD) {
+      un = i >> 5;
+      m = (i >> 2) & 7;
+      n = i & 3;
+      if (m >= p.M) continue;
+    } else {
+      un = i / (p.M * 8);
+      const int rem = i - un * p.M * 8;
+      m = rem >> 3;
+      n = rem & 7;
+    }
     float g = 0.f, u = 0.f;
-    for (int k = 0; k < KS; ++k) {
-      const float* tile = red + ((un * KS + k) * mq + (m >> 2)) * 64 + (m & 3);
-      g += tile[4 * n];
-      u += tile[4 * (n + 8)];
+    for (int k = 0; k < KI; ++k) {
+      if (FOLD) {
+        const float* tile = red + (un * KI + k) * 128 + m;
+        g += tile[8 * n];
+        g += tile[64 + 8 * n];
+        u += tile[8 * (n + 4)];
+        u += tile[64 + 8 * (n + 4)];
+      } else {
+        const float* tile = red + ((un * KI + k) * mq + (m >> 2)) * 64 + (m & 3);
+        g += tile[4 * n];
+        u += tile[4 * (n + 8)];
+      }
     }
     const float gv = round_bf(g);
     const float o = round_bf(gv * (1.f / (1.f + expf(-gv)))) * round_bf(u);
-    store_act(p, m, 8 * (g0 + un * G) + n, o);
+    store_act(p, m, UC * (g0 + un * G) + n, o);
   }
 }
 
@@ -1816,24 +1921,41 @@ struct GuPlan {
   size_t lds;
 };
 
+// Work split of nf4_gate_up_units: rows <= its waves with an even number of
+// k-steps take the folded units (4 + 4 columns, two k-steps per item, one
+// staged x row per wave), other shapes units of 8 + 8 columns, one k-step per
+// item.  U units over G <= CU-count workgroups, nu per workgroup, KI items
+// per unit, `tile` LDS bytes per item partial.
+bool units_fold(int M, int K) { return M <= std::min(GU_UNITS_W, 8) && (K / KSTEP) % 2 == 0; }
+struct UnitsShape {
+  int U, KI, G, nu;
+  size_t tile;
+};
+UnitsShape units_shape(int M, int I, int K) {
+  const bool f = units_fold(M, K);
+  UnitsShape u;
+  u.U = I / (f ? 4 : 8);
+  u.KI = K / KSTEP / (f ? 2 : 1);
+  u.G = std::min(u.U, g_gu_units_grid);
+  u.nu = (u.U + u.G - 1) / u.G;
+  u.tile = f ? 512 : (size_t)((M + 3) / 4 * 4) * 16 * 4;
+  return u;
+}
+
 // LDS of nf4_gate_up_units (x, then the item tiles) and whether it takes the
-// shape (units of 8 columns over at most one workgroup per CU, every item of
-// a wave in registers, 64 KiB of LDS).
+// shape (at most one workgroup per CU, every item of a wave in registers, 64
+// KiB of LDS up to 16 rows).
 size_t units_lds(int M, int I, int K) {
-  const int U = I / 8, KS = K / KSTEP;
-  const int G = std::min(U, g_gu_units_grid);
-  const int nu = (U + G - 1) / G;
-  return (size_t)M * (K + 8) * 2 + (size_t)nu * KS * ((M + 3) / 4 * 4) * 16 * 4;
+  const UnitsShape u = units_shape(M, I, K);
+  return (size_t)M * (K + 8) * 2 + (size_t)u.nu * u.KI * u.tile;
 }
 bool units_ok(int M, int I, int K) {
   if (M < 1 || M > 32 || I <= 0 || I % 8 || K <= 0 || K % KSTEP) return false;
   if ((int64_t)2 * I * K >= ((int64_t)1 << 32)) return false;  // 32-bit element offsets
-  const int U = I / 8, KS = K / KSTEP;
-  const int G = std::min(U, g_gu_units_grid);
-  const int nu = (U + G - 1) / G;
+  const UnitsShape u = units_shape(M, I, K);
   // up to 16 rows in 64 KiB of LDS; 17..32 rows (two row tiles) in up to 160 KiB
   const size_t cap = M <= 16 ? 65536 : (size_t)PART_LDS_BIG;
-  return (nu * KS + GU_UNITS_W - 1) / GU_UNITS_W <= GU_UNITS_IPW && units_lds(M, I, K) <= cap;
+  return (u.nu * u.KI + GU_UNITS_W - 1) / GU_UNITS_W <= GU_UNITS_IPW && units_lds(M, I, K) <= cap;
 }
 
 // 17..32 rows on the unit kernel with two row tiles (x and the item tiles in LDS).
@@ -2501,8 +2623,7 @@ int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absma
   }
   {
     // units kernel: at most one workgroup per CU, every item of a wave in registers
-    const int U = I / 8, KS = K / KSTEP;
-    const int G = std::min(U, g_gu_units_grid);
+    const int G = units_shape(M, I, K).G;
     const size_t lds = units_lds(M, I, K);
     if (units2) {
       if (int rc = allow_big_lds(nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, false, 2>)) return rc;
@@ -2511,8 +2632,15 @@ int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absma
       return launch_check("nf4_gate_up_units");
     }
     if (units_ok(M, I, K)) {
-      if (nrm)
+      const bool rows = units_fold(M, K);  // folded units, one staged x row per wave
+      if (nrm && rows)
+        nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, true, 1, true>
+            <<<dim3((unsigned)G), 64 * GU_UNITS_W, lds, st>>>(a);
+      else if (nrm)
         nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, true>
+            <<<dim3((unsigned)G), 64 * GU_UNITS_W, lds, st>>>(a);
+      else if (rows)
+        nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, false, 1, true>
             <<<dim3((unsigned)G), 64 * GU_UNITS_W, lds, st>>>(a);
       else
         nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, false>

@@ -328,7 +328,14 @@ class DecodeEngine:
                         "last K slice finishes + residual)")
             return "nf4_part_mfma (split-K)"
         if kind == "gate_up":
-            return "nf4_gate_up (SiLU*up fused)" if self.gu_fused else "nf4_part_mfma (split-K)"
+            if not self.gu_fused:
+                return "nf4_part_mfma (split-K)"
+            if self.B <= 8 and (self.H // 256) % 2 == 0:
+                return ("nf4_gate_up_units (4+4-column units of two k-steps"
+                        + (", input RMSNorm staged" if self.fold else "") + ", SiLU*up fused)")
+            if self.B <= 16 or (self.B <= 32 and self.B * (self.H + 8) * 2 <= 120 * 1024):
+                return "nf4_gate_up_units (8+8-column units, SiLU*up fused)"
+            return "nf4_gate_up_wide (x in 512-column chunks, SiLU*up fused)"
         if kind == "down":
             return ("nf4_fold_residual (whole K per 8 columns, residual)" if self.fold
                     else "nf4_part_mfma (split-K)")
