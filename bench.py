@@ -244,9 +244,10 @@ def _emit(args, value, unit, ms_step, workload, extra):
 def run_cfg4(args):
     """G = 32 (4 prompts x 8 samples), prompts U[128, 512],
     responses lognormal (median 200, sigma 0.75) capped at 1024, blocks reserved
-    one block ahead and freed as rows stop (DecodeEngine.run_paged).  One timed
-    step = one rollout: fork the 8 samples of each prefilled prompt, decode until
-    every row stops (blocks released on the way)."""
+    one block ahead and freed as rows stop (DecodeEngine.run_paged), the rows
+    still decoding moved to a 16- and then an 8-row engine once they fit.  One
+    timed step = one rollout: fork the 8 samples of each prefilled prompt,
+    decode until every row stops (blocks released on the way)."""
     import numpy as np
     import torch
 
@@ -273,6 +274,9 @@ def run_cfg4(args):
     parents = [prefill(pre, pool, tuple(p), width) for p in prompts]
     del pre
     eng = DecodeEngine(model, pool, G, width)
+    # row compaction: the rows still decoding move to a 16- and then an 8-row
+    # engine once they fit (the long tail of the group runs on the cheaper step)
+    ladder = eng.compaction_engines((16, 8))
     rows = [prompts[i // S] for i in range(G)]
 
     def rollout():
@@ -287,14 +291,14 @@ def run_cfg4(args):
     eng.capture()
     peak = 0
     for _ in range(args.warmup):
-        eng.run_paged(sids, NEW)
+        eng.run_paged(sids, NEW, compact=ladder)
         sids = rollout()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    nsteps = 0
+    nsteps, engines = 0, []
     for i in range(args.steps):
-        st = eng.run_paged(sids, NEW)
-        nsteps, peak = st["steps"], st["peak_blocks"]
+        st = eng.run_paged(sids, NEW, compact=ladder)
+        nsteps, peak, engines = st["steps"], st["peak_blocks"], st["engines"]
         if i + 1 < args.steps:
             sids = rollout()
     torch.cuda.synchronize()
@@ -308,6 +312,7 @@ def run_cfg4(args):
           "U[128,512], responses lognormal(median 200, sigma 0.75) capped at 1024, blocks "
           "freed as rows stop; step = one ragged rollout",
           dict(prompt_lens=lens, response_tokens=sum(stops), decode_steps_per_rollout=nsteps,
+               engines_rows=engines,
                us_per_decode_step=round(elapsed / args.steps / max(nsteps, 1) * 1e6, 2),
                peak_blocks=peak, pool_blocks=pool.num_blocks))
 

@@ -782,8 +782,48 @@ class DecodeEngine:
         for _ in range(steps):
             self.step()
 
+    def compaction_engines(self, sizes=(16, 8)) -> list:
+        """Greedy engines of fewer rows (``sizes`` below this engine's) over the
+        same model, pool and block-table width, for ``run_paged(...,
+        compact=...)``: once the rows still decoding fit a smaller engine,
+        their state moves there and the rollout goes on with that engine's
+        cheaper step.  Sampling engines are not compacted: a row's draws are
+        keyed by its row index, which compaction changes."""
+        if self.sampling:
+            raise ValueError("row compaction renumbers rows, which changes sampled draws "
+                             "(keyed by the row index); it is for greedy decoding")
+        return [DecodeEngine(self.model, self.pool, n, self.max_blocks, max_pos=self.max_pos)
+                for n in sorted({int(n) for n in sizes if 0 < int(n) < self.B}, reverse=True)]
+
+    def _ready_for(self, width: int) -> None:
+        """A generated buffer of ``width`` columns and a captured step, every row idle."""
+        if self.graph is not None and self.generated is not None and \
+                self.generated.shape[1] == width:
+            return
+        B, dev = self.B, self.device
+        z = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.start(z, z, torch.full((B, 1), -1, dtype=torch.int32, device=dev), z, width)
+        self.capture()
+
+    def _take_rows(self, src: "DecodeEngine", rows: list) -> None:
+        """Rows ``rows`` of ``src`` (state, block tables, tokens generated so
+        far) become rows 0 .. len(rows) - 1 of this engine; the others idle."""
+        n = len(rows)
+        idx = torch.tensor(rows, dtype=torch.long, device=self.device)
+        for name in ("tokens", "pos", "count", "limit", "active"):
+            dst = getattr(self, name)
+            dst.zero_()
+            dst[:n].copy_(getattr(src, name).index_select(0, idx))
+        self.eos.copy_(src.eos)
+        self.pad.copy_(src.pad)
+        self.block_tables.fill_(-1)
+        self.block_tables[:n].copy_(src.block_tables.index_select(0, idx))
+        self.generated.copy_(src.pad.view(1, 1).expand_as(self.generated))
+        self.generated[:n].copy_(src.generated.index_select(0, idx))
+        self._masks()
+
     def run_paged(self, sids: list, max_steps: int, chunk: Optional[int] = None,
-                  check_invariants: bool = False) -> dict:
+                  check_invariants: bool = False, compact: Optional[list] = None) -> dict:
         """Decode until every row has stopped (or ``max_steps``), allocating each
         row's KV blocks one chunk ahead and releasing them when the row stops.
 
@@ -799,44 +839,78 @@ class DecodeEngine:
         whole call instead (``paged_kv.py:626-645``); BASELINE config 4 asks
         for blocks allocated and freed as sequences finish.
 
-        Returns ``dict(steps, peak_blocks)``: decode steps run and the most
-        blocks in use at once.
+        ``compact`` (engines from ``compaction_engines``): at a chunk boundary
+        where the rows still decoding fit a smaller engine, they move to the
+        smallest that holds them (``_take_rows``) and the following steps run
+        on it; at the end every row's tokens are back in this engine's
+        ``generated``.  A long-tailed group (config 4: lognormal lengths, most
+        rows done long before the longest) then spends its tail on the step of
+        8 rows instead of 32.  Each row's arithmetic is its own in every
+        engine, but the engines' kernels sum in different orders, so a token
+        can differ where the top two logits are within rounding.
+
+        Returns ``dict(steps, peak_blocks, engines)``: decode steps run, the
+        most blocks in use at once and the row counts of the engines used.
         """
         pool = self.pool
         chunk = chunk or pool.block_size
+        ladder = sorted((e for e in (compact or ()) if e.B < self.B), key=lambda e: e.B)
+        eng, used = self, [self]
+        origin = list(range(len(sids)))  # row of eng -> row of this engine
         live = {b: s for b, s in enumerate(sids)}
         steps = peak = 0
         while True:
-            pos = self.pos.cpu().tolist()
-            act = self.active.cpu().tolist()
+            pos = eng.pos.cpu().tolist()
+            act = eng.active.cpu().tolist()
             for b in [b for b in live if not act[b]]:
                 pool.free(live.pop(b))
-                self.block_tables[b].fill_(-1)
+                eng.block_tables[b].fill_(-1)
             if not live or steps >= max_steps:
                 break
+            fit = [e for e in ladder if len(live) <= e.B < eng.B]
+            if fit:
+                dst = fit[0]
+                dst._ready_for(self.generated.shape[1])
+                if eng is not self:
+                    self._put_back(eng, origin)
+                rows = sorted(live)
+                dst._take_rows(eng, rows)
+                origin = [origin[b] for b in rows]
+                live = {i: live[b] for i, b in enumerate(rows)}
+                pos = [pos[b] for b in rows]
+                eng = dst
+                used.append(dst)
             n = min(chunk, max_steps - steps)
             for b, sid in live.items():
                 have = len(pool.blocks[sid])
                 pool.set_length(sid, pos[b])
                 pool.reserve(sid, pos[b] + n)  # slots pos .. pos + n - 1
                 bl = pool.blocks[sid]
-                if len(bl) > self.max_blocks:
+                if len(bl) > eng.max_blocks:
                     raise RuntimeError(f"row {b} needs {len(bl)} blocks; the engine's block "
-                                       f"table holds {self.max_blocks}")
+                                       f"table holds {eng.max_blocks}")
                 if len(bl) > have:
-                    self.block_tables[b, have:len(bl)].copy_(
+                    eng.block_tables[b, have:len(bl)].copy_(
                         torch.tensor(bl[have:], dtype=torch.int32))
             if check_invariants:
                 pool.check_invariants()
             peak = max(peak, pool.num_blocks - pool.num_free)
             for _ in range(n):
-                self.step()
+                eng.step()
             steps += n
         for b in list(live):  # rows cut off by max_steps
             pool.free(live.pop(b))
-            self.block_tables[b].fill_(-1)
-        self.verify_handover()
-        return dict(steps=steps, peak_blocks=peak)
+            eng.block_tables[b].fill_(-1)
+        if eng is not self:
+            self._put_back(eng, origin)
+        for e in used:
+            e.verify_handover()
+        return dict(steps=steps, peak_blocks=peak, engines=[e.B for e in used])
+
+    def _put_back(self, eng: "DecodeEngine", origin: list) -> None:
+        """Copy rows 0 .. len(origin) - 1 of ``eng.generated`` to this engine's rows ``origin``."""
+        idx = torch.tensor(origin, dtype=torch.long, device=self.device)
+        self.generated.index_copy_(0, idx, eng.generated[:len(origin)])
 
 
 class PrefillEngine(DecodeEngine):

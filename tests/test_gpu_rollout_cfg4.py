@@ -133,7 +133,8 @@ def test_cfg4_blocks_allocated_ahead_and_freed(dev):
         assert np.all(gen[b, s:] == 0) and np.all(gen[b, :s] >= 0)
 
 
-def test_cfg4_headline_shape_ragged_group_matches_oracle(dev):
+@pytest.mark.parametrize("compact", [False, True])
+def test_cfg4_headline_shape_ragged_group_matches_oracle(dev, compact):
     """Config 4's recipe on the Qwen2-1.5B shape (two layers): G = 32 rows = 4
     prompts x 8 samples, prompts U[128, 512], lognormal stops (sigma 0.75,
     median scaled to 24 and capped at 48 steps for test time), chunked prefill
@@ -144,7 +145,10 @@ def test_cfg4_headline_shape_ragged_group_matches_oracle(dev):
     batched as 4 rows of one step): at every step of every row the GPU's token
     equals the oracle's argmax wherever the oracle's top-2 margin exceeds 1e-2
     of max|logit|; the 8 samples of a prompt are equal up to their stops and
-    pad after; every block returns to the free list."""
+    pad after; every block returns to the free list.  With ``compact`` the rows
+    still decoding move to a 16- and then an 8-row engine once they fit
+    (``run_paged(compact=...)``), so their later tokens come from those
+    engines' steps."""
     from grpo_mi355x.core.kv_pool import PagedKVPool
     from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill
     from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
@@ -186,8 +190,11 @@ def test_cfg4_headline_shape_ragged_group_matches_oracle(dev):
     eng.start(**start)
     eng.capture()
     eng.start(**start)
-    stats = eng.run_paged(sids, new, check_invariants=True)
+    stats = eng.run_paged(sids, new, check_invariants=True,
+                          compact=eng.compaction_engines((16, 8)) if compact else None)
     torch.cuda.synchronize()
+    if compact:  # 10 rows left after 32 steps
+        assert stats["engines"] == [32, 16]
     assert pool.num_free == pool.num_blocks and not pool.blocks
     gen = eng.generated.cpu().numpy()
     for b in range(B):
@@ -271,7 +278,8 @@ def _oracle_check_steps(oracle, prompt, gen, steps, width, chunk=256):
 
 
 @pytest.mark.timeout(600)
-def test_cfg4_long_tail_rows_match_oracle_at_sampled_steps(dev):
+@pytest.mark.parametrize("compact", [False, True])
+def test_cfg4_long_tail_rows_match_oracle_at_sampled_steps(dev, compact):
     """Config 4's long tail on the Qwen2-1.5B shape (two layers): G = 32 rows =
     4 prompts x 8 samples, prompts U[128, 512], lognormal stops (median 200,
     sigma 0.75, capped at 1024) with one row of prompt 0 running 1160 tokens, so
@@ -281,7 +289,8 @@ def test_cfg4_long_tail_rows_match_oracle_at_sampled_steps(dev):
     oracle, teacher-forced on the GPU's tokens, recomputes the long row at
     steps 0, 255, 511, 767, 1023 and 1159 and each other prompt's longest row
     at its last step: the GPU's token equals the oracle's argmax wherever the
-    oracle's top-2 margin exceeds 1e-2 of max|logit|."""
+    oracle's top-2 margin exceeds 1e-2 of max|logit|.  With ``compact`` the
+    long row spends its tail on the 8-row engine (``run_paged(compact=...)``)."""
     from grpo_mi355x.core.kv_pool import PagedKVPool
     from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill
     from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
@@ -317,8 +326,12 @@ def test_cfg4_long_tail_rows_match_oracle_at_sampled_steps(dev):
     eng.start(**start)
     eng.capture()
     eng.start(**start)
-    stats = eng.run_paged(sids, new, check_invariants=True)  # also checks the hand-overs
+    # also checks the hand-overs of every engine used
+    stats = eng.run_paged(sids, new, check_invariants=True,
+                          compact=eng.compaction_engines((16, 8)) if compact else None)
     torch.cuda.synchronize()
+    if compact:
+        assert stats["engines"][0] == 32 and stats["engines"][-1] == 8
     assert long_steps <= stats["steps"] <= long_steps + 16
     assert pool.num_free == pool.num_blocks and not pool.blocks
     gen = eng.generated.cpu().numpy()

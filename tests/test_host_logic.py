@@ -158,7 +158,7 @@ def test_run_paged_reserves_ahead_and_frees_stopped_rows():
 
     class Stand:
         def __init__(self):
-            self.pool, self.max_blocks = pool, 8
+            self.pool, self.max_blocks, self.B = pool, 8, 3
             self.pos = torch.full((3,), 6, dtype=torch.int32)
             self.count = torch.zeros(3, dtype=torch.int32)
             self.active = torch.ones(3, dtype=torch.bool)
@@ -190,6 +190,91 @@ def test_run_paged_reserves_ahead_and_frees_stopped_rows():
     assert stats["peak_blocks"] <= 1 + 3 + 2 + 2 + 5
     assert pool.num_free == pool.num_blocks and not pool.blocks
     assert torch.all(s.block_tables == -1)
+
+
+def test_run_paged_compaction_moves_live_rows_to_smaller_engines():
+    """run_paged with compaction engines (host stand-ins for the graph step,
+    whose next token depends only on the row's own token and position): once
+    the rows still decoding fit a smaller engine, their state moves to the
+    smallest that holds them; every row's tokens end up in the first engine's
+    ``generated``, equal to a run without compaction, blocks are still
+    reserved one chunk ahead and all freed, and every engine used has its
+    hand-overs checked."""
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine
+
+    limits = [3, 40, 9, 17, 2, 33, 5, 21]
+
+    class Stand:
+        _take_rows = DecodeEngine._take_rows
+        _put_back = DecodeEngine._put_back
+        _masks = DecodeEngine._masks
+
+        def __init__(self, pool, B):
+            self.pool, self.B, self.max_blocks, self.device = pool, B, 16, torch.device("cpu")
+            i32 = dict(dtype=torch.int32)
+            self.tokens = torch.zeros(B, dtype=torch.int64)
+            self.pos, self.count, self.limit = (torch.zeros(B, **i32) for _ in range(3))
+            self.append_pos, self.attn_len = torch.zeros(B, **i32), torch.zeros(B, **i32)
+            self.active = torch.zeros(B, dtype=torch.bool)
+            self.eos = torch.full((1,), -1, dtype=torch.int64)
+            self.pad = torch.full((1,), 7, dtype=torch.int64)
+            self.block_tables = torch.full((B, 16), -1, **i32)
+            self.generated, self.graph = None, None
+            self.steps_run = self.verified = 0
+
+        def _ready_for(self, width):
+            if self.generated is None:
+                self.generated = torch.full((self.B, width), 7, dtype=torch.int64)
+            self.graph = True
+
+        def verify_handover(self):
+            self.verified += 1
+
+        def step(self):
+            self.steps_run += 1
+            for b in range(self.B):
+                if not self.active[b]:
+                    continue
+                blk = int(self.block_tables[b, int(self.pos[b]) // 4])
+                assert blk >= 0 and self.pool.refcount[blk] == 1
+                nxt = (int(self.tokens[b]) * 31 + int(self.pos[b])) % 1000
+                self.generated[b, int(self.count[b])] = nxt
+                self.tokens[b] = nxt
+                self.pos[b] += 1
+                self.count[b] += 1
+                if int(self.count[b]) >= int(self.limit[b]):
+                    self.active[b] = False
+            self._masks()
+
+    def run(compact):
+        pool = PagedKVPool(1, 256, 1, 8, block_size=4)
+        parent = pool.allocate(6)
+        pool.set_length(parent, 6)
+        sids = pool.fork(parent, 8, reserve_tokens=7)
+        pool.free(parent)
+        big = Stand(pool, 8)
+        big._ready_for(48)
+        big.tokens.copy_(torch.arange(8) + 5)
+        big.pos.fill_(6)
+        big.limit.copy_(torch.tensor(limits))
+        big.active.copy_(big.limit > 0)
+        big.block_tables.copy_(pool.block_table(sids, 16))
+        big._masks()
+        ladder = [Stand(pool, 4), Stand(pool, 2)] if compact else None
+        stats = DecodeEngine.run_paged(big, sids, 48, check_invariants=True, compact=ladder)
+        assert pool.num_free == pool.num_blocks and not pool.blocks
+        return big, stats, ladder
+
+    ref, st0, _ = run(False)
+    big, st1, ladder = run(True)
+    assert torch.equal(big.generated, ref.generated)
+    assert [int((ref.generated[b] != 7).sum()) for b in range(8)] == limits
+    assert st0["engines"] == [8] and st1["engines"] == [8, 4, 2]
+    assert st1["steps"] == st0["steps"] == 40
+    # 4 rows left after 12 steps, 2 after 24: the 2-row engine ran the last 16
+    assert (big.steps_run, ladder[0].steps_run, ladder[1].steps_run) == (12, 12, 16)
+    assert big.verified == 1 and all(e.verified == 1 for e in ladder)
 
 
 def test_torch_advance_stays_inside_the_generated_buffer():
