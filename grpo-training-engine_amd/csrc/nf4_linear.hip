@@ -1487,14 +1487,6 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
   }
 #pragma unroll
   for (int t = 1; t < GUU_LA && t < IPW; ++t) load_item(t);
-  // ROWS: the first item's weights are decoded before the barrier, in the
-  // SIMD's idle time while the other waves finish their staging
-  uint4 bw0[8];
-  if (ROWS) {
-    const Lut lt0 = make_lut(code, av[0]);
-#pragma unroll
-    for (int j = 0; j < 8; ++j) bw0[j] = decode8(word(wv[j >> 2], j & 3), lt0);
-  }
   __syncthreads();
 
   const uint16_t* xrow[MT];
@@ -1508,14 +1500,13 @@ __global__ void __launch_bounds__(64 * W) nf4_gate_up_units(GuArgs p) {
     if (t >= my_items) break;
     if (t + GUU_LA < IPW) load_item(t + GUU_LA);
     const int k = (wave + W * t) % KI;
-    const bool pre = ROWS && t == 0;  // decoded before the barrier
-    const Lut lt = make_lut(code, pre ? 0.f : av[t]);
+    const Lut lt = make_lut(code, av[t]);
     f32x4_t acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const uint4 bw = pre ? bw0[j] : decode8(word(wv[2 * t + (j >> 2)], j & 3), lt);
+      const uint4 bw = decode8(word(wv[2 * t + (j >> 2)], j & 3), lt);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
         acc[mt] = mfma16x16x32(*reinterpret_cast<const uint4*>(xrow[mt] + k * KI_STEP + 8 * j),
