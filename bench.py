@@ -474,9 +474,10 @@ def run_cfg1(args):
     shuffled block tables, q/K/V ~ N(0, 1) bf16, float32 softmax and output.
 
     R independent instances (own pool, table permutation, q) of >= 512 MB in
-    total are launched back to back (``grpo_paged_attn_decode``: the split
-    kernel and the merge), so no call finds its K/V in the 256 MB MALL.  One
-    step = one replay of the R calls."""
+    total are launched back to back (``grpo_paged_attn_decode_merged``: one
+    launch per call, the last-arriving context split of each (sequence, KV
+    head) merging the pair's splits), so no call finds its K/V in the 256 MB
+    MALL.  One step = one replay of the R calls."""
     import numpy as np
     import torch
 
@@ -515,6 +516,7 @@ def run_cfg1(args):
     us = _eager_time(fns, dev, max(args.steps, 1)) if args.eager else \
         _graph_time(fns, dev, max(args.steps, 1) * 5)
     achieved = call_bytes / (us * 1e-6) / 1e9
+    ops.attention_handover_check(dev)  # the in-kernel merges ran on one XCD per pair
     log(f"config 1: {R} rotating instances, {us:.2f} us per call, {achieved:.1f} GB/s")
     cpu = None
     if not args.no_cpu_baseline:
@@ -548,8 +550,8 @@ def run_cfg1(args):
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                      "traffic": measured_traffic(ATTN_TRAFFIC_FILE),
-                     "kernel": "grpo_paged_attn_decode: paged_attn_split + paged_attn_merge "
-                               "per call"},
+                     "kernel": "grpo_paged_attn_decode_merged: paged_attn_split with the "
+                               "in-kernel merge (one launch per call)"},
         "cpu_baseline": cpu}), flush=True)
 
 

@@ -82,6 +82,7 @@ struct AttnArgs {
   int* mcnt;
   int* xcd_err;
   uint16_t* mout;
+  float* mout_f32;  // float32 merge output [B][Hq * D] instead of mout (plain attention)
   // ... and, with lora_r > 0, the pair's share of the next linear's LoRA-A
   // product: lora_t[b][kvh][r] = sum over the pair's Hq / Hkv heads of
   // mout[b, k] * lora_a[r][k] (float32; the consumer sums the Hkv shares)
@@ -519,7 +520,12 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
       O.z += f[w] * v.z;
       O.w += f[w] * v.w;
     }
-    if (p.direct_out || single) {
+    if (single && p.mout_f32) {
+      // the whole context in this split, float32 output: out = O / max(L, 1e-6)
+      const float den = fmaxf(L, 1e-6f);
+      *reinterpret_cast<float4*>(p.mout_f32 + ((int64_t)b * p.Hq + kvh * GQ + h) * FD + d4) =
+          make_float4(O.x / den, O.y / den, O.z / den, O.w / den);
+    } else if (p.direct_out || single) {
       // the whole context in this split: out = O / max(L, 1e-6), bf16
       const float den = fmaxf(L, 1e-6f);
       const uint2 ov = make_uint2(pack_bf2(O.x / den, O.y / den), pack_bf2(O.z / den, O.w / den));
@@ -584,12 +590,18 @@ __global__ void __launch_bounds__(AT) paged_attn_split(AttnArgs p) {
           }
       }
       const float den = fmaxf(L, 1e-6f);
-      const uint2 o2 = make_uint2(pack_bf2(O.x / den, O.y / den), pack_bf2(O.z / den, O.w / den));
-      *reinterpret_cast<uint2*>(p.mout + ((int64_t)b * p.Hq + kvh * GQ + mh) * FD + md4) = o2;
-      xr[0] = bf_lo(o2.x);
-      xr[1] = bf_hi(o2.x);
-      xr[2] = bf_lo(o2.y);
-      xr[3] = bf_hi(o2.y);
+      if (p.mout_f32) {
+        *reinterpret_cast<float4*>(p.mout_f32 + ((int64_t)b * p.Hq + kvh * GQ + mh) * FD + md4) =
+            make_float4(O.x / den, O.y / den, O.z / den, O.w / den);
+      } else {
+        const uint2 o2 =
+            make_uint2(pack_bf2(O.x / den, O.y / den), pack_bf2(O.z / den, O.w / den));
+        *reinterpret_cast<uint2*>(p.mout + ((int64_t)b * p.Hq + kvh * GQ + mh) * FD + md4) = o2;
+        xr[0] = bf_lo(o2.x);
+        xr[1] = bf_hi(o2.x);
+        xr[2] = bf_lo(o2.y);
+        xr[3] = bf_hi(o2.y);
+      }
     }
   }
   if (p.lora_r <= 0) return;
@@ -885,6 +897,58 @@ extern "C" int grpo_paged_attn_decode(const void* q, int64_t q_stride_b, int64_t
   a.S = 1;
   paged_attn_generic<<<dim3(Hq, B), GEN_T, 0, st>>>(a);
   return launch_check("paged_attn_generic");
+}
+
+extern "C" int grpo_paged_attn_decode_merged(
+    const void* q, int64_t q_stride_b, int64_t q_stride_h, const void* k_cache,
+    const void* v_cache, int64_t num_blocks, const int32_t* block_tables, int64_t bt_stride,
+    const int32_t* context_lens, void* out, int out_bf16, int B, int Hq, int Hkv, int D,
+    int block_size, int max_blocks, float scale, void* workspace, size_t workspace_bytes,
+    int* counters, int* xcd_err, grpo_stream_t stream) {
+  const AttnPlan plan = plan_attn(B > 0 ? B : 1, Hq > 0 ? Hq : 1, Hkv > 0 ? Hkv : 1,
+                                  D > 0 ? D : 1, block_size > 0 ? block_size : 1, max_blocks);
+  const bool aligned = (reinterpret_cast<uintptr_t>(q) & 15u) == 0 && q_stride_b % 8 == 0 &&
+                       q_stride_h % 8 == 0 && (reinterpret_cast<uintptr_t>(k_cache) & 15u) == 0 &&
+                       (reinterpret_cast<uintptr_t>(v_cache) & 15u) == 0 &&
+                       (reinterpret_cast<uintptr_t>(out) & 15u) == 0;
+  if (B <= 0 || Hq <= 0 || Hkv <= 0 || Hq % Hkv != 0 || !plan.fast || !aligned ||
+      max_blocks <= 0 || !q || !k_cache || !v_cache || !block_tables || !context_lens || !out)
+    // one launch already (the generic kernel), or an argument error it reports
+    return grpo_paged_attn_decode(q, q_stride_b, q_stride_h, k_cache, v_cache, num_blocks,
+                                  block_tables, bt_stride, context_lens, out, out_bf16, B, Hq,
+                                  Hkv, D, block_size, max_blocks, scale, workspace,
+                                  workspace_bytes, stream);
+  if (num_blocks < 0) return einval("bad attention dimensions");
+  if (!counters || !xcd_err) return einval("the in-kernel merge needs its counters and error word");
+  if ((reinterpret_cast<uintptr_t>(counters) & 127u) != 0)
+    return einval("merge counters must be 128-byte aligned");
+  AttnArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.qsb = q_stride_b;
+  a.qsh = q_stride_h;
+  a.kc = static_cast<uint16_t*>(const_cast<void*>(k_cache));
+  a.vc = static_cast<uint16_t*>(const_cast<void*>(v_cache));
+  a.num_blocks = num_blocks;
+  a.bt = block_tables;
+  a.bts = bt_stride;
+  a.cl = context_lens;
+  a.out = out;
+  a.out_bf16 = out_bf16;
+  a.B = B;
+  a.Hq = Hq;
+  a.Hkv = Hkv;
+  a.D = D;
+  a.BS = block_size;
+  a.max_blocks = max_blocks;
+  a.scale = scale;
+  if (int rc = use_workspace(a, plan, workspace, workspace_bytes)) return rc;
+  a.mcnt = counters;
+  a.xcd_err = xcd_err;
+  if (out_bf16)
+    a.mout = static_cast<uint16_t*>(out);
+  else
+    a.mout_f32 = static_cast<float*>(out);
+  return launch_split_gq<false>(a, as_stream(stream));
 }
 
 namespace {

@@ -185,6 +185,11 @@ SIGNATURES = {
         [_VP, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32,
          _I32, _F32, _VP, _SZ, _VP],
     ),
+    "grpo_paged_attn_decode_merged": (
+        _I32,
+        [_VP, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32,
+         _I32, _F32, _VP, _SZ, _VP, _VP, _VP],
+    ),
     "grpo_paged_attn_merge": (_I32, [_VP, _VP, _I32, _I32, _I32, _I32, _I32, _I32, _VP, _I32,
                                      _VP]),
     "grpo_nf4_tile_supported": (_I32, [_I32, _I32, _I32, _I32, _I32, _I32]),

@@ -394,6 +394,49 @@ def paged_attention_workspace_bytes(b: int, hq: int, hkv: int, d: int, bs: int,
     return int(_lib.library().grpo_paged_attn_workspace_bytes(b, hq, hkv, d, bs, max_blocks))
 
 
+# One-launch attention (grpo_paged_attn_decode_merged): per device, the int32
+# arrival counters of the in-kernel merge (zero, left zero by every call) and
+# the XCD error word.  Calls on one device share them, as they share the
+# workspace: calls that overlap on two streams must be ordered by the caller.
+_attn_merge: dict = {}
+ATTN_ONE_LAUNCH = True
+
+
+def _attn_merge_state(lib, device, b: int, hkv: int):
+    need = max(int(lib.grpo_paged_attn_merge_counter_bytes(b, hkv)) // 4, 1)
+    key = device if isinstance(device, torch.device) else torch.device(device)
+    st = _attn_merge.get(key)
+    if st is None or st[0].numel() < need:
+        err = st[1] if st is not None else torch.zeros(1, dtype=torch.int32, device=key)
+        st = (torch.zeros(need, dtype=torch.int32, device=key), err)
+        _attn_merge[key] = st
+    return st
+
+
+def attention_handover_check(device=None) -> None:
+    """Check the one-launch attention calls made so far on ``device`` (host
+    sync): their in-kernel merge hands each (sequence, KV head)'s split
+    partials to the last-arriving split through an L2 counter, which is
+    correct only when the pair's splits ran on one XCD.  The kernel flags a
+    pair that did not, and such a pair leaves its counter non-zero; either
+    raises ``RuntimeError`` (those calls' outputs are not valid), clears the
+    state and turns the one-launch form off (``ATTN_ONE_LAUNCH``) for later
+    calls, which then take the split launch + merge launch."""
+    global ATTN_ONE_LAUNCH
+    keys = [torch.device(device)] if device is not None else list(_attn_merge)
+    for key in keys:
+        st = _attn_merge.get(key)
+        if st is None:
+            continue
+        if int(st[1].item()) != 0 or bool((st[0] != 0).any()):
+            st[0].zero_()
+            st[1].zero_()
+            ATTN_ONE_LAUNCH = False
+            raise RuntimeError("paged attention: the context splits of a (sequence, KV head) "
+                               "pair did not run on one XCD; outputs of the one-launch calls "
+                               "since the last check are not valid (one-launch form now off)")
+
+
 def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                            block_tables: torch.Tensor, context_lens: torch.Tensor, scale: float,
                            out_dtype: torch.dtype = torch.float32,
@@ -401,9 +444,12 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
                            no_alloc: bool = False) -> torch.Tensor:
     """GQA paged decode attention; ``q [B, Hq, D]`` bf16 -> ``[B, Hq, D]`` out_dtype.
 
+    One launch (``grpo_paged_attn_decode_merged``: the last-arriving context
+    split of each (sequence, KV head) merges the pair's splits) while
+    ``ATTN_ONE_LAUNCH``; ``attention_handover_check`` verifies those calls.
     ``no_alloc`` calls ``grpo_paged_attn_decode_noalloc`` (split partials in the
-    library's per-GPU scratch array, no workspace); ``out`` must then be given
-    for the call to allocate nothing at all."""
+    library's per-GPU scratch array, no workspace, split + merge launches);
+    ``out`` must then be given for the call to allocate nothing at all."""
     lib = _lib.device_library()
     _need_cuda(q, k_cache, v_cache, block_tables, context_lens)
     _check_cache(k_cache, v_cache)
@@ -434,10 +480,16 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
         return out
     nbytes = int(lib.grpo_paged_attn_workspace_bytes(b, hq, hkv, d, bs, max_blocks))
     ws = workspace("paged_attn", nbytes, q.device)
-    rc = lib.grpo_paged_attn_decode(
-        q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), nb,
-        block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(), out.data_ptr(),
-        1 if out_dtype == torch.bfloat16 else 0, b, hq, hkv, d, bs, max_blocks, float(scale),
-        _lib.ptr(ws), 0 if ws is None else ws.numel(), _lib.stream_handle(q.device))
-    _lib.check(rc, "grpo_paged_attn_decode")
+    args = (q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), nb,
+            block_tables.data_ptr(), block_tables.stride(0), context_lens.data_ptr(),
+            out.data_ptr(), 1 if out_dtype == torch.bfloat16 else 0, b, hq, hkv, d, bs,
+            max_blocks, float(scale), _lib.ptr(ws), 0 if ws is None else ws.numel())
+    if ATTN_ONE_LAUNCH:
+        cnt, err = _attn_merge_state(lib, q.device, b, hkv)
+        rc = lib.grpo_paged_attn_decode_merged(*args, cnt.data_ptr(), err.data_ptr(),
+                                               _lib.stream_handle(q.device))
+        _lib.check(rc, "grpo_paged_attn_decode_merged")
+    else:
+        rc = lib.grpo_paged_attn_decode(*args, _lib.stream_handle(q.device))
+        _lib.check(rc, "grpo_paged_attn_decode")
     return out

@@ -289,6 +289,28 @@ int grpo_paged_attn_decode(const void* q, int64_t q_stride_b, int64_t q_stride_h
                            int Hkv, int D, int block_size, int max_blocks, float scale,
                            void* workspace, size_t workspace_bytes, grpo_stream_t stream);
 
+/* grpo_paged_attn_decode in one launch on the fast path (D = 128, block 16,
+ * Hq / Hkv <= 8, 16-byte aligned q, caches and out): the context split of each
+ * (sequence, KV head) that arrives last merges the pair's splits in the kernel
+ * (the order and formula of the merge launch: out bit-identical to
+ * grpo_paged_attn_decode), in float32 or bf16 as out_bf16 says.  Replaces
+ * _paged_attention_decode_kernel (src/triton_kernels/paged_kv.py:63-251), which
+ * is one launch.  The hand-over runs through an int32 counter per pair
+ * (counters: grpo_paged_attn_merge_counter_bytes(B, Hkv) bytes, 128-byte
+ * aligned, ZERO before the first call and left zero by every call; calls that
+ * share them must be ordered on one stream) and relies on the pair's splits
+ * running on one XCD; every arrival checks its XCD and sets *xcd_err = 1 when a
+ * pair's splits did not share one (that call's output is then invalid; the
+ * caller checks the word after a batch of calls).  Other shapes run the one
+ * generic launch of grpo_paged_attn_decode (counters unused). */
+int grpo_paged_attn_decode_merged(const void* q, int64_t q_stride_b, int64_t q_stride_h,
+                                  const void* k_cache, const void* v_cache, int64_t num_blocks,
+                                  const int32_t* block_tables, int64_t bt_stride,
+                                  const int32_t* context_lens, void* out, int out_bf16, int B,
+                                  int Hq, int Hkv, int D, int block_size, int max_blocks,
+                                  float scale, void* workspace, size_t workspace_bytes,
+                                  int* counters, int* xcd_err, grpo_stream_t stream);
+
 /* Merge of the split partials grpo_paged_attn_decode_qkv left in
  * attn_workspace (same B, Hq, Hkv, D, block_size, max_blocks and
  * context_lens) into out [B, Hq, D] (float32, or bf16 when out_bf16 != 0):

@@ -120,6 +120,42 @@ def test_generic_path(dev, d, bs, hq, hkv):
     check(run_attn(dev, q, kc, vc, tables, cl, s), ref_attn(q, kc, vc, tables, cl, s))
 
 
+@pytest.mark.parametrize("case", ["cfg1", "edges", "gqa8"])
+def test_one_launch_equals_split_plus_merge(dev, case, monkeypatch):
+    """The one-launch attention (``grpo_paged_attn_decode_merged``, the default
+    of ``ops.paged_attention_decode``) against the split kernel + merge launch
+    on the same inputs: float32 and bf16 outputs identical bit for bit (the
+    last-arriving split merges in the merge kernel's order and formula), over
+    three calls in a row through the same counters, which are back at zero,
+    with the XCD check word clear (``attention_handover_check``)."""
+    ops = _ops()
+    if case == "cfg1":
+        ctx = rng(3).integers(512, 1025, 4).tolist()
+        q, kc, vc, tables, cl = paged_case(11, ctx, 12, 2, 128, 16)
+    elif case == "edges":  # ctx 0 and 1, split boundaries, one long row
+        ctx = [0, 1, 15, 16, 17, 639, 640, 641, 4096, 1000, 2]
+        q, kc, vc, tables, cl = paged_case(12, ctx, 12, 2, 128, 16, table_width=300)
+    else:
+        ctx = rng(4).integers(1, 2000, 6).tolist()
+        q, kc, vc, tables, cl = paged_case(13, ctx, 32, 4, 128, 16)
+    s = 1 / math.sqrt(128)
+    want = {}
+    monkeypatch.setattr(ops, "ATTN_ONE_LAUNCH", False)
+    for dt in (torch.float32, torch.bfloat16):
+        want[dt] = run_attn(dev, q, kc, vc, tables, cl, s, out_dtype=dt).cpu()
+    monkeypatch.setattr(ops, "ATTN_ONE_LAUNCH", True)
+    for call in range(3):
+        for dt in (torch.float32, torch.bfloat16):
+            print(f"one-launch attention {case} call {call} {dt}", flush=True)
+            got = run_attn(dev, q, kc, vc, tables, cl, s, out_dtype=dt).cpu()
+            assert torch.equal(got.view(torch.int32 if dt == torch.float32 else torch.int16),
+                               want[dt].view(torch.int32 if dt == torch.float32 else torch.int16))
+    ops.attention_handover_check(dev)
+    cnt, err = ops._attn_merge[torch.device(dev)]
+    assert int(err.item()) == 0 and not bool((cnt != 0).any())
+    check(want[torch.float32], ref_attn(q, kc, vc, tables, cl, s))
+
+
 def test_invalid_block_ids_are_skipped(dev):
     q, kc, vc, tables, cl = paged_case(7, [40, 40], 12, 2, 128, 16)
     bad = tables.copy()
