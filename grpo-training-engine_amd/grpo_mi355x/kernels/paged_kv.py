@@ -143,6 +143,8 @@ def paged_kv_decode(
         last_tokens = next_tokens
         if eos_token_id >= 0:
             finished = finished | (next_tokens == eos_token_id)
+    # the one-launch attention's in-kernel merges ran on one XCD per pair
+    ops.attention_handover_check(input_ids.device)
     return generated
 
 
