@@ -355,3 +355,35 @@ def test_verify_handover_raises_and_switches_the_hand_overs_off():
             assert not DecodeEngine.ATTN_MERGE and not DecodeEngine.O_FIN
     finally:
         DecodeEngine.ATTN_MERGE, DecodeEngine.O_FIN = saved
+
+
+def test_attention_handover_check_raises_and_switches_the_one_launch_form_off():
+    """ops.attention_handover_check: clear counters and word pass; a set XCD
+    word or a counter left non-zero raises RuntimeError, clears the state and
+    turns the one-launch attention off for later calls (the split + merge
+    launches, which hand nothing over)."""
+    from grpo_mi355x.kernels import ops
+
+    saved = (dict(ops._attn_merge), ops.ATTN_ONE_LAUNCH)
+    dev = torch.device("cpu")
+    try:
+        ops._attn_merge.clear()
+        ops.ATTN_ONE_LAUNCH = True
+        ops._attn_merge[dev] = (torch.zeros(64, dtype=torch.int32),
+                                torch.zeros(1, dtype=torch.int32))
+        ops.attention_handover_check(dev)
+        ops.attention_handover_check()  # every device
+        assert ops.ATTN_ONE_LAUNCH
+        for cnt, err in (([0] * 63 + [0x10], 0), ([0] * 64, 1)):
+            ops.ATTN_ONE_LAUNCH = True
+            ops._attn_merge[dev] = (torch.tensor(cnt, dtype=torch.int32),
+                                    torch.tensor([err], dtype=torch.int32))
+            with pytest.raises(RuntimeError, match="XCD"):
+                ops.attention_handover_check(dev)
+            assert not ops.ATTN_ONE_LAUNCH
+            c, e = ops._attn_merge[dev]
+            assert not bool((c != 0).any()) and int(e.item()) == 0
+    finally:
+        ops._attn_merge.clear()
+        ops._attn_merge.update(saved[0])
+        ops.ATTN_ONE_LAUNCH = saved[1]
