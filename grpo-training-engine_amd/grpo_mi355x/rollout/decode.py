@@ -2,20 +2,26 @@
 
 ``DecodeEngine`` runs one decode step of a ``Qwen2ForCausalLM`` (NF4 + LoRA) for
 a fixed batch of sequences on a ``PagedKVPool``: the reference's ``_step``
-(``src/triton_kernels/paged_kv.py:690-820``) as a fixed list of C-ABI launches
-per layer --
+(``src/triton_kernels/paged_kv.py:690-820``) as a fixed list of C-ABI launches.
+Up to 8 rows, five per layer --
 
-  add+RMSNorm(down partials) -> q|k|v NF4+LoRA partials (one launch) ->
-  paged GQA attention (finishes q|k|v, RoPE, KV append; split partials) ->
-  o_proj NF4+LoRA partials (merges the attention splits while staging x) ->
-  add+RMSNorm (finishes o_proj) -> gate|up NF4 partials (one launch) ->
-  down NF4 partials (finishes gate|up and applies SiLU*mul while staging x)
+  q|k|v NF4+LoRA split-K partials (the input RMSNorm staged from h and the
+  per-group sums of squares) -> paged GQA attention (finishes q|k|v, RoPE,
+  KV append; split partials) -> o_proj split-K (merges the attention splits
+  while staging x; the last K slice of each column group adds the epilogue
+  and the residual, writes h and its sums of squares) -> gate|up + SiLU*up
+  (the post-attention RMSNorm staged) -> down_proj over the whole K per 8
+  columns (residual add, h and sums of squares out)
 
--- then the final norm, the bf16 lm_head GEMV with the first argmax pass, and
-one kernel that finishes the argmax and advances every row's state.  Each NF4 linear
-is a split-K launch that writes float32 partial sums; the op that consumes its
-output sums them and applies the linear's epilogue (bias, LoRA, bf16 rounding)
-itself, so no launch is spent on finishing a linear.  Lengths, block tables
+-- after an embedding launch that also writes layer 0's norm statistic, and
+followed by the bf16 lm_head GEMV (the final norm staged) with the first
+argmax pass and one kernel that finishes the argmax and advances every row's
+state.  Wider batches run the norms as launches of their own (add + RMSNorm
+of the previous linear's partial sums), the attention merge as a launch, and
+down_proj as split-K partials.  A split-K linear writes float32 partial sums
+and the op that consumes its output sums them and applies the linear's
+epilogue (bias, LoRA, bf16 rounding) itself, so no launch is spent on
+finishing a linear.  Lengths, block tables
 and the token buffer live on the device, so the whole step (including the
 per-row bookkeeping) is captured once into a HIP graph and replayed with no
 host synchronisation.  Rows stop at EOS or at a per-row length cap; a stopped
