@@ -860,6 +860,14 @@ class DecodeEngine:
         """
         pool = self.pool
         chunk = chunk or pool.block_size
+        if compact and getattr(self, "sampling", False):
+            raise ValueError("row compaction is for greedy decoding (sampled draws are keyed "
+                             "by the row index)")
+        for e in compact or ():
+            if e.pool is not pool or e.max_blocks != self.max_blocks or \
+                    getattr(e, "sampling", False):
+                raise ValueError("compaction engines must be greedy engines over this engine's "
+                                 "pool and block-table width (compaction_engines)")
         ladder = sorted((e for e in (compact or ()) if e.B < self.B), key=lambda e: e.B)
         eng, used = self, [self]
         origin = list(range(len(sids)))  # row of eng -> row of this engine
