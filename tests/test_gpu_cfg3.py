@@ -182,3 +182,80 @@ def test_cfg3_full_depth_rollouts_keep_the_xcd_check_clear(dev):
     for b, s in enumerate(stops):
         assert np.all(outs[0][b, s:] == 0)
     assert len({tuple(r[:64]) for r in outs[0]}) == 1  # one prompt, greedy: equal prefixes
+
+
+def test_cfg3_full_depth_logits_within_the_rounding_spread(dev):
+    """All 28 layers of the Qwen2-1.5B shape against the oracle, one decode step
+    of 4 rows forked from a 128-token prompt (cached by the chunked prefill;
+    the oracle starts from the same cache).  The 1e-2 bound of the ops holds
+    through 2 layers (the test above); through 28 layers the float32
+    summation-order differences of the NF4 linears (products exact, >= 97 %
+    of outputs bit-identical per linear) compound, so the yardstick is the
+    spread between this build's own kernel families on the same inputs: the
+    4-row step (folded down_proj, staged norms, o_proj's in-kernel finish)
+    against a 12-row and a 32-row engine (split-K down_proj, separate norm
+    launches, other K splits).  The oracle's distance must be within twice the
+    largest such spread and below 5e-2 of max|logit| (2.9e-2 and 2.8e-2
+    measured; 7.4e-3 and 4.2e-3 at 2 layers, 1.7e-2 and 1.2e-2 at 8), and the
+    greedy tokens must equal the oracle's wherever its top-2 margin exceeds
+    5e-2 of max|logit|."""
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill
+    from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
+
+    cfg = Qwen2Config.qwen2_1_5b()
+    L = cfg.num_hidden_layers
+    model = build_random_model(cfg, dev, seed=7)
+    G, bs, P = 4, 16, 128
+    g = np.random.default_rng(3)
+    prompt = g.integers(0, cfg.vocab_size, P).tolist()
+    width = -(-(P + 4) // bs)
+    pool = PagedKVPool(L, width * (G + 1) + 8, cfg.num_key_value_heads, cfg.head_dim, bs,
+                       device=dev)
+    print("cfg3 full depth: prefill", flush=True)
+    pre = PrefillEngine(model, pool, 64, width)
+    sid = prefill(pre, pool, tuple(prompt), width)
+    torch.cuda.synchronize()
+    del pre
+    kids = pool.fork(sid, G, reserve_tokens=P + 2)
+    pool.free(sid)
+    tables = pool.block_table(kids, width).cpu()
+    toks = np.concatenate([[prompt[-1]], g.integers(0, cfg.vocab_size, G - 1)])
+    kcs = [bits(pool.k[i]) for i in range(L)]
+    vcs = [bits(pool.v[i]) for i in range(L)]
+    print("cfg3 full depth: oracle step", flush=True)
+    w, c = export(model)
+    oracle = Qwen2DecodeOracle(w, c)
+    lo_bits, nxt = oracle.step(toks, kcs, vcs, tables.numpy(), np.full(G, P - 1))
+    lo = bf16_bits_to_f32(lo_bits)
+
+    def step0(B):
+        print(f"cfg3 full depth: {B}-row engine", flush=True)
+        eng = DecodeEngine(model, pool, B, width, keep_logits=True)
+        tok = torch.zeros(B, dtype=torch.int64)
+        tok[:G] = torch.from_numpy(toks)
+        tbl = torch.full((B, width), -1, dtype=torch.int32)
+        tbl[:G] = tables
+        lim = torch.zeros(B, dtype=torch.int32)
+        lim[:G] = 1  # rows past G idle: no append, length 0
+        eng.start(tok.to(dev), torch.full((B,), P - 1, device=dev), tbl.to(dev), lim.to(dev), 1)
+        eng.step()
+        torch.cuda.synchronize()
+        eng.verify_handover()
+        return bf16_bits_to_f32(bits(eng.logits))[:G]
+
+    fams = {B: step0(B) for B in (G, 12, 32)}
+
+    def dist(a, b):
+        return max(rel_err(a[i], b[i]) for i in range(G))
+
+    spread = max(dist(fams[G], fams[12]), dist(fams[G], fams[32]), dist(fams[12], fams[32]))
+    to_oracle = dist(fams[G], lo)
+    print(f"cfg3 full depth: oracle distance {to_oracle:.2e}, kernel-family spread {spread:.2e}",
+          flush=True)
+    assert to_oracle <= 5e-2 and to_oracle <= 2 * spread
+    for B, lg in fams.items():
+        for i in range(G):
+            srt = np.sort(lo[i])
+            if srt[-1] - srt[-2] > 5e-2 * np.abs(lo[i]).max():
+                assert int(np.argmax(lg[i])) == int(nxt[i]), (B, i)
