@@ -1289,8 +1289,9 @@ __global__ void __launch_bounds__(128 * S) nf4_gate_up_silu(GuArgs p) {
   }
 }
 
-// gate|up + SiLU in units of 8 output columns over a grid of at most one
-// workgroup per CU.  Unit u covers act columns 8u .. 8u+7: the MFMA tile's 16
+// gate|up + SiLU in units of 8 output columns (4 for the decode step's folded
+// units, FOLD below) over a grid of at most one workgroup per CU.  Unit u
+// covers act columns 8u .. 8u+7: the MFMA tile's 16
 // B-columns are gate rows 8u .. 8u+7 (lanes n < 8) and up rows I+8u .. I+8u+7
 // (lanes n >= 8), so the SiLU pairs a tile's columns n and n + 8.  Workgroup
 // g takes units g, g + G, g + 2G, ...; its W waves take the (unit, k-step)
