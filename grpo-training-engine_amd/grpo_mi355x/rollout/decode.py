@@ -292,6 +292,16 @@ class DecodeEngine:
                 # arrival counters: zero before the first launch, left zero by every launch
                 self.o_cnt = torch.zeros(cb.value // 4, dtype=torch.int32, device=dev)
                 self.ss_post = torch.zeros(B, G, dtype=torch.float32, device=dev)
+        # wide batches (more rows than o_proj's split staging takes) with more
+        # than one context split: the attention merges its splits in the kernel
+        # and writes the bf16 rows o_proj reads (no merge launch)
+        self.wide_merge = False
+        if (self.ATTN_MERGE and self.attn_fused and B > self.ATTN_STAGE_MAX_ROWS
+                and self.attn_splits > 1):
+            self.wide_merge = True
+            self.m_cnt = torch.zeros(
+                int(self.lib.grpo_paged_attn_merge_counter_bytes(B, self.Hkv)) // 4,
+                dtype=torch.int32, device=dev)
         # the embedding's row statistic for layer 0's input norm
         self.ss_embed = torch.zeros(B, int(self.lib.grpo_embedding_sumsq_groups()),
                                     dtype=torch.float32, device=dev)
@@ -370,9 +380,11 @@ class DecodeEngine:
     # default: at config 3 the attention's in-kernel merge and LoRA-A product
     # cost 3.4 us per launch against 1.2 us saved in o_proj (3345 against
     # 3503 tok/s); o_proj merging the splits while it stages x (O_FIN) is
-    # faster.  The in-kernel hand-overs are checked after every run
-    # (verify_handover), which switches ATTN_MERGE and O_FIN off for later
-    # engines if one fails.
+    # faster.  ATTN_MERGE alone applies to wide batches (more than 16 rows),
+    # whose o_proj reads merged bf16 rows: the attention merges its splits
+    # instead of a merge launch.  The in-kernel hand-overs are checked after
+    # every run (verify_handover), which switches ATTN_MERGE and O_FIN off for
+    # later engines if one fails.
     O_TILE = False
     ATTN_MERGE = True
     # o_proj + its epilogue + residual add in one launch through the last
@@ -515,10 +527,20 @@ class DecodeEngine:
         if wide:
             # wide batches: o_proj stages the merged bf16 rows as plain x
             # (merging the splits while staging repeats the merge in every
-            # workgroup of a K slice: ~0.4 GB of partial-sum reads at 64 rows)
-            merge = [] if direct else [("attn_merge", lambda: chk(lib.grpo_paged_attn_merge(
-                wsa, self.attn_len.data_ptr(), self.B, Hq, Hkv, D, pool.block_size,
-                self.max_blocks, ao, 1, st), "attn_merge"))]
+            # workgroup of a K slice: ~0.4 GB of partial-sum reads at 64 rows);
+            # the attention merges them itself (wide_merge) or a merge launch does
+            if self.wide_merge:
+                attention = ("attention", lambda: chk(lib.grpo_paged_attn_decode_qkv_merged(
+                    L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
+                    self.max_pos, self.append_pos.data_ptr(), self.attn_len.data_ptr(), kc, vc,
+                    pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
+                    pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n,
+                    self.m_cnt.data_ptr(), self.xcd_err.data_ptr(), ao, None, 0, None, st),
+                    "attention"))
+            merge = [] if direct or self.wide_merge else [
+                ("attn_merge", lambda: chk(lib.grpo_paged_attn_merge(
+                    wsa, self.attn_len.data_ptr(), self.B, Hq, Hkv, D, pool.block_size,
+                    self.max_blocks, ao, 1, st), "attn_merge"))]
             return [attention] + merge + [
                 ("o", lambda: chk(lib.grpo_nf4_linear_partials(
                     ao, Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
