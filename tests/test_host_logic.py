@@ -169,6 +169,10 @@ def test_run_paged_reserves_ahead_and_frees_stopped_rows():
         def verify_handover(self):
             self.verified += 1
 
+        def run(self, n):
+            for _ in range(n):
+                self.step()
+
         def step(self):
             self.in_use.append(pool.num_blocks - pool.num_free)
             for b in range(3):
@@ -230,6 +234,10 @@ def test_run_paged_compaction_moves_live_rows_to_smaller_engines():
 
         def verify_handover(self):
             self.verified += 1
+
+        def run(self, n):
+            for _ in range(n):
+                self.step()
 
         def step(self):
             self.steps_run += 1
