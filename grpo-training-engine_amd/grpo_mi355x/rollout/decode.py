@@ -938,6 +938,8 @@ class DecodeEngine:
                     self._put_back(eng, origin)
                 rows = sorted(live)
                 dst._take_rows(eng, rows)
+                eng.active.zero_()  # the moved rows go on in dst only
+                eng._masks()
                 origin = [origin[b] for b in rows]
                 live = {i: live[b] for i, b in enumerate(rows)}
                 pos = [pos[b] for b in rows]

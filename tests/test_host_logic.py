@@ -283,6 +283,8 @@ def test_run_paged_compaction_moves_live_rows_to_smaller_engines():
     # 4 rows left after 12 steps, 2 after 24: the 2-row engine ran the last 16
     assert (big.steps_run, ladder[0].steps_run, ladder[1].steps_run) == (12, 12, 16)
     assert big.verified == 1 and all(e.verified == 1 for e in ladder)
+    # the engines rows moved away from are left idle
+    assert not bool(big.active.any()) and not bool(ladder[0].active.any())
     # engines over another pool, or a sampling engine, are refused
     other = Stand(PagedKVPool(1, 16, 1, 8, block_size=4), 4)
     with pytest.raises(ValueError, match="compaction engines"):
