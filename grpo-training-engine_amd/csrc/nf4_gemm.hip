@@ -1,0 +1,469 @@
+// NF4 (+ bias, + LoRA) linear for batches of more than 64 rows on gfx950: one
+// MFMA GEMM launch that decodes the 4-bit weight in registers and applies the
+// reference epilogue in the kernel.  Restates _lora_forward_kernel
+// (src/triton_kernels/lora_forward.py:107-260) for any M:
+//   acc = sum_k x[m,k] * bf16(code[q(n,k)] * absmax)   (float32 accumulation)
+//   v = bf16(acc); v = bf16(v + bias[n])                (:243-247)
+//   t = bf16(x A^T)  (rank r <= 32)                     (:210-236)
+//   u = bf16(bf16(t . B[n, :]) * bf16(scaling)); y = bf16(v + u)   (:249-257)
+//
+//  * Tile: a workgroup (4 waves) owns 128 rows m x 128 columns n; wave w owns
+//    all 128 rows x columns 32 w .. 32 w + 31 as 8 x 2 tiles of
+//    v_mfma_f32_16x16x32_bf16 (A = x rows from LDS, B = W rows decoded in the
+//    wave's registers).  Two workgroups per CU (80 KiB of LDS each).
+//  * Stage = 128 K values.  Lane (n = lane % 16, group g = lane / 16) of a
+//    column tile holds the 32 nibbles [32 g, 32 g + 32) of its weight row (one
+//    16-byte load) and their absmax (blocksize >= 32); per stage it builds the
+//    block's bf16 codebook bf16(code[j] * absmax) in registers and decodes
+//    8 K values per MFMA with v_perm byte lookups (nf4_decode.hpp), in the
+//    order [0,2,4,6,1,3,5,7]; x is staged in LDS permuted the same way.
+//  * x is double-buffered in LDS: stage s + 1's x and weights are loaded while
+//    stage s's MFMAs run; one barrier per stage.
+//  * LoRA: wave w also multiplies rows 32 w .. 32 w + 31 by A (one or two
+//    16-rank column tiles; A is bf16, no decode).  After the K loop t goes to
+//    LDS in bf16 and t . B[n, :] is one more MFMA per output tile (K = 32
+//    ranks, ranks >= r zero).
+//  * Output: the bf16 tile passes through LDS so every thread stores 16-byte
+//    row chunks.
+//  * Edges: rows >= M read row M - 1 and are not stored; columns >= N read
+//    row N - 1 of W and are not stored; a last stage past K (K % 128 != 0)
+//    stages zero x (its weight loads are clamped into the row).
+//  * Workgroup -> tile: the dispatcher places workgroup i on XCD i mod 8, so
+//    the workgroups of one column tile (all row tiles) get ids with equal
+//    residues mod 8 and read that tile's weights through one L2.
+#include <algorithm>
+
+#include "linear_parts.hpp"
+#include "nf4_decode.hpp"
+
+using namespace grpo;
+
+namespace {
+
+constexpr int GM_BM = 128;            // rows per workgroup
+constexpr int GM_BN = 128;            // columns per workgroup
+constexpr int GM_KS = 128;            // K values per stage
+constexpr int GM_T = 256;             // threads (4 waves)
+constexpr int GM_XS = GM_KS + 8;      // LDS row stride of a staged x stage (elements)
+constexpr int GM_TS = 32 + 8;         // LDS row stride of t (elements)
+constexpr int GM_OS = GM_BN + 8;      // LDS row stride of the output tile (elements)
+constexpr int GM_RT = GM_BM / 16;     // row tiles per wave
+constexpr int GM_MAX_R = 32;
+constexpr size_t GM_LDS =
+    (size_t)(2 * GM_BM * GM_XS + GM_BM * GM_TS) * 2;  // 79,872 bytes
+static_assert(GM_BM * GM_OS <= 2 * GM_BM * GM_XS, "output tile reuses the x stages");
+
+struct GemmArgs {
+  const uint16_t* x;
+  int64_t ldx;
+  const uint8_t* w;
+  const float* absmax;
+  const float* code16;
+  int bs_shift;
+  int64_t wrow0;         // weight row of output column 0 (a segment of a stacked weight)
+  const uint16_t* bias;  // [N] or null
+  const uint16_t* la;    // [r][K] (r > 0)
+  const uint16_t* lb;    // [N][r] (r > 0)
+  int r;
+  float scaling;
+  uint16_t* y;
+  int64_t ldy;
+  int M, N, K;
+  int MT, NT;  // row and column tiles
+  int nst;     // stages
+  int kst;     // stages per K slice (gridDim.y slices)
+  bool yvec;   // 16-byte stores of y rows (y aligned, ldy and N multiples of 8)
+  bool lbvec;  // 16-byte loads of B rows (lb aligned, r % 8 == 0)
+  // K split over gridDim.y slices: float32 partial sums part[slice][m][n]
+  // (slice stride psl, row stride ldp) and, from column tile 0, the LoRA t
+  // partials tpart[slice][m][16] (slice stride tsl); the epilogue then runs in
+  // the finish kernel.  part == null: one slice, epilogue in this kernel.
+  float* part;
+  int64_t ldp, psl;
+  float* tpart;
+  int64_t tsl;
+};
+
+// TC: LoRA rank tiles of 16 (0: no LoRA, 1: r <= 16, 2: r <= 32).
+template <int TC>
+__global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
+  constexpr bool LORA = TC > 0;
+  extern __shared__ __align__(16) uint16_t lds[];
+  uint16_t* const ts = lds + 2 * GM_BM * GM_XS;  // t [128][GM_TS] bf16
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int ln = lane & 15, lg = lane >> 4;
+  const int b = blockIdx.x, slot = b >> 3;
+  const int nt = (slot / p.MT) * 8 + (b & 7), mt = slot - (slot / p.MT) * p.MT;
+  if (nt >= p.NT) return;  // padding workgroups of the XCD grouping
+  const int m0 = mt * GM_BM, n0 = nt * GM_BN;
+
+  float code[16];
+#pragma unroll
+  for (int j = 0; j < 16; ++j) code[j] = p.code16[j];
+
+  // x staging: thread (row r0 + 16 u, chunk c) for u < 8; 16 threads per row
+  const int r0 = tid >> 4, c8 = 8 * (tid & 15);
+  const uint16_t* xr[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) xr[u] = p.x + (int64_t)min(m0 + r0 + 16 * u, p.M - 1) * p.ldx;
+  // weight rows of this lane's two column tiles
+  const uint8_t* wr[2];
+  int64_t we[2];
+#pragma unroll
+  for (int ct = 0; ct < 2; ++ct) {
+    const int n = min(n0 + 32 * wave + 16 * ct + ln, p.N - 1);
+    we[ct] = (p.wrow0 + n) * p.K;
+    wr[ct] = p.w + we[ct] / 2;
+  }
+  // LoRA A rows: rank 16 tc + ln of this lane.  Ranks >= r read rank r - 1:
+  // their t columns are finite and meet zero B entries, so they add nothing
+  // (no select, which the compiler turns into a predicated load).
+  const uint16_t* ar[LORA ? TC : 1];
+#pragma unroll
+  for (int tc = 0; tc < TC; ++tc) ar[tc] = p.la + (int64_t)min(16 * tc + ln, p.r - 1) * p.K;
+
+  uint4 xv[8];
+  uint4 wv[2];
+  float av[2];
+  auto load_stage = [&](int st) __attribute__((always_inline)) {
+    const int k0 = st * GM_KS;
+    const int kx = min(k0 + c8, p.K - 8);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) xv[u] = *reinterpret_cast<const uint4*>(xr[u] + kx);
+    const int kc = min(k0 + 32 * lg, p.K - 32);
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      wv[ct] = *reinterpret_cast<const uint4*>(wr[ct] + kc / 2);
+      av[ct] = p.absmax[(we[ct] + kc) >> p.bs_shift];
+    }
+  };
+  auto store_x = [&](int st) __attribute__((always_inline)) {
+    uint16_t* buf = lds + (st & 1) * GM_BM * GM_XS;
+    const bool kin = st * GM_KS + c8 < p.K;
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      *reinterpret_cast<uint4*>(buf + (r0 + 16 * u) * GM_XS + c8) =
+          kin ? deinterleave8(xv[u]) : make_uint4(0, 0, 0, 0);
+  };
+
+  f32x4_t acc[GM_RT][2];
+#pragma unroll
+  for (int rt = 0; rt < GM_RT; ++rt) acc[rt][0] = acc[rt][1] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  f32x4_t tacc[2][LORA ? TC : 1];  // [row tile of the wave's 32 rows][rank tile]
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int tc = 0; tc < TC; ++tc) tacc[i][tc] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  const int st0 = blockIdx.y * p.kst, st1 = min(p.nst, st0 + p.kst);
+  load_stage(st0);
+  store_x(st0);
+  __syncthreads();
+  for (int st = st0; st < st1; ++st) {
+    // This stage's LoRA A loads go out before the next stage's prefetch (loads
+    // retire in order) and are used after the stage's weight MFMAs.
+    uint4 la4[LORA ? TC : 1][4];
+    if (LORA) {
+      const int kc = min(st * GM_KS + 32 * lg, p.K - 32);
+#pragma unroll
+      for (int tc = 0; tc < TC; ++tc)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          la4[tc][s] = *reinterpret_cast<const uint4*>(ar[tc] + kc + 8 * s);
+    }
+    const uint4 wc0 = wv[0], wc1 = wv[1];
+    const float ac0 = av[0], ac1 = av[1];
+    // The prefetch is unconditional (the last stage re-reads itself): after a
+    // conditional load the compiler waits for every load with vmcnt(0).
+    const bool more = st + 1 < st1;
+    load_stage(min(st + 1, st1 - 1));
+    // keep the loads here, ahead of this stage's MFMAs
+    __builtin_amdgcn_sched_barrier(0);
+    const uint16_t* buf = lds + (st & 1) * GM_BM * GM_XS + ln * GM_XS + 32 * lg;
+    const Lut t0 = make_lut(code, ac0), t1 = make_lut(code, ac1);
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      uint4 a[GM_RT];
+#pragma unroll
+      for (int rt = 0; rt < GM_RT; ++rt)
+        a[rt] = *reinterpret_cast<const uint4*>(buf + rt * 16 * GM_XS + 8 * s);
+      const uint4 b0 = decode8(word(wc0, s), t0);
+      const uint4 b1 = decode8(word(wc1, s), t1);
+#pragma unroll
+      for (int rt = 0; rt < GM_RT; ++rt) {
+        acc[rt][0] = mfma16x16x32(a[rt], b0, acc[rt][0]);
+        acc[rt][1] = mfma16x16x32(a[rt], b1, acc[rt][1]);
+      }
+    }
+    if (LORA) {
+      // rows 32 w .. 32 w + 31 of this wave times the A ranks (ranks >= r zero)
+      const uint16_t* tb = buf + 32 * wave * GM_XS;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint4 a0 = *reinterpret_cast<const uint4*>(tb + 8 * s);
+        const uint4 a1 = *reinterpret_cast<const uint4*>(tb + 16 * GM_XS + 8 * s);
+#pragma unroll
+        for (int tc = 0; tc < TC; ++tc) {
+          const uint4 lb = deinterleave8(la4[tc][s]);
+          tacc[0][tc] = mfma16x16x32(a0, lb, tacc[0][tc]);
+          tacc[1][tc] = mfma16x16x32(a1, lb, tacc[1][tc]);
+        }
+      }
+    }
+    if (more) store_x(st + 1);
+    __syncthreads();
+  }
+
+  if (p.part) {
+    // K slice: float32 partial sums (and column tile 0's LoRA t partials)
+    float* pp = p.part + blockIdx.y * p.psl;
+#pragma unroll
+    for (int rt = 0; rt < GM_RT; ++rt)
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct) {
+        const int n = n0 + 32 * wave + 16 * ct + ln;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int m = m0 + rt * 16 + 4 * lg + q;
+          if (m < p.M && n < p.N) pp[(int64_t)m * p.ldp + n] = acc[rt][ct][q];
+        }
+      }
+    if (LORA && nt == 0) {
+      float* tp = p.tpart + blockIdx.y * p.tsl;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int m = m0 + 32 * wave + 16 * i + 4 * lg + q;
+          if (m < p.M) tp[(int64_t)m * 16 + ln] = tacc[i][0][q];
+        }
+    }
+    return;
+  }
+
+  // ---- epilogue
+  f32x4_t u[GM_RT][2];
+  if (LORA) {
+    // t rows 32 w + 16 i + 4 lg + q, ranks 16 tc + ln, rounded to bf16
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int tc = 0; tc < 2; ++tc)
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          ts[(32 * wave + 16 * i + 4 * lg + q) * GM_TS + 16 * tc + ln] =
+              tc < TC ? f2bf(tacc[i][tc < TC ? tc : 0][q]) : (uint16_t)0;
+    // B rows: ranks 8 lg .. 8 lg + 7 of column n (ranks >= r zero)
+    uint4 bv[2];
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct) {
+      const int n = min(n0 + 32 * wave + 16 * ct + ln, p.N - 1);
+      const uint16_t* br = p.lb + (int64_t)n * p.r;
+      if (p.lbvec) {
+        bv[ct] = 8 * lg < p.r ? *reinterpret_cast<const uint4*>(br + 8 * lg)
+                              : make_uint4(0, 0, 0, 0);
+      } else {
+        uint32_t h[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = 8 * lg + j < p.r ? br[8 * lg + j] : 0u;
+        bv[ct] = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16),
+                            h[6] | (h[7] << 16));
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < GM_RT; ++rt) {
+      const uint4 tv = *reinterpret_cast<const uint4*>(ts + (rt * 16 + ln) * GM_TS + 8 * lg);
+#pragma unroll
+      for (int ct = 0; ct < 2; ++ct)
+        u[rt][ct] = mfma16x16x32(tv, bv[ct], f32x4_t{0.f, 0.f, 0.f, 0.f});
+    }
+  }
+  float bias[2] = {0.f, 0.f};
+  if (p.bias) {
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+      bias[ct] = bf2f(p.bias[min(n0 + 32 * wave + 16 * ct + ln, p.N - 1)]);
+  }
+  const float sc = round_bf(p.scaling);
+  // bf16 tile [128][GM_OS] in the x stage buffers (free after the loop's last barrier)
+  uint16_t* os = lds;
+#pragma unroll
+  for (int rt = 0; rt < GM_RT; ++rt)
+#pragma unroll
+    for (int ct = 0; ct < 2; ++ct)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float v = round_bf(acc[rt][ct][q]);
+        if (p.bias) v = round_bf(v + bias[ct]);
+        if (LORA) v = round_bf(v + round_bf(round_bf(u[rt][ct][q]) * sc));
+        os[(rt * 16 + 4 * lg + q) * GM_OS + 32 * wave + 16 * ct + ln] = f2bf(v);
+      }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int row = r0 + 16 * i, m = m0 + row, n = n0 + c8;
+    if (m >= p.M || n >= p.N) continue;
+    const uint4 v = *reinterpret_cast<const uint4*>(os + row * GM_OS + c8);
+    uint16_t* dst = p.y + (int64_t)m * p.ldy + n;
+    if (p.yvec) {
+      *reinterpret_cast<uint4*>(dst) = v;
+    } else {
+      const uint32_t h[4] = {v.x, v.y, v.z, v.w};
+      for (int j = 0; j < 8 && n + j < p.N; ++j)
+        dst[j] = (uint16_t)(h[j >> 1] >> (16 * (j & 1)));
+    }
+  }
+}
+
+bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
+
+template <typename Kern>
+int allow_lds(Kern kernel) {
+  static const int rc = hip_check(
+      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)GM_LDS),
+      "hipFuncSetAttribute");
+  return rc;
+}
+
+bool gemm_ok(int M, int N, int K, int r, int blocksize) {
+  return M >= 1 && N >= 1 && K >= 32 && K % 32 == 0 && r >= 0 && r <= GM_MAX_R &&
+         pow2(blocksize) && blocksize >= 32;
+}
+
+}  // namespace
+
+namespace grpo {
+
+bool nf4_gemm_ok(int M, int N, int K, int r, int blocksize) {
+  return gemm_ok(M, N, K, r, blocksize);
+}
+
+GemmPlan nf4_gemm_plan(int M, int K, int r, int nseg, const int* seg_end) {
+  const int nst = (int)cdiv(K, GM_KS);
+  GemmPlan pl{1, nst, 0, 0};
+  const int64_t mt = cdiv(M, GM_BM);
+  int64_t tiles = 0;
+  bool split_ok = r <= 16 && nseg >= 1 && nseg <= MAXSEG;
+  for (int s = 0, start = 0; s < nseg; start = seg_end[s], ++s) {
+    tiles += mt * cdiv(seg_end[s] - start, GM_BN);
+    split_ok = split_ok && seg_end[s] % 16 == 0;
+  }
+  if (!split_ok || nst < 6) return pl;
+  // Time model (us) of S K slices, from measurements on MI355X: a workgroup
+  // stage (128 K values) takes about 2.2 us whatever the tile count (its loads'
+  // latency), 512 workgroups run at once; a split adds the float32 partial
+  // sums (written and read back, ~4 TB/s), the finish launch and, with LoRA,
+  // the finish's per-output rank sums (~8 ns per 1000 outputs).
+  const int N = seg_end[nseg - 1];
+  const double outs = (double)M * N;
+  auto est = [&](int S, int* kst, int* slices) {
+    *kst = (int)cdiv(nst, S);
+    *slices = (int)cdiv(nst, *kst);
+    double t = (double)cdiv(tiles * *slices, 512) * *kst * 2.2;
+    if (*slices > 1) t += *slices * outs * 8.0 / 4e6 + 4.0 + (r > 0 ? outs * 8e-6 : 0.0);
+    return t;
+  };
+  double best = 0.0;
+  for (int S = 1; S <= std::min(MAX_SLICES, nst / 3); ++S) {
+    int kst, slices;
+    const double t = est(S, &kst, &slices);
+    if (S == 1 || t < best) {
+      best = t;
+      pl.S = slices;
+      pl.kst = kst;
+    }
+  }
+  if (pl.S > 1) {
+    pl.part_bytes = (size_t)pl.S * M * N * 4;
+    pl.tpart_bytes = r > 0 ? (size_t)pl.S * nseg * M * 16 * 4 : 0;
+  }
+  return pl;
+}
+
+int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wrow0,
+                    const float* absmax, const float* code16, int blocksize,
+                    const uint16_t* bias, const uint16_t* la, const uint16_t* lb, int r,
+                    float scaling, uint16_t* y, int64_t ldy, int M, int N, int K,
+                    hipStream_t st, const GemmSplit* split) {
+  if (M < 0 || N < 0 || K < 0 || r < 0 || wrow0 < 0) return einval("negative dimension");
+  if (M == 0 || N == 0) return GRPO_OK;
+  if (!gemm_ok(M, N, K, r, blocksize)) {
+    set_error("shape not supported by the NF4 GEMM (K %% 32 == 0, r <= 32, power-of-two "
+              "blocksize >= 32)");
+    return GRPO_EUNSUPPORTED;
+  }
+  if (!x || !w || !absmax || !code16 || !y) return einval("null pointer");
+  if (r > 0 && (!la || !lb)) return einval("r > 0 needs lora_a and lora_b");
+  if (ldx < K || ldx % 8 != 0 || !aligned16(x)) return einval("x rows must be 16-byte aligned");
+  if (!aligned16(w)) return einval("w must be 16-byte aligned");
+  if (r > 0 && !aligned16(la)) return einval("lora_a must be 16-byte aligned");
+  if (ldy < N) return einval("ldy smaller than N");
+  GemmArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.w = w;
+  a.absmax = absmax;
+  a.code16 = code16;
+  a.bs_shift = __builtin_ctz((unsigned)blocksize);
+  a.wrow0 = wrow0;
+  a.bias = bias;
+  a.la = la;
+  a.lb = lb;
+  a.r = r;
+  a.scaling = scaling;
+  a.y = y;
+  a.ldy = ldy;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.MT = (int)cdiv(M, GM_BM);
+  a.NT = (int)cdiv(N, GM_BN);
+  a.nst = (int)cdiv(K, GM_KS);
+  a.kst = a.nst;
+  a.yvec = aligned16(y) && ldy % 8 == 0 && N % 8 == 0;
+  a.lbvec = r > 0 && aligned16(lb) && r % 8 == 0;
+  unsigned slices = 1;
+  if (split && split->S > 1) {
+    if (r > 16) return einval("a K-split NF4 GEMM takes r <= 16");
+    if (!split->part || (r > 0 && !split->tpart)) return einval("null partial-sum buffer");
+    a.kst = split->kst;
+    slices = (unsigned)split->S;
+    if ((int64_t)(slices - 1) * a.kst >= a.nst) return einval("empty K slice");
+    a.part = split->part;
+    a.ldp = split->ldp;
+    a.psl = split->psl;
+    a.tpart = split->tpart;
+    a.tsl = split->tsl;
+  }
+  const unsigned groups = (unsigned)cdiv(a.NT, 8);
+  const dim3 grid(groups * 8u * (unsigned)a.MT, slices);
+  if (r > 16) {
+    if (int rc = allow_lds(nf4_gemm_mfma<2>)) return rc;
+    nf4_gemm_mfma<2><<<grid, GM_T, GM_LDS, st>>>(a);
+  } else if (r > 0) {
+    if (int rc = allow_lds(nf4_gemm_mfma<1>)) return rc;
+    nf4_gemm_mfma<1><<<grid, GM_T, GM_LDS, st>>>(a);
+  } else {
+    if (int rc = allow_lds(nf4_gemm_mfma<0>)) return rc;
+    nf4_gemm_mfma<0><<<grid, GM_T, GM_LDS, st>>>(a);
+  }
+  return launch_check("nf4_gemm_mfma");
+}
+
+}  // namespace grpo
+
+extern "C" int grpo_nf4_gemm_supported(int M, int N, int K, int r, int blocksize) {
+  return gemm_ok(M, N, K, r, blocksize) ? 1 : 0;
+}
+
+extern "C" int grpo_nf4_gemm(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                             const float* code16, int blocksize, const void* bias,
+                             const void* lora_a, const void* lora_b, int r, float scaling,
+                             void* y, int64_t ldy, int M, int N, int K, grpo_stream_t stream) {
+  return nf4_gemm_launch(static_cast<const uint16_t*>(x), ldx, w, 0, absmax, code16, blocksize,
+                         static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(lora_a),
+                         static_cast<const uint16_t*>(lora_b), r, scaling,
+                         static_cast<uint16_t*>(y), ldy, M, N, K, as_stream(stream), nullptr);
+}

@@ -2049,7 +2049,8 @@ __global__ void __launch_bounds__(256) nf4_linear_generic(GenArgs p) {
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // One NF4 (+ LoRA) linear into y: split-K partials + finish when the shape,
-// alignment and workspace allow it, the generic kernel otherwise.
+// alignment and workspace allow it (M <= 64), else the NF4 GEMM, else the
+// generic kernel.
 int run_linear(const GenArgs& g, void* workspace, size_t workspace_bytes, hipStream_t st) {
   bool fast = part_shape_ok(g.M, g.N, g.K, g.r, g.nseg, g.blocksize, g.seg_end) &&
               g.ldx % 8 == 0 && aligned16(g.x) && aligned16(g.w);
@@ -2082,13 +2083,77 @@ int run_linear(const GenArgs& g, void* workspace, size_t workspace_bytes, hipStr
       return rc;
     return run_finish(&h, g.y, g.ldy, st);
   }
+  // Wider batches: the NF4 GEMM, one launch per segment of the stacked weight.
+  bool gemm = g.ldx % 8 == 0 && aligned16(g.x) && aligned16(g.w);
+  for (int s = 0, start = 0; gemm && s < g.nseg; start = g.seg_end[s], ++s)
+    gemm = nf4_gemm_ok(g.M, g.seg_end[s] - start, g.K, g.r, g.blocksize) &&
+           (g.r == 0 || aligned16(g.la[s]));
+  if (gemm) {
+    // Few tiles and a long K: the K slices write float32 partial sums (LinParts
+    // layout over all segments) and nf4_finish applies the epilogue.
+    // A workspace smaller than the plan's partial sums runs the linear unsplit.
+    GemmPlan pl = nf4_gemm_plan(g.M, g.K, g.r, g.nseg, g.seg_end);
+    if (pl.S > 1 && (!workspace || workspace_bytes < align256(pl.part_bytes) + pl.tpart_bytes))
+      pl.S = 1;
+    GemmSplit sp{};
+    grpo_linear_parts_t h{};
+    if (pl.S > 1) {
+      sp.S = pl.S;
+      sp.kst = pl.kst;
+      sp.ldp = g.N;
+      sp.psl = (int64_t)g.M * g.N;
+      sp.tsl = (int64_t)g.nseg * g.M * 16;
+      h.part = static_cast<float*>(workspace);
+      h.tpart = g.r > 0 ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
+                                                   align256(pl.part_bytes))
+                        : nullptr;
+      h.splits = pl.S;
+      h.M = g.M;
+      h.N = g.N;
+      h.K = g.K;
+      h.nseg = g.nseg;
+      h.r = g.r;
+      for (int s = 0; s < g.nseg; ++s) {
+        h.seg_end[s] = g.seg_end[s];
+        h.bias[s] = g.bias[s];
+        h.lora_b[s] = g.lb[s];
+      }
+      h.scaling = g.scaling;
+    }
+    for (int s = 0, start = 0; s < g.nseg; start = g.seg_end[s], ++s) {
+      sp.part = h.part ? h.part + start : nullptr;
+      sp.tpart = h.tpart ? h.tpart + (int64_t)s * g.M * 16 : nullptr;
+      if (int rc = nf4_gemm_launch(g.x, g.ldx, g.w, start, g.absmax, g.code16, g.blocksize,
+                                   g.bias[s], g.la[s], g.lb[s], g.r, g.scaling, g.y + start,
+                                   g.ldy, g.M, g.seg_end[s] - start, g.K, st,
+                                   pl.S > 1 ? &sp : nullptr))
+        return rc;
+    }
+    return pl.S > 1 ? run_finish(&h, g.y, g.ldy, st) : GRPO_OK;
+  }
   const int64_t total = (int64_t)g.M * g.N;
   nf4_linear_generic<<<dim3((unsigned)cdiv(total, 256)), 256, 0, st>>>(g);
   return launch_check("nf4_linear_generic");
 }
 
-size_t workspace_bytes_for(int M, int N, int K, int r, int nseg, int blocksize) {
-  if (!part_shape_ok(M, N, K, r, nseg, blocksize, nullptr)) return 0;
+size_t workspace_bytes_for(int M, int N, int K, int r, int nseg, int blocksize,
+                           const int* seg_end) {
+  if (!part_shape_ok(M, N, K, r, nseg, blocksize, seg_end)) {
+    // The NF4 GEMM: partial sums when it splits K.  Without the segment ends
+    // (a size query) the plan of one N-column segment bounds every split of N
+    // (more segments make at least as many tiles, so no more slices).
+    GemmPlan pl;
+    if (seg_end) {
+      for (int s = 0, start = 0; s < nseg; start = seg_end[s], ++s)
+        if (!nf4_gemm_ok(M, seg_end[s] - start, K, r, blocksize)) return 0;
+      pl = nf4_gemm_plan(M, K, r, nseg, seg_end);
+    } else {
+      if (!nf4_gemm_ok(M, N, K, r, blocksize)) return 0;
+      pl = nf4_gemm_plan(M, K, r, 1, &N);
+      pl.tpart_bytes = r > 0 ? (size_t)pl.S * nseg * M * 16 * 4 : 0;
+    }
+    return pl.S > 1 ? align256(pl.part_bytes) + pl.tpart_bytes : 0;
+  }
   const PartPlan pl = plan_part(M, N, K, r, nseg);
   return align256(pl.part_bytes) + pl.tpart_bytes;
 }
@@ -2239,7 +2304,7 @@ extern "C" int grpo_nf4_linear_finish(const grpo_linear_parts_t* parts, void* y,
 
 extern "C" size_t grpo_nf4_lora_linear_workspace_bytes(int M, int N, int K, int r, int nseg,
                                                        int blocksize) {
-  return workspace_bytes_for(M, N, K, r, nseg, blocksize);
+  return workspace_bytes_for(M, N, K, r, nseg, blocksize, nullptr);
 }
 
 extern "C" int grpo_nf4_lora_linear(const void* x, int64_t ldx, const uint8_t* w,

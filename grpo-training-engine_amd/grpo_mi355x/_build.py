@@ -21,7 +21,7 @@ NATIVE_DIR = PKG_DIR / "_native"
 LIB_PATH = NATIVE_DIR / "libgrpo_hip.so"
 ARCH = "gfx950"
 
-SOURCES = ("capi.hip", "nf4_linear.hip", "nf4_tile.hip", "paged_attention.hip",
+SOURCES = ("capi.hip", "nf4_linear.hip", "nf4_tile.hip", "nf4_gemm.hip", "paged_attention.hip",
            "decode_ops.hip", "lm_head.hip", "sampling.hip", "nf4_backward.hip")
 
 

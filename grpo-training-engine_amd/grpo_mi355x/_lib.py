@@ -89,6 +89,12 @@ SIGNATURES = {
         [_VP, _I64, _VP, _VP, _VP, _I32, _VP, _VP, _VP, _I32, _F32, _VP, _I64, _I32, _I32, _I32,
          _VP, _SZ, _VP],
     ),
+    "grpo_nf4_gemm_supported": (_I32, [_I32, _I32, _I32, _I32, _I32]),
+    "grpo_nf4_gemm": (
+        _I32,
+        [_VP, _I64, _VP, _VP, _VP, _I32, _VP, _VP, _VP, _I32, _F32, _VP, _I64, _I32, _I32, _I32,
+         _VP],
+    ),
     "grpo_nf4_lora_linear_grouped": (
         _I32,
         [_VP, _I64, _VP, _VP, _VP, _I32, _I32, _VP, _VP, _VP, _VP, _I32, _F32, _VP, _I64, _I32,

@@ -12,9 +12,10 @@ Same call surface and dispatch as the reference's
 * shape/dtype/device problems -> ``ValueError`` (``_validate_inputs``,
   ``:435-487``); rank <= 0 -> ``ValueError`` (``:670-671``).
 
-The fused forward is ``grpo_nf4_lora_linear`` (split-K kernel) up to 64 rows
-and, for training-sized batches, the weight dequantized once (bit-exact) plus
-bf16 GEMMs with the same rounding points.  The backward (``:761-930``) keeps the
+The fused forward is ``grpo_nf4_lora_linear``: the split-K kernel up to 64
+rows, the NF4 GEMM (weight decoded in the kernel, epilogue fused) beyond, and
+for the largest training batches (``fused_forward_rows``) the weight
+dequantized once (bit-exact) plus bf16 GEMMs with the same rounding points.  The backward (``:761-930``) keeps the
 reference's gradients and rounding points: grad_x's NF4 product on the fused
 ``grpo_nf4_grad_x`` kernel (LoRA part added in its store) below
 ``GRAD_X_GEMM_MIN_ROWS`` rows for the shapes it tiles, otherwise dequantize +
@@ -103,6 +104,17 @@ def _bf16_scalar(v: float) -> float:
 GRAD_X_GEMM_MIN_ROWS = 1024
 
 
+def fused_forward_rows(k: int) -> int:
+    """Most rows for which the forward runs the fused NF4 GEMM rather than the
+    dequantized weight + hipBLASLt.  Measured on MI355X over the Qwen2-1.5B
+    projection shapes (r = 16): the fused GEMM is faster up to 4096 rows for
+    K = 1536 (e.g. gate at 4096 rows: 217 us against 257 us) and up to 1024
+    rows for down_proj's K = 8960 (96 against 84 us at 1024 rows with LoRA, 73
+    against 84 without); from 8192 rows hipBLASLt's GEMM wins for every shape.
+    """
+    return 4096 if k <= 4096 else 1024
+
+
 class FusedLoRAFunction(torch.autograd.Function):
     """Forward = one fused NF4+LoRA kernel launch (``lora_forward.py:653-759``);
     backward = the reference's gradients (``:761-930``): grad_x from the NF4
@@ -123,7 +135,9 @@ class FusedLoRAFunction(torch.autograd.Function):
             w = w.view(torch.uint8)
         x_flat = x.contiguous().view(m, k)
         out = torch.empty((m, n), device=x.device, dtype=x.dtype)
-        if m > 0 and n > 0 and ops.nf4_linear_plan(m, n, k, r, 1, blocksize) is None:
+        fused = (ops.nf4_linear_plan(m, n, k, r, 1, blocksize) is not None
+                 or (m <= fused_forward_rows(k) and ops.nf4_gemm_supported(m, n, k, r, blocksize)))
+        if m > 0 and n > 0 and not fused:
             # rows beyond the split-K kernel's (training batches): W dequantized
             # once (bit-exact), then bf16 GEMMs with the kernel's rounding points
             # (lora_forward.py:246-257): bf16(x W^T), + bias, t = bf16(x A^T),

@@ -145,8 +145,9 @@ def nf4_lora_linear(x2d: torch.Tensor, packed: torch.Tensor, absmax: torch.Tenso
     """``y[M, N] = W_nf4(x) + bias + B(A(x)) * scaling`` (bf16).
 
     Up to 32 rows: the one-launch tile kernel (``grpo_nf4_tile_linear``, LoRA A
-    packed once per tensor version); otherwise split-K partial sums + finish
-    (two launches) on the fast path, one generic launch for other shapes.
+    packed once per tensor version); up to 64 rows split-K partial sums +
+    finish (two launches); beyond, the NF4 GEMM (one launch, or K slices +
+    finish when the tiles are few); one generic launch for other shapes.
     """
     lib = _lib.device_library()
     _need_cuda(x2d, packed, absmax, code, bias, lora_a, lora_b)
@@ -325,6 +326,12 @@ def ctypes_byref(obj):
     import ctypes
 
     return ctypes.byref(obj)
+
+
+def nf4_gemm_supported(m: int, n: int, k: int, r: int, blocksize: int) -> bool:
+    """True if the NF4 GEMM (``grpo_nf4_gemm``; more than 64 rows) takes this
+    shape (alignment aside)."""
+    return bool(_lib.library().grpo_nf4_gemm_supported(m, n, k, r, int(blocksize)))
 
 
 def nf4_linear_plan(m: int, n: int, k: int, r: int, nseg: int,

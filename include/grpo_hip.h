@@ -227,13 +227,28 @@ size_t grpo_nf4_lora_linear_workspace_bytes(int M, int N, int K, int r, int nseg
  *   y       : bf16 [M, N], row stride ldy
  *   workspace: grpo_nf4_lora_linear_workspace_bytes(...) bytes (no
  *             initialisation needed); two launches (partials + finish).
- * Shapes outside the split-K path take a one-thread-per-output kernel with
- * the same arithmetic and need no workspace. */
+ * Shapes outside the split-K path (M > 64) take the NF4 GEMM
+ * (grpo_nf4_gemm below; no workspace), and shapes outside both a
+ * one-thread-per-output kernel with the same arithmetic. */
 int grpo_nf4_lora_linear(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
                          const float* code16, int blocksize, const void* bias, const void* lora_a,
                          const void* lora_b, int r, float scaling, void* y, int64_t ldy, int M,
                          int N, int K, void* workspace, size_t workspace_bytes,
                          grpo_stream_t stream);
+
+/* NF4 (+ bias, + LoRA) linear for batches of more than 64 rows: one MFMA GEMM
+ * launch, the weight decoded in registers, the reference epilogue in the
+ * kernel -- _lora_forward_kernel for any M (src/triton_kernels/lora_forward.py:
+ * 107-260, the forward of FusedLoRAFunction :653-759).  Same arguments and
+ * result as grpo_nf4_lora_linear, no workspace.  Requires K % 32 == 0, r <= 32,
+ * a power-of-two blocksize >= 32, x rows and w (and lora_a) 16-byte aligned
+ * (ldx % 8 == 0); any M and N.  grpo_nf4_gemm_supported: 1 if the shape is
+ * taken (alignment aside), else 0. */
+int grpo_nf4_gemm_supported(int M, int N, int K, int r, int blocksize);
+int grpo_nf4_gemm(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                  const float* code16, int blocksize, const void* bias, const void* lora_a,
+                  const void* lora_b, int r, float scaling, void* y, int64_t ldy, int M, int N,
+                  int K, grpo_stream_t stream);
 
 /* Grouped form: the output rows are split into nseg (1..4) consecutive
  * segments of seg_rows[s] rows, stacked in ONE NF4 weight (w/absmax cover all
