@@ -68,6 +68,11 @@ def parse():
                     help="time the backward's NF4 input-gradient product (grpo_nf4_grad_x and "
                          "dequantize + bf16 GEMM) at Qwen2-1.5B training shapes, M = 4096 "
                          "(an extra measurement, not the headline)")
+    ap.add_argument("--wide-linear", action="store_true",
+                    help="time the NF4+LoRA linear beyond the decode batches (the NF4 GEMM, "
+                         "grpo_nf4_gemm, against dequantize + hipBLASLt): the reference "
+                         "harness shape and the Qwen2-1.5B projections at 512 and 4096 rows "
+                         "(an extra measurement, not the headline)")
     ap.add_argument("--config", type=int, default=3, choices=(1, 2, 3, 4, 5),
                     help="BASELINE config: 3 (default, the headline metric), 1 (one layer of "
                          "paged decode attention), 2 (NF4+LoRA linear at M=8), 4 (G=32 ragged "
@@ -713,6 +718,79 @@ def run_grad_x(args):
         "shapes": rows}), flush=True)
 
 
+def run_wide_linear(args):
+    """y = the fused NF4 + LoRA linear (bias, r = 16, scaling 2) for more than 64
+    rows: the reference harness shape (tools/benchmark_lora_layer.py:68-75:
+    4 x 64 rows, 1024 x 1024) and the Qwen2-1.5B projections (q/o 1536 x 1536,
+    k/v 256 x 1536, gate/up 8960 x 1536, down 1536 x 8960) at 512 rows (a
+    prefill chunk) and 4096 rows (a training batch).  The NF4 GEMM (one
+    grpo_nf4_lora_linear call: nf4_gemm_mfma, K slices + nf4_finish when the
+    tiles are few) against the weight dequantized + hipBLASLt (the path it
+    replaces), both timed with HIP events on the stream they run on.  Random
+    bf16 x, random NF4 bytes.  One JSON line; roofline = bf16 MFMA."""
+    import torch
+    import torch.nn.functional as F
+
+    from grpo_mi355x import _lib
+    from grpo_mi355x.kernels import ops
+    from grpo_mi355x.kernels.lora_forward import _bf16_scalar
+
+    _lib.device_library()
+    dev = torch.device("cuda:0")
+    reps = max(args.steps, 1) * 10
+    code = torch.linspace(-1.0, 1.0, 16, device=dev)
+    shapes = [("harness", 256, 1024, 1024)]
+    for m in (512, 4096):
+        shapes += [(f"q/o@{m}", m, 1536, 1536), (f"k/v@{m}", m, 256, 1536),
+                   (f"gate/up@{m}", m, 8960, 1536), (f"down@{m}", m, 1536, 8960)]
+    r, rows = 16, []
+    for (name, m, n, k) in shapes:
+        g = torch.Generator(device=dev).manual_seed(m + n + k)
+        x = torch.randn(m, k, device=dev, generator=g).to(torch.bfloat16)
+        packed = torch.randint(0, 256, (n * k // 2,), dtype=torch.uint8, device=dev, generator=g)
+        absmax = torch.rand(n * k // 64, device=dev, generator=g) * 0.05
+        a = (torch.randn(r, k, device=dev, generator=g) * 0.01).to(torch.bfloat16)
+        b = (torch.randn(n, r, device=dev, generator=g) * 0.01).to(torch.bfloat16)
+        bias = (torch.randn(n, device=dev, generator=g) * 0.01).to(torch.bfloat16)
+        out = torch.empty(m, n, device=dev, dtype=torch.bfloat16)
+        fused = lambda: ops.nf4_lora_linear(x, packed, absmax, code, 64, n, bias=bias, lora_a=a,
+                                            lora_b=b, scaling=2.0, out=out)
+
+        def dequant_gemm():
+            wb = ops.nf4_dequant(packed, absmax, code, n * k, 64).view(n, k)
+            acc = F.linear(x, wb) + bias
+            return torch.add(acc, F.linear(F.linear(x, a), b) * _bf16_scalar(2.0))
+
+        row = dict(shape=name, M=m, N=n, K=k)
+        for key, fn in (("nf4_gemm", fused), ("dequant_gemm", dequant_gemm)):
+            for _ in range(3):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            us = e0.elapsed_time(e1) / reps * 1e3
+            row[key] = dict(us=round(us, 1), tflops=round(2 * m * n * k / us / 1e6, 1))
+        log(f"{name} M={m} N={n} K={k}: {row}")
+        rows.append(row)
+    tot = sum(r_["nf4_gemm"]["us"] for r_ in rows)
+    flops = sum(2 * r_["M"] * r_["N"] * r_["K"] for r_ in rows)
+    ach = flops / tot / 1e6
+    print(json.dumps({
+        "metric": "NF4+LoRA linear TFLOP/s beyond 64 rows (NF4 GEMM, all shapes)",
+        "value": round(ach, 1), "unit": "TFLOP/s", "n_gpus": 1, "steps": reps, "warmup": 3,
+        "higher_is_better": True, "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (random bf16 x, random NF4 bytes)",
+        "config": {"workload": "fused NF4+LoRA forward at prefill and training batches",
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(ach, 1), "peak": 2500.0,
+                     "unit": "TFLOP/s", "frac": round(ach / 2500.0, 4), "traffic": None},
+        "shapes": rows}), flush=True)
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -722,6 +800,8 @@ def main():
         sys.exit(2)
     if args.grad_x:
         return run_grad_x(args)
+    if args.wide_linear:
+        return run_wide_linear(args)
     if args.config != 3:
         from grpo_mi355x import _lib
 

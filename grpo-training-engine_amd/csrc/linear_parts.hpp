@@ -56,6 +56,8 @@ struct GemmPlan {
 };
 bool nf4_gemm_ok(int M, int N, int K, int r, int blocksize);
 GemmPlan nf4_gemm_plan(int M, int K, int r, int nseg, const int* seg_end);
+// The finish of a K-split GEMM (16 rows per workgroup).
+int nf4_gemm_finish(const grpo_linear_parts_t* h, uint16_t* y, int64_t ldy, hipStream_t st);
 int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wrow0,
                     const float* absmax, const float* code16, int blocksize,
                     const uint16_t* bias, const uint16_t* la, const uint16_t* lb, int r,

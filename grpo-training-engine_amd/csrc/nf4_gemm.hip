@@ -316,6 +316,81 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
   }
 }
 
+// Epilogue of a K-split GEMM: y[m, n] from the partial sums, a workgroup per
+// 16 rows x 64 columns, a thread per (row, four columns): every thread's
+// partial sums go out at once (one memory round trip).  The LoRA t of the 16
+// rows is summed once into LDS (slice order, as every consumer sums them) and
+// the 64 columns' LoRA B rows are staged in LDS once (the per-row finish of
+// the decode batches loads them for every row: 32 bytes of B per output).
+constexpr int FR_ROWS = 16, FR_COLS = 64;
+
+__global__ void __launch_bounds__(256) nf4_finish_rows(LinParts o, uint16_t* __restrict__ y,
+                                                       int64_t ldy) {
+  __shared__ float ts[FR_ROWS][MAXSEG * 16];
+  __shared__ uint4 lbs[FR_COLS * 2];  // B rows (r == 16, 16-byte aligned): two halves per column
+  const int tid = threadIdx.x;
+  const int m0 = blockIdx.y * FR_ROWS, c0 = blockIdx.x * FR_COLS;
+  const int rows = min(FR_ROWS, o.M - m0);
+  const int row = tid >> 4, n = c0 + 4 * (tid & 15);
+  const int m = m0 + row;
+  Fetch4<> f;  // lin_fetch4 without the B rows (staged below)
+  if (m < o.M && n < o.N) {
+    const float4* p = reinterpret_cast<const float4*>(o.part + (int64_t)m * o.N + n);
+    const int64_t stride = (int64_t)o.M * o.N / 4;
+#pragma unroll
+    for (int k = 0; k < MAX_SLICES; ++k)
+      if (k < o.S) f.part[k] = p[k * stride];
+    f.seg = lin_seg(o, n);
+    f.nl = n - (f.seg > 0 ? sel_seg(o.seg_end, f.seg - 1) : 0);
+    const uint16_t* bias = sel_seg(o.bias, f.seg);
+    if (bias && o.bias_vec) f.bias = *reinterpret_cast<const uint2*>(bias + f.nl);
+  }
+  if (o.r > 0) {
+    const int per_row = o.nseg * 4;
+    const int64_t stride = (int64_t)o.nseg * o.M * 4;  // float4s per slice
+    for (int i = tid; i < rows * per_row; i += 256) {
+      const int rr = i / per_row, it = i - rr * per_row;
+      const int seg = it >> 2, q = it & 3;
+      const float4* p =
+          reinterpret_cast<const float4*>(o.tpart + ((int64_t)seg * o.M + m0 + rr) * 16) + q;
+      float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+      for (int k = 0; k < o.S; ++k) {
+        const float4 v = p[k * stride];
+        acc.x += v.x;
+        acc.y += v.y;
+        acc.z += v.z;
+        acc.w += v.w;
+      }
+      float* t = &ts[rr][seg * 16 + 4 * q];
+      t[0] = round_bf(acc.x);
+      t[1] = round_bf(acc.y);
+      t[2] = round_bf(acc.z);
+      t[3] = round_bf(acc.w);
+    }
+    if (o.lb_vec && tid < FR_COLS * 2) {
+      const int col = min(c0 + (tid >> 1), o.N - 1);
+      const int seg = lin_seg(o, col);
+      const int nl = col - (seg > 0 ? sel_seg(o.seg_end, seg - 1) : 0);
+      lbs[tid] = reinterpret_cast<const uint4*>(sel_seg(o.lb, seg) + (int64_t)nl * 16)[tid & 1];
+    }
+  }
+  __syncthreads();
+  if (m >= o.M || n >= o.N) return;
+  if (o.r > 0 && o.lb_vec) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f.lb[j] = lbs[8 * (tid & 15) + j];
+  }
+  float v[4];
+  lin_finish4(o, ts[row], f, v);
+  uint16_t* yr = y + (int64_t)m * ldy + n;
+  if (aligned8(yr)) {
+    *reinterpret_cast<uint2*>(yr) = make_uint2(pack_bf2(v[0], v[1]), pack_bf2(v[2], v[3]));
+  } else {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) yr[c] = f2bf(v[c]);
+  }
+}
+
 bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
 template <typename Kern>
@@ -355,14 +430,14 @@ GemmPlan nf4_gemm_plan(int M, int K, int r, int nseg, const int* seg_end) {
   // stage (128 K values) takes about 2.2 us whatever the tile count (its loads'
   // latency), 512 workgroups run at once; a split adds the float32 partial
   // sums (written and read back, ~4 TB/s), the finish launch and, with LoRA,
-  // the finish's per-output rank sums (~8 ns per 1000 outputs).
+  // the finish's per-output rank sums (~2 ns per 1000 outputs).
   const int N = seg_end[nseg - 1];
   const double outs = (double)M * N;
   auto est = [&](int S, int* kst, int* slices) {
     *kst = (int)cdiv(nst, S);
     *slices = (int)cdiv(nst, *kst);
     double t = (double)cdiv(tiles * *slices, 512) * *kst * 2.2;
-    if (*slices > 1) t += *slices * outs * 8.0 / 4e6 + 4.0 + (r > 0 ? outs * 8e-6 : 0.0);
+    if (*slices > 1) t += *slices * outs * 8.0 / 4e6 + 4.0 + (r > 0 ? outs * 2e-6 : 0.0);
     return t;
   };
   double best = 0.0;
@@ -450,6 +525,16 @@ int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wr
     nf4_gemm_mfma<0><<<grid, GM_T, GM_LDS, st>>>(a);
   }
   return launch_check("nf4_gemm_mfma");
+}
+
+int nf4_gemm_finish(const grpo_linear_parts_t* h, uint16_t* y, int64_t ldy, hipStream_t st) {
+  LinParts o;
+  if (int rc = make_parts(h, &o)) return rc;
+  if (!y) return einval("null y");
+  if (ldy < o.N) return einval("ldy smaller than N");
+  nf4_finish_rows<<<dim3((unsigned)cdiv(o.N, FR_COLS), (unsigned)cdiv(o.M, FR_ROWS)), 256, 0,
+                    st>>>(o, y, ldy);
+  return launch_check("nf4_finish_rows");
 }
 
 }  // namespace grpo

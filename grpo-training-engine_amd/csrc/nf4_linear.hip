@@ -2129,7 +2129,7 @@ int run_linear(const GenArgs& g, void* workspace, size_t workspace_bytes, hipStr
                                    pl.S > 1 ? &sp : nullptr))
         return rc;
     }
-    return pl.S > 1 ? run_finish(&h, g.y, g.ldy, st) : GRPO_OK;
+    return pl.S > 1 ? nf4_gemm_finish(&h, g.y, g.ldy, st) : GRPO_OK;
   }
   const int64_t total = (int64_t)g.M * g.N;
   nf4_linear_generic<<<dim3((unsigned)cdiv(total, 256)), 256, 0, st>>>(g);
