@@ -28,9 +28,10 @@
 //  * Edges: rows >= M read row M - 1 and are not stored; columns >= N read
 //    row N - 1 of W and are not stored; a last stage past K (K % 128 != 0)
 //    stages zero x (its weight loads are clamped into the row).
-//  * Workgroup -> tile: the dispatcher places workgroup i on XCD i mod 8, so
-//    the workgroups of one column tile (all row tiles) get ids with equal
-//    residues mod 8 and read that tile's weights through one L2.
+//  * Workgroup -> tile: the dispatcher places workgroup i on XCD i mod 8; the
+//    tiles, column tile by column tile, are cut into 8 equal runs and run x
+//    goes to the ids = x mod 8, so the row tiles of a column tile read its
+//    weights through one L2 and every XCD gets the same number of tiles.
 #include <algorithm>
 
 #include "linear_parts.hpp"
@@ -52,6 +53,8 @@ constexpr int GM_MAX_R = 32;
 constexpr size_t GM_LDS =
     (size_t)(2 * GM_BM * GM_XS + GM_BM * GM_TS) * 2;  // 79,872 bytes
 static_assert(GM_BM * GM_OS <= 2 * GM_BM * GM_XS, "output tile reuses the x stages");
+constexpr int GM_PS = GM_BN + 4;      // LDS row stride of a float32 partial-sum tile
+static_assert(GM_BM * GM_PS * 2 <= 2 * GM_BM * GM_XS, "partial-sum tile reuses the x stages");
 
 struct GemmArgs {
   const uint16_t* x;
@@ -92,9 +95,14 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
   uint16_t* const ts = lds + 2 * GM_BM * GM_XS;  // t [128][GM_TS] bf16
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int ln = lane & 15, lg = lane >> 4;
-  const int b = blockIdx.x, slot = b >> 3;
-  const int nt = (slot / p.MT) * 8 + (b & 7), mt = slot - (slot / p.MT) * p.MT;
-  if (nt >= p.NT) return;  // padding workgroups of the XCD grouping
+  // Tiles t = nt * MT + mt in order, in 8 contiguous runs of equal length
+  // (+-1): run x goes to the workgroups with ids = x mod 8, which the
+  // dispatcher places on one XCD, so the row tiles of a column tile share
+  // that tile's weights through one L2 and every XCD gets the same work.
+  const int b = blockIdx.x, run = b & 7, T = p.MT * p.NT;
+  const int t = ((run * T) >> 3) + (b >> 3);
+  if (t >= (((run + 1) * T) >> 3)) return;  // past the end of this run
+  const int nt = t / p.MT, mt = t - nt * p.MT;
   const int m0 = mt * GM_BM, n0 = nt * GM_BN;
 
   float code[16];
@@ -215,19 +223,27 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
   }
 
   if (p.part) {
-    // K slice: float32 partial sums (and column tile 0's LoRA t partials)
-    float* pp = p.part + blockIdx.y * p.psl;
+    // K slice: float32 partial sums (and column tile 0's LoRA t partials).
+    // The tile passes through LDS (the x stages are free after the loop's last
+    // barrier) so every thread stores 16-byte row chunks (N % 16 == 0 here).
+    float* const ps = reinterpret_cast<float*>(lds);  // [128][GM_PS]
 #pragma unroll
     for (int rt = 0; rt < GM_RT; ++rt)
 #pragma unroll
-      for (int ct = 0; ct < 2; ++ct) {
-        const int n = n0 + 32 * wave + 16 * ct + ln;
+      for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int m = m0 + rt * 16 + 4 * lg + q;
-          if (m < p.M && n < p.N) pp[(int64_t)m * p.ldp + n] = acc[rt][ct][q];
-        }
-      }
+        for (int q = 0; q < 4; ++q)
+          ps[(rt * 16 + 4 * lg + q) * GM_PS + 32 * wave + 16 * ct + ln] = acc[rt][ct][q];
+    __syncthreads();
+    float* pp = p.part + blockIdx.y * p.psl;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int c = tid + GM_T * i, row = c >> 5, c4 = 4 * (c & 31);
+      const int m = m0 + row, n = n0 + c4;
+      if (m < p.M && n < p.N)
+        *reinterpret_cast<float4*>(pp + (int64_t)m * p.ldp + n) =
+            *reinterpret_cast<const float4*>(ps + row * GM_PS + c4);
+    }
     if (LORA && nt == 0) {
       float* tp = p.tpart + blockIdx.y * p.tsl;
 #pragma unroll
@@ -512,8 +528,7 @@ int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wr
     a.tpart = split->tpart;
     a.tsl = split->tsl;
   }
-  const unsigned groups = (unsigned)cdiv(a.NT, 8);
-  const dim3 grid(groups * 8u * (unsigned)a.MT, slices);
+  const dim3 grid(8u * (unsigned)cdiv((int64_t)a.MT * a.NT, 8), slices);
   if (r > 16) {
     if (int rc = allow_lds(nf4_gemm_mfma<2>)) return rc;
     nf4_gemm_mfma<2><<<grid, GM_T, GM_LDS, st>>>(a);
