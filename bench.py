@@ -257,7 +257,7 @@ def run_cfg4(args):
     import torch
 
     from grpo_mi355x.core.kv_pool import PagedKVPool
-    from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill, prefill_chunk
+    from grpo_mi355x.rollout.decode import DecodeEngine, prefill, prefill_engine
     from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
 
     dev = torch.device("cuda:0")
@@ -275,7 +275,7 @@ def run_cfg4(args):
     G = P * S
     pool = PagedKVPool(cfg.num_hidden_layers, P * width + G * (width + 1),
                        cfg.num_key_value_heads, cfg.head_dim, BS, device=dev)
-    pre = PrefillEngine(model, pool, prefill_chunk(max(lens) - 1), width)
+    pre = prefill_engine(model, pool, max(lens) - 1, width)
     parents = [prefill(pre, pool, tuple(p), width) for p in prompts]
     del pre
     eng = DecodeEngine(model, pool, G, width)
@@ -812,7 +812,7 @@ def main():
 
     from grpo_mi355x import _lib
     from grpo_mi355x.core.kv_pool import PagedKVPool
-    from grpo_mi355x.rollout.decode import DecodeEngine, PrefillEngine, prefill, prefill_chunk
+    from grpo_mi355x.rollout.decode import DecodeEngine, prefill, prefill_engine
     from grpo_mi355x.rollout.qwen2 import Qwen2Config, build_random_model
 
     _lib.device_library()
@@ -833,7 +833,7 @@ def main():
     pool = PagedKVPool(cfg.num_hidden_layers, width * (G + 2), cfg.num_key_value_heads,
                        cfg.head_dim, BS, device=dev)
     # chunked prefill of the shared prompt (not part of the timed decode)
-    pre = PrefillEngine(model, pool, prefill_chunk(P - 1), width)
+    pre = prefill_engine(model, pool, P - 1, width)
     pre.capture()
     torch.cuda.synchronize()
     # one untimed prefill (first use of the pool blocks and of the graph), then

@@ -1033,6 +1033,200 @@ class PrefillEngine(DecodeEngine):
             self.step()
 
 
+class GemmPrefillEngine:
+    """Chunked paged prefill with wide chunks: up to ``chunk`` (default 512)
+    prompt tokens of one sequence per pass, every linear on the NF4 GEMM
+    (``grpo_nf4_lora_linear`` beyond 64 rows: ``nf4_gemm_mfma``), so a
+    511-token prompt reads each NF4 weight once per row tile of one pass
+    instead of once per 64-token chunk.
+
+    The rows are positions p .. p + c - 1 sharing the sequence's block table,
+    as in ``PrefillEngine``, and every launch keeps the decode step's rounding
+    points: embedding -> per layer RMSNorm (+ the residual add of the previous
+    layer's down_proj) -> q|k|v (grouped: one GEMM per projection, bias and
+    LoRA in the kernel) -> RoPE + K/V append (``grpo_rope_append``) ->
+    attention over p + i + 1 tokens (``grpo_paged_attn_decode``) -> o_proj ->
+    residual add + RMSNorm -> gate|up -> SiLU*up -> down_proj.  The reference
+    prefills with one transformers forward and a per-token scatter of K/V
+    (``paged_kv.py:547-586``).  Only the cache is filled: the last layer stops
+    after its append (its attention and MLP feed nothing that is kept).  The
+    pass is captured once into a HIP graph; rows past the end of a short last
+    chunk are masked (slot -1, length 0)."""
+
+    def __init__(self, model: Qwen2ForCausalLM, pool: PagedKVPool, chunk: int, max_blocks: int,
+                 max_pos: Optional[int] = None):
+        self.lib = _lib.device_library()
+        cfg = model.config
+        self.model, self.pool, self.cfg = model, pool, cfg
+        self.B, self.max_blocks = chunk, max_blocks
+        dev = pool.k.device
+        self.device = dev
+        H, D = cfg.hidden_size, cfg.head_dim
+        self.Hq, self.Hkv, self.D, self.H = (cfg.num_attention_heads, cfg.num_key_value_heads, D,
+                                             H)
+        self.I, self.V = cfg.intermediate_size, cfg.vocab_size
+        self.nqkv = (self.Hq + 2 * self.Hkv) * D
+        self.bs = cfg.nf4_blocksize
+        self.max_pos = max_pos or max_blocks * pool.block_size
+        self.cos, self.sin = model.model.rotary_emb.tables(self.max_pos)
+        bf = dict(dtype=torch.bfloat16, device=dev)
+        i32 = dict(dtype=torch.int32, device=dev)
+        B = chunk
+        self.tokens = torch.zeros(B, dtype=torch.int64, device=dev)
+        self.append_pos = torch.full((B,), -1, **i32)
+        self.attn_len = torch.zeros(B, **i32)
+        self.block_tables = torch.full((B, max_blocks), -1, **i32)
+        self.h = torch.zeros(B, H, **bf)
+        self.x = torch.zeros(B, H, **bf)
+        self.y = torch.zeros(B, H, **bf)            # o_proj and down_proj outputs
+        self.qkv = torch.zeros(B, self.nqkv, **bf)
+        self.q_rot = torch.zeros(B, self.Hq, D, **bf)
+        self.attn_out = torch.zeros(B, self.Hq * D, **bf)
+        self.gu = torch.zeros(B, 2 * self.I, **bf)
+        self.act = torch.zeros(B, self.I, **bf)
+        self._rows = torch.arange(B, dtype=torch.int32, device=dev)
+        self._keep = []
+        self.layers = []
+        ws = 0
+        for layer in model.model.layers:
+            at, mlp = layer.self_attn, layer.mlp
+            projs = [at.q_proj, at.k_proj, at.v_proj]
+            r = projs[0].rank
+            arr = ctypes.c_void_p * 4
+            bias = arr(*[p.base_layer.bias.data_ptr() if p.base_layer.bias is not None else None
+                         for p in projs], None)
+            la = arr(*[p.lora_A.weight.data_ptr() if r > 0 else None for p in projs], None)
+            lb = arr(*[p.lora_B.weight.data_ptr() if r > 0 else None for p in projs], None)
+            seg = (ctypes.c_int * 4)(*at.qkv.seg_rows, 0)
+            self._keep += [bias, la, lb, seg]
+            o = at.o_proj
+            oq = o.base_layer.weight.quant_state
+            dq = mlp.down_proj.weight.quant_state
+            self.layers.append(dict(
+                in_norm=layer.input_layernorm.weight, post_norm=layer.post_attention_layernorm.weight,
+                eps=float(layer.input_layernorm.variance_epsilon),
+                qkv=at.qkv, bias=bias, la=la, lb=lb, seg=seg, r=r, scaling=float(projs[0].scaling),
+                o_w=o.base_layer.weight, o_absmax=float_absmax(oq), o_code=oq.code,
+                o_bias=o.base_layer.bias, o_la=o.lora_A.weight, o_lb=o.lora_B.weight,
+                o_r=o.rank, o_scaling=float(o.scaling),
+                gu=mlp.gate_up, down_w=mlp.down_proj.weight, down_absmax=float_absmax(dq),
+                down_code=dq.code))
+            for (n, k, rr, nseg) in ((self.nqkv, H, r, 3), (H, self.Hq * D, o.rank, 1),
+                                     (2 * self.I, H, 0, 1), (H, self.I, 0, 1)):
+                ws = max(ws, int(self.lib.grpo_nf4_lora_linear_workspace_bytes(
+                    B, n, k, rr, nseg, self.bs)))
+        # one workspace for every linear (they run one after another on one stream)
+        self.ws = torch.empty(max(ws, 16), dtype=torch.uint8, device=dev)
+        self.ws_attn = ops.workspace("paged_attn_prefill", max(ops.paged_attention_workspace_bytes(
+            B, self.Hq, self.Hkv, D, pool.block_size, max_blocks), 1), dev)
+        self.embed = model.model.embed_tokens.weight
+        self.graph: Optional[torch.cuda.CUDAGraph] = None
+
+    def launches(self) -> list:
+        """[(kind, launch())] of one pass, bound to torch's current stream."""
+        lib, st, chk = self.lib, _lib.stream_handle(self.device), _lib.check
+        B, H, I, D, Hq, Hkv = self.B, self.H, self.I, self.D, self.Hq, self.Hkv
+        pool, bs = self.pool, self.bs
+        h, x, y = self.h.data_ptr(), self.x.data_ptr(), self.y.data_ptr()
+        qkv, q, ao = self.qkv.data_ptr(), self.q_rot.data_ptr(), self.attn_out.data_ptr()
+        gu, act = self.gu.data_ptr(), self.act.data_ptr()
+        ws, ws_n = self.ws.data_ptr(), self.ws.numel()
+        wsa, wsa_n = self.ws_attn.data_ptr(), self.ws_attn.numel()
+        bt, ap, al = self.block_tables.data_ptr(), self.append_pos.data_ptr(), self.attn_len.data_ptr()
+        ptr = _lib.ptr
+
+        def linear(xp, ldx, w, absmax, code, bias, la, lb, r, sc, out, n, k):
+            return chk(lib.grpo_nf4_lora_linear(
+                xp, ldx, w.data_ptr(), absmax.data_ptr(), code.data_ptr(), bs, ptr(bias),
+                ptr(la) if r > 0 else None, ptr(lb) if r > 0 else None, r, sc, out, n, B, n, k,
+                ws, ws_n, st), "prefill linear")
+
+        out = [("embedding", lambda: chk(lib.grpo_embedding(
+            self.tokens.data_ptr(), self.embed.data_ptr(), self.V, H, h, B, st), "embedding"))]
+        last = len(self.layers) - 1
+        for li, L in enumerate(self.layers):
+            kc, vc = (t.data_ptr() for t in pool.layer(li))
+            # h += the previous layer's down_proj output; x = RMSNorm(h)
+            res = None if li == 0 else y
+            out.append(("rmsnorm", lambda L=L, res=res: chk(lib.grpo_add_rmsnorm(
+                res if res is not None else h, h if res is not None else None,
+                h if res is not None else None, L["in_norm"].data_ptr(), x, B, H, L["eps"], st),
+                "rmsnorm")))
+            qs = L["qkv"]
+            out.append(("qkv", lambda L=L, qs=qs: chk(lib.grpo_nf4_lora_linear_grouped(
+                x, H, qs.packed.data_ptr(), qs.absmax.data_ptr(), qs.code.data_ptr(), bs, 3,
+                L["seg"], L["bias"], L["la"], L["lb"], L["r"], L["scaling"], qkv, self.nqkv, B,
+                H, ws, ws_n, st), "qkv")))
+            out.append(("append", lambda kc=kc, vc=vc: chk(lib.grpo_rope_append(
+                qkv, self.nqkv, Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
+                self.max_pos, ap, q, kc, vc, pool.num_blocks, bt, self.max_blocks,
+                pool.block_size, self.max_blocks, B, st), "append")))
+            if li == last:
+                break  # the last layer's attention and MLP feed nothing kept
+            out.append(("attention", lambda kc=kc, vc=vc: chk(lib.grpo_paged_attn_decode(
+                q, Hq * D, D, kc, vc, pool.num_blocks, bt, self.max_blocks, al, ao, 1, B, Hq,
+                Hkv, D, pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n, st),
+                "attention")))
+            out.append(("o", lambda L=L: linear(
+                ao, Hq * D, L["o_w"], L["o_absmax"], L["o_code"], L["o_bias"], L["o_la"],
+                L["o_lb"], L["o_r"], L["o_scaling"], y, H, Hq * D)))
+            out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm(
+                y, h, h, L["post_norm"].data_ptr(), x, B, H, L["eps"], st), "post_norm")))
+            g = L["gu"]
+            out.append(("gate_up", lambda g=g: chk(lib.grpo_nf4_lora_linear(
+                x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), bs, None,
+                None, None, 0, 1.0, gu, 2 * I, B, 2 * I, H, ws, ws_n, st), "gate_up")))
+            out.append(("silu_mul", lambda: chk(lib.grpo_silu_mul(gu, 2 * I, I, act, I, B, st),
+                                                "silu_mul")))
+            out.append(("down", lambda L=L: linear(
+                act, I, L["down_w"], L["down_absmax"], L["down_code"], None, None, None, 0, 1.0,
+                y, H, I)))
+        return out
+
+    def _forward(self):
+        for _, fn in self.launches():
+            fn()
+
+    def capture(self):
+        """Record one pass into a HIP graph (after a warm-up pass that appends
+        nothing: every row masked)."""
+        self.append_pos.fill_(-1)
+        self.attn_len.zero_()
+        s = torch.cuda.Stream(device=self.device)
+        s.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(s):
+            self._forward()
+        torch.cuda.current_stream(self.device).wait_stream(s)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            self._forward()
+        self.graph = g
+
+    def step(self):
+        if self.graph is not None:
+            self.graph.replay()
+        else:
+            self._forward()
+
+    def run_prompt(self, table: torch.Tensor, prompt: torch.Tensor, n: int):
+        """Cache tokens ``prompt[0 .. n-1]`` at positions 0 .. n-1 of the sequence
+        whose block table row is ``table`` ([1, w] int32, its blocks reserved)."""
+        if self.graph is None:
+            self.capture()
+        w = table.shape[1]
+        self.block_tables.fill_(-1)
+        self.block_tables[:, :w].copy_(table.view(1, w).expand(self.B, w))
+        none = torch.full_like(self._rows, -1)
+        for p in range(0, n, self.B):
+            c = min(self.B, n - p)
+            valid = self._rows < c
+            self.tokens.zero_()
+            self.tokens[:c].copy_(prompt[p:p + c])
+            self.append_pos.copy_(torch.where(valid, self._rows + p, none))
+            self.attn_len.copy_(torch.where(valid, self._rows + (p + 1), none + 1))
+            self.step()
+
+
 def release_decode_caches(model=None) -> None:
     """Free what the decode path keeps between rollouts, e.g. before the
     training phase: the tile-order lm_head copy on ``model`` (and on its
@@ -1064,6 +1258,25 @@ def prefill_chunk(n: int, cap: int = 64) -> int:
     return max(1, min(cap, n))
 
 
+# Prompts of more than this many cached tokens prefill on the NF4 GEMM
+# (``GemmPrefillEngine``, chunks of up to GEMM_PREFILL_CHUNK rows); shorter ones
+# on the decode step's launches (``PrefillEngine``).
+GEMM_PREFILL_MIN = 64
+GEMM_PREFILL_CHUNK = 512
+
+
+def prefill_engine(model: Qwen2ForCausalLM, pool: PagedKVPool, n: int, width: int,
+                   max_pos: Optional[int] = None):
+    """The prefill engine for prompts of up to ``n`` cached tokens over block
+    tables of ``width`` entries: ``GemmPrefillEngine`` beyond GEMM_PREFILL_MIN
+    tokens (chunk = n rounded up to 64, at most GEMM_PREFILL_CHUNK), else a
+    ``PrefillEngine`` of ``prefill_chunk(n)`` rows."""
+    if n > GEMM_PREFILL_MIN:
+        chunk = min(GEMM_PREFILL_CHUNK, (n + 63) // 64 * 64)
+        return GemmPrefillEngine(model, pool, chunk, width, max_pos=max_pos)
+    return PrefillEngine(model, pool, prefill_chunk(n), width, max_pos=max_pos)
+
+
 @torch.no_grad()
 def prefill(engine1: DecodeEngine, pool: PagedKVPool, prompt: tuple, width: int) -> int:
     """Prefill of ``prompt[:-1]`` into a new pool sequence: chunked when
@@ -1071,7 +1284,7 @@ def prefill(engine1: DecodeEngine, pool: PagedKVPool, prompt: tuple, width: int)
     through a B = 1 decode engine."""
     sid = pool.allocate(len(prompt))
     n = len(prompt) - 1
-    if n > 0 and isinstance(engine1, PrefillEngine):
+    if n > 0 and isinstance(engine1, (PrefillEngine, GemmPrefillEngine)):
         dev = engine1.device
         engine1.run_prompt(pool.block_table([sid], width, device=dev),
                            torch.tensor(prompt, dtype=torch.int64, device=dev), n)
@@ -1131,7 +1344,7 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
     nblocks = len(uniq) * width + B * (width + 1)
     pool = PagedKVPool(cfg.num_hidden_layers, nblocks, cfg.num_key_value_heads, cfg.head_dim,
                        block_size, device=dev)
-    pre = PrefillEngine(model, pool, prefill_chunk(max(len(r) for r in uniq) - 1), width)
+    pre = prefill_engine(model, pool, max(len(r) for r in uniq) - 1, width)
     parents = {p: prefill(pre, pool, p, width) for p in uniq}
     del pre
     sids = []
@@ -1161,5 +1374,5 @@ def paged_kv_decode_model(model: Qwen2ForCausalLM, input_ids: torch.Tensor,
     return eng.generated.clone()
 
 
-__all__ = ["DecodeEngine", "PrefillEngine", "paged_kv_decode_model", "prefill",
-           "prefill_chunk", "release_decode_caches"]
+__all__ = ["DecodeEngine", "PrefillEngine", "GemmPrefillEngine", "paged_kv_decode_model",
+           "prefill", "prefill_chunk", "prefill_engine", "release_decode_caches"]
