@@ -32,6 +32,25 @@ inline int launch_check(const char* name) { return hip_check(hipGetLastError(), 
 
 inline hipStream_t as_stream(grpo_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
+// Lets kernel KERN use up to BYTES of dynamic LDS, less its static LDS (the
+// two share gfx950's 160 KiB): hipFuncSetAttribute once per kernel (the kernel
+// is a template argument because the instantiations of one kernel template
+// share a function type).
+template <auto KERN, int BYTES>
+int allow_dynamic_lds() {
+  static const int rc = [] {
+    hipFuncAttributes fa{};
+    if (int e = hip_check(hipFuncGetAttributes(&fa, reinterpret_cast<const void*>(KERN)),
+                          "hipFuncGetAttributes"))
+      return e;
+    return hip_check(hipFuncSetAttribute(reinterpret_cast<const void*>(KERN),
+                                         hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         BYTES - (int)fa.sharedSizeBytes),
+                     "hipFuncSetAttribute");
+  }();
+  return rc;
+}
+
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 __host__ __device__ inline bool aligned16(const void* ptr) {
@@ -60,6 +79,31 @@ __device__ __forceinline__ uint32_t pack_bf2(float lo, float hi) {
 }
 __device__ __forceinline__ float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t p) { return __uint_as_float(p & 0xFFFF0000u); }
+
+// float16 (IEEE half) counterparts, round-to-nearest-even.  The empty asm
+// keeps f a float32 value: without it the compiler contracts a product feeding
+// the conversion into v_fma_mixlo_f16 (one rounding of the exact product, and
+// -0 * ... + 0 = +0), where the reference rounds the float32 product first.
+__device__ __forceinline__ uint16_t f2h(float f) {
+  asm("" : "+v"(f));
+  return __builtin_bit_cast(uint16_t, (_Float16)f);
+}
+__device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ float round_h(float f) { return h2f(f2h(f)); }
+__device__ __forceinline__ uint32_t pack_h2(float lo, float hi) {
+  return (uint32_t)f2h(lo) | ((uint32_t)f2h(hi) << 16);
+}
+// The 16-bit float type of a kernel instance: bf16 (F16 = false) or float16.
+template <bool F16>
+__device__ __forceinline__ uint16_t f2e(float f) { return F16 ? f2h(f) : f2bf(f); }
+template <bool F16>
+__device__ __forceinline__ float e2f(uint16_t b) { return F16 ? h2f(b) : bf2f(b); }
+template <bool F16>
+__device__ __forceinline__ float round_e(float f) { return F16 ? round_h(f) : round_bf(f); }
+template <bool F16>
+__device__ __forceinline__ uint32_t pack_e2(float lo, float hi) {
+  return F16 ? pack_h2(lo, hi) : pack_bf2(lo, hi);
+}
 
 __device__ __forceinline__ uint32_t perm(uint32_t hi, uint32_t lo, uint32_t sel) {
   return __builtin_amdgcn_perm(hi, lo, sel);
@@ -222,6 +266,16 @@ __device__ __forceinline__ bool xcd_arrive(int* cnt, int n, int* err) {
 
 __device__ __forceinline__ f32x4_t mfma16x16x32(uint4 a, uint4 b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a), as_bf16x8(b), c, 0, 0, 0);
+}
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+// v_mfma_f32_16x16x32_f16 (F16) or _bf16 on operands given as 16-bit patterns.
+template <bool F16>
+__device__ __forceinline__ f32x4_t mfma16x16x32_e(uint4 a, uint4 b, f32x4_t c) {
+  if constexpr (F16)
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  else
+    return mfma16x16x32(a, b, c);
 }
 
 }  // namespace grpo

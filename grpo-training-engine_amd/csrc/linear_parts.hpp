@@ -62,7 +62,7 @@ int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wr
                     const float* absmax, const float* code16, int blocksize,
                     const uint16_t* bias, const uint16_t* la, const uint16_t* lb, int r,
                     float scaling, uint16_t* y, int64_t ldy, int M, int N, int K,
-                    hipStream_t st, const GemmSplit* split);
+                    hipStream_t st, const GemmSplit* split, bool f16 = false);
 
 // Segment of column n, branch-free: the segment ends are increasing (checked by
 // make_parts) and n < N = the last end.  (A loop over seg_end made the compiler

@@ -31,15 +31,6 @@ constexpr int LM_WAVES = GRPO_LM_WAVES;  // vocabulary tiles per workgroup (x st
 constexpr int ADV_T = 1024;
 constexpr size_t LM_LDS_MAX = 163840;  // gfx950: 160 KiB of LDS per workgroup
 
-// Lets a kernel use more than 64 KiB of dynamic LDS (once per instantiation).
-template <typename K>
-int allow_lds(K kernel) {
-  static const int rc = hip_check(
-      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)LM_LDS_MAX),
-      "hipFuncSetAttribute");
-  return rc;
-}
 
 struct LmArgs {
   const uint16_t* x;
@@ -154,7 +145,7 @@ __global__ void __launch_bounds__(64 * LM_WAVES) lm_head_argmax_kernel(LmArgs p)
   {
     const int chunks = p.K / 8, total = p.M * chunks;
     // after x in the dynamic LDS (a static array would lower the dynamic limit
-    // that allow_lds sets for every instantiation)
+    // that allow_dynamic_lds sets for every instantiation)
     float* sInv = reinterpret_cast<float*>(xs + p.M * xstride);
     if (NORM) {
       // wave w: 1 / rms of row w from its group sums (4 per lane, clamped
@@ -474,13 +465,13 @@ int run_lm_head(const void* x, int64_t ldx, const void* w, int V, int K, int M, 
       return einval("lm_head: vocabulary too large for the wide kernel");
     const dim3 wgrid((unsigned)G), wblock(64 * LM_WIDE_WAVES);
     if (M <= 16) {
-      if (int rc = allow_lds(lm_head_argmax_wide<1>)) return rc;
+      if (int rc = allow_dynamic_lds<lm_head_argmax_wide<1>, (int)LM_LDS_MAX>()) return rc;
       lm_head_argmax_wide<1><<<wgrid, wblock, clds, st>>>(a, KC);
     } else if (M <= 32) {
-      if (int rc = allow_lds(lm_head_argmax_wide<2>)) return rc;
+      if (int rc = allow_dynamic_lds<lm_head_argmax_wide<2>, (int)LM_LDS_MAX>()) return rc;
       lm_head_argmax_wide<2><<<wgrid, wblock, clds, st>>>(a, KC);
     } else {
-      if (int rc = allow_lds(lm_head_argmax_wide<4>)) return rc;
+      if (int rc = allow_dynamic_lds<lm_head_argmax_wide<4>, (int)LM_LDS_MAX>()) return rc;
       lm_head_argmax_wide<4><<<wgrid, wblock, clds, st>>>(a, KC);
     }
     return launch_check("lm_head_argmax_wide");
@@ -490,16 +481,16 @@ int run_lm_head(const void* x, int64_t ldx, const void* w, int V, int K, int M, 
     a.nG = nrm->groups;
     a.nw = nrm->weight;
     a.neps = nrm->eps;
-    if (int rc = allow_lds(lm_head_argmax_kernel<1, true>)) return rc;
+    if (int rc = allow_dynamic_lds<lm_head_argmax_kernel<1, true>, (int)LM_LDS_MAX>()) return rc;
     lm_head_argmax_kernel<1, true><<<grid, block, lds, st>>>(a);
   } else if (M <= 16) {
-    if (int rc = allow_lds(lm_head_argmax_kernel<1, false>)) return rc;
+    if (int rc = allow_dynamic_lds<lm_head_argmax_kernel<1, false>, (int)LM_LDS_MAX>()) return rc;
     lm_head_argmax_kernel<1, false><<<grid, block, lds, st>>>(a);
   } else if (M <= 32) {
-    if (int rc = allow_lds(lm_head_argmax_kernel<2, false>)) return rc;
+    if (int rc = allow_dynamic_lds<lm_head_argmax_kernel<2, false>, (int)LM_LDS_MAX>()) return rc;
     lm_head_argmax_kernel<2, false><<<grid, block, lds, st>>>(a);
   } else {
-    if (int rc = allow_lds(lm_head_argmax_kernel<4, false>)) return rc;
+    if (int rc = allow_dynamic_lds<lm_head_argmax_kernel<4, false>, (int)LM_LDS_MAX>()) return rc;
     lm_head_argmax_kernel<4, false><<<grid, block, lds, st>>>(a);
   }
   return launch_check("lm_head_argmax");

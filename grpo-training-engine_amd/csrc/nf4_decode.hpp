@@ -3,7 +3,8 @@
 // Weight format (bitsandbytes Params4bit, read by the reference in
 // src/triton_kernels/lora_forward.py:171-206): W[N,K] flattened row-major,
 // element e = n*K + k, byte e/2, even e = high nibble; one float32 absmax per
-// `blocksize` flat elements; value = bf16_rne(code[q] * absmax).
+// `blocksize` flat elements; value = bf16_rne(code[q] * absmax) (float16_rne
+// for float16 adapters).
 #pragma once
 
 #include "common.hpp"
@@ -34,12 +35,15 @@ struct Lut {
   uint32_t hb[4], lb[4];
 };
 
+// F16: the table holds float16(code[j] * a) instead (the reference's cast to a
+// float16 LoRA dtype, lora_forward.py:206); decode8 moves bytes only.
+template <bool F16 = false>
 __device__ __forceinline__ Lut make_lut(const float (&code)[16], float a) {
   Lut t;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const uint32_t p01 = pack_bf2(code[4 * i] * a, code[4 * i + 1] * a);
-    const uint32_t p23 = pack_bf2(code[4 * i + 2] * a, code[4 * i + 3] * a);
+    const uint32_t p01 = pack_e2<F16>(code[4 * i] * a, code[4 * i + 1] * a);
+    const uint32_t p23 = pack_e2<F16>(code[4 * i + 2] * a, code[4 * i + 3] * a);
     t.hb[i] = perm(p23, p01, 0x07050301u);
     t.lb[i] = perm(p23, p01, 0x06040200u);
   }

@@ -33,6 +33,7 @@
 //    goes to the ids = x mod 8, so the row tiles of a column tile read its
 //    weights through one L2 and every XCD gets the same number of tiles.
 #include <algorithm>
+#include <type_traits>
 
 #include "linear_parts.hpp"
 #include "nf4_decode.hpp"
@@ -87,8 +88,10 @@ struct GemmArgs {
   int64_t tsl;
 };
 
-// TC: LoRA rank tiles of 16 (0: no LoRA, 1: r <= 16, 2: r <= 32).
-template <int TC>
+// TC: LoRA rank tiles of 16 (0: no LoRA, 1: r <= 16, 2: r <= 32).  F16: x,
+// the weight values, LoRA, bias and y in float16 instead of bf16 (the
+// reference's float16 X_DTYPE / LORA_DTYPE, lora_forward.py:141-143, 745-749).
+template <int TC, bool F16>
 __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
   constexpr bool LORA = TC > 0;
   extern __shared__ __align__(16) uint16_t lds[];
@@ -188,7 +191,7 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
     // keep the loads here, ahead of this stage's MFMAs
     __builtin_amdgcn_sched_barrier(0);
     const uint16_t* buf = lds + (st & 1) * GM_BM * GM_XS + ln * GM_XS + 32 * lg;
-    const Lut t0 = make_lut(code, ac0), t1 = make_lut(code, ac1);
+    const Lut t0 = make_lut<F16>(code, ac0), t1 = make_lut<F16>(code, ac1);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       uint4 a[GM_RT];
@@ -199,8 +202,8 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
       const uint4 b1 = decode8(word(wc1, s), t1);
 #pragma unroll
       for (int rt = 0; rt < GM_RT; ++rt) {
-        acc[rt][0] = mfma16x16x32(a[rt], b0, acc[rt][0]);
-        acc[rt][1] = mfma16x16x32(a[rt], b1, acc[rt][1]);
+        acc[rt][0] = mfma16x16x32_e<F16>(a[rt], b0, acc[rt][0]);
+        acc[rt][1] = mfma16x16x32_e<F16>(a[rt], b1, acc[rt][1]);
       }
     }
     if (LORA) {
@@ -213,8 +216,8 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
 #pragma unroll
         for (int tc = 0; tc < TC; ++tc) {
           const uint4 lb = deinterleave8(la4[tc][s]);
-          tacc[0][tc] = mfma16x16x32(a0, lb, tacc[0][tc]);
-          tacc[1][tc] = mfma16x16x32(a1, lb, tacc[1][tc]);
+          tacc[0][tc] = mfma16x16x32_e<F16>(a0, lb, tacc[0][tc]);
+          tacc[1][tc] = mfma16x16x32_e<F16>(a1, lb, tacc[1][tc]);
         }
       }
     }
@@ -268,7 +271,7 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
 #pragma unroll
         for (int q = 0; q < 4; ++q)
           ts[(32 * wave + 16 * i + 4 * lg + q) * GM_TS + 16 * tc + ln] =
-              tc < TC ? f2bf(tacc[i][tc < TC ? tc : 0][q]) : (uint16_t)0;
+              tc < TC ? f2e<F16>(tacc[i][tc < TC ? tc : 0][q]) : (uint16_t)0;
     // B rows: ranks 8 lg .. 8 lg + 7 of column n (ranks >= r zero)
     uint4 bv[2];
 #pragma unroll
@@ -292,16 +295,16 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
       const uint4 tv = *reinterpret_cast<const uint4*>(ts + (rt * 16 + ln) * GM_TS + 8 * lg);
 #pragma unroll
       for (int ct = 0; ct < 2; ++ct)
-        u[rt][ct] = mfma16x16x32(tv, bv[ct], f32x4_t{0.f, 0.f, 0.f, 0.f});
+        u[rt][ct] = mfma16x16x32_e<F16>(tv, bv[ct], f32x4_t{0.f, 0.f, 0.f, 0.f});
     }
   }
   float bias[2] = {0.f, 0.f};
   if (p.bias) {
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
-      bias[ct] = bf2f(p.bias[min(n0 + 32 * wave + 16 * ct + ln, p.N - 1)]);
+      bias[ct] = e2f<F16>(p.bias[min(n0 + 32 * wave + 16 * ct + ln, p.N - 1)]);
   }
-  const float sc = round_bf(p.scaling);
+  const float sc = round_e<F16>(p.scaling);
   // bf16 tile [128][GM_OS] in the x stage buffers (free after the loop's last barrier)
   uint16_t* os = lds;
 #pragma unroll
@@ -310,10 +313,10 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
     for (int ct = 0; ct < 2; ++ct)
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
-        float v = round_bf(acc[rt][ct][q]);
-        if (p.bias) v = round_bf(v + bias[ct]);
-        if (LORA) v = round_bf(v + round_bf(round_bf(u[rt][ct][q]) * sc));
-        os[(rt * 16 + 4 * lg + q) * GM_OS + 32 * wave + 16 * ct + ln] = f2bf(v);
+        float v = round_e<F16>(acc[rt][ct][q]);
+        if (p.bias) v = round_e<F16>(v + bias[ct]);
+        if (LORA) v = round_e<F16>(v + round_e<F16>(round_e<F16>(u[rt][ct][q]) * sc));
+        os[(rt * 16 + 4 * lg + q) * GM_OS + 32 * wave + 16 * ct + ln] = f2e<F16>(v);
       }
   __syncthreads();
 #pragma unroll
@@ -409,14 +412,6 @@ __global__ void __launch_bounds__(256) nf4_finish_rows(LinParts o, uint16_t* __r
 
 bool pow2(int v) { return v > 0 && (v & (v - 1)) == 0; }
 
-template <typename Kern>
-int allow_lds(Kern kernel) {
-  static const int rc = hip_check(
-      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)GM_LDS),
-      "hipFuncSetAttribute");
-  return rc;
-}
 
 bool gemm_ok(int M, int N, int K, int r, int blocksize) {
   return M >= 1 && N >= 1 && K >= 32 && K % 32 == 0 && r >= 0 && r <= GM_MAX_R &&
@@ -477,7 +472,7 @@ int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wr
                     const float* absmax, const float* code16, int blocksize,
                     const uint16_t* bias, const uint16_t* la, const uint16_t* lb, int r,
                     float scaling, uint16_t* y, int64_t ldy, int M, int N, int K,
-                    hipStream_t st, const GemmSplit* split) {
+                    hipStream_t st, const GemmSplit* split, bool f16) {
   if (M < 0 || N < 0 || K < 0 || r < 0 || wrow0 < 0) return einval("negative dimension");
   if (M == 0 || N == 0) return GRPO_OK;
   if (!gemm_ok(M, N, K, r, blocksize)) {
@@ -518,6 +513,7 @@ int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wr
   unsigned slices = 1;
   if (split && split->S > 1) {
     if (r > 16) return einval("a K-split NF4 GEMM takes r <= 16");
+    if (f16) return einval("a K-split NF4 GEMM is bf16 only");
     if (!split->part || (r > 0 && !split->tpart)) return einval("null partial-sum buffer");
     a.kst = split->kst;
     slices = (unsigned)split->S;
@@ -529,17 +525,23 @@ int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wr
     a.tsl = split->tsl;
   }
   const dim3 grid(8u * (unsigned)cdiv((int64_t)a.MT * a.NT, 8), slices);
-  if (r > 16) {
-    if (int rc = allow_lds(nf4_gemm_mfma<2>)) return rc;
-    nf4_gemm_mfma<2><<<grid, GM_T, GM_LDS, st>>>(a);
-  } else if (r > 0) {
-    if (int rc = allow_lds(nf4_gemm_mfma<1>)) return rc;
-    nf4_gemm_mfma<1><<<grid, GM_T, GM_LDS, st>>>(a);
+  const int tc = r > 16 ? 2 : (r > 0 ? 1 : 0);
+  int rc = GRPO_OK;
+  auto go = [&](auto tag) {
+    constexpr auto kern = decltype(tag)::value;
+    if (!(rc = allow_dynamic_lds<kern, (int)GM_LDS>())) kern<<<grid, GM_T, GM_LDS, st>>>(a);
+  };
+  using KernT = void (*)(GemmArgs);
+  if (f16) {
+    if (tc == 2) go(std::integral_constant<KernT, nf4_gemm_mfma<2, true>>{});
+    else if (tc == 1) go(std::integral_constant<KernT, nf4_gemm_mfma<1, true>>{});
+    else go(std::integral_constant<KernT, nf4_gemm_mfma<0, true>>{});
   } else {
-    if (int rc = allow_lds(nf4_gemm_mfma<0>)) return rc;
-    nf4_gemm_mfma<0><<<grid, GM_T, GM_LDS, st>>>(a);
+    if (tc == 2) go(std::integral_constant<KernT, nf4_gemm_mfma<2, false>>{});
+    else if (tc == 1) go(std::integral_constant<KernT, nf4_gemm_mfma<1, false>>{});
+    else go(std::integral_constant<KernT, nf4_gemm_mfma<0, false>>{});
   }
-  return launch_check("nf4_gemm_mfma");
+  return rc ? rc : launch_check("nf4_gemm_mfma");
 }
 
 int nf4_gemm_finish(const grpo_linear_parts_t* h, uint16_t* y, int64_t ldy, hipStream_t st) {
@@ -565,5 +567,18 @@ extern "C" int grpo_nf4_gemm(const void* x, int64_t ldx, const uint8_t* w, const
   return nf4_gemm_launch(static_cast<const uint16_t*>(x), ldx, w, 0, absmax, code16, blocksize,
                          static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(lora_a),
                          static_cast<const uint16_t*>(lora_b), r, scaling,
-                         static_cast<uint16_t*>(y), ldy, M, N, K, as_stream(stream), nullptr);
+                         static_cast<uint16_t*>(y), ldy, M, N, K, as_stream(stream), nullptr,
+                         false);
+}
+
+extern "C" int grpo_nf4_gemm_f16(const void* x, int64_t ldx, const uint8_t* w,
+                                 const float* absmax, const float* code16, int blocksize,
+                                 const void* bias, const void* lora_a, const void* lora_b, int r,
+                                 float scaling, void* y, int64_t ldy, int M, int N, int K,
+                                 grpo_stream_t stream) {
+  return nf4_gemm_launch(static_cast<const uint16_t*>(x), ldx, w, 0, absmax, code16, blocksize,
+                         static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(lora_a),
+                         static_cast<const uint16_t*>(lora_b), r, scaling,
+                         static_cast<uint16_t*>(y), ldy, M, N, K, as_stream(stream), nullptr,
+                         true);
 }

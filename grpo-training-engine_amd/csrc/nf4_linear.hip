@@ -57,6 +57,9 @@ int g_target_waves = GRPO_TARGET_WAVES;  // launch-shape target: 8 waves per CU 
 
 // ------------------------------------------------------------- dequant --
 
+// F16: float16_rne(code * absmax) instead of bf16 (the weight cast to a float16
+// grad / LoRA dtype in the reference's backward and forward).
+template <bool F16>
 __global__ void __launch_bounds__(256) nf4_dequant_vec(const uint2* __restrict__ w,
                                                        const float* __restrict__ absmax,
                                                        const float* __restrict__ code16,
@@ -75,13 +78,14 @@ __global__ void __launch_bounds__(256) nf4_dequant_vec(const uint2* __restrict__
       const uint32_t byte = ((j < 4 ? p.x : p.y) >> (8 * (j & 3))) & 0xFFu;
       const float hi = code[byte >> 4] * a;   // element 2j (even): high nibble
       const float lo = code[byte & 15u] * a;  // element 2j+1 (odd): low nibble
-      o[j] = pack_bf2(hi, lo);
+      o[j] = pack_e2<F16>(hi, lo);
     }
     out[2 * i] = make_uint4(o[0], o[1], o[2], o[3]);
     out[2 * i + 1] = make_uint4(o[4], o[5], o[6], o[7]);
   }
 }
 
+template <bool F16>
 __global__ void __launch_bounds__(256) nf4_dequant_scalar(const uint8_t* __restrict__ w,
                                                           const float* __restrict__ absmax,
                                                           const float* __restrict__ code16,
@@ -91,7 +95,7 @@ __global__ void __launch_bounds__(256) nf4_dequant_scalar(const uint8_t* __restr
   for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < numel; e += stride) {
     const uint32_t byte = w[e >> 1];
     const uint32_t q = (e & 1) ? (byte & 15u) : (byte >> 4);
-    out[e] = f2bf(code16[q] * absmax[e / blocksize]);
+    out[e] = f2e<F16>(code16[q] * absmax[e / blocksize]);
   }
 }
 
@@ -885,21 +889,12 @@ PartPlan plan_part(int M, int N, int K, int r, int nseg) {
 // share are fetched from HBM into one L2 only.
 constexpr int NUM_XCD = 8;
 
-// Lets an instantiation use more than 64 KiB of dynamic LDS (once per kernel).
-template <typename Kern>
-int allow_big_lds(Kern kernel) {
-  static const int rc = hip_check(
-      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, PART_LDS_BIG),
-      "hipFuncSetAttribute");
-  return rc;
-}
 
 template <int MT, int KPW, int XSRC, bool FIN = false>
 int launch_part_k(const PartArgs& a, const PartPlan& pl, const dim3& grid, const dim3& block,
                   hipStream_t st) {
   if (pl.lds > (size_t)PART_LDS_MAX)
-    if (int rc = allow_big_lds(nf4_part_mfma<MT, KPW, XSRC, FIN>)) return rc;
+    if (int rc = allow_dynamic_lds<nf4_part_mfma<MT, KPW, XSRC, FIN>, PART_LDS_BIG>()) return rc;
   nf4_part_mfma<MT, KPW, XSRC, FIN><<<grid, block, pl.lds, st>>>(a);
   return launch_check("nf4_part_mfma");
 }
@@ -2241,8 +2236,11 @@ extern "C" int grpo_nf4_absmax_expand(const uint8_t* absmax_q, const float* code
   return launch_check("nf4_absmax_expand");
 }
 
-extern "C" int grpo_nf4_dequant(const uint8_t* w, const float* absmax, const float* code16,
-                                void* out, int64_t numel, int blocksize, grpo_stream_t stream) {
+namespace {
+
+template <bool F16>
+int run_dequant(const uint8_t* w, const float* absmax, const float* code16, void* out,
+                int64_t numel, int blocksize, grpo_stream_t stream) {
   if (numel < 0) return einval("numel < 0");
   if (blocksize <= 0) return einval("blocksize must be > 0");
   if (numel == 0) return GRPO_OK;
@@ -2252,15 +2250,28 @@ extern "C" int grpo_nf4_dequant(const uint8_t* w, const float* absmax, const flo
       aligned16(out)) {
     const int64_t nvec = numel / 16;
     const int64_t blocks = std::min<int64_t>(cdiv(nvec, 256), 8192);
-    nf4_dequant_vec<<<dim3((unsigned)blocks), 256, 0, st>>>(
+    nf4_dequant_vec<F16><<<dim3((unsigned)blocks), 256, 0, st>>>(
         reinterpret_cast<const uint2*>(w), absmax, code16, reinterpret_cast<uint4*>(out), nvec,
         blocksize);
   } else {
     const int64_t blocks = std::min<int64_t>(cdiv(numel, 256), 8192);
-    nf4_dequant_scalar<<<dim3((unsigned)blocks), 256, 0, st>>>(
+    nf4_dequant_scalar<F16><<<dim3((unsigned)blocks), 256, 0, st>>>(
         w, absmax, code16, reinterpret_cast<uint16_t*>(out), numel, blocksize);
   }
   return launch_check("nf4_dequant");
+}
+
+}  // namespace
+
+extern "C" int grpo_nf4_dequant(const uint8_t* w, const float* absmax, const float* code16,
+                                void* out, int64_t numel, int blocksize, grpo_stream_t stream) {
+  return run_dequant<false>(w, absmax, code16, out, numel, blocksize, stream);
+}
+
+extern "C" int grpo_nf4_dequant_f16(const uint8_t* w, const float* absmax, const float* code16,
+                                    void* out, int64_t numel, int blocksize,
+                                    grpo_stream_t stream) {
+  return run_dequant<true>(w, absmax, code16, out, numel, blocksize, stream);
 }
 
 extern "C" int grpo_nf4_linear_plan(int M, int N, int K, int r, int nseg, int blocksize,
@@ -2678,7 +2689,7 @@ int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absma
     switch ((M + 15) / 16) {
 #define GUW_CASE(MT)                                                        \
   case MT:                                                                  \
-    if (int rc = allow_big_lds(nf4_gate_up_wide<MT>)) return rc;            \
+    if (int rc = allow_dynamic_lds<nf4_gate_up_wide<MT>, PART_LDS_BIG>()) return rc; \
     nf4_gate_up_wide<MT><<<grid, block, wlds, st>>>(a);                     \
     break;
       GUW_CASE(2) GUW_CASE(3) GUW_CASE(4)
@@ -2692,7 +2703,8 @@ int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absma
     const int G = units_shape(M, I, K).G;
     const size_t lds = units_lds(M, I, K);
     if (units2) {
-      if (int rc = allow_big_lds(nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, false, 2>)) return rc;
+      constexpr auto kern = nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, false, 2>;
+      if (int rc = allow_dynamic_lds<kern, PART_LDS_BIG>()) return rc;
       nf4_gate_up_units<GU_UNITS_W, GU_UNITS_IPW, false, 2>
           <<<dim3((unsigned)G), 64 * GU_UNITS_W, lds, st>>>(a);
       return launch_check("nf4_gate_up_units");

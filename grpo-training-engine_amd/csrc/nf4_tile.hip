@@ -470,19 +470,12 @@ TilePlan plan_tile(int M, int N, int K, int r, int nseg, int blocksize, bool nor
   return t;
 }
 
-template <typename Kern>
-int tile_allow_lds(Kern kernel) {
-  static const int rc = hip_check(
-      hipFuncSetAttribute(reinterpret_cast<const void*>(kernel),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, TILE_LDS_MAX),
-      "hipFuncSetAttribute");
-  return rc;
-}
 
 template <int MT, int KPW, int XS, int EPI, bool FOLD>
 int launch_tile_k(const TileArgs& a, const TilePlan& pl, hipStream_t st) {
+  constexpr auto kern = nf4_tile_mfma<MT, KPW, XS, EPI, FOLD>;
   if (pl.lds > 65536)
-    if (int rc = tile_allow_lds(nf4_tile_mfma<MT, KPW, XS, EPI, FOLD>)) return rc;
+    if (int rc = allow_dynamic_lds<kern, TILE_LDS_MAX>()) return rc;
   const int tc = FOLD ? 8 : 16;
   nf4_tile_mfma<MT, KPW, XS, EPI, FOLD>
       <<<dim3(a.N / tc), dim3(64 * (pl.WD + pl.WL)), pl.lds, st>>>(a);

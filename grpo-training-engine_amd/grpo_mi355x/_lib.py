@@ -73,6 +73,7 @@ SIGNATURES = {
     "grpo_init": (_I32, []),
     "grpo_last_error": (_c.c_char_p, []),
     "grpo_nf4_dequant": (_I32, [_VP, _VP, _VP, _VP, _I64, _I32, _VP]),
+    "grpo_nf4_dequant_f16": (_I32, [_VP, _VP, _VP, _VP, _I64, _I32, _VP]),
     "grpo_nf4_absmax_expand": (_I32, [_VP, _VP, _VP, _I32, _F32, _I64, _VP, _VP]),
     "grpo_nf4_grad_x": (_I32, [_VP, _I64, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _I64, _VP,
                                 _I64, _VP]),
@@ -91,6 +92,11 @@ SIGNATURES = {
     ),
     "grpo_nf4_gemm_supported": (_I32, [_I32, _I32, _I32, _I32, _I32]),
     "grpo_nf4_gemm": (
+        _I32,
+        [_VP, _I64, _VP, _VP, _VP, _I32, _VP, _VP, _VP, _I32, _F32, _VP, _I64, _I32, _I32, _I32,
+         _VP],
+    ),
+    "grpo_nf4_gemm_f16": (
         _I32,
         [_VP, _I64, _VP, _VP, _VP, _I32, _VP, _VP, _VP, _I32, _F32, _VP, _I64, _I32, _I32, _I32,
          _VP],

@@ -184,18 +184,22 @@ class Linear4bitNF4(nn.Module):
             qs.to(target)
         return self
 
-    def dequantize(self) -> torch.Tensor:
-        """bf16 ``[out_features, in_features]`` (bit-exact NF4 dequantization)."""
+    def dequantize(self, dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+        """``[out_features, in_features]`` in bf16 (or float16): bit-exact NF4
+        dequantization."""
         from ..kernels.ops import nf4_dequant
 
         qs = self.weight.quant_state
         n = self.out_features * self.in_features
-        w = nf4_dequant(self.weight.data.view(-1), float_absmax(qs), qs.code, n, qs.blocksize)
+        w = nf4_dequant(self.weight.data.view(-1), float_absmax(qs), qs.code, n, qs.blocksize,
+                        dtype=dtype)
         return w.view(self.out_features, self.in_features)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        w = self.dequantize()
-        bias = None if self.bias is None else self.bias.to(x.dtype)
+        # computes in x's dtype when that is float16 (bitsandbytes' Linear4bit
+        # returns the input's dtype), in bf16 otherwise
+        w = self.dequantize(torch.float16 if x.dtype == torch.float16 else torch.bfloat16)
+        bias = None if self.bias is None else self.bias.to(w.dtype)
         return F.linear(x.to(w.dtype), w, bias)
 
     def extra_repr(self) -> str:

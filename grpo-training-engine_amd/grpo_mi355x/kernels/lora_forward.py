@@ -15,7 +15,11 @@ Same call surface and dispatch as the reference's
 The fused forward is ``grpo_nf4_lora_linear``: the split-K kernel up to 64
 rows, the NF4 GEMM (weight decoded in the kernel, epilogue fused) beyond, and
 for the largest training batches (``fused_forward_rows``) the weight
-dequantized once (bit-exact) plus bf16 GEMMs with the same rounding points.  The backward (``:761-930``) keeps the
+dequantized once (bit-exact) plus bf16 GEMMs with the same rounding points.
+float16 x with float16 adapters (the reference's float16 X_DTYPE / LORA_DTYPE,
+``:141-143, 745-749``) runs the NF4 GEMM's float16 form at any M, every
+rounding point float16; mixed dtypes raise ``ValueError`` (the caller's torch
+branch then serves them, as for any shape the kernels do not take).  The backward (``:761-930``) keeps the
 reference's gradients and rounding points: grad_x's NF4 product on the fused
 ``grpo_nf4_grad_x`` kernel (LoRA part added in its store) below
 ``GRAD_X_GEMM_MIN_ROWS`` rows for the shapes it tiles, otherwise dequantize +
@@ -89,11 +93,17 @@ def _extract_quant_state(weight_4bit: torch.Tensor, quant_state):
     return absmax, code, int(quant_state.blocksize)
 
 
+def _scalar_as(v: float, dtype: torch.dtype) -> float:
+    """``v`` rounded to ``dtype`` (bf16 or float16), as a Python float:
+    ``t * _scalar_as(v, t.dtype)`` is dtype(float(t) * dtype(v)), the
+    reference's product with a 0-dim tensor of the LoRA dtype
+    (lora_forward.py:836-837), without a host-to-device copy."""
+    return float(torch.tensor(float(v), dtype=dtype))
+
+
 def _bf16_scalar(v: float) -> float:
-    """``v`` rounded to bf16, as a Python float: ``t * _bf16_scalar(v)`` on a bf16
-    tensor is bf16(float(t) * bf16(v)), the reference's product with a bf16
-    0-dim tensor (lora_forward.py:836-837), without a host-to-device copy."""
-    return float(torch.tensor(float(v), dtype=torch.bfloat16))
+    """``_scalar_as(v, torch.bfloat16)``."""
+    return _scalar_as(v, torch.bfloat16)
 
 
 # Rows of grad_out from which grad_x's NF4 product runs as dequantize + bf16
@@ -126,28 +136,30 @@ class FusedLoRAFunction(torch.autograd.Function):
         m, n, k, r = _validate_inputs(x, weight_4bit, quant_state, lora_A, lora_B)
         if r <= 0:
             raise ValueError(f"LoRA rank must be > 0, got {r}.")
-        if x.dtype != torch.bfloat16 or lora_A.dtype != torch.bfloat16:
-            raise ValueError("the HIP NF4+LoRA kernel computes in bfloat16; got "
-                             f"x {x.dtype}, lora {lora_A.dtype}.")
+        if lora_A.dtype != x.dtype:
+            raise ValueError("the HIP NF4+LoRA kernels take x and the adapters in one dtype "
+                             f"(bfloat16 or float16); got x {x.dtype}, lora {lora_A.dtype}.")
+        dt = x.dtype
         absmax, code, blocksize = _extract_quant_state(weight_4bit, quant_state)
         w = weight_4bit.contiguous().view(-1)
         if w.dtype != torch.uint8:
             w = w.view(torch.uint8)
         x_flat = x.contiguous().view(m, k)
         out = torch.empty((m, n), device=x.device, dtype=x.dtype)
-        fused = (ops.nf4_linear_plan(m, n, k, r, 1, blocksize) is not None
-                 or (m <= fused_forward_rows(k) and ops.nf4_gemm_supported(m, n, k, r, blocksize)))
+        gemm_ok = m <= fused_forward_rows(k) and ops.nf4_gemm_supported(m, n, k, r, blocksize)
+        fused = gemm_ok or (dt == torch.bfloat16
+                            and ops.nf4_linear_plan(m, n, k, r, 1, blocksize) is not None)
         if m > 0 and n > 0 and not fused:
-            # rows beyond the split-K kernel's (training batches): W dequantized
-            # once (bit-exact), then bf16 GEMMs with the kernel's rounding points
-            # (lora_forward.py:246-257): bf16(x W^T), + bias, t = bf16(x A^T),
-            # u = bf16(bf16(t B^T) * bf16(scaling)), y = bf16(acc + u)
-            wb = ops.nf4_dequant(w, absmax, code, n * k, blocksize).view(n, k)
+            # the largest batches: W dequantized once (bit-exact), then GEMMs
+            # with the kernel's rounding points (lora_forward.py:246-257):
+            # dt(x W^T), + bias, t = dt(x A^T), u = dt(dt(t B^T) * dt(scaling)),
+            # y = dt(acc + u), dt = bf16 or float16
+            wb = ops.nf4_dequant(w, absmax, code, n * k, blocksize, dtype=dt).view(n, k)
             acc = F.linear(x_flat, wb)
             if bias is not None:
                 acc = acc + bias.to(acc.dtype)
             u = F.linear(F.linear(x_flat, lora_A), lora_B)
-            out = torch.add(acc, u * _bf16_scalar(scaling))
+            out = torch.add(acc, u * _scalar_as(scaling, dt))
         elif m > 0 and n > 0:
             ops.nf4_lora_linear(x_flat, w, absmax, code, blocksize, n, bias=bias,
                                 lora_a=lora_A, lora_b=lora_B, scaling=float(scaling), out=out)
@@ -161,21 +173,24 @@ class FusedLoRAFunction(torch.autograd.Function):
         x_flat, lora_A, lora_B, w, absmax, code = ctx.saved_tensors
         m, k = x_flat.shape
         n = lora_B.shape[0]
+        dt = x_flat.dtype  # the adapters' dtype too (checked in forward)
         g = grad_out.contiguous().view(m, n)
-        if g.dtype != torch.bfloat16:
-            g = g.to(torch.bfloat16)
+        if g.dtype != dt:
+            g = g.to(dt)
         grad_bias = g.sum(dim=0) if ctx.has_bias else None  # lora_forward.py:790
-        # scaled_grad = bf16(g * bf16(scaling)) (:836-837); grad_intermediate,
-        # grad_x_lora, xA, grad_B, grad_A: bf16 GEMMs, float32 accumulation (:839-928)
-        sg = g * _bf16_scalar(ctx.scaling)
+        # scaled_grad = dt(g * dt(scaling)) (:836-837); grad_intermediate,
+        # grad_x_lora, xA, grad_B, grad_A: dt GEMMs, float32 accumulation (:839-928)
+        sg = g * _scalar_as(ctx.scaling, dt)
         gi = torch.matmul(sg, lora_B)
         gxl = torch.matmul(gi, lora_A)
-        if m >= GRAD_X_GEMM_MIN_ROWS or not ops.nf4_grad_x_supported(n, k, ctx.blocksize):
-            # many rows, or a shape the fused kernel does not tile (the
-            # reference's masked kernel takes any shape, :262-348): W
-            # dequantized once (bit-exact HIP kernel), then a plain bf16 GEMM
-            # -- the same rounding points as the fused kernel
-            wb = ops.nf4_dequant(w, absmax, code, n * k, ctx.blocksize).view(n, k)
+        if (dt != torch.bfloat16 or m >= GRAD_X_GEMM_MIN_ROWS
+                or not ops.nf4_grad_x_supported(n, k, ctx.blocksize)):
+            # float16, many rows, or a shape the fused bf16 kernel does not
+            # tile (the reference's masked kernel takes any shape, :262-348): W
+            # dequantized once to the gradient's dtype (bit-exact HIP kernel,
+            # the reference's cast of W to grad_block.dtype, :343), then a
+            # plain GEMM -- the same rounding points as the fused kernel
+            wb = ops.nf4_dequant(w, absmax, code, n * k, ctx.blocksize, dtype=dt).view(n, k)
             grad_x = torch.add(torch.matmul(g, wb), gxl)
         else:
             grad_x = ops.nf4_grad_x(g, w, absmax, code, ctx.blocksize, n, k, addend=gxl)

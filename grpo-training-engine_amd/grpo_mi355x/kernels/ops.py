@@ -79,8 +79,12 @@ def nf4_absmax_expand(absmax_q: torch.Tensor, code2: torch.Tensor, absmax2: torc
 
 
 def nf4_dequant(packed: torch.Tensor, absmax: torch.Tensor, code: torch.Tensor, numel: int,
-                blocksize: int, out: torch.Tensor | None = None) -> torch.Tensor:
-    """Bit-exact NF4 dequantization to a flat bf16 tensor of ``numel`` elements."""
+                blocksize: int, out: torch.Tensor | None = None,
+                dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """Bit-exact NF4 dequantization to a flat tensor of ``numel`` elements:
+    ``dtype(code[q] * absmax)``, bf16 or float16 (round to nearest even)."""
+    if dtype not in (torch.bfloat16, torch.float16):
+        raise ValueError(f"dequantization to bfloat16 or float16, got {dtype}.")
     lib = _lib.device_library()
     _need_cuda(packed, absmax, code)
     _need_dtype(packed, torch.uint8, "packed weight")
@@ -94,9 +98,12 @@ def nf4_dequant(packed: torch.Tensor, absmax: torch.Tensor, code: torch.Tensor, 
         raise ValueError("code must have 16 entries.")
     packed, absmax, code = packed.contiguous(), absmax.contiguous(), code.contiguous()
     if out is None:
-        out = torch.empty(numel, dtype=torch.bfloat16, device=packed.device)
-    rc = lib.grpo_nf4_dequant(packed.data_ptr(), absmax.data_ptr(), code.data_ptr(),
-                              out.data_ptr(), numel, blocksize, _lib.stream_handle(packed.device))
+        out = torch.empty(numel, dtype=dtype, device=packed.device)
+    elif out.dtype != dtype:
+        raise ValueError(f"out must be {dtype}.")
+    fn = lib.grpo_nf4_dequant_f16 if dtype == torch.float16 else lib.grpo_nf4_dequant
+    rc = fn(packed.data_ptr(), absmax.data_ptr(), code.data_ptr(), out.data_ptr(), numel,
+            blocksize, _lib.stream_handle(packed.device))
     _lib.check(rc, "grpo_nf4_dequant")
     return out
 
@@ -148,11 +155,16 @@ def nf4_lora_linear(x2d: torch.Tensor, packed: torch.Tensor, absmax: torch.Tenso
     packed once per tensor version); up to 64 rows split-K partial sums +
     finish (two launches); beyond, the NF4 GEMM (one launch, or K slices +
     finish when the tiles are few); one generic launch for other shapes.
+    float16 x (with float16 LoRA and bias) runs the NF4 GEMM's float16 form for
+    any M (``y`` float16).
     """
     lib = _lib.device_library()
     _need_cuda(x2d, packed, absmax, code, bias, lora_a, lora_b)
     if x2d.ndim != 2:
         raise ValueError(f"x must be 2-D [M, K], got {tuple(x2d.shape)}.")
+    if x2d.dtype == torch.float16:
+        return _nf4_lora_linear_f16(lib, x2d, packed, absmax, code, blocksize, n, bias, lora_a,
+                                    lora_b, scaling, out)
     _need_dtype(x2d, torch.bfloat16, "x")
     m, k = x2d.shape
     if x2d.stride(1) != 1:
@@ -326,6 +338,44 @@ def ctypes_byref(obj):
     import ctypes
 
     return ctypes.byref(obj)
+
+
+def _nf4_lora_linear_f16(lib, x2d, packed, absmax, code, blocksize, n, bias, lora_a, lora_b,
+                         scaling, out):
+    """float16 x and adapters: the NF4 GEMM's float16 form (``grpo_nf4_gemm_f16``,
+    every rounding point float16, any M)."""
+    m, k = x2d.shape
+    if x2d.stride(1) != 1 or x2d.stride(0) % 8 or x2d.data_ptr() % 16:
+        x2d = x2d.contiguous()
+    r = 0
+    if lora_a is not None:
+        r = lora_a.shape[0]
+        if lora_a.shape != (r, k) or lora_b is None or lora_b.shape != (n, r):
+            raise ValueError("lora_A must be [r, K] and lora_B [N, r].")
+        _need_dtype(lora_a, torch.float16, "lora_A")
+        _need_dtype(lora_b, torch.float16, "lora_B")
+        lora_a, lora_b = lora_a.contiguous(), lora_b.contiguous()
+    if bias is not None:
+        if bias.numel() != n:
+            raise ValueError(f"bias must have {n} elements.")
+        bias = bias.to(torch.float16).contiguous()
+    if packed.numel() * 2 < n * k:
+        raise ValueError("packed weight smaller than N*K/2 bytes.")
+    if not nf4_gemm_supported(m, n, k, r, blocksize):
+        raise ValueError(f"float16 NF4 linear: shape M={m} N={n} K={k} r={r} blocksize="
+                         f"{blocksize} is outside the NF4 GEMM (K % 32, r <= 32).")
+    if out is None:
+        out = torch.empty((m, n), dtype=torch.float16, device=x2d.device)
+    elif out.shape != (m, n) or out.stride(1) != 1 or out.dtype != torch.float16:
+        raise ValueError("out must be a float16 [M, N] tensor with unit column stride.")
+    if m == 0 or n == 0:
+        return out
+    rc = lib.grpo_nf4_gemm_f16(
+        x2d.data_ptr(), x2d.stride(0), packed.data_ptr(), absmax.data_ptr(), code.data_ptr(),
+        int(blocksize), _lib.ptr(bias), _lib.ptr(lora_a), _lib.ptr(lora_b), r, float(scaling),
+        out.data_ptr(), out.stride(0), m, n, k, _lib.stream_handle(x2d.device))
+    _lib.check(rc, "grpo_nf4_gemm_f16")
+    return out
 
 
 def nf4_gemm_supported(m: int, n: int, k: int, r: int, blocksize: int) -> bool:

@@ -64,6 +64,11 @@ int grpo_nf4_absmax_expand(const uint8_t* absmax_q, const float* code2, const fl
  */
 int grpo_nf4_dequant(const uint8_t* w, const float* absmax, const float* code16, void* out,
                      int64_t numel, int blocksize, grpo_stream_t stream);
+/* The same in float16: out[e] = float16_rne(code16[q_e] * absmax[e/blocksize]),
+ * the weight as the reference casts it for float16 gradients
+ * (_lora_grad_x_base_kernel, lora_forward.py:343). */
+int grpo_nf4_dequant_f16(const uint8_t* w, const float* absmax, const float* code16, void* out,
+                         int64_t numel, int blocksize, grpo_stream_t stream);
 
 /* Input gradient of the NF4 linear (training side of the fused NF4 + LoRA
  * linear): out[m, k] = bf16(sum_n grad[m, n] * W[n, k]) with W =
@@ -249,6 +254,14 @@ int grpo_nf4_gemm(const void* x, int64_t ldx, const uint8_t* w, const float* abs
                   const float* code16, int blocksize, const void* bias, const void* lora_a,
                   const void* lora_b, int r, float scaling, void* y, int64_t ldy, int M, int N,
                   int K, grpo_stream_t stream);
+/* grpo_nf4_gemm in float16: x, lora_a, lora_b, bias and y float16, the weight
+ * values float16_rne(code * absmax), every rounding point float16 -- the
+ * reference kernel with X_DTYPE = LORA_DTYPE = float16 (lora_forward.py:
+ * 141-143, 745-749).  Any M (no K split). */
+int grpo_nf4_gemm_f16(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                      const float* code16, int blocksize, const void* bias, const void* lora_a,
+                      const void* lora_b, int r, float scaling, void* y, int64_t ldy, int M, int N,
+                      int K, grpo_stream_t stream);
 
 /* Grouped form: the output rows are split into nseg (1..4) consecutive
  * segments of seg_rows[s] rows, stacked in ONE NF4 weight (w/absmax cover all

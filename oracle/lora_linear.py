@@ -1,7 +1,7 @@
 """NF4-dequant linear with the fused LoRA term -- test oracle.
 
 Restates ``_lora_forward_kernel`` (``src/triton_kernels/lora_forward.py:107-260``)
-with its rounding points:
+with its rounding points (bf16; float16 throughout with ``dtype="f16"``):
 
 1. ``acc = sum_k bf16(x[m,k]) * bf16(w[n,k])`` accumulated in float32
    (``:204-208``; here accumulated in float64, then rounded to float32);
@@ -21,7 +21,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .bf16 import bf16_bits_to_f32, f32_to_bf16_bits, round_bf16
+from .bf16 import bf16_bits_to_f32, f32_to_bf16_bits, from_bits, round_bf16, round_to, to_bits
 from .nf4 import NF4_CODE, dequantize_nf4
 
 
@@ -31,44 +31,49 @@ def _mm(a: np.ndarray, b: np.ndarray) -> np.ndarray:
 
 
 def nf4_weight_bf16(packed, absmax, n: int, k: int, blocksize: int,
-                    code: np.ndarray = NF4_CODE, nested: dict | None = None) -> np.ndarray:
-    """Dequantized weight ``[N, K]`` as float32 holding exact bf16 values."""
-    bits = dequantize_nf4(packed, absmax, n * k, blocksize, code, nested)
-    return bf16_bits_to_f32(bits).reshape(n, k)
+                    code: np.ndarray = NF4_CODE, nested: dict | None = None,
+                    dtype: str = "bf16") -> np.ndarray:
+    """Dequantized weight ``[N, K]`` as float32 holding exact bf16 values
+    (float16 values with ``dtype="f16"``)."""
+    bits = dequantize_nf4(packed, absmax, n * k, blocksize, code, nested, dtype)
+    return from_bits(bits, dtype).reshape(n, k)
 
 
 def nf4_lora_linear(x_bits, packed, absmax, n: int, k: int, blocksize: int,
                     bias_bits=None, a_bits=None, b_bits=None, scaling: float = 1.0,
                     code: np.ndarray = NF4_CODE, nested: dict | None = None,
-                    weight_f32: np.ndarray | None = None) -> np.ndarray:
+                    weight_f32: np.ndarray | None = None, dtype: str = "bf16") -> np.ndarray:
     """``y = W_nf4(x) + bias + B(A(x)) * scaling``; bf16 bits in, bf16 bits out.
 
     ``x_bits`` is ``[M, K]`` bf16 bits; ``a_bits`` ``[r, K]``; ``b_bits``
     ``[N, r]``.  ``a_bits=None`` (or r = 0) drops the LoRA term, which is the
     plain NF4 linear of the MLP projections.  ``weight_f32`` may pass a
     pre-dequantized weight (from ``nf4_weight_bf16``) to skip that step.
+    ``dtype="f16"``: every operand, the weight values and every rounding point
+    in float16 (the reference kernel with X_DTYPE = LORA_DTYPE = float16).
     """
-    x = bf16_bits_to_f32(np.asarray(x_bits)).reshape(-1, k)
+    rd = lambda v: round_to(v, dtype)
+    x = from_bits(np.asarray(x_bits), dtype).reshape(-1, k)
     w = weight_f32 if weight_f32 is not None else nf4_weight_bf16(
-        packed, absmax, n, k, blocksize, code, nested)
-    acc = round_bf16(_mm(x, w.T))
+        packed, absmax, n, k, blocksize, code, nested, dtype)
+    acc = rd(_mm(x, w.T))
     if bias_bits is not None:
-        acc = round_bf16(acc + bf16_bits_to_f32(bias_bits).reshape(1, n))
+        acc = rd(acc + from_bits(bias_bits, dtype).reshape(1, n))
     if a_bits is not None and np.asarray(a_bits).size > 0:
-        a = bf16_bits_to_f32(a_bits).reshape(-1, k)
-        b = bf16_bits_to_f32(b_bits).reshape(n, -1)
-        t = round_bf16(_mm(x, a.T))
-        u = round_bf16(_mm(t, b.T))
-        s = round_bf16(np.float32(scaling))
-        u = round_bf16(u * s)
-        acc = round_bf16(acc + u)
-    return f32_to_bf16_bits(acc)
+        a = from_bits(a_bits, dtype).reshape(-1, k)
+        b = from_bits(b_bits, dtype).reshape(n, -1)
+        t = rd(_mm(x, a.T))
+        u = rd(_mm(t, b.T))
+        s = rd(np.float32(scaling))
+        u = rd(u * s)
+        acc = rd(acc + u)
+    return to_bits(acc, dtype)
 
 
 def nf4_lora_backward(g_bits, x_bits, packed, absmax, n: int, k: int, blocksize: int,
                       a_bits, b_bits, scaling: float, has_bias: bool = False,
                       code: np.ndarray = NF4_CODE, nested: dict | None = None,
-                      exact: bool = False):
+                      exact: bool = False, dtype: str = "bf16"):
     """Gradients of ``nf4_lora_linear`` as ``FusedLoRAFunction.backward`` computes
     them (``src/triton_kernels/lora_forward.py:761-930``), each product
     accumulated in float64, rounded to float32, then to bf16 where the reference
@@ -86,20 +91,21 @@ def nf4_lora_backward(g_bits, x_bits, packed, absmax, n: int, k: int, blocksize:
     ``exact=True`` returns the same four products in float64 with no rounding
     at all (the linear map's true adjoint, used to pin the formulas).  Returns
     float arrays ``(grad_x [M, K], grad_A [r, K], grad_B [N, r], grad_bias or
-    None)``.
+    None)``.  ``dtype="f16"``: float16 inputs, weight values and roundings.
     """
-    g = bf16_bits_to_f32(np.asarray(g_bits)).reshape(-1, n).astype(np.float64)
-    x = bf16_bits_to_f32(np.asarray(x_bits)).reshape(-1, k).astype(np.float64)
-    w = nf4_weight_bf16(packed, absmax, n, k, blocksize, code, nested).astype(np.float64)
-    a = bf16_bits_to_f32(a_bits).reshape(-1, k).astype(np.float64)
-    b = bf16_bits_to_f32(b_bits).reshape(n, -1).astype(np.float64)
+    g = from_bits(np.asarray(g_bits), dtype).reshape(-1, n).astype(np.float64)
+    x = from_bits(np.asarray(x_bits), dtype).reshape(-1, k).astype(np.float64)
+    w = nf4_weight_bf16(packed, absmax, n, k, blocksize, code, nested,
+                        dtype).astype(np.float64)
+    a = from_bits(a_bits, dtype).reshape(-1, k).astype(np.float64)
+    b = from_bits(b_bits, dtype).reshape(n, -1).astype(np.float64)
     if exact:
         sg = g * float(scaling)
         gi = sg @ b
         return g @ w + gi @ a, gi.T @ x, sg.T @ (x @ a.T), (g.sum(0) if has_bias else None)
-    rb = lambda v: round_bf16(np.asarray(v).astype(np.float32))
+    rb = lambda v: round_to(np.asarray(v).astype(np.float32), dtype)
     base = rb(g @ w)
-    sg = rb(g * float(np.ravel(round_bf16(np.float32(scaling)))[0]))
+    sg = rb(g * float(np.ravel(round_to(np.float32(scaling), dtype))[0]))
     gi = rb(sg.astype(np.float64) @ b)
     gxl = rb(gi.astype(np.float64) @ a)
     grad_x = rb(base + gxl)

@@ -23,7 +23,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .bf16 import f32_to_bf16_bits
+from .bf16 import f32_to_bf16_bits, to_bits
 
 # The 16 NF4 levels published with QLoRA (Dettmers et al. 2023, appendix E),
 # identical to bitsandbytes' ``nf4`` map.  Pinned in tests against the closed
@@ -161,22 +161,25 @@ def quantize_absmax_nested(absmax, blocksize2: int = 256, code2=None):
 
 
 def dequantize_nf4(packed, absmax, numel: int, blocksize: int,
-                   code: np.ndarray = NF4_CODE, nested: dict | None = None) -> np.ndarray:
+                   code: np.ndarray = NF4_CODE, nested: dict | None = None,
+                   dtype: str = "bf16") -> np.ndarray:
     """Bit-exact NF4 dequantization; returns bfloat16 bit patterns (uint16).
 
     ``w = bf16_rne(float32(code[q]) * float32(a))`` per element
-    (``lora_forward.py:183-206``).
+    (``lora_forward.py:183-206``); ``dtype="f16"`` rounds to float16 instead
+    (the reference's cast to a float16 LoRA / gradient dtype, ``:206, 343``).
     """
     if nested is None and numel % blocksize == 0 and blocksize % 2 == 0:
-        return _dequantize_blocked(packed, absmax, numel, blocksize, code)
+        return _dequantize_blocked(packed, absmax, numel, blocksize, code, dtype)
     q = nibbles(packed, numel)
     c = np.asarray(code, dtype=np.float32)[q]
     a = block_scales(absmax, numel, blocksize, nested)
     w = (c * a).astype(np.float32)
-    return f32_to_bf16_bits(w)
+    return to_bits(w, dtype)
 
 
-def _dequantize_blocked(packed, absmax, numel: int, blocksize: int, code) -> np.ndarray:
+def _dequantize_blocked(packed, absmax, numel: int, blocksize: int, code,
+                        dtype: str = "bf16") -> np.ndarray:
     """Same values as the element-wise path, computed per whole block.
 
     A 256-entry table gives (code[hi], code[lo]) per byte; each block of
@@ -190,4 +193,4 @@ def _dequantize_blocked(packed, absmax, numel: int, blocksize: int, code) -> np.
     by = np.asarray(packed, dtype=np.uint8).reshape(-1)[: numel // 2].reshape(nblk, blocksize // 2)
     a = np.asarray(absmax, dtype=np.float32).reshape(-1)[:nblk]
     w = lut[by] * a[:, None, None]  # [nblk, bs/2, 2] float32
-    return f32_to_bf16_bits(w.reshape(-1))
+    return to_bits(w.reshape(-1), dtype)

@@ -135,3 +135,89 @@ def test_backward_linearity_identities():
         var = (x, a, b)[pick]
         rhs = float((grads[pick].astype(np.float64) * bf16_bits_to_f32(var)).sum())
         assert abs(lhs - rhs) <= 2e-2 * abs(lhs), (pick, lhs, rhs)
+
+
+# ---- float16 form (the reference kernel with X_DTYPE = LORA_DTYPE = float16)
+
+def _f16(t):
+    """float32 numpy -> torch float16 (torch's own rounding)."""
+    return torch.from_numpy(np.asarray(t, np.float32)).to(torch.float16)
+
+
+def test_dequant_f16_all_bytes_against_torch_rounding():
+    """float16(code[q] * absmax) per element: the oracle's float16 dequantization
+    equals torch's float32 product rounded by ``.to(torch.float16)`` for all
+    256 bytes at scales across float16's range (overflow to inf, subnormals)."""
+    from oracle.bf16 import f16_bits_to_f32
+    from oracle.nf4 import NF4_CODE, dequantize_nf4
+
+    packed = np.tile(np.arange(256, dtype=np.uint8), 8)
+    absmax = np.array([0.0, 1e-6, 3e-5, 7e4, 1.0, 0.5, 123.456, 7e-3] * 8, np.float32)
+    got = dequantize_nf4(packed, absmax, 4096, 64, dtype="f16")
+    q = np.stack([packed >> 4, packed & 15], axis=1).reshape(-1)
+    prod = torch.from_numpy(NF4_CODE[q]) * torch.from_numpy(np.repeat(absmax, 64))
+    want = prod.to(torch.float16).view(torch.int16).numpy().view(np.uint16)
+    assert np.array_equal(got, want)
+    assert np.isinf(f16_bits_to_f32(got)).any()  # the 7e4 block overflows float16
+
+
+def test_linear_f16_matches_torch_float16_ops():
+    """The float16 oracle against the same linear spelled with torch's float16
+    CPU ops (F.linear and elementwise ops each rounding to float16 -- an
+    independent implementation of the rounding points): >= 99 % of outputs
+    bit-identical, the rest one summation-order ulp away.  Rounding any step to
+    bf16 instead would move most outputs."""
+    from oracle.bf16 import f16_bits_to_f32, f32_to_f16_bits
+
+    g = rng(40)
+    for (m, n, k, r) in [(8, 256, 512, 16), (5, 96, 256, 8), (6, 64, 128, 0)]:
+        w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+        packed, absmax = quantize_nf4(w, 64)
+        x = f32_to_f16_bits(g.standard_normal((m, k)))
+        bias = f32_to_f16_bits(g.standard_normal(n) * 0.02)
+        a = f32_to_f16_bits(g.standard_normal((r, k)) * 0.01) if r else None
+        b = f32_to_f16_bits(g.standard_normal((n, r)) * 0.01) if r else None
+        got = nf4_lora_linear(x, packed, absmax, n, k, 64, bias_bits=bias, a_bits=a, b_bits=b,
+                              scaling=2.0, dtype="f16")
+        xt = _f16(f16_bits_to_f32(x))
+        wt = _f16(nf4_weight_bf16(packed, absmax, n, k, 64, dtype="f16"))
+        y = F.linear(xt, wt) + _f16(f16_bits_to_f32(bias))
+        if r:
+            t = F.linear(xt, _f16(f16_bits_to_f32(a)))
+            u = F.linear(t, _f16(f16_bits_to_f32(b))) * torch.tensor(2.0, dtype=torch.float16)
+            y = y + u
+        want = y.view(torch.int16).numpy().view(np.uint16)
+        assert np.mean(got == want) >= 0.99
+        assert rel_err(f16_bits_to_f32(got), f16_bits_to_f32(want)) <= 2e-3
+
+
+def test_backward_f16_matches_torch_float16_ops():
+    """The float16 backward oracle against torch's float16 CPU ops at the same
+    points (g @ W, g * s, @ B, @ A, x @ A^T, the weight gradients, Σ g):
+    within 2e-3 of the larger value, >= 95 % bit-identical per tensor."""
+    from oracle.bf16 import f16_bits_to_f32, f32_to_f16_bits
+    from oracle.lora_linear import nf4_lora_backward
+
+    g = rng(41)
+    m, n, k, r = 9, 96, 256, 16
+    w = (g.standard_normal((n, k)) * 0.02).astype(np.float32)
+    packed, absmax = quantize_nf4(w, 64)
+    x = f32_to_f16_bits(g.standard_normal((m, k)))
+    a = f32_to_f16_bits(g.standard_normal((r, k)) * 0.05)
+    b = f32_to_f16_bits(g.standard_normal((n, r)) * 0.2)
+    gr = f32_to_f16_bits(g.standard_normal((m, n)))
+    got = nf4_lora_backward(gr, x, packed, absmax, n, k, 64, a, b, 2.0, has_bias=True,
+                            dtype="f16")
+    gt, xt = _f16(f16_bits_to_f32(gr)), _f16(f16_bits_to_f32(x))
+    at, bt = _f16(f16_bits_to_f32(a)), _f16(f16_bits_to_f32(b))
+    wt = _f16(nf4_weight_bf16(packed, absmax, n, k, 64, dtype="f16"))
+    sg = gt * torch.tensor(2.0, dtype=torch.float16)
+    gi = sg @ bt
+    grad_x = gt @ wt + gi @ at
+    grad_a = gi.t() @ xt
+    grad_b = sg.t() @ (xt @ at.t())
+    grad_bias = gt.float().sum(0).half()
+    for mine, ref in zip(got, (grad_x, grad_a, grad_b, grad_bias)):
+        ref = ref.float().numpy()
+        assert rel_err(mine, ref) <= 2e-3
+        assert np.mean(np.float32(mine) == ref) >= 0.95
