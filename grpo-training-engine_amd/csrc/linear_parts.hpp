@@ -37,7 +37,8 @@ int make_parts(const grpo_linear_parts_t* h, LinParts* d);
 
 // Host: the NF4 GEMM (nf4_gemm.hip) for batches of more than 64 rows: y[M, N]
 // = the reference epilogue of x W^T with W rows wrow0 .. wrow0 + N - 1 of a
-// stacked NF4 weight, one bias / LoRA pair.  nf4_gemm_ok: the shapes it takes.
+// stacked NF4 weight, one bias / LoRA pair per output segment.  nf4_gemm_ok:
+// the shapes it takes (per segment).
 // With split (S > 1) the launch writes float32 partial sums over S K slices
 // of kst stages (part[s][m][n] at slice stride psl, row stride ldp; LoRA t
 // partials tpart[s][m][16] at slice stride tsl, r <= 16) for nf4_finish.
@@ -45,10 +46,19 @@ int make_parts(const grpo_linear_parts_t* h, LinParts* d);
 // bytes of the whole (grouped) linear in the LinParts layout.
 struct GemmSplit {
   int S, kst;
-  float* part;
+  float* part;    // column 0 of the whole linear
   int64_t ldp, psl;
-  float* tpart;
-  int64_t tsl;
+  float* tpart;   // segment s at tpart + s * tseg
+  int64_t tsl, tseg;
+};
+// The output segments of one launch (consecutive column ranges of a stacked
+// weight and of y, each with its own bias and LoRA pair).
+struct GemmSegs {
+  int nseg;
+  int seg_end[MAXSEG];
+  const uint16_t* bias[MAXSEG];
+  const uint16_t* la[MAXSEG];
+  const uint16_t* lb[MAXSEG];
 };
 struct GemmPlan {
   int S, kst;
@@ -60,9 +70,8 @@ GemmPlan nf4_gemm_plan(int M, int K, int r, int nseg, const int* seg_end);
 int nf4_gemm_finish(const grpo_linear_parts_t* h, uint16_t* y, int64_t ldy, hipStream_t st);
 int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wrow0,
                     const float* absmax, const float* code16, int blocksize,
-                    const uint16_t* bias, const uint16_t* la, const uint16_t* lb, int r,
-                    float scaling, uint16_t* y, int64_t ldy, int M, int N, int K,
-                    hipStream_t st, const GemmSplit* split, bool f16 = false);
+                    const GemmSegs& segs, int r, float scaling, uint16_t* y, int64_t ldy, int M,
+                    int K, hipStream_t st, const GemmSplit* split, bool f16 = false);
 
 // Segment of column n, branch-free: the segment ends are increasing (checked by
 // make_parts) and n < N = the last end.  (A loop over seg_end made the compiler

@@ -64,10 +64,17 @@ struct GemmArgs {
   const float* absmax;
   const float* code16;
   int bs_shift;
-  int64_t wrow0;         // weight row of output column 0 (a segment of a stacked weight)
-  const uint16_t* bias;  // [N] or null
-  const uint16_t* la;    // [r][K] (r > 0)
-  const uint16_t* lb;    // [N][r] (r > 0)
+  int64_t wrow0;         // weight row of output column 0 (of segment 0)
+  // Up to 4 segments: consecutive column ranges [seg_end[s-1], seg_end[s]) of
+  // one stacked weight and of y, each with its own bias and LoRA pair (the
+  // q|k|v projections of one launch); seg_tile[s] = first column tile of
+  // segment s (seg_tile[nseg..4] = NT).
+  int nseg;
+  int seg_end[MAXSEG];
+  int seg_tile[MAXSEG + 1];
+  const uint16_t* bias[MAXSEG];  // [N_s] or null
+  const uint16_t* la[MAXSEG];    // [r][K] (r > 0)
+  const uint16_t* lb[MAXSEG];    // [N_s][r] (r > 0)
   int r;
   float scaling;
   uint16_t* y;
@@ -84,8 +91,8 @@ struct GemmArgs {
   // the finish kernel.  part == null: one slice, epilogue in this kernel.
   float* part;
   int64_t ldp, psl;
-  float* tpart;
-  int64_t tsl;
+  float* tpart;  // segment s at tpart + s * tseg
+  int64_t tsl, tseg;
 };
 
 // TC: LoRA rank tiles of 16 (0: no LoRA, 1: r <= 16, 2: r <= 32).  F16: x,
@@ -106,7 +113,16 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
   const int t = ((run * T) >> 3) + (b >> 3);
   if (t >= (((run + 1) * T) >> 3)) return;  // past the end of this run
   const int nt = t / p.MT, mt = t - nt * p.MT;
-  const int m0 = mt * GM_BM, n0 = nt * GM_BN;
+  // the segment of column tile nt (uniform per workgroup) and its columns
+  const int seg = (nt >= p.seg_tile[1]) + (nt >= p.seg_tile[2]) + (nt >= p.seg_tile[3]);
+  const int c0 = seg > 0 ? sel4(p.seg_end[0], p.seg_end[1], p.seg_end[2], p.seg_end[3],
+                                seg - 1) : 0;
+  const int N = sel4(p.seg_end[0], p.seg_end[1], p.seg_end[2], p.seg_end[3], seg) - c0;
+  const uint16_t* const sbias = sel4(p.bias[0], p.bias[1], p.bias[2], p.bias[3], seg);
+  const uint16_t* const sla = sel4(p.la[0], p.la[1], p.la[2], p.la[3], seg);
+  const uint16_t* const slb = sel4(p.lb[0], p.lb[1], p.lb[2], p.lb[3], seg);
+  const int lt = nt - sel4(p.seg_tile[0], p.seg_tile[1], p.seg_tile[2], p.seg_tile[3], seg);
+  const int m0 = mt * GM_BM, n0 = lt * GM_BN;  // n0: column within the segment
 
   float code[16];
 #pragma unroll
@@ -122,8 +138,8 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
   int64_t we[2];
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
-    const int n = min(n0 + 32 * wave + 16 * ct + ln, p.N - 1);
-    we[ct] = (p.wrow0 + n) * p.K;
+    const int n = min(n0 + 32 * wave + 16 * ct + ln, N - 1);
+    we[ct] = (p.wrow0 + c0 + n) * p.K;
     wr[ct] = p.w + we[ct] / 2;
   }
   // LoRA A rows: rank 16 tc + ln of this lane.  Ranks >= r read rank r - 1:
@@ -131,7 +147,7 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
   // (no select, which the compiler turns into a predicated load).
   const uint16_t* ar[LORA ? TC : 1];
 #pragma unroll
-  for (int tc = 0; tc < TC; ++tc) ar[tc] = p.la + (int64_t)min(16 * tc + ln, p.r - 1) * p.K;
+  for (int tc = 0; tc < TC; ++tc) ar[tc] = sla + (int64_t)min(16 * tc + ln, p.r - 1) * p.K;
 
   uint4 xv[8];
   uint4 wv[2];
@@ -238,17 +254,17 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
         for (int q = 0; q < 4; ++q)
           ps[(rt * 16 + 4 * lg + q) * GM_PS + 32 * wave + 16 * ct + ln] = acc[rt][ct][q];
     __syncthreads();
-    float* pp = p.part + blockIdx.y * p.psl;
+    float* pp = p.part + blockIdx.y * p.psl + c0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int c = tid + GM_T * i, row = c >> 5, c4 = 4 * (c & 31);
       const int m = m0 + row, n = n0 + c4;
-      if (m < p.M && n < p.N)
+      if (m < p.M && n < N)
         *reinterpret_cast<float4*>(pp + (int64_t)m * p.ldp + n) =
             *reinterpret_cast<const float4*>(ps + row * GM_PS + c4);
     }
-    if (LORA && nt == 0) {
-      float* tp = p.tpart + blockIdx.y * p.tsl;
+    if (LORA && lt == 0) {
+      float* tp = p.tpart + blockIdx.y * p.tsl + seg * p.tseg;
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
@@ -276,8 +292,8 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
     uint4 bv[2];
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct) {
-      const int n = min(n0 + 32 * wave + 16 * ct + ln, p.N - 1);
-      const uint16_t* br = p.lb + (int64_t)n * p.r;
+      const int n = min(n0 + 32 * wave + 16 * ct + ln, N - 1);
+      const uint16_t* br = slb + (int64_t)n * p.r;
       if (p.lbvec) {
         bv[ct] = 8 * lg < p.r ? *reinterpret_cast<const uint4*>(br + 8 * lg)
                               : make_uint4(0, 0, 0, 0);
@@ -299,10 +315,10 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
     }
   }
   float bias[2] = {0.f, 0.f};
-  if (p.bias) {
+  if (sbias) {
 #pragma unroll
     for (int ct = 0; ct < 2; ++ct)
-      bias[ct] = e2f<F16>(p.bias[min(n0 + 32 * wave + 16 * ct + ln, p.N - 1)]);
+      bias[ct] = e2f<F16>(sbias[min(n0 + 32 * wave + 16 * ct + ln, N - 1)]);
   }
   const float sc = round_e<F16>(p.scaling);
   // bf16 tile [128][GM_OS] in the x stage buffers (free after the loop's last barrier)
@@ -314,7 +330,7 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         float v = round_e<F16>(acc[rt][ct][q]);
-        if (p.bias) v = round_e<F16>(v + bias[ct]);
+        if (sbias) v = round_e<F16>(v + bias[ct]);
         if (LORA) v = round_e<F16>(v + round_e<F16>(round_e<F16>(u[rt][ct][q]) * sc));
         os[(rt * 16 + 4 * lg + q) * GM_OS + 32 * wave + 16 * ct + ln] = f2e<F16>(v);
       }
@@ -322,14 +338,14 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int row = r0 + 16 * i, m = m0 + row, n = n0 + c8;
-    if (m >= p.M || n >= p.N) continue;
+    if (m >= p.M || n >= N) continue;
     const uint4 v = *reinterpret_cast<const uint4*>(os + row * GM_OS + c8);
-    uint16_t* dst = p.y + (int64_t)m * p.ldy + n;
+    uint16_t* dst = p.y + (int64_t)m * p.ldy + c0 + n;
     if (p.yvec) {
       *reinterpret_cast<uint4*>(dst) = v;
     } else {
       const uint32_t h[4] = {v.x, v.y, v.z, v.w};
-      for (int j = 0; j < 8 && n + j < p.N; ++j)
+      for (int j = 0; j < 8 && n + j < N; ++j)
         dst[j] = (uint16_t)(h[j >> 1] >> (16 * (j & 1)));
     }
   }
@@ -470,21 +486,26 @@ GemmPlan nf4_gemm_plan(int M, int K, int r, int nseg, const int* seg_end) {
 
 int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wrow0,
                     const float* absmax, const float* code16, int blocksize,
-                    const uint16_t* bias, const uint16_t* la, const uint16_t* lb, int r,
-                    float scaling, uint16_t* y, int64_t ldy, int M, int N, int K,
-                    hipStream_t st, const GemmSplit* split, bool f16) {
-  if (M < 0 || N < 0 || K < 0 || r < 0 || wrow0 < 0) return einval("negative dimension");
-  if (M == 0 || N == 0) return GRPO_OK;
-  if (!gemm_ok(M, N, K, r, blocksize)) {
-    set_error("shape not supported by the NF4 GEMM (K %% 32 == 0, r <= 32, power-of-two "
-              "blocksize >= 32)");
-    return GRPO_EUNSUPPORTED;
+                    const GemmSegs& sg, int r, float scaling, uint16_t* y, int64_t ldy, int M,
+                    int K, hipStream_t st, const GemmSplit* split, bool f16) {
+  if (M < 0 || K < 0 || r < 0 || wrow0 < 0) return einval("negative dimension");
+  if (sg.nseg < 1 || sg.nseg > MAXSEG) return einval("nseg must be in [1, 4]");
+  int NT = 0, prev = 0;
+  for (int s = 0; s < sg.nseg; ++s) {
+    if (sg.seg_end[s] <= prev) return einval("segment ends must increase");
+    if (!gemm_ok(M, sg.seg_end[s] - prev, K, r, blocksize)) {
+      set_error("shape not supported by the NF4 GEMM (K %% 32 == 0, r <= 32, power-of-two "
+                "blocksize >= 32)");
+      return GRPO_EUNSUPPORTED;
+    }
+    NT += (int)cdiv(sg.seg_end[s] - prev, GM_BN);
+    prev = sg.seg_end[s];
   }
+  const int N = prev;
+  if (M == 0) return GRPO_OK;
   if (!x || !w || !absmax || !code16 || !y) return einval("null pointer");
-  if (r > 0 && (!la || !lb)) return einval("r > 0 needs lora_a and lora_b");
   if (ldx < K || ldx % 8 != 0 || !aligned16(x)) return einval("x rows must be 16-byte aligned");
   if (!aligned16(w)) return einval("w must be 16-byte aligned");
-  if (r > 0 && !aligned16(la)) return einval("lora_a must be 16-byte aligned");
   if (ldy < N) return einval("ldy smaller than N");
   GemmArgs a{};
   a.x = x;
@@ -494,9 +515,26 @@ int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wr
   a.code16 = code16;
   a.bs_shift = __builtin_ctz((unsigned)blocksize);
   a.wrow0 = wrow0;
-  a.bias = bias;
-  a.la = la;
-  a.lb = lb;
+  a.nseg = sg.nseg;
+  a.yvec = aligned16(y) && ldy % 8 == 0;
+  a.lbvec = r > 0 && r % 8 == 0;
+  for (int s = 0, tile = 0; s < MAXSEG; ++s) {
+    const bool on = s < sg.nseg;
+    a.seg_end[s] = on ? sg.seg_end[s] : N;
+    a.seg_tile[s] = on ? tile : NT;
+    if (on) {
+      const int ns = sg.seg_end[s] - (s > 0 ? sg.seg_end[s - 1] : 0);
+      tile += (int)cdiv(ns, GM_BN);
+      a.bias[s] = sg.bias[s];
+      a.la[s] = r > 0 ? sg.la[s] : nullptr;
+      a.lb[s] = r > 0 ? sg.lb[s] : nullptr;
+      if (r > 0 && (!sg.la[s] || !sg.lb[s])) return einval("r > 0 needs lora_a and lora_b");
+      if (r > 0 && !aligned16(sg.la[s])) return einval("lora_a must be 16-byte aligned");
+      a.yvec = a.yvec && sg.seg_end[s] % 8 == 0;
+      a.lbvec = a.lbvec && aligned16(sg.lb[s]);
+    }
+  }
+  a.seg_tile[MAXSEG] = NT;
   a.r = r;
   a.scaling = scaling;
   a.y = y;
@@ -505,11 +543,9 @@ int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wr
   a.N = N;
   a.K = K;
   a.MT = (int)cdiv(M, GM_BM);
-  a.NT = (int)cdiv(N, GM_BN);
+  a.NT = NT;
   a.nst = (int)cdiv(K, GM_KS);
   a.kst = a.nst;
-  a.yvec = aligned16(y) && ldy % 8 == 0 && N % 8 == 0;
-  a.lbvec = r > 0 && aligned16(lb) && r % 8 == 0;
   unsigned slices = 1;
   if (split && split->S > 1) {
     if (r > 16) return einval("a K-split NF4 GEMM takes r <= 16");
@@ -523,6 +559,7 @@ int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wr
     a.psl = split->psl;
     a.tpart = split->tpart;
     a.tsl = split->tsl;
+    a.tseg = split->tseg;
   }
   const dim3 grid(8u * (unsigned)cdiv((int64_t)a.MT * a.NT, 8), slices);
   const int tc = r > 16 ? 2 : (r > 0 ? 1 : 0);
@@ -560,15 +597,33 @@ extern "C" int grpo_nf4_gemm_supported(int M, int N, int K, int r, int blocksize
   return gemm_ok(M, N, K, r, blocksize) ? 1 : 0;
 }
 
+namespace {
+
+int gemm_one(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
+             const float* code16, int blocksize, const void* bias, const void* lora_a,
+             const void* lora_b, int r, float scaling, void* y, int64_t ldy, int M, int N, int K,
+             grpo_stream_t stream, bool f16) {
+  if (N < 0) return einval("negative dimension");
+  if (N == 0) return GRPO_OK;
+  GemmSegs sg{};
+  sg.nseg = 1;
+  sg.seg_end[0] = N;
+  sg.bias[0] = static_cast<const uint16_t*>(bias);
+  sg.la[0] = static_cast<const uint16_t*>(lora_a);
+  sg.lb[0] = static_cast<const uint16_t*>(lora_b);
+  return nf4_gemm_launch(static_cast<const uint16_t*>(x), ldx, w, 0, absmax, code16, blocksize,
+                         sg, r, scaling, static_cast<uint16_t*>(y), ldy, M, K,
+                         as_stream(stream), nullptr, f16);
+}
+
+}  // namespace
+
 extern "C" int grpo_nf4_gemm(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
                              const float* code16, int blocksize, const void* bias,
                              const void* lora_a, const void* lora_b, int r, float scaling,
                              void* y, int64_t ldy, int M, int N, int K, grpo_stream_t stream) {
-  return nf4_gemm_launch(static_cast<const uint16_t*>(x), ldx, w, 0, absmax, code16, blocksize,
-                         static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(lora_a),
-                         static_cast<const uint16_t*>(lora_b), r, scaling,
-                         static_cast<uint16_t*>(y), ldy, M, N, K, as_stream(stream), nullptr,
-                         false);
+  return gemm_one(x, ldx, w, absmax, code16, blocksize, bias, lora_a, lora_b, r, scaling, y, ldy,
+                  M, N, K, stream, false);
 }
 
 extern "C" int grpo_nf4_gemm_f16(const void* x, int64_t ldx, const uint8_t* w,
@@ -576,9 +631,6 @@ extern "C" int grpo_nf4_gemm_f16(const void* x, int64_t ldx, const uint8_t* w,
                                  const void* bias, const void* lora_a, const void* lora_b, int r,
                                  float scaling, void* y, int64_t ldy, int M, int N, int K,
                                  grpo_stream_t stream) {
-  return nf4_gemm_launch(static_cast<const uint16_t*>(x), ldx, w, 0, absmax, code16, blocksize,
-                         static_cast<const uint16_t*>(bias), static_cast<const uint16_t*>(lora_a),
-                         static_cast<const uint16_t*>(lora_b), r, scaling,
-                         static_cast<uint16_t*>(y), ldy, M, N, K, as_stream(stream), nullptr,
-                         true);
+  return gemm_one(x, ldx, w, absmax, code16, blocksize, bias, lora_a, lora_b, r, scaling, y, ldy,
+                  M, N, K, stream, true);
 }

@@ -2078,7 +2078,7 @@ int run_linear(const GenArgs& g, void* workspace, size_t workspace_bytes, hipStr
       return rc;
     return run_finish(&h, g.y, g.ldy, st);
   }
-  // Wider batches: the NF4 GEMM, one launch per segment of the stacked weight.
+  // Wider batches: the NF4 GEMM, one launch for all segments of the stacked weight.
   bool gemm = g.ldx % 8 == 0 && aligned16(g.x) && aligned16(g.w);
   for (int s = 0, start = 0; gemm && s < g.nseg; start = g.seg_end[s], ++s)
     gemm = nf4_gemm_ok(g.M, g.seg_end[s] - start, g.K, g.r, g.blocksize) &&
@@ -2092,12 +2092,21 @@ int run_linear(const GenArgs& g, void* workspace, size_t workspace_bytes, hipStr
       pl.S = 1;
     GemmSplit sp{};
     grpo_linear_parts_t h{};
+    GemmSegs sg{};
+    sg.nseg = g.nseg;
+    for (int s = 0; s < g.nseg; ++s) {
+      sg.seg_end[s] = g.seg_end[s];
+      sg.bias[s] = g.bias[s];
+      sg.la[s] = g.la[s];
+      sg.lb[s] = g.lb[s];
+    }
     if (pl.S > 1) {
       sp.S = pl.S;
       sp.kst = pl.kst;
       sp.ldp = g.N;
       sp.psl = (int64_t)g.M * g.N;
       sp.tsl = (int64_t)g.nseg * g.M * 16;
+      sp.tseg = (int64_t)g.M * 16;
       h.part = static_cast<float*>(workspace);
       h.tpart = g.r > 0 ? reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) +
                                                    align256(pl.part_bytes))
@@ -2115,15 +2124,12 @@ int run_linear(const GenArgs& g, void* workspace, size_t workspace_bytes, hipStr
       }
       h.scaling = g.scaling;
     }
-    for (int s = 0, start = 0; s < g.nseg; start = g.seg_end[s], ++s) {
-      sp.part = h.part ? h.part + start : nullptr;
-      sp.tpart = h.tpart ? h.tpart + (int64_t)s * g.M * 16 : nullptr;
-      if (int rc = nf4_gemm_launch(g.x, g.ldx, g.w, start, g.absmax, g.code16, g.blocksize,
-                                   g.bias[s], g.la[s], g.lb[s], g.r, g.scaling, g.y + start,
-                                   g.ldy, g.M, g.seg_end[s] - start, g.K, st,
-                                   pl.S > 1 ? &sp : nullptr))
-        return rc;
-    }
+    sp.part = h.part;
+    sp.tpart = h.tpart;
+    // one launch for every segment
+    if (int rc = nf4_gemm_launch(g.x, g.ldx, g.w, 0, g.absmax, g.code16, g.blocksize, sg, g.r,
+                                 g.scaling, g.y, g.ldy, g.M, g.K, st, pl.S > 1 ? &sp : nullptr))
+      return rc;
     return pl.S > 1 ? nf4_gemm_finish(&h, g.y, g.ldy, st) : GRPO_OK;
   }
   const int64_t total = (int64_t)g.M * g.N;

@@ -117,7 +117,8 @@ def test_gemm_supported_query(dev):
 
 def test_grouped_qkv_wide_batch(dev):
     """grpo_nf4_lora_linear_grouped at 100 rows: q|k|v of one stacked weight,
-    each segment with its own bias and LoRA pair, one GEMM launch per segment."""
+    each segment with its own bias and LoRA pair, one GEMM launch for the three
+    segments (and K slices + one finish)."""
     _l = _lib()
     lib = _l.device_library()
     m, k, r, bs = 100, 1536, 16, 64
