@@ -66,6 +66,12 @@ struct GemmPlan {
 };
 bool nf4_gemm_ok(int M, int N, int K, int r, int blocksize);
 GemmPlan nf4_gemm_plan(int M, int K, int r, int nseg, const int* seg_end);
+// The MLP's gate|up projection + SiLU*up on the NF4 GEMM (more than 64 rows):
+// act[M, I] = bf16(bf16(silu(x Wg^T)) * bf16(x Wu^T)), W = [2I, K] stacked.
+bool nf4_gemm_silu_ok(int M, int I, int K, int blocksize);
+int nf4_gemm_silu_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                         const float* code16, int blocksize, int I, int K, int M, uint16_t* act,
+                         int64_t lda, hipStream_t st);
 // The finish of a K-split GEMM (16 rows per workgroup).
 int nf4_gemm_finish(const grpo_linear_parts_t* h, uint16_t* y, int64_t ldy, hipStream_t st);
 int nf4_gemm_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, int64_t wrow0,

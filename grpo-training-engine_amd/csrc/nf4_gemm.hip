@@ -93,14 +93,20 @@ struct GemmArgs {
   int64_t ldp, psl;
   float* tpart;  // segment s at tpart + s * tseg
   int64_t tsl, tseg;
+  int silu_I;    // SILU kernels: I (y = act [M, I], row stride ldy)
 };
 
 // TC: LoRA rank tiles of 16 (0: no LoRA, 1: r <= 16, 2: r <= 32).  F16: x,
 // the weight values, LoRA, bias and y in float16 instead of bf16 (the
 // reference's float16 X_DTYPE / LORA_DTYPE, lora_forward.py:141-143, 745-749).
-template <int TC, bool F16>
+// SILU: the MLP's gate|up projection of the stacked [2I, K] weight (no bias,
+// no LoRA) with act = bf16(bf16(silu(g)) * u) applied in the epilogue: the
+// tile's columns are 64 gate columns j0 .. j0 + 63 (waves 0, 1) and the same
+// 64 up columns (waves 2, 3), and y is act [M, I].
+template <int TC, bool F16, bool SILU = false>
 __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
   constexpr bool LORA = TC > 0;
+  static_assert(!SILU || (TC == 0 && !F16), "gate|up + SiLU: bf16, no LoRA");
   extern __shared__ __align__(16) uint16_t lds[];
   uint16_t* const ts = lds + 2 * GM_BM * GM_XS;  // t [128][GM_TS] bf16
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -139,7 +145,12 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
 #pragma unroll
   for (int ct = 0; ct < 2; ++ct) {
     const int n = min(n0 + 32 * wave + 16 * ct + ln, N - 1);
-    we[ct] = (p.wrow0 + c0 + n) * p.K;
+    if (SILU) {  // gate row j (waves 0, 1) or up row I + j (waves 2, 3)
+      const int j = min(lt * (GM_BN / 2) + 32 * (wave & 1) + 16 * ct + ln, p.silu_I - 1);
+      we[ct] = ((int64_t)(wave >> 1) * p.silu_I + j) * p.K;
+    } else {
+      we[ct] = (p.wrow0 + c0 + n) * p.K;
+    }
     wr[ct] = p.w + we[ct] / 2;
   }
   // LoRA A rows: rank 16 tc + ln of this lane.  Ranks >= r read rank r - 1:
@@ -335,6 +346,39 @@ __global__ void __launch_bounds__(GM_T, 2) nf4_gemm_mfma(GemmArgs p) {
         os[(rt * 16 + 4 * lg + q) * GM_OS + 32 * wave + 16 * ct + ln] = f2e<F16>(v);
       }
   __syncthreads();
+  if (SILU) {
+    // act columns j0 .. j0 + 63: thread (row r0 + 32 i, 8 columns 8 (tid % 8)),
+    // the gate values at tile columns 0..63, the up values at 64..127
+    const int j0 = lt * (GM_BN / 2), rs = tid >> 3, cc = 8 * (tid & 7);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = rs + 32 * i, m = m0 + row;
+      if (m >= p.M || j0 + cc >= p.silu_I) continue;
+      const uint4 gv = *reinterpret_cast<const uint4*>(os + row * GM_OS + cc);
+      const uint4 uv = *reinterpret_cast<const uint4*>(os + row * GM_OS + 64 + cc);
+      const uint32_t gw[4] = {gv.x, gv.y, gv.z, gv.w}, uw[4] = {uv.x, uv.y, uv.z, uv.w};
+      uint32_t o[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float r2[2];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const float g = h ? bf_hi(gw[q]) : bf_lo(gw[q]);
+          const float u = h ? bf_hi(uw[q]) : bf_lo(uw[q]);
+          r2[h] = round_bf(g * (1.f / (1.f + expf(-g)))) * u;  // as silu_mul_kernel
+        }
+        o[q] = pack_bf2(r2[0], r2[1]);
+      }
+      uint16_t* dst = p.y + (int64_t)m * p.ldy + j0 + cc;
+      if (p.yvec) {
+        *reinterpret_cast<uint4*>(dst) = make_uint4(o[0], o[1], o[2], o[3]);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) dst[j] = (uint16_t)(o[j >> 1] >> (16 * (j & 1)));
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const int row = r0 + 16 * i, m = m0 + row, n = n0 + c8;
@@ -589,6 +633,53 @@ int nf4_gemm_finish(const grpo_linear_parts_t* h, uint16_t* y, int64_t ldy, hipS
   nf4_finish_rows<<<dim3((unsigned)cdiv(o.N, FR_COLS), (unsigned)cdiv(o.M, FR_ROWS)), 256, 0,
                     st>>>(o, y, ldy);
   return launch_check("nf4_finish_rows");
+}
+
+bool nf4_gemm_silu_ok(int M, int I, int K, int blocksize) {
+  return I >= 8 && I % 8 == 0 && gemm_ok(M, 2 * I, K, 0, blocksize);
+}
+
+int nf4_gemm_silu_launch(const uint16_t* x, int64_t ldx, const uint8_t* w, const float* absmax,
+                         const float* code16, int blocksize, int I, int K, int M, uint16_t* act,
+                         int64_t lda, hipStream_t st) {
+  if (M < 0 || I < 0 || K < 0) return einval("negative dimension");
+  if (M == 0 || I == 0) return GRPO_OK;
+  if (!nf4_gemm_silu_ok(M, I, K, blocksize)) {
+    set_error("shape not supported by the NF4 GEMM's gate|up SiLU form (I %% 8 == 0, K %% 32 "
+              "== 0, power-of-two blocksize >= 32)");
+    return GRPO_EUNSUPPORTED;
+  }
+  if (!x || !w || !absmax || !code16 || !act) return einval("null pointer");
+  if (ldx < K || ldx % 8 != 0 || !aligned16(x)) return einval("x rows must be 16-byte aligned");
+  if (!aligned16(w)) return einval("w must be 16-byte aligned");
+  if (lda < I) return einval("lda smaller than I");
+  GemmArgs a{};
+  a.x = x;
+  a.ldx = ldx;
+  a.w = w;
+  a.absmax = absmax;
+  a.code16 = code16;
+  a.bs_shift = __builtin_ctz((unsigned)blocksize);
+  a.nseg = 1;
+  a.M = M;
+  a.K = K;
+  a.MT = (int)cdiv(M, GM_BM);
+  a.NT = (int)cdiv(I, GM_BN / 2);
+  for (int s = 0; s < MAXSEG; ++s) {
+    a.seg_end[s] = 2 * I;
+    a.seg_tile[s] = s == 0 ? 0 : a.NT;
+  }
+  a.seg_tile[MAXSEG] = a.NT;
+  a.y = act;
+  a.ldy = lda;
+  a.yvec = aligned16(act) && lda % 8 == 0;
+  a.nst = a.kst = (int)cdiv(K, GM_KS);
+  a.silu_I = I;
+  const dim3 grid(8u * (unsigned)cdiv((int64_t)a.MT * a.NT, 8));
+  constexpr auto kern = nf4_gemm_mfma<0, false, true>;
+  if (int rc = allow_dynamic_lds<kern, (int)GM_LDS>()) return rc;
+  kern<<<grid, GM_T, GM_LDS, st>>>(a);
+  return launch_check("nf4_gemm_mfma (gate|up SiLU)");
 }
 
 }  // namespace grpo

@@ -2508,7 +2508,8 @@ extern "C" int grpo_nf4_gate_up_silu_supported(int M, int I, int K, int blocksiz
   GuPlan pl;
   size_t lds;
   return plan_gu(M, I, K, blocksize, &pl) || units2_ok(M, I, K, blocksize) ||
-                 gu_wide_ok(M, I, K, blocksize, &lds)
+                 gu_wide_ok(M, I, K, blocksize, &lds) ||
+                 (M > 64 && nf4_gemm_silu_ok(M, I, K, blocksize))
              ? 1
              : 0;
 }
@@ -2653,6 +2654,10 @@ int run_gate_up(const void* x, int64_t ldx, const uint8_t* w, const float* absma
                 int act_tiles, hipStream_t st, const NormSource* nrm) {
   GuPlan pl;
   size_t wlds = 0;
+  // more than 64 rows (prefill chunks): the NF4 GEMM's gate|up SiLU form
+  if (M > 64 && !act_tiles && !nrm && nf4_gemm_silu_ok(M, I, K, blocksize))
+    return nf4_gemm_silu_launch(static_cast<const uint16_t*>(x), ldx, w, absmax, code16,
+                                blocksize, I, K, M, static_cast<uint16_t*>(act), lda, st);
   // 17..32 rows whose x and item tiles fit LDS run the units kernel on two row
   // tiles (x staged once, no chunk barriers; config 4's 32 x 8960 x 1536: 14.3
   // -> 13.2 us per traced launch, 6522 -> 6842 tok/s), the other wide shapes

@@ -1046,7 +1046,8 @@ class GemmPrefillEngine:
     layer's down_proj) -> q|k|v (grouped: one GEMM per projection, bias and
     LoRA in the kernel) -> RoPE + K/V append (``grpo_rope_append``) ->
     attention over p + i + 1 tokens (``grpo_paged_attn_decode``) -> o_proj ->
-    residual add + RMSNorm -> gate|up -> SiLU*up -> down_proj.  The reference
+    residual add + RMSNorm -> gate|up with SiLU*up in its epilogue
+    (``grpo_nf4_gate_up_silu``) -> down_proj.  The reference
     prefills with one transformers forward and a per-token scatter of K/V
     (``paged_kv.py:547-586``).  Only the cache is filled: the last layer stops
     after its append (its attention and MLP feed nothing that is kept).  The
@@ -1120,6 +1121,7 @@ class GemmPrefillEngine:
         self.ws_attn = ops.workspace("paged_attn_prefill", max(ops.paged_attention_workspace_bytes(
             B, self.Hq, self.Hkv, D, pool.block_size, max_blocks), 1), dev)
         self.embed = model.model.embed_tokens.weight
+        self.gu_fused = bool(self.lib.grpo_nf4_gate_up_silu_supported(B, self.I, H, self.bs))
         self.graph: Optional[torch.cuda.CUDAGraph] = None
 
     def launches(self) -> list:
@@ -1173,11 +1175,16 @@ class GemmPrefillEngine:
             out.append(("rmsnorm", lambda L=L: chk(lib.grpo_add_rmsnorm(
                 y, h, h, L["post_norm"].data_ptr(), x, B, H, L["eps"], st), "post_norm")))
             g = L["gu"]
-            out.append(("gate_up", lambda g=g: chk(lib.grpo_nf4_lora_linear(
-                x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), bs, None,
-                None, None, 0, 1.0, gu, 2 * I, B, 2 * I, H, ws, ws_n, st), "gate_up")))
-            out.append(("silu_mul", lambda: chk(lib.grpo_silu_mul(gu, 2 * I, I, act, I, B, st),
-                                                "silu_mul")))
+            if self.gu_fused:  # gate|up with SiLU*up in the GEMM's epilogue
+                out.append(("gate_up", lambda g=g: chk(lib.grpo_nf4_gate_up_silu(
+                    x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), bs, I, H,
+                    B, act, I, st), "gate_up")))
+            else:
+                out.append(("gate_up", lambda g=g: chk(lib.grpo_nf4_lora_linear(
+                    x, H, g.packed.data_ptr(), g.absmax.data_ptr(), g.code.data_ptr(), bs, None,
+                    None, None, 0, 1.0, gu, 2 * I, B, 2 * I, H, ws, ws_n, st), "gate_up")))
+                out.append(("silu_mul", lambda: chk(lib.grpo_silu_mul(
+                    gu, 2 * I, I, act, I, B, st), "silu_mul")))
             out.append(("down", lambda L=L: linear(
                 act, I, L["down_w"], L["down_absmax"], L["down_code"], None, None, None, 0, 1.0,
                 y, H, I)))

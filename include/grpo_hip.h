@@ -493,7 +493,10 @@ int grpo_nf4_linear_partials_silu(const grpo_linear_parts_t* gate_up, const uint
  *   17..32 rows whose x [M, K] and unit tiles fit 160 KiB of LDS: the unit
  *     kernel on two 16-row tiles;
  *   other 17..64-row shapes with I % 8 == 0 and at most 12 units per CU: x
- *     staged in 512-column chunks, unit accumulators in registers across K. */
+ *     staged in 512-column chunks, unit accumulators in registers across K;
+ *   more than 64 rows (prefill chunks): the NF4 GEMM with 64 gate and the
+ *     same 64 up columns per tile and SiLU*up in its epilogue (I % 8 == 0,
+ *     K % 32 == 0, power-of-two blocksize >= 32). */
 int grpo_nf4_gate_up_silu(const void* x, int64_t ldx, const uint8_t* w, const float* absmax,
                           const float* code16, int blocksize, int I, int K, int M, void* act,
                           int64_t lda, grpo_stream_t stream);

@@ -119,6 +119,16 @@ def test_gate_up_silu_matches_oracle(dev, m, i, k):
     _check_gate_up_silu(dev, m, i, k, 8)
 
 
+@pytest.mark.parametrize("m,i,k", [(65, 8960, 1536), (130, 256, 512), (512, 8960, 1536),
+                                   (200, 1000, 96)])
+def test_gate_up_silu_wide_batches_match_oracle(dev, m, i, k):
+    """More than 64 rows (prefill chunks): the NF4 GEMM with 64 gate and the
+    same 64 up columns per tile, SiLU*up in its epilogue; ragged row tiles
+    (65, 130, 200), I not a multiple of 64 (1000), K not a multiple of 128 (96)."""
+    _check_gate_up_silu(dev, m, i, k, 8)
+    _check_gate_up_silu(dev, m, i, k, 3)
+
+
 @pytest.mark.parametrize("m,i,k", [(40, 8960, 1536), (5, 4112, 512), (24, 8960, 1536)])
 def test_gate_up_silu_unaligned_act_rows(dev, m, i, k):
     """act rows of I + 3 columns: the wide kernel's epilogue then stores
@@ -177,7 +187,10 @@ def test_gate_up_silu_rejects_unsupported(dev):
     from grpo_mi355x import _lib
 
     lib = _lib.device_library()
-    assert lib.grpo_nf4_gate_up_silu_supported(65, 256, 512, 64) == 0  # M > 64
+    # more than 64 rows: the NF4 GEMM's form (I % 8, K % 32, blocksize >= 32)
+    assert lib.grpo_nf4_gate_up_silu_supported(65, 256, 512, 64) == 1
+    assert lib.grpo_nf4_gate_up_silu_supported(65, 250, 512, 64) == 0  # I % 8
+    assert lib.grpo_nf4_gate_up_silu_supported(65, 256, 500, 64) == 0  # K % 32
     assert lib.grpo_nf4_gate_up_silu_supported(8, 250, 512, 64) == 0   # I % 16
     assert lib.grpo_nf4_gate_up_silu_supported(32, 250, 512, 64) == 0  # I % 8
     assert lib.grpo_nf4_gate_up_silu_supported(8, 256, 500, 64) == 0   # K % 256
@@ -188,5 +201,7 @@ def test_gate_up_silu_rejects_unsupported(dev):
     # unit kernel (32 rows take it on two row tiles)
     assert lib.grpo_nf4_gate_up_silu_supported(40, 24584, 512, 64) == 0
     assert lib.grpo_nf4_gate_up_silu_supported(32, 24584, 512, 64) == 1
-    assert lib.grpo_nf4_gate_up_silu(None, 512, None, None, None, 64, 256, 512, 65, None, 256,
+    assert lib.grpo_nf4_gate_up_silu(None, 512, None, None, None, 64, 250, 512, 65, None, 256,
                                      None) == -2  # GRPO_EUNSUPPORTED
+    assert lib.grpo_nf4_gate_up_silu(None, 512, None, None, None, 64, 256, 512, 65, None, 256,
+                                     None) == -1  # a taken shape, null pointers: GRPO_EINVAL
