@@ -85,15 +85,21 @@ def kv_bytes_per_token(cfg) -> int:
     return 2 * cfg.num_key_value_heads * cfg.head_dim * 2 * cfg.num_hidden_layers
 
 
-def rollout_bytes(cfg, model, stops, prompt_len, group, block_size=16):
+def rollout_bytes(cfg, model, stops, prompt_len, group, block_size=16, lm_screen=False):
     """Algorithmic HBM bytes of one rollout (weights once per decode step + KV read).
 
     KV is counted per active row and step at its full context (logical bytes);
     the physical count reads the shared prompt blocks once per step instead of
-    once per row.
+    once per row.  With the screened lm_head (lm_screen) the head reads the
+    int8 copy (V * H bytes + 8 per vocabulary row) instead of the bf16 weight;
+    the candidate rows' bf16 bytes (a few KiB per row) are not counted.
     """
     wb = model.weight_bytes()
-    per_step_weights = wb["nf4"] + wb["absmax"] + wb["lora"] + wb["lm_head"]
+    head = wb["lm_head"]
+    if lm_screen:
+        V = cfg.vocab_size
+        head = head // 2 + 8 * V
+    per_step_weights = wb["nf4"] + wb["absmax"] + wb["lora"] + head
     kv_tok = kv_bytes_per_token(cfg)
     shared = ((prompt_len - 1) // block_size) * block_size  # tokens in shared full blocks
     steps = max(stops)
@@ -895,7 +901,7 @@ def main():
     tokens = sum(stops) * args.steps
     value = tokens / elapsed
     ms_rollout = elapsed / args.steps * 1e3
-    rb = rollout_bytes(cfg, model, stops, P, G, BS)
+    rb = rollout_bytes(cfg, model, stops, P, G, BS, lm_screen=eng.lm_screen)
     step_ms = ms_rollout / nsteps
     alg = rb["weights"] + rb["kv_logical"]
     log(f"{value:.1f} tok/s, {ms_rollout:.2f} ms/rollout, {step_ms * 1e3:.1f} us/decode step")
@@ -978,6 +984,7 @@ def main():
             "alg_bytes_per_rollout": alg,
             "kv_bytes_logical": rb["kv_logical"], "kv_bytes_physical": rb["kv_physical"],
             "weight_bytes_per_step": rb["weight_per_step"],
+            "lm_head": "int8 screen + bf16 candidate rows" if eng.lm_screen else "bf16",
             "achieved_GBs": round(alg / (elapsed / args.steps) / 1e9, 1),
             "frac_of_peak": round(alg / (elapsed / args.steps) / 1e9 / PEAK_HBM_GBS, 4),
         },

@@ -232,6 +232,17 @@ class DecodeEngine:
                      and bool(self.lib.grpo_nf4_linear_residual_supported(B, H, I, bs))
                      and bool(self.lib.grpo_nf4_gate_up_silu_tiles_norm_supported(B, I, H, bs)))
         self.ss = torch.zeros(B, max(H // 8, 1), dtype=torch.float32, device=dev)
+        # greedy steps of <= 8 rows: the screened lm_head (int8 bounds, the
+        # candidate tiles recomputed in bf16; the same token, half the bytes)
+        self.lm_screen = (self.LM_SCREEN and self.lm_tiled and self.fold and not self.sampling
+                          and not self.keep_logits and B <= 8 and self.V <= 262144)
+        self.lm_q8 = self.ws_scr = None
+        if self.lm_screen:
+            self.lm_q8 = self._lm_q8(self.model, self.lm_head, dev)
+            # its hand-over counters start zero and every call leaves them so
+            self.ws_scr = torch.zeros(
+                int(self.lib.grpo_lm_head_screen_workspace_bytes(B, self.V)), dtype=torch.uint8,
+                device=dev)
         # the post-attention norm's statistic: per-64-column sums of squares of
         # h from grpo_linear_finish_residual (or from the o_proj kernels below)
         self.ss_post = torch.zeros(B, max(H // 64, 1), dtype=torch.float32, device=dev)
@@ -393,6 +404,10 @@ class DecodeEngine:
     O_FIN = True
     # lm_head weight read in the kernel's tile order
     LM_TILES = True
+    # greedy lm_head screened by int8 bounds (grpo_lm_head_screen_norm +
+    # grpo_lm_head_exact_advance_norm): bit-identical tokens from half the
+    # weight bytes (config 3: lm_head + advance 80 -> 60 us per step)
+    LM_SCREEN = True
 
     @staticmethod
     def _lm_tiles(model, w: torch.Tensor, dev) -> torch.Tensor:
@@ -411,6 +426,26 @@ class DecodeEngine:
                                                   _lib.stream_handle(dev)), "lm_weight_tiles")
         model._grpo_lm_tiles = (key, wt)
         return wt
+
+    @staticmethod
+    def _lm_q8(model, w: torch.Tensor, dev):
+        """The int8 copy of the lm_head weight for the screened argmax
+        (grpo_lm_head_q8_tiles: V * H bytes + two float32 per vocabulary row),
+        built once per model and weight version and kept on the model like the
+        tile-order copy (0.23 GB at Qwen2-1.5B) until release_decode_caches."""
+        key = (w.data_ptr(), w._version, tuple(w.shape))
+        cache = getattr(model, "_grpo_lm_q8", None)
+        if cache is not None and cache[0] == key:
+            return cache[1]
+        lib = _lib.device_library()
+        V, K = w.shape
+        wq = torch.empty(V * K, dtype=torch.uint8, device=dev)
+        scale = torch.empty(V, dtype=torch.float32, device=dev)
+        rnorm = torch.empty(V, dtype=torch.float32, device=dev)
+        _lib.check(lib.grpo_lm_head_q8_tiles(w.data_ptr(), V, K, wq.data_ptr(), scale.data_ptr(),
+                                              rnorm.data_ptr(), _lib.stream_handle(dev)), "lm_q8")
+        model._grpo_lm_q8 = (key, (wq, scale, rnorm))
+        return model._grpo_lm_q8[1]
 
     def launches(self) -> list:
         """[(kind, launch())] of one forward pass, in order, bound to torch's
@@ -613,6 +648,8 @@ class DecodeEngine:
         h, x = self.h.data_ptr(), self.x.data_ptr()
         if self.fold and self.lm_fused:
             # the lm_head kernel stages the final norm from h and down_proj's sums
+            if self.lm_screen:
+                return self._head_launches_screen(st)
             return self._head_launches_norm(st)
         if self.fold:  # h is finished: the final norm reads it alone
             out = [("rmsnorm", lambda: chk(lib.grpo_add_rmsnorm(
@@ -690,6 +727,29 @@ class DecodeEngine:
                 None if gen is None else gen.data_ptr(), 0 if gen is None else gen.shape[1],
                 self.append_pos.data_ptr(), self.attn_len.data_ptr(), st), "advance")))
         return out
+
+    def _head_launches_screen(self, st) -> list:
+        """The greedy head from the int8 screen: bounds of every logit, then the
+        exact bf16 logits of the candidate tiles' candidate rows, the first
+        index of the maximum and the row advance (the final norm staged by both
+        launches from h and the last down_proj's sums of squares)."""
+        lib, chk, B, H = self.lib, _lib.check, self.B, self.H
+        h, ss = self.h.data_ptr(), self.ss.data_ptr()
+        wq, scale, rnorm = self.lm_q8
+        ws, gen = self.ws_scr, self.generated
+        return [
+            ("lm_head", lambda: chk(lib.grpo_lm_head_screen_norm(
+                h, H, ss, H // 8, self.final_norm.data_ptr(), self.final_eps, wq.data_ptr(),
+                scale.data_ptr(), rnorm.data_ptr(), self.V, H, B, ws.data_ptr(), ws.numel(), st),
+                "lm_screen")),
+            ("advance", lambda: chk(lib.grpo_lm_head_exact_advance_norm(
+                h, H, ss, H // 8, self.final_norm.data_ptr(), self.final_eps,
+                self.lm_w.data_ptr(), self.V, H, B, ws.data_ptr(), self.xcd_err.data_ptr(),
+                self.next.data_ptr(), self.tokens.data_ptr(), self.pos.data_ptr(),
+                self.count.data_ptr(), self.limit.data_ptr(), self.active.data_ptr(),
+                self.eos.data_ptr(), None if gen is None else gen.data_ptr(),
+                0 if gen is None else gen.shape[1], self.append_pos.data_ptr(),
+                self.attn_len.data_ptr(), st), "lm_exact_advance"))]
 
     def nf4_launches(self) -> list:
         """[(kind, algorithmic bytes, launch())] of every NF4 linear of one step."""
@@ -793,12 +853,15 @@ class DecodeEngine:
         hand-overs off (``ATTN_MERGE``, ``O_FIN``) for engines built later, which
         then take the launches that need no hand-over."""
         bad = int(self.xcd_err.item()) != 0
-        for cnt in (self.m_cnt, getattr(self, "o_cnt", None) if self.o_fin else None):
+        ws_scr = getattr(self, "ws_scr", None)  # the screened lm_head's counters
+        lm_cnt = ws_scr[:1024] if ws_scr is not None else None
+        for cnt in (self.m_cnt, getattr(self, "o_cnt", None) if self.o_fin else None, lm_cnt):
             if cnt is not None and bool((cnt != 0).any()):
                 bad = True
         if bad:
             DecodeEngine.ATTN_MERGE = False
             DecodeEngine.O_FIN = False
+            DecodeEngine.LM_SCREEN = False
             raise RuntimeError("decode step: a group of workgroups that hands data over "
                                "through L2 did not run on one XCD; the results of this run "
                                "are not valid (in-kernel hand-overs now off; run again)")
@@ -1243,8 +1306,9 @@ def release_decode_caches(model=None) -> None:
 
     models = [] if model is None else [model, adapt._cache.get(model)]
     for m in models:
-        if m is not None and hasattr(m, "_grpo_lm_tiles"):
-            del m._grpo_lm_tiles
+        for attr in ("_grpo_lm_tiles", "_grpo_lm_q8"):
+            if m is not None and hasattr(m, attr):
+                delattr(m, attr)
     ops._packed_a.clear()
 
 

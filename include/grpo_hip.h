@@ -702,6 +702,69 @@ int grpo_decode_advance(const void* lm_workspace, int M, int V, int64_t* next_to
                         uint8_t* active, const int64_t* eos, int64_t* generated, int64_t gen_ld,
                         int32_t* append_pos, int32_t* attn_len, grpo_stream_t stream);
 
+/* Screened greedy lm_head: the token of grpo_lm_head_argmax[_norm] +
+ * grpo_decode_advance (the first index of the largest bf16 logit, bit for
+ * bit), reading an int8 copy of W to bound every logit and the bf16 tiles
+ * only where the maximum can be.  No reference counterpart as a separate
+ * step: the reference computes every logit (paged_kv.py:800-806) and takes the
+ * argmax (:444-445); this gives the same token from fewer bytes.
+ *
+ * grpo_lm_head_q8_tiles: per vocabulary row v, scale[v] = max_k |W[v, k]| / 127
+ * (float32), q = rint(W / scale) in [-127, 127] stored as q + 128 in wq_tiles
+ * (V * K bytes, 16-byte aligned) in the order of the screening kernel's loads,
+ * rnorm[v] = ||W[v, :] - scale[v] q[v, :]||_2 rounded up.  Once per weight.
+ * V % 16 == 0, K % 256 == 0.  A row with a non-finite weight gets scale NaN
+ * (its tiles are then always recomputed). */
+int grpo_lm_head_q8_tiles(const void* w, int V, int K, void* wq_tiles, float* scale, float* rnorm,
+                          grpo_stream_t stream);
+
+/* Workspace of the screen and the exact pass: int32 arrival counters [8][32]
+ * (ZERO before the first exact pass, left zero by each), the exact pass's
+ * per-workgroup bests (float [8][15], int32 [8][15]), then from byte offset
+ * 2048 the screen's bounds: float [M][V / 16] (per row and 16-row tile, an
+ * upper bound of the tile's float32 logits), float [M][W] (per row and
+ * screening workgroup, W = min(V / 16, 256), a lower bound of the largest
+ * logit among its tiles) and float [M][V] (per row and vocabulary row, an
+ * upper bound of that logit). */
+size_t grpo_lm_head_screen_workspace_bytes(int M, int V);
+
+/* The screen: for x [M, K] (M <= 8; the _norm form stages x = RMSNorm(h) as
+ * grpo_lm_head_argmax_norm does), bounds |logit - estimate| <= e from the int8
+ * weight (Cauchy-Schwarz on the weight's rounding, the float16 rounding of x,
+ * and the float32 summation error of both passes) and writes the bounds to the
+ * workspace. */
+int grpo_lm_head_screen(const void* x, int64_t ldx, const void* wq_tiles, const float* scale,
+                        const float* rnorm, int V, int K, int M, void* workspace,
+                        size_t workspace_bytes, grpo_stream_t stream);
+int grpo_lm_head_screen_norm(const void* h, int64_t ldh, const float* sumsq, int groups,
+                             const void* norm_weight, float eps, const void* wq_tiles,
+                             const float* scale, const float* rnorm, int V, int K, int M,
+                             void* workspace, size_t workspace_bytes, grpo_stream_t stream);
+
+/* The exact pass after the screen (same x, M, V, K, workspace): per row, 15
+ * workgroups on one XCD recompute, with grpo_lm_head_argmax_tiles' arithmetic
+ * on the same operands, every 16-row tile of w_tiles
+ * (grpo_lm_head_weight_tiles layout) whose upper bound reaches the row's
+ * threshold (the largest lower bound, less the width of a bf16 rounding
+ * interval); the last of them to arrive (an L2 counter in the workspace)
+ * writes the first index of the largest bf16 logit to next_tokens.  As in
+ * grpo_paged_attn_decode_qkv_merged, *xcd_err (may be NULL) becomes 1 if a
+ * row's workgroups ran on two XCDs (that call's tokens are then not valid; a
+ * counter is left non-zero).  The _advance_norm form stages x = RMSNorm(h) and
+ * then does grpo_decode_advance's bookkeeping (next_tokens may be NULL
+ * there); a row that is not active keeps its token and computes nothing.
+ * Calls sharing a workspace must not overlap. */
+int grpo_lm_head_exact_argmax(const void* x, int64_t ldx, const void* w_tiles, int V, int K, int M,
+                              void* screen_workspace, int* xcd_err, int64_t* next_tokens,
+                              grpo_stream_t stream);
+int grpo_lm_head_exact_advance_norm(const void* h, int64_t ldh, const float* sumsq, int groups,
+                                    const void* norm_weight, float eps, const void* w_tiles, int V,
+                                    int K, int M, void* screen_workspace, int* xcd_err,
+                                    int64_t* next_tokens, int64_t* tokens, int32_t* pos,
+                                    int32_t* count, const int32_t* limit, uint8_t* active,
+                                    const int64_t* eos, int64_t* generated, int64_t gen_ld,
+                                    int32_t* append_pos, int32_t* attn_len, grpo_stream_t stream);
+
 /* out[m] = first index of the maximum of logits[m, :V] (bf16, row stride ld);
  * greedy sampling of _sample_tokens / fused_logits_sampling (paged_kv.py:444-445,
  * fused_ops.py:232-234). */

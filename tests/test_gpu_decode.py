@@ -343,12 +343,48 @@ def test_release_decode_caches_frees_the_lm_head_copy(dev):
     pool = PagedKVPool(1, 16, 2, 128, 16, device=dev)
     eng = DecodeEngine(model, pool, 4, 4)
     assert eng.lm_tiled and hasattr(model, "_grpo_lm_tiles")
+    assert eng.lm_screen and hasattr(model, "_grpo_lm_q8")
     first = eng.lm_w.clone()
     ops.packed_lora_a(model.model.layers[0].self_attn.o_proj.lora_A.weight)
     assert len(ops._packed_a) > 0
     del eng
     release_decode_caches(model)
     assert not hasattr(model, "_grpo_lm_tiles") and len(ops._packed_a) == 0
+    assert not hasattr(model, "_grpo_lm_q8")
     eng = DecodeEngine(model, pool, 4, 4)
     torch.cuda.synchronize()
     assert torch.equal(eng.lm_w.view(torch.int16), first.view(torch.int16))
+
+
+def test_screened_head_gives_the_tokens_of_the_full_head(dev, monkeypatch):
+    """The greedy decode step with the screened lm_head (int8 bounds, exact bf16
+    logits of the candidate rows; LM_SCREEN) generates exactly the tokens of
+    the step with the full bf16 lm_head, over graph-replayed rollouts with rows
+    that stop at different lengths, and leaves its hand-over counters zero."""
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine
+
+    model = _model(dev, layers=2)
+    B, bs, width, new = 8, 16, 8, 40
+    outs = []
+    for screen in (True, False):
+        monkeypatch.setattr(DecodeEngine, "LM_SCREEN", screen)
+        pool = PagedKVPool(2, B * width, 2, 128, bs, device=dev)
+        sids = [pool.allocate(width * bs) for _ in range(B)]
+        eng = DecodeEngine(model, pool, B, width)
+        assert eng.lm_screen == screen
+        g = torch.Generator().manual_seed(7)
+        tok = torch.randint(0, 1000, (B,), generator=g).to(dev)
+        limits = torch.tensor([40, 3, 17, 40, 1, 29, 40, 8], device=dev)
+        eng.start(tok, torch.zeros(B, device=dev), pool.block_table(sids, width, device=dev),
+                  limits, new)
+        eng.capture()
+        for _ in range(2):  # two rollouts of graph replays (16-step graphs, then single steps)
+            eng.start(tok, torch.zeros(B, device=dev), pool.block_table(sids, width, device=dev),
+                      limits, new)
+            eng.run(new)
+        torch.cuda.synchronize()
+        eng.verify_handover()
+        outs.append(eng.generated.clone())
+    print("generated (screened):", outs[0][:, :8].tolist(), flush=True)
+    assert torch.equal(outs[0], outs[1])

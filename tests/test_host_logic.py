@@ -344,34 +344,44 @@ def test_fork_into_a_nearly_full_pool_changes_nothing():
 def test_verify_handover_raises_and_switches_the_hand_overs_off():
     """DecodeEngine.verify_handover: a set XCD check word, or a hand-over
     counter left non-zero, raises RuntimeError and turns the in-kernel
-    hand-overs (attention merge, o_proj finish) off for engines built later;
-    clear words and counters pass."""
+    hand-overs (attention merge, o_proj finish, the screened lm_head's exact
+    pass) off for engines built later; clear words and counters pass."""
     from types import SimpleNamespace
 
     from grpo_mi355x.rollout.decode import DecodeEngine
 
-    saved = (DecodeEngine.ATTN_MERGE, DecodeEngine.O_FIN)
+    saved = (DecodeEngine.ATTN_MERGE, DecodeEngine.O_FIN, DecodeEngine.LM_SCREEN)
 
-    def stand(err=0, mcnt=None, ocnt=None, o_fin=False):
+    def stand(err=0, mcnt=None, ocnt=None, o_fin=False, lmcnt=None):
+        ws = None
+        if lmcnt is not None:  # the screened lm_head's workspace: counters in its first 1 KiB
+            ws = torch.zeros(4096, dtype=torch.uint8)
+            ws[:1024].view(torch.int32)[: len(lmcnt)] = torch.tensor(lmcnt, dtype=torch.int32)
         return SimpleNamespace(
             xcd_err=torch.tensor([err], dtype=torch.int32),
             m_cnt=None if mcnt is None else torch.tensor(mcnt, dtype=torch.int32),
-            o_cnt=None if ocnt is None else torch.tensor(ocnt, dtype=torch.int32), o_fin=o_fin)
+            o_cnt=None if ocnt is None else torch.tensor(ocnt, dtype=torch.int32), o_fin=o_fin,
+            ws_scr=ws)
+
+    def on():
+        DecodeEngine.ATTN_MERGE, DecodeEngine.O_FIN, DecodeEngine.LM_SCREEN = True, True, True
 
     try:
-        DecodeEngine.ATTN_MERGE, DecodeEngine.O_FIN = True, True
-        DecodeEngine.verify_handover(stand(mcnt=[0] * 64, ocnt=[0] * 32, o_fin=True))
-        assert DecodeEngine.ATTN_MERGE and DecodeEngine.O_FIN
+        on()
+        DecodeEngine.verify_handover(stand(mcnt=[0] * 64, ocnt=[0] * 32, o_fin=True,
+                                           lmcnt=[0] * 256))
+        assert DecodeEngine.ATTN_MERGE and DecodeEngine.O_FIN and DecodeEngine.LM_SCREEN
         # o_proj finish counters are ignored when that path is not in use
         DecodeEngine.verify_handover(stand(ocnt=[5], o_fin=False))
-        assert DecodeEngine.ATTN_MERGE and DecodeEngine.O_FIN
-        for bad in (stand(err=1), stand(mcnt=[0, 0, 0x100, 0]), stand(ocnt=[0, 3], o_fin=True)):
-            DecodeEngine.ATTN_MERGE, DecodeEngine.O_FIN = True, True
+        assert DecodeEngine.ATTN_MERGE and DecodeEngine.O_FIN and DecodeEngine.LM_SCREEN
+        for bad in (stand(err=1), stand(mcnt=[0, 0, 0x100, 0]), stand(ocnt=[0, 3], o_fin=True),
+                    stand(lmcnt=[0] * 32 + [0x20])):
+            on()
             with pytest.raises(RuntimeError, match="XCD"):
                 DecodeEngine.verify_handover(bad)
-            assert not DecodeEngine.ATTN_MERGE and not DecodeEngine.O_FIN
+            assert not (DecodeEngine.ATTN_MERGE or DecodeEngine.O_FIN or DecodeEngine.LM_SCREEN)
     finally:
-        DecodeEngine.ATTN_MERGE, DecodeEngine.O_FIN = saved
+        DecodeEngine.ATTN_MERGE, DecodeEngine.O_FIN, DecodeEngine.LM_SCREEN = saved
 
 
 def test_attention_handover_check_raises_and_switches_the_one_launch_form_off():
