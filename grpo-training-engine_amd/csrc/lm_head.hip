@@ -565,6 +565,15 @@ __device__ __forceinline__ float nan_max(float a, float b) {
   return (a != a || b != b) ? __builtin_nanf("") : fmaxf(a, b);
 }
 
+// bf16 bits of the smallest bf16 value >= f (an upper bound kept in 16 bits;
+// NaN stays NaN, +-inf stay): a positive value with dropped bits rounds its
+// magnitude up, a negative one truncates toward zero.
+__device__ __forceinline__ uint32_t bf16_up(float f) {
+  const uint32_t u = __float_as_uint(f);
+  if (f != f) return 0x7FC0u;
+  return (u >> 16) + ((u & 0xFFFFu) != 0u && f > 0.f ? 1u : 0u);
+}
+
 // One wave per vocabulary row; each lane handles 8 consecutive k per step
 // (one 8-byte piece of the screening tile order).
 __global__ void __launch_bounds__(256) lm_q8_kernel(const uint16_t* __restrict__ w,
@@ -647,7 +656,7 @@ struct ScreenArgs {
   const float* rnorm;
   float* ub;         // [M][NT]: largest zhat + e of the tile
   float* lbw;        // [M][nwg]: largest zhat - e of the workgroup
-  float* uv;         // [M][V]: zhat + e of every vocabulary row
+  uint16_t* uv;      // [V][8]: zhat + e of every vocabulary row, rows m < M, bf16 rounded up
   int nwg;
 };
 
@@ -772,7 +781,10 @@ __global__ void __launch_bounds__(64 * SC_W) lm_screen_kernel(ScreenArgs s) {
                                  q8_to_f16(w[jj].z, w[jj].w), acc);
     }
     if (ks == KS - 1) {
-      // lane (n = ln, group lg) holds sum_k x16[m][k] q[v][k] for m = 4 lg + r
+      // lane (n = ln, group lg) holds sum_k x16[m][k] q[v][k] for m = 4 lg + r;
+      // its four rows' bounds of vocabulary row v go out rounded up to bf16 in
+      // one 8-byte store (uv [v][8]: the tile's 256 bytes in one instruction)
+      float Ur[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int m = 4 * lg + r;
@@ -782,8 +794,8 @@ __global__ void __launch_bounds__(64 * SC_W) lm_screen_kernel(ScreenArgs s) {
           const float e = (sA[m] * rn + sB[m] * sc) * (1.f + 0x1p-16f) + fabsf(zh) * 0x1p-20f;
           U = zh + e;
           L = zh - e;
-          s.uv[(int64_t)m * p.V + tile * 16 + ln] = U;
         }
+        Ur[r] = U;
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) {
           U = nan_max(U, __shfl_xor(U, o));
@@ -792,6 +804,10 @@ __global__ void __launch_bounds__(64 * SC_W) lm_screen_kernel(ScreenArgs s) {
         if (ln == 0 && m < p.M) s.ub[(int64_t)m * p.NT + tile] = U;
         Lw[r] = nan_max(Lw[r], L);
       }
+      if (lg < 2)
+        *reinterpret_cast<uint2*>(s.uv + ((int64_t)tile * 16 + ln) * 8 + 4 * lg) =
+            make_uint2(bf16_up(Ur[0]) | (bf16_up(Ur[1]) << 16),
+                       bf16_up(Ur[2]) | (bf16_up(Ur[3]) << 16));
       acc = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
   };
@@ -824,7 +840,7 @@ struct ExactArgs {
   LmArgs lm;  // x source (NORM: h, sums of squares, norm weight), W in tile order, V, K, M, NT
   const float* ub;
   const float* lbw;
-  const float* uv;
+  const uint16_t* uv;
   int nwg;
   float* bestv;  // [8][EX_C]
   int* besti;    // [8][EX_C]
@@ -974,7 +990,7 @@ __global__ void __launch_bounds__(64 * EX_WAVES) lm_exact_advance_kernel(ExactAr
     constexpr int KB = 6;  // k-steps whose loads are in flight together
     uint4 w[KB][8];
     auto slot = [&](int tile) __attribute__((always_inline)) {
-      return !(e.uv[(int64_t)m * p.V + tile * 16 + ln] < thr);
+      return !(bf2f(e.uv[((int64_t)tile * 16 + ln) * 8 + m]) < thr);
     };
     auto load_ks = [&](int tile, int ks0, bool cs) __attribute__((always_inline)) {
       const uint16_t* wtile = p.w + (int64_t)tile * KS * 8 * 64 * 8;
@@ -1146,7 +1162,7 @@ constexpr size_t WS_UB = (WS_BESTI + 8 * EX_C * 4 + 255) / 256 * 256;
 
 size_t screen_ws_bytes(int M, int V) {
   const int NT = V / 16;
-  return WS_UB + ((size_t)M * NT + (size_t)M * screen_nwg(NT) + (size_t)M * V) * sizeof(float);
+  return WS_UB + ((size_t)M * NT + (size_t)M * screen_nwg(NT) + 3 + (size_t)4 * V) * sizeof(float);
 }
 
 int check_screen(const void* x, int64_t ldx, int V, int K, int M) {
@@ -1191,7 +1207,8 @@ int run_screen(const void* x, int64_t ldx, const LmNorm* nrm, const void* wq, co
   s.ub = reinterpret_cast<float*>(static_cast<char*>(ws) + WS_UB);
   s.nwg = screen_nwg(a.NT);
   s.lbw = s.ub + (size_t)M * a.NT;
-  s.uv = s.lbw + (size_t)M * s.nwg;
+  s.uv = reinterpret_cast<uint16_t*>(s.lbw + (size_t)M * s.nwg +
+                                     ((4 - ((size_t)M * (a.NT + s.nwg)) % 4) % 4));
   const size_t lds = (size_t)M * (K + 8) * 4 + (8 + 8 + 8 + SC_W * 8) * sizeof(float);
   if (nrm) {
     if (int rc = allow_dynamic_lds<lm_screen_kernel<true>, (int)LM_LDS_MAX>()) return rc;
@@ -1233,7 +1250,8 @@ int run_exact(const void* x, int64_t ldx, const LmNorm* nrm, const void* w_tiles
   e.ub = reinterpret_cast<const float*>(wb + WS_UB);
   e.nwg = screen_nwg(a.NT);
   e.lbw = e.ub + (size_t)M * a.NT;
-  e.uv = e.lbw + (size_t)M * e.nwg;
+  e.uv = reinterpret_cast<const uint16_t*>(e.lbw + (size_t)M * e.nwg +
+                                           ((4 - ((size_t)M * (a.NT + e.nwg)) % 4) % 4));
   e.bestv = reinterpret_cast<float*>(wb + WS_BESTV);
   e.besti = reinterpret_cast<int*>(wb + WS_BESTI);
   e.cnt = reinterpret_cast<int*>(wb + WS_CNT);

@@ -724,8 +724,9 @@ int grpo_lm_head_q8_tiles(const void* w, int V, int K, void* wq_tiles, float* sc
  * 2048 the screen's bounds: float [M][V / 16] (per row and 16-row tile, an
  * upper bound of the tile's float32 logits), float [M][W] (per row and
  * screening workgroup, W = min(V / 16, 256), a lower bound of the largest
- * logit among its tiles) and float [M][V] (per row and vocabulary row, an
- * upper bound of that logit). */
+ * logit among its tiles) and, from the next 16-byte boundary, bf16 [V][8]
+ * (per vocabulary row and row m < M, an upper bound of that logit, rounded
+ * up). */
 size_t grpo_lm_head_screen_workspace_bytes(int M, int V);
 
 /* The screen: for x [M, K] (M <= 8; the _norm form stages x = RMSNorm(h) as
