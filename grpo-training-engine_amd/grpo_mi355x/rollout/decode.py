@@ -106,7 +106,8 @@ class DecodeEngine:
         self.next = torch.zeros(B, dtype=torch.int64, device=dev)
         self._prepare_layers()
         self.graph: Optional[torch.cuda.CUDAGraph] = None
-        self.graph_multi: Optional[torch.cuda.CUDAGraph] = None  # MULTI_STEP steps
+        # MULTI_STEP steps, by the block width the attention splits are planned for
+        self.graph_multi: dict = {}
 
     # ------------------------------------------------------------- set-up --
     def _prepare_layers(self):
@@ -550,6 +551,10 @@ class DecodeEngine:
         lib, chk, pool = self.lib, _lib.check, self.pool
         Hq, Hkv, D = self.Hq, self.Hkv, self.D
         wsa, wsa_n = self.ws_attn.data_ptr(), self.ws_attn.numel()
+        # context splits planned for pw blocks (>= every row's context in the
+        # steps these launches run: _live_width), the same for the attention
+        # and the o_proj staging or merge that reads its partials
+        pw = self._pw or self.max_blocks
         wide = self.B > self.ATTN_STAGE_MAX_ROWS
         # one context split: the attention writes its bf16 output itself
         direct = wide and self.attn_splits == 1
@@ -558,7 +563,7 @@ class DecodeEngine:
             L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
             self.max_pos, self.append_pos.data_ptr(), self.attn_len.data_ptr(), kc, vc,
             pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
-            pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n,
+            pool.block_size, pw, 1.0 / math.sqrt(D), wsa, wsa_n,
             ao if direct else None, st), "attention"))
         if wide:
             # wide batches: o_proj stages the merged bf16 rows as plain x
@@ -570,13 +575,13 @@ class DecodeEngine:
                     L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
                     self.max_pos, self.append_pos.data_ptr(), self.attn_len.data_ptr(), kc, vc,
                     pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
-                    pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n,
+                    pool.block_size, pw, 1.0 / math.sqrt(D), wsa, wsa_n,
                     self.m_cnt.data_ptr(), self.xcd_err.data_ptr(), ao, None, 0, None, st),
                     "attention"))
             merge = [] if direct or self.wide_merge else [
                 ("attn_merge", lambda: chk(lib.grpo_paged_attn_merge(
                     wsa, self.attn_len.data_ptr(), self.B, Hq, Hkv, D, pool.block_size,
-                    self.max_blocks, ao, 1, st), "attn_merge"))]
+                    pw, ao, 1, st), "attn_merge"))]
             return [attention] + merge + [
                 ("o", lambda: chk(lib.grpo_nf4_linear_partials(
                     ao, Hq * D, L["o_w"].data_ptr(), L["o_absmax"].data_ptr(),
@@ -593,21 +598,21 @@ class DecodeEngine:
                     L["qkv_parts"], Hq, Hkv, D, self.cos.data_ptr(), self.sin.data_ptr(),
                     self.max_pos, self.append_pos.data_ptr(), self.attn_len.data_ptr(), kc, vc,
                     pool.num_blocks, self.block_tables.data_ptr(), self.max_blocks,
-                    pool.block_size, self.max_blocks, 1.0 / math.sqrt(D), wsa, wsa_n,
+                    pool.block_size, pw, 1.0 / math.sqrt(D), wsa, wsa_n,
                     self.m_cnt.data_ptr(), self.xcd_err.data_ptr(), ao,
                     la.data_ptr() if L["o_tile"].r > 0 else None, L["o_tile"].r,
                     self.o_lora_t.data_ptr(), st), "attention"))
                 return [merged, o_tile]
             merge = ("attn_merge", lambda: chk(lib.grpo_paged_attn_merge(
                 wsa, self.attn_len.data_ptr(), self.B, Hq, Hkv, D, pool.block_size,
-                self.max_blocks, ao, 1, st), "attn_merge"))
+                pw, ao, 1, st), "attn_merge"))
             return [attention, merge, o_tile]
         if self.o_fin:
             h = self.h.data_ptr()
             return [
                 attention,
                 ("o", lambda: chk(lib.grpo_nf4_linear_attn_residual(
-                    wsa, self.attn_len.data_ptr(), Hq, Hkv, D, pool.block_size, self.max_blocks,
+                    wsa, self.attn_len.data_ptr(), Hq, Hkv, D, pool.block_size, pw,
                     L["o_w"].data_ptr(), L["o_absmax"].data_ptr(), L["o_code"].data_ptr(),
                     self.bs, L["o_la"], L["o_parts"], self.o_tpart.data_ptr(),
                     self.o_cnt.data_ptr(), self.xcd_err.data_ptr(), h, h, self.H,
@@ -615,7 +620,7 @@ class DecodeEngine:
         return [
             attention,
             ("o", lambda: chk(lib.grpo_nf4_linear_partials_attn(
-                wsa, self.attn_len.data_ptr(), Hq, Hkv, D, pool.block_size, self.max_blocks,
+                wsa, self.attn_len.data_ptr(), Hq, Hkv, D, pool.block_size, pw,
                 L["o_w"].data_ptr(), L["o_absmax"].data_ptr(), L["o_code"].data_ptr(), self.bs,
                 L["o_la"], L["o_parts"], st), "o_proj"))]
 
@@ -810,9 +815,12 @@ class DecodeEngine:
                 self.generated = torch.full((B, max_new_tokens), pad_token_id, dtype=torch.int64,
                                             device=self.device)
                 self.graph = None  # the recorded step writes into this buffer
-                self.graph_multi = None
+                self.graph_multi = {}
             self.generated.fill_(pad_token_id)
         self._masks()
+        # bound on every row's position for run()'s choice of split plan (one
+        # host sync per batch)
+        self._pos_hi = int(positions.max()) if positions.numel() else 0
 
     def capture(self):
         """Record one step into a HIP graph (after two warm-up steps on a side stream)."""
@@ -832,7 +840,7 @@ class DecodeEngine:
             self._step()
         self._restore(saved)
         self.graph = g
-        self.graph_multi = None  # recorded at its first use (run)
+        self.graph_multi = {}  # recorded at their first use (run)
 
     def _restore(self, saved):
         for t, v in zip((self.tokens, self.pos, self.count, self.active), saved):
@@ -876,29 +884,64 @@ class DecodeEngine:
     # instead of one per step (7 us per step less at config 3)
     MULTI_STEP = 16
 
-    def _multi_graph(self) -> torch.cuda.CUDAGraph:
-        if self.graph_multi is None:
+    # Attention splits planned for the live context: the attention and the
+    # o_proj that reads its partials plan their context splits for pw blocks
+    # instead of the table width, pw covering every row's context in the
+    # graph's MULTI_STEP steps (rounded up to a multiple of an eighth of the
+    # table: at most 8 recorded graphs).  Fewer split slots for o_proj to
+    # stage while the contexts are short.  Where the table width plans 8
+    # blocks per split (config 3's 64-block tables), every width does, and
+    # the splits, and so the results, are the same as at the full width.
+    LIVE_WIDTH = True
+    _pw: Optional[int] = None  # plan width of the launches being built (None: the table's)
+    _pos_hi: Optional[int] = None
+
+    def _live_width(self, ctx: int) -> int:
+        """Plan width (blocks) covering contexts of up to ``ctx`` tokens."""
+        full = self.max_blocks
+        if not (self.LIVE_WIDTH and getattr(self, "attn_fused", False)
+                and getattr(self, "attn_splits", 1) > 1):
+            return full
+        unit = max(8, -(-full // 8))
+        need = -(-max(ctx, 1) // self.pool.block_size)
+        return min(full, -(-need // unit) * unit)
+
+    def _multi_graph(self, pw: Optional[int] = None) -> torch.cuda.CUDAGraph:
+        pw = pw or self.max_blocks
+        g = self.graph_multi.get(pw)
+        if g is None:
             # recording executes nothing: the row state is untouched
             s = torch.cuda.Stream(device=self.device)
             s.wait_stream(torch.cuda.current_stream(self.device))
             g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, stream=s):
-                for _ in range(self.MULTI_STEP):
-                    self._step()
+            self._pw = pw
+            try:
+                with torch.cuda.graph(g, stream=s):
+                    for _ in range(self.MULTI_STEP):
+                        self._step()
+            finally:
+                self._pw = None
             torch.cuda.current_stream(self.device).wait_stream(s)
-            self.graph_multi = g
-        return self.graph_multi
+            self.graph_multi[pw] = g
+        return g
 
     def run(self, steps: int):
         """``steps`` decode steps: graph replays of MULTI_STEP steps, then
-        single steps (rows that stop in between do nothing in later steps)."""
+        single steps (rows that stop in between do nothing in later steps).
+        Each replay's attention splits are planned for the contexts its steps
+        can reach (every row's position advances by at most one per step)."""
         if self.graph is not None and steps >= self.MULTI_STEP:
-            g = self._multi_graph()
             while steps >= self.MULTI_STEP:
-                g.replay()
+                pw = (self._live_width(self._pos_hi + self.MULTI_STEP)
+                      if self._pos_hi is not None else None)
+                self._multi_graph(pw).replay()
+                if self._pos_hi is not None:
+                    self._pos_hi += self.MULTI_STEP
                 steps -= self.MULTI_STEP
         for _ in range(steps):
             self.step()
+            if self._pos_hi is not None:
+                self._pos_hi += 1
 
     def compaction_engines(self, sizes=(16, 8)) -> list:
         """Greedy engines of fewer rows (``sizes`` below this engine's) over the
@@ -939,6 +982,7 @@ class DecodeEngine:
         self.generated.copy_(src.pad.view(1, 1).expand_as(self.generated))
         self.generated[:n].copy_(src.generated.index_select(0, idx))
         self._masks()
+        self._pos_hi = src._pos_hi
 
     def run_paged(self, sids: list, max_steps: int, chunk: Optional[int] = None,
                   check_invariants: bool = False, compact: Optional[list] = None) -> dict:
@@ -1023,6 +1067,7 @@ class DecodeEngine:
             if check_invariants:
                 pool.check_invariants()
             peak = max(peak, pool.num_blocks - pool.num_free)
+            eng._pos_hi = max(pos)
             eng.run(n)
             steps += n
         for b in list(live):  # rows cut off by max_steps

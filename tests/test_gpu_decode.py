@@ -388,3 +388,41 @@ def test_screened_head_gives_the_tokens_of_the_full_head(dev, monkeypatch):
         outs.append(eng.generated.clone())
     print("generated (screened):", outs[0][:, :8].tolist(), flush=True)
     assert torch.equal(outs[0], outs[1])
+
+
+def test_live_width_split_plan_gives_the_tokens_of_the_table_width(dev, monkeypatch):
+    """run() with the attention splits planned for the live contexts
+    (LIVE_WIDTH: each 16-step graph's attention and o_proj plan their splits
+    for the blocks its steps can reach) generates exactly the tokens of the
+    plan for the whole block table, over rollouts whose contexts grow across
+    several plan widths, with rows that stop at different lengths."""
+    from grpo_mi355x.core.kv_pool import PagedKVPool
+    from grpo_mi355x.rollout.decode import DecodeEngine
+
+    model = _model(dev, layers=2)
+    B, bs, width, new = 8, 16, 64, 200
+    outs, widths = [], []
+    for live in (True, False):
+        monkeypatch.setattr(DecodeEngine, "LIVE_WIDTH", live)
+        pool = PagedKVPool(2, B * width, 2, 128, bs, device=dev)
+        sids = [pool.allocate(width * bs) for _ in range(B)]
+        eng = DecodeEngine(model, pool, B, width)
+        assert eng.attn_splits > 1
+        g = torch.Generator().manual_seed(11)
+        tok = torch.randint(0, 1000, (B,), generator=g).to(dev)
+        pos = torch.tensor([0, 37, 80, 129, 170, 211, 260, 300], device=dev)
+        limits = torch.tensor([200, 3, 117, 200, 1, 29, 160, 64], device=dev)
+        table = pool.block_table(sids, width, device=dev)
+        eng.start(tok, pos, table, limits, new)
+        eng.capture()
+        for _ in range(2):
+            eng.start(tok, pos, table, limits, new)
+            eng.run(new)
+        torch.cuda.synchronize()
+        eng.verify_handover()
+        outs.append(eng.generated.clone())
+        widths.append(sorted(eng.graph_multi))
+    print("plan widths recorded:", widths, flush=True)
+    # positions 300 .. 500: widths 24 and 32 of the 64-block table
+    assert widths[0] == [24, 32] and widths[1] == [width]
+    assert torch.equal(outs[0], outs[1])

@@ -414,3 +414,55 @@ def test_attention_handover_check_raises_and_switches_the_one_launch_form_off():
         ops._attn_merge.clear()
         ops._attn_merge.update(saved[0])
         ops.ATTN_ONE_LAUNCH = saved[1]
+
+
+def test_live_width_covers_every_context_of_a_graph_replay():
+    """run() picks, for each 16-step graph replay, an attention plan width
+    (blocks) that covers every context its steps can reach -- the bound on the
+    rows' positions plus 16 tokens -- rounded up to an eighth of the table;
+    single steps run the table-width graph; without context splits (or with
+    LIVE_WIDTH off) the table width is kept."""
+    from grpo_mi355x.rollout.decode import DecodeEngine
+
+    class Pool:
+        block_size = 16
+
+    class Stand:
+        LIVE_WIDTH = True
+        MULTI_STEP = 16
+        _live_width = DecodeEngine._live_width
+
+        def __init__(self, full, splits=8):
+            self.max_blocks, self.attn_splits, self.attn_fused = full, splits, True
+            self.pool, self.graph, self.replayed, self.singles = Pool(), True, [], 0
+            self._pos_hi = None
+
+        def _multi_graph(self, pw=None):
+            outer = self
+
+            class G:
+                def replay(self):
+                    outer.replayed.append(pw)
+            return G()
+
+        def step(self):
+            self.singles += 1
+
+    s = Stand(64)
+    assert [s._live_width(c) for c in (1, 128, 129, 512, 513, 1024)] == [8, 8, 16, 32, 40, 64]
+    s._pos_hi = 511  # contexts 512 .. 527 in the first replay
+    DecodeEngine.run(s, 16 * 9 + 5)
+    assert s.replayed == [40] * 8 + [48] and s.singles == 5
+    assert s._pos_hi == 511 + 16 * 9 + 5
+    # the widths cover the contexts: a replay from position bound P reaches P + 16
+    for k, pw in enumerate(s.replayed):
+        assert pw * 16 >= 511 + 16 * k + 16
+    big = Stand(256)  # unit 32 blocks
+    assert [big._live_width(c) for c in (600, 2048, 4096, 5000)] == [64, 128, 256, 256]
+    assert Stand(64, splits=1)._live_width(100) == 64
+    off = Stand(64)
+    off.LIVE_WIDTH = False
+    assert off._live_width(100) == 64
+    none = Stand(64)  # no position bound (start not called): the table width
+    DecodeEngine.run(none, 32)
+    assert none.replayed == [None, None]
