@@ -892,6 +892,9 @@ class DecodeEngine:
     # stage while the contexts are short.  Where the table width plans 8
     # blocks per split (config 3's 64-block tables), every width does, and
     # the splits, and so the results, are the same as at the full width.
+    # Only where every split of every (row, KV head) pair still has a CU of its
+    # own (B * Hkv * 8 <= 256): more workgroups than CUs run in two rounds
+    # (config 4's 32-row engine: 8867 tok/s planned live against 8927).
     LIVE_WIDTH = True
     _pw: Optional[int] = None  # plan width of the launches being built (None: the table's)
     _pos_hi: Optional[int] = None
@@ -900,7 +903,7 @@ class DecodeEngine:
         """Plan width (blocks) covering contexts of up to ``ctx`` tokens."""
         full = self.max_blocks
         if not (self.LIVE_WIDTH and getattr(self, "attn_fused", False)
-                and getattr(self, "attn_splits", 1) > 1):
+                and getattr(self, "attn_splits", 1) > 1 and self.B * self.Hkv * 8 <= 256):
             return full
         unit = max(8, -(-full // 8))
         need = -(-max(ctx, 1) // self.pool.block_size)

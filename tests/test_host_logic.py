@@ -420,8 +420,9 @@ def test_live_width_covers_every_context_of_a_graph_replay():
     """run() picks, for each 16-step graph replay, an attention plan width
     (blocks) that covers every context its steps can reach -- the bound on the
     rows' positions plus 16 tokens -- rounded up to an eighth of the table;
-    single steps run the table-width graph; without context splits (or with
-    LIVE_WIDTH off) the table width is kept."""
+    single steps run the table-width graph; without context splits, with
+    more split workgroups than CUs, or with LIVE_WIDTH off the table width is
+    kept."""
     from grpo_mi355x.rollout.decode import DecodeEngine
 
     class Pool:
@@ -432,8 +433,9 @@ def test_live_width_covers_every_context_of_a_graph_replay():
         MULTI_STEP = 16
         _live_width = DecodeEngine._live_width
 
-        def __init__(self, full, splits=8):
+        def __init__(self, full, splits=8, rows=8):
             self.max_blocks, self.attn_splits, self.attn_fused = full, splits, True
+            self.B, self.Hkv = rows, 2
             self.pool, self.graph, self.replayed, self.singles = Pool(), True, [], 0
             self._pos_hi = None
 
@@ -460,6 +462,8 @@ def test_live_width_covers_every_context_of_a_graph_replay():
     big = Stand(256)  # unit 32 blocks
     assert [big._live_width(c) for c in (600, 2048, 4096, 5000)] == [64, 128, 256, 256]
     assert Stand(64, splits=1)._live_width(100) == 64
+    # 32 rows x 2 KV heads x 8 splits would be two rounds of workgroups
+    assert Stand(64, rows=16)._live_width(100) == 8 and Stand(64, rows=32)._live_width(100) == 64
     off = Stand(64)
     off.LIVE_WIDTH = False
     assert off._live_width(100) == 64
