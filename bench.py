@@ -285,9 +285,10 @@ def run_cfg4(args):
     parents = [prefill(pre, pool, tuple(p), width) for p in prompts]
     del pre
     eng = DecodeEngine(model, pool, G, width)
-    # row compaction: the rows still decoding move to a 16- and then an 8-row
-    # engine once they fit (the long tail of the group runs on the cheaper step)
-    ladder = eng.compaction_engines((16, 8))
+    # row compaction: the rows still decoding move to a 24-, a 16- and then an
+    # 8-row engine once they fit (the long tail of the group runs on the
+    # cheaper steps)
+    ladder = eng.compaction_engines((24, 16, 8))
     rows = [prompts[i // S] for i in range(G)]
 
     def rollout():

@@ -946,7 +946,7 @@ class DecodeEngine:
             if self._pos_hi is not None:
                 self._pos_hi += 1
 
-    def compaction_engines(self, sizes=(16, 8)) -> list:
+    def compaction_engines(self, sizes=(24, 16, 8)) -> list:
         """Greedy engines of fewer rows (``sizes`` below this engine's) over the
         same model, pool and block-table width, for ``run_paged(...,
         compact=...)``: once the rows still decoding fit a smaller engine,
