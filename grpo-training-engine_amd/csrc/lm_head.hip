@@ -1221,12 +1221,17 @@ int run_screen(const void* x, int64_t ldx, const LmNorm* nrm, const void* wq, co
 }
 
 int run_exact(const void* x, int64_t ldx, const LmNorm* nrm, const void* w_tiles, int V, int K,
-              int M, void* ws, int* xcd_err, int64_t* next_out, int64_t* tokens, int32_t* pos,
+              int M, void* ws, size_t ws_bytes, int* xcd_err, int64_t* next_out, int64_t* tokens, int32_t* pos,
               int32_t* count, const int32_t* limit, uint8_t* active, const int64_t* eos,
               int64_t* generated, int64_t gen_ld, int32_t* append_pos, int32_t* attn_len,
               hipStream_t st) {
   if (int rc = check_screen(x, ldx, V, K, M)) return rc;
   if (!w_tiles || !ws || !aligned16(w_tiles)) return einval("null or misaligned pointer");
+  if (ws_bytes < screen_ws_bytes(M, V)) {
+    set_error("invalid argument: workspace of %zu bytes needed, %zu given",
+              screen_ws_bytes(M, V), ws_bytes);
+    return GRPO_EWORKSPACE;
+  }
   if (tokens && (!pos || !count || !limit || !active || !eos || !append_pos || !attn_len))
     return einval("null row state");
   if (generated && gen_ld <= 0) return einval("gen_ld must be > 0");
@@ -1319,25 +1324,28 @@ extern "C" int grpo_lm_head_screen_norm(const void* h, int64_t ldh, const float*
 }
 
 extern "C" int grpo_lm_head_exact_argmax(const void* x, int64_t ldx, const void* w_tiles, int V,
-                                         int K, int M, void* screen_workspace, int* xcd_err,
+                                         int K, int M, void* screen_workspace,
+                                         size_t workspace_bytes, int* xcd_err,
                                          int64_t* next_tokens, grpo_stream_t stream) {
   if (!next_tokens) return einval("null next_tokens");
-  return run_exact(x, ldx, nullptr, w_tiles, V, K, M, screen_workspace, xcd_err, next_tokens,
+  return run_exact(x, ldx, nullptr, w_tiles, V, K, M, screen_workspace, workspace_bytes, xcd_err,
+                   next_tokens,
                    nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, nullptr, 0, nullptr,
                    nullptr, as_stream(stream));
 }
 
 extern "C" int grpo_lm_head_exact_advance_norm(
     const void* h, int64_t ldh, const float* sumsq, int groups, const void* norm_weight, float eps,
-    const void* w_tiles, int V, int K, int M, void* screen_workspace, int* xcd_err,
-    int64_t* next_tokens, int64_t* tokens, int32_t* pos, int32_t* count, const int32_t* limit, uint8_t* active,
+    const void* w_tiles, int V, int K, int M, void* screen_workspace, size_t workspace_bytes,
+    int* xcd_err, int64_t* next_tokens, int64_t* tokens, int32_t* pos, int32_t* count, const int32_t* limit, uint8_t* active,
     const int64_t* eos, int64_t* generated, int64_t gen_ld, int32_t* append_pos,
     int32_t* attn_len, grpo_stream_t stream) {
   if (!sumsq || !norm_weight) return einval("null pointer");
   if (groups < 1 || groups > LM_NORM_MAX_GROUPS) return einval("groups must be in [1, 256]");
   if (!aligned16(norm_weight)) return einval("norm_weight must be 16-byte aligned");
   const LmNorm n{sumsq, groups, static_cast<const uint16_t*>(norm_weight), eps};
-  return run_exact(h, ldh, &n, w_tiles, V, K, M, screen_workspace, xcd_err, next_tokens, tokens,
+  return run_exact(h, ldh, &n, w_tiles, V, K, M, screen_workspace, workspace_bytes, xcd_err,
+                   next_tokens, tokens,
                    pos, count, limit, active, eos, generated, gen_ld, append_pos, attn_len,
                    as_stream(stream));
 }

@@ -182,10 +182,10 @@ SIGNATURES = {
     "grpo_lm_head_screen_norm": (
         _I32, [_VP, _I64, _VP, _I32, _VP, _F32, _VP, _VP, _VP, _I32, _I32, _I32, _VP, _SZ, _VP]),
     "grpo_lm_head_exact_argmax": (
-        _I32, [_VP, _I64, _VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP]),
+        _I32, [_VP, _I64, _VP, _I32, _I32, _I32, _VP, _SZ, _VP, _VP, _VP]),
     "grpo_lm_head_exact_advance_norm": (
-        _I32, [_VP, _I64, _VP, _I32, _VP, _F32, _VP, _I32, _I32, _I32, _VP, _VP, _VP, _VP, _VP,
-               _VP, _VP, _VP, _VP, _VP, _I64, _VP, _VP, _VP]),
+        _I32, [_VP, _I64, _VP, _I32, _VP, _F32, _VP, _I32, _I32, _I32, _VP, _SZ, _VP, _VP, _VP,
+               _VP, _VP, _VP, _VP, _VP, _VP, _I64, _VP, _VP, _VP]),
     "grpo_nf4_linear_residual": (
         _I32, [_VP, _I64, _I32, _VP, _VP, _VP, _I32, _I32, _I32, _I32, _VP, _I64, _VP, _I64,
                _VP, _VP]),

@@ -749,7 +749,8 @@ class DecodeEngine:
                 "lm_screen")),
             ("advance", lambda: chk(lib.grpo_lm_head_exact_advance_norm(
                 h, H, ss, H // 8, self.final_norm.data_ptr(), self.final_eps,
-                self.lm_w.data_ptr(), self.V, H, B, ws.data_ptr(), self.xcd_err.data_ptr(),
+                self.lm_w.data_ptr(), self.V, H, B, ws.data_ptr(), ws.numel(),
+                self.xcd_err.data_ptr(),
                 self.next.data_ptr(), self.tokens.data_ptr(), self.pos.data_ptr(),
                 self.count.data_ptr(), self.limit.data_ptr(), self.active.data_ptr(),
                 self.eos.data_ptr(), None if gen is None else gen.data_ptr(),

@@ -754,13 +754,15 @@ int grpo_lm_head_screen_norm(const void* h, int64_t ldh, const float* sumsq, int
  * counter is left non-zero).  The _advance_norm form stages x = RMSNorm(h) and
  * then does grpo_decode_advance's bookkeeping (next_tokens may be NULL
  * there); a row that is not active keeps its token and computes nothing.
- * Calls sharing a workspace must not overlap. */
+ * workspace_bytes is checked against grpo_lm_head_screen_workspace_bytes(M, V)
+ * (GRPO_EWORKSPACE below it).  Calls sharing a workspace must not overlap. */
 int grpo_lm_head_exact_argmax(const void* x, int64_t ldx, const void* w_tiles, int V, int K, int M,
-                              void* screen_workspace, int* xcd_err, int64_t* next_tokens,
-                              grpo_stream_t stream);
+                              void* screen_workspace, size_t workspace_bytes, int* xcd_err,
+                              int64_t* next_tokens, grpo_stream_t stream);
 int grpo_lm_head_exact_advance_norm(const void* h, int64_t ldh, const float* sumsq, int groups,
                                     const void* norm_weight, float eps, const void* w_tiles, int V,
-                                    int K, int M, void* screen_workspace, int* xcd_err,
+                                    int K, int M, void* screen_workspace,
+                                    size_t workspace_bytes, int* xcd_err,
                                     int64_t* next_tokens, int64_t* tokens, int32_t* pos,
                                     int32_t* count, const int32_t* limit, uint8_t* active,
                                     const int64_t* eos, int64_t* generated, int64_t gen_ld,

@@ -104,6 +104,18 @@ def test_argument_errors_return_negative_codes(lib):
     d.seg_end[0] = 256
     d.r = 16
     assert lib.grpo_add_rmsnorm_parts(d, None, None, None, None, 1e-6, None) < 0  # no tpart
+    # the screened lm_head's passes check the workspace against its size (before
+    # any launch: the addresses below are never dereferenced)
+    V, K, M, fake = 4096, 512, 4, 1 << 20
+    need = lib.grpo_lm_head_screen_workspace_bytes(M, V)
+    assert need > 2048
+    assert lib.grpo_lm_head_screen(fake, K, fake, fake, fake, V, K, M, fake, need - 1,
+                                   None) == -3  # GRPO_EWORKSPACE
+    assert lib.grpo_lm_head_exact_argmax(fake, K, fake, V, K, M, fake, need - 1, None, fake,
+                                         None) == -3
+    assert b"workspace" in lib.grpo_last_error()
+    assert lib.grpo_lm_head_exact_argmax(fake, K, fake, V, K, 9, fake, need, None, fake,
+                                         None) < 0  # rows
 
 
 def test_check_maps_codes_to_reference_exceptions(lib):

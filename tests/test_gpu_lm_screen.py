@@ -64,7 +64,8 @@ def _screened(lib, _l, x, wq, scale, rnorm, wt, V, K, dev):
     nxt = torch.full((M,), -7, dtype=torch.int64, device=dev)
     err = torch.zeros(1, dtype=torch.int32, device=dev)
     _l.check(lib.grpo_lm_head_exact_argmax(x.data_ptr(), x.stride(0), wt.data_ptr(), V, K, M,
-                                           ws.data_ptr(), err.data_ptr(), nxt.data_ptr(), st),
+                                           ws.data_ptr(), ws.numel(), err.data_ptr(),
+                                           nxt.data_ptr(), st),
              "exact")
     torch.cuda.synchronize()
     # the hand-over ran on one XCD per row and left its counters at zero
@@ -209,7 +210,7 @@ def test_screened_advance_norm_matches_full(dev):
                                           V, K, M, sws.data_ptr(), sws.numel(), st), "screen")
     _l.check(lib.grpo_lm_head_exact_advance_norm(
         h.data_ptr(), K, ss.data_ptr(), K // 8, nw.data_ptr(), 1e-6, wt.data_ptr(), V, K, M,
-        sws.data_ptr(), err.data_ptr(), b["nxt"].data_ptr(), b["tokens"].data_ptr(), b["pos"].data_ptr(),
+        sws.data_ptr(), sws.numel(), err.data_ptr(), b["nxt"].data_ptr(), b["tokens"].data_ptr(), b["pos"].data_ptr(),
         b["count"].data_ptr(), b["limit"].data_ptr(), b["active"].data_ptr(), b["eos"].data_ptr(),
         b["gen"].data_ptr(), 9, b["app"].data_ptr(), b["alen"].data_ptr(), st), "exact")
     torch.cuda.synchronize()
