@@ -21,8 +21,13 @@ NATIVE_DIR = PKG_DIR / "_native"
 LIB_PATH = NATIVE_DIR / "libgrpo_hip.so"
 ARCH = "gfx950"
 
-SOURCES = ("capi.hip", "nf4_linear.hip", "nf4_tile.hip", "nf4_gemm.hip", "paged_attention.hip",
-           "decode_ops.hip", "lm_head.hip", "sampling.hip", "nf4_backward.hip")
+SOURCES = ("capi.hip", "nf4_linear.hip", "nf4_fold.hip", "nf4_tile.hip", "nf4_gemm.hip",
+           "paged_attention.hip", "decode_ops.hip", "lm_head.hip", "sampling.hip",
+           "nf4_backward.hip")
+
+# Flags of one source only: the folded down_proj kernel is scheduled for
+# instruction-level parallelism (it runs two waves per SIMD; nf4_fold.hip).
+SOURCE_FLAGS = {"nf4_fold.hip": ("-mllvm", "-amdgpu-sched-strategy=max-ilp")}
 
 
 def hipcc() -> str:
@@ -40,12 +45,6 @@ COMPILE_FLAGS = (
     # Keep the compiler from emitting packed-FP32 VALU ops (v_pk_*_f32).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 )
-
-
-def build_command(out: Path) -> list[str]:
-    """One hipcc command that compiles and links every source (reference form)."""
-    srcs = [str(CSRC / s) for s in SOURCES if (CSRC / s).exists()]
-    return [hipcc(), *COMPILE_FLAGS, "-shared", "-o", str(out), *srcs]
 
 
 def _run(cmd: list[str]) -> None:
@@ -78,7 +77,7 @@ def build_library(verbose: bool = False, jobs: int = 0, incremental: bool = Fals
         return (not incremental or not o.exists()
                 or o.stat().st_mtime < max(s.stat().st_mtime, hdr))
 
-    cmds = [[cc, *COMPILE_FLAGS, "-c", "-o", str(o), str(s)]
+    cmds = [[cc, *COMPILE_FLAGS, *SOURCE_FLAGS.get(s.name, ()), "-c", "-o", str(o), str(s)]
             for s, o in zip(srcs, objs) if stale(s, o)]
     jobs = jobs or max(1, min(len(cmds), os.cpu_count() or 1))
     if verbose:
