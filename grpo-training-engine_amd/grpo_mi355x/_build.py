@@ -25,9 +25,13 @@ SOURCES = ("capi.hip", "nf4_linear.hip", "nf4_fold.hip", "nf4_tile.hip", "nf4_ge
            "paged_attention.hip", "decode_ops.hip", "lm_head.hip", "sampling.hip",
            "nf4_backward.hip")
 
-# Flags of one source only: the folded down_proj kernel is scheduled for
-# instruction-level parallelism (it runs two waves per SIMD; nf4_fold.hip).
-SOURCE_FLAGS = {"nf4_fold.hip": ("-mllvm", "-amdgpu-sched-strategy=max-ilp")}
+# Flags of one source only (machine-scheduler strategies measured per source
+# on the decode step): the folded down_proj kernel is scheduled for
+# instruction-level parallelism (it runs two waves per SIMD; nf4_fold.hip), the
+# attention kernels for clauses of memory operations (same registers; config 3
+# 3637 -> 3670 tok/s).
+SOURCE_FLAGS = {"nf4_fold.hip": ("-mllvm", "-amdgpu-sched-strategy=max-ilp"),
+                "paged_attention.hip": ("-mllvm", "-amdgpu-sched-strategy=max-memory-clause")}
 
 
 def hipcc() -> str:
