@@ -144,3 +144,16 @@ def test_no_device_means_import_error():
         kernels.lora_fused_forward(torch.zeros(1, 1, 4))
     with pytest.raises(ImportError):
         kernels.paged_kv_decode(None, torch.zeros(1, 1, dtype=torch.long))
+
+
+def test_build_compiles_every_source_with_its_flags():
+    """Every HIP source in csrc/ is built, each per-source flag set names a
+    built source, and the per-source flags are machine-scheduler strategies
+    only (they change instruction order, not results)."""
+    from grpo_mi355x import _build
+
+    csrc = {p.name for p in _build.CSRC.glob("*.hip")}
+    assert csrc == set(_build.SOURCES)
+    assert set(_build.SOURCE_FLAGS) <= set(_build.SOURCES)
+    for flags in _build.SOURCE_FLAGS.values():
+        assert flags[0] == "-mllvm" and flags[1].startswith("-amdgpu-sched-strategy=")
