@@ -1304,10 +1304,12 @@ __global__ void __launch_bounds__(128 * S) nf4_gate_up_silu(GuArgs p) {
 // of 8-column units differs by at most one unit, not by one 16-column pair).
 // Item partial tiles meet in LDS and are summed in k-step order.
 constexpr int GUU_XU = 6;  // x chunks per thread loaded before the weights
+// Items whose weights are in flight ahead of the one decoded: one (config 3
+// 3670 -> 3686 tok/s and config 4 9214 -> 9284 against two; three gave 3618).
 #ifndef GRPO_GUU_LA
-#define GRPO_GUU_LA 2
+#define GRPO_GUU_LA 1
 #endif
-constexpr int GUU_LA = GRPO_GUU_LA;  // items whose weights are in flight ahead of the one decoded
+constexpr int GUU_LA = GRPO_GUU_LA;
 
 // MT row tiles of 16 (MT = 2: 17..32 rows, whose x of K <= 1536 still fits
 // LDS whole with the item tiles: config 4's G = 32).  ROWS (M <= 8, the
